@@ -1,0 +1,166 @@
+/*
+ * quipsharp_hip.h -- C ABI of libquipsharp_hip.so, the MI355X (gfx950) kernels
+ * behind the quipsharp_amd Python package.
+ *
+ * Conventions
+ *   - Every pointer argument is a device pointer unless stated otherwise;
+ *     tensors are dense with the strides given in elements.
+ *   - Every entry point enqueues work on `stream` (a hipStream_t; NULL is the
+ *     default stream) and returns without synchronising.  Entry points are
+ *     reentrant: the library keeps no mutable global state besides the
+ *     per-thread error string.
+ *   - Return value: QS_OK, or an error code with a message available from
+ *     qs_last_error() on the calling thread.  Argument errors are detected on
+ *     the host before anything is launched.
+ *   - No entry point allocates memory; callers pass workspaces.
+ *
+ * Reference: numbersletter/quipsharp (pure PyTorch).  Each entry point names
+ * the reference function(s) whose computation it performs.
+ */
+#ifndef QUIPSHARP_HIP_H
+#define QUIPSHARP_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void *qs_stream_t;
+
+enum {
+  QS_OK = 0,
+  QS_ERR_INVALID = 1,     /* bad argument (shape, stride, dtype, null pointer) */
+  QS_ERR_HIP = 2,         /* the HIP runtime reported an error */
+  QS_ERR_UNSUPPORTED = 3  /* valid request outside what these kernels implement */
+};
+
+enum { QS_STAGE_E8P = 0, QS_STAGE_E8_1BIT = 1 };          /* residual-VQ stage codebooks */
+enum { QS_DTYPE_F32 = 0, QS_DTYPE_F16 = 1, QS_DTYPE_BF16 = 2 };
+enum { QS_LAYOUT_ROWMAJOR = 0, QS_LAYOUT_TILED = 1 };     /* packed-code layouts */
+
+#define QS_ABI_VERSION 1
+#define QS_MAX_STAGES 4
+#define QS_MAX_KRON 64 /* largest odd factor of a Kronecker transform */
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *qs_last_error(void);
+int qs_abi_version(void);
+
+/* Host copies of the device codebook tables, 256 x 8 fp32 each (host pointer).
+ * quipsharp/codebooks/e8p.py:84-89 build_abs_table;
+ * quipsharp/codebooks/e8_1bit.py:66-70 build_table. */
+int qs_e8p_abs_table(float *out_host);
+int qs_e81_table(float *out_host);
+
+/* ---------------------------------------------------------------------------
+ * Codebook encode / decode
+ * ------------------------------------------------------------------------- */
+
+/* Residual-VQ nearest-codeword encode of nvec 8-vectors, bit-exact with the
+ * reference's fp32 CPU arithmetic (ties resolved the same way).
+ *   quipsharp/rvq.py:69-80 rvq_quantize, with stage codebooks
+ *   quipsharp/codebooks/e8p.py:104-171 (E8PCodebook.quantize) and
+ *   quipsharp/codebooks/e8_1bit.py:80-83 (E8OneBitCodebook.quantize).
+ * A single stage of scale 1.0 is exactly E8PCodebook.quantize /
+ * E8OneBitCodebook.quantize.  The input is first divided by in_div and the
+ * summed output multiplied by out_mul (IEEE fp32; 1.0 leaves values
+ * unchanged), which is ``codebook.quantize(x / s)`` followed by ``vals * s``
+ * of the scale sweep quipsharp/rvq.py:28-37.
+ *   x      [nvec][ldx] fp32 (first 8 of each row used)
+ *   kinds, scales: host arrays of nstages (1..QS_MAX_STAGES) entries
+ *   vals   [nvec][ldv] fp32 output, the summed dequantized approximation (may be NULL)
+ *   codes  output, element (s, k) at codes + s*code_stage_stride + k*code_stride,
+ *          code_bytes 2 (int16/uint16), 4 (int32) or 8 (int64); may be NULL. */
+int qs_rvq_encode(const float *x, int64_t ldx, int64_t nvec, int nstages, const int *kinds,
+                  const float *scales, float in_div, float out_mul, float *vals, int64_t ldv,
+                  void *codes, int code_bytes, int64_t code_stage_stride, int64_t code_stride,
+                  qs_stream_t stream);
+
+/* out[i] = in[i] / divisor, IEEE fp32 (torch's CPU ``tensor / float``,
+ * e.g. quipsharp/quantize.py:85 ``what / layer_scale``).  out may equal in. */
+int qs_div_f32(const float *in, float *out, int64_t count, float divisor, qs_stream_t stream);
+
+/* Decode: out[k][0..7] = (sum_s fl(Q_s(code_s,k) * scales[s])) * out_scale,
+ * every product and sum rounded as in quipsharp/rvq.py:83-88 followed by the
+ * ``* layer.scale`` of quipsharp/quantize.py:113.  Codes are read as unsigned
+ * 16-bit values (E8P) or 8-bit values (E8 1-bit) of width code_bytes. */
+int qs_rvq_decode(const void *codes, int code_bytes, int64_t code_stage_stride, int64_t nvec,
+                  int nstages, const int *kinds, const float *scales, float out_scale,
+                  float *out, qs_stream_t stream);
+
+/* One BlockLDLQ rounding step on block column k, fused:
+ *   target = base + delta            (dinv == NULL, base pass, ldlq.py:126-128)
+ *   target = base + delta @ dinv     (dinv = 8x8 fp32, refinement, ldlq.py:136-138)
+ *   q      = rvq_quantize(target)    (the codebook callback, quantize.py:90-93)
+ *   wq[r][0..7] = q ; resid[r][0..7] = w[r][0..7] - q  (resid may be NULL)
+ *   codes  written like qs_rvq_encode.
+ * base, w, wq, resid are row-strided views (ld* elements per row) of m rows;
+ * delta is [m][8] contiguous.  base may alias wq. */
+int qs_ldlq_step(const float *base, int64_t ldbase, const float *delta, const float *dinv,
+                 const float *w, int64_t ldw, float *wq, int64_t ldwq, float *resid,
+                 int64_t ldresid, int64_t m, int nstages, const int *kinds, const float *scales,
+                 void *codes, int code_bytes, int64_t code_stage_stride, int64_t code_stride,
+                 qs_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Randomized Hadamard transform
+ * ------------------------------------------------------------------------- */
+
+/* out = post_axis (.) T_n( pre_axis (.) pre_inner (.) in ) along the middle axis
+ * of in viewed as [outer][n][inner] (fp32, contiguous; out may equal in).
+ *   kron_p == 1 : T_n is the orthonormal Sylvester Walsh-Hadamard transform,
+ *                 bit-exact with quipsharp/hadamard.py:17-40 fwht (stages
+ *                 h = 1,2,4,... then * fl(n^-1/2)); n a power of two.
+ *   kron_p  > 1 : n = kron_p * 2^k with kron_p odd; T_n = K (x) H_{2^k}, the
+ *                 Walsh-Hadamard stages first, then the kron_p x kron_p
+ *                 orthogonal symmetric matrix kron_mat (device, fp32, row-major)
+ *                 along the outer index.  New transform kind for dims the
+ *                 reference routes to RFFT (quipsharp/incoherence.py:115-131).
+ * pre_axis/post_axis: length n, pre_inner: length inner; any may be NULL.
+ * Signs used by incoherence_process (quipsharp/incoherence.py:48-71),
+ * reconstruct_* (:74-83) and transform_input/output (:86-93). */
+int qs_rht_f32(const float *in, float *out, int64_t outer, int64_t n, int64_t inner,
+               const float *pre_axis, const float *pre_inner, const float *post_axis, int kron_p,
+               const float *kron_mat, qs_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Quantized linear forward (quipsharp/quantize.py:116-124 linear_forward,
+ * quipsharp/checkpoint.py:141-146 QuantizedLinear.forward)
+ * ------------------------------------------------------------------------- */
+
+/* Repack reference-layout codes (int16/int32/int64 [m][T], T = n/8, one stage)
+ * into the kernel layout.  QS_LAYOUT_TILED needs m % 16 == 0 and n % 256 == 0:
+ * tiles of 16 rows x 32 codes, each code re-encoded so both halves of the
+ * codeword index a 4096-entry table directly.  stage_kind selects E8P
+ * (16-bit output) or E8 1-bit (8-bit output).  QS_LAYOUT_ROWMAJOR keeps the
+ * order and writes the low 16 (8) bits. */
+int qs_pack_codes(const void *codes, int code_bytes, int64_t m, int64_t n, int stage_kind,
+                  int layout, void *out, qs_stream_t stream);
+
+/* Workspace bytes needed by qs_linear_forward for this shape and batch. */
+size_t qs_linear_workspace_bytes(int64_t m, int64_t n, int64_t batch, int layout);
+
+/* y = su (.) T_m( layer_scale * W_hat @ T_n(sv (.) x) ) + bias for batch rows,
+ * with W_hat decoded on the fly from packed codes:
+ *   W_hat[r] = s0 * E8P(codes0[r]) (+ s1 * E8_1bit(codes1[r]) when codes1 != NULL)
+ *   x      [batch][ldx] in x_dtype, y [batch][ldy] in y_dtype
+ *   codes0 packed E8P codes; codes1 packed second-stage codes or NULL, of kind
+ *          kind1 (QS_STAGE_E8_1BIT, or QS_STAGE_E8P on the row-major layout)
+ *   sv [n], su [m] fp32 sign vectors; kron_* as in qs_rht_f32 (p = 1: FWHT)
+ *   bias [m] fp32 or NULL
+ * Activations enter the matrix cores as fp16 (per-row power-of-two scaled),
+ * decoded weights are exact in fp16, accumulation is fp32. */
+int qs_linear_forward(const void *x, int x_dtype, int64_t ldx, int64_t batch, int64_t n, int64_t m,
+                      const void *codes0, const void *codes1, int kind1, int layout, const float *sv,
+                      const float *su, int kron_pn, const float *kron_n, int kron_pm,
+                      const float *kron_m, float s0, float s1, float layer_scale,
+                      const float *bias, void *y, int y_dtype, int64_t ldy, void *workspace,
+                      size_t workspace_bytes, qs_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QUIPSHARP_HIP_H */

@@ -1,0 +1,124 @@
+"""Codebook construction and the quantized ``nn.Module`` (quipsharp/checkpoint.py:56-156).
+
+``QuantizedLinear`` keeps the reference's buffers (int16 ``codes``, fp32
+``scale``, ``su``/``sv`` signs, optional ``bias``) so state dicts move
+between the two implementations; on first use on a device the codes are
+repacked once into the kernel layout (a non-persistent cache), and
+``forward`` runs the fused decode + transform + matvec kernels in the
+activation dtype (bf16/fp16/fp32) without a dense weight.
+"""
+import torch
+from torch import nn, Tensor
+
+from .codebooks.e8_1bit import E8OneBitCodebook
+from .codebooks.e8p import E8PCodebook
+from .incoherence import IncoherenceSigns, KronSigns
+from .quantize import PackedCodes, QuantizedLayer, RVQCodebookAdapter, _forward_params, forward_packed
+from .rvq import RVQStage, fit_residual_stage_scale, fit_stage_scale
+
+
+def num_rvq_stages(bits: str) -> int:
+    """quipsharp/checkpoint.py:56-57."""
+    return 1 if bits == "2bit" else 2
+
+
+def build_codebook(bits: str, device, seed: int = 0):
+    """(codebook, fitted input scale) for "2bit" (E8P), "3bit" (E8P + E8 1-bit)
+    or "4bit" (E8P + E8P) -- quipsharp/checkpoint.py:60-77, same seeds and
+    sample counts, so the same scales are chosen."""
+    e8p = E8PCodebook(device=device)
+    e8p_scale = fit_stage_scale(e8p, seed=seed, device=device, n_samples=20_000)
+    if bits == "2bit":
+        return e8p, e8p_scale
+    second = E8OneBitCodebook(device=device) if bits == "3bit" else E8PCodebook(device=device)
+    second_scale = fit_residual_stage_scale([RVQStage(e8p, e8p_scale)], second, seed=seed + 1, device=device,
+                                            n_samples=20_000)
+    rvq_cb = RVQCodebookAdapter([RVQStage(e8p, e8p_scale), RVQStage(second, second_scale)])
+    rvq_scale = fit_stage_scale(rvq_cb, seed=seed + 2, device=device, n_samples=20_000)
+    return rvq_cb, rvq_scale
+
+
+class QuantizedLinear(nn.Module):
+    """Drop-in for a quantized nn.Linear (quipsharp/checkpoint.py:80-146).
+
+    transform_kind: "rht" (power-of-two dims) or "krht" (Kronecker transform
+    for other dims).  "rfft" checkpoints of the reference are not supported.
+    """
+
+    def __init__(self, in_features: int, out_features: int, g: int, transform_kind: str, num_stages: int = 1,
+                 has_bias: bool = False):
+        super().__init__()
+        if transform_kind not in ("rht", "krht"):
+            raise NotImplementedError(f"transform_kind {transform_kind!r} is not supported (rht, krht)")
+        self.in_features = in_features
+        self.out_features = out_features
+        self.g = g
+        self.transform_kind = transform_kind
+        self.num_stages = num_stages
+        self.codebook = None  # assigned by the caller
+        self.register_buffer("bias", torch.zeros(out_features) if has_bias else None)
+        T = in_features // g
+        shape = (out_features, T) if num_stages == 1 else (num_stages, out_features, T)
+        self.register_buffer("codes", torch.zeros(shape, dtype=torch.int16))
+        self.register_buffer("scale", torch.zeros(()))
+        self.register_buffer("su", torch.zeros(out_features))
+        self.register_buffer("sv", torch.zeros(in_features))
+        self._packed = None
+        self._packed_key = None
+
+    @classmethod
+    def from_quantized_layer(cls, layer: QuantizedLayer, bias: Tensor = None) -> "QuantizedLinear":
+        m, n = layer.shape
+        kind = getattr(layer.signs, "kind", None)
+        if kind not in ("rht", "krht"):
+            raise NotImplementedError("only Hadamard / Kronecker-transformed layers are supported")
+        stages = layer.codes.shape[0] if layer.codes.dim() == 3 else 1
+        mod = cls(in_features=n, out_features=m, g=layer.g, transform_kind=kind, num_stages=stages,
+                  has_bias=bias is not None)
+        with torch.no_grad():
+            mod.codes.copy_(layer.codes)
+            mod.scale.copy_(torch.as_tensor(layer.scale, dtype=torch.float32))
+            if bias is not None:
+                mod.bias.copy_(bias.float())
+            mod.su.copy_(layer.signs.su)
+            mod.sv.copy_(layer.signs.sv)
+        return mod
+
+    def _quantized_layer(self) -> QuantizedLayer:
+        cls = IncoherenceSigns if self.transform_kind == "rht" else KronSigns
+        codes = self.codes.to(torch.int64) & 0xFFFF
+        return QuantizedLayer(codes=codes, signs=cls(su=self.su, sv=self.sv), g=self.g,
+                              shape=(self.out_features, self.in_features), scale=self.scale.item())
+
+    def _load_from_state_dict(self, *args, **kwargs):
+        self._packed = None
+        return super()._load_from_state_dict(*args, **kwargs)
+
+    def _apply(self, fn, *args, **kwargs):
+        self._packed = None
+        return super()._apply(fn, *args, **kwargs)
+
+    def packed(self, kinds):
+        key = (self.codes.data_ptr(), self.codes.device, tuple(kinds))
+        if self._packed is None or self._packed_key != key:
+            self._packed = PackedCodes(self.codes, self.out_features, self.in_features, kinds)
+            self._packed_key = key
+            self._scale_f = float(self.scale.item())
+        return self._packed
+
+    def forward(self, x: Tensor) -> Tensor:
+        """quipsharp/checkpoint.py:141-146: y = transform_output(x2 @ W_hat^T) + bias
+        in fp32, returned in x.dtype."""
+        kinds, s0, s1 = _forward_params(self.codebook, self.num_stages)
+        packed = self.packed(kinds)
+        return forward_packed(x, packed, self.su, self.sv, s0, s1, self._scale_f, bias=self.bias,
+                              out_dtype=x.dtype)
+
+
+def replace_with_quantized_linear_(parent: nn.Module, attr: str, layer: QuantizedLayer, codebook,
+                                   bias: Tensor = None) -> QuantizedLinear:
+    """quipsharp/checkpoint.py:149-156."""
+    qlin = QuantizedLinear.from_quantized_layer(layer, bias=bias)
+    qlin.codebook = codebook
+    setattr(parent, attr, qlin)
+    return qlin

@@ -1,0 +1,138 @@
+"""BlockLDLQ (quipsharp/ldlq.py) on the GPU.
+
+``block_ldl`` factors H = L blockdiag(D) L^T with torch-ROCm linear algebra
+(rocSOLVER Cholesky, batched block inverses).  ``block_ldlq`` runs the
+reference's rounding schedule -- base pass over blocks T-1..0 with feedback
+from the already-rounded tail, then ``tune_iters`` refinement sweeps with the
+full Hessian -- keeping the residual W - Wq up to date block by block instead
+of recomputing it.  With one of the library's codebooks,
+``block_ldlq_native`` fuses each step's target formation, residual-VQ
+encode, and the Wq / residual / code updates into a single kernel launch;
+the feedback products stay on rocBLAS.
+"""
+import torch
+from torch import Tensor
+
+from . import _lib
+
+
+def block_ldl(H: Tensor, g: int, damping: float = 1e-2):
+    """g-block LDL, H = L @ blockdiag(D) @ L^T (quipsharp/ldlq.py:39-84).
+    Returns L (n, n) unit block-lower-triangular and D (T, g, g)."""
+    n = H.shape[0]
+    assert n % g == 0, f"block size {g} must evenly divide n={n}"
+    T = n // g
+    M = H.clone()
+    mean_diag = M.diagonal().mean()
+    if damping:
+        M += damping * mean_diag * torch.eye(n, device=H.device, dtype=H.dtype)
+    try:
+        L0 = torch.linalg.cholesky(M)
+    except torch.linalg.LinAlgError:
+        # fp32 Cholesky failed: retry in fp64, adding damping only if needed
+        M = M.double()
+        extra = 0.0
+        for attempt in range(4):
+            try:
+                L0 = torch.linalg.cholesky(M)
+                break
+            except torch.linalg.LinAlgError:
+                if attempt == 3:
+                    raise
+                step = float(mean_diag) * (damping if damping else 1e-2) * 10 ** attempt
+                extra += step
+                M += step * torch.eye(n, device=H.device, dtype=torch.float64)
+        print(f"block_ldl: fp32 Cholesky failed (n={n}); succeeded in fp64 with "
+              f"{extra / float(mean_diag):.0e} x mean_diag extra damping", flush=True)
+    DL = torch.diagonal(L0.reshape(T, g, T, g), dim1=0, dim2=2).permute(2, 0, 1).contiguous()
+    D = DL @ DL.transpose(-1, -2)
+    DL_inv = torch.linalg.inv(DL)
+    # block column i of L0 times DL_inv[i], all blocks in one batched product
+    Lb = L0.reshape(n, T, g).permute(1, 0, 2).contiguous()
+    L = torch.matmul(Lb, DL_inv).permute(1, 0, 2).reshape(n, n)
+    return L.to(H.dtype), D.to(H.dtype)
+
+
+def block_diag_from_stack(D: Tensor) -> Tensor:
+    """(T, g, g) -> (n, n) block-diagonal (quipsharp/ldlq.py:87-94)."""
+    return torch.block_diag(*D.unbind(0))
+
+
+def _diag_inv(H: Tensor, g: int) -> Tensor:
+    n = H.shape[0]
+    T = n // g
+    blocks = torch.diagonal(H.reshape(T, g, T, g), dim1=0, dim2=2).permute(2, 0, 1).contiguous()
+    return torch.linalg.inv(blocks)
+
+
+def block_ldlq(W: Tensor, L: Tensor, g: int, quantize_fn, H: Tensor = None, tune_iters: int = 10) -> Tensor:
+    """BlockLDLQ with a caller-supplied rounding callback
+    (quipsharp/ldlq.py:97-141).  quantize_fn(target (m, g), k) -> (m, g)."""
+    _lib.require_gpu(W, L, H, what="block_ldlq")
+    m, n = W.shape
+    assert n % g == 0
+    T = n // g
+    Wq = torch.zeros_like(W)
+    E = W.clone()  # W - Wq, updated block by block
+    for k in reversed(range(T)):
+        ck = slice(k * g, (k + 1) * g)
+        tail = slice((k + 1) * g, n)
+        target = W[:, ck] + E[:, tail] @ L[tail, ck]
+        Wq[:, ck] = quantize_fn(target, k)
+        E[:, ck] = W[:, ck] - Wq[:, ck]
+    if H is not None and tune_iters > 0:
+        dinv = _diag_inv(H, g)
+        for _ in range(tune_iters):
+            for k in reversed(range(T)):
+                ck = slice(k * g, (k + 1) * g)
+                target = Wq[:, ck] + (E @ H[:, ck]) @ dinv[k]
+                Wq[:, ck] = quantize_fn(target, k)
+                E[:, ck] = W[:, ck] - Wq[:, ck]
+    return Wq
+
+
+def block_ldlq_native(W: Tensor, L: Tensor, kinds, scales, H: Tensor = None, tune_iters: int = 10):
+    """BlockLDLQ with the library's residual-VQ codebook (g = 8), one fused
+    kernel per rounding step.  Returns (Wq (m, n), codes int64 (S, m, T))."""
+    _lib.require_gpu(W, L, H, what="block_ldlq")
+    g = 8
+    W = W.float().contiguous()
+    L = L.float().contiguous()
+    m, n = W.shape
+    assert n % g == 0
+    T = n // g
+    S = len(kinds)
+    Wq = torch.zeros_like(W)
+    E = W.clone()
+    codes = torch.zeros(S, m, T, dtype=torch.int64, device=W.device)
+    fb = torch.empty(m, g, dtype=torch.float32, device=W.device)
+    kinds_c = _lib.int_array(kinds)
+    scales_c = _lib.float_array([float(s) for s in scales])
+    lib = _lib.lib()
+    stream = _lib.stream_of(W)
+    esz = W.element_size()
+    wp, wqp, ep, cp = W.data_ptr(), Wq.data_ptr(), E.data_ptr(), codes.data_ptr()
+
+    def step(k, base_ptr, dinv_ptr):
+        _lib.check(lib.qs_ldlq_step(
+            base_ptr, n, fb.data_ptr(), dinv_ptr, wp + k * g * esz, n, wqp + k * g * esz, n,
+            ep + k * g * esz, n, m, S, kinds_c, scales_c, cp + k * 8, 8, m * T, T, stream))
+
+    for k in reversed(range(T)):
+        ck = slice(k * g, (k + 1) * g)
+        tail = slice((k + 1) * g, n)
+        if k == T - 1:
+            fb.zero_()
+        else:
+            torch.mm(E[:, tail], L[tail, ck], out=fb)
+        step(k, wp + k * g * esz, None)
+    if H is not None and tune_iters > 0:
+        H = H.float().contiguous()
+        dinv = _diag_inv(H, g).contiguous()
+        dp = dinv.data_ptr()
+        for _ in range(tune_iters):
+            for k in reversed(range(T)):
+                ck = slice(k * g, (k + 1) * g)
+                torch.mm(E, H[:, ck], out=fb)
+                step(k, wqp + k * g * esz, dp + k * g * g * 4)
+    return Wq, codes

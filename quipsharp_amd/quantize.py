@@ -1,0 +1,221 @@
+"""QuIP# without fine-tuning (Algorithm 1) and the quantized-linear forward
+(Algorithm 2) on gfx950 -- quipsharp/quantize.py.
+
+``linear_forward`` never materializes the dense weight: the codes are packed
+once into the kernel layout and decoded on the fly inside the matrix-core
+matvec, between the two randomized-Hadamard transforms.
+"""
+from dataclasses import dataclass
+
+import torch
+from torch import Tensor
+
+from . import _lib
+from .codebooks.e8p import _decode
+from .hadamard import hartley_matrix, kron_factor
+from .incoherence import incoherence_process_auto
+from .ldlq import block_ldl, block_ldlq, block_ldlq_native
+from .rvq import RVQStage, rvq_dequantize, rvq_quantize
+
+
+@dataclass
+class QuantizedLayer:
+    """quipsharp/quantize.py:22-28."""
+    codes: Tensor  # (m, T) or (S, m, T), per-block codes
+    signs: object  # IncoherenceSigns / KronSigns
+    g: int
+    shape: tuple
+    scale: float
+
+
+class RVQCodebookAdapter:
+    """Residual-VQ stages behind the single-codebook protocol (quipsharp/quantize.py:31-45)."""
+
+    def __init__(self, stages):
+        self.stages = stages
+
+    def native_stages(self):
+        """(kinds, scales) when every stage is one of the library's codebooks."""
+        kinds, scales = [], []
+        for st in self.stages:
+            nat = getattr(st.codebook, "native_stages", None)
+            if nat is None:
+                return None
+            k, s = nat()
+            if len(k) != 1 or s[0] != 1.0:
+                return None
+            kinds.append(k[0])
+            scales.append(float(st.scale))
+        return kinds, scales
+
+    def quantize(self, x: Tensor):
+        vals, codes = rvq_quantize(x, self.stages)
+        return vals, torch.stack(codes, dim=0)
+
+    def dequantize(self, code: Tensor) -> Tensor:
+        return rvq_dequantize([code[i] for i in range(code.shape[0])], self.stages)
+
+
+def _stages_of(codebook):
+    nat = getattr(codebook, "native_stages", None)
+    return nat() if nat is not None else None
+
+
+def _div(x: Tensor, d: float) -> Tensor:
+    """x / d with an IEEE fp32 divide (torch's GPU division by a Python float
+    multiplies by a rounded reciprocal instead)."""
+    xf = x.float().contiguous()
+    out = torch.empty_like(xf)
+    _lib.check(_lib.lib().qs_div_f32(_lib.ptr(xf), _lib.ptr(out), xf.numel(), float(d), _lib.stream_of(xf)))
+    return out
+
+
+def quantize_linear(W: Tensor, H: Tensor, codebook, g: int = 8, damping: float = 1e-2, generator=None,
+                    codebook_scale: float = 1.0, tune_iters: int = 10):
+    """Algorithm 1 for one linear layer (quipsharp/quantize.py:48-104) on the
+    GPU.  Returns (QuantizedLayer, W_hat_q) like the reference."""
+    _lib.require_gpu(W, H, what="quantize_linear")
+    W = W.float()
+    H = H.float()
+    H = H + damping * H.diagonal().mean() * torch.eye(H.shape[0], device=H.device, dtype=H.dtype)
+    what, hhat, signs = incoherence_process_auto(W, H, generator=generator)
+    L, _ = block_ldl(hhat, g, damping=0.0)
+    rms = what.double().pow(2).mean().float().sqrt().item()
+    layer_scale = rms * codebook_scale
+    what_scaled = _div(what, layer_scale)
+    stages = _stages_of(codebook)
+    if stages is not None and g == 8:
+        what_q_scaled, codes = block_ldlq_native(what_scaled, L, stages[0], stages[1], H=hhat,
+                                                 tune_iters=tune_iters)
+        codes_stacked = codes[0] if len(stages[0]) == 1 else codes
+    else:
+        T = what.shape[1] // g
+        blocks = [None] * T
+
+        def quantize_fn(target, k):
+            vals, code = codebook.quantize(target)
+            blocks[k] = code  # keyed by block index; blocks are revisited
+            return vals
+
+        what_q_scaled = block_ldlq(what_scaled, L, g, quantize_fn, H=hhat, tune_iters=tune_iters)
+        codes_stacked = torch.stack(blocks, dim=-1)
+    what_q = what_q_scaled * layer_scale
+    layer = QuantizedLayer(codes=codes_stacked, signs=signs, g=g, shape=tuple(W.shape), scale=layer_scale)
+    return layer, what_q
+
+
+def dequantize_linear(layer: QuantizedLayer, codebook) -> Tensor:
+    """Dense W_hat from the codes (quipsharp/quantize.py:107-113), bit-exact."""
+    m, n = layer.shape
+    stages = _stages_of(codebook)
+    if stages is not None:
+        codes = layer.codes if layer.codes.dim() == 3 else layer.codes.unsqueeze(0)
+        out = _decode(codes, stages[0], stages[1], out_scale=layer.scale)
+        return out.reshape(m, n)
+    T = n // layer.g
+    blocks = [codebook.dequantize(layer.codes[..., k]) for k in range(T)]
+    return torch.cat(blocks, dim=-1) * layer.scale
+
+
+# ---------------------------------------------------------------------------
+# forward
+# ---------------------------------------------------------------------------
+class PackedCodes:
+    """Codes of one layer in the layout the forward kernels stream."""
+
+    def __init__(self, codes: Tensor, m: int, n: int, kinds):
+        _lib.require_gpu(codes, what="pack_codes")
+        S = codes.shape[0] if codes.dim() == 3 else 1
+        codes = codes if codes.dim() == 3 else codes.unsqueeze(0)
+        if S > 2:
+            raise NotImplementedError("the forward kernels take one or two residual stages")
+        if kinds[0] != _lib.QS_STAGE_E8P:
+            raise NotImplementedError("the first stage must be E8P")
+        tiled = m % 16 == 0 and n % 256 == 0 and (S == 1 or kinds[1] == _lib.QS_STAGE_E8_1BIT)
+        self.layout = _lib.QS_LAYOUT_TILED if tiled else _lib.QS_LAYOUT_ROWMAJOR
+        self.m, self.n = m, n
+        self.kind1 = kinds[1] if S == 2 else _lib.QS_STAGE_E8_1BIT
+        T = n // 8
+        lib = _lib.lib()
+        stream = _lib.stream_of(codes)
+        self.codes0 = torch.empty(m * T, dtype=torch.int16, device=codes.device)
+        self.codes1 = None
+        c0 = codes[0].contiguous()
+        _lib.check(lib.qs_pack_codes(_lib.ptr(c0), c0.element_size(), m, n, _lib.QS_STAGE_E8P, self.layout,
+                                     _lib.ptr(self.codes0), stream))
+        if S == 2:
+            c1 = codes[1].contiguous()
+            if self.kind1 == _lib.QS_STAGE_E8P:
+                self.codes1 = torch.empty(m * T, dtype=torch.int16, device=codes.device)
+            else:
+                self.codes1 = torch.empty(m * T, dtype=torch.uint8, device=codes.device)
+            _lib.check(lib.qs_pack_codes(_lib.ptr(c1), c1.element_size(), m, n, self.kind1, self.layout,
+                                         _lib.ptr(self.codes1), stream))
+
+    def nbytes(self):
+        return self.codes0.numel() * 2 + (0 if self.codes1 is None else self.codes1.numel() *
+                                          self.codes1.element_size())
+
+
+def forward_packed(x: Tensor, packed: PackedCodes, su: Tensor, sv: Tensor, s0: float, s1: float,
+                   layer_scale: float, bias: Tensor = None, out_dtype=None, workspace: Tensor = None) -> Tensor:
+    """y = su (.) T_m(layer_scale * W_hat @ T_n(sv (.) x)) + bias for x (..., n),
+    computed in the library (fp32 accumulation; output in ``out_dtype``,
+    default x.dtype)."""
+    _lib.require_gpu(x, su, sv, bias, what="linear forward")
+    m, n = packed.m, packed.n
+    if x.shape[-1] != n:
+        raise ValueError(f"expected last dim {n}, got {x.shape[-1]}")
+    out_dtype = out_dtype or x.dtype
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, n)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    B = x2.shape[0]
+    y = torch.empty(B, m, dtype=out_dtype, device=x.device)
+    if B == 0:
+        return y.reshape(*lead, m)
+    fm, fn = kron_factor(m), kron_factor(n)
+    if fm is None or fn is None:
+        raise ValueError(f"dims ({m}, {n}) need the form p * 2^k with odd p <= {_lib.QS_MAX_KRON}")
+    Km = hartley_matrix(fm[0], x.device) if fm[0] > 1 else None
+    Kn = hartley_matrix(fn[0], x.device) if fn[0] > 1 else None
+    lib = _lib.lib()
+    need = lib.qs_linear_workspace_bytes(m, n, B, packed.layout)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=x.device)
+    _lib.check(lib.qs_linear_forward(
+        _lib.ptr(x2), _lib.dtype_code(x2.dtype), x2.stride(0), B, n, m, _lib.ptr(packed.codes0),
+        _lib.ptr(packed.codes1), packed.kind1, packed.layout, _lib.ptr(sv), _lib.ptr(su), fn[0], _lib.ptr(Kn),
+        fm[0], _lib.ptr(Km), float(s0), float(s1), float(layer_scale), _lib.ptr(bias), _lib.ptr(y),
+        _lib.dtype_code(out_dtype), m, _lib.ptr(workspace), workspace.numel(), _lib.stream_of(x2)))
+    return y.reshape(*lead, m)
+
+
+def _forward_params(codebook, num_stages):
+    stages = _stages_of(codebook)
+    if stages is None:
+        raise NotImplementedError("linear_forward decodes the library's codebooks (E8P, E8 1-bit residual VQ)")
+    kinds, scales = stages
+    if len(kinds) != num_stages:
+        raise ValueError(f"codebook has {len(kinds)} stages, codes have {num_stages}")
+    s0 = scales[0]
+    s1 = scales[1] if len(scales) > 1 else 0.0
+    return kinds, s0, s1
+
+
+def linear_forward(x: Tensor, layer: QuantizedLayer, codebook) -> Tensor:
+    """Algorithm 2 (quipsharp/quantize.py:116-124) with the fused kernels; x
+    (..., n) -> (..., m) in x.dtype.  The packed codes are cached on ``layer``."""
+    m, n = layer.shape
+    S = layer.codes.shape[0] if layer.codes.dim() == 3 else 1
+    kinds, s0, s1 = _forward_params(codebook, S)
+    packed = getattr(layer, "_packed", None)
+    if packed is None or packed[0] is not layer.codes:
+        packed = (layer.codes, PackedCodes(layer.codes, m, n, kinds))
+        layer._packed = packed
+    signs = layer.signs
+    if not hasattr(signs, "su"):
+        raise NotImplementedError("linear_forward supports Hadamard / Kronecker sign transforms")
+    return forward_packed(x, packed[1], signs.su.float().contiguous(), signs.sv.float().contiguous(), s0, s1,
+                          layer.scale)

@@ -1,0 +1,81 @@
+"""The C ABI library: loads without a GPU, exports every entry point declared
+in include/quipsharp_hip.h, and rejects bad arguments on the host (nothing is
+launched by these calls)."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from conftest import ROOT
+from oracle import cref
+
+
+@pytest.fixture(scope="module")
+def L():
+    from quipsharp_amd import _lib
+    return _lib.lib()
+
+
+def declared():
+    text = open(os.path.join(ROOT, "include", "quipsharp_hip.h")).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(qs_[a-z0-9_]+)\s*\(", text, re.M)))
+
+
+def test_header_declares_entry_points():
+    names = declared()
+    assert "qs_linear_forward" in names and "qs_rvq_encode" in names and len(names) >= 12
+
+
+def test_library_exports_every_declared_symbol(L):
+    lib = ctypes.CDLL(os.path.join(ROOT, "quipsharp_amd", "libquipsharp_hip.so"))
+    for name in declared():
+        assert hasattr(lib, name), name
+
+
+def test_python_binding_covers_the_header():
+    from quipsharp_amd import _lib
+    assert sorted(_lib.EXPORTED) == declared()
+
+
+def test_abi_version(L):
+    assert L.qs_abi_version() == 1
+
+
+def test_tables_equal_oracle(L):
+    a = np.zeros((256, 8), np.float32)
+    b = np.zeros((256, 8), np.float32)
+    assert L.qs_e8p_abs_table(a.ctypes.data) == 0
+    assert L.qs_e81_table(b.ctypes.data) == 0
+    assert np.array_equal(a, cref.e8p_abs_table())
+    assert np.array_equal(b, cref.e81_table())
+
+
+def test_argument_errors_are_reported(L):
+    from quipsharp_amd import _lib
+    rc = L.qs_rvq_encode(ctypes.c_void_p(16), 8, 4, 0, _lib.int_array([0]), _lib.float_array([1.0]), 1.0, 1.0, None, 8,
+                         None, 8, 4, 1, None)
+    assert rc == 1 and b"nstages" in L.qs_last_error()
+    rc = L.qs_rht_f32(ctypes.c_void_p(16), ctypes.c_void_p(16), 1, 12, 1, None, None, None, 1, None, None)
+    assert rc == 1 and b"power of two" in L.qs_last_error()
+    rc = L.qs_rht_f32(ctypes.c_void_p(16), ctypes.c_void_p(16), 1, 11008, 1, None, None, None, 43, None, None)
+    assert rc == 1 and b"kron_mat" in L.qs_last_error()
+    rc = L.qs_pack_codes(ctypes.c_void_p(16), 8, 20, 512, 0, 1, ctypes.c_void_p(16), None)
+    assert rc == 1 and b"tiled" in L.qs_last_error()
+    rc = L.qs_div_f32(ctypes.c_void_p(16), ctypes.c_void_p(16), 4, 0.0, None)
+    assert rc == 1 and b"divisor" in L.qs_last_error()
+
+
+def test_zero_sized_calls_are_noops(L):
+    from quipsharp_amd import _lib
+    assert L.qs_rvq_encode(None, 8, 0, 1, _lib.int_array([0]), _lib.float_array([1.0]), 1.0, 1.0, None, 8,
+                           None, 8, 0, 1, None) == 0
+    assert L.qs_div_f32(None, None, 0, 2.0, None) == 0
+
+
+def test_workspace_size(L):
+    from quipsharp_amd import _lib
+    a = L.qs_linear_workspace_bytes(4096, 4096, 1, _lib.QS_LAYOUT_TILED)
+    b = L.qs_linear_workspace_bytes(4096, 11008, 16, _lib.QS_LAYOUT_TILED)
+    assert a >= 4096 * 2 + 4096 * 4 and b > a and a % 256 == 0

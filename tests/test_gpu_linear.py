@@ -1,0 +1,172 @@
+"""GPU parity: the fused quantized-linear forward (decode + transforms +
+matvec) against the reference's golden outputs and a dense fp64 oracle at the
+Llama-2-7B layer shapes.  Tolerance: relative 1e-3 (norm-wise) with fp32
+accumulation; dequantization is bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import golden
+from oracle import cref
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-3
+
+
+def fwht64(x, axis=-1):
+    """fp64 orthonormal Walsh-Hadamard along axis (numpy)."""
+    x = np.moveaxis(np.array(x, dtype=np.float64), axis, -1)
+    n = x.shape[-1]
+    shp = x.shape
+    y = x.reshape(-1, n)
+    h = 1
+    while h < n:
+        y = y.reshape(-1, n // (2 * h), 2, h)
+        y = np.stack((y[:, :, 0] + y[:, :, 1], y[:, :, 0] - y[:, :, 1]), axis=2)
+        h *= 2
+    return np.moveaxis(y.reshape(shp) / np.sqrt(n), -1, axis)
+
+
+def hartley(p):
+    a = np.arange(p)
+    ang = 2 * np.pi * ((a[:, None] * a[None, :]) % p) / p
+    return (np.cos(ang) + np.sin(ang)) / np.sqrt(p)
+
+
+def T64(x):
+    """fp64 transform along the last dim: K_p (x) H_L (H_n when p == 1)."""
+    n = x.shape[-1]
+    L = n & -n
+    p = n // L
+    y = fwht64(x.reshape(x.shape[:-1] + (p, L)), -1)
+    if p > 1:
+        y = np.einsum("ab,...bl->...al", hartley(p), y)
+    return y.reshape(x.shape)
+
+
+def dense_forward(x, codes0, codes1, s0, s1, su, sv, scale, bias=None):
+    m, T = codes0.shape
+    W = cref.e8p_decode(codes0).reshape(m, T * 8).astype(np.float64) * s0
+    if codes1 is not None:
+        W += cref.e81_table()[codes1].reshape(m, T * 8).astype(np.float64) * s1
+    x2 = T64(x.astype(np.float64) * sv)
+    y = T64(x2 @ W.T * scale) * su
+    return y if bias is None else y + bias
+
+
+def rel_err(got, want):
+    return np.linalg.norm(got - want) / np.linalg.norm(want)
+
+
+def run(dev, x, codes0, codes1, s0, s1, su, sv, scale, bias=None, out_dtype=torch.float32):
+    from quipsharp_amd.quantize import PackedCodes, forward_packed
+    m, T = codes0.shape
+    kinds = [0] if codes1 is None else [0, 1]
+    c = torch.from_numpy(codes0.astype(np.int64)).to(dev)
+    if codes1 is not None:
+        c = torch.stack([c, torch.from_numpy(codes1.astype(np.int64)).to(dev)])
+    packed = PackedCodes(c, m, T * 8, kinds)
+    t = lambda a: None if a is None else torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dev)
+    xt = x if isinstance(x, torch.Tensor) else t(x)
+    y = forward_packed(xt, packed, t(su), t(sv), s0, s1, scale, bias=t(bias), out_dtype=out_dtype)
+    return y, packed
+
+
+def test_linear_forward_golden(dev):
+    """linear_forward on the reference's random-code layers (golden y)."""
+    from quipsharp_amd.codebooks.e8p import E8PCodebook
+    from quipsharp_amd.codebooks.e8_1bit import E8OneBitCodebook
+    from quipsharp_amd.incoherence import IncoherenceSigns
+    from quipsharp_amd.quantize import QuantizedLayer, RVQCodebookAdapter, dequantize_linear, linear_forward
+    from quipsharp_amd.rvq import RVQStage
+    lf = golden("linear.npz")
+    cb = E8PCodebook(dev)
+    books = {"e8p": cb, "rvq3": RVQCodebookAdapter([RVQStage(cb, 1.03), RVQStage(E8OneBitCodebook(dev), 0.47)])}
+    for name, book in books.items():
+        codes = torch.from_numpy(lf[name + "_codes"].astype(np.int64)).to(dev)
+        m, n = lf[name + "_deq"].shape
+        signs = IncoherenceSigns(su=torch.from_numpy(lf[name + "_su"]).to(dev),
+                                 sv=torch.from_numpy(lf[name + "_sv"]).to(dev))
+        layer = QuantizedLayer(codes=codes, signs=signs, g=8, shape=(m, n), scale=float(lf[name + "_scale"]))
+        deq = dequantize_linear(layer, book).cpu().numpy()
+        assert np.array_equal(deq, lf[name + "_deq"]), name
+        y = linear_forward(torch.from_numpy(lf[name + "_x"]).to(dev), layer, book).cpu().numpy()
+        err = rel_err(y, lf[name + "_y"])
+        print(f"{name}: rel err vs reference {err:.2e}", flush=True)
+        assert err < REL_TOL, (name, err)
+
+
+@pytest.mark.parametrize("m,n", [(4096, 4096), (11008, 4096), (4096, 11008), (1024, 4096), (3584, 3584)])
+@pytest.mark.parametrize("B", [1, 4, 16])
+def test_forward_vs_dense_fp64(dev, m, n, B):
+    print(f"case: forward m={m} n={n} B={B}", flush=True)
+    rng = np.random.default_rng(m * 7 + n + B)
+    codes = rng.integers(0, 65536, (m, n // 8))
+    su = rng.choice([-1.0, 1.0], m)
+    sv = rng.choice([-1.0, 1.0], n)
+    x = rng.standard_normal((B, n)).astype(np.float32)
+    scale = float(np.float32(0.0135))
+    y, packed = run(dev, x, codes, None, 1.0, 0.0, su, sv, scale)
+    assert packed.layout == 1
+    want = dense_forward(x, codes, None, 1.0, 0.0, su, sv, scale)
+    err = rel_err(y.cpu().numpy(), want)
+    print(f"  rel err {err:.2e}", flush=True)
+    assert err < REL_TOL
+
+
+@pytest.mark.parametrize("B", [1, 17])
+def test_forward_rvq3_vs_dense(dev, B):
+    m, n = 4096, 4096
+    rng = np.random.default_rng(B)
+    c0 = rng.integers(0, 65536, (m, n // 8))
+    c1 = rng.integers(0, 256, (m, n // 8))
+    su, sv = rng.choice([-1.0, 1.0], m), rng.choice([-1.0, 1.0], n)
+    x = rng.standard_normal((B, n)).astype(np.float32)
+    y, packed = run(dev, x, c0, c1, 0.95, 0.5, su, sv, 0.01)
+    assert packed.layout == 1
+    want = dense_forward(x, c0, c1, 0.95, 0.5, su, sv, 0.01)
+    assert rel_err(y.cpu().numpy(), want) < REL_TOL
+
+
+@pytest.mark.parametrize("m,n", [(40, 96), (48, 144), (200, 64)])
+def test_forward_rowmajor_fallback(dev, m, n):
+    rng = np.random.default_rng(m + n)
+    codes = rng.integers(0, 65536, (m, n // 8))
+    su, sv = rng.choice([-1.0, 1.0], m), rng.choice([-1.0, 1.0], n)
+    x = rng.standard_normal((3, n)).astype(np.float32)
+    bias = rng.standard_normal(m)
+    y, packed = run(dev, x, codes, None, 1.0, 0.0, su, sv, 0.02, bias=bias)
+    assert packed.layout == 0
+    want = dense_forward(x, codes, None, 1.0, 0.0, su, sv, 0.02, bias)
+    assert rel_err(y.cpu().numpy(), want) < 1e-5
+
+
+def test_forward_bf16_io_and_bias(dev):
+    m, n = 4096, 4096
+    rng = np.random.default_rng(3)
+    codes = rng.integers(0, 65536, (m, n // 8))
+    su, sv = rng.choice([-1.0, 1.0], m), rng.choice([-1.0, 1.0], n)
+    bias = rng.standard_normal(m).astype(np.float32) * 0.1
+    xb = torch.from_numpy(rng.standard_normal((2, n)).astype(np.float32)).to(dev).bfloat16()
+    y, _ = run(dev, xb, codes, None, 1.0, 0.0, su, sv, 0.0135, bias=bias, out_dtype=torch.bfloat16)
+    assert y.dtype == torch.bfloat16
+    want = dense_forward(xb.float().cpu().numpy(), codes, None, 1.0, 0.0, su, sv, 0.0135, bias)
+    got = y.float().cpu().numpy()
+    # bf16 output: within rounding of the fp32 result plus the 1e-3 path tolerance
+    assert np.all(np.abs(got - want) <= 2 ** -8 * np.abs(want) + 2e-3 * np.abs(want).max())
+
+
+def test_forward_large_activation_range(dev):
+    """Activations far outside fp16 range are handled by the per-row
+    power-of-two scaling of the input transform."""
+    m, n = 1024, 4096
+    rng = np.random.default_rng(9)
+    codes = rng.integers(0, 65536, (m, n // 8))
+    su, sv = rng.choice([-1.0, 1.0], m), rng.choice([-1.0, 1.0], n)
+    x = (rng.standard_normal((2, n)) * np.array([[3e5], [1e-6]])).astype(np.float32)
+    y, _ = run(dev, x, codes, None, 1.0, 0.0, su, sv, 0.01)
+    want = dense_forward(x, codes, None, 1.0, 0.0, su, sv, 0.01)
+    g = y.cpu().numpy()
+    for b in range(2):
+        assert rel_err(g[b], want[b]) < REL_TOL
