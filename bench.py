@@ -1,0 +1,366 @@
+#!/usr/bin/env python3
+"""E8P decode-matvec benchmark on one MI355X.
+
+Workload: the Llama-2-7B quantized-linear stack -- per decoder layer q, k, v,
+o (4096x4096), gate, up (11008x4096) and down (4096x11008) -- 32 decoder
+layers (1.62 GB of E8P codes, about 6x the Infinity Cache), bf16
+activations, batch 1 (decode; batch 16 reported alongside).  E8P 2-bit codes
+are random uint16 from a seeded generator with an fp16 per-layer scale and
+seeded RHT signs; the 11008-wide dims use the Kronecker transform (43 x 256).
+A step is one pass through the 224 linears in dependency order (q/k/v read
+the layer input, o reads q, gate/up read o, down reads gate, the next layer
+reads down), replayed from a HIP graph.
+
+Also reported: quantize s/layer for a 4096x4096 layer (E8P 2-bit
+BlockLDLQ with 10 refinement sweeps) and the reference's CPU path timed on
+this host (torch-CPU restatement, oracle/torch_path.py).
+
+Prints one JSON line.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+LLAMA2_7B = [("q", 4096, 4096), ("k", 4096, 4096), ("v", 4096, 4096), ("o", 4096, 4096),
+             ("gate", 11008, 4096), ("up", 11008, 4096), ("down", 4096, 11008)]
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--layers", type=int, default=32)
+    p.add_argument("--skip-quantize", action="store_true")
+    p.add_argument("--skip-cpu", action="store_true")
+    p.add_argument("--skip-batch16", action="store_true")
+    return p.parse_args()
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def linear_bytes(m, n, B):
+    """Algorithmic HBM bytes of one quantized-linear call: 2-byte codes per 8
+    weights, bf16 activations in and out, 1-bit signs, fp16 scale."""
+    return m * n // 8 * 2 + 2 * B * (n + m) + math.ceil((m + n) / 8) + 2
+
+
+def mv_bytes(m, n, B):
+    """Algorithmic bytes of one decode-matvec launch: codes, fp16 activations
+    in, fp32 partial outputs."""
+    return m * n // 8 * 2 + 2 * B * n + 4 * B * m
+
+
+class Stack:
+    """The synthetic 32-layer Llama-2-7B linear stack on the GPU."""
+
+    def __init__(self, layers, dev):
+        import torch
+        from quipsharp_amd.quantize import PackedCodes
+        from quipsharp_amd.hadamard import rademacher
+        self.dev = dev
+        gen = torch.Generator(device=dev).manual_seed(0)
+        cpu_gen = torch.Generator().manual_seed(0)
+        scale = float(torch.tensor(0.0135, dtype=torch.float16).float())
+        self.layers = []
+        for _ in range(layers):
+            lin = {}
+            for name, m, n in LLAMA2_7B:
+                codes = torch.randint(0, 65536, (m, n // 8), generator=gen, device=dev, dtype=torch.int32)
+                packed = PackedCodes(codes, m, n, [0])
+                del codes
+                su = rademacher(m, device=dev, generator=cpu_gen)
+                sv = rademacher(n, device=dev, generator=cpu_gen)
+                lin[name] = (packed, su, sv, scale)
+            self.layers.append(lin)
+        torch.cuda.synchronize()
+
+    def code_bytes(self):
+        return sum(p[0].nbytes() for lin in self.layers for p in lin.values())
+
+
+class Runner:
+    """Issues the step's 224 linear calls through the C ABI with preallocated
+    buffers, so the step can be captured in a HIP graph."""
+
+    def __init__(self, stack, B):
+        import torch
+        from quipsharp_amd import _lib
+        from quipsharp_amd.hadamard import hartley_matrix
+        self.stack, self.B = stack, B
+        dev = stack.dev
+        self.lib = _lib.lib()
+        self._lib = _lib
+        g = torch.Generator(device=dev).manual_seed(1)
+        self.x = torch.randn(B, 4096, generator=g, device=dev).bfloat16()
+        self.buf = {k: torch.empty(B, m, dtype=torch.bfloat16, device=dev) for k, m, _ in LLAMA2_7B}
+        ws = max(self.lib.qs_linear_workspace_bytes(m, n, B, _lib.QS_LAYOUT_TILED) for _, m, n in LLAMA2_7B)
+        self.ws = torch.empty(ws, dtype=torch.uint8, device=dev)
+        self.K43 = hartley_matrix(43, dev)
+        self.src = {"q": None, "k": None, "v": None, "o": "q", "gate": "o", "up": "o", "down": "gate"}
+
+    def _call(self, x, lin, out, m, n, stream, events):
+        L, _lib = self.lib, self._lib
+        packed, su, sv, scale = lin
+        kn = 43 if n == 11008 else 1
+        km = 43 if m == 11008 else 1
+        rc = L.qs_linear_forward(
+            x.data_ptr(), _lib.QS_DTYPE_BF16, n, self.B, n, m, packed.codes0.data_ptr(), None, 0, packed.layout,
+            sv.data_ptr(), su.data_ptr(), kn, self.K43.data_ptr() if kn > 1 else None, km,
+            self.K43.data_ptr() if km > 1 else None, 1.0, 0.0, scale, None, out.data_ptr(), _lib.QS_DTYPE_BF16, m,
+            self.ws.data_ptr(), self.ws.numel(), events[0] if events else None, events[1] if events else None,
+            stream)
+        if rc:
+            _lib.check(rc)
+
+    def step(self, events=None):
+        import torch
+        stream = torch.cuda.current_stream(self.stack.dev).cuda_stream
+        x = self.x
+        ei = 0
+        for lin in self.stack.layers:
+            for name, m, n in LLAMA2_7B:
+                src = x if self.src[name] is None else self.buf[self.src[name]]
+                ev = None
+                if events is not None:
+                    ev = events[ei]
+                    ei += 1
+                self._call(src, lin[name], self.buf[name], m, n, stream, ev)
+            x = self.buf["down"]
+        return self.buf["down"]
+
+    def launches_per_step(self):
+        return len(self.stack.layers) * len(LLAMA2_7B)
+
+    def bytes_per_step(self):
+        return len(self.stack.layers) * sum(linear_bytes(m, n, self.B) for _, m, n in LLAMA2_7B)
+
+    def mv_bytes_per_step(self):
+        return len(self.stack.layers) * sum(mv_bytes(m, n, self.B) for _, m, n in LLAMA2_7B)
+
+
+def time_graph(runner, steps, warmup):
+    import torch
+    dev = runner.stack.dev
+    # eager reference output for the graph check
+    ref = runner.step().clone()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream(device=dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        runner.step()
+    torch.cuda.current_stream(dev).wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        runner.step()
+    for _ in range(max(warmup, 1)):
+        graph.replay()
+    torch.cuda.synchronize()
+    out = runner.buf["down"]
+    if not torch.equal(out, ref):
+        raise RuntimeError("graph replay differs from the eager step")
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(steps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    if not torch.equal(runner.buf["down"], ref):
+        raise RuntimeError("graph replays are not reproducible")
+    return e0.elapsed_time(e1) / steps  # ms
+
+
+def time_mv_kernels(runner, passes=3):
+    """Average duration of the decode-matvec launches, from HIP events recorded
+    on the launch stream around each launch (the stream is kept busy so the
+    launches run back to back)."""
+    import torch
+    from quipsharp_amd import _lib
+    n = runner.launches_per_step()
+    evs = []
+    for _ in range(n):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        b.record()
+        evs.append((a, b))
+    torch.cuda.synchronize()
+    handles = [(a.cuda_event, b.cuda_event) for a, b in evs]
+    total_ms = 0.0
+    for _ in range(passes):
+        _lib.check(_lib.lib().qs_busy_wait(30_000_000, _lib._vp(torch.cuda.current_stream().cuda_stream)))
+        runner.step(events=handles)
+        torch.cuda.synchronize()
+        total_ms += sum(a.elapsed_time(b) for a, b in evs)
+    return total_ms / passes / n  # ms per launch
+
+
+def gpu_quantize(dev):
+    import torch
+    from quipsharp_amd.checkpoint import build_codebook
+    from quipsharp_amd.quantize import quantize_linear, linear_forward
+    g = torch.Generator().manual_seed(0)
+    W = torch.randn(4096, 4096, generator=g) * 0.02
+    X = torch.randn(2048, 4096, generator=g)
+    x = torch.randn(4096, generator=g)
+    Wd, Xd = W.to(dev), X.to(dev)
+    H = Xd.T @ Xd / 2048
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    cb, s = build_codebook("2bit", dev, 0)
+    torch.cuda.synchronize()
+    t_cb = time.perf_counter() - t0
+    torch.manual_seed(0)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    layer, what_q = quantize_linear(Wd, H, cb, g=8, damping=1e-2, codebook_scale=s, tune_iters=10)
+    torch.cuda.synchronize()
+    t_q = time.perf_counter() - t0
+    y = linear_forward(x.to(dev), layer, cb)
+    W_q = layer.signs.reconstruct_weight(what_q)
+    E = W_q - Wd
+    proxy = torch.trace(E.double() @ H.double() @ E.T.double()).item() / torch.trace(
+        Wd.double() @ H.double() @ Wd.T.double()).item()
+    return {"quantize_s_per_layer": round(t_q, 4), "codebook_fit_s": round(t_cb, 4), "codebook_scale": s,
+            "relative_proxy_loss": round(proxy, 5), "forward_ok": bool(torch.isfinite(y).all().item())}
+
+
+def cpu_baseline(dev_layers_sample=1):
+    """The reference's CPU path (torch-CPU restatement) on this host:
+    forward for one decoder layer's 7 linears at batch 1 (dense dequantize
+    loop + matmul; RHT for power-of-two dims, RFFT for 11008), and a timed
+    sample of the 4096x4096 quantize extrapolated to the full layer."""
+    import torch
+    from oracle import torch_path
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    # forward, one decoder layer
+    t_fwd = 0.0
+    nbytes = 0
+    for name, m, n in LLAMA2_7B:
+        codes = torch.randint(0, 65536, (m, n // 8), generator=g)
+        x = torch.randn(1, n, generator=g)
+        kw = {}
+        if m == 4096 and n == 4096:
+            kw = dict(su=torch.randint(0, 2, (m,), generator=g).float() * 2 - 1,
+                      sv=torch.randint(0, 2, (n,), generator=g).float() * 2 - 1)
+        else:
+            ph = lambda k: torch.polar(torch.ones(k), torch.rand(k, generator=g) * 2 * math.pi)
+            kw = dict(phase_u=ph(m // 2), phase_v=ph(n // 2))
+        t0 = time.perf_counter()
+        torch_path.linear_forward(x, codes, 0.0135, **kw)
+        t_fwd += time.perf_counter() - t0
+        nbytes += linear_bytes(m, n, 1)
+    # quantize sample at 4096 x 4096
+    W = torch.randn(4096, 4096, generator=torch.Generator().manual_seed(0)) * 0.02
+    X = torch.randn(2048, 4096, generator=torch.Generator().manual_seed(1))
+    H = X.T @ X / 2048
+    H = H + 1e-2 * H.diagonal().mean() * torch.eye(4096)
+    su = torch.randint(0, 2, (4096,), generator=g).float() * 2 - 1
+    sv = torch.randint(0, 2, (4096,), generator=g).float() * 2 - 1
+    t0 = time.perf_counter()
+    what = torch_path.fwht(torch_path.fwht(W * su[:, None] * sv[None, :], 0), 1)
+    hhat = torch_path.fwht(torch_path.fwht(H * sv[:, None] * sv[None, :], 0), 1)
+    L = torch_path.block_ldl(hhat, 8)
+    what = what / (what.pow(2).mean().sqrt().item() * 0.95)
+    t_setup = time.perf_counter() - t0
+    T = 512
+    base_k = [T - 1, 3 * T // 4, T // 2, T // 4, 0]
+    t0 = time.perf_counter()
+    torch_path.quantize_steps(what, L, hhat, base_k)
+    t_base = (time.perf_counter() - t0) / len(base_k)
+    tune_k = [T - 1, T // 2, 0]
+    t0 = time.perf_counter()
+    torch_path.quantize_steps(what, L, hhat, tune_k, tune=True)
+    t_tune = (time.perf_counter() - t0) / len(tune_k)
+    q_total = t_setup + T * t_base + 10 * T * t_tune
+    return {
+        "forward_GBps": nbytes / t_fwd / 1e9, "forward_s_per_decoder_layer": t_fwd,
+        "quantize_s_per_layer_extrapolated": q_total, "quantize_step_s": {"base": t_base, "tune": t_tune},
+        "threads": threads,
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build runs its kernels on a single MI355X "
+              f"(no multi-GPU path); got --gpus {args.gpus}", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    t_setup = time.perf_counter()
+    stack = Stack(args.layers, dev)
+    log(f"stack: {args.layers} layers, {stack.code_bytes() / 1e9:.2f} GB of codes, "
+        f"setup {time.perf_counter() - t_setup:.1f}s")
+    r1 = Runner(stack, 1)
+    ms = time_graph(r1, args.steps, args.warmup)
+    mv_ms = time_mv_kernels(r1)
+    bps = r1.bytes_per_step()
+    value = bps / (ms * 1e-3) / 1e9
+    mv_avg_bytes = r1.mv_bytes_per_step() / r1.launches_per_step()
+    achieved = mv_avg_bytes / (mv_ms * 1e-3) / 1e9
+    log(f"batch 1: {ms:.3f} ms/step, {value:.1f} GB/s, mv kernel avg {mv_ms * 1e3:.2f} us -> {achieved:.1f} GB/s")
+    extra = {}
+    if not args.skip_batch16:
+        r16 = Runner(stack, 16)
+        ms16 = time_graph(r16, max(args.steps // 2, 1), args.warmup)
+        mv16 = time_mv_kernels(r16, passes=1)
+        flops = 2 * 16 * args.layers * sum(m * n for _, m, n in LLAMA2_7B)
+        extra["batch16"] = {"ms_per_step": round(ms16, 4), "GBps": round(r16.bytes_per_step() / ms16 / 1e6, 1),
+                            "tok_per_s": round(16 * 1e3 / ms16, 1), "TFLOPs": round(flops / ms16 / 1e9, 2),
+                            "mv_kernel_avg_us": round(mv16 * 1e3, 3)}
+        log(f"batch 16: {ms16:.3f} ms/step")
+        del r16
+    if not args.skip_quantize:
+        extra["quantize_4096x4096_e8p_2bit"] = gpu_quantize(dev)
+        log(f"quantize: {extra['quantize_4096x4096_e8p_2bit']}")
+    cpu = None
+    if not args.skip_cpu:
+        log("timing the reference CPU path ...")
+        c = cpu_baseline()
+        cpu = {"value": round(c["forward_GBps"], 3), "unit": "GB/s", "cores": c["threads"], "kind": "port",
+               "sample": "reference forward (dense dequantize loop + fp32 matmul, RHT / RFFT transforms) of one "
+                         "Llama-2-7B decoder layer's 7 linears at batch 1, torch-CPU restatement; quantize "
+                         "4096x4096 E8P 2-bit extrapolated from 5 base-pass and 3 refinement steps",
+               "forward_s_per_decoder_layer": round(c["forward_s_per_decoder_layer"], 3),
+               "quantize_s_per_layer": round(c["quantize_s_per_layer_extrapolated"], 1)}
+        if "quantize_4096x4096_e8p_2bit" in extra:
+            extra["quantize_speedup_vs_cpu"] = round(
+                c["quantize_s_per_layer_extrapolated"] / extra["quantize_4096x4096_e8p_2bit"]["quantize_s_per_layer"], 1)
+    line = {
+        "metric": "E8P decode-matvec HBM GB/s (% peak) + batch-1 tok/s; quantize s/layer",
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "e8p-2bit codes, fp16 x fp16 -> fp32 accumulate (bf16 in/out)", "data": "synthetic",
+        "config": {"workload": "Llama-2-7B quantized-linear stack (q,k,v,o 4096x4096; gate,up 11008x4096; "
+                               "down 4096x11008) x %d decoder layers, E8P 2-bit random codes, batch 1" % args.layers,
+                   "global_batch": 1, "layers": args.layers, "linears_per_step": r1.launches_per_step(),
+                   "code_bytes": stack.code_bytes(), "parallelism": "none (1 GPU)"},
+        "tok_per_s": round(1e3 / ms, 1), "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "roofline": {"bound": "hbm", "kernel": "mv_tiled_kernel", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "avg_launch_us": round(mv_ms * 1e3, 3), "bytes_per_launch": int(mv_avg_bytes),
+                     "traffic": None},
+        "cpu_baseline": cpu,
+    }
+    line.update(extra)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -151,13 +151,20 @@ size_t qs_linear_workspace_bytes(int64_t m, int64_t n, int64_t batch, int layout
  *   sv [n], su [m] fp32 sign vectors; kron_* as in qs_rht_f32 (p = 1: FWHT)
  *   bias [m] fp32 or NULL
  * Activations enter the matrix cores as fp16 (per-row power-of-two scaled),
- * decoded weights are exact in fp16, accumulation is fp32. */
+ * decoded weights are exact in fp16, accumulation is fp32.
+ * mv_begin / mv_end: optional hipEvent_t recorded on `stream` right before
+ * the first and right after the last decode-matvec launch (NULL: none). */
 int qs_linear_forward(const void *x, int x_dtype, int64_t ldx, int64_t batch, int64_t n, int64_t m,
                       const void *codes0, const void *codes1, int kind1, int layout, const float *sv,
                       const float *su, int kron_pn, const float *kron_n, int kron_pm,
                       const float *kron_m, float s0, float s1, float layer_scale,
                       const float *bias, void *y, int y_dtype, int64_t ldy, void *workspace,
-                      size_t workspace_bytes, qs_stream_t stream);
+                      size_t workspace_bytes, void *mv_begin, void *mv_end, qs_stream_t stream);
+
+/* Measurement helper: enqueue a kernel that keeps `stream` busy for about
+ * `nanoseconds` (bounded; at most 1 s), so that work enqueued after it runs
+ * back to back on the GPU while the host is still submitting. */
+int qs_busy_wait(int64_t nanoseconds, qs_stream_t stream);
 
 #ifdef __cplusplus
 }

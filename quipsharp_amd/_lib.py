@@ -42,8 +42,9 @@ _SIGNATURES = {
     "qs_pack_codes": ([_vp, _int, _i64, _i64, _int, _int, _vp, _vp], _int),
     "qs_linear_workspace_bytes": ([_i64, _i64, _i64, _int], ctypes.c_size_t),
     "qs_linear_forward": ([_vp, _int, _i64, _i64, _i64, _i64, _vp, _vp, _int, _int, _vp, _vp, _int, _vp,
-                           _int, _vp, _f32, _f32, _f32, _vp, _vp, _int, _i64, _vp, ctypes.c_size_t, _vp],
-                          _int),
+                           _int, _vp, _f32, _f32, _f32, _vp, _vp, _int, _i64, _vp, ctypes.c_size_t, _vp, _vp,
+                           _vp], _int),
+    "qs_busy_wait": ([_i64, _vp], _int),
 }
 
 EXPORTED = tuple(_SIGNATURES)

@@ -38,10 +38,22 @@ constexpr int kMaxWaves = 16;
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+constexpr int kMaxParts = 16;  // work-groups per batch row for odd-factor transforms
+
 struct WsLayout {
   size_t x2h, sg, xtot, xmul, x2, y1p, total;
   int S, SG, W;
 };
+
+// Work-groups per batch row of the input / output transform: the odd-factor
+// stage is split over up to 16 of them (each computes L/G columns).
+int parts_for(int64_t len, int p) {
+  if (p == 1) return 1;
+  const int64_t L = len / p;
+  int64_t g = L / 8;
+  if (g > kMaxParts) g = kMaxParts;
+  return g < 1 ? 1 : (int)g;
+}
 
 WsLayout ws_layout(int64_t m, int64_t n, int64_t batch, int layout) {
   WsLayout L{};
@@ -53,7 +65,7 @@ WsLayout ws_layout(int64_t m, int64_t n, int64_t batch, int layout) {
     L.W = (L.S + L.SG - 1) / L.SG;
     L.x2h = off; off = align256(off + (size_t)B * n * 2);
     L.sg = off; off = align256(off + (size_t)B * (n / 8) * 2);
-    L.xtot = off; off = align256(off + (size_t)B * 4);
+    L.xtot = off; off = align256(off + (size_t)B * kMaxParts * 4);
     L.xmul = off; off = align256(off + (size_t)B * 4);
   } else {
     L.S = 0;
@@ -85,28 +97,17 @@ struct XinArgs {
   const void* x;
   int x_dtype;
   int64_t ldx;
-  int n, L, p;
+  int n, logL, p, G;
   const float* K;
   float scale;
   const float* sv;
   int tiled;
   _Float16* x2h;
   _Float16* sg;
-  float* xtot;
+  float* xtot;  // [B][kMaxParts] partial sums of the rounded group sums
   float* xmul;
   float* x2;
 };
-
-__device__ float block_reduce_max(float v, float* red) {
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  if (lane == 0) red[w] = v;
-  __syncthreads();
-  float r = 0.0f;
-  for (int i = 0; i < (int)(blockDim.x >> 6); ++i) r = fmaxf(r, red[i]);
-  __syncthreads();
-  return r;
-}
 
 // Deterministic block sum: per-wave tree, then waves in order.
 __device__ float block_reduce_sum(float v, float* red) {
@@ -120,43 +121,90 @@ __device__ float block_reduce_sum(float v, float* red) {
   return r;
 }
 
+// x2 = T_n(sv (.) x) for one batch row (grid = batch * G).  Tiled path: the
+// row is scaled by 2^-e, e from the row's L2 norm (an upper bound of every
+// transformed element), and written as fp16 together with the fp16 sums of
+// each 8-column group; each of the G work-groups of a row writes the groups
+// of its share of the columns b.
 __global__ __launch_bounds__(kRowThreads) void xin_kernel(XinArgs A) {
-  extern __shared__ float buf[];
+  extern __shared__ float sm[];
   __shared__ float red[kRowThreads / 64];
-  const int64_t b = blockIdx.x;
-  for (int i = threadIdx.x; i < A.n; i += blockDim.x)
-    buf[i] = load_as_float(A.x, A.x_dtype, b * A.ldx + i) * A.sv[i];
-  __syncthreads();
-  lds_rht(buf, A.n, A.L, A.p, A.K, A.scale);
+  float* buf = sm;
+  float* Ks = sm + padded_len(A.n);
+  const int64_t b = blockIdx.x / A.G;
+  const int part = blockIdx.x - (int)(b * A.G);
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  float ss = 0.0f;
+  for (int i = tid; i < A.n; i += nthr) {
+    const float v = load_as_float(A.x, A.x_dtype, b * A.ldx + i) * A.sv[i];
+    buf[pad_idx(i)] = v;
+    ss = __builtin_fmaf(v, v, ss);
+  }
+  if (A.p > 1)
+    for (int i = tid; i < A.p * A.p; i += nthr) Ks[i] = A.K[i];
+  const float norm2 = block_reduce_sum(ss, red);  // ends with a barrier
+  lds_fwht(buf, A.n, A.logL, tid, nthr);
   if (!A.tiled) {
-    for (int i = threadIdx.x; i < A.n; i += blockDim.x) A.x2[b * A.n + i] = buf[i];
+    if (A.p == 1) {
+      for (int i = tid; i < A.n; i += nthr) A.x2[b * A.n + i] = buf[pad_idx(i)] * A.scale;
+    } else {
+      for (int i = tid; i < A.n; i += nthr) buf[pad_idx(i)] = buf[pad_idx(i)] * A.scale;
+      __syncthreads();
+      const int L = 1 << A.logL, cw = L / A.G;
+      float* x2 = A.x2 + b * A.n;
+      kron_cols(buf, Ks, A.p, A.logL, part * cw, (part + 1) * cw, tid, nthr,
+                [&](int a, int c, float v) { x2[(a << A.logL) + c] = v; });
+    }
     return;
   }
-  float amax = 0.0f;
-  for (int i = threadIdx.x; i < A.n; i += blockDim.x) amax = fmaxf(amax, fabsf(buf[i]));
-  amax = block_reduce_max(amax, red);
   int e = 0;
-  if (amax > 0.0f && amax < INFINITY) {
+  if (norm2 > 0.0f && norm2 < INFINITY) {
     int ex;
-    frexpf(amax, &ex);  // amax < 2^ex
-    e = ex - 14;        // scaled maximum in [2^13, 2^14)
+    frexpf(sqrtf(norm2) * 1.0001f, &ex);  // |x2_i| <= ||x|| < 2^ex
+    e = ex - 14;
   }
-  for (int i = threadIdx.x; i < A.n; i += blockDim.x)
-    A.x2h[b * A.n + i] = (_Float16)ldexpf(buf[i], -e);
-  const int T = A.n / 8;
-  float part = 0.0f;
-  for (int g = threadIdx.x; g < T; g += blockDim.x) {
-    float s = ldexpf(buf[8 * g], -e);
+  const float mul = ldexpf(A.scale, -e);
+  const int L = 1 << A.logL;
+  const int cw = L / A.G;          // columns of this work-group (multiple of 8)
+  const int units = A.p * (cw >> 3);
+  const int T = A.n >> 3;
+  float part_sum = 0.0f;
+  for (int u = tid; u < units; u += nthr) {
+    const int a = u / (cw >> 3);
+    const int c0 = part * cw + ((u - a * (cw >> 3)) << 3);
+    float v[8];
+    if (A.p == 1) {
 #pragma unroll
-    for (int i = 1; i < 8; ++i) s = s + ldexpf(buf[8 * g + i], -e);
-    const _Float16 h = (_Float16)s;
-    A.sg[b * T + g] = h;
-    part += (float)h;
+      for (int k = 0; k < 8; ++k) v[k] = buf[pad_idx(c0 + k)] * mul;
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = 0.0f;
+      const float* Kr = Ks + a * A.p;
+      for (int c = 0; c < A.p; ++c) {
+        const float kv = Kr[c];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = __builtin_fmaf(kv, buf[pad_idx((c << A.logL) + c0 + k)], v[k]);
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = v[k] * mul;
+    }
+    const int i0 = (a << A.logL) + c0;
+    _Float16 h[8];
+    float gsum = v[0];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      h[k] = (_Float16)v[k];
+      if (k) gsum = gsum + v[k];
+    }
+    *reinterpret_cast<uint4*>(A.x2h + b * A.n + i0) = __builtin_bit_cast(uint4, h);
+    const _Float16 hs = (_Float16)gsum;
+    A.sg[b * T + (i0 >> 3)] = hs;
+    part_sum += (float)hs;
   }
-  const float tot = block_reduce_sum(part, red);
-  if (threadIdx.x == 0) {
-    A.xtot[b] = tot;
-    A.xmul[b] = ldexpf(1.0f, e);
+  const float tot = block_reduce_sum(part_sum, red);
+  if (tid == 0) {
+    A.xtot[b * kMaxParts + part] = tot;
+    if (part == 0) A.xmul[b] = ldexpf(1.0f, e);
   }
 }
 
@@ -178,49 +226,70 @@ __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
   return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
 }
 
+constexpr int kPrefetch = 4;  // code tiles loaded ahead per wave
+
 template <bool HAS2>
 __global__ __launch_bounds__(kMaxWaves * 64) void mv_tiled_kernel(MvArgs A) {
   __shared__ uint2 lut_hi[4096];
   __shared__ uint2 lut_lo[4096];
   __shared__ uint4 lut1[HAS2 ? 256 : 1];
+  __shared__ uint4 tab16[256];
   __shared__ float red[kMaxWaves][16][kMaxTileBatch];
 
-  const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  const int lane = tid & 63;
+  const int w = tid >> 6;
   const int q = lane >> 4, r16 = lane & 15;
   const int RB = A.m >> 4;
   const int nitems = RB * A.SG;
   const int T = A.n >> 3;
 
-  // Signed half-codeword tables.  hi[H*256 + a]: coordinates 0..3 of row a,
-  // H = (f1 f2 f3 q); lo[q*2048 + a*8 + f]: coordinates 4..7, f = (f4 f5 f6),
-  // coordinate 7 flipped by q^f4^f5^f6.
-  for (int e = threadIdx.x; e < 4096; e += blockDim.x) {
-    {
-      const int H = e >> 8, a = e & 255;
-      const int f1 = (H >> 3) & 1, f2 = (H >> 2) & 1, f3 = (H >> 1) & 1, qq = H & 1;
-      const int f0 = qq ^ f1 ^ f2 ^ f3;
-      const float c0 = f0 ? -kE8P.v[a][0] : kE8P.v[a][0];
-      const float c1 = f1 ? -kE8P.v[a][1] : kE8P.v[a][1];
-      const float c2 = f2 ? -kE8P.v[a][2] : kE8P.v[a][2];
-      const float c3 = f3 ? -kE8P.v[a][3] : kE8P.v[a][3];
-      lut_hi[e] = make_uint2(pack_h2(c0, c1), pack_h2(c2, c3));
-    }
-    {
-      const int qq = e >> 11, a = (e >> 3) & 255, f = e & 7;
-      const int f4 = (f >> 2) & 1, f5 = (f >> 1) & 1, f6 = f & 1;
-      const int f7 = qq ^ f4 ^ f5 ^ f6;
-      const float c4 = f4 ? -kE8P.v[a][4] : kE8P.v[a][4];
-      const float c5 = f5 ? -kE8P.v[a][5] : kE8P.v[a][5];
-      const float c6 = f6 ? -kE8P.v[a][6] : kE8P.v[a][6];
-      const float c7 = f7 ? -kE8P.v[a][7] : kE8P.v[a][7];
-      lut_lo[e] = make_uint2(pack_h2(c4, c5), pack_h2(c6, c7));
+  // Issue this wave's first code-tile loads before building the tables.
+  uint4 pre[kPrefetch];
+  uint2 pre1[kPrefetch];
+#pragma unroll
+  for (int k = 0; k < kPrefetch; ++k) {
+    const int it = blockIdx.x + k * gridDim.x;
+    pre[k] = make_uint4(0, 0, 0, 0);
+    pre1[k] = make_uint2(0, 0);
+    if (it < nitems) {
+      const int sg = it / RB, rb = it - sg * RB;
+      const int sl = sg * A.W + w;
+      if (sl < A.S) {
+        const size_t tile = ((size_t)rb * A.S + sl) * 64 + lane;
+        pre[k] = *reinterpret_cast<const uint4*>(A.codes0 + tile * 8);
+        if (HAS2) pre1[k] = *reinterpret_cast<const uint2*>(A.codes1 + tile * 8);
+      }
     }
   }
-  if (HAS2) {
-    for (int e = threadIdx.x; e < 256; e += blockDim.x)
+
+  // fp16 copy of the abs table, then the signed half-codeword tables:
+  // hi[H*256 + a] = coordinates 0..3 of row a with flips (f0..f3) from
+  // H = (f1 f2 f3 q), f0 = q^f1^f2^f3; lo[q*2048 + a*8 + (f4 f5 f6)] =
+  // coordinates 4..7, coordinate 7 flipped by q^f4^f5^f6.
+  for (int r = tid; r < 256; r += nthr)
+    tab16[r] = make_uint4(pack_h2(kE8P.v[r][0], kE8P.v[r][1]), pack_h2(kE8P.v[r][2], kE8P.v[r][3]),
+                          pack_h2(kE8P.v[r][4], kE8P.v[r][5]), pack_h2(kE8P.v[r][6], kE8P.v[r][7]));
+  if (HAS2)
+    for (int e = tid; e < 256; e += nthr)
       lut1[e] = make_uint4(pack_h2(kE81.v[e][0], kE81.v[e][1]), pack_h2(kE81.v[e][2], kE81.v[e][3]),
                            pack_h2(kE81.v[e][4], kE81.v[e][5]), pack_h2(kE81.v[e][6], kE81.v[e][7]));
+  __syncthreads();
+  for (int e = tid; e < 4096; e += nthr) {
+    {
+      const uint32_t H = e >> 8, a = e & 255;
+      const uint32_t f1 = (H >> 3) & 1, f2 = (H >> 2) & 1, f3 = (H >> 1) & 1;
+      const uint32_t f0 = (H & 1) ^ f1 ^ f2 ^ f3;
+      const uint4 t = tab16[a];
+      lut_hi[e] = make_uint2(t.x ^ ((f0 << 15) | (f1 << 31)), t.y ^ ((f2 << 15) | (f3 << 31)));
+    }
+    {
+      const uint32_t qq = e >> 11, a = (e >> 3) & 255;
+      const uint32_t f4 = (e >> 2) & 1, f5 = (e >> 1) & 1, f6 = e & 1;
+      const uint32_t f7 = qq ^ f4 ^ f5 ^ f6;
+      const uint4 t = tab16[a];
+      lut_lo[e] = make_uint2(t.z ^ ((f4 << 15) | (f5 << 31)), t.w ^ ((f6 << 15) | (f7 << 31)));
+    }
   }
   __syncthreads();
 
@@ -231,7 +300,8 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mv_tiled_kernel(MvArgs A) {
 #pragma unroll
   for (int c = 0; c < 8; ++c) xb[c] = hzero;
 
-  for (int it = blockIdx.x; it < nitems; it += gridDim.x) {
+  int k = 0;
+  for (int it = blockIdx.x; it < nitems; it += gridDim.x, ++k) {
     const int sg = it / RB, rb = it - sg * RB;
     const int sl = sg * A.W + w;
     const bool active = sl < A.S;
@@ -247,10 +317,21 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mv_tiled_kernel(MvArgs A) {
     floatx4 accs = {0.f, 0.f, 0.f, 0.f};
     floatx4 acc2 = {0.f, 0.f, 0.f, 0.f};
     if (active) {
-      const size_t tile = ((size_t)rb * A.S + sl) * 64 + lane;
-      const uint4 cw = *reinterpret_cast<const uint4*>(A.codes0 + tile * 8);
+      uint4 cw;
       uint2 cw1 = make_uint2(0, 0);
-      if (HAS2) cw1 = *reinterpret_cast<const uint2*>(A.codes1 + tile * 8);
+      if (k < kPrefetch) {
+        cw = pre[0];
+        cw1 = pre1[0];
+#pragma unroll
+        for (int j = 0; j + 1 < kPrefetch; ++j) {  // rotate the prefetch ring
+          pre[j] = pre[j + 1];
+          pre1[j] = pre1[j + 1];
+        }
+      } else {
+        const size_t tile = ((size_t)rb * A.S + sl) * 64 + lane;
+        cw = *reinterpret_cast<const uint4*>(A.codes0 + tile * 8);
+        if (HAS2) cw1 = *reinterpret_cast<const uint2*>(A.codes1 + tile * 8);
+      }
       const uint32_t wd[4] = {cw.x, cw.y, cw.z, cw.w};
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
@@ -271,6 +352,12 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mv_tiled_kernel(MvArgs A) {
           half8, make_uint4((wd[0] & 0x10001u) * 0x3C00u, (wd[1] & 0x10001u) * 0x3C00u,
                             (wd[2] & 0x10001u) * 0x3C00u, (wd[3] & 0x10001u) * 0x3C00u));
       accs = __builtin_amdgcn_mfma_f32_16x16x32_f16(ash, xs, accs, 0, 0, 0);
+    } else if (k < kPrefetch) {
+#pragma unroll
+      for (int j = 0; j + 1 < kPrefetch; ++j) {
+        pre[j] = pre[j + 1];
+        pre1[j] = pre1[j + 1];
+      }
     }
     // lane holds rows 4q..4q+3 of the tile for batch column r16
     if (r16 < A.B) {
@@ -283,7 +370,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mv_tiled_kernel(MvArgs A) {
     }
     __syncthreads();
     const int nw = A.S - sg * A.W < A.W ? A.S - sg * A.W : A.W;
-    for (int u = threadIdx.x; u < 16 * A.B; u += blockDim.x) {
+    for (int u = tid; u < 16 * A.B; u += nthr) {
       const int row = u / A.B, bc = u - row * A.B;
       float s = red[0][row][bc];
       for (int ww = 1; ww < nw; ++ww) s += red[ww][row][bc];
@@ -372,10 +459,11 @@ __global__ __launch_bounds__(256) void mv_generic_kernel(MvgArgs A) {
 // ---------------------------------------------------------------------------
 struct YoutArgs {
   const float* y1p;
-  int SG, B, m, L, p;
+  int SG, B, m, logL, p, G;
   const float* K;
   float scale;
-  const float* xtot;  // NULL on the row-major path
+  const float* xtot;  // [B][kMaxParts] or NULL on the row-major path
+  int xparts;
   const float* xmul;
   float s0, layer_scale;
   const float* su;
@@ -385,23 +473,47 @@ struct YoutArgs {
   int64_t ldy;
 };
 
+// y = su (.) T_m(layer_scale * 2^e * (sum of partials - s0 X / 4)) + bias for
+// one batch row (grid = batch * G; with an odd factor each work-group
+// transforms the whole row and writes its share of the columns).
 __global__ __launch_bounds__(kRowThreads) void yout_kernel(YoutArgs A) {
-  extern __shared__ float buf[];
-  const int b = blockIdx.x;
-  const float shift = A.xtot ? -0.25f * A.s0 * A.xtot[b] : 0.0f;
+  extern __shared__ float sm[];
+  float* buf = sm;
+  float* Ks = sm + padded_len(A.m);
+  const int b = blockIdx.x / A.G;
+  const int part = blockIdx.x - b * A.G;
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  float xt = 0.0f;
+  if (A.xtot)
+    for (int j = 0; j < A.xparts; ++j) xt += A.xtot[b * kMaxParts + j];
+  const float shift = -0.25f * A.s0 * xt;
   const float mul = A.layer_scale * (A.xmul ? A.xmul[b] : 1.0f);
-  for (int i = threadIdx.x; i < A.m; i += blockDim.x) {
+  for (int i = tid; i < A.m; i += nthr) {
     float s = A.y1p[(size_t)b * A.m + i];
     for (int g = 1; g < A.SG; ++g) s += A.y1p[((size_t)g * A.B + b) * A.m + i];
-    buf[i] = (s + shift) * mul;
+    buf[pad_idx(i)] = (s + shift) * mul;
   }
+  if (A.p > 1)
+    for (int i = tid; i < A.p * A.p; i += nthr) Ks[i] = A.K[i];
   __syncthreads();
-  lds_rht(buf, A.m, A.L, A.p, A.K, A.scale);
-  for (int i = threadIdx.x; i < A.m; i += blockDim.x) {
-    float v = buf[i] * A.su[i];
+  lds_fwht(buf, A.m, A.logL, tid, nthr);
+  if (A.p == 1) {
+    for (int i = tid; i < A.m; i += nthr) {
+      float v = buf[pad_idx(i)] * A.scale * A.su[i];
+      if (A.bias) v = v + A.bias[i];
+      store_from_float(A.y, A.y_dtype, (int64_t)b * A.ldy + i, v);
+    }
+    return;
+  }
+  for (int i = tid; i < A.m; i += nthr) buf[pad_idx(i)] = buf[pad_idx(i)] * A.scale;
+  __syncthreads();
+  const int cw = (1 << A.logL) / A.G;
+  kron_cols(buf, Ks, A.p, A.logL, part * cw, (part + 1) * cw, tid, nthr, [&](int a, int c, float v) {
+    const int i = (a << A.logL) + c;
+    v = v * A.su[i];
     if (A.bias) v = v + A.bias[i];
     store_from_float(A.y, A.y_dtype, (int64_t)b * A.ldy + i, v);
-  }
+  });
 }
 
 // Raises a kernel's dynamic-LDS limit when needed (remembers the largest value
@@ -425,10 +537,35 @@ int check_transform(int64_t len, int p, const float* K, const char* which) {
   return QS_OK;
 }
 
+// Spins until the wall clock (100 MHz on gfx9-class parts) has advanced by
+// `ticks`, sleeping between reads; the iteration cap bounds the kernel even if
+// the clock misbehaves.
+__global__ void busy_wait_kernel(uint64_t ticks, uint64_t max_iters) {
+  const uint64_t t0 = wall_clock64();
+  for (uint64_t it = 0; it < max_iters; ++it) {
+    if (wall_clock64() - t0 >= ticks) break;
+    __builtin_amdgcn_s_sleep(32);
+  }
+}
+
 }  // namespace
 }  // namespace qs
 
 using namespace qs;
+
+extern "C" int qs_busy_wait(int64_t nanoseconds, qs_stream_t stream) {
+  QS_REQUIRE(nanoseconds >= 0 && nanoseconds <= 1000000000ll, "busy wait must be in [0, 1 s]");
+  int dev = 0, khz = 0;
+  QS_HIP(hipGetDevice(&dev));
+  QS_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev));
+  if (khz <= 0) khz = 100000;
+  const uint64_t ticks = (uint64_t)((double)nanoseconds * khz / 1e6);
+  // a sleep of 32 units is at least ~0.8 us, so ns/100 iterations outlast the wait
+  const uint64_t max_iters = (uint64_t)nanoseconds / 100 + 1000;
+  hipLaunchKernelGGL(busy_wait_kernel, dim3(1), dim3(64), 0, as_stream(stream), ticks, max_iters);
+  QS_LAUNCHED("busy_wait_kernel");
+  return QS_OK;
+}
 
 extern "C" size_t qs_linear_workspace_bytes(int64_t m, int64_t n, int64_t batch, int layout) {
   if (m <= 0 || n <= 0 || batch <= 0) return 0;
@@ -440,7 +577,7 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
                                  const float* su, int kron_pn, const float* kron_n, int kron_pm,
                                  const float* kron_m, float s0, float s1, float layer_scale, const float* bias,
                                  void* y, int y_dtype, int64_t ldy, void* workspace, size_t workspace_bytes,
-                                 qs_stream_t stream) {
+                                 void* mv_begin, void* mv_end, qs_stream_t stream) {
   QS_REQUIRE(batch >= 0 && n > 0 && m > 0 && n % 8 == 0, "bad shape batch=%lld n=%lld m=%lld", (long long)batch,
              (long long)n, (long long)m);
   QS_REQUIRE(x_dtype >= QS_DTYPE_F32 && x_dtype <= QS_DTYPE_BF16 && y_dtype >= QS_DTYPE_F32 &&
@@ -469,9 +606,12 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
   hipStream_t s = as_stream(stream);
   char* ws = static_cast<char*>(workspace);
   const int Ln = (int)(n / kron_pn), Lm = (int)(m / kron_pm);
-  rc = set_lds((const void*)xin_kernel, (size_t)n * 4, &g_xin_lds);
+  const size_t xin_lds = ((size_t)padded_len((int)n) + (size_t)kron_pn * kron_pn) * 4;
+  const size_t yout_lds = ((size_t)padded_len((int)m) + (size_t)kron_pm * kron_pm) * 4;
+  const int Gx = parts_for(n, kron_pn), Gy = parts_for(m, kron_pm);
+  rc = set_lds((const void*)xin_kernel, xin_lds, &g_xin_lds);
   if (rc) return rc;
-  rc = set_lds((const void*)yout_kernel, (size_t)m * 4, &g_yout_lds);
+  rc = set_lds((const void*)yout_kernel, yout_lds, &g_yout_lds);
   if (rc) return rc;
 
   for (int64_t b0 = 0; b0 < batch; b0 += kMaxTileBatch) {
@@ -484,8 +624,9 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
     XA.x_dtype = x_dtype;
     XA.ldx = ldx;
     XA.n = (int)n;
-    XA.L = Ln;
+    XA.logL = log2_exact(Ln);
     XA.p = kron_pn;
+    XA.G = Gx;
     XA.K = kron_n;
     XA.scale = inv_sqrt_len(Ln);
     XA.sv = sv;
@@ -495,10 +636,11 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
     XA.xtot = reinterpret_cast<float*>(ws + W.xtot);
     XA.xmul = reinterpret_cast<float*>(ws + W.xmul);
     XA.x2 = reinterpret_cast<float*>(ws + W.x2);
-    hipLaunchKernelGGL(xin_kernel, dim3(B), dim3(kRowThreads), (size_t)n * 4, s, XA);
+    hipLaunchKernelGGL(xin_kernel, dim3(B * Gx), dim3(kRowThreads), xin_lds, s, XA);
     QS_LAUNCHED("xin_kernel");
 
     float* y1p = reinterpret_cast<float*>(ws + W.y1p);
+    if (mv_begin && b0 == 0) QS_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(mv_begin), s));
     if (layout == QS_LAYOUT_TILED) {
       MvArgs MA{};
       MA.codes0 = static_cast<const uint16_t*>(codes0);
@@ -536,14 +678,17 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
       hipLaunchKernelGGL(mv_generic_kernel, dim3((unsigned)((m + 3) / 4)), dim3(256), 0, s, GA);
       QS_LAUNCHED("mv_generic_kernel");
     }
+    if (mv_end && b0 + kMaxTileBatch >= batch) QS_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(mv_end), s));
 
     YoutArgs YA{};
     YA.y1p = y1p;
     YA.SG = W.SG;
     YA.B = B;
     YA.m = (int)m;
-    YA.L = Lm;
+    YA.logL = log2_exact(Lm);
     YA.p = kron_pm;
+    YA.G = Gy;
+    YA.xparts = Gx;
     YA.K = kron_m;
     YA.scale = inv_sqrt_len(Lm);
     YA.xtot = layout == QS_LAYOUT_TILED ? XA.xtot : nullptr;
@@ -555,7 +700,7 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
     YA.y = yb;
     YA.y_dtype = y_dtype;
     YA.ldy = ldy;
-    hipLaunchKernelGGL(yout_kernel, dim3(B), dim3(kRowThreads), (size_t)m * 4, s, YA);
+    hipLaunchKernelGGL(yout_kernel, dim3(B * Gy), dim3(kRowThreads), yout_lds, s, YA);
     QS_LAUNCHED("yout_kernel");
   }
   return QS_OK;

@@ -3,76 +3,94 @@
 // i = a*L + b.  T_n applies the Sylvester Walsh-Hadamard stages over b (h = 1,
 // 2, 4, ..., exactly the butterfly order of quipsharp/hadamard.py:37-43), the
 // scale fl(L^-1/2), and then, when p > 1, the p x p orthogonal matrix K over a.
+//
+// The Walsh-Hadamard stages run in rounds of up to four: each thread loads the
+// 16 elements of one butterfly group (stride h0) from LDS, applies the round's
+// stages in registers in ascending order, and writes them back -- one barrier
+// per round instead of one per stage.  LDS arrays are padded by one float per
+// 32 (pad_idx) so the strided group loads do not pile onto one bank.
 #pragma once
 
 #include "qs_common.h"
 
 namespace qs {
 
-// Walsh-Hadamard stages over the low log2(L) index bits of buf[0..n), all
-// threads of the block participating.  Ends with a barrier.
-__device__ __forceinline__ void lds_fwht_stages(float* buf, int n, int L) {
-  const int half = n >> 1;
-  for (int h = 1; h < L; h <<= 1) {
-    for (int t = threadIdx.x; t < half; t += blockDim.x) {
-      // t enumerates the n/2 butterflies of this stage
-      const int blk = t / h, off = t - blk * h;
-      const int i = blk * 2 * h + off;
-      const float a = buf[i], b = buf[i + h];
-      buf[i] = a + b;
-      buf[i + h] = a - b;
-    }
-    __syncthreads();
-  }
-}
+__device__ __forceinline__ int pad_idx(int i) { return i + (i >> 5); }
+__host__ __device__ constexpr int padded_len(int n) { return n + (n >> 5) + 1; }
 
-// buf[i] *= scale, then the K stage over a when p > 1.  Ends with a barrier.
-// K is p x p fp32, row-major, in global memory.
-__device__ __forceinline__ void lds_scale_kron(float* buf, int n, int L, int p, const float* K, float scale) {
-  for (int i = threadIdx.x; i < n; i += blockDim.x) buf[i] = buf[i] * scale;
-  __syncthreads();
-  if (p <= 1) return;
-  // Work unit = (column b, share of <= 16 outputs a).  All reads of an
-  // iteration complete before its writes (barrier), so the update is in place.
-  const int parts = (p + 15) / 16;
-  const int per = (p + parts - 1) / parts;
-  const int cols = (int)blockDim.x / parts > 0 ? (int)blockDim.x / parts : 1;
-  for (int b0 = 0; b0 < L; b0 += cols) {
-    const int t = threadIdx.x;
-    const int part = t / cols;
-    const int b = b0 + t % cols;
-    const bool active = part < parts && b < L;
-    const int a0 = part * per;
-    const int a1 = a0 + per < p ? a0 + per : p;
-    float acc[16];
-    if (active) {
+template <int BITS>
+__device__ __forceinline__ void fwht_round(float* buf, int n, int logL, int logh0, int tid, int nthr) {
+  constexpr int R = 1 << BITS;
+  const int L = 1 << logL;
+  const int groups_per_seg = L >> BITS;
+  const int ngroups = (n >> logL) * groups_per_seg;
+  const int h0 = 1 << logh0;
+  for (int g = tid; g < ngroups; g += nthr) {
+    const int a = g >> (logL - BITS);
+    const int gi = g & (groups_per_seg - 1);
+    const int blk = gi >> logh0, off = gi & (h0 - 1);
+    const int base = (a << logL) + (blk << (logh0 + BITS)) + off;
+    float v[R];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        if (a0 + j < a1) {
-          const float* Kr = K + (a0 + j) * p;
-          float s = 0.0f;
-          for (int c = 0; c < p; ++c) s = __builtin_fmaf(Kr[c], buf[c * L + b], s);
-          acc[j] = s;
+    for (int j = 0; j < R; ++j) v[j] = buf[pad_idx(base + (j << logh0))];
+#pragma unroll
+    for (int s = 0; s < BITS; ++s) {
+      const int hh = 1 << s;
+#pragma unroll
+      for (int j = 0; j < R; ++j) {
+        if ((j & hh) == 0) {
+          const float x = v[j], y = v[j + hh];
+          v[j] = x + y;
+          v[j + hh] = x - y;
         }
       }
     }
-    __syncthreads();
-    if (active) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j)
-        if (a0 + j < a1) buf[(a0 + j) * L + b] = acc[j];
-    }
+    for (int j = 0; j < R; ++j) buf[pad_idx(base + (j << logh0))] = v[j];
+  }
+}
+
+// All Walsh-Hadamard stages over the low logL index bits of the padded buffer
+// (threads tid < nthr of the block participate; every thread of the block
+// must call this, it contains barriers).  Ends with a barrier.
+__device__ __forceinline__ void lds_fwht(float* buf, int n, int logL, int tid, int nthr) {
+  int done = 0;
+  while (done < logL) {
+    const int bits = logL - done >= 4 ? 4 : logL - done;
+    if (bits == 4) fwht_round<4>(buf, n, logL, done, tid, nthr);
+    else if (bits == 3) fwht_round<3>(buf, n, logL, done, tid, nthr);
+    else if (bits == 2) fwht_round<2>(buf, n, logL, done, tid, nthr);
+    else fwht_round<1>(buf, n, logL, done, tid, nthr);
+    done += bits;
     __syncthreads();
   }
 }
 
-// Full T_n in place.  scale must be fl(L^-1/2).
-__device__ __forceinline__ void lds_rht(float* buf, int n, int L, int p, const float* K, float scale) {
-  lds_fwht_stages(buf, n, L);
-  lds_scale_kron(buf, n, L, p, K, scale);
+// out[a][b] = sum_c K[a][c] * in[c][b] for columns b in [b0, b1), all a < p,
+// reading the padded buffer `in` and writing `out(a, b)` through a functor.
+// K is p x p fp32 in LDS.  No barrier.
+template <class Out>
+__device__ __forceinline__ void kron_cols(const float* in, const float* K, int p, int logL, int b0, int b1,
+                                          int tid, int nthr, Out out) {
+  const int cols = b1 - b0;
+  const int total = p * cols;
+  for (int u = tid; u < total; u += nthr) {
+    const int a = u / cols;
+    const int b = b0 + (u - a * cols);
+    const float* Kr = K + a * p;
+    float s = 0.0f;
+    for (int c = 0; c < p; ++c) s = __builtin_fmaf(Kr[c], in[pad_idx((c << logL) + b)], s);
+    out(a, b, s);
+  }
 }
 
 // fl(L ** -0.5) computed like Python's float power, then rounded to fp32.
 inline float inv_sqrt_len(int64_t L) { return (float)__builtin_pow((double)L, -0.5); }
+
+inline int log2_exact(int64_t v) {
+  int k = 0;
+  while ((1ll << k) < v) ++k;
+  return k;
+}
 
 }  // namespace qs

@@ -22,30 +22,52 @@ constexpr int kTileC = 64;          // inner columns per column-pass tile
 struct RowArgs {
   const float* in;
   float* out;
-  int n, L, p;
+  int n, logL, p, G;
   const float* K;
   const float* pre;
   const float* post;
   float scale;
 };
 
+// One work-group per (row, column share): the whole row is staged in LDS and
+// transformed; with an odd factor each of the G work-groups of a row computes
+// the K stage for L/G of the columns b and writes those outputs.
 __global__ __launch_bounds__(kRowThreads) void rht_rows_kernel(RowArgs A) {
-  extern __shared__ float buf[];
-  const int64_t row = blockIdx.x;
+  extern __shared__ float sm[];
+  float* buf = sm;
+  float* Ks = sm + padded_len(A.n);
+  const int64_t row = blockIdx.x / A.G;
+  const int part = blockIdx.x - (int)(row * A.G);
+  const int tid = threadIdx.x, nthr = blockDim.x;
   const float* src = A.in + row * A.n;
-  for (int i = threadIdx.x; i < A.n; i += blockDim.x) {
+  for (int i = tid; i < A.n; i += nthr) {
     float v = src[i];
     if (A.pre) v = v * A.pre[i];
-    buf[i] = v;
+    buf[pad_idx(i)] = v;
   }
+  if (A.p > 1)
+    for (int i = tid; i < A.p * A.p; i += nthr) Ks[i] = A.K[i];
   __syncthreads();
-  lds_rht(buf, A.n, A.L, A.p, A.K, A.scale);
+  lds_fwht(buf, A.n, A.logL, tid, nthr);
   float* dst = A.out + row * A.n;
-  for (int i = threadIdx.x; i < A.n; i += blockDim.x) {
-    float v = buf[i];
-    if (A.post) v = v * A.post[i];
-    dst[i] = v;
+  if (A.p == 1) {
+    for (int i = tid; i < A.n; i += nthr) {
+      float v = buf[pad_idx(i)] * A.scale;
+      if (A.post) v = v * A.post[i];
+      dst[i] = v;
+    }
+    return;
   }
+  for (int i = tid; i < A.n; i += nthr) buf[pad_idx(i)] = buf[pad_idx(i)] * A.scale;
+  __syncthreads();
+  const int L = 1 << A.logL;
+  const int cw = L / A.G;
+  const float* post = A.post;
+  kron_cols(buf, Ks, A.p, A.logL, part * cw, (part + 1) * cw, tid, nthr, [&](int a, int b, float v) {
+    const int i = (a << A.logL) + b;
+    if (post) v = v * post[i];
+    dst[i] = v;
+  });
 }
 
 // One radix pass of Walsh-Hadamard stages h0, 2*h0, ..., h0*(R/2) on the axis.
@@ -161,13 +183,16 @@ extern "C" int qs_rht_f32(const float* in, float* out, int64_t outer, int64_t n,
   const float scale = inv_sqrt_len(L);
   if (inner == 1) {
     QS_REQUIRE(n <= kMaxRowLen, "row transform supports n <= %d (got %lld)", kMaxRowLen, (long long)n);
-    QS_REQUIRE(outer < (1ll << 31), "too many rows");
-    const size_t lds = (size_t)n * sizeof(float);
+    // Work-groups of one row read the whole row: split the odd-factor stage over
+    // several of them only when the output does not overwrite the input.
+    const int G = (kron_p > 1 && in != out) ? (L / 8 < 16 ? (int)(L / 8 > 0 ? L / 8 : 1) : 16) : 1;
+    QS_REQUIRE(outer * G < (1ll << 31), "too many rows");
+    const size_t lds = ((size_t)padded_len((int)n) + (kron_p > 1 ? (size_t)kron_p * kron_p : 0)) * sizeof(float);
     if (lds > 65536)
       QS_HIP(hipFuncSetAttribute((const void*)rht_rows_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                  (int)lds));
-    RowArgs A{in, out, (int)n, (int)L, kron_p, kron_mat, pre_axis, post_axis, scale};
-    hipLaunchKernelGGL(rht_rows_kernel, dim3((unsigned)outer), dim3(kRowThreads), lds, s, A);
+    RowArgs A{in, out, (int)n, log2_exact(L), kron_p, G, kron_mat, pre_axis, post_axis, scale};
+    hipLaunchKernelGGL(rht_rows_kernel, dim3((unsigned)(outer * G)), dim3(kRowThreads), lds, s, A);
     QS_LAUNCHED("rht_rows_kernel");
     return QS_OK;
   }

@@ -158,7 +158,8 @@ class PackedCodes:
 
 
 def forward_packed(x: Tensor, packed: PackedCodes, su: Tensor, sv: Tensor, s0: float, s1: float,
-                   layer_scale: float, bias: Tensor = None, out_dtype=None, workspace: Tensor = None) -> Tensor:
+                   layer_scale: float, bias: Tensor = None, out_dtype=None, workspace: Tensor = None,
+                   out: Tensor = None, mv_events=None) -> Tensor:
     """y = su (.) T_m(layer_scale * W_hat @ T_n(sv (.) x)) + bias for x (..., n),
     computed in the library (fp32 accumulation; output in ``out_dtype``,
     default x.dtype)."""
@@ -172,7 +173,7 @@ def forward_packed(x: Tensor, packed: PackedCodes, su: Tensor, sv: Tensor, s0: f
     if x2.stride(-1) != 1:
         x2 = x2.contiguous()
     B = x2.shape[0]
-    y = torch.empty(B, m, dtype=out_dtype, device=x.device)
+    y = out.reshape(B, m) if out is not None else torch.empty(B, m, dtype=out_dtype, device=x.device)
     if B == 0:
         return y.reshape(*lead, m)
     fm, fn = kron_factor(m), kron_factor(n)
@@ -188,7 +189,9 @@ def forward_packed(x: Tensor, packed: PackedCodes, su: Tensor, sv: Tensor, s0: f
         _lib.ptr(x2), _lib.dtype_code(x2.dtype), x2.stride(0), B, n, m, _lib.ptr(packed.codes0),
         _lib.ptr(packed.codes1), packed.kind1, packed.layout, _lib.ptr(sv), _lib.ptr(su), fn[0], _lib.ptr(Kn),
         fm[0], _lib.ptr(Km), float(s0), float(s1), float(layer_scale), _lib.ptr(bias), _lib.ptr(y),
-        _lib.dtype_code(out_dtype), m, _lib.ptr(workspace), workspace.numel(), _lib.stream_of(x2)))
+        _lib.dtype_code(y.dtype), m, _lib.ptr(workspace), workspace.numel(),
+        None if mv_events is None else _lib._vp(mv_events[0]), None if mv_events is None else _lib._vp(mv_events[1]),
+        _lib.stream_of(x2)))
     return y.reshape(*lead, m)
 
 
