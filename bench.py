@@ -56,9 +56,16 @@ def linear_bytes(m, n, B):
 
 
 def mv_bytes(m, n, B):
-    """Algorithmic bytes of one decode-matvec launch: codes, fp16 activations
-    in, fp32 partial outputs."""
+    """Algorithmic bytes of one decode-matvec launch.  At B <= 2 the launch is
+    the one-kernel forward (codes, signs, bf16 activations in and out: the
+    whole linear); at larger batches it is the tiled matvec alone (codes, fp16
+    activations in, fp32 partial outputs)."""
+    if B <= 2:
+        return linear_bytes(m, n, B)
     return m * n // 8 * 2 + 2 * B * n + 4 * B * m
+
+
+MV_KERNEL = {True: "linear_fused_kernel", False: "mv_tiled_kernel"}
 
 
 class Stack:
@@ -105,7 +112,7 @@ class Runner:
         self.x = torch.randn(B, 4096, generator=g, device=dev).bfloat16()
         self.buf = {k: torch.empty(B, m, dtype=torch.bfloat16, device=dev) for k, m, _ in LLAMA2_7B}
         ws = max(self.lib.qs_linear_workspace_bytes(m, n, B, _lib.QS_LAYOUT_TILED) for _, m, n in LLAMA2_7B)
-        self.ws = torch.empty(ws, dtype=torch.uint8, device=dev)
+        self.ws = torch.zeros(ws, dtype=torch.uint8, device=dev)  # counter region must start at zero
         self.K43 = hartley_matrix(43, dev)
         self.src = {"q": None, "k": None, "v": None, "o": "q", "gate": "o", "up": "o", "down": "gate"}
 
@@ -352,7 +359,7 @@ def main():
                    "global_batch": 1, "layers": args.layers, "linears_per_step": r1.launches_per_step(),
                    "code_bytes": stack.code_bytes(), "parallelism": "none (1 GPU)"},
         "tok_per_s": round(1e3 / ms, 1), "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
-        "roofline": {"bound": "hbm", "kernel": "mv_tiled_kernel", "achieved": round(achieved, 1),
+        "roofline": {"bound": "hbm", "kernel": MV_KERNEL[True], "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "avg_launch_us": round(mv_ms * 1e3, 3), "bytes_per_launch": int(mv_avg_bytes),
                      "traffic": None},

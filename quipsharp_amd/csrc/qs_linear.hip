@@ -23,6 +23,14 @@
 #include "qs_rht_dev.h"
 
 namespace qs {
+
+int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, int m, const void* codes0,
+                        const void* codes1, const float* sv, const float* su, int pn, const float* Kn, int pm,
+                        const float* Km, float s0, float s1, float layer_scale, const float* bias, void* y,
+                        int y_dtype, int64_t ldy, unsigned* counter, float* xmul, float* y1p, int S, int SG, int W,
+                        int ncu, hipStream_t stream, bool* out_done);
+bool fused_eligible(int64_t batch, int64_t n, int64_t m, int pn);
+
 namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -55,10 +63,12 @@ int parts_for(int64_t len, int p) {
   return g < 1 ? 1 : (int)g;
 }
 
+// The first 256 bytes of every workspace hold the fused kernel's completion
+// counter; it must be zero before the first call and every call leaves it zero.
 WsLayout ws_layout(int64_t m, int64_t n, int64_t batch, int layout) {
   WsLayout L{};
   const int64_t B = batch < kMaxTileBatch ? batch : kMaxTileBatch;
-  size_t off = 0;
+  size_t off = 256;
   if (layout == QS_LAYOUT_TILED) {
     L.S = (int)(n / 256);
     L.SG = (L.S + kMaxWaves - 1) / kMaxWaves;
@@ -605,6 +615,48 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
 
   hipStream_t s = as_stream(stream);
   char* ws = static_cast<char*>(workspace);
+  if (layout == QS_LAYOUT_TILED && fused_eligible(batch, n, m, kron_pn) &&
+      (reinterpret_cast<uintptr_t>(sv) & 15) == 0) {
+    float* y1p = reinterpret_cast<float*>(ws + W.y1p);
+    float* xmul = reinterpret_cast<float*>(ws + W.xmul);
+    if (mv_begin) QS_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(mv_begin), s));
+    bool done = false;
+    rc = launch_linear_fused(x, x_dtype, ldx, (int)batch, (int)n, (int)m, codes0, codes1, sv, su, kron_pn, kron_n,
+                             kron_pm, kron_m, s0, s1, layer_scale, bias, y, y_dtype, ldy,
+                             reinterpret_cast<unsigned*>(ws), xmul, y1p, W.S, W.SG, W.W, cu_count(), s, &done);
+    if (rc) return rc;
+    if (mv_end) QS_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(mv_end), s));
+    if (!done) {
+      const int Lm = (int)(m / kron_pm);
+      const size_t yout_lds = ((size_t)padded_len((int)m) + (size_t)kron_pm * kron_pm) * 4;
+      const int Gy = parts_for(m, kron_pm);
+      rc = set_lds((const void*)yout_kernel, yout_lds, &g_yout_lds);
+      if (rc) return rc;
+      YoutArgs YA{};
+      YA.y1p = y1p;
+      YA.SG = W.SG;
+      YA.B = (int)batch;
+      YA.m = (int)m;
+      YA.logL = log2_exact(Lm);
+      YA.p = kron_pm;
+      YA.G = Gy;
+      YA.K = kron_m;
+      YA.scale = inv_sqrt_len(Lm);
+      YA.xtot = nullptr;
+      YA.xparts = 0;
+      YA.xmul = xmul;
+      YA.s0 = s0;
+      YA.layer_scale = layer_scale;
+      YA.su = su;
+      YA.bias = bias;
+      YA.y = y;
+      YA.y_dtype = y_dtype;
+      YA.ldy = ldy;
+      hipLaunchKernelGGL(yout_kernel, dim3((unsigned)(batch * Gy)), dim3(kRowThreads), yout_lds, s, YA);
+      QS_LAUNCHED("yout_kernel");
+    }
+    return QS_OK;
+  }
   const int Ln = (int)(n / kron_pn), Lm = (int)(m / kron_pm);
   const size_t xin_lds = ((size_t)padded_len((int)n) + (size_t)kron_pn * kron_pn) * 4;
   const size_t yout_lds = ((size_t)padded_len((int)m) + (size_t)kron_pm * kron_pm) * 4;

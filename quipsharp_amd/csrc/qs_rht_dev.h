@@ -52,11 +52,16 @@ __device__ __forceinline__ void fwht_round(float* buf, int n, int logL, int logh
 
 // All Walsh-Hadamard stages over the low logL index bits of the padded buffer
 // (threads tid < nthr of the block participate; every thread of the block
-// must call this, it contains barriers).  Ends with a barrier.
+// must call this, it contains barriers).  The radix adapts so that every
+// participating thread owns about one butterfly group per round: a 4096-point
+// transform on 1024 threads runs six radix-4 rounds.  Ends with a barrier.
 __device__ __forceinline__ void lds_fwht(float* buf, int n, int logL, int tid, int nthr) {
+  int per = n / nthr;  // elements per thread
+  int rb = 2;
+  while (rb < 4 && (2 << rb) <= per) ++rb;  // radix 4, 8 or 16
   int done = 0;
   while (done < logL) {
-    const int bits = logL - done >= 4 ? 4 : logL - done;
+    const int bits = logL - done >= rb ? rb : logL - done;
     if (bits == 4) fwht_round<4>(buf, n, logL, done, tid, nthr);
     else if (bits == 3) fwht_round<3>(buf, n, logL, done, tid, nthr);
     else if (bits == 2) fwht_round<2>(buf, n, logL, done, tid, nthr);

@@ -184,7 +184,8 @@ def forward_packed(x: Tensor, packed: PackedCodes, su: Tensor, sv: Tensor, s0: f
     lib = _lib.lib()
     need = lib.qs_linear_workspace_bytes(m, n, B, packed.layout)
     if workspace is None or workspace.numel() < need:
-        workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=x.device)
+        # zero-initialised: the first 256 bytes are the fused kernel's counter
+        workspace = torch.zeros(max(need, 256), dtype=torch.uint8, device=x.device)
     _lib.check(lib.qs_linear_forward(
         _lib.ptr(x2), _lib.dtype_code(x2.dtype), x2.stride(0), B, n, m, _lib.ptr(packed.codes0),
         _lib.ptr(packed.codes1), packed.kind1, packed.layout, _lib.ptr(sv), _lib.ptr(su), fn[0], _lib.ptr(Kn),

@@ -170,3 +170,39 @@ def test_forward_large_activation_range(dev):
     g = y.cpu().numpy()
     for b in range(2):
         assert rel_err(g[b], want[b]) < REL_TOL
+
+
+@pytest.mark.parametrize("m,n,B", [(4096, 4096, 1), (11008, 4096, 1), (4096, 11008, 2)])
+def test_forward_graph_replays(dev, m, n, B):
+    """The single-launch path keeps its completion counter in the workspace and
+    resets it in-kernel: captured in a HIP graph, every replay (with eager work
+    and synchronizations in between) must equal the eager result."""
+    from quipsharp_amd.quantize import PackedCodes, forward_packed
+    rng = np.random.default_rng(m + n + B)
+    codes = torch.from_numpy(rng.integers(0, 65536, (m, n // 8))).to(dev)
+    packed = PackedCodes(codes, m, n, [0])
+    su = torch.from_numpy(rng.choice([-1.0, 1.0], m).astype(np.float32)).to(dev)
+    sv = torch.from_numpy(rng.choice([-1.0, 1.0], n).astype(np.float32)).to(dev)
+    x = torch.randn(B, n, device=dev).bfloat16()
+    ws = torch.zeros(1 << 22, dtype=torch.uint8, device=dev)
+    out = torch.empty(B, m, device=dev, dtype=torch.bfloat16)
+    eager = forward_packed(x, packed, su, sv, 1.0, 0.0, 0.0135, workspace=ws).clone()
+    forward_packed(x, packed, su, sv, 1.0, 0.0, 0.0135, workspace=ws, out=out)
+    assert torch.equal(out, eager)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        forward_packed(x, packed, su, sv, 1.0, 0.0, 0.0135, workspace=ws, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        forward_packed(x, packed, su, sv, 1.0, 0.0, 0.0135, workspace=ws, out=out)
+    for rep in range(4):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), rep
+        # unrelated eager work between replays
+        _ = forward_packed(x, packed, su, sv, 1.0, 0.0, 0.0135, workspace=ws)
+        torch.cuda.synchronize()
