@@ -42,6 +42,9 @@ def parse():
     p.add_argument("--skip-quantize", action="store_true")
     p.add_argument("--skip-cpu", action="store_true")
     p.add_argument("--skip-batch16", action="store_true")
+    p.add_argument("--probe", action="store_true",
+                   help="hardware-counter probe: one eager step over a 2-layer stack, then a 256 MiB "
+                        "elementwise scale (reads and writes 256 MiB) for calibrating byte counters")
     return p.parse_args()
 
 
@@ -66,6 +69,20 @@ def mv_bytes(m, n, B):
 
 
 MV_KERNEL = {True: "linear_fused_kernel", False: "mv_tiled_kernel"}
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "linear_fused_llama2_7b_b1.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the batch-1 kernel, from the committed
+    hardware-counter summary (FETCH_SIZE + WRITE_SIZE, calibrated), or None."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
 
 
 class Stack:
@@ -191,9 +208,10 @@ def time_graph(runner, steps, warmup):
 
 
 def time_mv_kernels(runner, passes=3):
-    """Average duration of the decode-matvec launches, from HIP events recorded
-    on the launch stream around each launch (the stream is kept busy so the
-    launches run back to back)."""
+    """Average duration of the decode-matvec kernels, from HIP events attached
+    to each kernel's dispatch (hipExtLaunchKernelGGL start / stop events, the
+    interval a kernel trace reports as its duration).  The stream is kept busy
+    first so the launches queue back to back."""
     import torch
     from quipsharp_amd import _lib
     n = runner.launches_per_step()
@@ -310,6 +328,17 @@ def main():
     import torch
     dev = torch.device("cuda:0")
     torch.manual_seed(0)
+    if args.probe:
+        stack = Stack(2, dev)
+        r1 = Runner(stack, 1)
+        r1.step()
+        torch.cuda.synchronize()
+        a = torch.ones(64 << 20, dtype=torch.float32, device=dev)
+        b = torch.empty_like(a)
+        torch.mul(a, 2.0, out=b)
+        torch.cuda.synchronize()
+        print(json.dumps({"probe": "done", "linears": r1.launches_per_step(), "copy_bytes": a.numel() * 4}))
+        return
     t_setup = time.perf_counter()
     stack = Stack(args.layers, dev)
     log(f"stack: {args.layers} layers, {stack.code_bytes() / 1e9:.2f} GB of codes, "
@@ -362,7 +391,7 @@ def main():
         "roofline": {"bound": "hbm", "kernel": MV_KERNEL[True], "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "avg_launch_us": round(mv_ms * 1e3, 3), "bytes_per_launch": int(mv_avg_bytes),
-                     "traffic": None},
+                     "traffic": measured_traffic() if args.layers == 32 else None},
         "cpu_baseline": cpu,
     }
     line.update(extra)

@@ -152,8 +152,12 @@ size_t qs_linear_workspace_bytes(int64_t m, int64_t n, int64_t batch, int layout
  *   bias [m] fp32 or NULL
  * Activations enter the matrix cores as fp16 (per-row power-of-two scaled),
  * decoded weights are exact in fp16, accumulation is fp32.
- * mv_begin / mv_end: optional hipEvent_t recorded on `stream` right before
- * the first and right after the last decode-matvec launch (NULL: none). */
+ * The workspace must be zero before its first use (its first 256 bytes are a
+ * completion counter that every call leaves at zero); calls that may run
+ * concurrently need separate workspaces.
+ * mv_begin / mv_end: optional hipEvent_t attached to the start of the first
+ * and the end of the last decode-matvec kernel (hipExtLaunchKernelGGL start /
+ * stop events, so the interval is kernel execution only; NULL: none). */
 int qs_linear_forward(const void *x, int x_dtype, int64_t ldx, int64_t batch, int64_t n, int64_t m,
                       const void *codes0, const void *codes1, int kind1, int layout, const float *sv,
                       const float *su, int kron_pn, const float *kron_n, int kron_pm,

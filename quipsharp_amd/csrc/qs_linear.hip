@@ -20,7 +20,9 @@
 //                   partials, scales, T_m in LDS, su, bias, output dtype.
 #include <cmath>
 
-#include "qs_rht_dev.h"
+#include <hip/hip_ext.h>
+
+#include "qs_chunk_dev.h"
 
 namespace qs {
 
@@ -28,7 +30,7 @@ int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, i
                         const void* codes1, const float* sv, const float* su, int pn, const float* Kn, int pm,
                         const float* Km, float s0, float s1, float layer_scale, const float* bias, void* y,
                         int y_dtype, int64_t ldy, unsigned* counter, float* xmul, float* y1p, int S, int SG, int W,
-                        int ncu, hipStream_t stream, bool* out_done);
+                        int ncu, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop, bool* out_done);
 bool fused_eligible(int64_t batch, int64_t n, int64_t m, int pn);
 
 namespace {
@@ -526,6 +528,92 @@ __global__ __launch_bounds__(kRowThreads) void yout_kernel(YoutArgs A) {
   });
 }
 
+// The same output transform with the chunk scheme: one work-group per (batch
+// row, output chunk a of 256).  Every work-group sums the partials of all
+// chunks and runs their 256-point transforms (a few hundred VALU cycles per
+// wave, repeated in each work-group), then forms its own chunk row of
+// M = K_p (x) H_{L/256}: y[256 a + t] = sum_c M[a][c] Y[c][t].
+// Floats of the chunk buffer: the chunks, and at least the 1024 partial sums
+// of the final reduction that reuse it.
+__host__ __device__ inline int yc_rows_floats(int Sm) { return Sm * kYStride > 1024 ? Sm * kYStride : 1024; }
+
+struct YcArgs {
+  const float* y1p;
+  int SG, B, m, Sm, lsh, p;
+  const float* K;
+  float scale;
+  const float* xtot;  // [B][kMaxParts] or NULL
+  int xparts;
+  const float* xmul;  // [B] or NULL
+  float s0, layer_scale;
+  const float* su;
+  const float* bias;
+  void* y;
+  int y_dtype;
+  int64_t ldy;
+};
+
+__global__ __launch_bounds__(kRowThreads) void yout_chunk_kernel(YcArgs A) {
+  extern __shared__ __attribute__((aligned(16))) float smc[];
+  float* Y = smc;                                   // Sm x kYStride, at least 1024 floats
+  float* Ks = smc + yc_rows_floats(A.Sm);           // p x p
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int b = blockIdx.x / A.Sm, a = blockIdx.x - b * A.Sm;
+  const LaneX lx = lane_x_init();
+  float xt = 0.0f;
+  if (A.xtot)
+    for (int j = 0; j < A.xparts; ++j) xt += A.xtot[b * kMaxParts + j];
+  const float shift = -0.25f * A.s0 * xt;
+  if (A.p > 1)
+    for (int i = tid; i < A.p * A.p; i += kRowThreads) Ks[i] = A.K[i];
+  // output element of thread tid < 256 (loads issued early)
+  const int io = 256 * a + (tid & 255);
+  const float su_o = A.su[io];
+  const float bias_o = A.bias ? A.bias[io] : 0.0f;
+  float zv[kCPW][4];
+#pragma unroll
+  for (int u = 0; u < kCPW; ++u) {
+    const int c = w + kWaves * u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) zv[u][j] = 0.0f;
+    if (c < A.Sm) {
+      for (int g = 0; g < A.SG; ++g) {
+        const float4 v =
+            *reinterpret_cast<const float4*>(A.y1p + ((size_t)g * A.B + b) * A.m + 256 * c + 4 * lane);
+        zv[u][0] += v.x;
+        zv[u][1] += v.y;
+        zv[u][2] += v.z;
+        zv[u][3] += v.w;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) zv[u][j] += shift;
+    }
+  }
+  h256_chunks(zv, A.Sm, lane, lx);
+#pragma unroll
+  for (int u = 0; u < kCPW; ++u) {
+    const int c = w + kWaves * u;
+    if (c < A.Sm)
+      *reinterpret_cast<float4*>(Y + c * kYStride + 4 * lane) = make_float4(zv[u][0], zv[u][1], zv[u][2], zv[u][3]);
+  }
+  __syncthreads();
+  // four threads per output column t (one per wave quarter), each over the
+  // chunks c = part (mod 4); partial sums meet in LDS
+  {
+    const int t = tid & 255, part = tid >> 8;
+    float acc = 0.0f;
+    for (int c = part; c < A.Sm; c += 4) acc = __builtin_fmaf(mmat(a, c, A.lsh, A.p, Ks), Y[c * kYStride + t], acc);
+    __syncthreads();  // Y row 0 is reused for the partial sums
+    if (part > 0) Y[part * 256 + t] = acc;
+    __syncthreads();
+    if (part == 0) {
+      for (int k = 1; k < 4; ++k) acc += Y[k * 256 + t];
+      const float mul = A.scale * A.layer_scale * (A.xmul ? A.xmul[b] : 1.0f);
+      store_from_float(A.y, A.y_dtype, (int64_t)b * A.ldy + io, acc * mul * su_o + bias_o);
+    }
+  }
+}
+
 // Raises a kernel's dynamic-LDS limit when needed (remembers the largest value
 // set per kernel; a benign race at worst repeats the call).
 int set_lds(const void* fn, size_t bytes, int* done) {
@@ -536,6 +624,37 @@ int set_lds(const void* fn, size_t bytes, int* done) {
   return QS_OK;
 }
 int g_xin_lds = 0, g_yout_lds = 0;
+
+// Launches yout_chunk_kernel (m a multiple of 256, m <= kMaxN, m / p >= 256).
+int launch_yout_chunk(const float* y1p, int SG, int B, int64_t m, int p, const float* K, const float* xtot,
+                      int xparts, const float* xmul, float s0, float layer_scale, const float* su,
+                      const float* bias, void* y, int y_dtype, int64_t ldy, hipStream_t s) {
+  YcArgs A{};
+  A.y1p = y1p;
+  A.SG = SG;
+  A.B = B;
+  A.m = (int)m;
+  A.Sm = (int)(m / 256);
+  A.lsh = log2_exact(m / p / 256);
+  A.p = p;
+  A.K = K;
+  A.scale = inv_sqrt_len(m / p);
+  A.xtot = xtot;
+  A.xparts = xparts;
+  A.xmul = xmul;
+  A.s0 = s0;
+  A.layer_scale = layer_scale;
+  A.su = su;
+  A.bias = bias;
+  A.y = y;
+  A.y_dtype = y_dtype;
+  A.ldy = ldy;
+  const size_t lds = ((size_t)yc_rows_floats(A.Sm) + (size_t)p * p) * 4;
+  QS_REQUIRE(lds <= 65536, "chunk output transform: %zu bytes of LDS", lds);
+  hipLaunchKernelGGL(yout_chunk_kernel, dim3((unsigned)(B * A.Sm)), dim3(kRowThreads), lds, s, A);
+  QS_LAUNCHED("yout_chunk_kernel");
+  return QS_OK;
+}
 
 int check_transform(int64_t len, int p, const float* K, const char* which) {
   QS_REQUIRE(p >= 1 && (p & 1) && p <= QS_MAX_KRON, "%s: kron factor must be odd in [1, %d]", which, QS_MAX_KRON);
@@ -619,13 +738,15 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
       (reinterpret_cast<uintptr_t>(sv) & 15) == 0) {
     float* y1p = reinterpret_cast<float*>(ws + W.y1p);
     float* xmul = reinterpret_cast<float*>(ws + W.xmul);
-    if (mv_begin) QS_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(mv_begin), s));
     bool done = false;
     rc = launch_linear_fused(x, x_dtype, ldx, (int)batch, (int)n, (int)m, codes0, codes1, sv, su, kron_pn, kron_n,
                              kron_pm, kron_m, s0, s1, layer_scale, bias, y, y_dtype, ldy,
-                             reinterpret_cast<unsigned*>(ws), xmul, y1p, W.S, W.SG, W.W, cu_count(), s, &done);
+                             reinterpret_cast<unsigned*>(ws), xmul, y1p, W.S, W.SG, W.W, cu_count(), s,
+                             reinterpret_cast<hipEvent_t>(mv_begin), reinterpret_cast<hipEvent_t>(mv_end), &done);
     if (rc) return rc;
-    if (mv_end) QS_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(mv_end), s));
+    if (!done && chunk_transform_fits(m, kron_pm))
+      return launch_yout_chunk(y1p, W.SG, (int)batch, m, kron_pm, kron_m, nullptr, 0, xmul, s0, layer_scale, su,
+                               bias, y, y_dtype, ldy, s);
     if (!done) {
       const int Lm = (int)(m / kron_pm);
       const size_t yout_lds = ((size_t)padded_len((int)m) + (size_t)kron_pm * kron_pm) * 4;
@@ -692,7 +813,8 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
     QS_LAUNCHED("xin_kernel");
 
     float* y1p = reinterpret_cast<float*>(ws + W.y1p);
-    if (mv_begin && b0 == 0) QS_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(mv_begin), s));
+    hipEvent_t ev0 = b0 == 0 ? reinterpret_cast<hipEvent_t>(mv_begin) : nullptr;
+    hipEvent_t ev1 = b0 + kMaxTileBatch >= batch ? reinterpret_cast<hipEvent_t>(mv_end) : nullptr;
     if (layout == QS_LAYOUT_TILED) {
       MvArgs MA{};
       MA.codes0 = static_cast<const uint16_t*>(codes0);
@@ -711,9 +833,9 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
       const int items = (int)(m / 16) * W.SG;
       const int grid = items < cu_count() ? items : cu_count();
       if (codes1)
-        hipLaunchKernelGGL(mv_tiled_kernel<true>, dim3(grid), dim3(W.W * 64), 0, s, MA);
+        hipExtLaunchKernelGGL(mv_tiled_kernel<true>, dim3(grid), dim3(W.W * 64), 0, s, ev0, ev1, 0, MA);
       else
-        hipLaunchKernelGGL(mv_tiled_kernel<false>, dim3(grid), dim3(W.W * 64), 0, s, MA);
+        hipExtLaunchKernelGGL(mv_tiled_kernel<false>, dim3(grid), dim3(W.W * 64), 0, s, ev0, ev1, 0, MA);
       QS_LAUNCHED("mv_tiled_kernel");
     } else {
       MvgArgs GA{};
@@ -727,11 +849,17 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
       GA.B = B;
       GA.s0 = s0;
       GA.s1 = s1;
-      hipLaunchKernelGGL(mv_generic_kernel, dim3((unsigned)((m + 3) / 4)), dim3(256), 0, s, GA);
+      hipExtLaunchKernelGGL(mv_generic_kernel, dim3((unsigned)((m + 3) / 4)), dim3(256), 0, s, ev0, ev1, 0, GA);
       QS_LAUNCHED("mv_generic_kernel");
     }
-    if (mv_end && b0 + kMaxTileBatch >= batch) QS_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(mv_end), s));
 
+    if (chunk_transform_fits(m, kron_pm)) {
+      rc = launch_yout_chunk(y1p, W.SG, B, m, kron_pm, kron_m, layout == QS_LAYOUT_TILED ? XA.xtot : nullptr, Gx,
+                             layout == QS_LAYOUT_TILED ? XA.xmul : nullptr, s0, layer_scale, su, bias, yb, y_dtype,
+                             ldy, s);
+      if (rc) return rc;
+      continue;
+    }
     YoutArgs YA{};
     YA.y1p = y1p;
     YA.SG = W.SG;

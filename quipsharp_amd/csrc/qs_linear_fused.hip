@@ -13,8 +13,9 @@
 // Work-group j owns one slice group (up to 16 slices of 256 input columns,
 // one per wave) and a strided set of 16-row blocks, so each wave's activation
 // operand stays in registers for the whole launch.  Per work-group:
-//   1. issue the table, activation and first code-tile loads, in the order
-//      they are consumed; build the signed half-codeword LDS tables;
+//   1. issue the table and activation loads, build the signed half-codeword
+//      LDS tables; the first code tiles are requested once the activations
+//      have arrived;
 //   2. input transform (every work-group; only its own slices' rows of M):
 //      chunks -> LDS, MFMA over M rows of this group, fp16 operand per wave
 //      scaled by 2^-e (e from the row norm) plus the per-group sums for the
@@ -25,8 +26,10 @@
 //   4. completion: the stores are waited for, then one atomic per work-group
 //      on a counter; the last work-group reads the partials (write-through
 //      loads), applies S_u T_m(.) + bias with the same chunk/MFMA scheme and
-//      resets the counter.  m must be a multiple of 256 and <= 12288 for
-//      this; otherwise a separate output kernel runs (qs_linear.hip).
+//      resets the counter.  This is done for pure Walsh-Hadamard outputs
+//      (m a power of two, 256 <= m <= 8192); outputs with an odd factor run
+//      the chunk output kernel instead, one work-group per output chunk
+//      (qs_linear.hip), which spreads the K_p stage over many CUs.
 //
 // Cross-work-group visibility.  Partial sums are written with agent-scope
 // relaxed atomic stores and read with agent-scope relaxed atomic loads, which
@@ -34,7 +37,9 @@
 // (no per-XCD L2 copy is involved), and every work-group waits for its own
 // stores to complete (s_waitcnt) before its counter increment.  This avoids
 // an L2 write-back per wave that a device-scope fence would cost.
-#include "qs_rht_dev.h"
+#include <hip/hip_ext.h>
+
+#include "qs_chunk_dev.h"
 
 namespace qs {
 namespace {
@@ -46,18 +51,14 @@ __constant__ Table8 kE8P = make_e8p_table();
 __constant__ Table8 kE81 = make_e81_table();
 
 constexpr int kThreads = 1024;
-constexpr int kWaves = 16;
 constexpr int kMaxB = 2;
-constexpr int kMaxN = 12288;
-constexpr int kMaxS = kMaxN / 256;          // chunks of 256
-constexpr int kCPW = kMaxS / kWaves;        // chunks per wave (3)
 constexpr int kPrefetch = 4;
-constexpr int kYStride = 272;               // floats per chunk row (consecutive rows 16 banks apart)
 constexpr int kXStride = 264;               // halves per slice row of the fp16 operand buffer
 
 struct FusedArgs {
   const void* x;
   int x_dtype;
+  int x_vec;  // rows of 4 elements can be loaded as one 8- or 16-byte word
   int64_t ldx;
   int B;
   int n, Sn, lsh_n, pn;
@@ -102,67 +103,6 @@ __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
   return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
 }
 
-// Value of lane (lane ^ MASK).
-template <int MASK>
-__device__ __forceinline__ float lane_xor(float v) {
-  const int iv = __builtin_bit_cast(int, v);
-  int r;
-  if constexpr (MASK == 1) {
-    r = __builtin_amdgcn_update_dpp(0, iv, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
-  } else if constexpr (MASK == 2) {
-    r = __builtin_amdgcn_update_dpp(0, iv, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
-  } else if constexpr (MASK == 8) {
-    r = __builtin_amdgcn_update_dpp(0, iv, 0x128, 0xF, 0xF, false);  // row_ror:8
-  } else if constexpr (MASK == 4 || MASK == 16) {
-    r = __builtin_amdgcn_ds_swizzle(iv, 0x1F | (MASK << 10));  // bit mode, xor within 32 lanes
-  } else {
-    static_assert(MASK == 32, "lane mask");
-    r = __builtin_amdgcn_ds_bpermute((int)((__lane_id() ^ 32u) << 2), iv);
-  }
-  return __builtin_bit_cast(float, r);
-}
-
-template <int MASK, int NC>
-__device__ __forceinline__ void lane_stage(float (&v)[NC][4], int lane) {
-  const bool upper = (lane & MASK) != 0;
-#pragma unroll
-  for (int c = 0; c < NC; ++c)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float o = lane_xor<MASK>(v[c][j]);
-      v[c][j] = upper ? o - v[c][j] : v[c][j] + o;
-    }
-}
-
-// Unnormalised 256-point Walsh-Hadamard of each chunk held as element
-// t = 4 * lane + j in v[c][j].
-template <int NC>
-__device__ __forceinline__ void h256(float (&v)[NC][4], int lane) {
-#pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    const float a0 = v[c][0] + v[c][1], a1 = v[c][0] - v[c][1];
-    const float a2 = v[c][2] + v[c][3], a3 = v[c][2] - v[c][3];
-    v[c][0] = a0 + a2;
-    v[c][2] = a0 - a2;
-    v[c][1] = a1 + a3;
-    v[c][3] = a1 - a3;
-  }
-  lane_stage<1>(v, lane);
-  lane_stage<2>(v, lane);
-  lane_stage<4>(v, lane);
-  lane_stage<8>(v, lane);
-  lane_stage<16>(v, lane);
-  lane_stage<32>(v, lane);
-}
-
-// Entry (r, c) of M = K_p (x) H_{2^lsh}: chunk index r = a * 2^lsh + h.
-__device__ __forceinline__ float mmat(int r, int c, int lsh, int p, const float* Ks) {
-  const int hm = (1 << lsh) - 1;
-  float v = (__builtin_popcount(r & c & hm) & 1) ? -1.0f : 1.0f;
-  if (p > 1) v *= Ks[(r >> lsh) * p + (c >> lsh)];
-  return v;
-}
-
 // Activation chunks of batch row b (times sv), chunk c = w + 16 u.
 __device__ __forceinline__ void load_x(const FusedArgs& A, int b, int w, int lane, float (&v)[kCPW][4]) {
 #pragma unroll
@@ -174,10 +114,31 @@ __device__ __forceinline__ void load_x(const FusedArgs& A, int b, int w, int lan
       const int i0 = 256 * c + 4 * lane;
       const float4 s = *reinterpret_cast<const float4*>(A.sv + i0);
       const int64_t xi = (int64_t)b * A.ldx + i0;
-      v[u][0] = load_as_float(A.x, A.x_dtype, xi) * s.x;
-      v[u][1] = load_as_float(A.x, A.x_dtype, xi + 1) * s.y;
-      v[u][2] = load_as_float(A.x, A.x_dtype, xi + 2) * s.z;
-      v[u][3] = load_as_float(A.x, A.x_dtype, xi + 3) * s.w;
+      float x0, x1, x2, x3;
+      if (A.x_vec && A.x_dtype == QS_DTYPE_F32) {
+        const float4 t = *reinterpret_cast<const float4*>(static_cast<const float*>(A.x) + xi);
+        x0 = t.x, x1 = t.y, x2 = t.z, x3 = t.w;
+      } else if (A.x_vec) {
+        const uint2 t = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(A.x) + xi);
+        if (A.x_dtype == QS_DTYPE_BF16) {
+          x0 = __uint_as_float(t.x << 16), x1 = __uint_as_float(t.x & 0xFFFF0000u);
+          x2 = __uint_as_float(t.y << 16), x3 = __uint_as_float(t.y & 0xFFFF0000u);
+        } else {
+          x0 = (float)__builtin_bit_cast(_Float16, (uint16_t)(t.x & 0xFFFFu));
+          x1 = (float)__builtin_bit_cast(_Float16, (uint16_t)(t.x >> 16));
+          x2 = (float)__builtin_bit_cast(_Float16, (uint16_t)(t.y & 0xFFFFu));
+          x3 = (float)__builtin_bit_cast(_Float16, (uint16_t)(t.y >> 16));
+        }
+      } else {
+        x0 = load_as_float(A.x, A.x_dtype, xi);
+        x1 = load_as_float(A.x, A.x_dtype, xi + 1);
+        x2 = load_as_float(A.x, A.x_dtype, xi + 2);
+        x3 = load_as_float(A.x, A.x_dtype, xi + 3);
+      }
+      v[u][0] = x0 * s.x;
+      v[u][1] = x1 * s.y;
+      v[u][2] = x2 * s.z;
+      v[u][3] = x3 * s.w;
     }
   }
 }
@@ -212,6 +173,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   const int sg = blockIdx.x / A.Gr, jr = blockIdx.x - sg * A.Gr;
   const int sl = sg * A.W + w;
   const bool active = w < A.W && sl < A.S;
+  const LaneX lx = lane_x_init();
 
   // 1. loads, in the order they are needed: tables, K, activations, codes
   float trow[8], t1row[8];
@@ -230,17 +192,6 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   load_x(A, 0, w, lane, xv);
   uint4 pre[kPrefetch];
   uint2 pre1[kPrefetch];
-#pragma unroll
-  for (int k = 0; k < kPrefetch; ++k) {
-    const int rb = jr + k * A.Gr;
-    pre[k] = make_uint4(0, 0, 0, 0);
-    pre1[k] = make_uint2(0, 0);
-    if (active && rb < RB) {
-      const size_t tile = ((size_t)rb * A.S + sl) * 64 + lane;
-      pre[k] = *reinterpret_cast<const uint4*>(A.codes0 + tile * 8);
-      if (HAS2) pre1[k] = *reinterpret_cast<const uint2*>(A.codes1 + tile * 8);
-    }
-  }
   if (tid < 256) {
     tab16[tid] = make_uint4(pack_h2(trow[0], trow[1]), pack_h2(trow[2], trow[3]), pack_h2(trow[4], trow[5]),
                             pack_h2(trow[6], trow[7]));
@@ -252,20 +203,26 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   for (int k = 0; k < 4; ++k)
     if (A.pn > 1 && tid + kThreads * k < pp) Ks[tid + kThreads * k] = kv[k];
   __syncthreads();
-  for (int e = tid; e < 4096; e += kThreads) {
-    {
-      const uint32_t H = e >> 8, a = e & 255;
+  {
+    // LUT entries e = tid + 1024 k.  hi: abs row e & 255 = tid & 255 and flip
+    // nibble H = e >> 8 = (tid >> 8) + 4 k.  lo: abs row (e >> 3) & 255 (two
+    // rows, k even / odd), f4..f6 from e & 7 = tid & 7, q = e >> 11 = k >> 1.
+    const uint4 th = tab16[tid & 255];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t H = (uint32_t)(tid >> 8) + 4u * k;
       const uint32_t f1 = (H >> 3) & 1, f2 = (H >> 2) & 1, f3 = (H >> 1) & 1;
       const uint32_t f0 = (H & 1) ^ f1 ^ f2 ^ f3;
-      const uint4 t = tab16[a];
-      lut_hi[e] = make_uint2(t.x ^ ((f0 << 15) | (f1 << 31)), t.y ^ ((f2 << 15) | (f3 << 31)));
+      lut_hi[tid + kThreads * k] = make_uint2(th.x ^ ((f0 << 15) | (f1 << 31)), th.y ^ ((f2 << 15) | (f3 << 31)));
     }
-    {
-      const uint32_t qq = e >> 11, a = (e >> 3) & 255;
-      const uint32_t f4 = (e >> 2) & 1, f5 = (e >> 1) & 1, f6 = e & 1;
-      const uint32_t f7 = qq ^ f4 ^ f5 ^ f6;
-      const uint4 t = tab16[a];
-      lut_lo[e] = make_uint2(t.z ^ ((f4 << 15) | (f5 << 31)), t.w ^ ((f6 << 15) | (f7 << 31)));
+    const uint32_t f4 = (tid >> 2) & 1, f5 = (tid >> 1) & 1, f6 = tid & 1;
+    const uint32_t m45 = (f4 << 15) | (f5 << 31), p456 = f4 ^ f5 ^ f6;
+    const uint4 ta = tab16[(tid >> 3) & 255], tb = tab16[((tid >> 3) + 128) & 255];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint4 t = (k & 1) ? tb : ta;
+      const uint32_t f7 = (uint32_t)(k >> 1) ^ p456;
+      lut_lo[tid + kThreads * k] = make_uint2(t.z ^ m45, t.w ^ ((f6 << 15) | (f7 << 31)));
     }
   }
 
@@ -281,7 +238,22 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
       for (int j = 0; j < 4; ++j) ss = __builtin_fmaf(xv[u][j], xv[u][j], ss);
     for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
     if (lane == 0) wsum[w] = ss;
-    h256(xv, lane);
+    h256_chunks(xv, A.Sn, lane, lx);
+    if (b == 0) {
+      // first code tiles (issued once the activations are in, so the
+      // activation loads do not queue behind them)
+#pragma unroll
+      for (int k = 0; k < kPrefetch; ++k) {
+        const int rb = jr + k * A.Gr;
+        pre[k] = make_uint4(0, 0, 0, 0);
+        pre1[k] = make_uint2(0, 0);
+        if (active && rb < RB) {
+          const size_t tile = ((size_t)rb * A.S + sl) * 64 + lane;
+          pre[k] = *reinterpret_cast<const uint4*>(A.codes0 + tile * 8);
+          if (HAS2) pre1[k] = *reinterpret_cast<const uint2*>(A.codes1 + tile * 8);
+        }
+      }
+    }
     if (b > 0) __syncthreads();  // the previous row's MFMAs have read Y
     store_chunks(Y, A.Sn, w, lane, xv);
     __syncthreads();  // chunks, norms (and, the first time, the LUTs) complete
@@ -325,10 +297,9 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
     for (int c = 0; c < 8; ++c) {
       const half8 hv = *reinterpret_cast<const half8*>(row + 8 * c);
       xb[c] = hv;
-      float gsum = (float)hv[0];
-#pragma unroll
-      for (int k = 1; k < 8; ++k) gsum = gsum + (float)hv[k];
-      sh[c] = (_Float16)gsum;
+      const float g01 = (float)hv[0] + (float)hv[1], g23 = (float)hv[2] + (float)hv[3];
+      const float g45 = (float)hv[4] + (float)hv[5], g67 = (float)hv[6] + (float)hv[7];
+      sh[c] = (_Float16)((g01 + g23) + (g45 + g67));
       slice_shift += (float)sh[c];
     }
     xs = __builtin_bit_cast(half8, sh);
@@ -456,7 +427,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
           }
         }
       }
-      h256(zv, lane);
+      h256_chunks(zv, A.Sm, lane, lx);
       store_chunks(Y, A.Sm, w, lane, zv);
       __syncthreads();  // chunks (and Km) complete
       const float mul = A.scale_m * A.layer_scale * (b == 0 ? emul0 : emul1);
@@ -492,10 +463,6 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   if (tid == 0) __hip_atomic_store(A.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-bool transform_fits(int64_t len, int p) {
-  return len % 256 == 0 && len <= kMaxN && (len / p) >= 256;
-}
-
 }  // namespace
 
 // Host launcher used by qs_linear_forward (qs_linear.hip).
@@ -503,10 +470,14 @@ int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, i
                         const void* codes1, const float* sv, const float* su, int pn, const float* Kn, int pm,
                         const float* Km, float s0, float s1, float layer_scale, const float* bias, void* y,
                         int y_dtype, int64_t ldy, unsigned* counter, float* xmul, float* y1p, int S, int SG, int W,
-                        int ncu, hipStream_t stream, bool* out_done) {
+                        int ncu, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop, bool* out_done) {
   FusedArgs A{};
   A.x = x;
   A.x_dtype = x_dtype;
+  {
+    const uintptr_t align = x_dtype == QS_DTYPE_F32 ? 16 : 8;
+    A.x_vec = (reinterpret_cast<uintptr_t>(x) % align) == 0 && ldx % 4 == 0;
+  }
   A.ldx = ldx;
   A.B = B;
   A.n = n;
@@ -532,7 +503,9 @@ int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, i
   A.y1p = y1p;
   A.counter = counter;
   A.xmul = xmul;
-  A.out_in_kernel = transform_fits(m, pm);
+  // in-kernel output for pure Walsh-Hadamard outputs; an odd factor runs the
+  // chunk output kernel with one work-group per output chunk instead
+  A.out_in_kernel = pm == 1 && chunk_transform_fits(m, pm);
   if (A.out_in_kernel) {
     A.Sm = m / 256;
     A.lsh_m = log2_exact(m / pm / 256);
@@ -556,9 +529,11 @@ int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, i
   }
   const unsigned grid = (unsigned)(SG * Gr);
   if (codes1)
-    hipLaunchKernelGGL(linear_fused_kernel<true>, dim3(grid), dim3(kThreads), kLdsBytes, stream, A);
+    hipExtLaunchKernelGGL(linear_fused_kernel<true>, dim3(grid), dim3(kThreads), kLdsBytes, stream, ev_start, ev_stop,
+                          0, A);
   else
-    hipLaunchKernelGGL(linear_fused_kernel<false>, dim3(grid), dim3(kThreads), kLdsBytes, stream, A);
+    hipExtLaunchKernelGGL(linear_fused_kernel<false>, dim3(grid), dim3(kThreads), kLdsBytes, stream, ev_start,
+                          ev_stop, 0, A);
   QS_LAUNCHED("linear_fused_kernel");
   *out_done = A.out_in_kernel != 0;
   return QS_OK;
@@ -566,7 +541,7 @@ int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, i
 
 bool fused_eligible(int64_t batch, int64_t n, int64_t m, int pn) {
   (void)m;
-  return batch >= 1 && batch <= kMaxB && transform_fits(n, pn);
+  return batch >= 1 && batch <= kMaxB && chunk_transform_fits(n, pn);
 }
 
 }  // namespace qs

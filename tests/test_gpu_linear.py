@@ -206,3 +206,50 @@ def test_forward_graph_replays(dev, m, n, B):
         # unrelated eager work between replays
         _ = forward_packed(x, packed, su, sv, 1.0, 0.0, 0.0135, workspace=ws)
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B", [1, 2, 5])
+def test_forward_strided_unaligned_input(dev, dtype, B):
+    """Rows with a stride that is not a multiple of 4 and a start that is not
+    8-byte aligned take the element-wise activation loads."""
+    m, n = 4096, 4096
+    rng = np.random.default_rng(40 + B)
+    codes = rng.integers(0, 65536, (m, n // 8))
+    su, sv = rng.choice([-1.0, 1.0], m), rng.choice([-1.0, 1.0], n)
+    full = torch.from_numpy(rng.standard_normal((B, n + 3)).astype(np.float32)).to(dev).to(dtype)
+    x = full[:, 1:n + 1]
+    assert x.stride(0) == n + 3 and x.data_ptr() % 8 != 0
+    y, _ = run(dev, x, codes, None, 1.0, 0.0, su, sv, 0.0135)
+    want = dense_forward(x.float().cpu().numpy(), codes, None, 1.0, 0.0, su, sv, 0.0135)
+    assert rel_err(y.float().cpu().numpy(), want) < REL_TOL
+
+
+@pytest.mark.parametrize("m,n,B", [(11008, 4096, 2), (3584, 3584, 1), (11008, 4096, 7)])
+def test_forward_odd_factor_output_bias(dev, m, n, B):
+    """Odd-factor outputs go through the chunked output kernel (one work-group
+    per output chunk), with bias."""
+    rng = np.random.default_rng(m + 3 * B)
+    codes = rng.integers(0, 65536, (m, n // 8))
+    su, sv = rng.choice([-1.0, 1.0], m), rng.choice([-1.0, 1.0], n)
+    bias = rng.standard_normal(m).astype(np.float32)
+    x = rng.standard_normal((B, n)).astype(np.float32)
+    y, _ = run(dev, x, codes, None, 1.0, 0.0, su, sv, 0.0135, bias=bias)
+    want = dense_forward(x, codes, None, 1.0, 0.0, su, sv, 0.0135, bias)
+    assert rel_err(y.cpu().numpy(), want) < REL_TOL
+
+
+@pytest.mark.parametrize("m,n", [(256, 256), (768, 512), (512, 768), (1280, 256)])
+@pytest.mark.parametrize("B", [1, 3])
+def test_forward_small_chunk_counts(dev, m, n, B):
+    """One to five 256-chunks per side (768 = 3 x 256 and 1280 = 5 x 256 take
+    the odd-factor stage), single-launch and batched paths."""
+    rng = np.random.default_rng(m * 5 + n + B)
+    codes = rng.integers(0, 65536, (m, n // 8))
+    su, sv = rng.choice([-1.0, 1.0], m), rng.choice([-1.0, 1.0], n)
+    bias = rng.standard_normal(m).astype(np.float32)
+    x = rng.standard_normal((B, n)).astype(np.float32)
+    y, packed = run(dev, x, codes, None, 1.0, 0.0, su, sv, 0.02, bias=bias)
+    assert packed.layout == 1
+    want = dense_forward(x, codes, None, 1.0, 0.0, su, sv, 0.02, bias)
+    assert rel_err(y.cpu().numpy(), want) < REL_TOL
