@@ -9,7 +9,10 @@ are random uint16 from a seeded generator with an fp16 per-layer scale and
 seeded RHT signs; the 11008-wide dims use the Kronecker transform (43 x 256).
 A step is one pass through the 224 linears in dependency order (q/k/v read
 the layer input, o reads q, gate/up read o, down reads gate, the next layer
-reads down), replayed from a HIP graph.
+reads down), replayed from a HIP graph.  By default the linears that share an
+input run as one grouped launch (q/k/v, gate/up: qs_linear_forward_group), 4
+launches per layer; --per-linear makes the headline one qs_linear_forward per
+linear (7 per layer), and the other pattern is always reported alongside.
 
 Also reported: quantize s/layer for a 4096x4096 layer (E8P 2-bit
 BlockLDLQ with 10 refinement sweeps) and the reference's CPU path timed on
@@ -42,6 +45,10 @@ def parse():
     p.add_argument("--skip-quantize", action="store_true")
     p.add_argument("--skip-cpu", action="store_true")
     p.add_argument("--skip-batch16", action="store_true")
+    p.add_argument("--skip-alt", action="store_true", help="do not time the other call pattern")
+    p.add_argument("--per-linear", action="store_true",
+                   help="headline with one qs_linear_forward call per linear (the reference's call pattern) "
+                        "instead of grouped launches for linears that share an input")
     p.add_argument("--probe", action="store_true",
                    help="hardware-counter probe: one eager step over a 2-layer stack, then a 256 MiB "
                         "elementwise scale (reads and writes 256 MiB) for calibrating byte counters")
@@ -113,37 +120,79 @@ class Stack:
         return sum(p[0].nbytes() for lin in self.layers for p in lin.values())
 
 
-class Runner:
-    """Issues the step's 224 linear calls through the C ABI with preallocated
-    buffers, so the step can be captured in a HIP graph."""
+GROUPS = [("q", "k", "v"), ("o",), ("gate", "up"), ("down",)]   # linears of one launch, per layer
+SOURCE = {"q": None, "k": None, "v": None, "o": "q", "gate": "o", "up": "o", "down": "gate"}
+SHAPE = {name: (m, n) for name, m, n in LLAMA2_7B}
 
-    def __init__(self, stack, B):
+
+def launch_bytes(names, B):
+    """Algorithmic bytes of one launch of the linears `names` (one shared input)."""
+    m0, n = SHAPE[names[0]]
+    return sum(linear_bytes(*SHAPE[k], B) for k in names) - (len(names) - 1) * 2 * B * n
+
+
+class Runner:
+    """Issues one step through the C ABI with preallocated buffers, so it can
+    be captured in a HIP graph.  grouped=True launches the linears that share
+    an input together (qs_linear_forward_group: q/k/v, gate/up); otherwise one
+    qs_linear_forward per linear (the reference's call pattern)."""
+
+    def __init__(self, stack, B, grouped=True):
+        import ctypes
         import torch
         from quipsharp_amd import _lib
         from quipsharp_amd.hadamard import hartley_matrix
         self.stack, self.B = stack, B
+        self.grouped = grouped and B <= 2
         dev = stack.dev
         self.lib = _lib.lib()
         self._lib = _lib
         g = torch.Generator(device=dev).manual_seed(1)
         self.x = torch.randn(B, 4096, generator=g, device=dev).bfloat16()
         self.buf = {k: torch.empty(B, m, dtype=torch.bfloat16, device=dev) for k, m, _ in LLAMA2_7B}
-        ws = max(self.lib.qs_linear_workspace_bytes(m, n, B, _lib.QS_LAYOUT_TILED) for _, m, n in LLAMA2_7B)
-        self.ws = torch.zeros(ws, dtype=torch.uint8, device=dev)  # counter region must start at zero
         self.K43 = hartley_matrix(43, dev)
-        self.src = {"q": None, "k": None, "v": None, "o": "q", "gate": "o", "up": "o", "down": "gate"}
+        self.plan = GROUPS if self.grouped else [(name,) for name, _, _ in LLAMA2_7B]
+        if self.grouped:
+            ws = 0
+            for names in self.plan:
+                ms = (ctypes.c_int64 * len(names))(*[SHAPE[k][0] for k in names])
+                ws = max(ws, self.lib.qs_linear_group_workspace_bytes(SHAPE[names[0]][1], B, len(names), ms))
+        else:
+            ws = max(self.lib.qs_linear_workspace_bytes(m, n, B, _lib.QS_LAYOUT_TILED) for _, m, n in LLAMA2_7B)
+        self.ws = torch.zeros(ws, dtype=torch.uint8, device=dev)  # counter regions must start at zero
+        # per (layer, launch): the ctypes job array, built once
+        self.jobs = []
+        for lin in stack.layers:
+            per = []
+            for names in self.plan:
+                arr = (_lib.LinearJob * len(names))()
+                for j, k in enumerate(names):
+                    packed, su, sv, scale = lin[k]
+                    m = SHAPE[k][0]
+                    km = 43 if m == 11008 else 1
+                    arr[j] = _lib.LinearJob(packed.codes0.data_ptr(), None, m, su.data_ptr(), sv.data_ptr(), km,
+                                            self.K43.data_ptr() if km > 1 else None, 1.0, 0.0, scale, None,
+                                            self.buf[k].data_ptr(), m)
+                per.append(arr)
+            self.jobs.append(per)
 
-    def _call(self, x, lin, out, m, n, stream, events):
+    def _launch(self, li, gi, names, x, stream, events):
         L, _lib = self.lib, self._lib
-        packed, su, sv, scale = lin
+        n = SHAPE[names[0]][1]
         kn = 43 if n == 11008 else 1
-        km = 43 if m == 11008 else 1
-        rc = L.qs_linear_forward(
-            x.data_ptr(), _lib.QS_DTYPE_BF16, n, self.B, n, m, packed.codes0.data_ptr(), None, 0, packed.layout,
-            sv.data_ptr(), su.data_ptr(), kn, self.K43.data_ptr() if kn > 1 else None, km,
-            self.K43.data_ptr() if km > 1 else None, 1.0, 0.0, scale, None, out.data_ptr(), _lib.QS_DTYPE_BF16, m,
-            self.ws.data_ptr(), self.ws.numel(), events[0] if events else None, events[1] if events else None,
-            stream)
+        Kn = self.K43.data_ptr() if kn > 1 else None
+        e0, e1 = (events[0], events[1]) if events else (None, None)
+        if self.grouped:
+            rc = L.qs_linear_forward_group(x.data_ptr(), _lib.QS_DTYPE_BF16, n, self.B, n, kn, Kn, len(names),
+                                           self.jobs[li][gi], _lib.QS_DTYPE_BF16, self.ws.data_ptr(), self.ws.numel(),
+                                           e0, e1, stream)
+        else:
+            j = self.jobs[li][gi][0]
+            m = j.m
+            rc = L.qs_linear_forward(
+                x.data_ptr(), _lib.QS_DTYPE_BF16, n, self.B, n, m, j.codes0, None, 0, _lib.QS_LAYOUT_TILED, j.sv, j.su,
+                kn, Kn, j.kron_pm, j.kron_m, 1.0, 0.0, j.layer_scale, None, j.y, _lib.QS_DTYPE_BF16, m,
+                self.ws.data_ptr(), self.ws.numel(), e0, e1, stream)
         if rc:
             _lib.check(rc)
 
@@ -152,24 +201,27 @@ class Runner:
         stream = torch.cuda.current_stream(self.stack.dev).cuda_stream
         x = self.x
         ei = 0
-        for lin in self.stack.layers:
-            for name, m, n in LLAMA2_7B:
-                src = x if self.src[name] is None else self.buf[self.src[name]]
+        for li in range(len(self.stack.layers)):
+            for gi, names in enumerate(self.plan):
+                src = x if SOURCE[names[0]] is None else self.buf[SOURCE[names[0]]]
                 ev = None
                 if events is not None:
                     ev = events[ei]
                     ei += 1
-                self._call(src, lin[name], self.buf[name], m, n, stream, ev)
+                self._launch(li, gi, names, src, stream, ev)
             x = self.buf["down"]
         return self.buf["down"]
 
     def launches_per_step(self):
-        return len(self.stack.layers) * len(LLAMA2_7B)
+        return len(self.stack.layers) * len(self.plan)
 
     def bytes_per_step(self):
         return len(self.stack.layers) * sum(linear_bytes(m, n, self.B) for _, m, n in LLAMA2_7B)
 
     def mv_bytes_per_step(self):
+        """Algorithmic bytes of the step's decode-matvec launches."""
+        if self.B <= 2:
+            return len(self.stack.layers) * sum(launch_bytes(names, self.B) for names in self.plan)
         return len(self.stack.layers) * sum(mv_bytes(m, n, self.B) for _, m, n in LLAMA2_7B)
 
 
@@ -343,15 +395,27 @@ def main():
     stack = Stack(args.layers, dev)
     log(f"stack: {args.layers} layers, {stack.code_bytes() / 1e9:.2f} GB of codes, "
         f"setup {time.perf_counter() - t_setup:.1f}s")
-    r1 = Runner(stack, 1)
+    r1 = Runner(stack, 1, grouped=not args.per_linear)
     ms = time_graph(r1, args.steps, args.warmup)
     mv_ms = time_mv_kernels(r1)
     bps = r1.bytes_per_step()
     value = bps / (ms * 1e-3) / 1e9
     mv_avg_bytes = r1.mv_bytes_per_step() / r1.launches_per_step()
     achieved = mv_avg_bytes / (mv_ms * 1e-3) / 1e9
-    log(f"batch 1: {ms:.3f} ms/step, {value:.1f} GB/s, mv kernel avg {mv_ms * 1e3:.2f} us -> {achieved:.1f} GB/s")
+    log(f"batch 1 ({'grouped' if r1.grouped else 'per-linear'}): {ms:.3f} ms/step, {value:.1f} GB/s, "
+        f"mv kernel avg {mv_ms * 1e3:.2f} us -> {achieved:.1f} GB/s")
     extra = {}
+    if not args.skip_alt:
+        # the other call pattern, for comparison
+        r_alt = Runner(stack, 1, grouped=args.per_linear)
+        ms_alt = time_graph(r_alt, args.steps, args.warmup)
+        mv_alt = time_mv_kernels(r_alt, passes=1)
+        extra["grouped" if r_alt.grouped else "per_linear"] = {
+            "ms_per_step": round(ms_alt, 4), "GBps": round(bps / ms_alt / 1e6, 1), "tok_per_s": round(1e3 / ms_alt, 1),
+            "launches_per_step": r_alt.launches_per_step(), "mv_kernel_avg_us": round(mv_alt * 1e3, 3),
+            "mv_kernel_GBps": round(r_alt.mv_bytes_per_step() / r_alt.launches_per_step() / (mv_alt * 1e-3) / 1e9, 1)}
+        log(f"batch 1 ({'grouped' if r_alt.grouped else 'per-linear'}): {ms_alt:.3f} ms/step")
+        del r_alt
     if not args.skip_batch16:
         r16 = Runner(stack, 16)
         ms16 = time_graph(r16, max(args.steps // 2, 1), args.warmup)
@@ -385,13 +449,16 @@ def main():
         "dtype": "e8p-2bit codes, fp16 x fp16 -> fp32 accumulate (bf16 in/out)", "data": "synthetic",
         "config": {"workload": "Llama-2-7B quantized-linear stack (q,k,v,o 4096x4096; gate,up 11008x4096; "
                                "down 4096x11008) x %d decoder layers, E8P 2-bit random codes, batch 1" % args.layers,
-                   "global_batch": 1, "layers": args.layers, "linears_per_step": r1.launches_per_step(),
+                   "global_batch": 1, "layers": args.layers, "linears_per_step": 7 * args.layers,
+                   "launches_per_step": r1.launches_per_step(),
+                   "call_pattern": "grouped (q/k/v and gate/up share a launch)" if r1.grouped else
+                                   "one qs_linear_forward per linear",
                    "code_bytes": stack.code_bytes(), "parallelism": "none (1 GPU)"},
         "tok_per_s": round(1e3 / ms, 1), "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "kernel": MV_KERNEL[True], "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "avg_launch_us": round(mv_ms * 1e3, 3), "bytes_per_launch": int(mv_avg_bytes),
-                     "traffic": measured_traffic() if args.layers == 32 else None},
+                     "traffic": measured_traffic() if args.layers == 32 and r1.grouped else None},
         "cpu_baseline": cpu,
     }
     line.update(extra)

@@ -43,6 +43,7 @@ enum { QS_LAYOUT_ROWMAJOR = 0, QS_LAYOUT_TILED = 1 };     /* packed-code layouts
 #define QS_ABI_VERSION 1
 #define QS_MAX_STAGES 4
 #define QS_MAX_KRON 64 /* largest odd factor of a Kronecker transform */
+#define QS_MAX_GROUP 4 /* linears per qs_linear_forward_group call */
 
 /* Message of the last failed call on this thread ("" if none). */
 const char *qs_last_error(void);
@@ -164,6 +165,40 @@ int qs_linear_forward(const void *x, int x_dtype, int64_t ldx, int64_t batch, in
                       const float *kron_m, float s0, float s1, float layer_scale,
                       const float *bias, void *y, int y_dtype, int64_t ldy, void *workspace,
                       size_t workspace_bytes, void *mv_begin, void *mv_end, qs_stream_t stream);
+
+/* One linear of a grouped forward (all linears of a group share x and n). */
+typedef struct qs_linear_job {
+  const void *codes0;   /* packed E8P codes, QS_LAYOUT_TILED */
+  const void *codes1;   /* packed E8 1-bit codes or NULL (the same for every job of a call) */
+  int64_t m;
+  const float *su, *sv; /* [m], [n] fp32 signs */
+  int kron_pm;          /* odd factor of m; kron_m its p x p matrix (NULL when 1) */
+  const float *kron_m;
+  float s0, s1, layer_scale;
+  const float *bias;    /* [m] fp32 or NULL */
+  void *y;              /* [batch][ldy] in the call's y_dtype */
+  int64_t ldy;
+} qs_linear_job;
+
+/* Workspace bytes for qs_linear_forward_group: ms[count] output sizes. */
+size_t qs_linear_group_workspace_bytes(int64_t n, int64_t batch, int count, const int64_t *ms);
+
+/* Several linears that read the same input x in one launch: for each job,
+ * y_j = su_j (.) T_m( layer_scale_j * W_hat_j @ T_n(sv_j (.) x) ) + bias_j, the
+ * same as qs_linear_forward per job, with the GPU's work-groups shared between
+ * the jobs in proportion to m, so their latency chains overlap (q/k/v and
+ * gate/up of a decoder layer).  No counterpart in the reference, whose
+ * QuantizedLinear.forward (quipsharp/checkpoint.py:141-146) is one linear per
+ * call; callers that own several linears of one input use it.
+ * Requirements: 1 <= count <= QS_MAX_GROUP, batch <= 2, tiled layout, n a
+ * multiple of 256 with n <= 12288 and n / kron_pn >= 256, codes1 NULL for all
+ * jobs or for none.  The workspace (zero before first use, see
+ * qs_linear_forward) holds one region per job.  mv_begin / mv_end bracket the
+ * single decode-matvec kernel as in qs_linear_forward. */
+int qs_linear_forward_group(const void *x, int x_dtype, int64_t ldx, int64_t batch, int64_t n, int kron_pn,
+                            const float *kron_n, int count, const qs_linear_job *jobs, int y_dtype,
+                            void *workspace, size_t workspace_bytes, void *mv_begin, void *mv_end,
+                            qs_stream_t stream);
 
 /* Measurement helper: enqueue a kernel that keeps `stream` busy for about
  * `nanoseconds` (bounded; at most 1 s), so that work enqueued after it runs

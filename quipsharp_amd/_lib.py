@@ -19,8 +19,19 @@ QS_DTYPE_F32, QS_DTYPE_F16, QS_DTYPE_BF16 = 0, 1, 2
 QS_LAYOUT_ROWMAJOR, QS_LAYOUT_TILED = 0, 1
 QS_MAX_STAGES = 4
 QS_MAX_KRON = 64
+QS_MAX_GROUP = 4
 
 _vp = ctypes.c_void_p
+
+
+class LinearJob(ctypes.Structure):
+    """qs_linear_job (include/quipsharp_hip.h)."""
+    _fields_ = [("codes0", ctypes.c_void_p), ("codes1", ctypes.c_void_p), ("m", ctypes.c_int64),
+                ("su", ctypes.c_void_p), ("sv", ctypes.c_void_p), ("kron_pm", ctypes.c_int),
+                ("kron_m", ctypes.c_void_p), ("s0", ctypes.c_float), ("s1", ctypes.c_float),
+                ("layer_scale", ctypes.c_float), ("bias", ctypes.c_void_p), ("y", ctypes.c_void_p),
+                ("ldy", ctypes.c_int64)]
+
 _i64 = ctypes.c_int64
 _int = ctypes.c_int
 _f32 = ctypes.c_float
@@ -44,6 +55,9 @@ _SIGNATURES = {
     "qs_linear_forward": ([_vp, _int, _i64, _i64, _i64, _i64, _vp, _vp, _int, _int, _vp, _vp, _int, _vp,
                            _int, _vp, _f32, _f32, _f32, _vp, _vp, _int, _i64, _vp, ctypes.c_size_t, _vp, _vp,
                            _vp], _int),
+    "qs_linear_group_workspace_bytes": ([_i64, _i64, _int, ctypes.POINTER(ctypes.c_int64)], ctypes.c_size_t),
+    "qs_linear_forward_group": ([_vp, _int, _i64, _i64, _i64, _int, _vp, _int, ctypes.POINTER(LinearJob), _int,
+                                 _vp, ctypes.c_size_t, _vp, _vp, _vp], _int),
     "qs_busy_wait": ([_i64, _vp], _int),
 }
 

@@ -111,6 +111,40 @@ __device__ __forceinline__ float mmat(int r, int c, int lsh, int p, const float*
   return v;
 }
 
+// Row r of M . Y for the four columns 4 lane .. 4 lane + 3: sum over the S
+// chunks c of M[r][c] Y[c][4 lane + j].  r is the same for the whole wave, so
+// the coefficients are scalars: the Hadamard sign from a scalar popcount and
+// the K factor read once per lane (K[r's a][lane], p <= 64) and broadcast with
+// readlane.  Four chunks per step, loads first.
+__device__ __forceinline__ float4 mrow_times_chunks(const float* Y, int S, int r, int lsh, int p, const float* Ks,
+                                                    int lane) {
+  r = __builtin_amdgcn_readfirstlane(r);
+  const int hm = (1 << lsh) - 1;
+  const float krow = (p > 1 && lane < p) ? Ks[(r >> lsh) * p + lane] : 1.0f;
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (int c0 = 0; c0 < S; c0 += 4) {
+    float4 yv[4];
+    float cf[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int c = c0 + k < S ? c0 + k : S - 1;
+      yv[k] = *reinterpret_cast<const float4*>(Y + c * kYStride + 4 * lane);
+      float v = (__builtin_popcount(r & c & hm) & 1) ? -1.0f : 1.0f;
+      if (p > 1)
+        v *= __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, krow), c >> lsh));
+      cf[k] = c0 + k < S ? v : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      acc.x = __builtin_fmaf(cf[k], yv[k].x, acc.x);
+      acc.y = __builtin_fmaf(cf[k], yv[k].y, acc.y);
+      acc.z = __builtin_fmaf(cf[k], yv[k].z, acc.z);
+      acc.w = __builtin_fmaf(cf[k], yv[k].w, acc.w);
+    }
+  }
+  return acc;
+}
+
 // True when a length-len transform with odd factor p fits the chunk scheme.
 inline bool chunk_transform_fits(int64_t len, int p) {
   return len % 256 == 0 && len <= kMaxN && (len / p) >= 256;

@@ -23,15 +23,9 @@
 #include <hip/hip_ext.h>
 
 #include "qs_chunk_dev.h"
+#include "qs_linear_dev.h"
 
 namespace qs {
-
-int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, int m, const void* codes0,
-                        const void* codes1, const float* sv, const float* su, int pn, const float* Kn, int pm,
-                        const float* Km, float s0, float s1, float layer_scale, const float* bias, void* y,
-                        int y_dtype, int64_t ldy, unsigned* counter, float* xmul, float* y1p, int S, int SG, int W,
-                        int ncu, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop, bool* out_done);
-bool fused_eligible(int64_t batch, int64_t n, int64_t m, int pn);
 
 namespace {
 
@@ -553,12 +547,26 @@ struct YcArgs {
   int64_t ldy;
 };
 
-__global__ __launch_bounds__(kRowThreads) void yout_chunk_kernel(YcArgs A) {
+// Up to QS_MAX_GROUP output transforms in one launch; job g owns the
+// work-groups [wg0[g], wg0[g] + B * Sm_g).
+struct YcGroup {
+  int njobs;
+  int wg0[QS_MAX_GROUP];
+  YcArgs job[QS_MAX_GROUP];
+};
+
+__global__ __launch_bounds__(kRowThreads) void yout_chunk_kernel(YcGroup G) {
   extern __shared__ __attribute__((aligned(16))) float smc[];
+  int g = 0;
+#pragma unroll
+  for (int k = 1; k < QS_MAX_GROUP; ++k)
+    if (k < G.njobs && (int)blockIdx.x >= G.wg0[k]) g = k;
+  const YcArgs& A = G.job[g];
+  const int lb = (int)blockIdx.x - G.wg0[g];
   float* Y = smc;                                   // Sm x kYStride, at least 1024 floats
   float* Ks = smc + yc_rows_floats(A.Sm);           // p x p
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int b = blockIdx.x / A.Sm, a = blockIdx.x - b * A.Sm;
+  const int b = lb / A.Sm, a = lb - b * A.Sm;
   const LaneX lx = lane_x_init();
   float xt = 0.0f;
   if (A.xtot)
@@ -625,10 +633,11 @@ int set_lds(const void* fn, size_t bytes, int* done) {
 }
 int g_xin_lds = 0, g_yout_lds = 0;
 
-// Launches yout_chunk_kernel (m a multiple of 256, m <= kMaxN, m / p >= 256).
-int launch_yout_chunk(const float* y1p, int SG, int B, int64_t m, int p, const float* K, const float* xtot,
-                      int xparts, const float* xmul, float s0, float layer_scale, const float* su,
-                      const float* bias, void* y, int y_dtype, int64_t ldy, hipStream_t s) {
+// Fills one job of yout_chunk_kernel (m a multiple of 256, m <= kMaxN,
+// m / p >= 256).
+YcArgs yc_args(const float* y1p, int SG, int B, int64_t m, int p, const float* K, const float* xtot, int xparts,
+               const float* xmul, float s0, float layer_scale, const float* su, const float* bias, void* y,
+               int y_dtype, int64_t ldy) {
   YcArgs A{};
   A.y1p = y1p;
   A.SG = SG;
@@ -649,10 +658,66 @@ int launch_yout_chunk(const float* y1p, int SG, int B, int64_t m, int p, const f
   A.y = y;
   A.y_dtype = y_dtype;
   A.ldy = ldy;
-  const size_t lds = ((size_t)yc_rows_floats(A.Sm) + (size_t)p * p) * 4;
+  return A;
+}
+
+int launch_yout_chunk_group(int count, const YcArgs* jobs, hipStream_t s) {
+  YcGroup G{};
+  G.njobs = count;
+  int wg = 0;
+  size_t lds = 0;
+  for (int g = 0; g < count; ++g) {
+    G.job[g] = jobs[g];
+    G.wg0[g] = wg;
+    wg += jobs[g].B * jobs[g].Sm;
+    const size_t need = ((size_t)yc_rows_floats(jobs[g].Sm) + (size_t)jobs[g].p * jobs[g].p) * 4;
+    if (need > lds) lds = need;
+  }
   QS_REQUIRE(lds <= 65536, "chunk output transform: %zu bytes of LDS", lds);
-  hipLaunchKernelGGL(yout_chunk_kernel, dim3((unsigned)(B * A.Sm)), dim3(kRowThreads), lds, s, A);
+  hipLaunchKernelGGL(yout_chunk_kernel, dim3((unsigned)wg), dim3(kRowThreads), lds, s, G);
   QS_LAUNCHED("yout_chunk_kernel");
+  return QS_OK;
+}
+
+int launch_yout_chunk(const float* y1p, int SG, int B, int64_t m, int p, const float* K, const float* xtot,
+                      int xparts, const float* xmul, float s0, float layer_scale, const float* su,
+                      const float* bias, void* y, int y_dtype, int64_t ldy, hipStream_t s) {
+  const YcArgs A = yc_args(y1p, SG, B, m, p, K, xtot, xparts, xmul, s0, layer_scale, su, bias, y, y_dtype, ldy);
+  return launch_yout_chunk_group(1, &A, s);
+}
+
+// Output transform with the older whole-row kernel (outputs the chunk scheme
+// does not cover: m not a multiple of 256, or larger than kMaxN).
+int launch_yout_rows(const float* y1p, int SG, int B, int64_t m, int p, const float* K, const float* xtot,
+                     int xparts, const float* xmul, float s0, float layer_scale, const float* su, const float* bias,
+                     void* y, int y_dtype, int64_t ldy, hipStream_t s) {
+  const int L = (int)(m / p);
+  const size_t lds = ((size_t)padded_len((int)m) + (size_t)p * p) * 4;
+  const int G = parts_for(m, p);
+  int rc = set_lds((const void*)yout_kernel, lds, &g_yout_lds);
+  if (rc) return rc;
+  YoutArgs YA{};
+  YA.y1p = y1p;
+  YA.SG = SG;
+  YA.B = B;
+  YA.m = (int)m;
+  YA.logL = log2_exact(L);
+  YA.p = p;
+  YA.G = G;
+  YA.K = K;
+  YA.scale = inv_sqrt_len(L);
+  YA.xtot = xtot;
+  YA.xparts = xparts;
+  YA.xmul = xmul;
+  YA.s0 = s0;
+  YA.layer_scale = layer_scale;
+  YA.su = su;
+  YA.bias = bias;
+  YA.y = y;
+  YA.y_dtype = y_dtype;
+  YA.ldy = ldy;
+  hipLaunchKernelGGL(yout_kernel, dim3((unsigned)(B * G)), dim3(kRowThreads), lds, s, YA);
+  QS_LAUNCHED("yout_kernel");
   return QS_OK;
 }
 
@@ -736,55 +801,37 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
   char* ws = static_cast<char*>(workspace);
   if (layout == QS_LAYOUT_TILED && fused_eligible(batch, n, m, kron_pn) &&
       (reinterpret_cast<uintptr_t>(sv) & 15) == 0) {
-    float* y1p = reinterpret_cast<float*>(ws + W.y1p);
-    float* xmul = reinterpret_cast<float*>(ws + W.xmul);
-    bool done = false;
-    rc = launch_linear_fused(x, x_dtype, ldx, (int)batch, (int)n, (int)m, codes0, codes1, sv, su, kron_pn, kron_n,
-                             kron_pm, kron_m, s0, s1, layer_scale, bias, y, y_dtype, ldy,
-                             reinterpret_cast<unsigned*>(ws), xmul, y1p, W.S, W.SG, W.W, cu_count(), s,
-                             reinterpret_cast<hipEvent_t>(mv_begin), reinterpret_cast<hipEvent_t>(mv_end), &done);
+    FusedJobDesc d{};
+    d.codes0 = codes0;
+    d.codes1 = codes1;
+    d.m = m;
+    d.sv = sv;
+    d.su = su;
+    d.pm = kron_pm;
+    d.s0 = s0;
+    d.s1 = s1;
+    d.layer_scale = layer_scale;
+    d.bias = bias;
+    d.y = y;
+    d.ldy = ldy;
+    d.counter = reinterpret_cast<unsigned*>(ws);
+    d.xmul = reinterpret_cast<float*>(ws + W.xmul);
+    d.y1p = reinterpret_cast<float*>(ws + W.y1p);
+    rc = launch_linear_fused(x, x_dtype, ldx, (int)batch, (int)n, kron_pn, kron_n, y_dtype, 1, &d, W.S, W.SG, W.W,
+                             cu_count(), s, reinterpret_cast<hipEvent_t>(mv_begin),
+                             reinterpret_cast<hipEvent_t>(mv_end));
     if (rc) return rc;
-    if (!done && chunk_transform_fits(m, kron_pm))
-      return launch_yout_chunk(y1p, W.SG, (int)batch, m, kron_pm, kron_m, nullptr, 0, xmul, s0, layer_scale, su,
+    if (fused_output_in_kernel(m, kron_pm)) return QS_OK;
+    if (chunk_transform_fits(m, kron_pm))
+      return launch_yout_chunk(d.y1p, W.SG, (int)batch, m, kron_pm, kron_m, nullptr, 0, d.xmul, s0, layer_scale, su,
                                bias, y, y_dtype, ldy, s);
-    if (!done) {
-      const int Lm = (int)(m / kron_pm);
-      const size_t yout_lds = ((size_t)padded_len((int)m) + (size_t)kron_pm * kron_pm) * 4;
-      const int Gy = parts_for(m, kron_pm);
-      rc = set_lds((const void*)yout_kernel, yout_lds, &g_yout_lds);
-      if (rc) return rc;
-      YoutArgs YA{};
-      YA.y1p = y1p;
-      YA.SG = W.SG;
-      YA.B = (int)batch;
-      YA.m = (int)m;
-      YA.logL = log2_exact(Lm);
-      YA.p = kron_pm;
-      YA.G = Gy;
-      YA.K = kron_m;
-      YA.scale = inv_sqrt_len(Lm);
-      YA.xtot = nullptr;
-      YA.xparts = 0;
-      YA.xmul = xmul;
-      YA.s0 = s0;
-      YA.layer_scale = layer_scale;
-      YA.su = su;
-      YA.bias = bias;
-      YA.y = y;
-      YA.y_dtype = y_dtype;
-      YA.ldy = ldy;
-      hipLaunchKernelGGL(yout_kernel, dim3((unsigned)(batch * Gy)), dim3(kRowThreads), yout_lds, s, YA);
-      QS_LAUNCHED("yout_kernel");
-    }
-    return QS_OK;
+    return launch_yout_rows(d.y1p, W.SG, (int)batch, m, kron_pm, kron_m, nullptr, 0, d.xmul, s0, layer_scale, su,
+                            bias, y, y_dtype, ldy, s);
   }
-  const int Ln = (int)(n / kron_pn), Lm = (int)(m / kron_pm);
+  const int Ln = (int)(n / kron_pn);
   const size_t xin_lds = ((size_t)padded_len((int)n) + (size_t)kron_pn * kron_pn) * 4;
-  const size_t yout_lds = ((size_t)padded_len((int)m) + (size_t)kron_pm * kron_pm) * 4;
-  const int Gx = parts_for(n, kron_pn), Gy = parts_for(m, kron_pm);
+  const int Gx = parts_for(n, kron_pn);
   rc = set_lds((const void*)xin_kernel, xin_lds, &g_xin_lds);
-  if (rc) return rc;
-  rc = set_lds((const void*)yout_kernel, yout_lds, &g_yout_lds);
   if (rc) return rc;
 
   for (int64_t b0 = 0; b0 < batch; b0 += kMaxTileBatch) {
@@ -853,35 +900,107 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
       QS_LAUNCHED("mv_generic_kernel");
     }
 
-    if (chunk_transform_fits(m, kron_pm)) {
-      rc = launch_yout_chunk(y1p, W.SG, B, m, kron_pm, kron_m, layout == QS_LAYOUT_TILED ? XA.xtot : nullptr, Gx,
-                             layout == QS_LAYOUT_TILED ? XA.xmul : nullptr, s0, layer_scale, su, bias, yb, y_dtype,
+    const float* xtot = layout == QS_LAYOUT_TILED ? XA.xtot : nullptr;
+    const float* xmul = layout == QS_LAYOUT_TILED ? XA.xmul : nullptr;
+    if (chunk_transform_fits(m, kron_pm))
+      rc = launch_yout_chunk(y1p, W.SG, B, m, kron_pm, kron_m, xtot, Gx, xmul, s0, layer_scale, su, bias, yb, y_dtype,
                              ldy, s);
-      if (rc) return rc;
-      continue;
-    }
-    YoutArgs YA{};
-    YA.y1p = y1p;
-    YA.SG = W.SG;
-    YA.B = B;
-    YA.m = (int)m;
-    YA.logL = log2_exact(Lm);
-    YA.p = kron_pm;
-    YA.G = Gy;
-    YA.xparts = Gx;
-    YA.K = kron_m;
-    YA.scale = inv_sqrt_len(Lm);
-    YA.xtot = layout == QS_LAYOUT_TILED ? XA.xtot : nullptr;
-    YA.xmul = layout == QS_LAYOUT_TILED ? XA.xmul : nullptr;
-    YA.s0 = s0;
-    YA.layer_scale = layer_scale;
-    YA.su = su;
-    YA.bias = bias;
-    YA.y = yb;
-    YA.y_dtype = y_dtype;
-    YA.ldy = ldy;
-    hipLaunchKernelGGL(yout_kernel, dim3(B * Gy), dim3(kRowThreads), yout_lds, s, YA);
-    QS_LAUNCHED("yout_kernel");
+    else
+      rc = launch_yout_rows(y1p, W.SG, B, m, kron_pm, kron_m, xtot, Gx, xmul, s0, layer_scale, su, bias, yb, y_dtype,
+                            ldy, s);
+    if (rc) return rc;
   }
+  return QS_OK;
+}
+
+extern "C" size_t qs_linear_group_workspace_bytes(int64_t n, int64_t batch, int count, const int64_t* ms) {
+  if (n <= 0 || batch <= 0 || count < 1 || count > QS_MAX_GROUP || !ms) return 0;
+  size_t total = 0;
+  for (int g = 0; g < count; ++g) {
+    if (ms[g] <= 0) return 0;
+    total += ws_layout(ms[g], n, batch, QS_LAYOUT_TILED).total;
+  }
+  return total;
+}
+
+extern "C" int qs_linear_forward_group(const void* x, int x_dtype, int64_t ldx, int64_t batch, int64_t n,
+                                       int kron_pn, const float* kron_n, int count, const qs_linear_job* jobs,
+                                       int y_dtype, void* workspace, size_t workspace_bytes, void* mv_begin,
+                                       void* mv_end, qs_stream_t stream) {
+  QS_REQUIRE(count >= 1 && count <= QS_MAX_GROUP, "count must be in [1, %d]", QS_MAX_GROUP);
+  QS_REQUIRE(jobs && x && workspace, "null pointer");
+  QS_REQUIRE(x_dtype >= QS_DTYPE_F32 && x_dtype <= QS_DTYPE_BF16 && y_dtype >= QS_DTYPE_F32 &&
+                 y_dtype <= QS_DTYPE_BF16,
+             "bad dtype");
+  QS_REQUIRE(batch >= 0 && n > 0 && ldx >= n, "bad shape batch=%lld n=%lld", (long long)batch, (long long)n);
+  if (batch == 0) return QS_OK;
+  int rc = check_transform(n, kron_pn, kron_n, "input");
+  if (rc) return rc;
+  QS_REQUIRE(batch <= 2 && chunk_transform_fits(n, kron_pn),
+             "grouped forward needs batch <= 2 and n a multiple of 256 with n <= %d (got batch %lld, n %lld)", kMaxN,
+             (long long)batch, (long long)n);
+  QS_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255) == 0, "workspace must be 256-byte aligned");
+  size_t need = 0;
+  for (int g = 0; g < count; ++g) {
+    const qs_linear_job& j = jobs[g];
+    QS_REQUIRE(j.codes0 && j.su && j.sv && j.y, "job %d: null pointer", g);
+    QS_REQUIRE(j.m > 0 && j.m % 16 == 0 && j.ldy >= j.m, "job %d: bad m %lld / ldy", g, (long long)j.m);
+    rc = check_transform(j.m, j.kron_pm, j.kron_m, "output");
+    if (rc) return rc;
+    QS_REQUIRE((reinterpret_cast<uintptr_t>(j.codes0) & 15) == 0 &&
+                   (!j.codes1 || (reinterpret_cast<uintptr_t>(j.codes1) & 7) == 0) &&
+                   (reinterpret_cast<uintptr_t>(j.sv) & 15) == 0,
+               "job %d: packed codes and sv must be 16-byte aligned", g);
+    QS_REQUIRE((j.codes1 != nullptr) == (jobs[0].codes1 != nullptr), "all jobs need the same number of stages");
+    need += ws_layout(j.m, n, batch, QS_LAYOUT_TILED).total;
+  }
+  QS_REQUIRE(workspace_bytes >= need, "workspace too small: %zu < %zu", workspace_bytes, need);
+  hipStream_t s = as_stream(stream);
+  char* ws = static_cast<char*>(workspace);
+  FusedJobDesc d[QS_MAX_GROUP];
+  WsLayout W0{};
+  size_t off = 0;
+  for (int g = 0; g < count; ++g) {
+    const qs_linear_job& j = jobs[g];
+    const WsLayout W = ws_layout(j.m, n, batch, QS_LAYOUT_TILED);
+    if (g == 0) W0 = W;
+    d[g] = FusedJobDesc{};
+    d[g].codes0 = j.codes0;
+    d[g].codes1 = j.codes1;
+    d[g].m = j.m;
+    d[g].sv = j.sv;
+    d[g].su = j.su;
+    d[g].pm = j.kron_pm;
+    d[g].s0 = j.s0;
+    d[g].s1 = j.s1;
+    d[g].layer_scale = j.layer_scale;
+    d[g].bias = j.bias;
+    d[g].y = j.y;
+    d[g].ldy = j.ldy;
+    d[g].counter = reinterpret_cast<unsigned*>(ws + off);
+    d[g].xmul = reinterpret_cast<float*>(ws + off + W.xmul);
+    d[g].y1p = reinterpret_cast<float*>(ws + off + W.y1p);
+    off += W.total;
+  }
+  rc = launch_linear_fused(x, x_dtype, ldx, (int)batch, (int)n, kron_pn, kron_n, y_dtype, count, d, W0.S, W0.SG,
+                           W0.W, cu_count(), s, reinterpret_cast<hipEvent_t>(mv_begin),
+                           reinterpret_cast<hipEvent_t>(mv_end));
+  if (rc) return rc;
+  // outputs the kernel did not finish: chunked ones in one launch, others per job
+  YcArgs yc[QS_MAX_GROUP];
+  int nyc = 0;
+  for (int g = 0; g < count; ++g) {
+    const qs_linear_job& j = jobs[g];
+    if (fused_output_in_kernel(j.m, j.kron_pm)) continue;
+    if (chunk_transform_fits(j.m, j.kron_pm)) {
+      yc[nyc++] = yc_args(d[g].y1p, W0.SG, (int)batch, j.m, j.kron_pm, j.kron_m, nullptr, 0, d[g].xmul, j.s0,
+                          j.layer_scale, j.su, j.bias, j.y, y_dtype, j.ldy);
+    } else {
+      rc = launch_yout_rows(d[g].y1p, W0.SG, (int)batch, j.m, j.kron_pm, j.kron_m, nullptr, 0, d[g].xmul, j.s0,
+                            j.layer_scale, j.su, j.bias, j.y, y_dtype, j.ldy, s);
+      if (rc) return rc;
+    }
+  }
+  if (nyc) return launch_yout_chunk_group(nyc, yc, s);
   return QS_OK;
 }

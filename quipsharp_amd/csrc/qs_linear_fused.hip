@@ -40,6 +40,7 @@
 #include <hip/hip_ext.h>
 
 #include "qs_chunk_dev.h"
+#include "qs_linear_dev.h"
 
 namespace qs {
 namespace {
@@ -53,7 +54,28 @@ __constant__ Table8 kE81 = make_e81_table();
 constexpr int kThreads = 1024;
 constexpr int kMaxB = 2;
 constexpr int kPrefetch = 4;
+constexpr int kMaxJobs = QS_MAX_GROUP;
 constexpr int kXStride = 264;               // halves per slice row of the fp16 operand buffer
+
+// One linear of a launch.  Linears in one launch share the input x (and n);
+// each has its own codes, signs, scales, output and workspace region.
+struct FusedJob {
+  const float* sv;
+  const uint16_t* codes0;
+  const uint8_t* codes1;
+  int m, Gr, wg0;      // rows; row-block stride; first work-group of this linear
+  float s0, s1;
+  float* y1p;          // [SG][B][m]
+  unsigned* counter;   // zero between launches
+  float* xmul;         // [B] 2^e per batch row (for a separate output kernel)
+  int out_in_kernel;
+  int Sm, lsh_m;
+  float scale_m, layer_scale;
+  const float* su;
+  const float* bias;
+  void* y;
+  int64_t ldy;
+};
 
 struct FusedArgs {
   const void* x;
@@ -64,23 +86,10 @@ struct FusedArgs {
   int n, Sn, lsh_n, pn;
   const float* Kn;
   float scale_n;
-  const float* sv;
-  const uint16_t* codes0;
-  const uint8_t* codes1;
-  int m, S, SG, W, Gr;
-  float s0, s1;
-  float* y1p;          // [SG][B][m]
-  unsigned* counter;   // zero between launches
-  float* xmul;         // [B] 2^e per batch row (for a separate output kernel)
-  int out_in_kernel;
-  int Sm, lsh_m, pm;
-  const float* Km;
-  float scale_m, layer_scale;
-  const float* su;
-  const float* bias;
-  void* y;
+  int S, SG, W;
   int y_dtype;
-  int64_t ldy;
+  int njobs;
+  FusedJob job[kMaxJobs];
 };
 
 // LDS layout (bytes).  The half-codeword table staging area aliases the
@@ -93,7 +102,8 @@ constexpr int kOffRed = kOffLut1 + 4096;                    // 2 x 16 x 16 x kMa
 constexpr int kOffK = kOffRed + 2 * kWaves * 16 * kMaxB * 4;  // p x p floats (p <= 64)
 constexpr int kOffXH = kOffK + QS_MAX_KRON * QS_MAX_KRON * 4;  // kMaxB x 16 x kXStride halves
 constexpr int kOffTab = kOffXH;                             // 256 x uint4 (table staging)
-constexpr int kOffY = kOffXH + kMaxB * 16 * kXStride * 2;   // kMaxS x kYStride floats
+constexpr int kOffXS = kOffXH + kMaxB * 16 * kXStride * 2;  // kMaxB x 16 x 32 halves (group sums)
+constexpr int kOffY = kOffXS + kMaxB * 16 * 32 * 2;          // kMaxS x kYStride floats
 constexpr int kLdsBytes = kOffY + kMaxS * kYStride * 4;
 static_assert(kLdsBytes <= 160 * 1024 - 128, "LDS budget");
 static_assert(kMaxB * 16 * kXStride * 2 >= 4096, "table staging fits the operand buffer");
@@ -104,7 +114,8 @@ __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
 }
 
 // Activation chunks of batch row b (times sv), chunk c = w + 16 u.
-__device__ __forceinline__ void load_x(const FusedArgs& A, int b, int w, int lane, float (&v)[kCPW][4]) {
+__device__ __forceinline__ void load_x(const FusedArgs& A, const float* sv, int b, int w, int lane,
+                                       float (&v)[kCPW][4]) {
 #pragma unroll
   for (int u = 0; u < kCPW; ++u) {
     const int c = w + kWaves * u;
@@ -112,7 +123,7 @@ __device__ __forceinline__ void load_x(const FusedArgs& A, int b, int w, int lan
     for (int j = 0; j < 4; ++j) v[u][j] = 0.0f;
     if (c < A.Sn) {
       const int i0 = 256 * c + 4 * lane;
-      const float4 s = *reinterpret_cast<const float4*>(A.sv + i0);
+      const float4 s = *reinterpret_cast<const float4*>(sv + i0);
       const int64_t xi = (int64_t)b * A.ldx + i0;
       float x0, x1, x2, x3;
       if (A.x_vec && A.x_dtype == QS_DTYPE_F32) {
@@ -162,6 +173,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   float* red = reinterpret_cast<float*>(lds + kOffRed);
   float* Ks = reinterpret_cast<float*>(lds + kOffK);
   _Float16* XH = reinterpret_cast<_Float16*>(lds + kOffXH);
+  _Float16* XS = reinterpret_cast<_Float16*>(lds + kOffXS);
   float* Y = reinterpret_cast<float*>(lds + kOffY);
   __shared__ float wsum[kWaves];
   __shared__ int s_last;
@@ -169,8 +181,14 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
   const int q = lane >> 4, r16 = lane & 15;
-  const int RB = A.m >> 4;
-  const int sg = blockIdx.x / A.Gr, jr = blockIdx.x - sg * A.Gr;
+  int g = 0;
+#pragma unroll
+  for (int k = 1; k < kMaxJobs; ++k)
+    if (k < A.njobs && (int)blockIdx.x >= A.job[k].wg0) g = k;
+  const FusedJob& J = A.job[g];
+  const int lb = (int)blockIdx.x - J.wg0;  // work-group index within this linear
+  const int RB = J.m >> 4;
+  const int sg = lb / J.Gr, jr = lb - sg * J.Gr;
   const int sl = sg * A.W + w;
   const bool active = w < A.W && sl < A.S;
   const LaneX lx = lane_x_init();
@@ -189,7 +207,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
 #pragma unroll
   for (int k = 0; k < 4; ++k) kv[k] = (A.pn > 1 && tid + kThreads * k < pp) ? A.Kn[tid + kThreads * k] : 0.0f;
   float xv[kCPW][4];
-  load_x(A, 0, w, lane, xv);
+  load_x(A, J.sv, 0, w, lane, xv);
   uint4 pre[kPrefetch];
   uint2 pre1[kPrefetch];
   if (tid < 256) {
@@ -228,9 +246,8 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
 
   // 2. input transform, one batch row at a time, into fp16 operand rows
   float emul0 = 1.0f, emul1 = 1.0f;  // 2^e of batch rows 0 and 1
-  const int kt_n = (A.Sn + 3) >> 2;
   for (int b = 0; b < A.B; ++b) {
-    if (b > 0) load_x(A, b, w, lane, xv);
+    if (b > 0) load_x(A, J.sv, b, w, lane, xv);
     float ss = 0.0f;
 #pragma unroll
     for (int u = 0; u < kCPW; ++u)
@@ -244,13 +261,13 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
       // activation loads do not queue behind them)
 #pragma unroll
       for (int k = 0; k < kPrefetch; ++k) {
-        const int rb = jr + k * A.Gr;
+        const int rb = jr + k * J.Gr;
         pre[k] = make_uint4(0, 0, 0, 0);
         pre1[k] = make_uint2(0, 0);
         if (active && rb < RB) {
           const size_t tile = ((size_t)rb * A.S + sl) * 64 + lane;
-          pre[k] = *reinterpret_cast<const uint4*>(A.codes0 + tile * 8);
-          if (HAS2) pre1[k] = *reinterpret_cast<const uint2*>(A.codes1 + tile * 8);
+          pre[k] = *reinterpret_cast<const uint4*>(J.codes0 + tile * 8);
+          if (HAS2) pre1[k] = *reinterpret_cast<const uint2*>(J.codes1 + tile * 8);
         }
       }
     }
@@ -269,20 +286,25 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
     if (b == 0) emul0 = ldexpf(1.0f, e);
     else emul1 = ldexpf(1.0f, e);
     const float mul = ldexpf(A.scale_n, -e);
-    // rows of M for this group's slices, columns 16w..16w+15
-    const int r = sg * A.W + r16;
-    const bool rv = r16 < A.W && r < A.Sn;
-    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int t = 0; t < kt_n; ++t) {
-      const int c = 4 * t + q;
-      const float av = (rv && c < A.Sn) ? mmat(r, c, A.lsh_n, A.pn, Ks) : 0.0f;
-      const float bv = c < A.Sn ? Y[c * kYStride + 16 * w + r16] : 0.0f;
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
+    // this wave's slice row of M . Y: X2[sl][4 lane + j] = sum_c M[sl][c] Y[c][4 lane + j]
+    // (M[sl][c] is the same for the whole wave), as fp16 into the wave's own
+    // operand row
+    if (active) {
+      const float4 a = mrow_times_chunks(Y, A.Sn, sl, A.lsh_n, A.pn, Ks, lane);
+      const _Float16 h0 = (_Float16)(a.x * mul), h1 = (_Float16)(a.y * mul);
+      const _Float16 h2 = (_Float16)(a.z * mul), h3 = (_Float16)(a.w * mul);
+      const uint2 hv = make_uint2((uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16),
+                                  (uint32_t)__builtin_bit_cast(uint16_t, h2) | ((uint32_t)__builtin_bit_cast(uint16_t, h3) << 16));
+      *reinterpret_cast<uint2*>(XH + (b * 16 + w) * kXStride + 4 * lane) = hv;
+      // group sums of the fp16 values: group t / 8 spans lanes 2g and 2g + 1
+      const float s4 = ((float)h0 + (float)h1) + ((float)h2 + (float)h3);
+      const float s8 = s4 + lane_xor<1>(s4, lx);
+      if ((lane & 1) == 0) XS[(b * 16 + w) * 32 + (lane >> 1)] = (_Float16)s8;
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) XH[(b * 16 + 4 * q + j) * kXStride + 16 * w + r16] = (_Float16)(acc[j] * mul);
   }
-  __syncthreads();  // operand rows complete
+  // each wave reads back only the operand row it wrote itself
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   // MFMA operand of lane (q, b = r16): columns 64q..64q+63 of this wave's slice
   const half8 hzero = {0, 0, 0, 0, 0, 0, 0, 0};
   half8 xb[8];
@@ -291,28 +313,22 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
 #pragma unroll
   for (int c = 0; c < 8; ++c) xb[c] = hzero;
   if (active && r16 < A.B) {
-    _Float16 sh[8];
     const _Float16* row = XH + (r16 * 16 + w) * kXStride + 64 * q;
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const half8 hv = *reinterpret_cast<const half8*>(row + 8 * c);
-      xb[c] = hv;
-      const float g01 = (float)hv[0] + (float)hv[1], g23 = (float)hv[2] + (float)hv[3];
-      const float g45 = (float)hv[4] + (float)hv[5], g67 = (float)hv[6] + (float)hv[7];
-      sh[c] = (_Float16)((g01 + g23) + (g45 + g67));
-      slice_shift += (float)sh[c];
-    }
-    xs = __builtin_bit_cast(half8, sh);
+    for (int c = 0; c < 8; ++c) xb[c] = *reinterpret_cast<const half8*>(row + 8 * c);
+    xs = *reinterpret_cast<const half8*>(XS + (r16 * 16 + w) * 32 + 8 * q);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) slice_shift += (float)xs[c];
   }
   // slice total of S_g over the four q-lanes of batch row r16
   slice_shift += __shfl_xor(slice_shift, 16);
   slice_shift += __shfl_xor(slice_shift, 32);
-  if (blockIdx.x == 0 && tid < A.B) A.xmul[tid] = tid == 0 ? emul0 : emul1;
+  if (lb == 0 && tid < A.B) J.xmul[tid] = tid == 0 ? emul0 : emul1;
 
   // 3. row blocks
   const int nw = A.S - sg * A.W < A.W ? A.S - sg * A.W : A.W;
   int k = 0;  // iteration count: selects the reduction buffer
-  for (int rb = jr; rb < RB; rb += A.Gr, ++k) {
+  for (int rb = jr; rb < RB; rb += J.Gr, ++k) {
     floatx4 acc = {0.f, 0.f, 0.f, 0.f};
     floatx4 accs = {0.f, 0.f, 0.f, 0.f};
     floatx4 acc2 = {0.f, 0.f, 0.f, 0.f};
@@ -325,13 +341,13 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
     }
     {
       // keep kPrefetch tiles in flight
-      const int rbn = rb + kPrefetch * A.Gr;
+      const int rbn = rb + kPrefetch * J.Gr;
       pre[kPrefetch - 1] = make_uint4(0, 0, 0, 0);
       pre1[kPrefetch - 1] = make_uint2(0, 0);
       if (active && rbn < RB) {
         const size_t tile = ((size_t)rbn * A.S + sl) * 64 + lane;
-        pre[kPrefetch - 1] = *reinterpret_cast<const uint4*>(A.codes0 + tile * 8);
-        if (HAS2) pre1[kPrefetch - 1] = *reinterpret_cast<const uint2*>(A.codes1 + tile * 8);
+        pre[kPrefetch - 1] = *reinterpret_cast<const uint4*>(J.codes0 + tile * 8);
+        if (HAS2) pre1[kPrefetch - 1] = *reinterpret_cast<const uint2*>(J.codes1 + tile * 8);
       }
     }
     if (active) {
@@ -361,8 +377,8 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
     if (r16 < A.B) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        float v = A.s0 * (acc[j] + 0.5f * accs[j] - 0.25f * slice_shift);
-        if (HAS2) v = v + A.s1 * acc2[j];
+        float v = J.s0 * (acc[j] + 0.5f * accs[j] - 0.25f * slice_shift);
+        if (HAS2) v = v + J.s1 * acc2[j];
         rbuf[(w * 16 + 4 * q + j) * kMaxB + r16] = active ? v : 0.0f;
       }
     }
@@ -378,39 +394,35 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
       v += __shfl_xor(v, 8);
       if (o < 16 * A.B && ww == 0) {
         const int row = o / A.B, bc = o % A.B;
-        __hip_atomic_store(&A.y1p[((size_t)sg * A.B + bc) * A.m + rb * 16 + row], v, __ATOMIC_RELAXED,
+        __hip_atomic_store(&J.y1p[((size_t)sg * A.B + bc) * J.m + rb * 16 + row], v, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
       }
     }
   }
 
   // 4. completion: the last work-group applies the output transform
-  if (!A.out_in_kernel) return;
+  if (!J.out_in_kernel) return;
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial-sum stores have completed
   __syncthreads();
   if (tid == 0)
-    s_last = __hip_atomic_fetch_add(A.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+    s_last = __hip_atomic_fetch_add(J.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             (unsigned)(J.Gr * A.SG - 1);
   __syncthreads();
   if (!s_last) return;
   {
-    float* Km = Ks;  // the input K is dead
-    const int ppm = A.pm * A.pm;
-    if (A.pm > 1)
-      for (int i = tid; i < ppm; i += kThreads) Km[i] = A.Km[i];
-    const int kt_m = (A.Sm + 3) >> 2;
-    const int rt_m = (A.Sm + 15) >> 4;
-    // this lane's outputs: rows 16u + 4q + j of column 16w + r16 (row = chunk of 256)
+    // this lane's outputs: rows r = w + 16u (chunks of 256), columns 4 lane + j
     float suv[kCPW][4], biv[kCPW][4];
 #pragma unroll
-    for (int u = 0; u < kCPW; ++u)
+    for (int u = 0; u < kCPW; ++u) {
+      const int r = w + kWaves * u;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int r = 16 * u + 4 * q + j;
-        const int i = 256 * r + 16 * w + r16;
-        const bool ok = r < A.Sm;
-        suv[u][j] = ok ? A.su[i] : 0.0f;
-        biv[u][j] = (ok && A.bias) ? A.bias[i] : 0.0f;
+        const int i = 256 * r + 4 * lane + j;
+        const bool ok = r < J.Sm;
+        suv[u][j] = ok ? J.su[i] : 0.0f;
+        biv[u][j] = (ok && J.bias) ? J.bias[i] : 0.0f;
       }
+    }
     for (int b = 0; b < A.B; ++b) {
       float zv[kCPW][4];
 #pragma unroll
@@ -418,59 +430,46 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
         const int c = w + kWaves * u;
 #pragma unroll
         for (int j = 0; j < 4; ++j) zv[u][j] = 0.0f;
-        if (c < A.Sm) {
+        if (c < J.Sm) {
           for (int g = 0; g < A.SG; ++g) {
-            const float* src = A.y1p + ((size_t)g * A.B + b) * A.m + 256 * c + 4 * lane;
+            const float* src = J.y1p + ((size_t)g * A.B + b) * J.m + 256 * c + 4 * lane;
 #pragma unroll
             for (int j = 0; j < 4; ++j)
               zv[u][j] += __hip_atomic_load(src + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           }
         }
       }
-      h256_chunks(zv, A.Sm, lane, lx);
-      store_chunks(Y, A.Sm, w, lane, zv);
-      __syncthreads();  // chunks (and Km) complete
-      const float mul = A.scale_m * A.layer_scale * (b == 0 ? emul0 : emul1);
-      // wave w: output columns 16w..16w+15 of every row tile
-      floatx4 acc[kCPW];
-#pragma unroll
-      for (int u = 0; u < kCPW; ++u) acc[u] = floatx4{0.f, 0.f, 0.f, 0.f};
-      for (int t = 0; t < kt_m; ++t) {
-        const int c = 4 * t + q;
-        const float bv = c < A.Sm ? Y[c * kYStride + 16 * w + r16] : 0.0f;
-#pragma unroll
-        for (int u = 0; u < kCPW; ++u) {
-          if (u < rt_m) {
-            const int r = 16 * u + r16;
-            const float av = (r < A.Sm && c < A.Sm) ? mmat(r, c, A.lsh_m, A.pm, Km) : 0.0f;
-            acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[u], 0, 0, 0);
-          }
-        }
-      }
+      h256_chunks(zv, J.Sm, lane, lx);
+      if (b > 0) __syncthreads();  // the previous row's reads of Y are done
+      store_chunks(Y, J.Sm, w, lane, zv);
+      __syncthreads();  // chunks complete
+      const float mul = J.scale_m * J.layer_scale * (b == 0 ? emul0 : emul1);
 #pragma unroll
       for (int u = 0; u < kCPW; ++u) {
+        const int r = w + kWaves * u;
+        if (r < J.Sm) {
+          const float4 av = mrow_times_chunks(Y, J.Sm, r, J.lsh_m, 1, nullptr, lane);
+          const float a[4] = {av.x, av.y, av.z, av.w};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int r = 16 * u + 4 * q + j;
-          if (r < A.Sm)
-            store_from_float(A.y, A.y_dtype, (int64_t)b * A.ldy + 256 * r + 16 * w + r16,
-                             acc[u][j] * mul * suv[u][j] + biv[u][j]);
+          for (int j = 0; j < 4; ++j)
+            store_from_float(J.y, A.y_dtype, (int64_t)b * J.ldy + 256 * r + 4 * lane + j,
+                             a[j] * mul * suv[u][j] + biv[u][j]);
         }
       }
-      __syncthreads();  // Y is rewritten by the next batch row
     }
   }
-  if (tid == 0) __hip_atomic_store(A.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) __hip_atomic_store(J.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace
 
-// Host launcher used by qs_linear_forward (qs_linear.hip).
-int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, int m, const void* codes0,
-                        const void* codes1, const float* sv, const float* su, int pn, const float* Kn, int pm,
-                        const float* Km, float s0, float s1, float layer_scale, const float* bias, void* y,
-                        int y_dtype, int64_t ldy, unsigned* counter, float* xmul, float* y1p, int S, int SG, int W,
-                        int ncu, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop, bool* out_done) {
+// Host launcher used by qs_linear_forward and qs_linear_forward_group
+// (qs_linear.hip).  The CUs are shared between the linears in proportion to
+// their rows; each linear's work-groups form a contiguous block of the grid.
+int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, int pn, const float* Kn, int y_dtype,
+                        int count, const FusedJobDesc* jobs, int S, int SG, int W, int ncu, hipStream_t stream,
+                        hipEvent_t ev_start, hipEvent_t ev_stop) {
+  QS_REQUIRE(count >= 1 && count <= kMaxJobs, "1..%d linears per launch", kMaxJobs);
   FusedArgs A{};
   A.x = x;
   A.x_dtype = x_dtype;
@@ -486,39 +485,47 @@ int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, i
   A.pn = pn;
   A.Kn = Kn;
   A.scale_n = inv_sqrt_len(n / pn);
-  A.sv = sv;
-  A.codes0 = static_cast<const uint16_t*>(codes0);
-  A.codes1 = static_cast<const uint8_t*>(codes1);
-  A.m = m;
   A.S = S;
   A.SG = SG;
   A.W = W;
-  const int RB = m / 16;
-  int Gr = ncu / SG;
-  if (Gr < 1) Gr = 1;
-  if (Gr > RB) Gr = RB;
-  A.Gr = Gr;
-  A.s0 = s0;
-  A.s1 = s1;
-  A.y1p = y1p;
-  A.counter = counter;
-  A.xmul = xmul;
-  // in-kernel output for pure Walsh-Hadamard outputs; an odd factor runs the
-  // chunk output kernel with one work-group per output chunk instead
-  A.out_in_kernel = pm == 1 && chunk_transform_fits(m, pm);
-  if (A.out_in_kernel) {
-    A.Sm = m / 256;
-    A.lsh_m = log2_exact(m / pm / 256);
-  }
-  A.pm = pm;
-  A.Km = Km;
-  A.scale_m = inv_sqrt_len(m / pm);
-  A.layer_scale = layer_scale;
-  A.su = su;
-  A.bias = bias;
-  A.y = y;
   A.y_dtype = y_dtype;
-  A.ldy = ldy;
+  A.njobs = count;
+  int64_t mtot = 0;
+  for (int g = 0; g < count; ++g) mtot += jobs[g].m;
+  const bool has2 = jobs[0].codes1 != nullptr;
+  int wg = 0;
+  for (int g = 0; g < count; ++g) {
+    const FusedJobDesc& d = jobs[g];
+    QS_REQUIRE((d.codes1 != nullptr) == has2, "all linears of a launch need the same number of stages");
+    FusedJob& J = A.job[g];
+    J.sv = d.sv;
+    J.codes0 = static_cast<const uint16_t*>(d.codes0);
+    J.codes1 = static_cast<const uint8_t*>(d.codes1);
+    J.m = (int)d.m;
+    const int RB = (int)(d.m / 16);
+    int Gr = (int)((double)ncu / SG * (double)d.m / (double)mtot);
+    if (Gr < 1) Gr = 1;
+    if (Gr > RB) Gr = RB;
+    J.Gr = Gr;
+    J.wg0 = wg;
+    wg += Gr * SG;
+    J.s0 = d.s0;
+    J.s1 = d.s1;
+    J.y1p = d.y1p;
+    J.counter = d.counter;
+    J.xmul = d.xmul;
+    J.out_in_kernel = d.pm == 1 && chunk_transform_fits(d.m, d.pm);
+    if (J.out_in_kernel) {
+      J.Sm = (int)(d.m / 256);
+      J.lsh_m = log2_exact(d.m / 256);
+    }
+    J.scale_m = inv_sqrt_len(d.m / d.pm);
+    J.layer_scale = d.layer_scale;
+    J.su = d.su;
+    J.bias = d.bias;
+    J.y = d.y;
+    J.ldy = d.ldy;
+  }
   static int attr_done = 0;
   if (!attr_done) {
     QS_HIP(hipFuncSetAttribute((const void*)linear_fused_kernel<false>,
@@ -527,17 +534,17 @@ int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, i
                                hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes));
     attr_done = 1;
   }
-  const unsigned grid = (unsigned)(SG * Gr);
-  if (codes1)
-    hipExtLaunchKernelGGL(linear_fused_kernel<true>, dim3(grid), dim3(kThreads), kLdsBytes, stream, ev_start, ev_stop,
-                          0, A);
-  else
-    hipExtLaunchKernelGGL(linear_fused_kernel<false>, dim3(grid), dim3(kThreads), kLdsBytes, stream, ev_start,
+  if (has2)
+    hipExtLaunchKernelGGL(linear_fused_kernel<true>, dim3((unsigned)wg), dim3(kThreads), kLdsBytes, stream, ev_start,
                           ev_stop, 0, A);
+  else
+    hipExtLaunchKernelGGL(linear_fused_kernel<false>, dim3((unsigned)wg), dim3(kThreads), kLdsBytes, stream,
+                          ev_start, ev_stop, 0, A);
   QS_LAUNCHED("linear_fused_kernel");
-  *out_done = A.out_in_kernel != 0;
   return QS_OK;
 }
+
+bool fused_output_in_kernel(int64_t m, int pm) { return pm == 1 && chunk_transform_fits(m, pm); }
 
 bool fused_eligible(int64_t batch, int64_t n, int64_t m, int pn) {
   (void)m;

@@ -5,6 +5,7 @@
 once into the kernel layout and decoded on the fly inside the matrix-core
 matvec, between the two randomized-Hadamard transforms.
 """
+import ctypes
 from dataclasses import dataclass
 
 import torch
@@ -194,6 +195,63 @@ def forward_packed(x: Tensor, packed: PackedCodes, su: Tensor, sv: Tensor, s0: f
         None if mv_events is None else _lib._vp(mv_events[0]), None if mv_events is None else _lib._vp(mv_events[1]),
         _lib.stream_of(x2)))
     return y.reshape(*lead, m)
+
+
+def forward_packed_group(x: Tensor, linears, out_dtype=None, workspace: Tensor = None, outs=None,
+                         mv_events=None):
+    """Several linears that read the same x in one launch (qs_linear_forward_group):
+    ``linears`` is a sequence of (packed, su, sv, s0, s1, layer_scale, bias);
+    returns the list of outputs, each equal to ``forward_packed`` of that
+    linear.  Needs batch <= 2, the tiled layout and n a multiple of 256 up to
+    12288.  No counterpart in the reference (one linear per call there)."""
+    count = len(linears)
+    if not 1 <= count <= _lib.QS_MAX_GROUP:
+        raise ValueError(f"1..{_lib.QS_MAX_GROUP} linears per group, got {count}")
+    n = linears[0][0].n
+    if x.shape[-1] != n or any(lin[0].n != n for lin in linears):
+        raise ValueError("all linears of a group read the same input width")
+    _lib.require_gpu(x, *[t for lin in linears for t in (lin[1], lin[2], lin[6])], what="linear forward")
+    out_dtype = out_dtype or x.dtype
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, n)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    B = x2.shape[0]
+    fn = kron_factor(n)
+    if fn is None:
+        raise ValueError(f"n = {n} needs the form p * 2^k with odd p <= {_lib.QS_MAX_KRON}")
+    Kn = hartley_matrix(fn[0], x.device) if fn[0] > 1 else None
+    jobs = (_lib.LinearJob * count)()
+    ys = []
+    for g, (packed, su, sv, s0, s1, layer_scale, bias) in enumerate(linears):
+        m = packed.m
+        fm = kron_factor(m)
+        if fm is None:
+            raise ValueError(f"m = {m} needs the form p * 2^k with odd p <= {_lib.QS_MAX_KRON}")
+        Km = hartley_matrix(fm[0], x.device) if fm[0] > 1 else None
+        y = outs[g].reshape(B, m) if outs is not None else torch.empty(B, m, dtype=out_dtype, device=x.device)
+        ys.append(y)
+        jobs[g] = _lib.LinearJob(packed.codes0.data_ptr(), None if packed.codes1 is None else packed.codes1.data_ptr(),
+                                 m, su.data_ptr(), sv.data_ptr(), fm[0], None if Km is None else Km.data_ptr(),
+                                 float(s0), float(s1), float(layer_scale),
+                                 None if bias is None else bias.data_ptr(), y.data_ptr(), m)
+        if packed.layout != _lib.QS_LAYOUT_TILED:
+            raise ValueError("grouped forward needs the tiled code layout")
+    if B == 0:
+        return [y.reshape(*lead, y.shape[-1]) for y in ys]
+    if len({y.dtype for y in ys}) != 1:
+        raise ValueError("all outputs of a group share one dtype")
+    lib = _lib.lib()
+    ms = (ctypes.c_int64 * count)(*[lin[0].m for lin in linears])
+    need = lib.qs_linear_group_workspace_bytes(n, B, count, ms)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.zeros(max(need, 256), dtype=torch.uint8, device=x.device)
+    _lib.check(lib.qs_linear_forward_group(
+        _lib.ptr(x2), _lib.dtype_code(x2.dtype), x2.stride(0), B, n, fn[0], _lib.ptr(Kn), count, jobs,
+        _lib.dtype_code(ys[0].dtype), _lib.ptr(workspace), workspace.numel(),
+        None if mv_events is None else _lib._vp(mv_events[0]), None if mv_events is None else _lib._vp(mv_events[1]),
+        _lib.stream_of(x2)))
+    return [y.reshape(*lead, y.shape[-1]) for y in ys]
 
 
 def _forward_params(codebook, num_stages):

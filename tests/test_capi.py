@@ -79,3 +79,18 @@ def test_workspace_size(L):
     a = L.qs_linear_workspace_bytes(4096, 4096, 1, _lib.QS_LAYOUT_TILED)
     b = L.qs_linear_workspace_bytes(4096, 11008, 16, _lib.QS_LAYOUT_TILED)
     assert a >= 4096 * 2 + 4096 * 4 and b > a and a % 256 == 0
+
+
+def test_group_argument_errors(L):
+    import ctypes as ct
+    from quipsharp_amd import _lib
+    ms = (ct.c_int64 * 2)(4096, 11008)
+    assert L.qs_linear_group_workspace_bytes(4096, 1, 2, ms) > L.qs_linear_workspace_bytes(4096, 4096, 1, 1)
+    assert L.qs_linear_group_workspace_bytes(4096, 1, 0, ms) == 0
+    jobs = (_lib.LinearJob * 5)()
+    rc = L.qs_linear_forward_group(ct.c_void_p(256), 0, 4096, 1, 4096, 1, None, 5, jobs, 0, ct.c_void_p(256), 1 << 20,
+                                   None, None, None)
+    assert rc == 1 and b"count" in L.qs_last_error()
+    rc = L.qs_linear_forward_group(ct.c_void_p(256), 0, 4096, 3, 4096, 1, None, 1, jobs, 0, ct.c_void_p(256), 1 << 20,
+                                   None, None, None)
+    assert rc == 1 and b"batch" in L.qs_last_error()

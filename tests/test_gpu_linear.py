@@ -253,3 +253,98 @@ def test_forward_small_chunk_counts(dev, m, n, B):
     assert packed.layout == 1
     want = dense_forward(x, codes, None, 1.0, 0.0, su, sv, 0.02, bias)
     assert rel_err(y.cpu().numpy(), want) < REL_TOL
+
+
+def _rand_linear(dev, rng, m, n, stages=1, bias=False):
+    from quipsharp_amd.quantize import PackedCodes
+    c = torch.from_numpy(rng.integers(0, 65536, (m, n // 8))).to(dev)
+    kinds = [0]
+    if stages == 2:
+        c = torch.stack([c, torch.from_numpy(rng.integers(0, 256, (m, n // 8))).to(dev)])
+        kinds = [0, 1]
+    packed = PackedCodes(c, m, n, kinds)
+    su = torch.from_numpy(rng.choice([-1.0, 1.0], m).astype(np.float32)).to(dev)
+    sv = torch.from_numpy(rng.choice([-1.0, 1.0], n).astype(np.float32)).to(dev)
+    b = torch.from_numpy(rng.standard_normal(m).astype(np.float32)).to(dev) if bias else None
+    return (packed, su, sv, 0.97, 0.45 if stages == 2 else 0.0, 0.0135, b)
+
+
+@pytest.mark.parametrize("shapes,n,B,stages,bias", [
+    ([4096, 4096, 4096], 4096, 1, 1, False),   # q, k, v
+    ([4096, 4096, 4096], 4096, 2, 1, True),
+    ([11008, 11008], 4096, 1, 1, True),        # gate, up (odd-factor outputs)
+    ([4096, 1024, 11008, 512], 4096, 2, 1, False),
+    ([4096, 1024], 4096, 1, 2, False),         # 3-bit residual VQ
+    ([4096, 4096], 11008, 1, 1, False),        # odd-factor input
+])
+def test_forward_group_equals_single(dev, shapes, n, B, stages, bias):
+    """Each output of a grouped launch is bit-identical to the single-linear
+    call (same slices per work-group, same reduction order)."""
+    from quipsharp_amd.quantize import forward_packed, forward_packed_group
+    rng = np.random.default_rng(sum(shapes) + n + B)
+    lins = [_rand_linear(dev, rng, m, n, stages, bias) for m in shapes]
+    x = torch.randn(B, n, device=dev).bfloat16()
+    ys = forward_packed_group(x, lins)
+    for lin, y in zip(lins, ys):
+        want = forward_packed(x, *lin)
+        assert y.shape == want.shape and torch.equal(y, want)
+    # and against the dense oracle for one of them
+    packed, su, sv, s0, s1, sc, b = lins[0]
+    codes = lins[0][0]
+    m0 = shapes[0]
+    if stages == 1:
+        rng2 = np.random.default_rng(sum(shapes) + n + B)
+        c0 = rng2.integers(0, 65536, (m0, n // 8))
+        su_np = rng2.choice([-1.0, 1.0], m0)
+        sv_np = rng2.choice([-1.0, 1.0], n)
+        b_np = rng2.standard_normal(m0).astype(np.float32) if bias else None
+        want = dense_forward(x.float().cpu().numpy(), c0, None, s0, 0.0, su_np, sv_np, sc, b_np)
+        got = ys[0].float().cpu().numpy()
+        assert np.all(np.abs(got - want) <= 2 ** -8 * np.abs(want) + 2e-3 * np.abs(want).max())
+
+
+def test_forward_group_graph_replays(dev):
+    from quipsharp_amd import _lib
+    from quipsharp_amd.quantize import forward_packed_group
+    rng = np.random.default_rng(77)
+    lins = [_rand_linear(dev, rng, m, 4096) for m in (4096, 4096, 11008)]
+    x = torch.randn(1, 4096, device=dev).bfloat16()
+    lib = _lib.lib()
+    import ctypes
+    ms = (ctypes.c_int64 * 3)(4096, 4096, 11008)
+    ws = torch.zeros(lib.qs_linear_group_workspace_bytes(4096, 1, 3, ms), dtype=torch.uint8, device=dev)
+    outs = [torch.empty(1, m, device=dev, dtype=torch.bfloat16) for m in (4096, 4096, 11008)]
+    eager = [y.clone() for y in forward_packed_group(x, lins, workspace=ws)]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        forward_packed_group(x, lins, workspace=ws, outs=outs)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        forward_packed_group(x, lins, workspace=ws, outs=outs)
+    for rep in range(3):
+        for o in outs:
+            o.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert torch.equal(o, e), rep
+        forward_packed_group(x, lins, workspace=ws)
+        torch.cuda.synchronize()
+
+
+def test_forward_group_rejects(dev):
+    from quipsharp_amd._lib import QuipHipError
+    from quipsharp_amd.quantize import forward_packed_group
+    rng = np.random.default_rng(5)
+    a = _rand_linear(dev, rng, 1024, 4096)
+    b = _rand_linear(dev, rng, 1024, 4096, stages=2)
+    x = torch.randn(1, 4096, device=dev)
+    with pytest.raises(ValueError):
+        forward_packed_group(x, [a] * 5)
+    with pytest.raises(QuipHipError, match="stages"):
+        forward_packed_group(x, [a, b])
+    with pytest.raises(QuipHipError, match="batch"):
+        forward_packed_group(torch.randn(3, 4096, device=dev), [a])
