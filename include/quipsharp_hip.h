@@ -166,6 +166,16 @@ int qs_linear_forward(const void *x, int x_dtype, int64_t ldx, int64_t batch, in
                       const float *bias, void *y, int y_dtype, int64_t ldy, void *workspace,
                       size_t workspace_bytes, void *mv_begin, void *mv_end, qs_stream_t stream);
 
+/* y = layer_scale * W_hat @ x for batch rows, no transforms: the decode-matvec
+ * alone, for inputs already in the transformed basis (the reference's RFFT
+ * layers, whose transforms run as FFTs: quipsharp/rfft.py:37-60 around
+ * quipsharp/quantize.py:123).  Arguments as in qs_linear_forward (no signs,
+ * no bias); n, m <= 32768. */
+int qs_decode_matvec(const void *x, int x_dtype, int64_t ldx, int64_t batch, int64_t n, int64_t m,
+                     const void *codes0, const void *codes1, int kind1, int layout, float s0, float s1,
+                     float layer_scale, void *y, int y_dtype, int64_t ldy, void *workspace,
+                     size_t workspace_bytes, qs_stream_t stream);
+
 /* One linear of a grouped forward (all linears of a group share x and n). */
 typedef struct qs_linear_job {
   const void *codes0;   /* packed E8P codes, QS_LAYOUT_TILED */

@@ -55,6 +55,8 @@ _SIGNATURES = {
     "qs_linear_forward": ([_vp, _int, _i64, _i64, _i64, _i64, _vp, _vp, _int, _int, _vp, _vp, _int, _vp,
                            _int, _vp, _f32, _f32, _f32, _vp, _vp, _int, _i64, _vp, ctypes.c_size_t, _vp, _vp,
                            _vp], _int),
+    "qs_decode_matvec": ([_vp, _int, _i64, _i64, _i64, _i64, _vp, _vp, _int, _int, _f32, _f32, _f32, _vp, _int,
+                          _i64, _vp, ctypes.c_size_t, _vp], _int),
     "qs_linear_group_workspace_bytes": ([_i64, _i64, _int, ctypes.POINTER(ctypes.c_int64)], ctypes.c_size_t),
     "qs_linear_forward_group": ([_vp, _int, _i64, _i64, _i64, _int, _vp, _int, ctypes.POINTER(LinearJob), _int,
                                  _vp, ctypes.c_size_t, _vp, _vp, _vp], _int),

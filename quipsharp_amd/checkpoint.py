@@ -1,19 +1,27 @@
-"""Codebook construction and the quantized ``nn.Module`` (quipsharp/checkpoint.py:56-156).
+"""Codebook construction, the quantized ``nn.Module`` and the compact
+checkpoint format (quipsharp/checkpoint.py).
 
 ``QuantizedLinear`` keeps the reference's buffers (int16 ``codes``, fp32
-``scale``, ``su``/``sv`` signs, optional ``bias``) so state dicts move
-between the two implementations; on first use on a device the codes are
-repacked once into the kernel layout (a non-persistent cache), and
-``forward`` runs the fused decode + transform + matvec kernels in the
-activation dtype (bf16/fp16/fp32) without a dense weight.
+``scale``, ``su``/``sv`` signs or ``phase_u``/``phase_v`` RFFT phases,
+optional ``bias``) so state dicts move between the two implementations; on
+first use on a device the codes are repacked once into the kernel layout (a
+non-persistent cache), and ``forward`` runs the fused decode + transform +
+matvec kernels in the activation dtype (bf16/fp16/fp32) without a dense
+weight.  ``save_quantized_checkpoint`` / ``load_quantized_checkpoint`` read
+and write the reference's format (state dict + manifest).
 """
+import json
+from pathlib import Path
+
 import torch
 from torch import nn, Tensor
 
 from .codebooks.e8_1bit import E8OneBitCodebook
 from .codebooks.e8p import E8PCodebook
 from .incoherence import IncoherenceSigns, KronSigns
-from .quantize import PackedCodes, QuantizedLayer, RVQCodebookAdapter, _forward_params, forward_packed
+from .quantize import (PackedCodes, QuantizedLayer, RVQCodebookAdapter, _forward_params, decode_matvec,
+                       forward_packed)
+from .rfft import RFFTPhases
 from .rvq import RVQStage, fit_residual_stage_scale, fit_stage_scale
 
 
@@ -41,15 +49,17 @@ def build_codebook(bits: str, device, seed: int = 0):
 class QuantizedLinear(nn.Module):
     """Drop-in for a quantized nn.Linear (quipsharp/checkpoint.py:80-146).
 
-    transform_kind: "rht" (power-of-two dims) or "krht" (Kronecker transform
-    for other dims).  "rfft" checkpoints of the reference are not supported.
+    transform_kind: "rht" (power-of-two dims), "krht" (Kronecker transform,
+    this library's choice for other dims) or "rfft" (the reference's choice
+    for other dims: complex64 ``phase_u``/``phase_v`` buffers, FFTs in hipFFT
+    around the library's decode-matvec).
     """
 
     def __init__(self, in_features: int, out_features: int, g: int, transform_kind: str, num_stages: int = 1,
                  has_bias: bool = False):
         super().__init__()
-        if transform_kind not in ("rht", "krht"):
-            raise NotImplementedError(f"transform_kind {transform_kind!r} is not supported (rht, krht)")
+        if transform_kind not in ("rht", "krht", "rfft"):
+            raise NotImplementedError(f"transform_kind {transform_kind!r} is not supported (rht, krht, rfft)")
         self.in_features = in_features
         self.out_features = out_features
         self.g = g
@@ -61,8 +71,12 @@ class QuantizedLinear(nn.Module):
         shape = (out_features, T) if num_stages == 1 else (num_stages, out_features, T)
         self.register_buffer("codes", torch.zeros(shape, dtype=torch.int16))
         self.register_buffer("scale", torch.zeros(()))
-        self.register_buffer("su", torch.zeros(out_features))
-        self.register_buffer("sv", torch.zeros(in_features))
+        if transform_kind == "rfft":
+            self.register_buffer("phase_u", torch.zeros(out_features // 2, dtype=torch.complex64))
+            self.register_buffer("phase_v", torch.zeros(in_features // 2, dtype=torch.complex64))
+        else:
+            self.register_buffer("su", torch.zeros(out_features))
+            self.register_buffer("sv", torch.zeros(in_features))
         self._packed = None
         self._packed_key = None
 
@@ -70,8 +84,8 @@ class QuantizedLinear(nn.Module):
     def from_quantized_layer(cls, layer: QuantizedLayer, bias: Tensor = None) -> "QuantizedLinear":
         m, n = layer.shape
         kind = getattr(layer.signs, "kind", None)
-        if kind not in ("rht", "krht"):
-            raise NotImplementedError("only Hadamard / Kronecker-transformed layers are supported")
+        if kind not in ("rht", "krht", "rfft"):
+            raise NotImplementedError("only Hadamard, Kronecker and RFFT-transformed layers are supported")
         stages = layer.codes.shape[0] if layer.codes.dim() == 3 else 1
         mod = cls(in_features=n, out_features=m, g=layer.g, transform_kind=kind, num_stages=stages,
                   has_bias=bias is not None)
@@ -80,15 +94,23 @@ class QuantizedLinear(nn.Module):
             mod.scale.copy_(torch.as_tensor(layer.scale, dtype=torch.float32))
             if bias is not None:
                 mod.bias.copy_(bias.float())
-            mod.su.copy_(layer.signs.su)
-            mod.sv.copy_(layer.signs.sv)
+            if kind == "rfft":
+                mod.phase_u.copy_(layer.signs.phase_u)
+                mod.phase_v.copy_(layer.signs.phase_v)
+            else:
+                mod.su.copy_(layer.signs.su)
+                mod.sv.copy_(layer.signs.sv)
         return mod
 
     def _quantized_layer(self) -> QuantizedLayer:
-        cls = IncoherenceSigns if self.transform_kind == "rht" else KronSigns
         codes = self.codes.to(torch.int64) & 0xFFFF
-        return QuantizedLayer(codes=codes, signs=cls(su=self.su, sv=self.sv), g=self.g,
-                              shape=(self.out_features, self.in_features), scale=self.scale.item())
+        if self.transform_kind == "rfft":
+            signs = RFFTPhases(phase_u=self.phase_u, phase_v=self.phase_v)
+        else:
+            cls = IncoherenceSigns if self.transform_kind == "rht" else KronSigns
+            signs = cls(su=self.su, sv=self.sv)
+        return QuantizedLayer(codes=codes, signs=signs, g=self.g, shape=(self.out_features, self.in_features),
+                              scale=self.scale.item())
 
     def _load_from_state_dict(self, *args, **kwargs):
         self._packed = None
@@ -111,6 +133,13 @@ class QuantizedLinear(nn.Module):
         in fp32, returned in x.dtype."""
         kinds, s0, s1 = _forward_params(self.codebook, self.num_stages)
         packed = self.packed(kinds)
+        if self.transform_kind == "rfft":
+            phases = RFFTPhases(phase_u=self.phase_u, phase_v=self.phase_v)
+            y = phases.transform_output(decode_matvec(phases.transform_input(x.float()), packed, s0, s1,
+                                                      self._scale_f, out_dtype=torch.float32))
+            if self.bias is not None:
+                y = y + self.bias
+            return y.to(x.dtype)
         return forward_packed(x, packed, self.su, self.sv, s0, s1, self._scale_f, bias=self.bias,
                               out_dtype=x.dtype)
 
@@ -122,3 +151,58 @@ def replace_with_quantized_linear_(parent: nn.Module, attr: str, layer: Quantize
     qlin.codebook = codebook
     setattr(parent, attr, qlin)
     return qlin
+
+
+STATE_NAME = "quantized_state.pt"
+MANIFEST_NAME = "quip_config.json"
+
+
+def save_quantized_checkpoint(model: nn.Module, model_id: str, save_path, bits: str, block_size: int, seed: int,
+                              quantized_modules: list, tokenizer=None) -> None:
+    """quipsharp/checkpoint.py:159-186: the model's state dict (QuantizedLinear
+    buffers in the reference's names and dtypes) plus a JSON manifest listing
+    every replaced module as {"name", "in_features", "out_features",
+    "transform_kind", "has_bias"}."""
+    save_path = Path(save_path)
+    save_path.mkdir(parents=True, exist_ok=True)
+    state = {k: v.detach().cpu() for k, v in model.state_dict().items()}
+    torch.save(state, save_path / STATE_NAME)
+    manifest = {"model_id": model_id, "bits": bits, "block_size": block_size, "seed": seed,
+                "quantized_modules": quantized_modules}
+    (save_path / MANIFEST_NAME).write_text(json.dumps(manifest, indent=2))
+    if tokenizer is not None:
+        tokenizer.save_pretrained(save_path)
+
+
+def is_quantized_checkpoint(path) -> bool:
+    """quipsharp/checkpoint.py:189-190."""
+    return (Path(path) / MANIFEST_NAME).exists()
+
+
+def load_quantized_checkpoint(save_path, model: nn.Module, device="cuda") -> nn.Module:
+    """quipsharp/checkpoint.py:193-275 for a caller-supplied architecture
+    skeleton (`model`, e.g. built with ``from_config`` on the meta device):
+    every manifest entry becomes an empty QuantizedLinear of the recorded
+    shape and transform, the saved state dict is loaded with ``assign=True``
+    through ``torch.load(weights_only=True)`` (tensors only, nothing executed
+    from the file), the model moves to ``device`` and each QuantizedLinear
+    gets the codebook rebuilt from the manifest's bits and seed.  (The
+    reference builds the skeleton from the hub model id and can spread layers
+    over several devices; both are outside this library.)"""
+    save_path = Path(save_path)
+    manifest = json.loads((save_path / MANIFEST_NAME).read_text())
+    state = torch.load(save_path / STATE_NAME, map_location="cpu", weights_only=True)
+    stages = num_rvq_stages(manifest["bits"])
+    for info in manifest["quantized_modules"]:
+        parent_name, _, attr = info["name"].rpartition(".")
+        parent = model.get_submodule(parent_name) if parent_name else model
+        qlin = QuantizedLinear(info["in_features"], info["out_features"], manifest["block_size"],
+                               info["transform_kind"], num_stages=stages, has_bias=info.get("has_bias", False))
+        setattr(parent, attr, qlin)
+    model.load_state_dict(state, strict=True, assign=True)
+    model.to(device)
+    codebook, _ = build_codebook(manifest["bits"], device, manifest["seed"])
+    for info in manifest["quantized_modules"]:
+        model.get_submodule(info["name"]).codebook = codebook
+    model.eval()
+    return model

@@ -106,8 +106,9 @@ struct XinArgs {
   int n, logL, p, G;
   const float* K;
   float scale;
-  const float* sv;
+  const float* sv;     // NULL with identity
   int tiled;
+  int identity;        // no transform: x2 = x (decode-matvec only)
   _Float16* x2h;
   _Float16* sg;
   float* xtot;  // [B][kMaxParts] partial sums of the rounded group sums
@@ -142,21 +143,23 @@ __global__ __launch_bounds__(kRowThreads) void xin_kernel(XinArgs A) {
   const int tid = threadIdx.x, nthr = blockDim.x;
   float ss = 0.0f;
   for (int i = tid; i < A.n; i += nthr) {
-    const float v = load_as_float(A.x, A.x_dtype, b * A.ldx + i) * A.sv[i];
+    const float v = load_as_float(A.x, A.x_dtype, b * A.ldx + i) * (A.sv ? A.sv[i] : 1.0f);
     buf[pad_idx(i)] = v;
     ss = __builtin_fmaf(v, v, ss);
   }
   if (A.p > 1)
     for (int i = tid; i < A.p * A.p; i += nthr) Ks[i] = A.K[i];
   const float norm2 = block_reduce_sum(ss, red);  // ends with a barrier
-  lds_fwht(buf, A.n, A.logL, tid, nthr);
+  if (!A.identity) lds_fwht(buf, A.n, A.logL, tid, nthr);
+  // segment length of the odd-factor stage (the whole row without a transform)
+  const int L = A.identity ? A.n : 1 << A.logL;
   if (!A.tiled) {
     if (A.p == 1) {
       for (int i = tid; i < A.n; i += nthr) A.x2[b * A.n + i] = buf[pad_idx(i)] * A.scale;
     } else {
       for (int i = tid; i < A.n; i += nthr) buf[pad_idx(i)] = buf[pad_idx(i)] * A.scale;
       __syncthreads();
-      const int L = 1 << A.logL, cw = L / A.G;
+      const int cw = L / A.G;
       float* x2 = A.x2 + b * A.n;
       kron_cols(buf, Ks, A.p, A.logL, part * cw, (part + 1) * cw, tid, nthr,
                 [&](int a, int c, float v) { x2[(a << A.logL) + c] = v; });
@@ -170,7 +173,6 @@ __global__ __launch_bounds__(kRowThreads) void xin_kernel(XinArgs A) {
     e = ex - 14;
   }
   const float mul = ldexpf(A.scale, -e);
-  const int L = 1 << A.logL;
   const int cw = L / A.G;          // columns of this work-group (multiple of 8)
   const int units = A.p * (cw >> 3);
   const int T = A.n >> 3;
@@ -189,12 +191,12 @@ __global__ __launch_bounds__(kRowThreads) void xin_kernel(XinArgs A) {
       for (int c = 0; c < A.p; ++c) {
         const float kv = Kr[c];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] = __builtin_fmaf(kv, buf[pad_idx((c << A.logL) + c0 + k)], v[k]);
+        for (int k = 0; k < 8; ++k) v[k] = __builtin_fmaf(kv, buf[pad_idx(c * L + c0 + k)], v[k]);
       }
 #pragma unroll
       for (int k = 0; k < 8; ++k) v[k] = v[k] * mul;
     }
-    const int i0 = (a << A.logL) + c0;
+    const int i0 = a * L + c0;
     _Float16 h[8];
     float gsum = v[0];
 #pragma unroll
@@ -466,6 +468,7 @@ __global__ __launch_bounds__(256) void mv_generic_kernel(MvgArgs A) {
 struct YoutArgs {
   const float* y1p;
   int SG, B, m, logL, p, G;
+  int identity;  // no transform: y = layer_scale * y1 (+ bias); su NULL
   const float* K;
   float scale;
   const float* xtot;  // [B][kMaxParts] or NULL on the row-major path
@@ -502,10 +505,10 @@ __global__ __launch_bounds__(kRowThreads) void yout_kernel(YoutArgs A) {
   if (A.p > 1)
     for (int i = tid; i < A.p * A.p; i += nthr) Ks[i] = A.K[i];
   __syncthreads();
-  lds_fwht(buf, A.m, A.logL, tid, nthr);
+  if (!A.identity) lds_fwht(buf, A.m, A.logL, tid, nthr);
   if (A.p == 1) {
     for (int i = tid; i < A.m; i += nthr) {
-      float v = buf[pad_idx(i)] * A.scale * A.su[i];
+      float v = buf[pad_idx(i)] * A.scale * (A.su ? A.su[i] : 1.0f);
       if (A.bias) v = v + A.bias[i];
       store_from_float(A.y, A.y_dtype, (int64_t)b * A.ldy + i, v);
     }
@@ -690,10 +693,10 @@ int launch_yout_chunk(const float* y1p, int SG, int B, int64_t m, int p, const f
 // does not cover: m not a multiple of 256, or larger than kMaxN).
 int launch_yout_rows(const float* y1p, int SG, int B, int64_t m, int p, const float* K, const float* xtot,
                      int xparts, const float* xmul, float s0, float layer_scale, const float* su, const float* bias,
-                     void* y, int y_dtype, int64_t ldy, hipStream_t s) {
-  const int L = (int)(m / p);
+                     void* y, int y_dtype, int64_t ldy, hipStream_t s, bool identity = false) {
+  const int L = identity ? 1 : (int)(m / p);
   const size_t lds = ((size_t)padded_len((int)m) + (size_t)p * p) * 4;
-  const int G = parts_for(m, p);
+  const int G = identity ? 1 : parts_for(m, p);
   int rc = set_lds((const void*)yout_kernel, lds, &g_yout_lds);
   if (rc) return rc;
   YoutArgs YA{};
@@ -705,7 +708,8 @@ int launch_yout_rows(const float* y1p, int SG, int B, int64_t m, int p, const fl
   YA.p = p;
   YA.G = G;
   YA.K = K;
-  YA.scale = inv_sqrt_len(L);
+  YA.scale = identity ? 1.0f : inv_sqrt_len(L);
+  YA.identity = identity;
   YA.xtot = xtot;
   YA.xparts = xparts;
   YA.xmul = xmul;
@@ -746,6 +750,101 @@ __global__ void busy_wait_kernel(uint64_t ticks, uint64_t max_iters) {
 }  // namespace qs
 
 using namespace qs;
+
+// The batched path (and the decode-matvec without transforms): per block of
+// up to 16 batch rows, input transform -> decode-matvec -> output transform.
+static int forward_batched(const void* x, int x_dtype, int64_t ldx, int64_t batch, int64_t n, int64_t m,
+                    const void* codes0, const void* codes1, int kind1, int layout, const float* sv, const float* su,
+                    int kron_pn, const float* kron_n, int kron_pm, const float* kron_m, float s0, float s1,
+                    float layer_scale, const float* bias, void* y, int y_dtype, int64_t ldy, char* ws,
+                    const WsLayout& W, void* mv_begin, void* mv_end, hipStream_t s, bool identity) {
+  int rc = QS_OK;
+  const int Ln = identity ? 1 : (int)(n / kron_pn);
+  const size_t xin_lds = ((size_t)padded_len((int)n) + (size_t)kron_pn * kron_pn) * 4;
+  const int Gx = identity ? 1 : parts_for(n, kron_pn);
+  rc = set_lds((const void*)xin_kernel, xin_lds, &g_xin_lds);
+  if (rc) return rc;
+
+  for (int64_t b0 = 0; b0 < batch; b0 += kMaxTileBatch) {
+    const int B = (int)(batch - b0 < kMaxTileBatch ? batch - b0 : kMaxTileBatch);
+    const char* xb = static_cast<const char*>(x) + (size_t)b0 * ldx * dtype_bytes(x_dtype);
+    char* yb = static_cast<char*>(y) + (size_t)b0 * ldy * dtype_bytes(y_dtype);
+
+    XinArgs XA{};
+    XA.x = xb;
+    XA.x_dtype = x_dtype;
+    XA.ldx = ldx;
+    XA.n = (int)n;
+    XA.logL = log2_exact(Ln);
+    XA.p = kron_pn;
+    XA.G = Gx;
+    XA.K = kron_n;
+    XA.scale = identity ? 1.0f : inv_sqrt_len(Ln);
+    XA.sv = sv;
+    XA.identity = identity;
+    XA.tiled = layout == QS_LAYOUT_TILED;
+    XA.x2h = reinterpret_cast<_Float16*>(ws + W.x2h);
+    XA.sg = reinterpret_cast<_Float16*>(ws + W.sg);
+    XA.xtot = reinterpret_cast<float*>(ws + W.xtot);
+    XA.xmul = reinterpret_cast<float*>(ws + W.xmul);
+    XA.x2 = reinterpret_cast<float*>(ws + W.x2);
+    hipLaunchKernelGGL(xin_kernel, dim3(B * Gx), dim3(kRowThreads), xin_lds, s, XA);
+    QS_LAUNCHED("xin_kernel");
+
+    float* y1p = reinterpret_cast<float*>(ws + W.y1p);
+    hipEvent_t ev0 = b0 == 0 ? reinterpret_cast<hipEvent_t>(mv_begin) : nullptr;
+    hipEvent_t ev1 = b0 + kMaxTileBatch >= batch ? reinterpret_cast<hipEvent_t>(mv_end) : nullptr;
+    if (layout == QS_LAYOUT_TILED) {
+      MvArgs MA{};
+      MA.codes0 = static_cast<const uint16_t*>(codes0);
+      MA.codes1 = static_cast<const uint8_t*>(codes1);
+      MA.x2h = XA.x2h;
+      MA.sg = XA.sg;
+      MA.y1p = y1p;
+      MA.m = (int)m;
+      MA.n = (int)n;
+      MA.B = B;
+      MA.S = W.S;
+      MA.SG = W.SG;
+      MA.W = W.W;
+      MA.s0 = s0;
+      MA.s1 = s1;
+      const int items = (int)(m / 16) * W.SG;
+      const int grid = items < cu_count() ? items : cu_count();
+      if (codes1)
+        hipExtLaunchKernelGGL(mv_tiled_kernel<true>, dim3(grid), dim3(W.W * 64), 0, s, ev0, ev1, 0, MA);
+      else
+        hipExtLaunchKernelGGL(mv_tiled_kernel<false>, dim3(grid), dim3(W.W * 64), 0, s, ev0, ev1, 0, MA);
+      QS_LAUNCHED("mv_tiled_kernel");
+    } else {
+      MvgArgs GA{};
+      GA.codes0 = static_cast<const uint16_t*>(codes0);
+      GA.codes1 = codes1;
+      GA.kind1 = kind1;
+      GA.x2 = XA.x2;
+      GA.y1p = y1p;
+      GA.m = (int)m;
+      GA.n = (int)n;
+      GA.B = B;
+      GA.s0 = s0;
+      GA.s1 = s1;
+      hipExtLaunchKernelGGL(mv_generic_kernel, dim3((unsigned)((m + 3) / 4)), dim3(256), 0, s, ev0, ev1, 0, GA);
+      QS_LAUNCHED("mv_generic_kernel");
+    }
+
+    const float* xtot = layout == QS_LAYOUT_TILED ? XA.xtot : nullptr;
+    const float* xmul = layout == QS_LAYOUT_TILED ? XA.xmul : nullptr;
+    if (!identity && chunk_transform_fits(m, kron_pm))
+      rc = launch_yout_chunk(y1p, W.SG, B, m, kron_pm, kron_m, xtot, Gx, xmul, s0, layer_scale, su, bias, yb, y_dtype,
+                             ldy, s);
+    else
+      rc = launch_yout_rows(y1p, W.SG, B, m, kron_pm, kron_m, xtot, Gx, xmul, s0, layer_scale, su, bias, yb, y_dtype,
+                            ldy, s, identity);
+    if (rc) return rc;
+  }
+  return QS_OK;
+}
+
 
 extern "C" int qs_busy_wait(int64_t nanoseconds, qs_stream_t stream) {
   QS_REQUIRE(nanoseconds >= 0 && nanoseconds <= 1000000000ll, "busy wait must be in [0, 1 s]");
@@ -828,89 +927,9 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
     return launch_yout_rows(d.y1p, W.SG, (int)batch, m, kron_pm, kron_m, nullptr, 0, d.xmul, s0, layer_scale, su,
                             bias, y, y_dtype, ldy, s);
   }
-  const int Ln = (int)(n / kron_pn);
-  const size_t xin_lds = ((size_t)padded_len((int)n) + (size_t)kron_pn * kron_pn) * 4;
-  const int Gx = parts_for(n, kron_pn);
-  rc = set_lds((const void*)xin_kernel, xin_lds, &g_xin_lds);
-  if (rc) return rc;
-
-  for (int64_t b0 = 0; b0 < batch; b0 += kMaxTileBatch) {
-    const int B = (int)(batch - b0 < kMaxTileBatch ? batch - b0 : kMaxTileBatch);
-    const char* xb = static_cast<const char*>(x) + (size_t)b0 * ldx * dtype_bytes(x_dtype);
-    char* yb = static_cast<char*>(y) + (size_t)b0 * ldy * dtype_bytes(y_dtype);
-
-    XinArgs XA{};
-    XA.x = xb;
-    XA.x_dtype = x_dtype;
-    XA.ldx = ldx;
-    XA.n = (int)n;
-    XA.logL = log2_exact(Ln);
-    XA.p = kron_pn;
-    XA.G = Gx;
-    XA.K = kron_n;
-    XA.scale = inv_sqrt_len(Ln);
-    XA.sv = sv;
-    XA.tiled = layout == QS_LAYOUT_TILED;
-    XA.x2h = reinterpret_cast<_Float16*>(ws + W.x2h);
-    XA.sg = reinterpret_cast<_Float16*>(ws + W.sg);
-    XA.xtot = reinterpret_cast<float*>(ws + W.xtot);
-    XA.xmul = reinterpret_cast<float*>(ws + W.xmul);
-    XA.x2 = reinterpret_cast<float*>(ws + W.x2);
-    hipLaunchKernelGGL(xin_kernel, dim3(B * Gx), dim3(kRowThreads), xin_lds, s, XA);
-    QS_LAUNCHED("xin_kernel");
-
-    float* y1p = reinterpret_cast<float*>(ws + W.y1p);
-    hipEvent_t ev0 = b0 == 0 ? reinterpret_cast<hipEvent_t>(mv_begin) : nullptr;
-    hipEvent_t ev1 = b0 + kMaxTileBatch >= batch ? reinterpret_cast<hipEvent_t>(mv_end) : nullptr;
-    if (layout == QS_LAYOUT_TILED) {
-      MvArgs MA{};
-      MA.codes0 = static_cast<const uint16_t*>(codes0);
-      MA.codes1 = static_cast<const uint8_t*>(codes1);
-      MA.x2h = XA.x2h;
-      MA.sg = XA.sg;
-      MA.y1p = y1p;
-      MA.m = (int)m;
-      MA.n = (int)n;
-      MA.B = B;
-      MA.S = W.S;
-      MA.SG = W.SG;
-      MA.W = W.W;
-      MA.s0 = s0;
-      MA.s1 = s1;
-      const int items = (int)(m / 16) * W.SG;
-      const int grid = items < cu_count() ? items : cu_count();
-      if (codes1)
-        hipExtLaunchKernelGGL(mv_tiled_kernel<true>, dim3(grid), dim3(W.W * 64), 0, s, ev0, ev1, 0, MA);
-      else
-        hipExtLaunchKernelGGL(mv_tiled_kernel<false>, dim3(grid), dim3(W.W * 64), 0, s, ev0, ev1, 0, MA);
-      QS_LAUNCHED("mv_tiled_kernel");
-    } else {
-      MvgArgs GA{};
-      GA.codes0 = static_cast<const uint16_t*>(codes0);
-      GA.codes1 = codes1;
-      GA.kind1 = kind1;
-      GA.x2 = XA.x2;
-      GA.y1p = y1p;
-      GA.m = (int)m;
-      GA.n = (int)n;
-      GA.B = B;
-      GA.s0 = s0;
-      GA.s1 = s1;
-      hipExtLaunchKernelGGL(mv_generic_kernel, dim3((unsigned)((m + 3) / 4)), dim3(256), 0, s, ev0, ev1, 0, GA);
-      QS_LAUNCHED("mv_generic_kernel");
-    }
-
-    const float* xtot = layout == QS_LAYOUT_TILED ? XA.xtot : nullptr;
-    const float* xmul = layout == QS_LAYOUT_TILED ? XA.xmul : nullptr;
-    if (chunk_transform_fits(m, kron_pm))
-      rc = launch_yout_chunk(y1p, W.SG, B, m, kron_pm, kron_m, xtot, Gx, xmul, s0, layer_scale, su, bias, yb, y_dtype,
-                             ldy, s);
-    else
-      rc = launch_yout_rows(y1p, W.SG, B, m, kron_pm, kron_m, xtot, Gx, xmul, s0, layer_scale, su, bias, yb, y_dtype,
-                            ldy, s);
-    if (rc) return rc;
-  }
-  return QS_OK;
+  return forward_batched(x, x_dtype, ldx, batch, n, m, codes0, codes1, kind1, layout, sv, su, kron_pn, kron_n,
+                         kron_pm, kron_m, s0, s1, layer_scale, bias, y, y_dtype, ldy, ws, W, mv_begin, mv_end, s,
+                         false);
 }
 
 extern "C" size_t qs_linear_group_workspace_bytes(int64_t n, int64_t batch, int count, const int64_t* ms) {
@@ -1003,4 +1022,34 @@ extern "C" int qs_linear_forward_group(const void* x, int x_dtype, int64_t ldx, 
   }
   if (nyc) return launch_yout_chunk_group(nyc, yc, s);
   return QS_OK;
+}
+
+extern "C" int qs_decode_matvec(const void* x, int x_dtype, int64_t ldx, int64_t batch, int64_t n, int64_t m,
+                                const void* codes0, const void* codes1, int kind1, int layout, float s0, float s1,
+                                float layer_scale, void* y, int y_dtype, int64_t ldy, void* workspace,
+                                size_t workspace_bytes, qs_stream_t stream) {
+  QS_REQUIRE(batch >= 0 && n > 0 && m > 0 && n % 8 == 0, "bad shape batch=%lld n=%lld m=%lld", (long long)batch,
+             (long long)n, (long long)m);
+  QS_REQUIRE(x_dtype >= QS_DTYPE_F32 && x_dtype <= QS_DTYPE_BF16 && y_dtype >= QS_DTYPE_F32 &&
+                 y_dtype <= QS_DTYPE_BF16,
+             "bad dtype");
+  QS_REQUIRE(layout == QS_LAYOUT_TILED || layout == QS_LAYOUT_ROWMAJOR, "bad layout");
+  if (batch == 0) return QS_OK;
+  QS_REQUIRE(x && y && codes0 && workspace, "null pointer");
+  QS_REQUIRE(ldx >= n && ldy >= m, "row strides too small");
+  QS_REQUIRE(n <= kMaxLen && m <= kMaxLen, "dims exceed %d", kMaxLen);
+  if (layout == QS_LAYOUT_TILED)
+    QS_REQUIRE(m % 16 == 0 && n % 256 == 0, "tiled layout needs m %% 16 == 0 and n %% 256 == 0");
+  QS_REQUIRE(!codes1 || kind1 == QS_STAGE_E8_1BIT || (kind1 == QS_STAGE_E8P && layout == QS_LAYOUT_ROWMAJOR),
+             "second stage must be E8 1-bit (or E8P on the row-major layout)");
+  const WsLayout W = ws_layout(m, n, batch, layout);
+  QS_REQUIRE(workspace_bytes >= W.total, "workspace too small: %zu < %zu", workspace_bytes, W.total);
+  QS_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255) == 0, "workspace must be 256-byte aligned");
+  if (layout == QS_LAYOUT_TILED)
+    QS_REQUIRE((reinterpret_cast<uintptr_t>(codes0) & 15) == 0 &&
+                   (!codes1 || (reinterpret_cast<uintptr_t>(codes1) & 7) == 0),
+               "packed codes must be 16-byte aligned");
+  return forward_batched(x, x_dtype, ldx, batch, n, m, codes0, codes1, kind1, layout, nullptr, nullptr, 1, nullptr, 1,
+                         nullptr, s0, s1, layer_scale, nullptr, y, y_dtype, ldy, static_cast<char*>(workspace), W,
+                         nullptr, nullptr, as_stream(stream), true);
 }

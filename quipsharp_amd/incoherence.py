@@ -163,11 +163,17 @@ def incoherence_mu(W: Tensor) -> float:
     return (W.abs().max() * (m * n) ** 0.5 / W.norm()).item()
 
 
-def incoherence_process_auto(W: Tensor, H: Tensor, generator=None):
+def incoherence_process_auto(W: Tensor, H: Tensor, generator=None, transform: str = "auto"):
     """quipsharp/incoherence.py:115-131: the Walsh-Hadamard RHT when both dims
     are powers of two; otherwise the Kronecker RHT (where the reference uses
-    its RFFT)."""
+    its RFFT on both sides).  transform="rfft" takes the reference's branch
+    for non-power-of-two dims (quipsharp_amd.rfft)."""
     m, n = W.shape
+    if transform not in ("auto", "rfft"):
+        raise ValueError(f"transform must be 'auto' or 'rfft', got {transform!r}")
     if is_pow2(m) and is_pow2(n):
         return incoherence_process(W, H, generator=generator)
+    if transform == "rfft":
+        from .rfft import rfft_incoherence_process
+        return rfft_incoherence_process(W, H, generator=generator)
     return kron_incoherence_process(W, H, generator=generator)

@@ -72,14 +72,17 @@ def _div(x: Tensor, d: float) -> Tensor:
 
 
 def quantize_linear(W: Tensor, H: Tensor, codebook, g: int = 8, damping: float = 1e-2, generator=None,
-                    codebook_scale: float = 1.0, tune_iters: int = 10):
+                    codebook_scale: float = 1.0, tune_iters: int = 10, transform: str = "auto"):
     """Algorithm 1 for one linear layer (quipsharp/quantize.py:48-104) on the
-    GPU.  Returns (QuantizedLayer, W_hat_q) like the reference."""
+    GPU.  Returns (QuantizedLayer, W_hat_q) like the reference.  ``transform``:
+    "auto" (Walsh-Hadamard RHT for power-of-two dims, else the Kronecker RHT)
+    or "rfft" (the reference's choice for non-power-of-two dims, for
+    checkpoints that must match its format)."""
     _lib.require_gpu(W, H, what="quantize_linear")
     W = W.float()
     H = H.float()
     H = H + damping * H.diagonal().mean() * torch.eye(H.shape[0], device=H.device, dtype=H.dtype)
-    what, hhat, signs = incoherence_process_auto(W, H, generator=generator)
+    what, hhat, signs = incoherence_process_auto(W, H, generator=generator, transform=transform)
     L, _ = block_ldl(hhat, g, damping=0.0)
     rms = what.double().pow(2).mean().float().sqrt().item()
     layer_scale = rms * codebook_scale
@@ -197,6 +200,35 @@ def forward_packed(x: Tensor, packed: PackedCodes, su: Tensor, sv: Tensor, s0: f
     return y.reshape(*lead, m)
 
 
+def decode_matvec(x: Tensor, packed: PackedCodes, s0: float, s1: float, layer_scale: float,
+                  out_dtype=None, workspace: Tensor = None) -> Tensor:
+    """y = layer_scale * W_hat @ x with no transforms (qs_decode_matvec): the
+    forward of a layer whose transforms run elsewhere (the reference's RFFT
+    layers).  x (..., n) already in the transformed basis."""
+    _lib.require_gpu(x, what="decode-matvec")
+    m, n = packed.m, packed.n
+    if x.shape[-1] != n:
+        raise ValueError(f"expected last dim {n}, got {x.shape[-1]}")
+    out_dtype = out_dtype or x.dtype
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, n)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    B = x2.shape[0]
+    y = torch.empty(B, m, dtype=out_dtype, device=x.device)
+    if B == 0:
+        return y.reshape(*lead, m)
+    lib = _lib.lib()
+    need = lib.qs_linear_workspace_bytes(m, n, B, packed.layout)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.zeros(max(need, 256), dtype=torch.uint8, device=x.device)
+    _lib.check(lib.qs_decode_matvec(
+        _lib.ptr(x2), _lib.dtype_code(x2.dtype), x2.stride(0), B, n, m, _lib.ptr(packed.codes0),
+        _lib.ptr(packed.codes1), packed.kind1, packed.layout, float(s0), float(s1), float(layer_scale), _lib.ptr(y),
+        _lib.dtype_code(y.dtype), m, _lib.ptr(workspace), workspace.numel(), _lib.stream_of(x2)))
+    return y.reshape(*lead, m)
+
+
 def forward_packed_group(x: Tensor, linears, out_dtype=None, workspace: Tensor = None, outs=None,
                          mv_events=None):
     """Several linears that read the same x in one launch (qs_linear_forward_group):
@@ -277,7 +309,11 @@ def linear_forward(x: Tensor, layer: QuantizedLayer, codebook) -> Tensor:
         packed = (layer.codes, PackedCodes(layer.codes, m, n, kinds))
         layer._packed = packed
     signs = layer.signs
+    if getattr(signs, "kind", None) == "rfft":
+        # the reference's RFFT layers: FFT transforms (hipFFT) around the decode-matvec
+        x2 = signs.transform_input(x.float())
+        return signs.transform_output(decode_matvec(x2, packed[1], s0, s1, layer.scale, out_dtype=torch.float32))
     if not hasattr(signs, "su"):
-        raise NotImplementedError("linear_forward supports Hadamard / Kronecker sign transforms")
+        raise NotImplementedError("linear_forward supports Hadamard, Kronecker and RFFT transforms")
     return forward_packed(x, packed[1], signs.su.float().contiguous(), signs.sv.float().contiguous(), s0, s1,
                           layer.scale)

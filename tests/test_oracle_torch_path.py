@@ -40,3 +40,13 @@ def test_quantize_steps_teacher_forced():
     for i in range(4):
         _, c = torch_path.e8p_encode(t[i])
         assert np.array_equal(c.numpy(), q["target_codes"][i])
+
+
+def test_random_phase_draws_the_reference_phases():
+    """quipsharp_amd.rfft.random_phase with the fixture's generator seed draws
+    the reference's phases bit for bit (CPU draw, quipsharp/rfft.py:31-34)."""
+    import torch
+    from quipsharp_amd.rfft import random_phase
+    g = golden("rfft.npz")
+    ph = random_phase(72, generator=torch.Generator().manual_seed(3))
+    assert np.array_equal(torch.view_as_real(ph).numpy(), g["phase"])
