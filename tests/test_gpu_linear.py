@@ -348,3 +348,48 @@ def test_forward_group_rejects(dev):
         forward_packed_group(x, [a, b])
     with pytest.raises(QuipHipError, match="batch"):
         forward_packed_group(torch.randn(3, 4096, device=dev), [a])
+
+
+def _dense_weights(codes0, codes1, s0, s1):
+    W = cref.e8p_decode(codes0).reshape(codes0.shape[0], -1).astype(np.float64) * s0
+    if codes1 is not None:
+        W += cref.e81_table()[codes1].reshape(codes1.shape[0], -1).astype(np.float64) * s1
+    return W
+
+
+def _check_shape(dev, m, n, batches, stages, seed):
+    """Forward at (m, n) for each batch size against one fp64 dense oracle."""
+    rng = np.random.default_rng(seed)
+    c0 = rng.integers(0, 65536, (m, n // 8))
+    c1 = rng.integers(0, 256, (m, n // 8)) if stages == 2 else None
+    su, sv = rng.choice([-1.0, 1.0], m), rng.choice([-1.0, 1.0], n)
+    s0, s1, scale = (0.93, 0.41, 0.011) if stages == 2 else (1.0, 0.0, 0.0135)
+    W = _dense_weights(c0, c1, s0, s1)
+    for B in batches:
+        print(f"case: m={m} n={n} B={B} stages={stages}", flush=True)
+        x = rng.standard_normal((B, n)).astype(np.float32)
+        y, packed = run(dev, x, c0, c1, s0, s1, su, sv, scale)
+        assert packed.layout == 1
+        want = T64(T64(x.astype(np.float64) * sv) @ W.T * scale) * su
+        err = rel_err(y.cpu().numpy(), want)
+        print(f"  rel err {err:.2e}", flush=True)
+        assert err < REL_TOL, (m, n, B, err)
+
+
+@pytest.mark.parametrize("m,n", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)])
+def test_llama3_8b_rvq3_shapes(dev, m, n):
+    """3-bit residual VQ (E8P + E8 1-bit) at the Llama-3-8B layer shapes, batch 1 / 4 / 16
+    (14336 = 7 x 2048 takes the odd-factor transform)."""
+    _check_shape(dev, m, n, [1, 4, 16], 2, m + n)
+
+
+@pytest.mark.parametrize("m,n", [(3584, 3584), (512, 3584), (18944, 3584), (3584, 18944)])
+def test_qwen25_7b_shapes(dev, m, n):
+    """Qwen2.5-7B layer shapes (3584 = 7 x 512, 18944 = 37 x 512), batch 1."""
+    _check_shape(dev, m, n, [1], 1, m * 3 + n)
+
+
+@pytest.mark.parametrize("m,n", [(8192, 5120), (1024, 5120), (5120, 8192), (25600, 5120), (5120, 25600)])
+def test_qwen3_32b_shapes(dev, m, n):
+    """Qwen3-32B layer shapes (5120 = 5 x 1024, 25600 = 25 x 1024), batch 1 and 8."""
+    _check_shape(dev, m, n, [1, 8], 1, m + 7 * n)

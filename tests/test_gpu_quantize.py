@@ -215,3 +215,34 @@ def test_quantized_linear_module(dev, cbs):
     yb = qlin(x.bfloat16())
     assert yb.dtype == torch.bfloat16
     assert (yb.float() - qlin(x)).norm() / qlin(x).norm() < 0.05
+
+
+def test_quantize_heavy_tailed_non_pow2(dev):
+    """A Qwen2.5-shaped layer (512 x 3584, Kronecker transform on both sides)
+    with 1 % Student-t outliers: the quantized weight is the decode of the
+    returned codes, the forward agrees with it, and the proxy loss is small."""
+    from quipsharp_amd.checkpoint import build_codebook
+    from quipsharp_amd.quantize import dequantize_linear, linear_forward, quantize_linear
+    g = torch.Generator().manual_seed(0)
+    torch.manual_seed(0)
+    m, n = 512, 3584
+    W = torch.randn(m, n, generator=g) * 0.02
+    mask = torch.rand(m, n, generator=g) < 0.01
+    t = torch.distributions.StudentT(3.0).sample((m, n)) * 0.02
+    W = torch.where(mask, t, W).to(dev)
+    X = torch.randn(2048, n, generator=g).to(dev)
+    H = X.T @ X / 2048
+    cb, s = build_codebook("2bit", dev, 0)
+    layer, what_q = quantize_linear(W, H, cb, codebook_scale=s, tune_iters=2,
+                                    generator=torch.Generator().manual_seed(1))
+    assert layer.signs.kind == "krht"
+    deq = dequantize_linear(layer, cb)
+    assert torch.allclose(deq, what_q, rtol=0, atol=1e-6 * what_q.abs().max().item())
+    Wq = layer.signs.reconstruct_weight(what_q)
+    E = (Wq - W).double()
+    proxy = (torch.trace(E @ H.double() @ E.T) / torch.trace(W.double() @ H.double() @ W.double().T)).item()
+    assert proxy < 0.05, proxy
+    x = torch.randn(3, n, device=dev)
+    y = linear_forward(x, layer, cb)
+    want = x @ Wq.T
+    assert ((y - want).norm() / want.norm()).item() < 1e-3
