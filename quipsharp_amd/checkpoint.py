@@ -79,6 +79,7 @@ class QuantizedLinear(nn.Module):
             self.register_buffer("sv", torch.zeros(in_features))
         self._packed = None
         self._packed_key = None
+        self._ws = None  # forward workspace (zeroed once; reused, so the forward can be graph-captured)
 
     @classmethod
     def from_quantized_layer(cls, layer: QuantizedLayer, bias: Tensor = None) -> "QuantizedLinear":
@@ -118,6 +119,7 @@ class QuantizedLinear(nn.Module):
 
     def _apply(self, fn, *args, **kwargs):
         self._packed = None
+        self._ws = None
         return super()._apply(fn, *args, **kwargs)
 
     def packed(self, kinds):
@@ -140,8 +142,17 @@ class QuantizedLinear(nn.Module):
             if self.bias is not None:
                 y = y + self.bias
             return y.to(x.dtype)
+        ws = self._workspace(x, packed)
         return forward_packed(x, packed, self.su, self.sv, s0, s1, self._scale_f, bias=self.bias,
-                              out_dtype=x.dtype)
+                              out_dtype=x.dtype, workspace=ws)
+
+    def _workspace(self, x, packed):
+        from . import _lib
+        rows = x.numel() // x.shape[-1] if x.dim() else 1
+        need = _lib.lib().qs_linear_workspace_bytes(self.out_features, self.in_features, max(rows, 1), packed.layout)
+        if self._ws is None or self._ws.numel() < need or self._ws.device != x.device:
+            self._ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=x.device)
+        return self._ws
 
 
 def replace_with_quantized_linear_(parent: nn.Module, attr: str, layer: QuantizedLayer, codebook,

@@ -1,0 +1,230 @@
+"""Greedy-decode harness for a full quantized decoder (Qwen3-32B shape by
+default): every decoder linear is a QuantizedLinear with random E8P codes,
+the rest of the model (embeddings, norms, rotary tables, lm_head) is the
+transformers implementation in bf16 with random weights.  Built on the meta
+device and materialized on the GPU, so the 32B-parameter model never exists
+densely.  Decoding runs through StaticDecoder (static fp32 KV cache, device
+positions and mask) so that each step is one HIP-graph replay.  Reports
+prefill time and decode tok/s.
+
+    python -m quipsharp_amd.decode --batch 1 8 --prompt 512 --new 256
+"""
+import argparse
+import json
+import time
+
+import torch
+from torch import nn
+
+from .architectures import get_decoder_layers, get_linear_groups
+from .checkpoint import QuantizedLinear, build_codebook
+from .hadamard import is_pow2, kron_factor, rademacher
+
+QWEN3_32B = dict(hidden_size=5120, intermediate_size=25600, num_hidden_layers=64, num_attention_heads=64,
+                 num_key_value_heads=8, head_dim=128, vocab_size=151936, max_position_embeddings=40960,
+                 rms_norm_eps=1e-6, tie_word_embeddings=False)
+
+
+def _random_qlinear(lin, device, gen, cpu_gen, scale=0.0135):
+    n, m = lin.in_features, lin.out_features
+    kind = "rht" if is_pow2(n) and is_pow2(m) else "krht"
+    if kind == "krht" and (kron_factor(n) is None or kron_factor(m) is None):
+        raise ValueError(f"no transform for a {m} x {n} linear")
+    q = QuantizedLinear(n, m, 8, kind, has_bias=getattr(lin, "bias", None) is not None)
+    q = q.to(device)
+    with torch.no_grad():
+        q.codes.copy_(torch.randint(-32768, 32768, q.codes.shape, generator=gen, device=device, dtype=torch.int32)
+                      .to(torch.int16))
+        q.scale.fill_(scale)
+        q.su.copy_(rademacher(m, device=device, generator=cpu_gen))
+        q.sv.copy_(rademacher(n, device=device, generator=cpu_gen))
+        if q.bias is not None:
+            q.bias.zero_()
+    return q
+
+
+def random_quantized_model(config, device="cuda", seed=0):
+    """transformers causal LM of ``config`` with every decoder linear replaced
+    by a random-code QuantizedLinear (linear discovery as
+    architectures.get_linear_groups) and random bf16 for the rest."""
+    from transformers import AutoModelForCausalLM
+    with torch.device("meta"):
+        model = AutoModelForCausalLM.from_config(config, dtype=torch.bfloat16)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    cpu_gen = torch.Generator().manual_seed(seed)
+    codebook, _ = build_codebook("2bit", device, seed)
+    for i, layer in enumerate(get_decoder_layers(model)):
+        for group in get_linear_groups(layer, i):
+            for name, lin in group:
+                parent_name, _, attr = name.rpartition(".")
+                parent = layer.get_submodule(parent_name)
+                q = _random_qlinear(lin, device, gen, cpu_gen)
+                q.codebook = codebook
+                setattr(parent, attr, q)
+    # everything still on the meta device gets fresh storage on the GPU
+    for mod in model.modules():
+        if hasattr(mod, "inv_freq") and getattr(mod, "inv_freq").is_meta:
+            fresh = type(mod)(config=mod.config)
+            for k, v in fresh.named_buffers(recurse=False):
+                setattr(mod, k, v.to(device))
+            if hasattr(fresh, "attention_scaling"):
+                mod.attention_scaling = fresh.attention_scaling
+            continue
+        for k, p in list(mod.named_parameters(recurse=False)):
+            if p.is_meta:
+                if "norm" in type(mod).__name__.lower():
+                    t = torch.ones(p.shape, dtype=p.dtype, device=device)
+                else:
+                    t = torch.randn(p.shape, generator=gen, dtype=torch.float32, device=device).mul_(0.02)
+                    t = t.to(p.dtype)
+                setattr(mod, k, nn.Parameter(t, requires_grad=False))
+        for k, b in list(mod.named_buffers(recurse=False)):
+            if b is not None and b.is_meta:
+                setattr(mod, k, torch.zeros(b.shape, dtype=b.dtype, device=device))
+    model.eval()
+    return model
+
+
+@torch.no_grad()
+def greedy_decode(model, prompt_ids, new_tokens):
+    """Prefill ``prompt_ids`` (B, P), then ``new_tokens`` greedy steps with a
+    KV cache.  Returns (tokens (B, new_tokens), prefill s, decode s)."""
+    from transformers import DynamicCache
+    cache = DynamicCache()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    out = model(input_ids=prompt_ids, past_key_values=cache, use_cache=True)
+    nxt = out.logits[:, -1].argmax(-1, keepdim=True)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    toks = [nxt]
+    for _ in range(new_tokens - 1):
+        out = model(input_ids=nxt, past_key_values=cache, use_cache=True)
+        nxt = out.logits[:, -1].argmax(-1, keepdim=True)
+        toks.append(nxt)
+    torch.cuda.synchronize()
+    t2 = time.perf_counter()
+    return torch.cat(toks, 1), t1 - t0, t2 - t1
+
+
+class StaticDecoder:
+    """A graph-capturable decode step for Qwen3-style decoders built on the
+    transformers modules of ``model`` (embeddings, RMSNorms, q/k norms,
+    rotary tables, SwiGLU, lm_head) and its QuantizedLinear layers: a static
+    KV cache of ``max_len`` positions per layer, positions passed as a device
+    tensor, the causal mask built on the device, so one decode step can be
+    captured once and replayed.  Attention runs in fp32 (keys and values are
+    kept in fp32)."""
+
+    def __init__(self, model, batch, max_len):
+        cfg = model.config
+        self.model = model
+        self.layers = get_decoder_layers(model)
+        self.B, self.max_len = batch, max_len
+        self.nh, self.nkv, self.hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        dev = model.lm_head.weight.device
+        self.k = [torch.zeros(batch, self.nkv, max_len, self.hd, device=dev) for _ in self.layers]
+        self.v = [torch.zeros(batch, self.nkv, max_len, self.hd, device=dev) for _ in self.layers]
+        self.kpos = torch.arange(max_len, device=dev)
+
+    @torch.no_grad()
+    def step(self, ids, pos):
+        """Logits of the last position; ids (B, q), pos (q,) int64 positions."""
+        from transformers.models.qwen3.modeling_qwen3 import apply_rotary_pos_emb
+        import torch.nn.functional as F
+        m = self.model.model
+        B, q = ids.shape
+        h = m.embed_tokens(ids)
+        cos, sin = m.rotary_emb(h, pos.unsqueeze(0).expand(B, -1))
+        mask = self.kpos[None, :] <= pos[:, None]  # (q, max_len): key j visible to query at pos_i iff j <= pos_i
+        for i, L in enumerate(self.layers):
+            a = L.self_attn
+            x = L.input_layernorm(h)
+            qs = a.q_norm(a.q_proj(x).view(B, q, self.nh, self.hd)).transpose(1, 2)
+            ks = a.k_norm(a.k_proj(x).view(B, q, self.nkv, self.hd)).transpose(1, 2)
+            vs = a.v_proj(x).view(B, q, self.nkv, self.hd).transpose(1, 2)
+            qs, ks = apply_rotary_pos_emb(qs, ks, cos, sin)
+            self.k[i].index_copy_(2, pos, ks.float())
+            self.v[i].index_copy_(2, pos, vs.float())
+            o = F.scaled_dot_product_attention(qs.float(), self.k[i], self.v[i], attn_mask=mask, enable_gqa=True)
+            h = h + a.o_proj(o.transpose(1, 2).reshape(B, q, self.nh * self.hd).to(h.dtype))
+            x = L.post_attention_layernorm(h)
+            h = h + L.mlp.down_proj(L.mlp.act_fn(L.mlp.gate_proj(x)) * L.mlp.up_proj(x))
+        return self.model.lm_head(m.norm(h[:, -1:]))[:, -1]
+
+
+@torch.no_grad()
+def greedy_decode_static(model, prompt_ids, new_tokens, use_graph=True):
+    """Prefill and greedy decode with StaticDecoder; each decode step replayed
+    from one HIP graph unless use_graph=False.  Returns (tokens, prefill s,
+    decode s)."""
+    B, P = prompt_ids.shape
+    dev = prompt_ids.device
+    dec = StaticDecoder(model, B, P + new_tokens + 2)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    tok = dec.step(prompt_ids, torch.arange(P, device=dev)).argmax(-1, keepdim=True)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    pos = torch.full((1,), P, dtype=torch.long, device=dev)
+    toks = [tok.clone()]
+    if not use_graph:
+        for _ in range(new_tokens - 1):
+            tok = dec.step(tok, pos).argmax(-1, keepdim=True)
+            pos.add_(1)
+            toks.append(tok)
+        torch.cuda.synchronize()
+        return torch.cat(toks, 1), t1 - t0, time.perf_counter() - t1
+    # warm-up (writes position P with the right token, as the first replay will), then capture
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            dec.step(tok, pos)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        nxt = dec.step(tok, pos).argmax(-1, keepdim=True)
+    torch.cuda.synchronize()
+    t2 = time.perf_counter()
+    for _ in range(new_tokens - 1):
+        graph.replay()
+        tok.copy_(nxt)
+        pos.add_(1)
+        toks.append(nxt.clone())
+    torch.cuda.synchronize()
+    return torch.cat(toks, 1), t1 - t0, time.perf_counter() - t2
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--layers", type=int, default=64)
+    ap.add_argument("--batch", type=int, nargs="+", default=[1, 8])
+    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--new", type=int, default=256)
+    ap.add_argument("--eager", action="store_true", help="decode steps launched eagerly (no HIP graph)")
+    args = ap.parse_args()
+    from transformers import Qwen3Config
+    cfg = Qwen3Config(**dict(QWEN3_32B, num_hidden_layers=args.layers))
+    dev = torch.device("cuda:0")
+    t0 = time.perf_counter()
+    model = random_quantized_model(cfg, dev)
+    torch.cuda.synchronize()
+    build_s = time.perf_counter() - t0
+    code_bytes = sum(m.codes.numel() * 2 for m in model.modules() if isinstance(m, QuantizedLinear))
+    res = {"model": "Qwen3-32B shape (random init, E8P 2-bit decoder linears)", "layers": args.layers,
+           "code_bytes": code_bytes, "build_s": round(build_s, 1), "runs": []}
+    for B in args.batch:
+        g = torch.Generator().manual_seed(B)
+        ids = torch.randint(0, cfg.vocab_size, (B, args.prompt), generator=g).to(dev)
+        greedy_decode(model, ids[:, :16], 4)  # warm-up
+        toks, pre_s, dec_s = greedy_decode_static(model, ids, args.new, use_graph=not args.eager)
+        steps = args.new - 1
+        res["runs"].append({"batch": B, "graph": not args.eager, "prefill_s": round(pre_s, 3), "decode_s": round(dec_s, 3),
+                            "tok_per_s": round(B * steps / dec_s, 2), "ms_per_step": round(1e3 * dec_s / steps, 3),
+                            "first_tokens": toks[0, :8].tolist()})
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()
