@@ -13,9 +13,10 @@
 // Work-group j owns one slice group (up to 16 slices of 256 input columns,
 // one per wave) and a strided set of 16-row blocks, so each wave's activation
 // operand stays in registers for the whole launch.  Per work-group:
-//   1. issue the table and activation loads, build the signed half-codeword
-//      LDS tables; the first code tiles are requested once the activations
-//      have arrived;
+//   1. issue the activation loads, then the abs-table and K loads; the first
+//      code tiles are requested once the activations have arrived, and the
+//      signed half-codeword LDS tables are built after the input transform
+//      (off its critical path);
 //   2. input transform (every work-group; only its own slices' rows of M):
 //      chunks -> LDS, MFMA over M rows of this group, fp16 operand per wave
 //      scaled by 2^-e (e from the row norm) plus the per-group sums for the
@@ -92,21 +93,21 @@ struct FusedArgs {
   FusedJob job[kMaxJobs];
 };
 
-// LDS layout (bytes).  The half-codeword table staging area aliases the
-// operand buffer (it is dead before the first operand write); the output
-// transform of the last work-group reuses the K and Y regions.
+// LDS layout (bytes).  The abs-table staging area aliases the reduction
+// buffer (the table is dead before the first row block); the output
+// transform of the last work-group reuses the Y region.
 constexpr int kOffHi = 0;                                   // 4096 x uint2
 constexpr int kOffLo = 32768;                               // 4096 x uint2
 constexpr int kOffLut1 = 65536;                             // 256 x uint4
 constexpr int kOffRed = kOffLut1 + 4096;                    // 2 x 16 x 16 x kMaxB floats
 constexpr int kOffK = kOffRed + 2 * kWaves * 16 * kMaxB * 4;  // p x p floats (p <= 64)
+constexpr int kOffTab = kOffRed;                            // 256 x uint4 (table staging, before the row blocks)
 constexpr int kOffXH = kOffK + QS_MAX_KRON * QS_MAX_KRON * 4;  // kMaxB x 16 x kXStride halves
-constexpr int kOffTab = kOffXH;                             // 256 x uint4 (table staging)
 constexpr int kOffXS = kOffXH + kMaxB * 16 * kXStride * 2;  // kMaxB x 16 x 32 halves (group sums)
 constexpr int kOffY = kOffXS + kMaxB * 16 * 32 * 2;          // kMaxS x kYStride floats
 constexpr int kLdsBytes = kOffY + kMaxS * kYStride * 4;
 static_assert(kLdsBytes <= 160 * 1024 - 128, "LDS budget");
-static_assert(kMaxB * 16 * kXStride * 2 >= 4096, "table staging fits the operand buffer");
+static_assert(2 * kWaves * 16 * kMaxB * 4 >= 4096, "table staging fits the reduction buffer");
 
 __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
   _Float16 a = (_Float16)lo, b = (_Float16)hi;
@@ -193,7 +194,10 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   const bool active = w < A.W && sl < A.S;
   const LaneX lx = lane_x_init();
 
-  // 1. loads, in the order they are needed: tables, K, activations, codes
+  // 1. loads: the activations first (the transform waits for them), then the
+  //    abs table and K; the code tiles once the activations are in
+  float xv[kCPW][4];
+  load_x(A, J.sv, 0, w, lane, xv);
   float trow[8], t1row[8];
   if (tid < 256) {
 #pragma unroll
@@ -206,43 +210,8 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   const int pp = A.pn * A.pn;
 #pragma unroll
   for (int k = 0; k < 4; ++k) kv[k] = (A.pn > 1 && tid + kThreads * k < pp) ? A.Kn[tid + kThreads * k] : 0.0f;
-  float xv[kCPW][4];
-  load_x(A, J.sv, 0, w, lane, xv);
   uint4 pre[kPrefetch];
   uint2 pre1[kPrefetch];
-  if (tid < 256) {
-    tab16[tid] = make_uint4(pack_h2(trow[0], trow[1]), pack_h2(trow[2], trow[3]), pack_h2(trow[4], trow[5]),
-                            pack_h2(trow[6], trow[7]));
-    if (HAS2)
-      lut1[tid] = make_uint4(pack_h2(t1row[0], t1row[1]), pack_h2(t1row[2], t1row[3]),
-                             pack_h2(t1row[4], t1row[5]), pack_h2(t1row[6], t1row[7]));
-  }
-#pragma unroll
-  for (int k = 0; k < 4; ++k)
-    if (A.pn > 1 && tid + kThreads * k < pp) Ks[tid + kThreads * k] = kv[k];
-  __syncthreads();
-  {
-    // LUT entries e = tid + 1024 k.  hi: abs row e & 255 = tid & 255 and flip
-    // nibble H = e >> 8 = (tid >> 8) + 4 k.  lo: abs row (e >> 3) & 255 (two
-    // rows, k even / odd), f4..f6 from e & 7 = tid & 7, q = e >> 11 = k >> 1.
-    const uint4 th = tab16[tid & 255];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint32_t H = (uint32_t)(tid >> 8) + 4u * k;
-      const uint32_t f1 = (H >> 3) & 1, f2 = (H >> 2) & 1, f3 = (H >> 1) & 1;
-      const uint32_t f0 = (H & 1) ^ f1 ^ f2 ^ f3;
-      lut_hi[tid + kThreads * k] = make_uint2(th.x ^ ((f0 << 15) | (f1 << 31)), th.y ^ ((f2 << 15) | (f3 << 31)));
-    }
-    const uint32_t f4 = (tid >> 2) & 1, f5 = (tid >> 1) & 1, f6 = tid & 1;
-    const uint32_t m45 = (f4 << 15) | (f5 << 31), p456 = f4 ^ f5 ^ f6;
-    const uint4 ta = tab16[(tid >> 3) & 255], tb = tab16[((tid >> 3) + 128) & 255];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint4 t = (k & 1) ? tb : ta;
-      const uint32_t f7 = (uint32_t)(k >> 1) ^ p456;
-      lut_lo[tid + kThreads * k] = make_uint2(t.z ^ m45, t.w ^ ((f6 << 15) | (f7 << 31)));
-    }
-  }
 
   // 2. input transform, one batch row at a time, into fp16 operand rows
   float emul0 = 1.0f, emul1 = 1.0f;  // 2^e of batch rows 0 and 1
@@ -270,10 +239,21 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
           if (HAS2) pre1[k] = *reinterpret_cast<const uint2*>(J.codes1 + tile * 8);
         }
       }
+      // table staging and K (read after the barrier below)
+      if (tid < 256) {
+        tab16[tid] = make_uint4(pack_h2(trow[0], trow[1]), pack_h2(trow[2], trow[3]), pack_h2(trow[4], trow[5]),
+                                pack_h2(trow[6], trow[7]));
+        if (HAS2)
+          lut1[tid] = make_uint4(pack_h2(t1row[0], t1row[1]), pack_h2(t1row[2], t1row[3]),
+                                 pack_h2(t1row[4], t1row[5]), pack_h2(t1row[6], t1row[7]));
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (A.pn > 1 && tid + kThreads * k < pp) Ks[tid + kThreads * k] = kv[k];
     }
-    if (b > 0) __syncthreads();  // the previous row's MFMAs have read Y
+    if (b > 0) __syncthreads();  // the previous row's reads of Y are done
     store_chunks(Y, A.Sn, w, lane, xv);
-    __syncthreads();  // chunks, norms (and, the first time, the LUTs) complete
+    __syncthreads();  // chunks, norms (and, the first time, the staged table and K) complete
     float norm2 = 0.0f;
 #pragma unroll
     for (int i = 0; i < kWaves; ++i) norm2 += wsum[i];
@@ -302,9 +282,29 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
       if ((lane & 1) == 0) XS[(b * 16 + w) * 32 + (lane >> 1)] = (_Float16)s8;
     }
   }
-  // each wave reads back only the operand row it wrote itself
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  {
+    // LUT entries e = tid + 1024 k.  hi: abs row e & 255 = tid & 255 and flip
+    // nibble H = e >> 8 = (tid >> 8) + 4 k.  lo: abs row (e >> 3) & 255 (two
+    // rows, k even / odd), f4..f6 from e & 7 = tid & 7, q = e >> 11 = k >> 1.
+    const uint4 th = tab16[tid & 255];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t H = (uint32_t)(tid >> 8) + 4u * k;
+      const uint32_t f1 = (H >> 3) & 1, f2 = (H >> 2) & 1, f3 = (H >> 1) & 1;
+      const uint32_t f0 = (H & 1) ^ f1 ^ f2 ^ f3;
+      lut_hi[tid + kThreads * k] = make_uint2(th.x ^ ((f0 << 15) | (f1 << 31)), th.y ^ ((f2 << 15) | (f3 << 31)));
+    }
+    const uint32_t f4 = (tid >> 2) & 1, f5 = (tid >> 1) & 1, f6 = tid & 1;
+    const uint32_t m45 = (f4 << 15) | (f5 << 31), p456 = f4 ^ f5 ^ f6;
+    const uint4 ta = tab16[(tid >> 3) & 255], tb = tab16[((tid >> 3) + 128) & 255];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint4 t = (k & 1) ? tb : ta;
+      const uint32_t f7 = (uint32_t)(k >> 1) ^ p456;
+      lut_lo[tid + kThreads * k] = make_uint2(t.z ^ m45, t.w ^ ((f6 << 15) | (f7 << 31)));
+    }
+  }
+  __syncthreads();  // LUTs and operand rows complete; the table staging area is free again
   // MFMA operand of lane (q, b = r16): columns 64q..64q+63 of this wave's slice
   const half8 hzero = {0, 0, 0, 0, 0, 0, 0, 0};
   half8 xb[8];
