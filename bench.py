@@ -284,14 +284,14 @@ def time_mv_kernels(runner, passes=3):
     return total_ms / passes / n  # ms per launch
 
 
-def gpu_quantize(dev):
+def gpu_quantize(dev, n=4096, tune_iters=10):
     import torch
     from quipsharp_amd.checkpoint import build_codebook
     from quipsharp_amd.quantize import quantize_linear, linear_forward
     g = torch.Generator().manual_seed(0)
-    W = torch.randn(4096, 4096, generator=g) * 0.02
-    X = torch.randn(2048, 4096, generator=g)
-    x = torch.randn(4096, generator=g)
+    W = torch.randn(n, n, generator=g) * 0.02
+    X = torch.randn(2048, n, generator=g)
+    x = torch.randn(n, generator=g)
     Wd, Xd = W.to(dev), X.to(dev)
     H = Xd.T @ Xd / 2048
     torch.cuda.synchronize()
@@ -302,7 +302,7 @@ def gpu_quantize(dev):
     torch.manual_seed(0)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    layer, what_q = quantize_linear(Wd, H, cb, g=8, damping=1e-2, codebook_scale=s, tune_iters=10)
+    layer, what_q = quantize_linear(Wd, H, cb, g=8, damping=1e-2, codebook_scale=s, tune_iters=tune_iters)
     torch.cuda.synchronize()
     t_q = time.perf_counter() - t0
     y = linear_forward(x.to(dev), layer, cb)
@@ -384,6 +384,10 @@ def main():
         stack = Stack(2, dev)
         r1 = Runner(stack, 1)
         r1.step()
+        torch.cuda.synchronize()
+        Runner(stack, 16).step()           # batch-16 matvec
+        torch.cuda.synchronize()
+        gpu_quantize(dev, n=1024, tune_iters=1)  # encode / LDLQ kernels
         torch.cuda.synchronize()
         a = torch.ones(64 << 20, dtype=torch.float32, device=dev)
         b = torch.empty_like(a)
