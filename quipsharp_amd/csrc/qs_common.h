@@ -130,6 +130,30 @@ constexpr Table8 make_e81_table() {
   return t;
 }
 
+// fp16 bit pattern of a float that fp16 represents exactly (zero or normal).
+constexpr uint16_t f16_bits_exact(float f) {
+  const uint16_t sign = f < 0.0f ? 0x8000 : 0;
+  float a = f < 0.0f ? -f : f;
+  if (a == 0.0f) return sign;
+  int e = 0;
+  while (a >= 2.0f) a *= 0.5f, ++e;
+  while (a < 1.0f) a *= 2.0f, --e;
+  return (uint16_t)(sign | ((e + 15) << 10) | (int)((a - 1.0f) * 1024.0f));
+}
+
+// A Table8 as fp16 pairs: w[r][i] holds elements 2i (low half) and 2i + 1.
+struct Table8h {
+  uint32_t w[256][4];
+};
+
+constexpr Table8h pack_table_f16(const Table8& t) {
+  Table8h h{};
+  for (int r = 0; r < 256; ++r)
+    for (int i = 0; i < 4; ++i)
+      h.w[r][i] = (uint32_t)f16_bits_exact(t.v[r][2 * i]) | ((uint32_t)f16_bits_exact(t.v[r][2 * i + 1]) << 16);
+  return h;
+}
+
 constexpr Table8 kE8PHost = make_e8p_table();
 constexpr Table8 kE81Host = make_e81_table();
 
@@ -145,10 +169,9 @@ __device__ __forceinline__ float load_as_float(const void* p, int dtype, int64_t
 
 // Round-to-nearest-even fp32 -> bf16, NaN kept quiet.
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) return (uint16_t)((u >> 16) | 0x40);
-  uint32_t r = u + 0x7FFFu + ((u >> 16) & 1u);
-  return (uint16_t)(r >> 16);
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t r = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;  // round to nearest even
+  return (uint16_t)((u & 0x7FFFFFFFu) > 0x7F800000u ? ((u >> 16) | 0x40u) : r);  // NaN stays a quiet NaN
 }
 
 __device__ __forceinline__ void store_from_float(void* p, int dtype, int64_t i, float v) {

@@ -907,6 +907,7 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
     d.sv = sv;
     d.su = su;
     d.pm = kron_pm;
+    d.Km = kron_m;
     d.s0 = s0;
     d.s1 = s1;
     d.layer_scale = layer_scale;
@@ -990,6 +991,7 @@ extern "C" int qs_linear_forward_group(const void* x, int x_dtype, int64_t ldx, 
     d[g].sv = j.sv;
     d[g].su = j.su;
     d[g].pm = j.kron_pm;
+    d[g].Km = j.kron_m;
     d[g].s0 = j.s0;
     d[g].s1 = j.s1;
     d[g].layer_scale = j.layer_scale;

@@ -14,6 +14,7 @@ struct FusedJobDesc {
   const float* sv;
   const float* su;
   int pm;               // odd factor of m (output transform)
+  const float* Km;      // pm x pm K factor of the output transform (pm > 1)
   float s0, s1, layer_scale;
   const float* bias;
   void* y;

@@ -27,10 +27,11 @@
 //   4. completion: the stores are waited for, then one atomic per work-group
 //      on a counter; the last work-group reads the partials (write-through
 //      loads), applies S_u T_m(.) + bias with the same chunk/MFMA scheme and
-//      resets the counter.  This is done for pure Walsh-Hadamard outputs
-//      (m a power of two, 256 <= m <= 8192); outputs with an odd factor run
-//      the chunk output kernel instead, one work-group per output chunk
-//      (qs_linear.hip), which spreads the K_p stage over many CUs.
+//      resets the counter.  This covers every m of the chunk scheme
+//      (m = p 2^k, 256 | m, m <= 12288): for a power of two the chunk stage
+//      M is a +-1 Hadamard and runs row-wise on the VALU; with an odd factor
+//      M = K_p (x) H is dense and runs on the matrix cores with operands
+//      split into bf16 hi + lo parts.
 //
 // Cross-work-group visibility.  Partial sums are written with agent-scope
 // relaxed atomic stores and read with agent-scope relaxed atomic loads, which
@@ -47,10 +48,11 @@ namespace qs {
 namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-__constant__ Table8 kE8P = make_e8p_table();
-__constant__ Table8 kE81 = make_e81_table();
+__constant__ Table8h kE8Ph = pack_table_f16(make_e8p_table());
+__constant__ Table8h kE81h = pack_table_f16(make_e81_table());
 
 constexpr int kThreads = 1024;
 constexpr int kMaxB = 2;
@@ -70,7 +72,8 @@ struct FusedJob {
   unsigned* counter;   // zero between launches
   float* xmul;         // [B] 2^e per batch row (for a separate output kernel)
   int out_in_kernel;
-  int Sm, lsh_m;
+  int Sm, lsh_m, pm;
+  const float* Km;     // pm x pm (pm > 1)
   float scale_m, layer_scale;
   const float* su;
   const float* bias;
@@ -100,14 +103,33 @@ constexpr int kOffHi = 0;                                   // 4096 x uint2
 constexpr int kOffLo = 32768;                               // 4096 x uint2
 constexpr int kOffLut1 = 65536;                             // 256 x uint4
 constexpr int kOffRed = kOffLut1 + 4096;                    // 2 x 16 x 16 x kMaxB floats
-constexpr int kOffK = kOffRed + 2 * kWaves * 16 * kMaxB * 4;  // p x p floats (p <= 64)
+constexpr int kMStride = 72;                                // bf16 per row of a chunk-stage matrix (16-byte rows)
+constexpr int kOffMin = kOffRed + 2 * kWaves * 16 * kMaxB * 4;  // 2 x 16 x kMStride bf16: input chunk stage (hi, lo)
 constexpr int kOffTab = kOffRed;                            // 256 x uint4 (table staging, before the row blocks)
-constexpr int kOffXH = kOffK + QS_MAX_KRON * QS_MAX_KRON * 4;  // kMaxB x 16 x kXStride halves
+constexpr int kOffXH = kOffMin + 2 * 16 * kMStride * 2;     // kMaxB x 16 x kXStride halves
 constexpr int kOffXS = kOffXH + kMaxB * 16 * kXStride * 2;  // kMaxB x 16 x 32 halves (group sums)
 constexpr int kOffY = kOffXS + kMaxB * 16 * 32 * 2;          // kMaxS x kYStride floats
 constexpr int kLdsBytes = kOffY + kMaxS * kYStride * 4;
 static_assert(kLdsBytes <= 160 * 1024 - 128, "LDS budget");
+// Output chunk stage (last work-group, the LUTs are dead): the chunk matrix
+// M as bf16 hi / lo parts, rows and columns padded with zeros.
+constexpr int kMRows = 48, kMCols = 64;
+constexpr int kOffMh = 0;
+constexpr int kOffMl = kOffMh + kMRows * kMStride * 2;
+static_assert(kOffMl + kMRows * kMStride * 2 <= kOffLut1, "M fits the LUT region");
+static_assert(kMRows >= kMaxS && kMCols >= kMaxS, "M covers every chunk count");
+static_assert(kMRows * kMCols == 3 * 1024 && kCPW == 3, "three M entries / output rows per thread");
 static_assert(2 * kWaves * 16 * kMaxB * 4 >= 4096, "table staging fits the reduction buffer");
+
+// Two floats as bf16 pairs: the truncated high parts and the (truncated)
+// remainders, so a + b products from hi*hi + hi*lo + lo*hi carry ~16 bits.
+__device__ __forceinline__ void split_bf2(float a, float b, uint32_t& hi, uint32_t& lo) {
+  const uint32_t ua = __float_as_uint(a), ub = __float_as_uint(b);
+  const uint32_t ha = ua & 0xFFFF0000u, hb = ub & 0xFFFF0000u;
+  const uint32_t la = __float_as_uint(a - __uint_as_float(ha)), lb = __float_as_uint(b - __uint_as_float(hb));
+  hi = (ha >> 16) | hb;
+  lo = (la >> 16) | (lb & 0xFFFF0000u);
+}
 
 __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
   _Float16 a = (_Float16)lo, b = (_Float16)hi;
@@ -164,6 +186,118 @@ __device__ __forceinline__ void store_chunks(float* Y, int S, int w, int lane, c
   }
 }
 
+// Chunk stage on the matrix cores.  For 16 rows of a chunk matrix M (bf16 hi
+// / lo rows of kMStride in LDS, zero past the S chunks) and chunk rows Z in
+// LDS (kYStride floats), lane (q, r16) of a wave owning column t accumulates
+// acc[j] = sum_c M[row0 + 4 q + j][c] Z[c][t] over k-steps of 32 chunks.  Both operands are split into
+// bf16 hi + lo and multiplied as hi*hi + hi*lo (+ lo*hi when M has a low
+// part), fp32 accumulate: ~16 significant bits per product.
+struct ZOperand {
+  bf16x8 h, l;  // Z[c][t], c = 32 kb + 8 q + i
+};
+
+__device__ __forceinline__ ZOperand z_operand(const float* Z, int S, int t, int q, int kb) {
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c0 = 32 * kb + 8 * q + 2 * i;
+    const float z0 = c0 < S ? Z[c0 * kYStride + t] : 0.0f;
+    const float z1 = c0 + 1 < S ? Z[(c0 + 1) * kYStride + t] : 0.0f;
+    split_bf2(z0, z1, h[i], l[i]);
+  }
+  return ZOperand{__builtin_bit_cast(bf16x8, make_uint4(h[0], h[1], h[2], h[3])),
+                  __builtin_bit_cast(bf16x8, make_uint4(l[0], l[1], l[2], l[3]))};
+}
+
+// acc += M[row0 + r16][32 kb + 8 q ..] x z (the k-step kb of a tile).
+__device__ __forceinline__ floatx4 mstage_step(floatx4 acc, const uint16_t* Mh, const uint16_t* Ml, int row0,
+                                               const ZOperand& z, int kb, bool m_lo, int q, int r16) {
+  const int off = (row0 + r16) * kMStride + 32 * kb + 8 * q;
+  const bf16x8 ah = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(Mh + off));
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, z.h, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, z.l, acc, 0, 0, 0);
+  if (m_lo) {
+    const bf16x8 al = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(Ml + off));
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, z.h, acc, 0, 0, 0);
+  }
+  return acc;
+}
+
+// Chunks held as element t = lane + 64 j (the layout of load_partials).
+__device__ __forceinline__ void store_chunks_lanes(float* Y, int S, int w, int lane, const float (&v)[kCPW][4]) {
+#pragma unroll
+  for (int u = 0; u < kCPW; ++u) {
+    const int c = w + kWaves * u;
+    if (c < S) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) Y[c * kYStride + lane + 64 * j] = v[u][j];
+    }
+  }
+}
+
+constexpr int kMaxSG = (kMaxS + kWaves - 1) / kWaves;  // column groups of the partial sums
+
+// Partial sums of batch row b, summed over the column groups, for the chunks
+// c = w + 16 u of this wave, as element t = lane + 64 j (each load
+// instruction reads 256 contiguous bytes).  Every load is issued before the
+// first one is used.  (The 256-point transform is the same for any
+// assignment of the index bits to lanes and registers.)
+__device__ __forceinline__ void load_partials(const FusedJob& J, int SG, int B, int b, int w, int lane,
+                                              float (&zv)[kCPW][4]) {
+  float tmp[kMaxSG][kCPW][4];
+#pragma unroll
+  for (int g = 0; g < kMaxSG; ++g)
+#pragma unroll
+    for (int u = 0; u < kCPW; ++u) {
+      const int c = w + kWaves * u;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) tmp[g][u][j] = 0.0f;
+      if (g < SG && c < J.Sm) {
+        const float* src = J.y1p + ((size_t)g * B + b) * J.m + 256 * c + lane;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          tmp[g][u][j] = __hip_atomic_load(src + 64 * j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+#pragma unroll
+  for (int u = 0; u < kCPW; ++u)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float v = tmp[0][u][j];
+#pragma unroll
+      for (int g = 1; g < kMaxSG; ++g) v += tmp[g][u][j];
+      zv[u][j] = v;
+    }
+}
+
+// Output values out[a][j] to y[base + idx[a][j]] (idx < 0: no output), one
+// dtype dispatch for all of them.
+__device__ __forceinline__ void store_outputs(void* y, int dtype, int64_t base, const int (&idx)[3][4],
+                                              const float (&out)[3][4]) {
+  if (dtype == QS_DTYPE_F32) {
+    float* p = static_cast<float*>(y) + base;
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (idx[a][j] >= 0) p[idx[a][j]] = out[a][j];
+  } else if (dtype == QS_DTYPE_F16) {
+    _Float16* p = static_cast<_Float16*>(y) + base;
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (idx[a][j] >= 0) p[idx[a][j]] = (_Float16)out[a][j];
+  } else {
+    uint16_t* p = static_cast<uint16_t*>(y) + base;
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (idx[a][j] >= 0) p[idx[a][j]] = f32_to_bf16(out[a][j]);
+  }
+}
+
 template <bool HAS2>
 __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
@@ -172,7 +306,8 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   uint4* lut1 = reinterpret_cast<uint4*>(lds + kOffLut1);
   uint4* tab16 = reinterpret_cast<uint4*>(lds + kOffTab);
   float* red = reinterpret_cast<float*>(lds + kOffRed);
-  float* Ks = reinterpret_cast<float*>(lds + kOffK);
+  uint16_t* MinH = reinterpret_cast<uint16_t*>(lds + kOffMin);
+  uint16_t* MinL = MinH + 16 * kMStride;
   _Float16* XH = reinterpret_cast<_Float16*>(lds + kOffXH);
   _Float16* XS = reinterpret_cast<_Float16*>(lds + kOffXS);
   float* Y = reinterpret_cast<float*>(lds + kOffY);
@@ -198,18 +333,15 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   //    abs table and K; the code tiles once the activations are in
   float xv[kCPW][4];
   load_x(A, J.sv, 0, w, lane, xv);
-  float trow[8], t1row[8];
+  uint4 trow = make_uint4(0, 0, 0, 0), t1row = make_uint4(0, 0, 0, 0);  // fp16 table rows
   if (tid < 256) {
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      trow[k] = kE8P.v[tid][k];
-      if (HAS2) t1row[k] = kE81.v[tid][k];
-    }
+    trow = *reinterpret_cast<const uint4*>(kE8Ph.w[tid]);
+    if (HAS2) t1row = *reinterpret_cast<const uint4*>(kE81h.w[tid]);
   }
-  float kv[4];
-  const int pp = A.pn * A.pn;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) kv[k] = (A.pn > 1 && tid + kThreads * k < pp) ? A.Kn[tid + kThreads * k] : 0.0f;
+  // this wave's row of the input chunk stage: M[sl][c] for c = lane (Sn <= 48)
+  const bool m_ok = active && lane < A.Sn;
+  float mk = 1.0f;
+  if (A.pn > 1 && m_ok) mk = A.Kn[(sl >> A.lsh_n) * A.pn + (lane >> A.lsh_n)];
   uint4 pre[kPrefetch];
   uint2 pre1[kPrefetch];
 
@@ -222,7 +354,12 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
     for (int u = 0; u < kCPW; ++u)
 #pragma unroll
       for (int j = 0; j < 4; ++j) ss = __builtin_fmaf(xv[u][j], xv[u][j], ss);
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+    ss += lane_xor<32>(ss, lx);
+    ss += lane_xor<16>(ss, lx);
+    ss += lane_xor<8>(ss, lx);
+    ss += lane_xor<4>(ss, lx);
+    ss += lane_xor<2>(ss, lx);
+    ss += lane_xor<1>(ss, lx);
     if (lane == 0) wsum[w] = ss;
     h256_chunks(xv, A.Sn, lane, lx);
     if (b == 0) {
@@ -241,15 +378,17 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
       }
       // table staging and K (read after the barrier below)
       if (tid < 256) {
-        tab16[tid] = make_uint4(pack_h2(trow[0], trow[1]), pack_h2(trow[2], trow[3]), pack_h2(trow[4], trow[5]),
-                                pack_h2(trow[6], trow[7]));
-        if (HAS2)
-          lut1[tid] = make_uint4(pack_h2(t1row[0], t1row[1]), pack_h2(t1row[2], t1row[3]),
-                                 pack_h2(t1row[4], t1row[5]), pack_h2(t1row[6], t1row[7]));
+        tab16[tid] = trow;
+        if (HAS2) lut1[tid] = t1row;
       }
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        if (A.pn > 1 && tid + kThreads * k < pp) Ks[tid + kThreads * k] = kv[k];
+      {
+        const int hm = (1 << A.lsh_n) - 1;
+        const float v = m_ok ? ((__builtin_popcount(sl & lane & hm) & 1) ? -mk : mk) : 0.0f;
+        uint32_t hi, lo;
+        split_bf2(v, 0.0f, hi, lo);
+        MinH[w * kMStride + lane] = (uint16_t)hi;
+        MinL[w * kMStride + lane] = (uint16_t)lo;
+      }
     }
     if (b > 0) __syncthreads();  // the previous row's reads of Y are done
     store_chunks(Y, A.Sn, w, lane, xv);
@@ -266,20 +405,32 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
     if (b == 0) emul0 = ldexpf(1.0f, e);
     else emul1 = ldexpf(1.0f, e);
     const float mul = ldexpf(A.scale_n, -e);
-    // this wave's slice row of M . Y: X2[sl][4 lane + j] = sum_c M[sl][c] Y[c][4 lane + j]
-    // (M[sl][c] is the same for the whole wave), as fp16 into the wave's own
-    // operand row
-    if (active) {
-      const float4 a = mrow_times_chunks(Y, A.Sn, sl, A.lsh_n, A.pn, Ks, lane);
-      const _Float16 h0 = (_Float16)(a.x * mul), h1 = (_Float16)(a.y * mul);
-      const _Float16 h2 = (_Float16)(a.z * mul), h3 = (_Float16)(a.w * mul);
-      const uint2 hv = make_uint2((uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16),
-                                  (uint32_t)__builtin_bit_cast(uint16_t, h2) | ((uint32_t)__builtin_bit_cast(uint16_t, h3) << 16));
-      *reinterpret_cast<uint2*>(XH + (b * 16 + w) * kXStride + 4 * lane) = hv;
-      // group sums of the fp16 values: group t / 8 spans lanes 2g and 2g + 1
-      const float s4 = ((float)h0 + (float)h1) + ((float)h2 + (float)h3);
-      const float s8 = s4 + lane_xor<1>(s4, lx);
-      if ((lane & 1) == 0) XS[(b * 16 + w) * 32 + (lane >> 1)] = (_Float16)s8;
+    // chunk stage for this group's 16 slice rows: X2[s][t] = sum_c
+    // M[sg W + s][c] Y[c][t]; wave w computes columns t = 16 w + r16, rows
+    // s = 4 q + j, and writes them as fp16 operand rows
+    {
+      const int t = 16 * w + r16;
+      floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int kb = 0; kb < ((A.Sn + 31) >> 5); ++kb)
+        acc = mstage_step(acc, MinH, MinL, 0, z_operand(Y, A.Sn, t, q, kb), kb, A.pn > 1, q, r16);
+      float hs[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const _Float16 h = (_Float16)(acc[j] * mul);
+        XH[(b * 16 + 4 * q + j) * kXStride + t] = h;
+        hs[j] = (float)h;
+      }
+      // group sums of the fp16 values, group t / 8: lanes r16 & 7 = 0..7
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        hs[j] += lane_xor<1>(hs[j], lx);
+        hs[j] += lane_xor<2>(hs[j], lx);
+        hs[j] += lane_xor<4>(hs[j], lx);
+      }
+      if ((r16 & 7) == 0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) XS[(b * 16 + 4 * q + j) * 32 + (t >> 3)] = (_Float16)hs[j];
+      }
     }
   }
   {
@@ -321,8 +472,8 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
     for (int c = 0; c < 8; ++c) slice_shift += (float)xs[c];
   }
   // slice total of S_g over the four q-lanes of batch row r16
-  slice_shift += __shfl_xor(slice_shift, 16);
-  slice_shift += __shfl_xor(slice_shift, 32);
+  slice_shift += lane_xor<16>(slice_shift, lx);
+  slice_shift += lane_xor<32>(slice_shift, lx);
   if (lb == 0 && tid < A.B) J.xmul[tid] = tid == 0 ? emul0 : emul1;
 
   // 3. row blocks
@@ -388,10 +539,10 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
       const int o = tid >> 4, ww = tid & 15;
       float v = 0.0f;
       if (o < 16 * A.B && ww < nw) v = rbuf[(ww * 16 + o / A.B) * kMaxB + (o % A.B)];
-      v += __shfl_xor(v, 1);
-      v += __shfl_xor(v, 2);
-      v += __shfl_xor(v, 4);
-      v += __shfl_xor(v, 8);
+      v += lane_xor<1>(v, lx);
+      v += lane_xor<2>(v, lx);
+      v += lane_xor<4>(v, lx);
+      v += lane_xor<8>(v, lx);
       if (o < 16 * A.B && ww == 0) {
         const int row = o / A.B, bc = o % A.B;
         __hip_atomic_store(&J.y1p[((size_t)sg * A.B + bc) * J.m + rb * 16 + row], v, __ATOMIC_RELAXED,
@@ -410,52 +561,80 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   __syncthreads();
   if (!s_last) return;
   {
-    // this lane's outputs: rows r = w + 16u (chunks of 256), columns 4 lane + j
-    float suv[kCPW][4], biv[kCPW][4];
+    // Output chunk stage on the matrix cores (mstage_tile): lane (q, r16) of
+    // wave w produces column t = 16 w + r16 of rows r = 16 a + 4 q + j.
+    const int Sm = J.Sm;
+    const int t = 16 * w + r16;
+    // Loads, in the order they are waited for: the K entries of M (odd
+    // factor), the partial sums of batch row 0, su and bias; all in flight
+    // together (unconditional loads from valid addresses, selected where they
+    // are used: a load under a branch is waited for at the branch's end).
+    float kmv[3];
 #pragma unroll
-    for (int u = 0; u < kCPW; ++u) {
-      const int r = w + kWaves * u;
+    for (int i = 0; i < 3; ++i) {
+      const int e = tid + kThreads * i, r = e / kMCols, c = e % kMCols;
+      kmv[i] = 1.0f;
+      if (J.pm > 1) kmv[i] = J.Km[(r < Sm && c < Sm) ? (r >> J.lsh_m) * J.pm + (c >> J.lsh_m) : 0];
+    }
+    float zv[kCPW][4];
+    load_partials(J, A.SG, A.B, 0, w, lane, zv);
+    int oidx[3][4];
+    float suo[3][4], bio[3][4];
+    const float* const bsrc = J.bias ? J.bias : J.su;
+    const float bsel = J.bias ? 1.0f : 0.0f;
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int i = 256 * r + 4 * lane + j;
-        const bool ok = r < J.Sm;
-        suv[u][j] = ok ? J.su[i] : 0.0f;
-        biv[u][j] = (ok && J.bias) ? J.bias[i] : 0.0f;
+        const int r = 16 * a + 4 * q + j;
+        oidx[a][j] = r < Sm ? 256 * r + t : -1;
+        const int ii = oidx[a][j] >= 0 ? oidx[a][j] : 0;
+        suo[a][j] = J.su[ii];
+        bio[a][j] = bsrc[ii];
+      }
+    // M = K_p (x) H_{2^lsh_m} as bf16 hi / lo, zero-padded to 48 x 64
+    uint16_t* Mh = reinterpret_cast<uint16_t*>(lds + kOffMh);
+    uint16_t* Ml = reinterpret_cast<uint16_t*>(lds + kOffMl);
+    {
+      const int hm = (1 << J.lsh_m) - 1;
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        const int e = tid + kThreads * i, r = e / kMCols, c = e % kMCols;
+        float v = (r < Sm && c < Sm) ? kmv[i] : 0.0f;
+        if (__builtin_popcount(r & c & hm) & 1) v = -v;
+        uint32_t hi, lo;
+        split_bf2(v, 0.0f, hi, lo);
+        Mh[r * kMStride + c] = (uint16_t)hi;
+        Ml[r * kMStride + c] = (uint16_t)lo;
       }
     }
+    void* const yp = J.y;
+    const int64_t ldy = J.ldy;
+    const int ydt = A.y_dtype;
+    const float mul0 = J.scale_m * J.layer_scale;
+    const int nrt = (Sm + 15) >> 4, nkb = (Sm + 31) >> 5;
     for (int b = 0; b < A.B; ++b) {
-      float zv[kCPW][4];
-#pragma unroll
-      for (int u = 0; u < kCPW; ++u) {
-        const int c = w + kWaves * u;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) zv[u][j] = 0.0f;
-        if (c < J.Sm) {
-          for (int g = 0; g < A.SG; ++g) {
-            const float* src = J.y1p + ((size_t)g * A.B + b) * J.m + 256 * c + 4 * lane;
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              zv[u][j] += __hip_atomic_load(src + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          }
-        }
-      }
-      h256_chunks(zv, J.Sm, lane, lx);
+      if (b > 0) load_partials(J, A.SG, A.B, b, w, lane, zv);
+      h256_chunks(zv, Sm, lane, lx);
       if (b > 0) __syncthreads();  // the previous row's reads of Y are done
-      store_chunks(Y, J.Sm, w, lane, zv);
-      __syncthreads();  // chunks complete
-      const float mul = J.scale_m * J.layer_scale * (b == 0 ? emul0 : emul1);
+      store_chunks_lanes(Y, Sm, w, lane, zv);
+      __syncthreads();  // chunks (and, the first time, M) complete
+      const float mul = mul0 * (b == 0 ? emul0 : emul1);
+      floatx4 acc[3];
 #pragma unroll
-      for (int u = 0; u < kCPW; ++u) {
-        const int r = w + kWaves * u;
-        if (r < J.Sm) {
-          const float4 av = mrow_times_chunks(Y, J.Sm, r, J.lsh_m, 1, nullptr, lane);
-          const float a[4] = {av.x, av.y, av.z, av.w};
+      for (int a = 0; a < 3; ++a) acc[a] = floatx4{0.f, 0.f, 0.f, 0.f};
+      for (int kb = 0; kb < nkb; ++kb) {
+        const ZOperand z = z_operand(Y, Sm, t, q, kb);
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
-            store_from_float(J.y, A.y_dtype, (int64_t)b * J.ldy + 256 * r + 4 * lane + j,
-                             a[j] * mul * suv[u][j] + biv[u][j]);
-        }
+        for (int a = 0; a < 3; ++a)
+          if (a < nrt) acc[a] = mstage_step(acc[a], Mh, Ml, 16 * a, z, kb, J.pm > 1, q, r16);
       }
+      float out[3][4];
+#pragma unroll
+      for (int a = 0; a < 3; ++a)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) out[a][j] = acc[a][j] * mul * suo[a][j] + bsel * bio[a][j];
+      store_outputs(yp, ydt, (int64_t)b * ldy, oidx, out);
     }
   }
   if (tid == 0) __hip_atomic_store(J.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -514,11 +693,13 @@ int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, i
     J.y1p = d.y1p;
     J.counter = d.counter;
     J.xmul = d.xmul;
-    J.out_in_kernel = d.pm == 1 && chunk_transform_fits(d.m, d.pm);
+    J.out_in_kernel = chunk_transform_fits(d.m, d.pm);
     if (J.out_in_kernel) {
       J.Sm = (int)(d.m / 256);
-      J.lsh_m = log2_exact(d.m / 256);
+      J.lsh_m = log2_exact(d.m / d.pm / 256);
     }
+    J.pm = d.pm;
+    J.Km = d.Km;
     J.scale_m = inv_sqrt_len(d.m / d.pm);
     J.layer_scale = d.layer_scale;
     J.su = d.su;
@@ -544,7 +725,7 @@ int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, i
   return QS_OK;
 }
 
-bool fused_output_in_kernel(int64_t m, int pm) { return pm == 1 && chunk_transform_fits(m, pm); }
+bool fused_output_in_kernel(int64_t m, int pm) { return chunk_transform_fits(m, pm); }
 
 bool fused_eligible(int64_t batch, int64_t n, int64_t m, int pn) {
   (void)m;
