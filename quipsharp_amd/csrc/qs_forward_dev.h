@@ -1,0 +1,343 @@
+// Device building blocks shared by the forward kernels on the chunk scheme:
+// the one-launch kernel (qs_linear_fused.hip) and the batched input /
+// decode-matvec / output kernels (qs_linear_batched.hip).  Work-groups are
+// 16 waves of 64 lanes (1024 threads).
+#pragma once
+
+#include "qs_chunk_dev.h"
+
+namespace qs {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+namespace {
+// E8P abs table and E8 one-bit table rows as fp16 pairs (Table8h).
+__constant__ Table8h kE8Ph = pack_table_f16(make_e8p_table());
+__constant__ Table8h kE81h = pack_table_f16(make_e81_table());
+}  // namespace
+
+constexpr int kFwdThreads = 1024;
+
+// ---------------------------------------------------------------------------
+// Signed half-codeword LUTs, one byte per value
+// ---------------------------------------------------------------------------
+// Every E8P value is +-(k + 1/2), k < 4, whose fp16 pattern has a zero low
+// byte, so a LUT entry holds the four high bytes of a half codeword and
+// v_perm_b32 rebuilds the fp16 pairs.
+constexpr bool e8p_low_bytes_zero() {
+  for (int r = 0; r < 256; ++r)
+    for (int i = 0; i < 8; ++i)
+      if (f16_bits_exact(kE8PHost.v[r][i]) & 0xFF) return false;
+  return true;
+}
+static_assert(e8p_low_bytes_zero(), "E8P values are fp16 high bytes only");
+
+// fp16 pairs (values 0,1 and 2,3) from the four high bytes of a LUT entry.
+__device__ __forceinline__ uint32_t lut_pair_lo(uint32_t e) { return __builtin_amdgcn_perm(0u, e, 0x010C000Cu); }
+__device__ __forceinline__ uint32_t lut_pair_hi(uint32_t e) { return __builtin_amdgcn_perm(0u, e, 0x030C020Cu); }
+
+// 32-bit LDS word at byte address a.  For kernels without static LDS the
+// dynamic LDS starts at address 0 (their launchers check this), so a LUT
+// offset is the LDS address itself.
+typedef const __attribute__((address_space(3))) uint32_t* lds_u32_ptr;
+__device__ __forceinline__ uint32_t lds_word(uint32_t a) { return *reinterpret_cast<lds_u32_ptr>((size_t)a); }
+
+// Fills the two 4096-entry LUTs from the fp16 abs table staged in LDS
+// (tab16[256], uint4 rows), 1024 threads.  Entry e = tid + 1024 k of hi:
+// abs row e & 255, flip nibble H = e >> 8 = (f1 f2 f3 q), f0 = q^f1^f2^f3;
+// of lo: abs row (e >> 3) & 255, f4..f6 = e & 7, q = e >> 11, coordinate 7
+// flipped by q^f4^f5^f6.  A sign flip of value v is bit 7 of byte v (mod 4).
+__device__ __forceinline__ void fill_luts(const uint4* tab16, uint32_t* lut_hi, uint32_t* lut_lo, int tid) {
+  const uint4 th = tab16[tid & 255];
+  const uint32_t hh = __builtin_amdgcn_perm(th.y, th.x, 0x07050301u);  // high bytes of values 0..3
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t H = (uint32_t)(tid >> 8) + 4u * k;
+    const uint32_t f1 = (H >> 3) & 1, f2 = (H >> 2) & 1, f3 = (H >> 1) & 1;
+    const uint32_t f0 = (H & 1) ^ f1 ^ f2 ^ f3;
+    lut_hi[tid + kFwdThreads * k] = hh ^ ((f0 << 7) | (f1 << 15) | (f2 << 23) | (f3 << 31));
+  }
+  const uint32_t f4 = (tid >> 2) & 1, f5 = (tid >> 1) & 1, f6 = tid & 1;
+  const uint32_t m456 = (f4 << 7) | (f5 << 15) | (f6 << 23), p456 = f4 ^ f5 ^ f6;
+  const uint4 ta = tab16[(tid >> 3) & 255], tb = tab16[((tid >> 3) + 128) & 255];
+  const uint32_t la = __builtin_amdgcn_perm(ta.w, ta.z, 0x07050301u);  // high bytes of values 4..7
+  const uint32_t lb = __builtin_amdgcn_perm(tb.w, tb.z, 0x07050301u);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t f7 = (uint32_t)(k >> 1) ^ p456;
+    lut_lo[tid + kFwdThreads * k] = ((k & 1) ? lb : la) ^ m456 ^ (f7 << 31);
+  }
+}
+
+// MFMA A operand (8 fp16 values) of code word c (c odd: the upper 16 bits of
+// wv) from the LUTs at LDS addresses off_hi / off_lo.
+__device__ __forceinline__ half8 decode_code(uint32_t wv, int c, uint32_t off_hi, uint32_t off_lo) {
+  const uint32_t ha = (c & 1) ? ((wv >> 18) & 0x3FFCu) : ((wv >> 2) & 0x3FFCu);
+  const uint32_t la = (c & 1) ? ((wv >> 15) & 0x3FFCu) : ((wv << 1) & 0x3FFCu);
+  const uint32_t hv = lds_word(off_hi + ha);
+  const uint32_t lv = lds_word(off_lo + la);
+  return __builtin_bit_cast(half8, make_uint4(lut_pair_lo(hv), lut_pair_hi(hv), lut_pair_lo(lv), lut_pair_hi(lv)));
+}
+
+// fp16 shift operand of a tile: 1.0 where a code's shift bit is set.
+__device__ __forceinline__ half8 shift_operand(const uint32_t (&wd)[4]) {
+  return __builtin_bit_cast(half8, make_uint4((wd[0] & 0x10001u) * 0x3C00u, (wd[1] & 0x10001u) * 0x3C00u,
+                                              (wd[2] & 0x10001u) * 0x3C00u, (wd[3] & 0x10001u) * 0x3C00u));
+}
+
+// ---------------------------------------------------------------------------
+// Activation chunks
+// ---------------------------------------------------------------------------
+struct XSource {
+  const void* x;
+  int dtype;
+  int vec;  // rows of 4 elements can be loaded as one 8- or 16-byte word
+  int64_t ldx;
+  int S;    // chunks of 256
+};
+
+// Activation chunks of batch row b (times sv), chunk c = w + 16 u, as
+// element t = 4 lane + j.
+__device__ __forceinline__ void load_x(const XSource& X, const float* sv, int b, int w, int lane,
+                                       float (&v)[kCPW][4]) {
+#pragma unroll
+  for (int u = 0; u < kCPW; ++u) {
+    const int c = w + kWaves * u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[u][j] = 0.0f;
+    if (c < X.S) {
+      const int i0 = 256 * c + 4 * lane;
+      const float4 s = *reinterpret_cast<const float4*>(sv + i0);
+      const int64_t xi = (int64_t)b * X.ldx + i0;
+      float x0, x1, x2, x3;
+      if (X.vec && X.dtype == QS_DTYPE_F32) {
+        const float4 t = *reinterpret_cast<const float4*>(static_cast<const float*>(X.x) + xi);
+        x0 = t.x, x1 = t.y, x2 = t.z, x3 = t.w;
+      } else if (X.vec) {
+        const uint2 t = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(X.x) + xi);
+        if (X.dtype == QS_DTYPE_BF16) {
+          x0 = __uint_as_float(t.x << 16), x1 = __uint_as_float(t.x & 0xFFFF0000u);
+          x2 = __uint_as_float(t.y << 16), x3 = __uint_as_float(t.y & 0xFFFF0000u);
+        } else {
+          x0 = (float)__builtin_bit_cast(_Float16, (uint16_t)(t.x & 0xFFFFu));
+          x1 = (float)__builtin_bit_cast(_Float16, (uint16_t)(t.x >> 16));
+          x2 = (float)__builtin_bit_cast(_Float16, (uint16_t)(t.y & 0xFFFFu));
+          x3 = (float)__builtin_bit_cast(_Float16, (uint16_t)(t.y >> 16));
+        }
+      } else {
+        x0 = load_as_float(X.x, X.dtype, xi);
+        x1 = load_as_float(X.x, X.dtype, xi + 1);
+        x2 = load_as_float(X.x, X.dtype, xi + 2);
+        x3 = load_as_float(X.x, X.dtype, xi + 3);
+      }
+      v[u][0] = x0 * s.x;
+      v[u][1] = x1 * s.y;
+      v[u][2] = x2 * s.z;
+      v[u][3] = x3 * s.w;
+    }
+  }
+}
+
+// Chunks held as element t = 4 lane + j (the layout of load_x).
+__device__ __forceinline__ void store_chunks(float* Y, int S, int w, int lane, const float (&v)[kCPW][4]) {
+#pragma unroll
+  for (int u = 0; u < kCPW; ++u) {
+    const int c = w + kWaves * u;
+    if (c < S)
+      *reinterpret_cast<float4*>(Y + c * kYStride + 4 * lane) = make_float4(v[u][0], v[u][1], v[u][2], v[u][3]);
+  }
+}
+
+// Chunks held as element t = lane + 64 j (the layout of load_partials).
+__device__ __forceinline__ void store_chunks_lanes(float* Y, int S, int w, int lane, const float (&v)[kCPW][4]) {
+#pragma unroll
+  for (int u = 0; u < kCPW; ++u) {
+    const int c = w + kWaves * u;
+    if (c < S) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) Y[c * kYStride + lane + 64 * j] = v[u][j];
+    }
+  }
+}
+
+// Sum of a float over the 64 lanes of a wave (DPP / permlane exchanges).
+__device__ __forceinline__ float wave_sum(float v, LaneX lx) {
+  v += lane_xor<32>(v, lx);
+  v += lane_xor<16>(v, lx);
+  v += lane_xor<8>(v, lx);
+  v += lane_xor<4>(v, lx);
+  v += lane_xor<2>(v, lx);
+  v += lane_xor<1>(v, lx);
+  return v;
+}
+
+// 2^e with |x2_i| <= ||x|| 2^-e < 2^14 for the fp16 operand of a row of
+// squared norm norm2 (e = 0 for a zero or non-finite norm).
+__device__ __forceinline__ int operand_exponent(float norm2) {
+  int e = 0;
+  if (norm2 > 0.0f && norm2 < INFINITY) {
+    int ex;
+    frexpf(sqrtf(norm2) * 1.0001f, &ex);
+    e = ex - 14;
+  }
+  return e;
+}
+
+// ---------------------------------------------------------------------------
+// Chunk stage on the matrix cores
+// ---------------------------------------------------------------------------
+// For 16 rows of a chunk matrix M (bf16 hi / lo rows of kMStride in LDS, zero
+// past the S chunks) and chunk rows Z in LDS (kYStride floats), lane (q, r16)
+// of a wave owning column t accumulates acc[j] = sum_c M[row0 + 4 q + j][c]
+// Z[c][t] over k-steps of 32 chunks.  Both operands are split into bf16
+// hi + lo and multiplied as hi*hi + hi*lo (+ lo*hi when M has a low part),
+// fp32 accumulate: ~16 significant bits per product.
+constexpr int kMStride = 72;                 // bf16 per row (16-byte aligned rows)
+constexpr int kMRows = 48, kMCols = 64;      // a full chunk matrix, S <= 48
+constexpr int kMBytes = kMRows * kMStride * 2;  // one of hi / lo
+static_assert(kMRows >= kMaxS && kMCols >= kMaxS, "M covers every chunk count");
+static_assert(kMRows * kMCols == 3 * kFwdThreads && kCPW == 3, "three M entries / output rows per thread");
+
+// Two floats as bf16 pairs: the truncated high parts and the (truncated)
+// remainders.
+__device__ __forceinline__ void split_bf2(float a, float b, uint32_t& hi, uint32_t& lo) {
+  const uint32_t ua = __float_as_uint(a), ub = __float_as_uint(b);
+  const uint32_t ha = ua & 0xFFFF0000u, hb = ub & 0xFFFF0000u;
+  const uint32_t la = __float_as_uint(a - __uint_as_float(ha)), lb = __float_as_uint(b - __uint_as_float(hb));
+  hi = (ha >> 16) | hb;
+  lo = (la >> 16) | (lb & 0xFFFF0000u);
+}
+
+struct ZOperand {
+  bf16x8 h, l;  // Z[c][t], c = 32 kb + 8 q + i
+};
+
+__device__ __forceinline__ ZOperand z_operand(const float* Z, int S, int t, int q, int kb) {
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c0 = 32 * kb + 8 * q + 2 * i;
+    const float z0 = c0 < S ? Z[c0 * kYStride + t] : 0.0f;
+    const float z1 = c0 + 1 < S ? Z[(c0 + 1) * kYStride + t] : 0.0f;
+    split_bf2(z0, z1, h[i], l[i]);
+  }
+  return ZOperand{__builtin_bit_cast(bf16x8, make_uint4(h[0], h[1], h[2], h[3])),
+                  __builtin_bit_cast(bf16x8, make_uint4(l[0], l[1], l[2], l[3]))};
+}
+
+// acc += M[row0 + r16][32 kb + 8 q ..] x z (the k-step kb of a tile).
+__device__ __forceinline__ floatx4 mstage_step(floatx4 acc, const uint16_t* Mh, const uint16_t* Ml, int row0,
+                                               const ZOperand& z, int kb, bool m_lo, int q, int r16) {
+  const int off = (row0 + r16) * kMStride + 32 * kb + 8 * q;
+  const bf16x8 ah = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(Mh + off));
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, z.h, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, z.l, acc, 0, 0, 0);
+  if (m_lo) {
+    const bf16x8 al = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(Ml + off));
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, z.h, acc, 0, 0, 0);
+  }
+  return acc;
+}
+
+// The K entries of a full chunk matrix M = K_p (x) H_{2^lsh} (S x S) that
+// thread tid writes (entries e = tid + 1024 i, row e / 64, column e % 64);
+// loads only, so they can be issued ahead of other loads.
+__device__ __forceinline__ void mmat_load(float (&kv)[3], int S, int lsh, int p, const float* K, int tid) {
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const int e = tid + kFwdThreads * i, r = e / kMCols, c = e % kMCols;
+    kv[i] = 1.0f;
+    if (p > 1) kv[i] = K[(r < S && c < S) ? (r >> lsh) * p + (c >> lsh) : 0];
+  }
+}
+
+// Writes those entries (times the Hadamard signs, zero outside S x S) as
+// bf16 hi / lo.
+__device__ __forceinline__ void mmat_store(const float (&kv)[3], int S, int lsh, uint16_t* Mh, uint16_t* Ml,
+                                           int tid) {
+  const int hm = (1 << lsh) - 1;
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const int e = tid + kFwdThreads * i, r = e / kMCols, c = e % kMCols;
+    float v = (r < S && c < S) ? kv[i] : 0.0f;
+    if (__builtin_popcount(r & c & hm) & 1) v = -v;
+    uint32_t hi, lo;
+    split_bf2(v, 0.0f, hi, lo);
+    Mh[r * kMStride + c] = (uint16_t)hi;
+    Ml[r * kMStride + c] = (uint16_t)lo;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Output side
+// ---------------------------------------------------------------------------
+constexpr int kMaxSG = (kMaxS + kWaves - 1) / kWaves;  // column groups of the partial sums
+
+// Partial sums y1p[g][b][.] of batch row b (B rows per group), summed over
+// the SG column groups, for the chunks c = w + 16 u < Sm of this wave, as
+// element t = lane + 64 j (each load instruction reads 256 contiguous bytes).
+// Every load is issued before the first one is used.  ATOMIC: agent-scope
+// loads (partials written by other work-groups of the same launch).  (The
+// 256-point transform is the same for any assignment of the index bits to
+// lanes and registers.)
+template <bool ATOMIC>
+__device__ __forceinline__ void load_partials(const float* y1p, int m, int Sm, int SG, int B, int b, int w,
+                                              int lane, float (&zv)[kCPW][4]) {
+  float tmp[kMaxSG][kCPW][4];
+#pragma unroll
+  for (int g = 0; g < kMaxSG; ++g)
+#pragma unroll
+    for (int u = 0; u < kCPW; ++u) {
+      const int c = w + kWaves * u;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) tmp[g][u][j] = 0.0f;
+      if (g < SG && c < Sm) {
+        const float* src = y1p + ((size_t)g * B + b) * m + 256 * c + lane;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          tmp[g][u][j] = ATOMIC ? __hip_atomic_load(src + 64 * j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                : src[64 * j];
+      }
+    }
+#pragma unroll
+  for (int u = 0; u < kCPW; ++u)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float v = tmp[0][u][j];
+#pragma unroll
+      for (int g = 1; g < kMaxSG; ++g) v += tmp[g][u][j];
+      zv[u][j] = v;
+    }
+}
+
+// Output values out[a][j] to y[base + idx[a][j]] (idx < 0: no output), one
+// dtype dispatch for all of them.
+__device__ __forceinline__ void store_outputs(void* y, int dtype, int64_t base, const int (&idx)[3][4],
+                                              const float (&out)[3][4]) {
+  if (dtype == QS_DTYPE_F32) {
+    float* p = static_cast<float*>(y) + base;
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (idx[a][j] >= 0) p[idx[a][j]] = out[a][j];
+  } else if (dtype == QS_DTYPE_F16) {
+    _Float16* p = static_cast<_Float16*>(y) + base;
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (idx[a][j] >= 0) p[idx[a][j]] = (_Float16)out[a][j];
+  } else {
+    uint16_t* p = static_cast<uint16_t*>(y) + base;
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (idx[a][j] >= 0) p[idx[a][j]] = f32_to_bf16(out[a][j]);
+  }
+}
+
+}  // namespace qs

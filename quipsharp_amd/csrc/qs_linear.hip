@@ -759,6 +759,47 @@ static int forward_batched(const void* x, int x_dtype, int64_t ldx, int64_t batc
                     float layer_scale, const float* bias, void* y, int y_dtype, int64_t ldy, char* ws,
                     const WsLayout& W, void* mv_begin, void* mv_end, hipStream_t s, bool identity) {
   int rc = QS_OK;
+  if (!identity && layout == QS_LAYOUT_TILED && batched_eligible(n, kron_pn, m, kron_pm) &&
+      (reinterpret_cast<uintptr_t>(sv) & 15) == 0) {
+    // chunk-scheme passes of up to 16 rows (qs_linear_batched.hip)
+    for (int64_t b0 = 0; b0 < batch; b0 += kMaxTileBatch) {
+      BatchedPass P{};
+      P.B = (int)(batch - b0 < kMaxTileBatch ? batch - b0 : kMaxTileBatch);
+      P.x = static_cast<const char*>(x) + (size_t)b0 * ldx * dtype_bytes(x_dtype);
+      P.x_dtype = x_dtype;
+      P.ldx = ldx;
+      P.n = n;
+      P.m = m;
+      P.pn = kron_pn;
+      P.pm = kron_pm;
+      P.Kn = kron_n;
+      P.Km = kron_m;
+      P.sv = sv;
+      P.su = su;
+      P.codes0 = codes0;
+      P.codes1 = codes1;
+      P.s0 = s0;
+      P.s1 = s1;
+      P.layer_scale = layer_scale;
+      P.bias = bias;
+      P.y = static_cast<char*>(y) + (size_t)b0 * ldy * dtype_bytes(y_dtype);
+      P.y_dtype = y_dtype;
+      P.ldy = ldy;
+      P.S = W.S;
+      P.SG = W.SG;
+      P.W = W.W;
+      P.ncu = cu_count();
+      P.x2h = reinterpret_cast<_Float16*>(ws + W.x2h);
+      P.sg = reinterpret_cast<_Float16*>(ws + W.sg);
+      P.xmul = reinterpret_cast<float*>(ws + W.xmul);
+      P.y1p = reinterpret_cast<float*>(ws + W.y1p);
+      hipEvent_t ev0 = b0 == 0 ? reinterpret_cast<hipEvent_t>(mv_begin) : nullptr;
+      hipEvent_t ev1 = b0 + kMaxTileBatch >= batch ? reinterpret_cast<hipEvent_t>(mv_end) : nullptr;
+      rc = launch_linear_batched(P, s, ev0, ev1);
+      if (rc) return rc;
+    }
+    return QS_OK;
+  }
   const int Ln = identity ? 1 : (int)(n / kron_pn);
   const size_t xin_lds = ((size_t)padded_len((int)n) + (size_t)kron_pn * kron_pn) * 4;
   const int Gx = identity ? 1 : parts_for(n, kron_pn);

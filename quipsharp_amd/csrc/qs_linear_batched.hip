@@ -1,0 +1,458 @@
+// Quantized-linear forward for batches of 3..16 rows per pass (prefill
+// chunks, batched decode), the path QuantizedLinear.forward takes for more
+// than two activation rows (quipsharp/checkpoint.py:141-146 ->
+// quipsharp/quantize.py:116-124), on the chunk scheme of qs_chunk_dev.h.
+// Three launches per pass:
+//   bx_kernel  input transform, one work-group per batch row: activation
+//              chunks times S_v, 256-point transforms in registers, the chunk
+//              stage on the matrix cores, fp16 operand (scaled by 2^-e from the
+//              row norm) and its group sums to the workspace;
+//   bm_kernel  decode-matvec: work-group j owns one slice group (one 256-column
+//              slice per wave) and a strided set of 16-row blocks; each wave's
+//              operand (16 batch rows of its slice) stays in registers, codes
+//              stream through a 4-tile prefetch ring, the byte-per-value LUTs
+//              feed 16x16x32 MFMAs with all 16 batch columns in use, and the
+//              per-wave partials are reduced across the waves every two row
+//              blocks into the workspace;
+//   by_kernel  output transform, one work-group per batch row: partial sums,
+//              256-point transforms, chunk stage on the matrix cores,
+//              S_u (.) * scales + bias.
+#include <hip/hip_ext.h>
+
+#include "qs_forward_dev.h"
+#include "qs_linear_dev.h"
+
+namespace qs {
+namespace {
+
+constexpr int kThreads = kFwdThreads;
+constexpr int kTB = 16;  // batch rows per pass (the MFMA N dimension)
+constexpr int kPrefetch = 4;
+
+// ---------------------------------------------------------------------------
+// input transform
+// ---------------------------------------------------------------------------
+struct BxArgs {
+  const void* x;
+  int x_dtype, x_vec;
+  int64_t ldx;
+  int n, Sn, lsh_n, pn;
+  const float* Kn;
+  float scale_n;
+  const float* sv;
+  _Float16* x2h;  // [B][n] fp16 operand, index 256 slice + t
+  _Float16* sg;   // [B][n / 8] sums of 8 consecutive operand values
+  float* xmul;    // [B] 2^e
+};
+
+constexpr int kBxOffY = 0;                                  // kMaxS x kYStride floats
+constexpr int kBxOffMh = kBxOffY + kMaxS * kYStride * 4;
+constexpr int kBxOffMl = kBxOffMh + kMBytes;
+constexpr int kBxOffMisc = kBxOffMl + kMBytes;              // row norm parts
+constexpr int kBxLds = kBxOffMisc + 4 * kWaves;
+
+__global__ __launch_bounds__(kThreads) void bx_kernel(BxArgs A) {
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  float* Y = reinterpret_cast<float*>(lds + kBxOffY);
+  uint16_t* Mh = reinterpret_cast<uint16_t*>(lds + kBxOffMh);
+  uint16_t* Ml = reinterpret_cast<uint16_t*>(lds + kBxOffMl);
+  float* wsum = reinterpret_cast<float*>(lds + kBxOffMisc);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6;
+  const int q = lane >> 4, r16 = lane & 15;
+  const int b = blockIdx.x;
+  const LaneX lx = lane_x_init();
+
+  float xv[kCPW][4];
+  load_x(XSource{A.x, A.x_dtype, A.x_vec, A.ldx, A.Sn}, A.sv, b, w, lane, xv);
+  float kmv[3];
+  mmat_load(kmv, A.Sn, A.lsh_n, A.pn, A.Kn, tid);
+  float ss = 0.0f;
+#pragma unroll
+  for (int u = 0; u < kCPW; ++u)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ss = __builtin_fmaf(xv[u][j], xv[u][j], ss);
+  ss = wave_sum(ss, lx);
+  if (lane == 0) wsum[w] = ss;
+  h256_chunks(xv, A.Sn, lane, lx);
+  store_chunks(Y, A.Sn, w, lane, xv);
+  mmat_store(kmv, A.Sn, A.lsh_n, Mh, Ml, tid);
+  __syncthreads();
+  float norm2 = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) norm2 += wsum[i];
+  const int e = operand_exponent(norm2);
+  const float mul = ldexpf(A.scale_n, -e);
+  if (tid == 0) A.xmul[b] = ldexpf(1.0f, e);
+
+  // chunk stage: operand row (slice) s = 16 a + 4 q + j, column t = 16 w + r16
+  const int t = 16 * w + r16;
+  const int nrt = (A.Sn + 15) >> 4, nkb = (A.Sn + 31) >> 5;
+  floatx4 acc[3];
+#pragma unroll
+  for (int a = 0; a < 3; ++a) acc[a] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int kb = 0; kb < nkb; ++kb) {
+    const ZOperand z = z_operand(Y, A.Sn, t, q, kb);
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
+      if (a < nrt) acc[a] = mstage_step(acc[a], Mh, Ml, 16 * a, z, kb, A.pn > 1, q, r16);
+  }
+  _Float16* xrow = A.x2h + (size_t)b * A.n;
+  _Float16* srow = A.sg + (size_t)b * (A.n / 8);
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    if (a < nrt) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int s = 16 * a + 4 * q + j;
+        const _Float16 h = (_Float16)(acc[a][j] * mul);
+        // sum of the 8 fp16 values of group t / 8 (lanes r16 & 7 = 0..7)
+        float hs = (float)h;
+        hs += lane_xor<1>(hs, lx);
+        hs += lane_xor<2>(hs, lx);
+        hs += lane_xor<4>(hs, lx);
+        if (s < A.Sn) {
+          xrow[256 * s + t] = h;
+          if ((r16 & 7) == 0) srow[32 * s + (t >> 3)] = (_Float16)hs;
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// decode-matvec
+// ---------------------------------------------------------------------------
+struct BmArgs {
+  const uint16_t* codes0;
+  const uint8_t* codes1;
+  const _Float16* x2h;
+  const _Float16* sg;
+  float* y1p;  // [SG][B][m]
+  int m, n, B, S, SG, W, Gr;
+  int tpo;  // threads per output of the reduction: a power of two, tpo * kBmSlots * 16 * B <= 1024
+  float s0, s1;
+};
+
+constexpr int kBmSlots = 2;                  // row blocks reduced together
+constexpr int kBmSlot = kWaves * 16 * kTB;   // floats per slot: [wave][row][batch]
+constexpr int kBmOffHi = 0;                  // 4096 x uint32
+constexpr int kBmOffLo = 16384;              // 4096 x uint32
+constexpr int kBmOffLut1 = 32768;            // 256 x uint4
+constexpr int kBmOffTab = kBmOffLut1 + 4096; // 256 x uint4 (table staging)
+constexpr int kBmOffRed = kBmOffTab + 4096;  // kBmSlots x kBmSlot floats
+constexpr int kBmLds = kBmOffRed + kBmSlots * kBmSlot * 4;
+static_assert(kBmLds <= 160 * 1024, "LDS budget");
+
+template <bool HAS2>
+__global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  uint32_t* lut_hi = reinterpret_cast<uint32_t*>(lds + kBmOffHi);
+  uint32_t* lut_lo = reinterpret_cast<uint32_t*>(lds + kBmOffLo);
+  uint4* lut1 = reinterpret_cast<uint4*>(lds + kBmOffLut1);
+  uint4* tab16 = reinterpret_cast<uint4*>(lds + kBmOffTab);
+  float* red = reinterpret_cast<float*>(lds + kBmOffRed);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6;
+  const int q = lane >> 4, r16 = lane & 15;
+  const int RB = A.m >> 4;
+  const int sg = (int)blockIdx.x / A.Gr, jr = (int)blockIdx.x - sg * A.Gr;
+  const int sl = sg * A.W + w;
+  const bool active = w < A.W && sl < A.S;
+  const LaneX lx = lane_x_init();
+
+  // operand of lane (q, b = r16): columns 64 q .. 64 q + 63 of this wave's
+  // slice, and the sums of its eight groups of 8
+  const half8 hzero = {0, 0, 0, 0, 0, 0, 0, 0};
+  half8 xb[8];
+  half8 xs = hzero;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) xb[c] = hzero;
+  if (active && r16 < A.B) {
+    const _Float16* xrow = A.x2h + (size_t)r16 * A.n + 256 * sl + 64 * q;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) xb[c] = *reinterpret_cast<const half8*>(xrow + 8 * c);
+    xs = *reinterpret_cast<const half8*>(A.sg + (size_t)r16 * (A.n / 8) + 32 * sl + 8 * q);
+  }
+  uint4 pre[kPrefetch];
+  uint2 pre1[kPrefetch];
+#pragma unroll
+  for (int k = 0; k < kPrefetch; ++k) {
+    const int rb = jr + k * A.Gr;
+    pre[k] = make_uint4(0, 0, 0, 0);
+    pre1[k] = make_uint2(0, 0);
+    if (active && rb < RB) {
+      const size_t tile = ((size_t)rb * A.S + sl) * 64 + lane;
+      pre[k] = *reinterpret_cast<const uint4*>(A.codes0 + tile * 8);
+      if (HAS2) pre1[k] = *reinterpret_cast<const uint2*>(A.codes1 + tile * 8);
+    }
+  }
+  if (tid < 256) {
+    tab16[tid] = *reinterpret_cast<const uint4*>(kE8Ph.w[tid]);
+    if (HAS2) lut1[tid] = *reinterpret_cast<const uint4*>(kE81h.w[tid]);
+  }
+  __syncthreads();
+  fill_luts(tab16, lut_hi, lut_lo, tid);
+  __syncthreads();
+
+  float slice_shift = 0.0f;  // sum_g S_g over the slice, batch row r16
+#pragma unroll
+  for (int c = 0; c < 8; ++c) slice_shift += (float)xs[c];
+  slice_shift += lane_xor<16>(slice_shift, lx);
+  slice_shift += lane_xor<32>(slice_shift, lx);
+
+  const int nw = A.S - sg * A.W < A.W ? A.S - sg * A.W : A.W;
+  int k = 0;
+  for (int rb = jr; rb < RB; rb += A.Gr, ++k) {
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+    floatx4 accs = {0.f, 0.f, 0.f, 0.f};
+    floatx4 acc2 = {0.f, 0.f, 0.f, 0.f};
+    const uint4 cw = pre[0];
+    const uint2 cw1 = pre1[0];
+#pragma unroll
+    for (int j = 0; j + 1 < kPrefetch; ++j) {
+      pre[j] = pre[j + 1];
+      pre1[j] = pre1[j + 1];
+    }
+    {
+      const int rbn = rb + kPrefetch * A.Gr;
+      pre[kPrefetch - 1] = make_uint4(0, 0, 0, 0);
+      pre1[kPrefetch - 1] = make_uint2(0, 0);
+      if (active && rbn < RB) {
+        const size_t tile = ((size_t)rbn * A.S + sl) * 64 + lane;
+        pre[kPrefetch - 1] = *reinterpret_cast<const uint4*>(A.codes0 + tile * 8);
+        if (HAS2) pre1[kPrefetch - 1] = *reinterpret_cast<const uint2*>(A.codes1 + tile * 8);
+      }
+    }
+    if (active) {
+      const uint32_t wd[4] = {cw.x, cw.y, cw.z, cw.w};
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(decode_code(wd[c >> 1], c, kBmOffHi, kBmOffLo), xb[c], acc, 0,
+                                                     0, 0);
+        if (HAS2) {
+          const uint32_t idx = ((c < 4 ? cw1.x : cw1.y) >> (8 * (c & 3))) & 0xFFu;
+          acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, lut1[idx]), xb[c], acc2, 0, 0,
+                                                          0);
+        }
+      }
+      accs = __builtin_amdgcn_mfma_f32_16x16x32_f16(shift_operand(wd), xs, accs, 0, 0, 0);
+    }
+    // lane holds rows 4q..4q+3 of the tile for batch column r16
+    const int slot = k % kBmSlots;
+    float* rbuf = red + slot * kBmSlot;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float v = A.s0 * (acc[j] + 0.5f * accs[j] - 0.25f * slice_shift);
+      if (HAS2) v = v + A.s1 * acc2[j];
+      rbuf[(w * 16 + 4 * q + j) * kTB + r16] = active ? v : 0.0f;
+    }
+    if (slot == kBmSlots - 1 || rb + A.Gr >= RB) {
+      __syncthreads();
+      // output o = (s * 16 + row) * B + b of slot s <= slot, summed over the
+      // waves by tpo threads (waves part, part + tpo, ...), then across them;
+      // tpo depends on B only (a fixed summation order per output)
+      const int nout = (slot + 1) * 16 * A.B;
+      const int tpo = A.tpo;
+      const int o = tid / tpo, part = tid - o * tpo;
+      float v = 0.0f;
+      int s = 0, row = 0, bc = 0;
+      if (o < nout) {
+        s = o / (16 * A.B);
+        const int rr = o - s * 16 * A.B;
+        row = rr / A.B;
+        bc = rr - row * A.B;
+        for (int ww = part; ww < nw; ww += tpo) v += red[s * kBmSlot + (ww * 16 + row) * kTB + bc];
+      }
+      if (tpo >= 2) v += lane_xor<1>(v, lx);
+      if (tpo >= 4) v += lane_xor<2>(v, lx);
+      if (tpo >= 8) v += lane_xor<4>(v, lx);
+      if (tpo >= 16) v += lane_xor<8>(v, lx);
+      if (o < nout && part == 0) {
+        const int rbs = rb - (slot - s) * A.Gr;  // row block of slot s
+        A.y1p[((size_t)sg * A.B + bc) * A.m + rbs * 16 + row] = v;
+      }
+      __syncthreads();  // the slots are free again
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// output transform
+// ---------------------------------------------------------------------------
+struct ByArgs {
+  const float* y1p;  // [SG][B][m]
+  int SG, B, m, Sm, lsh_m, pm;
+  const float* Km;
+  const float* xmul;
+  float scale_m, layer_scale;
+  const float* su;
+  const float* bias;
+  void* y;
+  int y_dtype;
+  int64_t ldy;
+};
+
+constexpr int kByOffY = 0;
+constexpr int kByOffMh = kByOffY + kMaxS * kYStride * 4;
+constexpr int kByOffMl = kByOffMh + kMBytes;
+constexpr int kByLds = kByOffMl + kMBytes;
+
+__global__ __launch_bounds__(kThreads) void by_kernel(ByArgs A) {
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  float* Y = reinterpret_cast<float*>(lds + kByOffY);
+  uint16_t* Mh = reinterpret_cast<uint16_t*>(lds + kByOffMh);
+  uint16_t* Ml = reinterpret_cast<uint16_t*>(lds + kByOffMl);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6;
+  const int q = lane >> 4, r16 = lane & 15;
+  const int b = blockIdx.x;
+  const int Sm = A.Sm;
+  const int t = 16 * w + r16;
+  const LaneX lx = lane_x_init();
+
+  // loads in the order they are waited for: K entries of M, partial sums,
+  // su and bias (unconditional loads from valid addresses)
+  float kmv[3];
+  mmat_load(kmv, Sm, A.lsh_m, A.pm, A.Km, tid);
+  float zv[kCPW][4];
+  load_partials<false>(A.y1p, A.m, Sm, A.SG, A.B, b, w, lane, zv);
+  int oidx[3][4];
+  float suo[3][4], bio[3][4];
+  const float* const bsrc = A.bias ? A.bias : A.su;
+  const float bsel = A.bias ? 1.0f : 0.0f;
+#pragma unroll
+  for (int a = 0; a < 3; ++a)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = 16 * a + 4 * q + j;
+      oidx[a][j] = r < Sm ? 256 * r + t : -1;
+      const int ii = oidx[a][j] >= 0 ? oidx[a][j] : 0;
+      suo[a][j] = A.su[ii];
+      bio[a][j] = bsrc[ii];
+    }
+  const float mul = A.scale_m * A.layer_scale * A.xmul[b];
+  mmat_store(kmv, Sm, A.lsh_m, Mh, Ml, tid);
+  h256_chunks(zv, Sm, lane, lx);
+  store_chunks_lanes(Y, Sm, w, lane, zv);
+  __syncthreads();
+  const int nrt = (Sm + 15) >> 4, nkb = (Sm + 31) >> 5;
+  floatx4 acc[3];
+#pragma unroll
+  for (int a = 0; a < 3; ++a) acc[a] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int kb = 0; kb < nkb; ++kb) {
+    const ZOperand z = z_operand(Y, Sm, t, q, kb);
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
+      if (a < nrt) acc[a] = mstage_step(acc[a], Mh, Ml, 16 * a, z, kb, A.pm > 1, q, r16);
+  }
+  float out[3][4];
+#pragma unroll
+  for (int a = 0; a < 3; ++a)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) out[a][j] = acc[a][j] * mul * suo[a][j] + bsel * bio[a][j];
+  store_outputs(A.y, A.y_dtype, (int64_t)b * A.ldy, oidx, out);
+}
+
+int lds_checked(const void* fn, size_t bytes, int* done) {
+  if (!*done) {
+    hipFuncAttributes fa{};
+    QS_HIP(hipFuncGetAttributes(&fa, fn));
+    QS_REQUIRE(fa.sharedSizeBytes == 0, "batched forward kernels must not use static LDS");
+    QS_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes));
+    *done = 1;
+  }
+  return QS_OK;
+}
+
+}  // namespace
+
+bool batched_eligible(int64_t n, int pn, int64_t m, int pm) {
+  return chunk_transform_fits(n, pn) && chunk_transform_fits(m, pm);
+}
+
+int launch_linear_batched(const BatchedPass& P, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop) {
+  QS_REQUIRE(P.B >= 1 && P.B <= kTB, "batched pass: 1..%d rows", kTB);
+  QS_REQUIRE(batched_eligible(P.n, P.pn, P.m, P.pm), "batched pass: shapes outside the chunk scheme");
+  static int done_x = 0, done_m0 = 0, done_m1 = 0, done_y = 0;
+  int rc = lds_checked((const void*)bx_kernel, kBxLds, &done_x);
+  if (!rc) rc = lds_checked((const void*)bm_kernel<false>, kBmLds, &done_m0);
+  if (!rc) rc = lds_checked((const void*)bm_kernel<true>, kBmLds, &done_m1);
+  if (!rc) rc = lds_checked((const void*)by_kernel, kByLds, &done_y);
+  if (rc) return rc;
+
+  BxArgs X{};
+  X.x = P.x;
+  X.x_dtype = P.x_dtype;
+  {
+    const uintptr_t align = P.x_dtype == QS_DTYPE_F32 ? 16 : 8;
+    X.x_vec = (reinterpret_cast<uintptr_t>(P.x) % align) == 0 && P.ldx % 4 == 0;
+  }
+  X.ldx = P.ldx;
+  X.n = (int)P.n;
+  X.Sn = (int)(P.n / 256);
+  X.lsh_n = log2_exact((int)(P.n / P.pn / 256));
+  X.pn = P.pn;
+  X.Kn = P.Kn;
+  X.scale_n = inv_sqrt_len((int)(P.n / P.pn));
+  X.sv = P.sv;
+  X.x2h = P.x2h;
+  X.sg = P.sg;
+  X.xmul = P.xmul;
+  hipLaunchKernelGGL(bx_kernel, dim3(P.B), dim3(kThreads), kBxLds, stream, X);
+  QS_LAUNCHED("bx_kernel");
+
+  BmArgs M{};
+  M.codes0 = static_cast<const uint16_t*>(P.codes0);
+  M.codes1 = static_cast<const uint8_t*>(P.codes1);
+  M.x2h = P.x2h;
+  M.sg = P.sg;
+  M.y1p = P.y1p;
+  M.m = (int)P.m;
+  M.n = (int)P.n;
+  M.B = P.B;
+  M.S = P.S;
+  M.SG = P.SG;
+  M.W = P.W;
+  {
+    const int RB = (int)(P.m / 16);
+    int Gr = P.ncu / P.SG;
+    if (Gr < 1) Gr = 1;
+    if (Gr > RB) Gr = RB;
+    M.Gr = Gr;
+  }
+  M.tpo = 16;
+  while (M.tpo > 1 && M.tpo * kBmSlots * 16 * P.B > kThreads) M.tpo >>= 1;
+  M.s0 = P.s0;
+  M.s1 = P.s1;
+  const unsigned grid = (unsigned)(M.Gr * P.SG);
+  if (P.codes1)
+    hipExtLaunchKernelGGL(bm_kernel<true>, dim3(grid), dim3(kThreads), kBmLds, stream, ev_start, ev_stop, 0, M);
+  else
+    hipExtLaunchKernelGGL(bm_kernel<false>, dim3(grid), dim3(kThreads), kBmLds, stream, ev_start, ev_stop, 0, M);
+  QS_LAUNCHED("bm_kernel");
+
+  ByArgs Y{};
+  Y.y1p = P.y1p;
+  Y.SG = P.SG;
+  Y.B = P.B;
+  Y.m = (int)P.m;
+  Y.Sm = (int)(P.m / 256);
+  Y.lsh_m = log2_exact((int)(P.m / P.pm / 256));
+  Y.pm = P.pm;
+  Y.Km = P.Km;
+  Y.xmul = P.xmul;
+  Y.scale_m = inv_sqrt_len((int)(P.m / P.pm));
+  Y.layer_scale = P.layer_scale;
+  Y.su = P.su;
+  Y.bias = P.bias;
+  Y.y = P.y;
+  Y.y_dtype = P.y_dtype;
+  Y.ldy = P.ldy;
+  hipLaunchKernelGGL(by_kernel, dim3(P.B), dim3(kThreads), kByLds, stream, Y);
+  QS_LAUNCHED("by_kernel");
+  return QS_OK;
+}
+
+}  // namespace qs

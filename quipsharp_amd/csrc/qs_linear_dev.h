@@ -30,4 +30,33 @@ int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, i
 bool fused_eligible(int64_t batch, int64_t n, int64_t m, int pn);
 bool fused_output_in_kernel(int64_t m, int pm);
 
+// One pass (up to 16 rows) of the batched forward (qs_linear_batched.hip):
+// input transform, decode-matvec and output transform launches.
+struct BatchedPass {
+  const void* x;
+  int x_dtype;
+  int64_t ldx;
+  int B;                 // rows in this pass, 1..16
+  int64_t n, m;
+  int pn, pm;            // odd factors of n and m
+  const float* Kn;
+  const float* Km;
+  const float* sv;
+  const float* su;
+  const void* codes0;    // tiled layout
+  const void* codes1;    // E8 1-bit second stage or NULL
+  float s0, s1, layer_scale;
+  const float* bias;
+  void* y;
+  int y_dtype;
+  int64_t ldy;
+  int S, SG, W, ncu;     // slices, slice groups, waves per group, CUs
+  _Float16* x2h;         // workspace: [B][n] fp16 operand
+  _Float16* sg;          // workspace: [B][n / 8] group sums
+  float* xmul;           // workspace: [B]
+  float* y1p;            // workspace: [SG][B][m]
+};
+bool batched_eligible(int64_t n, int pn, int64_t m, int pm);
+int launch_linear_batched(const BatchedPass& P, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop);
+
 }  // namespace qs

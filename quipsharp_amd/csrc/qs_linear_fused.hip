@@ -5,33 +5,29 @@
 // Transforms.  A length-n transform T_n = K_p (x) H_L (n = p L, L = 2^k >= 256)
 // is split as T_n = M (x) H_256 over the index i = 256 c + t: a 256-point
 // Walsh-Hadamard inside each chunk c (one wave, four values per lane, two
-// stages in registers and six across lanes with DPP / swizzle exchanges, no
+// stages in registers and six across lanes with DPP / permlane exchanges, no
 // barrier), then the S x S matrix M = K_p (x) H_{L/256} (S = n / 256 <= 48)
-// across chunks, as fp32 16x16x4 MFMAs over 16-column tiles.  Entries of M are
-// generated on the fly (Hadamard signs from a popcount, K from LDS).
+// across chunks on the matrix cores (bf16 hi + lo operands, fp32 accumulate).
 //
 // Work-group j owns one slice group (up to 16 slices of 256 input columns,
 // one per wave) and a strided set of 16-row blocks, so each wave's activation
 // operand stays in registers for the whole launch.  Per work-group:
 //   1. issue the activation loads, then the abs-table and K loads; the first
 //      code tiles are requested once the activations have arrived, and the
-//      signed half-codeword LDS tables are built after the input transform
-//      (off its critical path);
-//   2. input transform (every work-group; only its own slices' rows of M):
-//      chunks -> LDS, MFMA over M rows of this group, fp16 operand per wave
-//      scaled by 2^-e (e from the row norm) plus the per-group sums for the
-//      +-1/4 shift term, whose -1/4 sum_g S_g part is folded in per slice;
+//      byte-per-value half-codeword LUTs are built after the input transform;
+//   2. input transform (every work-group; only its own 16 rows of M): chunks
+//      -> LDS, chunk stage, fp16 operand rows scaled by 2^-e (e from the row
+//      norm) plus the per-group sums for the +-1/4 shift term, whose
+//      -1/4 sum_g S_g part is folded in per slice;
 //   3. per row block: 8 MFMAs (+1 for the shift, +8 for an E8 1-bit second
-//      stage), a cross-wave tree reduction in LDS (double-buffered, one
-//      barrier), partial sums to the workspace as write-through stores;
+//      stage) into one of 8 LDS slots; every 8 row blocks (and after the
+//      last) the slots are reduced across the waves and the partial sums go
+//      to the workspace as write-through stores;
 //   4. completion: the stores are waited for, then one atomic per work-group
 //      on a counter; the last work-group reads the partials (write-through
-//      loads), applies S_u T_m(.) + bias with the same chunk/MFMA scheme and
-//      resets the counter.  This covers every m of the chunk scheme
-//      (m = p 2^k, 256 | m, m <= 12288): for a power of two the chunk stage
-//      M is a +-1 Hadamard and runs row-wise on the VALU; with an odd factor
-//      M = K_p (x) H is dense and runs on the matrix cores with operands
-//      split into bf16 hi + lo parts.
+//      loads), applies S_u T_m(.) + bias with the same chunk scheme and
+//      resets the counter (every m of the scheme: m = p 2^k, 256 | m,
+//      m <= 12288).
 //
 // Cross-work-group visibility.  Partial sums are written with agent-scope
 // relaxed atomic stores and read with agent-scope relaxed atomic loads, which
@@ -41,20 +37,14 @@
 // an L2 write-back per wave that a device-scope fence would cost.
 #include <hip/hip_ext.h>
 
-#include "qs_chunk_dev.h"
+#include "qs_forward_dev.h"
 #include "qs_linear_dev.h"
 
 namespace qs {
 namespace {
 
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-__constant__ Table8h kE8Ph = pack_table_f16(make_e8p_table());
-__constant__ Table8h kE81h = pack_table_f16(make_e81_table());
-
-constexpr int kThreads = 1024;
+constexpr int kThreads = kFwdThreads;
 constexpr int kMaxB = 2;
 constexpr int kPrefetch = 4;
 constexpr int kMaxJobs = QS_MAX_GROUP;
@@ -98,211 +88,36 @@ struct FusedArgs {
 
 // LDS layout (bytes).  The abs-table staging area aliases the reduction
 // buffer (the table is dead before the first row block); the output
-// transform of the last work-group reuses the Y region.
-constexpr int kOffHi = 0;                                   // 4096 x uint2
-constexpr int kOffLo = 32768;                               // 4096 x uint2
-constexpr int kOffLut1 = 65536;                             // 256 x uint4
-constexpr int kOffRed = kOffLut1 + 4096;                    // 2 x 16 x 16 x kMaxB floats
-constexpr int kMStride = 72;                                // bf16 per row of a chunk-stage matrix (16-byte rows)
-constexpr int kOffMin = kOffRed + 2 * kWaves * 16 * kMaxB * 4;  // 2 x 16 x kMStride bf16: input chunk stage (hi, lo)
+// transform of the last work-group reuses the LUT and Y regions.
+constexpr int kOffHi = 0;                                   // 4096 x uint32 (four fp16 high bytes)
+constexpr int kOffLo = 16384;                               // 4096 x uint32
+constexpr int kOffLut1 = 32768;                             // 256 x uint4
+constexpr int kRedSlots = 8;                                // row blocks reduced together
+constexpr int kRedSlot = kWaves * 16 * kMaxB;               // floats per slot: [wave][row][batch]
+constexpr int kOffRed = kOffLut1 + 4096;                    // kRedSlots x kRedSlot floats
+constexpr int kOffMin = kOffRed + kRedSlots * kRedSlot * 4;  // 2 x 16 x kMStride bf16: input chunk stage (hi, lo)
 constexpr int kOffTab = kOffRed;                            // 256 x uint4 (table staging, before the row blocks)
 constexpr int kOffXH = kOffMin + 2 * 16 * kMStride * 2;     // kMaxB x 16 x kXStride halves
 constexpr int kOffXS = kOffXH + kMaxB * 16 * kXStride * 2;  // kMaxB x 16 x 32 halves (group sums)
 constexpr int kOffY = kOffXS + kMaxB * 16 * 32 * 2;          // kMaxS x kYStride floats
-constexpr int kLdsBytes = kOffY + kMaxS * kYStride * 4;
+constexpr int kOffMisc = kOffY + kMaxS * kYStride * 4;      // row norms (16 floats), last-group flag
+constexpr int kLdsBytes = kOffMisc + 128;
 static_assert(kLdsBytes <= 160 * 1024 - 128, "LDS budget");
 // Output chunk stage (last work-group, the LUTs are dead): the chunk matrix
 // M as bf16 hi / lo parts, rows and columns padded with zeros.
-constexpr int kMRows = 48, kMCols = 64;
 constexpr int kOffMh = 0;
-constexpr int kOffMl = kOffMh + kMRows * kMStride * 2;
-static_assert(kOffMl + kMRows * kMStride * 2 <= kOffLut1, "M fits the LUT region");
-static_assert(kMRows >= kMaxS && kMCols >= kMaxS, "M covers every chunk count");
-static_assert(kMRows * kMCols == 3 * 1024 && kCPW == 3, "three M entries / output rows per thread");
-static_assert(2 * kWaves * 16 * kMaxB * 4 >= 4096, "table staging fits the reduction buffer");
+constexpr int kOffMl = kOffMh + kMBytes;
+static_assert(kOffMl + kMBytes <= kOffLut1, "M fits the LUT region");
+static_assert(kRedSlots * kRedSlot * 4 >= 4096, "table staging fits the reduction buffer");
+static_assert(kRedSlots * 16 * kMaxB * 4 == kThreads && kRedSlots * 16 * 8 == kThreads,
+              "one reduction pass: 8 threads per output at B = 1, 4 at B = 2");
 
-// Two floats as bf16 pairs: the truncated high parts and the (truncated)
-// remainders, so a + b products from hi*hi + hi*lo + lo*hi carry ~16 bits.
-__device__ __forceinline__ void split_bf2(float a, float b, uint32_t& hi, uint32_t& lo) {
-  const uint32_t ua = __float_as_uint(a), ub = __float_as_uint(b);
-  const uint32_t ha = ua & 0xFFFF0000u, hb = ub & 0xFFFF0000u;
-  const uint32_t la = __float_as_uint(a - __uint_as_float(ha)), lb = __float_as_uint(b - __uint_as_float(hb));
-  hi = (ha >> 16) | hb;
-  lo = (la >> 16) | (lb & 0xFFFF0000u);
-}
-
-__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
-  _Float16 a = (_Float16)lo, b = (_Float16)hi;
-  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
-}
-
-// Activation chunks of batch row b (times sv), chunk c = w + 16 u.
-__device__ __forceinline__ void load_x(const FusedArgs& A, const float* sv, int b, int w, int lane,
-                                       float (&v)[kCPW][4]) {
-#pragma unroll
-  for (int u = 0; u < kCPW; ++u) {
-    const int c = w + kWaves * u;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) v[u][j] = 0.0f;
-    if (c < A.Sn) {
-      const int i0 = 256 * c + 4 * lane;
-      const float4 s = *reinterpret_cast<const float4*>(sv + i0);
-      const int64_t xi = (int64_t)b * A.ldx + i0;
-      float x0, x1, x2, x3;
-      if (A.x_vec && A.x_dtype == QS_DTYPE_F32) {
-        const float4 t = *reinterpret_cast<const float4*>(static_cast<const float*>(A.x) + xi);
-        x0 = t.x, x1 = t.y, x2 = t.z, x3 = t.w;
-      } else if (A.x_vec) {
-        const uint2 t = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(A.x) + xi);
-        if (A.x_dtype == QS_DTYPE_BF16) {
-          x0 = __uint_as_float(t.x << 16), x1 = __uint_as_float(t.x & 0xFFFF0000u);
-          x2 = __uint_as_float(t.y << 16), x3 = __uint_as_float(t.y & 0xFFFF0000u);
-        } else {
-          x0 = (float)__builtin_bit_cast(_Float16, (uint16_t)(t.x & 0xFFFFu));
-          x1 = (float)__builtin_bit_cast(_Float16, (uint16_t)(t.x >> 16));
-          x2 = (float)__builtin_bit_cast(_Float16, (uint16_t)(t.y & 0xFFFFu));
-          x3 = (float)__builtin_bit_cast(_Float16, (uint16_t)(t.y >> 16));
-        }
-      } else {
-        x0 = load_as_float(A.x, A.x_dtype, xi);
-        x1 = load_as_float(A.x, A.x_dtype, xi + 1);
-        x2 = load_as_float(A.x, A.x_dtype, xi + 2);
-        x3 = load_as_float(A.x, A.x_dtype, xi + 3);
-      }
-      v[u][0] = x0 * s.x;
-      v[u][1] = x1 * s.y;
-      v[u][2] = x2 * s.z;
-      v[u][3] = x3 * s.w;
-    }
-  }
-}
-
-__device__ __forceinline__ void store_chunks(float* Y, int S, int w, int lane, const float (&v)[kCPW][4]) {
-#pragma unroll
-  for (int u = 0; u < kCPW; ++u) {
-    const int c = w + kWaves * u;
-    if (c < S)
-      *reinterpret_cast<float4*>(Y + c * kYStride + 4 * lane) = make_float4(v[u][0], v[u][1], v[u][2], v[u][3]);
-  }
-}
-
-// Chunk stage on the matrix cores.  For 16 rows of a chunk matrix M (bf16 hi
-// / lo rows of kMStride in LDS, zero past the S chunks) and chunk rows Z in
-// LDS (kYStride floats), lane (q, r16) of a wave owning column t accumulates
-// acc[j] = sum_c M[row0 + 4 q + j][c] Z[c][t] over k-steps of 32 chunks.  Both operands are split into
-// bf16 hi + lo and multiplied as hi*hi + hi*lo (+ lo*hi when M has a low
-// part), fp32 accumulate: ~16 significant bits per product.
-struct ZOperand {
-  bf16x8 h, l;  // Z[c][t], c = 32 kb + 8 q + i
-};
-
-__device__ __forceinline__ ZOperand z_operand(const float* Z, int S, int t, int q, int kb) {
-  uint32_t h[4], l[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int c0 = 32 * kb + 8 * q + 2 * i;
-    const float z0 = c0 < S ? Z[c0 * kYStride + t] : 0.0f;
-    const float z1 = c0 + 1 < S ? Z[(c0 + 1) * kYStride + t] : 0.0f;
-    split_bf2(z0, z1, h[i], l[i]);
-  }
-  return ZOperand{__builtin_bit_cast(bf16x8, make_uint4(h[0], h[1], h[2], h[3])),
-                  __builtin_bit_cast(bf16x8, make_uint4(l[0], l[1], l[2], l[3]))};
-}
-
-// acc += M[row0 + r16][32 kb + 8 q ..] x z (the k-step kb of a tile).
-__device__ __forceinline__ floatx4 mstage_step(floatx4 acc, const uint16_t* Mh, const uint16_t* Ml, int row0,
-                                               const ZOperand& z, int kb, bool m_lo, int q, int r16) {
-  const int off = (row0 + r16) * kMStride + 32 * kb + 8 * q;
-  const bf16x8 ah = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(Mh + off));
-  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, z.h, acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, z.l, acc, 0, 0, 0);
-  if (m_lo) {
-    const bf16x8 al = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(Ml + off));
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, z.h, acc, 0, 0, 0);
-  }
-  return acc;
-}
-
-// Chunks held as element t = lane + 64 j (the layout of load_partials).
-__device__ __forceinline__ void store_chunks_lanes(float* Y, int S, int w, int lane, const float (&v)[kCPW][4]) {
-#pragma unroll
-  for (int u = 0; u < kCPW; ++u) {
-    const int c = w + kWaves * u;
-    if (c < S) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) Y[c * kYStride + lane + 64 * j] = v[u][j];
-    }
-  }
-}
-
-constexpr int kMaxSG = (kMaxS + kWaves - 1) / kWaves;  // column groups of the partial sums
-
-// Partial sums of batch row b, summed over the column groups, for the chunks
-// c = w + 16 u of this wave, as element t = lane + 64 j (each load
-// instruction reads 256 contiguous bytes).  Every load is issued before the
-// first one is used.  (The 256-point transform is the same for any
-// assignment of the index bits to lanes and registers.)
-__device__ __forceinline__ void load_partials(const FusedJob& J, int SG, int B, int b, int w, int lane,
-                                              float (&zv)[kCPW][4]) {
-  float tmp[kMaxSG][kCPW][4];
-#pragma unroll
-  for (int g = 0; g < kMaxSG; ++g)
-#pragma unroll
-    for (int u = 0; u < kCPW; ++u) {
-      const int c = w + kWaves * u;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) tmp[g][u][j] = 0.0f;
-      if (g < SG && c < J.Sm) {
-        const float* src = J.y1p + ((size_t)g * B + b) * J.m + 256 * c + lane;
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          tmp[g][u][j] = __hip_atomic_load(src + 64 * j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-#pragma unroll
-  for (int u = 0; u < kCPW; ++u)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float v = tmp[0][u][j];
-#pragma unroll
-      for (int g = 1; g < kMaxSG; ++g) v += tmp[g][u][j];
-      zv[u][j] = v;
-    }
-}
-
-// Output values out[a][j] to y[base + idx[a][j]] (idx < 0: no output), one
-// dtype dispatch for all of them.
-__device__ __forceinline__ void store_outputs(void* y, int dtype, int64_t base, const int (&idx)[3][4],
-                                              const float (&out)[3][4]) {
-  if (dtype == QS_DTYPE_F32) {
-    float* p = static_cast<float*>(y) + base;
-#pragma unroll
-    for (int a = 0; a < 3; ++a)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (idx[a][j] >= 0) p[idx[a][j]] = out[a][j];
-  } else if (dtype == QS_DTYPE_F16) {
-    _Float16* p = static_cast<_Float16*>(y) + base;
-#pragma unroll
-    for (int a = 0; a < 3; ++a)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (idx[a][j] >= 0) p[idx[a][j]] = (_Float16)out[a][j];
-  } else {
-    uint16_t* p = static_cast<uint16_t*>(y) + base;
-#pragma unroll
-    for (int a = 0; a < 3; ++a)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (idx[a][j] >= 0) p[idx[a][j]] = f32_to_bf16(out[a][j]);
-  }
-}
 
 template <bool HAS2>
 __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
-  uint2* lut_hi = reinterpret_cast<uint2*>(lds + kOffHi);
-  uint2* lut_lo = reinterpret_cast<uint2*>(lds + kOffLo);
+  uint32_t* lut_hi = reinterpret_cast<uint32_t*>(lds + kOffHi);
+  uint32_t* lut_lo = reinterpret_cast<uint32_t*>(lds + kOffLo);
   uint4* lut1 = reinterpret_cast<uint4*>(lds + kOffLut1);
   uint4* tab16 = reinterpret_cast<uint4*>(lds + kOffTab);
   float* red = reinterpret_cast<float*>(lds + kOffRed);
@@ -311,8 +126,8 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   _Float16* XH = reinterpret_cast<_Float16*>(lds + kOffXH);
   _Float16* XS = reinterpret_cast<_Float16*>(lds + kOffXS);
   float* Y = reinterpret_cast<float*>(lds + kOffY);
-  __shared__ float wsum[kWaves];
-  __shared__ int s_last;
+  float* wsum = reinterpret_cast<float*>(lds + kOffMisc);
+  int& s_last = *reinterpret_cast<int*>(lds + kOffMisc + 4 * kWaves);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
@@ -332,7 +147,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   // 1. loads: the activations first (the transform waits for them), then the
   //    abs table and K; the code tiles once the activations are in
   float xv[kCPW][4];
-  load_x(A, J.sv, 0, w, lane, xv);
+  load_x(XSource{A.x, A.x_dtype, A.x_vec, A.ldx, A.Sn}, J.sv, 0, w, lane, xv);
   uint4 trow = make_uint4(0, 0, 0, 0), t1row = make_uint4(0, 0, 0, 0);  // fp16 table rows
   if (tid < 256) {
     trow = *reinterpret_cast<const uint4*>(kE8Ph.w[tid]);
@@ -348,18 +163,13 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   // 2. input transform, one batch row at a time, into fp16 operand rows
   float emul0 = 1.0f, emul1 = 1.0f;  // 2^e of batch rows 0 and 1
   for (int b = 0; b < A.B; ++b) {
-    if (b > 0) load_x(A, J.sv, b, w, lane, xv);
+    if (b > 0) load_x(XSource{A.x, A.x_dtype, A.x_vec, A.ldx, A.Sn}, J.sv, b, w, lane, xv);
     float ss = 0.0f;
 #pragma unroll
     for (int u = 0; u < kCPW; ++u)
 #pragma unroll
       for (int j = 0; j < 4; ++j) ss = __builtin_fmaf(xv[u][j], xv[u][j], ss);
-    ss += lane_xor<32>(ss, lx);
-    ss += lane_xor<16>(ss, lx);
-    ss += lane_xor<8>(ss, lx);
-    ss += lane_xor<4>(ss, lx);
-    ss += lane_xor<2>(ss, lx);
-    ss += lane_xor<1>(ss, lx);
+    ss = wave_sum(ss, lx);
     if (lane == 0) wsum[w] = ss;
     h256_chunks(xv, A.Sn, lane, lx);
     if (b == 0) {
@@ -396,12 +206,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
     float norm2 = 0.0f;
 #pragma unroll
     for (int i = 0; i < kWaves; ++i) norm2 += wsum[i];
-    int e = 0;
-    if (norm2 > 0.0f && norm2 < INFINITY) {
-      int ex;
-      frexpf(sqrtf(norm2) * 1.0001f, &ex);  // |x2_i| <= ||x|| < 2^ex
-      e = ex - 14;
-    }
+    const int e = operand_exponent(norm2);
     if (b == 0) emul0 = ldexpf(1.0f, e);
     else emul1 = ldexpf(1.0f, e);
     const float mul = ldexpf(A.scale_n, -e);
@@ -433,28 +238,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
       }
     }
   }
-  {
-    // LUT entries e = tid + 1024 k.  hi: abs row e & 255 = tid & 255 and flip
-    // nibble H = e >> 8 = (tid >> 8) + 4 k.  lo: abs row (e >> 3) & 255 (two
-    // rows, k even / odd), f4..f6 from e & 7 = tid & 7, q = e >> 11 = k >> 1.
-    const uint4 th = tab16[tid & 255];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint32_t H = (uint32_t)(tid >> 8) + 4u * k;
-      const uint32_t f1 = (H >> 3) & 1, f2 = (H >> 2) & 1, f3 = (H >> 1) & 1;
-      const uint32_t f0 = (H & 1) ^ f1 ^ f2 ^ f3;
-      lut_hi[tid + kThreads * k] = make_uint2(th.x ^ ((f0 << 15) | (f1 << 31)), th.y ^ ((f2 << 15) | (f3 << 31)));
-    }
-    const uint32_t f4 = (tid >> 2) & 1, f5 = (tid >> 1) & 1, f6 = tid & 1;
-    const uint32_t m45 = (f4 << 15) | (f5 << 31), p456 = f4 ^ f5 ^ f6;
-    const uint4 ta = tab16[(tid >> 3) & 255], tb = tab16[((tid >> 3) + 128) & 255];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint4 t = (k & 1) ? tb : ta;
-      const uint32_t f7 = (uint32_t)(k >> 1) ^ p456;
-      lut_lo[tid + kThreads * k] = make_uint2(t.z ^ m45, t.w ^ ((f6 << 15) | (f7 << 31)));
-    }
-  }
+  fill_luts(tab16, lut_hi, lut_lo, tid);
   __syncthreads();  // LUTs and operand rows complete; the table staging area is free again
   // MFMA operand of lane (q, b = r16): columns 64q..64q+63 of this wave's slice
   const half8 hzero = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -505,12 +289,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
       const uint32_t wd[4] = {cw.x, cw.y, cw.z, cw.w};
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
-        const uint32_t wv = wd[c >> 1];
-        const uint32_t ha = (c & 1) ? ((wv >> 17) & 0x7FF8u) : ((wv >> 1) & 0x7FF8u);
-        const uint32_t la = (c & 1) ? ((wv >> 14) & 0x7FF8u) : ((wv << 2) & 0x7FF8u);
-        const uint2 hv = *reinterpret_cast<const uint2*>(lds + kOffHi + ha);
-        const uint2 lv = *reinterpret_cast<const uint2*>(lds + kOffLo + la);
-        const half8 av = __builtin_bit_cast(half8, make_uint4(hv.x, hv.y, lv.x, lv.y));
+        const half8 av = decode_code(wd[c >> 1], c, kOffHi, kOffLo);
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, xb[c], acc, 0, 0, 0);
         if (HAS2) {
           const uint32_t idx = ((c < 4 ? cw1.x : cw1.y) >> (8 * (c & 3))) & 0xFFu;
@@ -518,13 +297,14 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
                                                           0);
         }
       }
-      const half8 ash = __builtin_bit_cast(
-          half8, make_uint4((wd[0] & 0x10001u) * 0x3C00u, (wd[1] & 0x10001u) * 0x3C00u,
-                            (wd[2] & 0x10001u) * 0x3C00u, (wd[3] & 0x10001u) * 0x3C00u));
-      accs = __builtin_amdgcn_mfma_f32_16x16x32_f16(ash, xs, accs, 0, 0, 0);
+      accs = __builtin_amdgcn_mfma_f32_16x16x32_f16(shift_operand(wd), xs, accs, 0, 0, 0);
     }
-    // partial of this slice for rows 4q..4q+3, batch column r16
-    float* rbuf = red + (k & 1) * (kWaves * 16 * kMaxB);
+    // partial of this slice for rows 4q..4q+3, batch column r16, into this
+    // row block's slot; the slots are reduced across the waves every
+    // kRedSlots row blocks (and after the last), so the waves decode without
+    // a barrier per row block
+    const int slot = k % kRedSlots;
+    float* rbuf = red + slot * kRedSlot;
     if (r16 < A.B) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -533,21 +313,33 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
         rbuf[(w * 16 + 4 * q + j) * kMaxB + r16] = active ? v : 0.0f;
       }
     }
-    __syncthreads();
-    // tree sum over the waves: thread (o, ww), o = row*B + b
-    {
-      const int o = tid >> 4, ww = tid & 15;
+    if (slot == kRedSlots - 1 || rb + J.Gr >= RB) {
+      __syncthreads();
+      // output o = (s * 16 + row) * B + b of slot s <= slot, summed over the
+      // waves by tpo threads (waves part, part + tpo, ...), then across them;
+      // tpo depends on B only, so every output is summed in the same order
+      // whatever the number of row blocks pending
+      const int nout = (slot + 1) * 16 * A.B;
+      const int tpo = A.B == 1 ? 8 : 4;  // kThreads / (kRedSlots * 16 * B)
+      const int o = tid / tpo, part = tid - o * tpo;
       float v = 0.0f;
-      if (o < 16 * A.B && ww < nw) v = rbuf[(ww * 16 + o / A.B) * kMaxB + (o % A.B)];
+      int s = 0, row = 0, bc = 0;
+      if (o < nout) {
+        s = o / (16 * A.B);
+        const int rr = o - s * 16 * A.B;
+        row = rr / A.B;
+        bc = rr - row * A.B;
+        for (int ww = part; ww < nw; ww += tpo) v += red[s * kRedSlot + (ww * 16 + row) * kMaxB + bc];
+      }
       v += lane_xor<1>(v, lx);
       v += lane_xor<2>(v, lx);
-      v += lane_xor<4>(v, lx);
-      v += lane_xor<8>(v, lx);
-      if (o < 16 * A.B && ww == 0) {
-        const int row = o / A.B, bc = o % A.B;
-        __hip_atomic_store(&J.y1p[((size_t)sg * A.B + bc) * J.m + rb * 16 + row], v, __ATOMIC_RELAXED,
+      if (tpo == 8) v += lane_xor<4>(v, lx);
+      if (o < nout && part == 0) {
+        const int rbs = rb - (slot - s) * J.Gr;  // row block of slot s
+        __hip_atomic_store(&J.y1p[((size_t)sg * A.B + bc) * J.m + rbs * 16 + row], v, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
       }
+      __syncthreads();  // the slots are free again
     }
   }
 
@@ -570,14 +362,9 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
     // together (unconditional loads from valid addresses, selected where they
     // are used: a load under a branch is waited for at the branch's end).
     float kmv[3];
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
-      const int e = tid + kThreads * i, r = e / kMCols, c = e % kMCols;
-      kmv[i] = 1.0f;
-      if (J.pm > 1) kmv[i] = J.Km[(r < Sm && c < Sm) ? (r >> J.lsh_m) * J.pm + (c >> J.lsh_m) : 0];
-    }
+    mmat_load(kmv, Sm, J.lsh_m, J.pm, J.Km, tid);
     float zv[kCPW][4];
-    load_partials(J, A.SG, A.B, 0, w, lane, zv);
+    load_partials<true>(J.y1p, J.m, Sm, A.SG, A.B, 0, w, lane, zv);
     int oidx[3][4];
     float suo[3][4], bio[3][4];
     const float* const bsrc = J.bias ? J.bias : J.su;
@@ -595,26 +382,14 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
     // M = K_p (x) H_{2^lsh_m} as bf16 hi / lo, zero-padded to 48 x 64
     uint16_t* Mh = reinterpret_cast<uint16_t*>(lds + kOffMh);
     uint16_t* Ml = reinterpret_cast<uint16_t*>(lds + kOffMl);
-    {
-      const int hm = (1 << J.lsh_m) - 1;
-#pragma unroll
-      for (int i = 0; i < 3; ++i) {
-        const int e = tid + kThreads * i, r = e / kMCols, c = e % kMCols;
-        float v = (r < Sm && c < Sm) ? kmv[i] : 0.0f;
-        if (__builtin_popcount(r & c & hm) & 1) v = -v;
-        uint32_t hi, lo;
-        split_bf2(v, 0.0f, hi, lo);
-        Mh[r * kMStride + c] = (uint16_t)hi;
-        Ml[r * kMStride + c] = (uint16_t)lo;
-      }
-    }
+    mmat_store(kmv, Sm, J.lsh_m, Mh, Ml, tid);
     void* const yp = J.y;
     const int64_t ldy = J.ldy;
     const int ydt = A.y_dtype;
     const float mul0 = J.scale_m * J.layer_scale;
     const int nrt = (Sm + 15) >> 4, nkb = (Sm + 31) >> 5;
     for (int b = 0; b < A.B; ++b) {
-      if (b > 0) load_partials(J, A.SG, A.B, b, w, lane, zv);
+      if (b > 0) load_partials<true>(J.y1p, J.m, Sm, A.SG, A.B, b, w, lane, zv);
       h256_chunks(zv, Sm, lane, lx);
       if (b > 0) __syncthreads();  // the previous row's reads of Y are done
       store_chunks_lanes(Y, Sm, w, lane, zv);
@@ -709,6 +484,11 @@ int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, i
   }
   static int attr_done = 0;
   if (!attr_done) {
+    hipFuncAttributes fa{};
+    QS_HIP(hipFuncGetAttributes(&fa, (const void*)linear_fused_kernel<false>));
+    QS_REQUIRE(fa.sharedSizeBytes == 0, "linear_fused_kernel: static LDS would move the LUT off address 0");
+    QS_HIP(hipFuncGetAttributes(&fa, (const void*)linear_fused_kernel<true>));
+    QS_REQUIRE(fa.sharedSizeBytes == 0, "linear_fused_kernel: static LDS would move the LUT off address 0");
     QS_HIP(hipFuncSetAttribute((const void*)linear_fused_kernel<false>,
                                hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes));
     QS_HIP(hipFuncSetAttribute((const void*)linear_fused_kernel<true>,
