@@ -136,7 +136,7 @@ struct BmArgs {
 
 constexpr int kBmSlots = 2;                  // row blocks reduced together
 constexpr int kBmSlot = kWaves * 16 * kTB;   // floats per slot: [wave][row][batch]
-constexpr int kBmOffHi = 0;                  // 4096 x uint32
+constexpr int kBmOffHi = 0;                  // 4096 x uint32 (four fp16 high bytes)
 constexpr int kBmOffLo = 16384;              // 4096 x uint32
 constexpr int kBmOffLut1 = 32768;            // 256 x uint4
 constexpr int kBmOffTab = kBmOffLut1 + 4096; // 256 x uint4 (table staging)
@@ -162,35 +162,40 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
   const bool active = w < A.W && sl < A.S;
   const LaneX lx = lane_x_init();
 
+  // All global loads here are unconditional (an idle lane reads a valid
+  // address it does not use), so the compiler waits for exactly the data in
+  // use: first the table rows, then the operand, then the code tiles.
+  uint4 trow = make_uint4(0, 0, 0, 0), t1row = make_uint4(0, 0, 0, 0);
+  trow = *reinterpret_cast<const uint4*>(kE8Ph.w[tid & 255]);
+  if (HAS2) t1row = *reinterpret_cast<const uint4*>(kE81h.w[tid & 255]);
   // operand of lane (q, b = r16): columns 64 q .. 64 q + 63 of this wave's
-  // slice, and the sums of its eight groups of 8
-  const half8 hzero = {0, 0, 0, 0, 0, 0, 0, 0};
+  // slice, and the sums of its eight groups of 8 (columns b >= B and idle
+  // waves compute values that are never stored)
+  const bool have = active && r16 < A.B;
+  const _Float16* xrow = A.x2h + (have ? (size_t)r16 * A.n + 256 * sl + 64 * q : 0);
   half8 xb[8];
-  half8 xs = hzero;
 #pragma unroll
-  for (int c = 0; c < 8; ++c) xb[c] = hzero;
-  if (active && r16 < A.B) {
-    const _Float16* xrow = A.x2h + (size_t)r16 * A.n + 256 * sl + 64 * q;
-#pragma unroll
-    for (int c = 0; c < 8; ++c) xb[c] = *reinterpret_cast<const half8*>(xrow + 8 * c);
-    xs = *reinterpret_cast<const half8*>(A.sg + (size_t)r16 * (A.n / 8) + 32 * sl + 8 * q);
-  }
+  for (int c = 0; c < 8; ++c) xb[c] = *reinterpret_cast<const half8*>(xrow + 8 * c);
+  const half8 xs =
+      *reinterpret_cast<const half8*>(A.sg + (have ? (size_t)r16 * (A.n / 8) + 32 * sl + 8 * q : 0));
+  // code tiles stream through a ring of kPrefetch registers (see the row
+  // loop); a tile past the end or of an idle wave reads tile 0 instead
+  // byte offset of this lane's 16 code bytes of row block rb (tile 0 past
+  // the end or for an idle wave); m n / 4 < 2^32 bytes of codes
+  auto code_off = [&](int rb) -> uint32_t {
+    return ((active && rb < RB) ? ((uint32_t)rb * (uint32_t)A.S + (uint32_t)sl) * 1024u : 0u) + 16u * lane;
+  };
   uint4 pre[kPrefetch];
-  uint2 pre1[kPrefetch];
+  uint2 pre1[kPrefetch] = {};
 #pragma unroll
   for (int k = 0; k < kPrefetch; ++k) {
-    const int rb = jr + k * A.Gr;
-    pre[k] = make_uint4(0, 0, 0, 0);
-    pre1[k] = make_uint2(0, 0);
-    if (active && rb < RB) {
-      const size_t tile = ((size_t)rb * A.S + sl) * 64 + lane;
-      pre[k] = *reinterpret_cast<const uint4*>(A.codes0 + tile * 8);
-      if (HAS2) pre1[k] = *reinterpret_cast<const uint2*>(A.codes1 + tile * 8);
-    }
+    const uint32_t off = code_off(jr + k * A.Gr);
+    pre[k] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(A.codes0) + off);
+    if (HAS2) pre1[k] = *reinterpret_cast<const uint2*>(A.codes1 + off / 2);
   }
   if (tid < 256) {
-    tab16[tid] = *reinterpret_cast<const uint4*>(kE8Ph.w[tid]);
-    if (HAS2) lut1[tid] = *reinterpret_cast<const uint4*>(kE81h.w[tid]);
+    tab16[tid] = trow;
+    if (HAS2) lut1[tid] = t1row;
   }
   __syncthreads();
   fill_luts(tab16, lut_hi, lut_lo, tid);
@@ -203,29 +208,23 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
   slice_shift += lane_xor<32>(slice_shift, lx);
 
   const int nw = A.S - sg * A.W < A.W ? A.S - sg * A.W : A.W;
-  int k = 0;
-  for (int rb = jr; rb < RB; rb += A.Gr, ++k) {
+  // The ring is unrolled and every step runs (a step past the last row
+  // block only refills its entry), so its registers are never copied and
+  // each step waits for its own tile only; an entry is refilled once its
+  // tile is decoded.
+  int k = 0;  // row blocks done: selects the reduction slot
+  for (int rb0 = jr; rb0 < RB; rb0 += kPrefetch * A.Gr) {
+#pragma unroll
+  for (int u = 0; u < kPrefetch; ++u) {
+    const int rb = rb0 + u * A.Gr;
+    const bool valid = rb < RB;
     floatx4 acc = {0.f, 0.f, 0.f, 0.f};
     floatx4 accs = {0.f, 0.f, 0.f, 0.f};
     floatx4 acc2 = {0.f, 0.f, 0.f, 0.f};
-    const uint4 cw = pre[0];
-    const uint2 cw1 = pre1[0];
-#pragma unroll
-    for (int j = 0; j + 1 < kPrefetch; ++j) {
-      pre[j] = pre[j + 1];
-      pre1[j] = pre1[j + 1];
-    }
-    {
-      const int rbn = rb + kPrefetch * A.Gr;
-      pre[kPrefetch - 1] = make_uint4(0, 0, 0, 0);
-      pre1[kPrefetch - 1] = make_uint2(0, 0);
-      if (active && rbn < RB) {
-        const size_t tile = ((size_t)rbn * A.S + sl) * 64 + lane;
-        pre[kPrefetch - 1] = *reinterpret_cast<const uint4*>(A.codes0 + tile * 8);
-        if (HAS2) pre1[kPrefetch - 1] = *reinterpret_cast<const uint2*>(A.codes1 + tile * 8);
-      }
-    }
-    if (active) {
+    const uint4 cw = pre[u];
+    const uint2 cw1 = pre1[u];
+    if (valid) {
+      // (idle waves decode tile 0; their results are not stored)
       const uint32_t wd[4] = {cw.x, cw.y, cw.z, cw.w};
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
@@ -239,16 +238,23 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
       }
       accs = __builtin_amdgcn_mfma_f32_16x16x32_f16(shift_operand(wd), xs, accs, 0, 0, 0);
     }
+    {
+      const uint32_t off = code_off(rb + kPrefetch * A.Gr);
+      pre[u] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(A.codes0) + off);
+      if (HAS2) pre1[u] = *reinterpret_cast<const uint2*>(A.codes1 + off / 2);
+    }
     // lane holds rows 4q..4q+3 of the tile for batch column r16
     const int slot = k % kBmSlots;
     float* rbuf = red + slot * kBmSlot;
+    if (valid) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float v = A.s0 * (acc[j] + 0.5f * accs[j] - 0.25f * slice_shift);
-      if (HAS2) v = v + A.s1 * acc2[j];
-      rbuf[(w * 16 + 4 * q + j) * kTB + r16] = active ? v : 0.0f;
+      for (int j = 0; j < 4; ++j) {
+        float v = A.s0 * (acc[j] + 0.5f * accs[j] - 0.25f * slice_shift);
+        if (HAS2) v = v + A.s1 * acc2[j];
+        rbuf[(w * 16 + 4 * q + j) * kTB + r16] = active ? v : 0.0f;
+      }
     }
-    if (slot == kBmSlots - 1 || rb + A.Gr >= RB) {
+    if (valid && (slot == kBmSlots - 1 || rb + A.Gr >= RB)) {
       __syncthreads();
       // output o = (s * 16 + row) * B + b of slot s <= slot, summed over the
       // waves by tpo threads (waves part, part + tpo, ...), then across them;
@@ -275,6 +281,8 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
       }
       __syncthreads();  // the slots are free again
     }
+    k += valid;
+  }
   }
 }
 

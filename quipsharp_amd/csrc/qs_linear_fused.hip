@@ -157,8 +157,17 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   const bool m_ok = active && lane < A.Sn;
   float mk = 1.0f;
   if (A.pn > 1 && m_ok) mk = A.Kn[(sl >> A.lsh_n) * A.pn + (lane >> A.lsh_n)];
+  // Code tiles stream through a ring of kPrefetch registers, refilled as
+  // they are consumed.  The loads are unconditional (a tile past the end or
+  // of an idle wave reads tile 0 instead) and the ring is unrolled, so the
+  // compiler waits for exactly the tile in use, never for the whole ring.
   uint4 pre[kPrefetch];
-  uint2 pre1[kPrefetch];
+  uint2 pre1[kPrefetch] = {};
+  // byte offset of this lane's 16 code bytes of row block rb (tile 0 past
+  // the end or for an idle wave); m n / 4 < 2^32 bytes of codes
+  auto code_off = [&](int rb) -> uint32_t {
+    return ((active && rb < RB) ? ((uint32_t)rb * (uint32_t)A.S + (uint32_t)sl) * 1024u : 0u) + 16u * lane;
+  };
 
   // 2. input transform, one batch row at a time, into fp16 operand rows
   float emul0 = 1.0f, emul1 = 1.0f;  // 2^e of batch rows 0 and 1
@@ -173,20 +182,8 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
     if (lane == 0) wsum[w] = ss;
     h256_chunks(xv, A.Sn, lane, lx);
     if (b == 0) {
-      // first code tiles (issued once the activations are in, so the
-      // activation loads do not queue behind them)
-#pragma unroll
-      for (int k = 0; k < kPrefetch; ++k) {
-        const int rb = jr + k * J.Gr;
-        pre[k] = make_uint4(0, 0, 0, 0);
-        pre1[k] = make_uint2(0, 0);
-        if (active && rb < RB) {
-          const size_t tile = ((size_t)rb * A.S + sl) * 64 + lane;
-          pre[k] = *reinterpret_cast<const uint4*>(J.codes0 + tile * 8);
-          if (HAS2) pre1[k] = *reinterpret_cast<const uint2*>(J.codes1 + tile * 8);
-        }
-      }
-      // table staging and K (read after the barrier below)
+      // table staging and K (read after the barrier below), before the
+      // code loads are issued so these stores do not wait for them
       if (tid < 256) {
         tab16[tid] = trow;
         if (HAS2) lut1[tid] = t1row;
@@ -198,6 +195,14 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
         split_bf2(v, 0.0f, hi, lo);
         MinH[w * kMStride + lane] = (uint16_t)hi;
         MinL[w * kMStride + lane] = (uint16_t)lo;
+      }
+      // first code tiles (issued once the activations are in, so the
+      // activation loads do not queue behind them)
+#pragma unroll
+      for (int k = 0; k < kPrefetch; ++k) {
+        const uint32_t off = code_off(jr + k * J.Gr);
+        pre[k] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(J.codes0) + off);
+        if (HAS2) pre1[k] = *reinterpret_cast<const uint2*>(J.codes1 + off / 2);
       }
     }
     if (b > 0) __syncthreads();  // the previous row's reads of Y are done
@@ -262,30 +267,22 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
 
   // 3. row blocks
   const int nw = A.S - sg * A.W < A.W ? A.S - sg * A.W : A.W;
-  int k = 0;  // iteration count: selects the reduction buffer
-  for (int rb = jr; rb < RB; rb += J.Gr, ++k) {
+  int k = 0;  // row blocks done: selects the reduction slot
+  for (int rb0 = jr; rb0 < RB; rb0 += kPrefetch * J.Gr) {
+#pragma unroll
+  for (int u = 0; u < kPrefetch; ++u) {
+    // every ring step runs (the ring registers are never copied); a step
+    // past the last row block only refills its entry
+    const int rb = rb0 + u * J.Gr;
+    const bool valid = rb < RB;
     floatx4 acc = {0.f, 0.f, 0.f, 0.f};
     floatx4 accs = {0.f, 0.f, 0.f, 0.f};
     floatx4 acc2 = {0.f, 0.f, 0.f, 0.f};
-    uint4 cw = pre[0];
-    uint2 cw1 = pre1[0];
-#pragma unroll
-    for (int j = 0; j + 1 < kPrefetch; ++j) {
-      pre[j] = pre[j + 1];
-      pre1[j] = pre1[j + 1];
-    }
-    {
-      // keep kPrefetch tiles in flight
-      const int rbn = rb + kPrefetch * J.Gr;
-      pre[kPrefetch - 1] = make_uint4(0, 0, 0, 0);
-      pre1[kPrefetch - 1] = make_uint2(0, 0);
-      if (active && rbn < RB) {
-        const size_t tile = ((size_t)rbn * A.S + sl) * 64 + lane;
-        pre[kPrefetch - 1] = *reinterpret_cast<const uint4*>(J.codes0 + tile * 8);
-        if (HAS2) pre1[kPrefetch - 1] = *reinterpret_cast<const uint2*>(J.codes1 + tile * 8);
-      }
-    }
-    if (active) {
+    const uint4 cw = pre[u];
+    const uint2 cw1 = pre1[u];
+    if (valid) {
+      // (idle waves decode tile 0 with a zero operand; their results are
+      // not stored)
       const uint32_t wd[4] = {cw.x, cw.y, cw.z, cw.w};
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
@@ -299,13 +296,20 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
       }
       accs = __builtin_amdgcn_mfma_f32_16x16x32_f16(shift_operand(wd), xs, accs, 0, 0, 0);
     }
+    {
+      // refill this ring entry (its tile is consumed) with the tile
+      // kPrefetch row blocks ahead
+      const uint32_t off = code_off(rb + kPrefetch * J.Gr);
+      pre[u] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(J.codes0) + off);
+      if (HAS2) pre1[u] = *reinterpret_cast<const uint2*>(J.codes1 + off / 2);
+    }
     // partial of this slice for rows 4q..4q+3, batch column r16, into this
     // row block's slot; the slots are reduced across the waves every
     // kRedSlots row blocks (and after the last), so the waves decode without
     // a barrier per row block
     const int slot = k % kRedSlots;
     float* rbuf = red + slot * kRedSlot;
-    if (r16 < A.B) {
+    if (valid && r16 < A.B) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         float v = J.s0 * (acc[j] + 0.5f * accs[j] - 0.25f * slice_shift);
@@ -313,7 +317,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
         rbuf[(w * 16 + 4 * q + j) * kMaxB + r16] = active ? v : 0.0f;
       }
     }
-    if (slot == kRedSlots - 1 || rb + J.Gr >= RB) {
+    if (valid && (slot == kRedSlots - 1 || rb + J.Gr >= RB)) {
       __syncthreads();
       // output o = (s * 16 + row) * B + b of slot s <= slot, summed over the
       // waves by tpo threads (waves part, part + tpo, ...), then across them;
@@ -341,6 +345,8 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
       }
       __syncthreads();  // the slots are free again
     }
+    k += valid;
+  }
   }
 
   // 4. completion: the last work-group applies the output transform
