@@ -32,6 +32,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0  # dense fp16 / bf16 matrix-core peak
 LLAMA2_7B = [("q", 4096, 4096), ("k", 4096, 4096), ("v", 4096, 4096), ("o", 4096, 4096),
              ("gate", 11008, 4096), ("up", 11008, 4096), ("down", 4096, 11008)]
 
@@ -46,6 +47,8 @@ def parse():
     p.add_argument("--skip-cpu", action="store_true")
     p.add_argument("--skip-batch16", action="store_true")
     p.add_argument("--skip-alt", action="store_true", help="do not time the other call pattern")
+    p.add_argument("--prefill", type=int, default=512,
+                   help="rows of the prefill (wide-batch) step also timed; 0 skips it")
     p.add_argument("--per-linear", action="store_true",
                    help="headline with one qs_linear_forward call per linear (the reference's call pattern) "
                         "instead of grouped launches for linears that share an input")
@@ -259,6 +262,26 @@ def time_graph(runner, steps, warmup):
     return e0.elapsed_time(e1) / steps  # ms
 
 
+def time_eager(runner, steps, warmup):
+    """ms per step, issued eagerly (the wide-batch path calls a library GEMM,
+    which is not captured in a graph)."""
+    import torch
+    for _ in range(max(warmup, 1)):
+        runner.step()
+    torch.cuda.synchronize()
+    ref = runner.buf["down"].clone()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        runner.step()
+    e1.record()
+    torch.cuda.synchronize()
+    if not torch.equal(runner.buf["down"], ref):
+        raise RuntimeError("prefill steps are not reproducible")
+    return e0.elapsed_time(e1) / steps
+
+
 def time_mv_kernels(runner, passes=3):
     """Average duration of the decode-matvec kernels, from HIP events attached
     to each kernel's dispatch (hipExtLaunchKernelGGL start / stop events, the
@@ -430,6 +453,19 @@ def main():
                             "mv_kernel_avg_us": round(mv16 * 1e3, 3)}
         log(f"batch 16: {ms16:.3f} ms/step")
         del r16
+    if args.prefill > 0:
+        P = args.prefill
+        rp = Runner(stack, P)
+        msp = time_eager(rp, max(args.steps // 4, 2), 2)
+        flops = 2 * P * args.layers * sum(m * n for _, m, n in LLAMA2_7B)
+        extra["prefill"] = {"rows": P, "ms_per_step": round(msp, 3), "tok_per_s": round(P * 1e3 / msp, 1),
+                            "TFLOPs": round(flops / msp / 1e9, 1),
+                            "mfma_frac_fp16_dense": round(flops / msp / 1e9 / MFMA_F16_PEAK_TFLOPS, 4),
+                            "path": "fp16 weight chunks (exact codebook values) x fp16 operand, rocBLAS GEMM "
+                                    "on the matrix cores"}
+        log(f"prefill {P} rows: {msp:.3f} ms/step, {flops / msp / 1e9:.1f} TFLOP/s")
+        del rp
+        torch.cuda.empty_cache()
     if not args.skip_quantize:
         extra["quantize_4096x4096_e8p_2bit"] = gpu_quantize(dev)
         log(f"quantize: {extra['quantize_4096x4096_e8p_2bit']}")

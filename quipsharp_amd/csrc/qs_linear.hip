@@ -45,9 +45,15 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 constexpr int kMaxParts = 16;  // work-groups per batch row for odd-factor transforms
 
 struct WsLayout {
-  size_t x2h, sg, xtot, xmul, x2, y1p, total;
+  size_t x2h, sg, xtot, xmul, x2, y1p, wq, wq2, total;
   int S, SG, W;
+  bool wide;
 };
+
+// From this many activation rows on, the tiled forward decodes the weights
+// into fp16 chunks once per call and multiplies them on the matrix cores
+// (qs_linear_wide.hip) instead of decoding them once per 16 rows.
+constexpr int64_t kWideMinBatch = 32;
 
 // Work-groups per batch row of the input / output transform: the odd-factor
 // stage is split over up to 16 of them (each computes L/G columns).
@@ -63,7 +69,8 @@ int parts_for(int64_t len, int p) {
 // counter; it must be zero before the first call and every call leaves it zero.
 WsLayout ws_layout(int64_t m, int64_t n, int64_t batch, int layout) {
   WsLayout L{};
-  const int64_t B = batch < kMaxTileBatch ? batch : kMaxTileBatch;
+  L.wide = layout == QS_LAYOUT_TILED && batch >= kWideMinBatch;
+  const int64_t B = L.wide ? batch : batch < kMaxTileBatch ? batch : kMaxTileBatch;
   size_t off = 256;
   if (layout == QS_LAYOUT_TILED) {
     L.S = (int)(n / 256);
@@ -79,7 +86,17 @@ WsLayout ws_layout(int64_t m, int64_t n, int64_t batch, int layout) {
     L.W = 0;
     L.x2 = off; off = align256(off + (size_t)B * n * 4);
   }
-  L.y1p = off; off = align256(off + (size_t)L.SG * B * m * 4);
+  if (L.wide) {
+    // y1 of all rows (one partial group) or the 16-row passes of the
+    // decode-matvec; two fp16 weight chunks
+    const size_t rows = (size_t)(L.SG * kMaxTileBatch > B ? L.SG * kMaxTileBatch : B);
+    L.y1p = off; off = align256(off + rows * m * 4);
+    const size_t chunk = (size_t)wide_chunk_rows(m, n) * n * 2;
+    L.wq = off; off = align256(off + chunk);
+    L.wq2 = off; off = align256(off + chunk);
+  } else {
+    L.y1p = off; off = align256(off + (size_t)L.SG * B * m * 4);
+  }
   L.total = off;
   return L;
 }
@@ -751,6 +768,98 @@ __global__ void busy_wait_kernel(uint64_t ticks, uint64_t max_iters) {
 
 using namespace qs;
 
+// The wide-batch path (tiled codes, kWideMinBatch rows or more): input
+// transform of every row, fp16 weight chunks times the fp16 operand on the
+// matrix cores (qs_linear_wide.hip), output transform of every row.  The
+// chunk-scheme row kernels take n and m they cover, the LDS-radix kernels
+// the rest.
+static int forward_wide(const void* x, int x_dtype, int64_t ldx, int64_t batch, int64_t n, int64_t m,
+                        const void* codes0, const void* codes1, const float* sv, const float* su, int kron_pn,
+                        const float* kron_n, int kron_pm, const float* kron_m, float s0, float s1, float layer_scale,
+                        const float* bias, void* y, int y_dtype, int64_t ldy, char* ws, const WsLayout& W,
+                        void* mv_begin, void* mv_end, hipStream_t s) {
+  QS_REQUIRE(batch <= (int64_t)1 << 30, "wide forward: at most 2^30 rows");
+  BatchedPass P{};
+  P.x = x;
+  P.x_dtype = x_dtype;
+  P.ldx = ldx;
+  P.B = (int)batch;
+  P.n = n;
+  P.m = m;
+  P.pn = kron_pn;
+  P.pm = kron_pm;
+  P.Kn = kron_n;
+  P.Km = kron_m;
+  P.sv = sv;
+  P.su = su;
+  P.layer_scale = layer_scale;
+  P.bias = bias;
+  P.y = y;
+  P.y_dtype = y_dtype;
+  P.ldy = ldy;
+  P.SG = 1;
+  P.x2h = reinterpret_cast<_Float16*>(ws + W.x2h);
+  P.sg = reinterpret_cast<_Float16*>(ws + W.sg);
+  P.xmul = reinterpret_cast<float*>(ws + W.xmul);
+  P.y1p = reinterpret_cast<float*>(ws + W.y1p);
+  int rc = QS_OK;
+  const bool sv_aligned = (reinterpret_cast<uintptr_t>(sv) & 15) == 0;
+  int Gx = 1;
+  if (chunk_transform_fits(n, kron_pn) && sv_aligned) {
+    rc = launch_bx_rows(P, s);
+  } else {
+    const size_t xin_lds = ((size_t)padded_len((int)n) + (size_t)kron_pn * kron_pn) * 4;
+    Gx = parts_for(n, kron_pn);
+    rc = set_lds((const void*)xin_kernel, xin_lds, &g_xin_lds);
+    if (rc) return rc;
+    const int Ln = (int)(n / kron_pn);
+    XinArgs XA{};
+    XA.x = x;
+    XA.x_dtype = x_dtype;
+    XA.ldx = ldx;
+    XA.n = (int)n;
+    XA.logL = log2_exact(Ln);
+    XA.p = kron_pn;
+    XA.G = Gx;
+    XA.K = kron_n;
+    XA.scale = inv_sqrt_len(Ln);
+    XA.sv = sv;
+    XA.identity = 0;
+    XA.tiled = 1;
+    XA.x2h = P.x2h;
+    XA.sg = P.sg;
+    XA.xtot = reinterpret_cast<float*>(ws + W.xtot);
+    XA.xmul = P.xmul;
+    XA.x2 = nullptr;
+    hipLaunchKernelGGL(xin_kernel, dim3((unsigned)(batch * Gx)), dim3(kRowThreads), xin_lds, s, XA);
+    QS_LAUNCHED("xin_kernel");
+  }
+  if (rc) return rc;
+
+  if (mv_begin) QS_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(mv_begin), s));
+  WideGemm G{};
+  G.codes0 = codes0;
+  G.codes1 = codes1;
+  G.m = m;
+  G.n = n;
+  G.B = (int)batch;
+  G.s0 = s0;
+  G.s1 = s1;
+  G.x2h = P.x2h;
+  G.y1 = P.y1p;
+  G.wbuf = reinterpret_cast<_Float16*>(ws + W.wq);
+  G.wbuf2 = reinterpret_cast<_Float16*>(ws + W.wq2);
+  G.ncu = cu_count();
+  rc = launch_linear_wide_gemm(G, s);
+  if (rc) return rc;
+  if (mv_end) QS_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(mv_end), s));
+
+  // the weights carry their +-1/4 shifts: no group-sum correction
+  if (chunk_transform_fits(m, kron_pm)) return launch_by_rows(P, s);
+  return launch_yout_rows(P.y1p, 1, (int)batch, m, kron_pm, kron_m, nullptr, 0, P.xmul, s0, layer_scale, su, bias, y,
+                          y_dtype, ldy, s);
+}
+
 // The batched path (and the decode-matvec without transforms): per block of
 // up to 16 batch rows, input transform -> decode-matvec -> output transform.
 static int forward_batched(const void* x, int x_dtype, int64_t ldx, int64_t batch, int64_t n, int64_t m,
@@ -759,6 +868,9 @@ static int forward_batched(const void* x, int x_dtype, int64_t ldx, int64_t batc
                     float layer_scale, const float* bias, void* y, int y_dtype, int64_t ldy, char* ws,
                     const WsLayout& W, void* mv_begin, void* mv_end, hipStream_t s, bool identity) {
   int rc = QS_OK;
+  if (!identity && W.wide)
+    return forward_wide(x, x_dtype, ldx, batch, n, m, codes0, codes1, sv, su, kron_pn, kron_n, kron_pm, kron_m, s0, s1,
+                        layer_scale, bias, y, y_dtype, ldy, ws, W, mv_begin, mv_end, s);
   if (!identity && layout == QS_LAYOUT_TILED && batched_eligible(n, kron_pn, m, kron_pm) &&
       (reinterpret_cast<uintptr_t>(sv) & 15) == 0) {
     // chunk-scheme passes of up to 16 rows (qs_linear_batched.hip)

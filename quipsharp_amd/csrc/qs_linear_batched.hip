@@ -380,16 +380,23 @@ bool batched_eligible(int64_t n, int pn, int64_t m, int pm) {
   return chunk_transform_fits(n, pn) && chunk_transform_fits(m, pm);
 }
 
-int launch_linear_batched(const BatchedPass& P, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop) {
-  QS_REQUIRE(P.B >= 1 && P.B <= kTB, "batched pass: 1..%d rows", kTB);
-  QS_REQUIRE(batched_eligible(P.n, P.pn, P.m, P.pm), "batched pass: shapes outside the chunk scheme");
+namespace {
+
+int check_lds() {
   static int done_x = 0, done_m0 = 0, done_m1 = 0, done_y = 0;
   int rc = lds_checked((const void*)bx_kernel, kBxLds, &done_x);
   if (!rc) rc = lds_checked((const void*)bm_kernel<false>, kBmLds, &done_m0);
   if (!rc) rc = lds_checked((const void*)bm_kernel<true>, kBmLds, &done_m1);
   if (!rc) rc = lds_checked((const void*)by_kernel, kByLds, &done_y);
-  if (rc) return rc;
+  return rc;
+}
 
+}  // namespace
+
+int launch_bx_rows(const BatchedPass& P, hipStream_t stream) {
+  QS_REQUIRE(chunk_transform_fits(P.n, P.pn), "input transform: n outside the chunk scheme");
+  int rc = check_lds();
+  if (rc) return rc;
   BxArgs X{};
   X.x = P.x;
   X.x_dtype = P.x_dtype;
@@ -410,6 +417,41 @@ int launch_linear_batched(const BatchedPass& P, hipStream_t stream, hipEvent_t e
   X.xmul = P.xmul;
   hipLaunchKernelGGL(bx_kernel, dim3(P.B), dim3(kThreads), kBxLds, stream, X);
   QS_LAUNCHED("bx_kernel");
+  return QS_OK;
+}
+
+int launch_by_rows(const BatchedPass& P, hipStream_t stream) {
+  QS_REQUIRE(chunk_transform_fits(P.m, P.pm), "output transform: m outside the chunk scheme");
+  QS_REQUIRE(P.SG >= 1 && P.SG <= kMaxSG, "output transform: 1..%d partial groups", kMaxSG);
+  int rc = check_lds();
+  if (rc) return rc;
+  ByArgs Y{};
+  Y.y1p = P.y1p;
+  Y.SG = P.SG;
+  Y.B = P.B;
+  Y.m = (int)P.m;
+  Y.Sm = (int)(P.m / 256);
+  Y.lsh_m = log2_exact((int)(P.m / P.pm / 256));
+  Y.pm = P.pm;
+  Y.Km = P.Km;
+  Y.xmul = P.xmul;
+  Y.scale_m = inv_sqrt_len((int)(P.m / P.pm));
+  Y.layer_scale = P.layer_scale;
+  Y.su = P.su;
+  Y.bias = P.bias;
+  Y.y = P.y;
+  Y.y_dtype = P.y_dtype;
+  Y.ldy = P.ldy;
+  hipLaunchKernelGGL(by_kernel, dim3(P.B), dim3(kThreads), kByLds, stream, Y);
+  QS_LAUNCHED("by_kernel");
+  return QS_OK;
+}
+
+int launch_linear_batched(const BatchedPass& P, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop) {
+  QS_REQUIRE(P.B >= 1 && P.B <= kTB, "batched pass: 1..%d rows", kTB);
+  QS_REQUIRE(batched_eligible(P.n, P.pn, P.m, P.pm), "batched pass: shapes outside the chunk scheme");
+  int rc = launch_bx_rows(P, stream);
+  if (rc) return rc;
 
   BmArgs M{};
   M.codes0 = static_cast<const uint16_t*>(P.codes0);
@@ -440,27 +482,7 @@ int launch_linear_batched(const BatchedPass& P, hipStream_t stream, hipEvent_t e
   else
     hipExtLaunchKernelGGL(bm_kernel<false>, dim3(grid), dim3(kThreads), kBmLds, stream, ev_start, ev_stop, 0, M);
   QS_LAUNCHED("bm_kernel");
-
-  ByArgs Y{};
-  Y.y1p = P.y1p;
-  Y.SG = P.SG;
-  Y.B = P.B;
-  Y.m = (int)P.m;
-  Y.Sm = (int)(P.m / 256);
-  Y.lsh_m = log2_exact((int)(P.m / P.pm / 256));
-  Y.pm = P.pm;
-  Y.Km = P.Km;
-  Y.xmul = P.xmul;
-  Y.scale_m = inv_sqrt_len((int)(P.m / P.pm));
-  Y.layer_scale = P.layer_scale;
-  Y.su = P.su;
-  Y.bias = P.bias;
-  Y.y = P.y;
-  Y.y_dtype = P.y_dtype;
-  Y.ldy = P.ldy;
-  hipLaunchKernelGGL(by_kernel, dim3(P.B), dim3(kThreads), kByLds, stream, Y);
-  QS_LAUNCHED("by_kernel");
-  return QS_OK;
+  return launch_by_rows(P, stream);
 }
 
 }  // namespace qs

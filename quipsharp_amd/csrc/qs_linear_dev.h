@@ -58,5 +58,28 @@ struct BatchedPass {
 };
 bool batched_eligible(int64_t n, int pn, int64_t m, int pm);
 int launch_linear_batched(const BatchedPass& P, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop);
+// The per-row input / output transform kernels of a pass on their own, for
+// any number of rows P.B (the output reads P.SG partial groups of P.B rows).
+int launch_bx_rows(const BatchedPass& P, hipStream_t stream);
+int launch_by_rows(const BatchedPass& P, hipStream_t stream);
+
+// Wide-batch GEMM (qs_linear_wide.hip): decode m x n codes into fp16 chunks
+// of wide_chunk_rows() rows and multiply by the fp16 operand on the matrix
+// cores, y1[B][m] = s0 X2 W0^T (+ s1 X2 W1^T).
+constexpr int64_t kWideChunkElems = (int64_t)16 << 20;  // fp16 elements per dequantized chunk
+struct WideGemm {
+  const void* codes0;
+  const void* codes1;
+  int64_t m, n;
+  int B;
+  float s0, s1;
+  const _Float16* x2h;   // [B][n]
+  float* y1;             // [B][m]
+  _Float16* wbuf;        // workspace: one chunk of stage-0 weights
+  _Float16* wbuf2;       // workspace: one chunk of stage-1 weights (codes1)
+  int ncu;
+};
+int64_t wide_chunk_rows(int64_t m, int64_t n);
+int launch_linear_wide_gemm(const WideGemm& G, hipStream_t stream);
 
 }  // namespace qs

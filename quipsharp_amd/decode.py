@@ -5,7 +5,8 @@ transformers implementation in bf16 with random weights.  Built on the meta
 device and materialized on the GPU, so the 32B-parameter model never exists
 densely.  Decoding runs through StaticDecoder (static fp32 KV cache, device
 positions and mask) so that each step is one HIP-graph replay.  Reports
-prefill time and decode tok/s.
+prefill time, decode tok/s and, per decoder linear of the first layer, the
+forward time and HBM GB/s at each batch size.
 
     python -m quipsharp_amd.decode --batch 1 8 --prompt 512 --new 256
 """
@@ -196,6 +197,53 @@ def greedy_decode_static(model, prompt_ids, new_tokens, use_graph=True):
     return torch.cat(toks, 1), t1 - t0, time.perf_counter() - t2
 
 
+def linear_bytes(m, n, B):
+    """Algorithmic HBM bytes of one quantized-linear call: 2-byte codes per 8
+    weights, bf16 activations in and out, 1-bit signs, fp16 scale."""
+    return m * n // 8 * 2 + 2 * B * (n + m) + -(-(m + n) // 8) + 2
+
+
+def linear_gbps(model, batches, reps=20):
+    """Per-linear forward time and HBM GB/s (algorithmic bytes) for the
+    decoder linears of the first layer, at each batch size: ``reps`` calls of
+    the module captured in one HIP graph, replayed and timed with events."""
+    layer = get_decoder_layers(model)[0]
+    out = []
+    dev = next(model.parameters()).device
+    for group in get_linear_groups(layer, 0):
+        for name, lin in group:
+            n, m = lin.in_features, lin.out_features
+            for B in batches:
+                x = torch.randn(B, n, device=dev).bfloat16()
+                with torch.no_grad():
+                    lin(x)  # workspace, packed codes
+                    torch.cuda.synchronize()
+                    s = torch.cuda.Stream(device=dev)
+                    s.wait_stream(torch.cuda.current_stream(dev))
+                    with torch.cuda.stream(s):
+                        lin(x)
+                    torch.cuda.current_stream(dev).wait_stream(s)
+                    torch.cuda.synchronize()
+                    g = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(g):
+                        for _ in range(reps):
+                            lin(x)
+                    g.replay()
+                    torch.cuda.synchronize()
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    for _ in range(5):
+                        g.replay()
+                    e1.record()
+                    torch.cuda.synchronize()
+                us = e0.elapsed_time(e1) * 1e3 / (5 * reps)
+                nb = linear_bytes(m, n, B)
+                out.append({"linear": name, "m": m, "n": n, "batch": B, "us": round(us, 2),
+                            "GBps": round(nb / (us * 1e-6) / 1e9, 1)})
+                del g
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--layers", type=int, default=64)
@@ -223,6 +271,7 @@ def main():
         res["runs"].append({"batch": B, "graph": not args.eager, "prefill_s": round(pre_s, 3), "decode_s": round(dec_s, 3),
                             "tok_per_s": round(B * steps / dec_s, 2), "ms_per_step": round(1e3 * dec_s / steps, 3),
                             "first_tokens": toks[0, :8].tolist()})
+    res["per_linear"] = linear_gbps(model, args.batch)
     print(json.dumps(res), flush=True)
 
 

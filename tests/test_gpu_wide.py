@@ -1,0 +1,111 @@
+"""GPU parity of the wide-batch forward (32 or more activation rows: the codes
+are decoded into fp16 weight chunks once per call and multiplied on the
+matrix cores) against the dense fp64 oracle.  Tolerance: relative 1e-3
+(norm-wise), as for the narrow paths; the dequantized weights are exact in
+fp16, so the error is the fp16 operand rounding and fp32 accumulation."""
+import numpy as np
+import pytest
+import torch
+
+from test_gpu_linear import REL_TOL, T64, _dense_weights, dense_forward, rel_err, run
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("m,n,B", [
+    (4096, 4096, 32),     # one weight chunk
+    (4096, 4096, 100),    # batch not a multiple of 16
+    (11008, 4096, 48),    # odd-factor outputs (43 x 256), three chunks
+    (4096, 11008, 40),    # odd-factor inputs, chunks of 1280 rows
+    (768, 512, 33),       # small: one chunk shorter than the chunk size
+])
+def test_wide_vs_dense_fp64(dev, m, n, B):
+    print(f"case: wide m={m} n={n} B={B}", flush=True)
+    rng = np.random.default_rng(m * 3 + n + B)
+    codes = rng.integers(0, 65536, (m, n // 8))
+    su, sv = rng.choice([-1.0, 1.0], m), rng.choice([-1.0, 1.0], n)
+    x = rng.standard_normal((B, n)).astype(np.float32)
+    y, packed = run(dev, x, codes, None, 1.0, 0.0, su, sv, 0.0135)
+    assert packed.layout == 1
+    want = dense_forward(x, codes, None, 1.0, 0.0, su, sv, 0.0135)
+    err = rel_err(y.cpu().numpy(), want)
+    print(f"  rel err {err:.2e}", flush=True)
+    assert err < REL_TOL
+
+
+@pytest.mark.parametrize("m,n,B", [(4096, 4096, 64), (14336, 4096, 33)])
+def test_wide_rvq3_vs_dense(dev, m, n, B):
+    """3-bit residual VQ: the E8 1-bit stage is a second GEMM accumulating
+    into the first (14336 rows: three full chunks and a half one)."""
+    print(f"case: wide rvq3 m={m} n={n} B={B}", flush=True)
+    rng = np.random.default_rng(m + B)
+    c0 = rng.integers(0, 65536, (m, n // 8))
+    c1 = rng.integers(0, 256, (m, n // 8))
+    su, sv = rng.choice([-1.0, 1.0], m), rng.choice([-1.0, 1.0], n)
+    x = rng.standard_normal((B, n)).astype(np.float32)
+    y, _ = run(dev, x, c0, c1, 0.93, 0.41, su, sv, 0.011)
+    want = dense_forward(x, c0, c1, 0.93, 0.41, su, sv, 0.011)
+    err = rel_err(y.cpu().numpy(), want)
+    print(f"  rel err {err:.2e}", flush=True)
+    assert err < REL_TOL
+
+
+@pytest.mark.parametrize("m,n,B", [(25600, 5120, 32), (5120, 25600, 32)])
+def test_wide_large_factor_shapes(dev, m, n, B):
+    """Qwen3-32B MLP shapes: 25600 = 25 x 1024 is transformed by the
+    LDS-radix row kernels, not the chunk-scheme ones."""
+    print(f"case: wide m={m} n={n} B={B}", flush=True)
+    rng = np.random.default_rng(m + 5 * n)
+    c0 = rng.integers(0, 65536, (m, n // 8))
+    su, sv = rng.choice([-1.0, 1.0], m), rng.choice([-1.0, 1.0], n)
+    W = _dense_weights(c0, None, 1.0, 0.0)
+    x = rng.standard_normal((B, n)).astype(np.float32)
+    y, _ = run(dev, x, c0, None, 1.0, 0.0, su, sv, 0.0135)
+    want = T64(T64(x.astype(np.float64) * sv) @ W.T * 0.0135) * su
+    err = rel_err(y.cpu().numpy(), want)
+    print(f"  rel err {err:.2e}", flush=True)
+    assert err < REL_TOL
+
+
+def test_wide_bf16_strided_bias(dev):
+    """bf16 activations read through a row stride, bf16 output, bias, and a
+    sign vector that is not 16-byte aligned (the LDS-radix input kernel)."""
+    m, n, B = 11008, 4096, 40
+    print(f"case: wide bf16 strided m={m} n={n} B={B}", flush=True)
+    rng = np.random.default_rng(77)
+    codes = rng.integers(0, 65536, (m, n // 8))
+    su, sv = rng.choice([-1.0, 1.0], m), rng.choice([-1.0, 1.0], n)
+    bias = rng.standard_normal(m).astype(np.float32)
+    x = rng.standard_normal((B, n)).astype(np.float32)
+    xb = torch.zeros(B, n + 64, dtype=torch.bfloat16, device=dev)
+    xb[:, :n] = torch.from_numpy(x).to(dev)
+    xs = xb[:, :n]
+    x_used = xs.float().cpu().numpy()
+    y, packed = run(dev, xs, codes, None, 1.0, 0.0, su, sv, 0.0135, bias=bias, out_dtype=torch.bfloat16)
+    assert y.dtype == torch.bfloat16
+    want = dense_forward(x_used, codes, None, 1.0, 0.0, su, sv, 0.0135, bias)
+    err = rel_err(y.float().cpu().numpy(), want)
+    print(f"  rel err {err:.2e}", flush=True)
+    assert err < 1e-2  # bf16 output rounding
+
+    from quipsharp_amd.quantize import forward_packed
+    svt = torch.from_numpy(np.concatenate([[0.0], sv]).astype(np.float32)).to(dev)[1:]
+    sut = torch.from_numpy(su.astype(np.float32)).to(dev)
+    y2 = forward_packed(torch.from_numpy(x).to(dev), packed, sut, svt, 1.0, 0.0, 0.0135,
+                        bias=torch.from_numpy(bias).to(dev), out_dtype=torch.float32)
+    err2 = rel_err(y2.cpu().numpy(), dense_forward(x, codes, None, 1.0, 0.0, su, sv, 0.0135, bias))
+    print(f"  unaligned sv: rel err {err2:.2e}", flush=True)
+    assert err2 < REL_TOL
+
+
+def test_wide_matches_narrow_path(dev):
+    """The first 16 rows of a wide call agree with a 16-row (batched path)
+    call on the same rows."""
+    m, n = 4096, 4096
+    rng = np.random.default_rng(5)
+    codes = rng.integers(0, 65536, (m, n // 8))
+    su, sv = rng.choice([-1.0, 1.0], m), rng.choice([-1.0, 1.0], n)
+    x = rng.standard_normal((64, n)).astype(np.float32)
+    yw, _ = run(dev, x, codes, None, 1.0, 0.0, su, sv, 0.0135)
+    yn, _ = run(dev, x[:16], codes, None, 1.0, 0.0, su, sv, 0.0135)
+    assert rel_err(yw[:16].cpu().numpy(), yn.cpu().numpy().astype(np.float64)) < 2e-4
