@@ -461,8 +461,8 @@ def main():
         extra["prefill"] = {"rows": P, "ms_per_step": round(msp, 3), "tok_per_s": round(P * 1e3 / msp, 1),
                             "TFLOPs": round(flops / msp / 1e9, 1),
                             "mfma_frac_fp16_dense": round(flops / msp / 1e9 / MFMA_F16_PEAK_TFLOPS, 4),
-                            "path": "fp16 weight chunks (exact codebook values) x fp16 operand, rocBLAS GEMM "
-                                    "on the matrix cores"}
+                            "path": "wg_kernel: E8P decode inside the GEMM loop, fp16 x fp16 -> fp32 MFMA "
+                                    "(16x16x32), codes' +-1/4 shifts via group-sum MFMAs"}
         log(f"prefill {P} rows: {msp:.3f} ms/step, {flops / msp / 1e9:.1f} TFLOP/s")
         del rp
         torch.cuda.empty_cache()

@@ -6,8 +6,7 @@ Each .hip file compiles to an object in quipsharp_amd/_build/, then one
 shared library is linked in the package directory so it travels with the
 source tree.  Code whose results must match the reference bit for bit
 (codebook encode/decode, Walsh-Hadamard) is compiled with
--ffp-contract=off; packed fp32 instructions are disabled everywhere.  The
-library links rocBLAS for the wide-batch (prefill) GEMM.
+-ffp-contract=off; packed fp32 instructions are disabled everywhere.
 """
 import concurrent.futures
 import os
@@ -51,9 +50,7 @@ def build(verbose=True):
     with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
         objs = list(ex.map(_compile, srcs))
     tmp = LIB + ".tmp"
-    rocm_lib = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib")
-    cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", tmp] + objs + [
-        "-L", rocm_lib, f"-Wl,-rpath,{rocm_lib}", "-lrocblas"]
+    cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", tmp] + objs
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")

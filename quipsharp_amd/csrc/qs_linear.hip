@@ -45,14 +45,15 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 constexpr int kMaxParts = 16;  // work-groups per batch row for odd-factor transforms
 
 struct WsLayout {
-  size_t x2h, sg, xtot, xmul, x2, y1p, wq, wq2, total;
+  size_t x2h, sg, xtot, xmul, x2, y1p, total;
   int S, SG, W;
   bool wide;
 };
 
-// From this many activation rows on, the tiled forward decodes the weights
-// into fp16 chunks once per call and multiplies them on the matrix cores
-// (qs_linear_wide.hip) instead of decoding them once per 16 rows.
+// From this many activation rows on, the tiled forward runs the wide GEMM
+// (qs_linear_wide.hip: each code decoded once per 256 activation rows, every
+// decoded fragment feeding several MFMAs) instead of decoding the codes once
+// per 16 rows.
 constexpr int64_t kWideMinBatch = 32;
 
 // Work-groups per batch row of the input / output transform: the odd-factor
@@ -63,42 +64,6 @@ int parts_for(int64_t len, int p) {
   int64_t g = L / 8;
   if (g > kMaxParts) g = kMaxParts;
   return g < 1 ? 1 : (int)g;
-}
-
-// The first 256 bytes of every workspace hold the fused kernel's completion
-// counter; it must be zero before the first call and every call leaves it zero.
-WsLayout ws_layout(int64_t m, int64_t n, int64_t batch, int layout) {
-  WsLayout L{};
-  L.wide = layout == QS_LAYOUT_TILED && batch >= kWideMinBatch;
-  const int64_t B = L.wide ? batch : batch < kMaxTileBatch ? batch : kMaxTileBatch;
-  size_t off = 256;
-  if (layout == QS_LAYOUT_TILED) {
-    L.S = (int)(n / 256);
-    L.SG = (L.S + kMaxWaves - 1) / kMaxWaves;
-    L.W = (L.S + L.SG - 1) / L.SG;
-    L.x2h = off; off = align256(off + (size_t)B * n * 2);
-    L.sg = off; off = align256(off + (size_t)B * (n / 8) * 2);
-    L.xtot = off; off = align256(off + (size_t)B * kMaxParts * 4);
-    L.xmul = off; off = align256(off + (size_t)B * 4);
-  } else {
-    L.S = 0;
-    L.SG = 1;
-    L.W = 0;
-    L.x2 = off; off = align256(off + (size_t)B * n * 4);
-  }
-  if (L.wide) {
-    // y1 of all rows (one partial group) or the 16-row passes of the
-    // decode-matvec; two fp16 weight chunks
-    const size_t rows = (size_t)(L.SG * kMaxTileBatch > B ? L.SG * kMaxTileBatch : B);
-    L.y1p = off; off = align256(off + rows * m * 4);
-    const size_t chunk = (size_t)wide_chunk_rows(m, n) * n * 2;
-    L.wq = off; off = align256(off + chunk);
-    L.wq2 = off; off = align256(off + chunk);
-  } else {
-    L.y1p = off; off = align256(off + (size_t)L.SG * B * m * 4);
-  }
-  L.total = off;
-  return L;
 }
 
 int cu_count() {
@@ -112,6 +77,42 @@ int cu_count() {
   }
   return cached[dev];
 }
+
+// The first 256 bytes of every workspace hold the fused kernel's completion
+// counter; it must be zero before the first call and every call leaves it zero.
+WsLayout ws_layout(int64_t m, int64_t n, int64_t batch, int layout) {
+  WsLayout L{};
+  L.wide = layout == QS_LAYOUT_TILED && batch >= kWideMinBatch;
+  const int64_t B = L.wide ? batch : batch < kMaxTileBatch ? batch : kMaxTileBatch;
+  size_t off = 256;
+  if (layout == QS_LAYOUT_TILED) {
+    L.S = (int)(n / 256);
+    L.SG = (L.S + kMaxWaves - 1) / kMaxWaves;
+    L.W = (L.S + L.SG - 1) / L.SG;
+    const size_t xrows = L.wide ? (size_t)(B + 15) / 16 * 16 : (size_t)B;  // fragment-major rows: 16s
+    L.x2h = off; off = align256(off + xrows * n * 2);
+    L.sg = off; off = align256(off + xrows * (n / 8) * 2);
+    L.xtot = off; off = align256(off + (size_t)B * kMaxParts * 4);
+    L.xmul = off; off = align256(off + (size_t)B * 4);
+  } else {
+    L.S = 0;
+    L.SG = 1;
+    L.W = 0;
+    L.x2 = off; off = align256(off + (size_t)B * n * 4);
+  }
+  if (L.wide) {
+    // partial groups of the wide GEMM, or the 16-row passes of the
+    // decode-matvec (which also takes this layout)
+    const int g0 = wide_splits(m, n, B, cu_count(), false), g1 = wide_splits(m, n, B, cu_count(), true);
+    const size_t a = (size_t)(g0 > g1 ? g0 : g1) * B, b = (size_t)L.SG * kMaxTileBatch;
+    L.y1p = off; off = align256(off + (a > b ? a : b) * m * 4);
+  } else {
+    L.y1p = off; off = align256(off + (size_t)L.SG * B * m * 4);
+  }
+  L.total = off;
+  return L;
+}
+
 
 // ---------------------------------------------------------------------------
 // input transform
@@ -131,6 +132,7 @@ struct XinArgs {
   float* xtot;  // [B][kMaxParts] partial sums of the rounded group sums
   float* xmul;
   float* x2;
+  int frag;     // x2h and sg fragment-major (wide GEMM operands; sg / 4)
 };
 
 // Deterministic block sum: per-wave tree, then waves in order.
@@ -221,9 +223,13 @@ __global__ __launch_bounds__(kRowThreads) void xin_kernel(XinArgs A) {
       h[k] = (_Float16)v[k];
       if (k) gsum = gsum + v[k];
     }
-    *reinterpret_cast<uint4*>(A.x2h + b * A.n + i0) = __builtin_bit_cast(uint4, h);
+    const size_t xo = A.frag ? frag_index(b, i0, A.n >> 8) : (size_t)(b * A.n + i0);
+    *reinterpret_cast<uint4*>(A.x2h + xo) = __builtin_bit_cast(uint4, h);
     const _Float16 hs = (_Float16)gsum;
-    A.sg[b * T + (i0 >> 3)] = hs;
+    if (A.frag)
+      A.sg[sg_frag_index(b, i0 >> 3, A.n >> 8)] = hs * (_Float16)0.25f;
+    else
+      A.sg[b * T + (i0 >> 3)] = hs;
     part_sum += (float)hs;
   }
   const float tot = block_reduce_sum(part_sum, red);
@@ -769,10 +775,10 @@ __global__ void busy_wait_kernel(uint64_t ticks, uint64_t max_iters) {
 using namespace qs;
 
 // The wide-batch path (tiled codes, kWideMinBatch rows or more): input
-// transform of every row, fp16 weight chunks times the fp16 operand on the
-// matrix cores (qs_linear_wide.hip), output transform of every row.  The
-// chunk-scheme row kernels take n and m they cover, the LDS-radix kernels
-// the rest.
+// transform of every row into the fragment-major fp16 operand, the GEMM with
+// the decode in its loop on the matrix cores (qs_linear_wide.hip), output
+// transform of every row.  The chunk-scheme row kernels take the n and m they
+// cover, the LDS-radix kernels the rest.
 static int forward_wide(const void* x, int x_dtype, int64_t ldx, int64_t batch, int64_t n, int64_t m,
                         const void* codes0, const void* codes1, const float* sv, const float* su, int kron_pn,
                         const float* kron_n, int kron_pm, const float* kron_m, float s0, float s1, float layer_scale,
@@ -802,6 +808,7 @@ static int forward_wide(const void* x, int x_dtype, int64_t ldx, int64_t batch, 
   P.sg = reinterpret_cast<_Float16*>(ws + W.sg);
   P.xmul = reinterpret_cast<float*>(ws + W.xmul);
   P.y1p = reinterpret_cast<float*>(ws + W.y1p);
+  P.frag = 1;
   int rc = QS_OK;
   const bool sv_aligned = (reinterpret_cast<uintptr_t>(sv) & 15) == 0;
   int Gx = 1;
@@ -831,33 +838,33 @@ static int forward_wide(const void* x, int x_dtype, int64_t ldx, int64_t batch, 
     XA.xtot = reinterpret_cast<float*>(ws + W.xtot);
     XA.xmul = P.xmul;
     XA.x2 = nullptr;
+    XA.frag = P.frag;
     hipLaunchKernelGGL(xin_kernel, dim3((unsigned)(batch * Gx)), dim3(kRowThreads), xin_lds, s, XA);
     QS_LAUNCHED("xin_kernel");
   }
   if (rc) return rc;
 
   if (mv_begin) QS_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(mv_begin), s));
-  WideGemm G{};
-  G.codes0 = codes0;
-  G.codes1 = codes1;
-  G.m = m;
-  G.n = n;
-  G.B = (int)batch;
-  G.s0 = s0;
-  G.s1 = s1;
-  G.x2h = P.x2h;
-  G.y1 = P.y1p;
-  G.wbuf = reinterpret_cast<_Float16*>(ws + W.wq);
-  G.wbuf2 = reinterpret_cast<_Float16*>(ws + W.wq2);
-  G.ncu = cu_count();
-  rc = launch_linear_wide_gemm(G, s);
+  WideMfma F{};
+  F.codes0 = codes0;
+  F.codes1 = codes1;
+  F.m = m;
+  F.n = n;
+  F.B = (int)batch;
+  F.s0 = s0;
+  F.s1 = s1;
+  F.x2f = P.x2h;
+  F.sgf = P.sg;
+  F.y1p = P.y1p;
+  F.SGk = wide_splits(m, n, batch, cu_count(), codes1 != nullptr);
+  rc = launch_linear_wide_mfma(F, s);
   if (rc) return rc;
   if (mv_end) QS_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(mv_end), s));
-
-  // the weights carry their +-1/4 shifts: no group-sum correction
+  // partial groups summed by the output kernels; the +-1/4 shifts are in y1
+  P.SG = F.SGk;
   if (chunk_transform_fits(m, kron_pm)) return launch_by_rows(P, s);
-  return launch_yout_rows(P.y1p, 1, (int)batch, m, kron_pm, kron_m, nullptr, 0, P.xmul, s0, layer_scale, su, bias, y,
-                          y_dtype, ldy, s);
+  return launch_yout_rows(P.y1p, F.SGk, (int)batch, m, kron_pm, kron_m, nullptr, 0, P.xmul, s0, layer_scale, su, bias,
+                          y, y_dtype, ldy, s);
 }
 
 // The batched path (and the decode-matvec without transforms): per block of

@@ -43,6 +43,7 @@ struct BxArgs {
   _Float16* x2h;  // [B][n] fp16 operand, index 256 slice + t
   _Float16* sg;   // [B][n / 8] sums of 8 consecutive operand values
   float* xmul;    // [B] 2^e
+  int frag;       // x2h and sg fragment-major (wide GEMM operands; sg / 4)
 };
 
 constexpr int kBxOffY = 0;                                  // kMaxS x kYStride floats
@@ -112,8 +113,13 @@ __global__ __launch_bounds__(kThreads) void bx_kernel(BxArgs A) {
         hs += lane_xor<2>(hs, lx);
         hs += lane_xor<4>(hs, lx);
         if (s < A.Sn) {
-          xrow[256 * s + t] = h;
-          if ((r16 & 7) == 0) srow[32 * s + (t >> 3)] = (_Float16)hs;
+          if (A.frag) {
+            A.x2h[frag_index(b, 256 * s + t, A.Sn)] = h;
+            if ((r16 & 7) == 0) A.sg[sg_frag_index(b, 32 * s + (t >> 3), A.Sn)] = (_Float16)hs * (_Float16)0.25f;
+          } else {
+            xrow[256 * s + t] = h;
+            if ((r16 & 7) == 0) srow[32 * s + (t >> 3)] = (_Float16)hs;
+          }
         }
       }
     }
@@ -415,6 +421,7 @@ int launch_bx_rows(const BatchedPass& P, hipStream_t stream) {
   X.x2h = P.x2h;
   X.sg = P.sg;
   X.xmul = P.xmul;
+  X.frag = P.frag;
   hipLaunchKernelGGL(bx_kernel, dim3(P.B), dim3(kThreads), kBxLds, stream, X);
   QS_LAUNCHED("bx_kernel");
   return QS_OK;

@@ -51,8 +51,9 @@ struct BatchedPass {
   int y_dtype;
   int64_t ldy;
   int S, SG, W, ncu;     // slices, slice groups, waves per group, CUs
-  _Float16* x2h;         // workspace: [B][n] fp16 operand
-  _Float16* sg;          // workspace: [B][n / 8] group sums
+  _Float16* x2h;         // workspace: [B][n] fp16 operand (fragment-major with frag)
+  _Float16* sg;          // workspace: [B][n / 8] group sums (fragment-major / 4 with frag)
+  int frag;              // input transform writes x2h and sg in the wide GEMM's fragment-major order
   float* xmul;           // workspace: [B]
   float* y1p;            // workspace: [SG][B][m]
 };
@@ -63,23 +64,44 @@ int launch_linear_batched(const BatchedPass& P, hipStream_t stream, hipEvent_t e
 int launch_bx_rows(const BatchedPass& P, hipStream_t stream);
 int launch_by_rows(const BatchedPass& P, hipStream_t stream);
 
-// Wide-batch GEMM (qs_linear_wide.hip): decode m x n codes into fp16 chunks
-// of wide_chunk_rows() rows and multiply by the fp16 operand on the matrix
-// cores, y1[B][m] = s0 X2 W0^T (+ s1 X2 W1^T).
-constexpr int64_t kWideChunkElems = (int64_t)16 << 20;  // fp16 elements per dequantized chunk
-struct WideGemm {
+// Fragment-major fp16 operand of the wide GEMM: row b, columns k .. k + 7 (k
+// a multiple of 8) are one 16-byte word, words ordered by [b / 16][k / 256]
+// [(k / 8) % 8][(k % 256) / 64][b % 16], so that the 64 lanes of a wave read
+// the B operand of one 16 x 16 x 32 MFMA step (16 rows, 32 columns in the
+// order the code tiles decode them) as 1 KiB of consecutive bytes.  Rows are
+// padded to a multiple of 16.  Returns the element index of (b, k).
+__host__ __device__ inline size_t frag_index(int64_t b, int64_t k, int S) {
+  const int64_t t = k & 255;
+  return (size_t)(((((b >> 4) * S + (k >> 8)) * 8 + ((t >> 3) & 7)) * 64 + (t >> 6) * 16 + (b & 15)) * 8 + (t & 7));
+}
+
+// Fragment-major group sums of the same operand, divided by 4: the sums of
+// row b over the 8-column groups G .. G + 7 of a 64-column quarter (G a
+// multiple of 8) are one 16-byte word, ordered [b / 16][G / 32][(G / 8) % 4]
+// [b % 16] -- the B operand of the MFMA that adds the codes' +-1/4 shifts.
+// Returns the element index of (b, G).
+__host__ __device__ inline size_t sg_frag_index(int64_t b, int64_t G, int S) {
+  return (size_t)((((((b >> 4) * S + (G >> 5)) * 4 + ((G >> 3) & 3)) * 16 + (b & 15)) * 8) + (G & 7));
+}
+
+// Wide-batch GEMM with the decode in the loop (qs_linear_wide.hip): y1p[g]
+// [B][m] = s0 X2 W0^T (+ s1 X2 W1^T) over the g-th of SGk groups of 256-column
+// slices, X2 fragment-major.
+struct WideMfma {
   const void* codes0;
   const void* codes1;
   int64_t m, n;
   int B;
   float s0, s1;
-  const _Float16* x2h;   // [B][n]
-  float* y1;             // [B][m]
-  _Float16* wbuf;        // workspace: one chunk of stage-0 weights
-  _Float16* wbuf2;       // workspace: one chunk of stage-1 weights (codes1)
-  int ncu;
+  const _Float16* x2f;
+  const _Float16* sgf;   // group sums / 4, fragment-major
+  float* y1p;            // [SGk][B][m]
+  int SGk;
 };
-int64_t wide_chunk_rows(int64_t m, int64_t n);
-int launch_linear_wide_gemm(const WideGemm& G, hipStream_t stream);
+// Slice groups for (m, n, B): enough work-groups for the chip, at most the
+// output kernel's partial-group limit.
+int wide_splits(int64_t m, int64_t n, int64_t B, int ncu, bool has2);
+int launch_linear_wide_mfma(const WideMfma& G, hipStream_t stream);
+
 
 }  // namespace qs
