@@ -410,6 +410,8 @@ def main():
         torch.cuda.synchronize()
         Runner(stack, 16).step()           # batch-16 matvec
         torch.cuda.synchronize()
+        Runner(stack, 512).step()          # prefill (wide GEMM)
+        torch.cuda.synchronize()
         gpu_quantize(dev, n=1024, tune_iters=1)  # encode / LDLQ kernels
         torch.cuda.synchronize()
         a = torch.ones(64 << 20, dtype=torch.float32, device=dev)

@@ -100,46 +100,71 @@ struct XSource {
   int S;    // chunks of 256
 };
 
-// Activation chunks of batch row b (times sv), chunk c = w + 16 u, as
-// element t = 4 lane + j.
-__device__ __forceinline__ void load_x(const XSource& X, const float* sv, int b, int w, int lane,
-                                       float (&v)[kCPW][4]) {
+// Activation chunks of batch row b as loaded (the words of x and of sv), so
+// that a row's loads can be issued one row ahead of their use.
+struct XRaw {
+  uint4 v[kCPW];
+  float4 s[kCPW];
+};
+__device__ __forceinline__ void load_x_raw(const XSource& X, const float* sv, int b, int w, int lane, XRaw& r) {
+#pragma unroll
+  for (int u = 0; u < kCPW; ++u) {
+    const int c = w + kWaves * u;
+    r.v[u] = make_uint4(0, 0, 0, 0);
+    r.s[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (c < X.S) {
+      const int i0 = 256 * c + 4 * lane;
+      r.s[u] = *reinterpret_cast<const float4*>(sv + i0);
+      const int64_t xi = (int64_t)b * X.ldx + i0;
+      if (X.vec && X.dtype == QS_DTYPE_F32) {
+        r.v[u] = *reinterpret_cast<const uint4*>(static_cast<const float*>(X.x) + xi);
+      } else if (X.vec) {
+        const uint2 t = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(X.x) + xi);
+        r.v[u] = make_uint4(t.x, t.y, 0, 0);
+      } else {
+        r.v[u] = make_uint4(__float_as_uint(load_as_float(X.x, X.dtype, xi)),
+                            __float_as_uint(load_as_float(X.x, X.dtype, xi + 1)),
+                            __float_as_uint(load_as_float(X.x, X.dtype, xi + 2)),
+                            __float_as_uint(load_as_float(X.x, X.dtype, xi + 3)));
+      }
+    }
+  }
+}
+
+// Activation chunks (times sv), chunk c = w + 16 u, as element t = 4 lane + j.
+__device__ __forceinline__ void finish_x(const XSource& X, const XRaw& r, int w, float (&v)[kCPW][4]) {
 #pragma unroll
   for (int u = 0; u < kCPW; ++u) {
     const int c = w + kWaves * u;
 #pragma unroll
     for (int j = 0; j < 4; ++j) v[u][j] = 0.0f;
     if (c < X.S) {
-      const int i0 = 256 * c + 4 * lane;
-      const float4 s = *reinterpret_cast<const float4*>(sv + i0);
-      const int64_t xi = (int64_t)b * X.ldx + i0;
+      const uint4 t = r.v[u];
       float x0, x1, x2, x3;
-      if (X.vec && X.dtype == QS_DTYPE_F32) {
-        const float4 t = *reinterpret_cast<const float4*>(static_cast<const float*>(X.x) + xi);
-        x0 = t.x, x1 = t.y, x2 = t.z, x3 = t.w;
-      } else if (X.vec) {
-        const uint2 t = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(X.x) + xi);
-        if (X.dtype == QS_DTYPE_BF16) {
-          x0 = __uint_as_float(t.x << 16), x1 = __uint_as_float(t.x & 0xFFFF0000u);
-          x2 = __uint_as_float(t.y << 16), x3 = __uint_as_float(t.y & 0xFFFF0000u);
-        } else {
-          x0 = (float)__builtin_bit_cast(_Float16, (uint16_t)(t.x & 0xFFFFu));
-          x1 = (float)__builtin_bit_cast(_Float16, (uint16_t)(t.x >> 16));
-          x2 = (float)__builtin_bit_cast(_Float16, (uint16_t)(t.y & 0xFFFFu));
-          x3 = (float)__builtin_bit_cast(_Float16, (uint16_t)(t.y >> 16));
-        }
+      if (X.vec && X.dtype == QS_DTYPE_BF16) {
+        x0 = __uint_as_float(t.x << 16), x1 = __uint_as_float(t.x & 0xFFFF0000u);
+        x2 = __uint_as_float(t.y << 16), x3 = __uint_as_float(t.y & 0xFFFF0000u);
+      } else if (X.vec && X.dtype == QS_DTYPE_F16) {
+        x0 = (float)__builtin_bit_cast(_Float16, (uint16_t)(t.x & 0xFFFFu));
+        x1 = (float)__builtin_bit_cast(_Float16, (uint16_t)(t.x >> 16));
+        x2 = (float)__builtin_bit_cast(_Float16, (uint16_t)(t.y & 0xFFFFu));
+        x3 = (float)__builtin_bit_cast(_Float16, (uint16_t)(t.y >> 16));
       } else {
-        x0 = load_as_float(X.x, X.dtype, xi);
-        x1 = load_as_float(X.x, X.dtype, xi + 1);
-        x2 = load_as_float(X.x, X.dtype, xi + 2);
-        x3 = load_as_float(X.x, X.dtype, xi + 3);
+        x0 = __uint_as_float(t.x), x1 = __uint_as_float(t.y), x2 = __uint_as_float(t.z), x3 = __uint_as_float(t.w);
       }
-      v[u][0] = x0 * s.x;
-      v[u][1] = x1 * s.y;
-      v[u][2] = x2 * s.z;
-      v[u][3] = x3 * s.w;
+      v[u][0] = x0 * r.s[u].x;
+      v[u][1] = x1 * r.s[u].y;
+      v[u][2] = x2 * r.s[u].z;
+      v[u][3] = x3 * r.s[u].w;
     }
   }
+}
+
+__device__ __forceinline__ void load_x(const XSource& X, const float* sv, int b, int w, int lane,
+                                       float (&v)[kCPW][4]) {
+  XRaw r;
+  load_x_raw(X, sv, b, w, lane, r);
+  finish_x(X, r, w, v);
 }
 
 // Chunks held as element t = 4 lane + j (the layout of load_x).
@@ -284,34 +309,47 @@ constexpr int kMaxSG = (kMaxS + kWaves - 1) / kWaves;  // column groups of the p
 // loads (partials written by other work-groups of the same launch).  (The
 // 256-point transform is the same for any assignment of the index bits to
 // lanes and registers.)
-template <bool ATOMIC>
-__device__ __forceinline__ void load_partials(const float* y1p, int m, int Sm, int SG, int B, int b, int w,
-                                              int lane, float (&zv)[kCPW][4]) {
-  float tmp[kMaxSG][kCPW][4];
+template <int G = kMaxSG>
+struct PRaw {
+  float v[G][kCPW][4];
+};
+template <bool ATOMIC, int G>
+__device__ __forceinline__ void load_partials_raw(const float* y1p, int m, int Sm, int SG, int B, int b, int w,
+                                                  int lane, PRaw<G>& r) {
 #pragma unroll
-  for (int g = 0; g < kMaxSG; ++g)
+  for (int g = 0; g < G; ++g)
 #pragma unroll
     for (int u = 0; u < kCPW; ++u) {
       const int c = w + kWaves * u;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) tmp[g][u][j] = 0.0f;
+      for (int j = 0; j < 4; ++j) r.v[g][u][j] = 0.0f;
       if (g < SG && c < Sm) {
         const float* src = y1p + ((size_t)g * B + b) * m + 256 * c + lane;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          tmp[g][u][j] = ATOMIC ? __hip_atomic_load(src + 64 * j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+          r.v[g][u][j] = ATOMIC ? __hip_atomic_load(src + 64 * j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
                                 : src[64 * j];
       }
     }
+}
+template <int G>
+__device__ __forceinline__ void sum_partials(const PRaw<G>& r, float (&zv)[kCPW][4]) {
 #pragma unroll
   for (int u = 0; u < kCPW; ++u)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      float v = tmp[0][u][j];
+      float v = r.v[0][u][j];
 #pragma unroll
-      for (int g = 1; g < kMaxSG; ++g) v += tmp[g][u][j];
+      for (int g = 1; g < G; ++g) v += r.v[g][u][j];
       zv[u][j] = v;
     }
+}
+template <bool ATOMIC>
+__device__ __forceinline__ void load_partials(const float* y1p, int m, int Sm, int SG, int B, int b, int w,
+                                              int lane, float (&zv)[kCPW][4]) {
+  PRaw<kMaxSG> r;
+  load_partials_raw<ATOMIC, kMaxSG>(y1p, m, Sm, SG, B, b, w, lane, r);
+  sum_partials(r, zv);
 }
 
 // Output values out[a][j] to y[base + idx[a][j]] (idx < 0: no output), one

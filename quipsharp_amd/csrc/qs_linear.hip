@@ -804,6 +804,7 @@ static int forward_wide(const void* x, int x_dtype, int64_t ldx, int64_t batch, 
   P.y_dtype = y_dtype;
   P.ldy = ldy;
   P.SG = 1;
+  P.ncu = cu_count();
   P.x2h = reinterpret_cast<_Float16*>(ws + W.x2h);
   P.sg = reinterpret_cast<_Float16*>(ws + W.sg);
   P.xmul = reinterpret_cast<float*>(ws + W.xmul);

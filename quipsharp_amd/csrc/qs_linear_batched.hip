@@ -36,6 +36,7 @@ struct BxArgs {
   const void* x;
   int x_dtype, x_vec;
   int64_t ldx;
+  int B;          // rows
   int n, Sn, lsh_n, pn;
   const float* Kn;
   float scale_n;
@@ -52,6 +53,8 @@ constexpr int kBxOffMl = kBxOffMh + kMBytes;
 constexpr int kBxOffMisc = kBxOffMl + kMBytes;              // row norm parts
 constexpr int kBxLds = kBxOffMisc + 4 * kWaves;
 
+// Rows b = blockIdx.x, + gridDim.x, ...: the next row's activations are
+// loaded while this row is transformed.
 __global__ __launch_bounds__(kThreads) void bx_kernel(BxArgs A) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
   float* Y = reinterpret_cast<float*>(lds + kBxOffY);
@@ -61,68 +64,78 @@ __global__ __launch_bounds__(kThreads) void bx_kernel(BxArgs A) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
   const int q = lane >> 4, r16 = lane & 15;
-  const int b = blockIdx.x;
   const LaneX lx = lane_x_init();
+  const XSource X{A.x, A.x_dtype, A.x_vec, A.ldx, A.Sn};
+  const int stride = (int)gridDim.x;
 
-  float xv[kCPW][4];
-  load_x(XSource{A.x, A.x_dtype, A.x_vec, A.ldx, A.Sn}, A.sv, b, w, lane, xv);
-  float kmv[3];
-  mmat_load(kmv, A.Sn, A.lsh_n, A.pn, A.Kn, tid);
-  float ss = 0.0f;
-#pragma unroll
-  for (int u = 0; u < kCPW; ++u)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) ss = __builtin_fmaf(xv[u][j], xv[u][j], ss);
-  ss = wave_sum(ss, lx);
-  if (lane == 0) wsum[w] = ss;
-  h256_chunks(xv, A.Sn, lane, lx);
-  store_chunks(Y, A.Sn, w, lane, xv);
-  mmat_store(kmv, A.Sn, A.lsh_n, Mh, Ml, tid);
-  __syncthreads();
-  float norm2 = 0.0f;
-#pragma unroll
-  for (int i = 0; i < kWaves; ++i) norm2 += wsum[i];
-  const int e = operand_exponent(norm2);
-  const float mul = ldexpf(A.scale_n, -e);
-  if (tid == 0) A.xmul[b] = ldexpf(1.0f, e);
-
-  // chunk stage: operand row (slice) s = 16 a + 4 q + j, column t = 16 w + r16
-  const int t = 16 * w + r16;
-  const int nrt = (A.Sn + 15) >> 4, nkb = (A.Sn + 31) >> 5;
-  floatx4 acc[3];
-#pragma unroll
-  for (int a = 0; a < 3; ++a) acc[a] = floatx4{0.f, 0.f, 0.f, 0.f};
-  for (int kb = 0; kb < nkb; ++kb) {
-    const ZOperand z = z_operand(Y, A.Sn, t, q, kb);
-#pragma unroll
-    for (int a = 0; a < 3; ++a)
-      if (a < nrt) acc[a] = mstage_step(acc[a], Mh, Ml, 16 * a, z, kb, A.pn > 1, q, r16);
+  XRaw xr;
+  load_x_raw(X, A.sv, (int)blockIdx.x, w, lane, xr);
+  {
+    float kmv[3];
+    mmat_load(kmv, A.Sn, A.lsh_n, A.pn, A.Kn, tid);
+    mmat_store(kmv, A.Sn, A.lsh_n, Mh, Ml, tid);
   }
-  _Float16* xrow = A.x2h + (size_t)b * A.n;
-  _Float16* srow = A.sg + (size_t)b * (A.n / 8);
+  for (int b = (int)blockIdx.x; b < A.B; b += stride) {
+    float xv[kCPW][4];
+    finish_x(X, xr, w, xv);
+    if (b + stride < A.B) load_x_raw(X, A.sv, b + stride, w, lane, xr);  // the next row
+    float ss = 0.0f;
 #pragma unroll
-  for (int a = 0; a < 3; ++a) {
-    if (a < nrt) {
+    for (int u = 0; u < kCPW; ++u)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int s = 16 * a + 4 * q + j;
-        const _Float16 h = (_Float16)(acc[a][j] * mul);
-        // sum of the 8 fp16 values of group t / 8 (lanes r16 & 7 = 0..7)
-        float hs = (float)h;
-        hs += lane_xor<1>(hs, lx);
-        hs += lane_xor<2>(hs, lx);
-        hs += lane_xor<4>(hs, lx);
-        if (s < A.Sn) {
-          if (A.frag) {
-            A.x2h[frag_index(b, 256 * s + t, A.Sn)] = h;
-            if ((r16 & 7) == 0) A.sg[sg_frag_index(b, 32 * s + (t >> 3), A.Sn)] = (_Float16)hs * (_Float16)0.25f;
-          } else {
-            xrow[256 * s + t] = h;
-            if ((r16 & 7) == 0) srow[32 * s + (t >> 3)] = (_Float16)hs;
+      for (int j = 0; j < 4; ++j) ss = __builtin_fmaf(xv[u][j], xv[u][j], ss);
+    ss = wave_sum(ss, lx);
+    if (lane == 0) wsum[w] = ss;
+    h256_chunks(xv, A.Sn, lane, lx);
+    store_chunks(Y, A.Sn, w, lane, xv);
+    __syncthreads();
+    float norm2 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) norm2 += wsum[i];
+    const int e = operand_exponent(norm2);
+    const float mul = ldexpf(A.scale_n, -e);
+    if (tid == 0) A.xmul[b] = ldexpf(1.0f, e);
+
+    // chunk stage: operand row (slice) s = 16 a + 4 q + j, column t = 16 w + r16
+    const int t = 16 * w + r16;
+    const int nrt = (A.Sn + 15) >> 4, nkb = (A.Sn + 31) >> 5;
+    floatx4 acc[3];
+#pragma unroll
+    for (int a = 0; a < 3; ++a) acc[a] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int kb = 0; kb < nkb; ++kb) {
+      const ZOperand z = z_operand(Y, A.Sn, t, q, kb);
+#pragma unroll
+      for (int a = 0; a < 3; ++a)
+        if (a < nrt) acc[a] = mstage_step(acc[a], Mh, Ml, 16 * a, z, kb, A.pn > 1, q, r16);
+    }
+    // destinations: natural rows, or the fragment-major operand whose index
+    // is a row part plus a column part (frag_index, sg_frag_index)
+    _Float16* xrow = A.x2h + (A.frag ? frag_index(b, 0, A.Sn) : (size_t)b * A.n);
+    _Float16* srow = A.sg + (A.frag ? sg_frag_index(b, 0, A.Sn) : (size_t)b * (A.n / 8));
+    const int xcol = A.frag ? ((t >> 3) & 7) * 512 + (t >> 6) * 128 + (t & 7) : t;     // + 4096 s (frag) / 256 s
+    const int scol = A.frag ? ((t >> 6) & 3) * 128 + ((t >> 3) & 7) : (t >> 3);        // + 512 s (frag) / 32 s
+    const int xs = A.frag ? 4096 : 256, ss_ = A.frag ? 512 : 32;
+    const _Float16 sgmul = A.frag ? (_Float16)0.25f : (_Float16)1.0f;
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+      if (a < nrt) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int s = 16 * a + 4 * q + j;
+          const _Float16 h = (_Float16)(acc[a][j] * mul);
+          // sum of the 8 fp16 values of group t / 8 (lanes r16 & 7 = 0..7)
+          float hs = (float)h;
+          hs += lane_xor<1>(hs, lx);
+          hs += lane_xor<2>(hs, lx);
+          hs += lane_xor<4>(hs, lx);
+          if (s < A.Sn) {
+            xrow[xs * s + xcol] = h;
+            if ((r16 & 7) == 0) srow[ss_ * s + scol] = (_Float16)hs * sgmul;
           }
         }
       }
     }
+    __syncthreads();  // Y and wsum are rewritten for the next row
   }
 }
 
@@ -313,6 +326,11 @@ constexpr int kByOffMh = kByOffY + kMaxS * kYStride * 4;
 constexpr int kByOffMl = kByOffMh + kMBytes;
 constexpr int kByLds = kByOffMl + kMBytes;
 
+// Rows b = blockIdx.x, + gridDim.x, ...; su, bias and M are loaded once.
+// With one partial group (G == 1) the next row's partial sums are loaded
+// while this row is transformed (with up to kMaxSG they would not fit the
+// registers alongside su and bias, and are loaded per row).
+template <int G>
 __global__ __launch_bounds__(kThreads) void by_kernel(ByArgs A) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
   float* Y = reinterpret_cast<float*>(lds + kByOffY);
@@ -321,17 +339,17 @@ __global__ __launch_bounds__(kThreads) void by_kernel(ByArgs A) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
   const int q = lane >> 4, r16 = lane & 15;
-  const int b = blockIdx.x;
   const int Sm = A.Sm;
   const int t = 16 * w + r16;
   const LaneX lx = lane_x_init();
+  const int stride = (int)gridDim.x;
 
   // loads in the order they are waited for: K entries of M, partial sums,
   // su and bias (unconditional loads from valid addresses)
   float kmv[3];
   mmat_load(kmv, Sm, A.lsh_m, A.pm, A.Km, tid);
-  float zv[kCPW][4];
-  load_partials<false>(A.y1p, A.m, Sm, A.SG, A.B, b, w, lane, zv);
+  PRaw<G> pr;
+  if (G == 1) load_partials_raw<false, G>(A.y1p, A.m, Sm, A.SG, A.B, (int)blockIdx.x, w, lane, pr);
   int oidx[3][4];
   float suo[3][4], bio[3][4];
   const float* const bsrc = A.bias ? A.bias : A.su;
@@ -346,27 +364,38 @@ __global__ __launch_bounds__(kThreads) void by_kernel(ByArgs A) {
       suo[a][j] = A.su[ii];
       bio[a][j] = bsrc[ii];
     }
-  const float mul = A.scale_m * A.layer_scale * A.xmul[b];
   mmat_store(kmv, Sm, A.lsh_m, Mh, Ml, tid);
-  h256_chunks(zv, Sm, lane, lx);
-  store_chunks_lanes(Y, Sm, w, lane, zv);
-  __syncthreads();
-  const int nrt = (Sm + 15) >> 4, nkb = (Sm + 31) >> 5;
-  floatx4 acc[3];
+  for (int b = (int)blockIdx.x; b < A.B; b += stride) {
+    float zv[kCPW][4];
+    if (G == 1) {
+      sum_partials(pr, zv);
+      if (b + stride < A.B) load_partials_raw<false, G>(A.y1p, A.m, Sm, A.SG, A.B, b + stride, w, lane, pr);
+    } else {
+      load_partials_raw<false, G>(A.y1p, A.m, Sm, A.SG, A.B, b, w, lane, pr);
+      sum_partials(pr, zv);
+    }
+    const float mul = A.scale_m * A.layer_scale * A.xmul[b];
+    h256_chunks(zv, Sm, lane, lx);
+    store_chunks_lanes(Y, Sm, w, lane, zv);
+    __syncthreads();
+    const int nrt = (Sm + 15) >> 4, nkb = (Sm + 31) >> 5;
+    floatx4 acc[3];
 #pragma unroll
-  for (int a = 0; a < 3; ++a) acc[a] = floatx4{0.f, 0.f, 0.f, 0.f};
-  for (int kb = 0; kb < nkb; ++kb) {
-    const ZOperand z = z_operand(Y, Sm, t, q, kb);
+    for (int a = 0; a < 3; ++a) acc[a] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int kb = 0; kb < nkb; ++kb) {
+      const ZOperand z = z_operand(Y, Sm, t, q, kb);
+#pragma unroll
+      for (int a = 0; a < 3; ++a)
+        if (a < nrt) acc[a] = mstage_step(acc[a], Mh, Ml, 16 * a, z, kb, A.pm > 1, q, r16);
+    }
+    float out[3][4];
 #pragma unroll
     for (int a = 0; a < 3; ++a)
-      if (a < nrt) acc[a] = mstage_step(acc[a], Mh, Ml, 16 * a, z, kb, A.pm > 1, q, r16);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) out[a][j] = acc[a][j] * mul * suo[a][j] + bsel * bio[a][j];
+    store_outputs(A.y, A.y_dtype, (int64_t)b * A.ldy, oidx, out);
+    __syncthreads();  // Y is rewritten for the next row
   }
-  float out[3][4];
-#pragma unroll
-  for (int a = 0; a < 3; ++a)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) out[a][j] = acc[a][j] * mul * suo[a][j] + bsel * bio[a][j];
-  store_outputs(A.y, A.y_dtype, (int64_t)b * A.ldy, oidx, out);
 }
 
 int lds_checked(const void* fn, size_t bytes, int* done) {
@@ -388,12 +417,20 @@ bool batched_eligible(int64_t n, int pn, int64_t m, int pm) {
 
 namespace {
 
+// Work-groups of a per-row kernel: one per row up to two per CU (each then
+// walks its rows with the next row's loads in flight).
+unsigned row_grid(int B, int ncu) {
+  const int cap = 2 * (ncu > 0 ? ncu : 256);
+  return (unsigned)(B < cap ? B : cap);
+}
+
 int check_lds() {
-  static int done_x = 0, done_m0 = 0, done_m1 = 0, done_y = 0;
+  static int done_x = 0, done_m0 = 0, done_m1 = 0, done_y1 = 0, done_y3 = 0;
   int rc = lds_checked((const void*)bx_kernel, kBxLds, &done_x);
   if (!rc) rc = lds_checked((const void*)bm_kernel<false>, kBmLds, &done_m0);
   if (!rc) rc = lds_checked((const void*)bm_kernel<true>, kBmLds, &done_m1);
-  if (!rc) rc = lds_checked((const void*)by_kernel, kByLds, &done_y);
+  if (!rc) rc = lds_checked((const void*)by_kernel<1>, kByLds, &done_y1);
+  if (!rc) rc = lds_checked((const void*)by_kernel<kMaxSG>, kByLds, &done_y3);
   return rc;
 }
 
@@ -411,6 +448,7 @@ int launch_bx_rows(const BatchedPass& P, hipStream_t stream) {
     X.x_vec = (reinterpret_cast<uintptr_t>(P.x) % align) == 0 && P.ldx % 4 == 0;
   }
   X.ldx = P.ldx;
+  X.B = P.B;
   X.n = (int)P.n;
   X.Sn = (int)(P.n / 256);
   X.lsh_n = log2_exact((int)(P.n / P.pn / 256));
@@ -422,7 +460,7 @@ int launch_bx_rows(const BatchedPass& P, hipStream_t stream) {
   X.sg = P.sg;
   X.xmul = P.xmul;
   X.frag = P.frag;
-  hipLaunchKernelGGL(bx_kernel, dim3(P.B), dim3(kThreads), kBxLds, stream, X);
+  hipLaunchKernelGGL(bx_kernel, dim3(row_grid(P.B, P.ncu)), dim3(kThreads), kBxLds, stream, X);
   QS_LAUNCHED("bx_kernel");
   return QS_OK;
 }
@@ -449,7 +487,10 @@ int launch_by_rows(const BatchedPass& P, hipStream_t stream) {
   Y.y = P.y;
   Y.y_dtype = P.y_dtype;
   Y.ldy = P.ldy;
-  hipLaunchKernelGGL(by_kernel, dim3(P.B), dim3(kThreads), kByLds, stream, Y);
+  if (P.SG == 1)
+    hipLaunchKernelGGL(by_kernel<1>, dim3(row_grid(P.B, P.ncu)), dim3(kThreads), kByLds, stream, Y);
+  else
+    hipLaunchKernelGGL(by_kernel<kMaxSG>, dim3(row_grid(P.B, P.ncu)), dim3(kThreads), kByLds, stream, Y);
   QS_LAUNCHED("by_kernel");
   return QS_OK;
 }

@@ -38,6 +38,7 @@ constexpr int kWgRowTiles = 8;     // 16-row code tiles per work-group
 template <bool HAS2>
 constexpr int wg_col_tiles() { return HAS2 ? 2 : 4; }
 constexpr int wg_cols(bool has2) { return 16 * (has2 ? 2 : 4) * (kWgThreads / 64); }
+constexpr int kWgRows = 16 * kWgRowTiles;
 constexpr int kWgCodeBuf = kWgRowTiles * 1024;           // code bytes of one slice
 constexpr int kWgOffCodes = kDqOffLut1 + 4096;           // 2 slices (the table staging before them)
 constexpr int kWgOffCodes1 = kWgOffCodes + 2 * kWgCodeBuf;  // 2 slices of second-stage bytes
@@ -262,6 +263,7 @@ __global__ __launch_bounds__(kWgThreads) void wg_kernel(WgArgs A) {
 }
 
 int wg_lds_done[2] = {0, 0};
+
 
 }  // namespace
 
