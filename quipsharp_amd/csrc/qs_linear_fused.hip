@@ -145,9 +145,11 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   const LaneX lx = lane_x_init();
 
   // 1. loads: the activations first (the transform waits for them), then the
-  //    abs table and K; the code tiles once the activations are in
-  float xv[kCPW][4];
-  load_x(XSource{A.x, A.x_dtype, A.x_vec, A.ldx, A.Sn}, J.sv, 0, w, lane, xv);
+  //    abs table and K; the code tiles once the activations are in.  The
+  //    LUTs are built from the table while the activations are in flight.
+  const XSource X{A.x, A.x_dtype, A.x_vec, A.ldx, A.Sn};
+  XRaw xr;
+  load_x_raw(X, J.sv, 0, w, lane, xr);
   uint4 trow = make_uint4(0, 0, 0, 0), t1row = make_uint4(0, 0, 0, 0);  // fp16 table rows
   if (tid < 256) {
     trow = *reinterpret_cast<const uint4*>(kE8Ph.w[tid]);
@@ -157,6 +159,14 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   const bool m_ok = active && lane < A.Sn;
   float mk = 1.0f;
   if (A.pn > 1 && m_ok) mk = A.Kn[(sl >> A.lsh_n) * A.pn + (lane >> A.lsh_n)];
+  if (tid < 256) {
+    tab16[tid] = trow;
+    if (HAS2) lut1[tid] = t1row;
+  }
+  __syncthreads();  // staged table complete
+  fill_luts(tab16, lut_hi, lut_lo, tid);
+  float xv[kCPW][4];
+  finish_x(X, xr, w, xv);
   // Code tiles stream through a ring of kPrefetch registers, refilled as
   // they are consumed.  The loads are unconditional (a tile past the end or
   // of an idle wave reads tile 0 instead) and the ring is unrolled, so the
@@ -172,7 +182,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   // 2. input transform, one batch row at a time, into fp16 operand rows
   float emul0 = 1.0f, emul1 = 1.0f;  // 2^e of batch rows 0 and 1
   for (int b = 0; b < A.B; ++b) {
-    if (b > 0) load_x(XSource{A.x, A.x_dtype, A.x_vec, A.ldx, A.Sn}, J.sv, b, w, lane, xv);
+    if (b > 0) load_x(X, J.sv, b, w, lane, xv);
     float ss = 0.0f;
 #pragma unroll
     for (int u = 0; u < kCPW; ++u)
@@ -182,12 +192,8 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
     if (lane == 0) wsum[w] = ss;
     h256_chunks(xv, A.Sn, lane, lx);
     if (b == 0) {
-      // table staging and K (read after the barrier below), before the
-      // code loads are issued so these stores do not wait for them
-      if (tid < 256) {
-        tab16[tid] = trow;
-        if (HAS2) lut1[tid] = t1row;
-      }
+      // K (read after the barrier below), before the code loads are issued
+      // so these stores do not wait for them
       {
         const int hm = (1 << A.lsh_n) - 1;
         const float v = m_ok ? ((__builtin_popcount(sl & lane & hm) & 1) ? -mk : mk) : 0.0f;
@@ -243,8 +249,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
       }
     }
   }
-  fill_luts(tab16, lut_hi, lut_lo, tid);
-  __syncthreads();  // LUTs and operand rows complete; the table staging area is free again
+  __syncthreads();  // operand rows complete
   // MFMA operand of lane (q, b = r16): columns 64q..64q+63 of this wave's slice
   const half8 hzero = {0, 0, 0, 0, 0, 0, 0, 0};
   half8 xb[8];
