@@ -50,11 +50,13 @@ struct WsLayout {
   bool wide;
 };
 
-// From this many activation rows on, the tiled forward runs the wide GEMM
-// (qs_linear_wide.hip: each code decoded once per 256 activation rows, every
-// decoded fragment feeding several MFMAs) instead of decoding the codes once
-// per 16 rows.
-constexpr int64_t kWideMinBatch = 32;
+// From this many activation rows on (more than one 16-row pass), the tiled
+// forward runs the wide GEMM (qs_linear_wide.hip: each code decoded once per
+// up to 256 activation rows, every decoded fragment feeding several MFMAs)
+// instead of decoding the codes once per 16 rows.  Measured at 17..48 rows
+// on the 7B shapes: 24 rows 28 / 34 / 52 us wide against 36 / 47 / 50 us in
+// two 16-row passes (4096x4096, 11008x4096, 4096x11008).
+constexpr int64_t kWideMinBatch = 17;
 
 // Work-groups per batch row of the input / output transform: the odd-factor
 // stage is split over up to 16 of them (each computes L/G columns).

@@ -1,4 +1,4 @@
-// Wide-batch quantized-linear forward (prefill: 32 or more activation rows
+// Wide-batch quantized-linear forward (prefill: 17 or more activation rows
 // per call), the path QuantizedLinear.forward takes for a long prompt
 // (quipsharp/checkpoint.py:141-146 -> quipsharp/quantize.py:116-124: the
 // reference decodes the whole weight and multiplies densely).  With many
@@ -33,11 +33,17 @@ constexpr int kDqOffLut1 = 32768;          // 256 x uint4 (E8 1-bit rows, fp16)
 // fragments through LDS.
 constexpr int kWgThreads = 256;
 constexpr int kWgRowTiles = 8;     // 16-row code tiles per work-group
-// 16-row activation tiles per wave: four (64 activation rows, 256 per
-// work-group), two with a second stage (whose accumulators take the registers)
-template <bool HAS2>
-constexpr int wg_col_tiles() { return HAS2 ? 2 : 4; }
-constexpr int wg_cols(bool has2) { return 16 * (has2 ? 2 : 4) * (kWgThreads / 64); }
+constexpr int kWgWaves = kWgThreads / 64;
+// 16-row activation tiles per wave (CT): four (64 activation rows per wave,
+// 256 per work-group) for wide batches, two with a second stage (whose
+// accumulators take the registers), and fewer for short batches so that no
+// wave multiplies tiles past the last row.  Wave w of work-group column ct
+// takes tiles 4 CT ct + w + 4 t, t < CT.
+inline int wg_ct(int64_t B, bool has2) {
+  const int64_t nbt = (B + 15) / 16;
+  const int ct = nbt <= kWgWaves ? 1 : nbt <= 2 * kWgWaves ? 2 : 4;
+  return has2 && ct > 2 ? 2 : ct;
+}
 constexpr int kWgRows = 16 * kWgRowTiles;
 constexpr int kWgCodeBuf = kWgRowTiles * 1024;           // code bytes of one slice
 constexpr int kWgOffCodes = kDqOffLut1 + 4096;           // 2 slices (the table staging before them)
@@ -62,9 +68,8 @@ struct WgArgs {
   float s0, s1;
 };
 
-template <bool HAS2>
+template <bool HAS2, int kWgColTiles>
 __global__ __launch_bounds__(kWgThreads) void wg_kernel(WgArgs A) {
-  constexpr int kWgColTiles = wg_col_tiles<HAS2>();
   extern __shared__ __attribute__((aligned(16))) char lds[];
   uint32_t* lut_hi = reinterpret_cast<uint32_t*>(lds + kDqOffHi);
   uint32_t* lut_lo = reinterpret_cast<uint32_t*>(lds + kDqOffLo);
@@ -121,7 +126,7 @@ __global__ __launch_bounds__(kWgThreads) void wg_kernel(WgArgs A) {
   const _Float16* sb[kWgColTiles];
 #pragma unroll
   for (int t = 0; t < kWgColTiles; ++t) {
-    int c = (ct * (kWgThreads / 64) + w) * kWgColTiles + t;
+    int c = kWgWaves * kWgColTiles * ct + w + kWgWaves * t;
     c = c < nbt ? c : nbt - 1;
     xb[t] = A.x2f + (size_t)c * A.S * 8 * 512 + 8 * lane;  // + (s * 8 + step) * 512 halves
     sb[t] = A.sgf + (size_t)c * A.S * 512 + 8 * lane;      // + s * 512 halves
@@ -134,9 +139,15 @@ __global__ __launch_bounds__(kWgThreads) void wg_kernel(WgArgs A) {
       dst[t] = *reinterpret_cast<const half8*>(xb[t] + ((size_t)s * 8 + step) * 512);
   };
 
+  // a wave with no activation tile of its own only helps copy the codes
+  // (with four tiles per wave, chosen for long batches, every wave but those
+  // of a ragged last column has work: no branch)
+  const bool wave_on = kWgColTiles == 4 || kWgWaves * kWgColTiles * ct + w < nbt;
   CodeCopy gc = load_codes(s_begin);
+  if (wave_on) {
 #pragma unroll
-  for (int k = 0; k < kWgAhead; ++k) load_b(s_begin, k, bring[k]);
+    for (int k = 0; k < kWgAhead; ++k) load_b(s_begin, k, bring[k]);
+  }
   if (tid < 256) {
     tab16[tid] = *reinterpret_cast<const uint4*>(kE8Ph.w[tid]);
     if (HAS2) lut1[tid] = *reinterpret_cast<const uint4*>(kE81h.w[tid]);
@@ -169,6 +180,7 @@ __global__ __launch_bounds__(kWgThreads) void wg_kernel(WgArgs A) {
         cw1[i] = *reinterpret_cast<const uint2*>(lds + kWgOffCodes1 + p * (kWgCodeBuf / 2) + 512 * i + 8 * lane);
     }
     gc = load_codes(s + 1);  // the next slice's tiles, stored after this slice
+    if (wave_on) {
     half8 sgs[kWgColTiles];  // group sums / 4 of this slice, used after its 8 steps
 #pragma unroll
     for (int t = 0; t < kWgColTiles; ++t) sgs[t] = *reinterpret_cast<const half8*>(sb[t] + (size_t)s * 512);
@@ -239,6 +251,7 @@ __global__ __launch_bounds__(kWgThreads) void wg_kernel(WgArgs A) {
       for (int t = 0; t < kWgColTiles; ++t)
         acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(so, sgs[t], acc[i][t], 0, 0, 0);
     }
+    }  // wave_on
     store_codes(p ^ 1, gc);
     __syncthreads();
   }
@@ -247,7 +260,7 @@ __global__ __launch_bounds__(kWgThreads) void wg_kernel(WgArgs A) {
   // row r16 of tile t: four consecutive outputs
 #pragma unroll
   for (int t = 0; t < kWgColTiles; ++t) {
-    const int b = ((ct * (kWgThreads / 64) + w) * kWgColTiles + t) * 16 + r16;
+    const int b = (kWgWaves * kWgColTiles * ct + w + kWgWaves * t) * 16 + r16;
     if (b >= A.B) continue;
     float* yrow = A.y1p + ((size_t)g * A.B + b) * A.m;
 #pragma unroll
@@ -262,13 +275,26 @@ __global__ __launch_bounds__(kWgThreads) void wg_kernel(WgArgs A) {
   }
 }
 
-int wg_lds_done[2] = {0, 0};
+template <bool HAS2, int CT>
+int launch_wg(const WgArgs& A, unsigned grid, hipStream_t stream) {
+  static int done = 0;
+  if (!done) {
+    hipFuncAttributes fa{};
+    QS_HIP(hipFuncGetAttributes(&fa, (const void*)wg_kernel<HAS2, CT>));
+    QS_REQUIRE(fa.sharedSizeBytes == 0, "wg_kernel must not use static LDS");
+    done = 1;
+  }
+  hipLaunchKernelGGL((wg_kernel<HAS2, CT>), dim3(grid), dim3(kWgThreads), kWgLds, stream, A);
+  QS_LAUNCHED("wg_kernel");
+  return QS_OK;
+}
 
 
 }  // namespace
 
 int wide_splits(int64_t m, int64_t n, int64_t B, int ncu, bool has2) {
-  const int64_t tiles = ((m / 16 + kWgRowTiles - 1) / kWgRowTiles) * ((B + wg_cols(has2) - 1) / wg_cols(has2));
+  const int64_t cols = 16 * kWgWaves * wg_ct(B, has2);
+  const int64_t tiles = ((m / 16 + kWgRowTiles - 1) / kWgRowTiles) * ((B + cols - 1) / cols);
   const int64_t S = n / 256;
   int64_t g = 1;
   while (g < kMaxSG && g < S && tiles * g < ncu) ++g;
@@ -280,13 +306,7 @@ int launch_linear_wide_mfma(const WideMfma& G, hipStream_t stream) {
   QS_REQUIRE(G.SGk >= 1 && G.SGk <= kMaxSG, "wide GEMM: 1..%d slice groups", kMaxSG);
   QS_REQUIRE(G.m * G.n / 4 < ((int64_t)1 << 40), "wide GEMM: codes too large");
   const bool has2 = G.codes1 != nullptr;
-  const void* kfn = has2 ? (const void*)wg_kernel<true> : (const void*)wg_kernel<false>;
-  if (!wg_lds_done[has2]) {
-    hipFuncAttributes fa{};
-    QS_HIP(hipFuncGetAttributes(&fa, kfn));
-    QS_REQUIRE(fa.sharedSizeBytes == 0, "wg_kernel must not use static LDS");
-    wg_lds_done[has2] = 1;
-  }
+  const int CT = wg_ct(G.B, has2);
   WgArgs A{};
   A.codes0 = static_cast<const uint16_t*>(G.codes0);
   A.codes1 = static_cast<const uint8_t*>(G.codes1);
@@ -298,19 +318,17 @@ int launch_linear_wide_mfma(const WideMfma& G, hipStream_t stream) {
   A.S = (int)(G.n / 256);
   A.RB = (int)(G.m / 16);
   A.nrt = (A.RB + kWgRowTiles - 1) / kWgRowTiles;
-  A.nct = (G.B + wg_cols(has2) - 1) / wg_cols(has2);
+  A.nct = (G.B + 16 * kWgWaves * CT - 1) / (16 * kWgWaves * CT);
   A.SGk = G.SGk;
   A.spg = (A.S + G.SGk - 1) / G.SGk;
   A.s0 = G.s0;
   A.s1 = G.s1;
   const int64_t grid = (int64_t)A.nrt * A.nct * A.SGk;
   QS_REQUIRE(grid < ((int64_t)1 << 31), "wide GEMM: grid too large");
-  if (has2)
-    hipLaunchKernelGGL(wg_kernel<true>, dim3((unsigned)grid), dim3(kWgThreads), kWgLds, stream, A);
-  else
-    hipLaunchKernelGGL(wg_kernel<false>, dim3((unsigned)grid), dim3(kWgThreads), kWgLds, stream, A);
-  QS_LAUNCHED("wg_kernel");
-  return QS_OK;
+  const unsigned g = (unsigned)grid;
+  if (has2) return CT == 1 ? launch_wg<true, 1>(A, g, stream) : launch_wg<true, 2>(A, g, stream);
+  return CT == 1 ? launch_wg<false, 1>(A, g, stream)
+                 : CT == 2 ? launch_wg<false, 2>(A, g, stream) : launch_wg<false, 4>(A, g, stream);
 }
 
 }  // namespace qs

@@ -1,4 +1,4 @@
-"""GPU parity of the wide-batch forward (32 or more activation rows: the codes
+"""GPU parity of the wide-batch forward (17 or more activation rows: the codes
 are decoded into fp16 weight chunks once per call and multiplied on the
 matrix cores) against the dense fp64 oracle.  Tolerance: relative 1e-3
 (norm-wise), as for the narrow paths; the dequantized weights are exact in
@@ -13,11 +13,15 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("m,n,B", [
-    (4096, 4096, 32),     # one weight chunk
+    (4096, 4096, 17),     # smallest wide batch: one tile per wave, three waves idle
+    (4096, 4096, 32),     # one tile per wave for two waves
     (4096, 4096, 100),    # batch not a multiple of 16
-    (11008, 4096, 48),    # odd-factor outputs (43 x 256), three chunks
-    (4096, 11008, 40),    # odd-factor inputs, chunks of 1280 rows
+    (11008, 4096, 48),    # odd-factor outputs (43 x 256), 86 weight row tiles
+    (4096, 11008, 40),    # odd-factor inputs: 43 slices in 3 slice groups of 15, 15, 13
     (768, 512, 33),       # small: one chunk shorter than the chunk size
+    (256, 256, 40),       # one slice, one weight row tile (two 16-row blocks past the end)
+    (1024, 2048, 300),    # four activation tiles per wave, ragged last work-group column
+    (2048, 1024, 129),    # two tiles per wave, one row past a tile
 ])
 def test_wide_vs_dense_fp64(dev, m, n, B):
     print(f"case: wide m={m} n={n} B={B}", flush=True)
@@ -33,10 +37,11 @@ def test_wide_vs_dense_fp64(dev, m, n, B):
     assert err < REL_TOL
 
 
-@pytest.mark.parametrize("m,n,B", [(4096, 4096, 64), (14336, 4096, 33)])
+@pytest.mark.parametrize("m,n,B", [(4096, 4096, 64), (14336, 4096, 33), (2048, 1024, 200)])
 def test_wide_rvq3_vs_dense(dev, m, n, B):
-    """3-bit residual VQ: the E8 1-bit stage is a second GEMM accumulating
-    into the first (14336 rows: three full chunks and a half one)."""
+    """3-bit residual VQ: the E8 1-bit stage is a second set of MFMAs and
+    accumulators, combined with its own scale at the end (14336 = 7 x 2048
+    output rows; 200 rows: two tiles per wave)."""
     print(f"case: wide rvq3 m={m} n={n} B={B}", flush=True)
     rng = np.random.default_rng(m + B)
     c0 = rng.integers(0, 65536, (m, n // 8))
