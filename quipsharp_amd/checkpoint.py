@@ -10,6 +10,7 @@ matvec kernels in the activation dtype (bf16/fp16/fp32) without a dense
 weight.  ``save_quantized_checkpoint`` / ``load_quantized_checkpoint`` read
 and write the reference's format (state dict + manifest).
 """
+import ctypes
 import json
 from pathlib import Path
 
@@ -120,6 +121,7 @@ class QuantizedLinear(nn.Module):
     def _apply(self, fn, *args, **kwargs):
         self._packed = None
         self._ws = None
+        self._group_ws = None
         return super()._apply(fn, *args, **kwargs)
 
     def packed(self, kinds):
@@ -153,6 +155,42 @@ class QuantizedLinear(nn.Module):
         if self._ws is None or self._ws.numel() < need or self._ws.device != x.device:
             self._ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=x.device)
         return self._ws
+
+
+def grouped_forward(x: Tensor, linears):
+    """Outputs of several QuantizedLinear modules that read the same x, in
+    one launch when the library's grouped forward covers them (1-2 rows, rht /
+    krht transforms, n a multiple of 256 up to 12288; qs_linear_forward_group)
+    and one call each otherwise.  Each output equals ``lin(x)``.  No
+    counterpart in the reference, which calls the linears one by one; meant
+    for callers that own several linears of one input (q/k/v, gate/up)."""
+    from . import _lib
+    from .hadamard import kron_factor
+    from .quantize import forward_packed_group
+    n = x.shape[-1]
+    rows = x.numel() // n if n else 0
+    fn = kron_factor(n) if n else None
+    ok = (1 <= len(linears) <= _lib.QS_MAX_GROUP and 1 <= rows <= 2 and n % 256 == 0 and n <= 12288
+          and fn is not None and n // fn[0] >= 256
+          and all(isinstance(l, QuantizedLinear) and l.transform_kind in ("rht", "krht") and l.in_features == n
+                  for l in linears))
+    if not ok:
+        return [l(x) for l in linears]
+    jobs = []
+    for l in linears:
+        kinds, s0, s1 = _forward_params(l.codebook, l.num_stages)
+        packed = l.packed(kinds)
+        if packed.layout != _lib.QS_LAYOUT_TILED:
+            return [l(x) for l in linears]
+        jobs.append((packed, l.su, l.sv, s0, s1, l._scale_f, l.bias))
+    lead = linears[0]
+    ms = (ctypes.c_int64 * len(linears))(*[l.out_features for l in linears])
+    need = _lib.lib().qs_linear_group_workspace_bytes(n, rows, len(linears), ms)
+    ws = getattr(lead, "_group_ws", None)
+    if ws is None or ws.numel() < need or ws.device != x.device:
+        ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=x.device)  # zeroed once, reused
+        lead._group_ws = ws
+    return forward_packed_group(x, jobs, out_dtype=x.dtype, workspace=ws)
 
 
 def replace_with_quantized_linear_(parent: nn.Module, attr: str, layer: QuantizedLayer, codebook,

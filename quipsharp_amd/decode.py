@@ -18,7 +18,7 @@ import torch
 from torch import nn
 
 from .architectures import get_decoder_layers, get_linear_groups
-from .checkpoint import QuantizedLinear, build_codebook
+from .checkpoint import QuantizedLinear, build_codebook, grouped_forward
 from .hadamard import is_pow2, kron_factor, rademacher
 
 QWEN3_32B = dict(hidden_size=5120, intermediate_size=25600, num_hidden_layers=64, num_attention_heads=64,
@@ -115,7 +115,9 @@ class StaticDecoder:
     KV cache of ``max_len`` positions per layer, positions passed as a device
     tensor, the causal mask built on the device, so one decode step can be
     captured once and replayed.  Attention runs in fp32 (keys and values are
-    kept in fp32)."""
+    kept in fp32).  q/k/v and gate/up, which read the same input, go through
+    one grouped launch each when the step has at most two rows
+    (checkpoint.grouped_forward)."""
 
     def __init__(self, model, batch, max_len):
         cfg = model.config
@@ -141,16 +143,18 @@ class StaticDecoder:
         for i, L in enumerate(self.layers):
             a = L.self_attn
             x = L.input_layernorm(h)
-            qs = a.q_norm(a.q_proj(x).view(B, q, self.nh, self.hd)).transpose(1, 2)
-            ks = a.k_norm(a.k_proj(x).view(B, q, self.nkv, self.hd)).transpose(1, 2)
-            vs = a.v_proj(x).view(B, q, self.nkv, self.hd).transpose(1, 2)
+            qo, ko, vo = grouped_forward(x, [a.q_proj, a.k_proj, a.v_proj])
+            qs = a.q_norm(qo.view(B, q, self.nh, self.hd)).transpose(1, 2)
+            ks = a.k_norm(ko.view(B, q, self.nkv, self.hd)).transpose(1, 2)
+            vs = vo.view(B, q, self.nkv, self.hd).transpose(1, 2)
             qs, ks = apply_rotary_pos_emb(qs, ks, cos, sin)
             self.k[i].index_copy_(2, pos, ks.float())
             self.v[i].index_copy_(2, pos, vs.float())
             o = F.scaled_dot_product_attention(qs.float(), self.k[i], self.v[i], attn_mask=mask, enable_gqa=True)
             h = h + a.o_proj(o.transpose(1, 2).reshape(B, q, self.nh * self.hd).to(h.dtype))
             x = L.post_attention_layernorm(h)
-            h = h + L.mlp.down_proj(L.mlp.act_fn(L.mlp.gate_proj(x)) * L.mlp.up_proj(x))
+            go, uo = grouped_forward(x, [L.mlp.gate_proj, L.mlp.up_proj])
+            h = h + L.mlp.down_proj(L.mlp.act_fn(go) * uo)
         return self.model.lm_head(m.norm(h[:, -1:]))[:, -1]
 
 

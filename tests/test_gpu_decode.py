@@ -81,3 +81,24 @@ def test_static_decoder_matches_transformers(dev):
     a, _, _ = greedy_decode_static(model, ids, 8, use_graph=False)
     b, _, _ = greedy_decode_static(model, ids, 8)
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("rows", [1, 2, 3])
+def test_grouped_forward_equals_separate_calls(dev, rows):
+    """checkpoint.grouped_forward: one launch for q/k/v (and gate/up) at 1-2
+    rows, bit-identical to calling the modules one by one; one call each
+    beyond."""
+    from quipsharp_amd.architectures import get_decoder_layers
+    from quipsharp_amd.checkpoint import grouped_forward
+    from quipsharp_amd.decode import random_quantized_model
+    model = random_quantized_model(_tiny_config(), dev, seed=3)
+    layer = get_decoder_layers(model)[0]
+    x = torch.randn(rows, 512, generator=torch.Generator().manual_seed(rows)).to(dev).bfloat16()
+    with torch.no_grad():
+        for mods in ([layer.self_attn.q_proj, layer.self_attn.k_proj, layer.self_attn.v_proj],
+                     [layer.mlp.gate_proj, layer.mlp.up_proj]):
+            got = grouped_forward(x, mods)
+            want = [m(x) for m in mods]
+            assert len(got) == len(want)
+            for g_, w_ in zip(got, want):
+                assert g_.dtype == w_.dtype and torch.equal(g_, w_)
