@@ -344,6 +344,29 @@ __device__ __forceinline__ void sum_partials(const PRaw<G>& r, float (&zv)[kCPW]
       zv[u][j] = v;
     }
 }
+// The same sum for any number of groups, one group at a time (groups in
+// ascending order, as sum_partials adds them).
+__device__ __forceinline__ void sum_partials_loop(const float* y1p, int m, int Sm, int SG, int B, int b, int w,
+                                                  int lane, float (&zv)[kCPW][4]) {
+#pragma unroll
+  for (int u = 0; u < kCPW; ++u)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) zv[u][j] = 0.0f;
+  for (int g = 0; g < SG; ++g)
+#pragma unroll
+    for (int u = 0; u < kCPW; ++u) {
+      const int c = w + kWaves * u;
+      if (c < Sm) {
+        const float* src = y1p + ((size_t)g * B + b) * m + 256 * c + lane;
+        float t[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) t[j] = src[64 * j];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) zv[u][j] = g == 0 ? t[j] : zv[u][j] + t[j];
+      }
+    }
+}
+
 template <bool ATOMIC>
 __device__ __forceinline__ void load_partials(const float* y1p, int m, int Sm, int SG, int B, int b, int w,
                                               int lane, float (&zv)[kCPW][4]) {

@@ -54,7 +54,7 @@ struct WsLayout {
 // forward runs the wide GEMM (qs_linear_wide.hip: each code decoded once per
 // up to 256 activation rows, every decoded fragment feeding several MFMAs)
 // instead of decoding the codes once per 16 rows.  Measured at 17..48 rows
-// on the 7B shapes: 24 rows 28 / 34 / 52 us wide against 36 / 47 / 50 us in
+// on the 7B shapes: 24 rows 23 / 34 / 35 us wide against 36 / 47 / 50 us in
 // two 16-row passes (4096x4096, 11008x4096, 4096x11008).
 constexpr int64_t kWideMinBatch = 17;
 

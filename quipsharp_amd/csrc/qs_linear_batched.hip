@@ -329,7 +329,8 @@ constexpr int kByLds = kByOffMl + kMBytes;
 // Rows b = blockIdx.x, + gridDim.x, ...; su, bias and M are loaded once.
 // With one partial group (G == 1) the next row's partial sums are loaded
 // while this row is transformed (with up to kMaxSG they would not fit the
-// registers alongside su and bias, and are loaded per row).
+// registers alongside su and bias, and are loaded per row); G == 0 sums any
+// number of groups one at a time.
 template <int G>
 __global__ __launch_bounds__(kThreads) void by_kernel(ByArgs A) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
@@ -348,8 +349,8 @@ __global__ __launch_bounds__(kThreads) void by_kernel(ByArgs A) {
   // su and bias (unconditional loads from valid addresses)
   float kmv[3];
   mmat_load(kmv, Sm, A.lsh_m, A.pm, A.Km, tid);
-  PRaw<G> pr;
-  if (G == 1) load_partials_raw<false, G>(A.y1p, A.m, Sm, A.SG, A.B, (int)blockIdx.x, w, lane, pr);
+  PRaw<1> pr;
+  if constexpr (G == 1) load_partials_raw<false, 1>(A.y1p, A.m, Sm, A.SG, A.B, (int)blockIdx.x, w, lane, pr);
   int oidx[3][4];
   float suo[3][4], bio[3][4];
   const float* const bsrc = A.bias ? A.bias : A.su;
@@ -367,12 +368,15 @@ __global__ __launch_bounds__(kThreads) void by_kernel(ByArgs A) {
   mmat_store(kmv, Sm, A.lsh_m, Mh, Ml, tid);
   for (int b = (int)blockIdx.x; b < A.B; b += stride) {
     float zv[kCPW][4];
-    if (G == 1) {
+    if constexpr (G == 1) {
       sum_partials(pr, zv);
-      if (b + stride < A.B) load_partials_raw<false, G>(A.y1p, A.m, Sm, A.SG, A.B, b + stride, w, lane, pr);
+      if (b + stride < A.B) load_partials_raw<false, 1>(A.y1p, A.m, Sm, A.SG, A.B, b + stride, w, lane, pr);
+    } else if constexpr (G == 0) {
+      sum_partials_loop(A.y1p, A.m, Sm, A.SG, A.B, b, w, lane, zv);
     } else {
-      load_partials_raw<false, G>(A.y1p, A.m, Sm, A.SG, A.B, b, w, lane, pr);
-      sum_partials(pr, zv);
+      PRaw<G> pg;
+      load_partials_raw<false, G>(A.y1p, A.m, Sm, A.SG, A.B, b, w, lane, pg);
+      sum_partials(pg, zv);
     }
     const float mul = A.scale_m * A.layer_scale * A.xmul[b];
     h256_chunks(zv, Sm, lane, lx);
@@ -425,12 +429,13 @@ unsigned row_grid(int B, int ncu) {
 }
 
 int check_lds() {
-  static int done_x = 0, done_m0 = 0, done_m1 = 0, done_y1 = 0, done_y3 = 0;
+  static int done_x = 0, done_m0 = 0, done_m1 = 0, done_y1 = 0, done_y3 = 0, done_y0 = 0;
   int rc = lds_checked((const void*)bx_kernel, kBxLds, &done_x);
   if (!rc) rc = lds_checked((const void*)bm_kernel<false>, kBmLds, &done_m0);
   if (!rc) rc = lds_checked((const void*)bm_kernel<true>, kBmLds, &done_m1);
   if (!rc) rc = lds_checked((const void*)by_kernel<1>, kByLds, &done_y1);
   if (!rc) rc = lds_checked((const void*)by_kernel<kMaxSG>, kByLds, &done_y3);
+  if (!rc) rc = lds_checked((const void*)by_kernel<0>, kByLds, &done_y0);
   return rc;
 }
 
@@ -467,7 +472,7 @@ int launch_bx_rows(const BatchedPass& P, hipStream_t stream) {
 
 int launch_by_rows(const BatchedPass& P, hipStream_t stream) {
   QS_REQUIRE(chunk_transform_fits(P.m, P.pm), "output transform: m outside the chunk scheme");
-  QS_REQUIRE(P.SG >= 1 && P.SG <= kMaxSG, "output transform: 1..%d partial groups", kMaxSG);
+  QS_REQUIRE(P.SG >= 1 && P.SG <= kWideMaxGroups, "output transform: 1..%d partial groups", kWideMaxGroups);
   int rc = check_lds();
   if (rc) return rc;
   ByArgs Y{};
@@ -489,8 +494,10 @@ int launch_by_rows(const BatchedPass& P, hipStream_t stream) {
   Y.ldy = P.ldy;
   if (P.SG == 1)
     hipLaunchKernelGGL(by_kernel<1>, dim3(row_grid(P.B, P.ncu)), dim3(kThreads), kByLds, stream, Y);
-  else
+  else if (P.SG <= kMaxSG)
     hipLaunchKernelGGL(by_kernel<kMaxSG>, dim3(row_grid(P.B, P.ncu)), dim3(kThreads), kByLds, stream, Y);
+  else
+    hipLaunchKernelGGL(by_kernel<0>, dim3(row_grid(P.B, P.ncu)), dim3(kThreads), kByLds, stream, Y);
   QS_LAUNCHED("by_kernel");
   return QS_OK;
 }

@@ -87,6 +87,8 @@ __host__ __device__ inline size_t sg_frag_index(int64_t b, int64_t G, int S) {
 // Wide-batch GEMM with the decode in the loop (qs_linear_wide.hip): y1p[g]
 // [B][m] = s0 X2 W0^T (+ s1 X2 W1^T) over the g-th of SGk groups of 256-column
 // slices, X2 fragment-major.
+// Slice groups of the wide GEMM (partial sums summed by the output kernels).
+constexpr int kWideMaxGroups = 8;
 struct WideMfma {
   const void* codes0;
   const void* codes1;

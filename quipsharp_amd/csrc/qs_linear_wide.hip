@@ -297,13 +297,13 @@ int wide_splits(int64_t m, int64_t n, int64_t B, int ncu, bool has2) {
   const int64_t tiles = ((m / 16 + kWgRowTiles - 1) / kWgRowTiles) * ((B + cols - 1) / cols);
   const int64_t S = n / 256;
   int64_t g = 1;
-  while (g < kMaxSG && g < S && tiles * g < ncu) ++g;
+  while (g < kWideMaxGroups && g < S && tiles * g < ncu) ++g;
   return (int)g;
 }
 
 int launch_linear_wide_mfma(const WideMfma& G, hipStream_t stream) {
   QS_REQUIRE(G.m % 16 == 0 && G.n % 256 == 0 && G.B >= 1, "wide GEMM: m %% 16, n %% 256");
-  QS_REQUIRE(G.SGk >= 1 && G.SGk <= kMaxSG, "wide GEMM: 1..%d slice groups", kMaxSG);
+  QS_REQUIRE(G.SGk >= 1 && G.SGk <= kWideMaxGroups, "wide GEMM: 1..%d slice groups", kWideMaxGroups);
   QS_REQUIRE(G.m * G.n / 4 < ((int64_t)1 << 40), "wide GEMM: codes too large");
   const bool has2 = G.codes1 != nullptr;
   const int CT = wg_ct(G.B, has2);
