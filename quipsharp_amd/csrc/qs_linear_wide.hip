@@ -79,8 +79,15 @@ __global__ __launch_bounds__(kWgThreads) void wg_kernel(WgArgs A) {
   const int lane = tid & 63, w = tid >> 6;
   const int q = lane >> 4, r16 = lane & 15;
 
-  // tile order: weight-row tiles fastest, then activation tiles, then groups
-  int bid = (int)blockIdx.x;
+  // Tiles are ordered weight-row tiles fastest, then activation tiles, then
+  // slice groups, and dealt to the XCDs in contiguous runs: work-group i runs
+  // on XCD i % 8, so tile (i % 8) * ceil(T / 8) + i / 8 keeps each XCD's L2 on
+  // a few activation columns and slice groups (the grid is rounded up to a
+  // multiple of 8; the surplus work-groups exit at once).
+  const int T = A.nrt * A.nct * A.SGk;
+  const int per = (T + 7) >> 3;
+  int bid = ((int)blockIdx.x & 7) * per + ((int)blockIdx.x >> 3);
+  if (bid >= T) return;
   const int rt = bid % A.nrt;
   bid /= A.nrt;
   const int ct = bid % A.nct;
@@ -323,8 +330,9 @@ int launch_linear_wide_mfma(const WideMfma& G, hipStream_t stream) {
   A.spg = (A.S + G.SGk - 1) / G.SGk;
   A.s0 = G.s0;
   A.s1 = G.s1;
-  const int64_t grid = (int64_t)A.nrt * A.nct * A.SGk;
-  QS_REQUIRE(grid < ((int64_t)1 << 31), "wide GEMM: grid too large");
+  const int64_t tiles = (int64_t)A.nrt * A.nct * A.SGk;
+  QS_REQUIRE(tiles < ((int64_t)1 << 30), "wide GEMM: grid too large");
+  const int64_t grid = (tiles + 7) / 8 * 8;  // XCD-contiguous tile order (see wg_kernel)
   const unsigned g = (unsigned)grid;
   if (has2) return CT == 1 ? launch_wg<true, 1>(A, g, stream) : launch_wg<true, 2>(A, g, stream);
   return CT == 1 ? launch_wg<false, 1>(A, g, stream)
