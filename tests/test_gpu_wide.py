@@ -22,6 +22,8 @@ pytestmark = pytest.mark.gpu
     (256, 256, 40),       # one slice, one weight row tile (two 16-row blocks past the end)
     (1024, 2048, 300),    # four activation tiles per wave, ragged last work-group column
     (2048, 1024, 129),    # two tiles per wave, one row past a tile
+    (1024, 2048, 500),    # two work-group columns of 256 rows, the second ragged
+    (784, 1024, 420),     # 49 row blocks: the last work-group row holds one; m = 49 x 16
 ])
 def test_wide_vs_dense_fp64(dev, m, n, B):
     print(f"case: wide m={m} n={n} B={B}", flush=True)
