@@ -750,6 +750,40 @@ int launch_yout_rows(const float* y1p, int SG, int B, int64_t m, int p, const fl
   return QS_OK;
 }
 
+// Input transform of B rows with the LDS-radix kernel (any n the transforms
+// allow): fp16 operand rows x2h (fragment-major with frag), group sums sg,
+// the rows' 2^e in xmul, partial group-sum totals in xtot.
+int launch_xin_rows(const void* x, int x_dtype, int64_t ldx, int64_t B, int64_t n, int p, const float* K,
+                    const float* sv, _Float16* x2h, _Float16* sg, float* xtot, float* xmul, int frag, hipStream_t s) {
+  const size_t xin_lds = ((size_t)padded_len((int)n) + (size_t)p * p) * 4;
+  const int G = parts_for(n, p);
+  int rc = set_lds((const void*)xin_kernel, xin_lds, &g_xin_lds);
+  if (rc) return rc;
+  const int L = (int)(n / p);
+  XinArgs XA{};
+  XA.x = x;
+  XA.x_dtype = x_dtype;
+  XA.ldx = ldx;
+  XA.n = (int)n;
+  XA.logL = log2_exact(L);
+  XA.p = p;
+  XA.G = G;
+  XA.K = K;
+  XA.scale = inv_sqrt_len(L);
+  XA.sv = sv;
+  XA.identity = 0;
+  XA.tiled = 1;
+  XA.x2h = x2h;
+  XA.sg = sg;
+  XA.xtot = xtot;
+  XA.xmul = xmul;
+  XA.x2 = nullptr;
+  XA.frag = frag;
+  hipLaunchKernelGGL(xin_kernel, dim3((unsigned)(B * G)), dim3(kRowThreads), xin_lds, s, XA);
+  QS_LAUNCHED("xin_kernel");
+  return QS_OK;
+}
+
 int check_transform(int64_t len, int p, const float* K, const char* which) {
   QS_REQUIRE(p >= 1 && (p & 1) && p <= QS_MAX_KRON, "%s: kron factor must be odd in [1, %d]", which, QS_MAX_KRON);
   QS_REQUIRE(len % p == 0, "%s: length %lld not divisible by %d", which, (long long)len, p);
@@ -814,37 +848,11 @@ static int forward_wide(const void* x, int x_dtype, int64_t ldx, int64_t batch, 
   P.frag = 1;
   int rc = QS_OK;
   const bool sv_aligned = (reinterpret_cast<uintptr_t>(sv) & 15) == 0;
-  int Gx = 1;
-  if (chunk_transform_fits(n, kron_pn) && sv_aligned) {
+  if (chunk_transform_fits(n, kron_pn) && sv_aligned)
     rc = launch_bx_rows(P, s);
-  } else {
-    const size_t xin_lds = ((size_t)padded_len((int)n) + (size_t)kron_pn * kron_pn) * 4;
-    Gx = parts_for(n, kron_pn);
-    rc = set_lds((const void*)xin_kernel, xin_lds, &g_xin_lds);
-    if (rc) return rc;
-    const int Ln = (int)(n / kron_pn);
-    XinArgs XA{};
-    XA.x = x;
-    XA.x_dtype = x_dtype;
-    XA.ldx = ldx;
-    XA.n = (int)n;
-    XA.logL = log2_exact(Ln);
-    XA.p = kron_pn;
-    XA.G = Gx;
-    XA.K = kron_n;
-    XA.scale = inv_sqrt_len(Ln);
-    XA.sv = sv;
-    XA.identity = 0;
-    XA.tiled = 1;
-    XA.x2h = P.x2h;
-    XA.sg = P.sg;
-    XA.xtot = reinterpret_cast<float*>(ws + W.xtot);
-    XA.xmul = P.xmul;
-    XA.x2 = nullptr;
-    XA.frag = P.frag;
-    hipLaunchKernelGGL(xin_kernel, dim3((unsigned)(batch * Gx)), dim3(kRowThreads), xin_lds, s, XA);
-    QS_LAUNCHED("xin_kernel");
-  }
+  else
+    rc = launch_xin_rows(x, x_dtype, ldx, batch, n, kron_pn, kron_n, sv, P.x2h, P.sg, reinterpret_cast<float*>(ws + W.xtot),
+                         P.xmul, P.frag, s);
   if (rc) return rc;
 
   if (mv_begin) QS_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(mv_begin), s));
@@ -881,9 +889,11 @@ static int forward_batched(const void* x, int x_dtype, int64_t ldx, int64_t batc
   if (!identity && W.wide)
     return forward_wide(x, x_dtype, ldx, batch, n, m, codes0, codes1, sv, su, kron_pn, kron_n, kron_pm, kron_m, s0, s1,
                         layer_scale, bias, y, y_dtype, ldy, ws, W, mv_begin, mv_end, s);
-  if (!identity && layout == QS_LAYOUT_TILED && batched_eligible(n, kron_pn, m, kron_pm) &&
-      (reinterpret_cast<uintptr_t>(sv) & 15) == 0) {
-    // chunk-scheme passes of up to 16 rows (qs_linear_batched.hip)
+  if (!identity && layout == QS_LAYOUT_TILED) {
+    // passes of up to 16 rows: input transform, decode-matvec on all 16 MFMA
+    // columns, output transform (qs_linear_batched.hip); an n or m outside
+    // the chunk scheme takes the LDS-radix row kernel for that side
+    const bool sv_aligned = (reinterpret_cast<uintptr_t>(sv) & 15) == 0;
     for (int64_t b0 = 0; b0 < batch; b0 += kMaxTileBatch) {
       BatchedPass P{};
       P.B = (int)(batch - b0 < kMaxTileBatch ? batch - b0 : kMaxTileBatch);
@@ -917,7 +927,21 @@ static int forward_batched(const void* x, int x_dtype, int64_t ldx, int64_t batc
       P.y1p = reinterpret_cast<float*>(ws + W.y1p);
       hipEvent_t ev0 = b0 == 0 ? reinterpret_cast<hipEvent_t>(mv_begin) : nullptr;
       hipEvent_t ev1 = b0 + kMaxTileBatch >= batch ? reinterpret_cast<hipEvent_t>(mv_end) : nullptr;
-      rc = launch_linear_batched(P, s, ev0, ev1);
+      if (batched_eligible(n, kron_pn, m, kron_pm) && sv_aligned) {
+        rc = launch_linear_batched(P, s, ev0, ev1);
+      } else {
+        if (chunk_transform_fits(n, kron_pn) && sv_aligned)
+          rc = launch_bx_rows(P, s);
+        else
+          rc = launch_xin_rows(P.x, x_dtype, ldx, P.B, n, kron_pn, kron_n, sv, P.x2h, P.sg,
+                               reinterpret_cast<float*>(ws + W.xtot), P.xmul, 0, s);
+        if (!rc) rc = launch_bm(P, s, ev0, ev1);
+        if (!rc && chunk_transform_fits(m, kron_pm))
+          rc = launch_by_rows(P, s);
+        else if (!rc)
+          rc = launch_yout_rows(P.y1p, P.SG, P.B, m, kron_pm, kron_m, nullptr, 0, P.xmul, s0, layer_scale, su, bias,
+                                P.y, y_dtype, ldy, s);
+      }
       if (rc) return rc;
     }
     return QS_OK;

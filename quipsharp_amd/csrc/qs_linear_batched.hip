@@ -502,12 +502,13 @@ int launch_by_rows(const BatchedPass& P, hipStream_t stream) {
   return QS_OK;
 }
 
-int launch_linear_batched(const BatchedPass& P, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop) {
+int launch_bm(const BatchedPass& P, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop) {
   QS_REQUIRE(P.B >= 1 && P.B <= kTB, "batched pass: 1..%d rows", kTB);
-  QS_REQUIRE(batched_eligible(P.n, P.pn, P.m, P.pm), "batched pass: shapes outside the chunk scheme");
-  int rc = launch_bx_rows(P, stream);
+  QS_REQUIRE(P.m % 16 == 0 && P.n % 256 == 0 && P.S == (int)(P.n / 256) && P.SG >= 1 && P.W >= 1 &&
+                 P.W <= kWaves && P.SG * P.W >= P.S,
+             "decode-matvec: bad slice grouping");
+  int rc = check_lds();
   if (rc) return rc;
-
   BmArgs M{};
   M.codes0 = static_cast<const uint16_t*>(P.codes0);
   M.codes1 = static_cast<const uint8_t*>(P.codes1);
@@ -537,7 +538,16 @@ int launch_linear_batched(const BatchedPass& P, hipStream_t stream, hipEvent_t e
   else
     hipExtLaunchKernelGGL(bm_kernel<false>, dim3(grid), dim3(kThreads), kBmLds, stream, ev_start, ev_stop, 0, M);
   QS_LAUNCHED("bm_kernel");
-  return launch_by_rows(P, stream);
+  return QS_OK;
+}
+
+int launch_linear_batched(const BatchedPass& P, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop) {
+  QS_REQUIRE(P.B >= 1 && P.B <= kTB, "batched pass: 1..%d rows", kTB);
+  QS_REQUIRE(batched_eligible(P.n, P.pn, P.m, P.pm), "batched pass: shapes outside the chunk scheme");
+  int rc = launch_bx_rows(P, stream);
+  if (!rc) rc = launch_bm(P, stream, ev_start, ev_stop);
+  if (!rc) rc = launch_by_rows(P, stream);
+  return rc;
 }
 
 }  // namespace qs

@@ -63,6 +63,9 @@ int launch_linear_batched(const BatchedPass& P, hipStream_t stream, hipEvent_t e
 // any number of rows P.B (the output reads P.SG partial groups of P.B rows).
 int launch_bx_rows(const BatchedPass& P, hipStream_t stream);
 int launch_by_rows(const BatchedPass& P, hipStream_t stream);
+// The decode-matvec of a pass on its own (any n; operand rows in x2h / sg,
+// natural layout), y1p[SG][B][m].
+int launch_bm(const BatchedPass& P, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop);
 
 // Fragment-major fp16 operand of the wide GEMM: row b, columns k .. k + 7 (k
 // a multiple of 8) are one 16-byte word, words ordered by [b / 16][k / 256]
