@@ -4,20 +4,15 @@
 //   y = su (.) T_m( layer_scale * W_hat @ T_n(sv (.) x) ) + bias,
 //   W_hat[r] = s0 * E8P(code0[r]) (+ s1 * E81(code1[r]))
 //
-// Three launches:
-//   xin_kernel      one work-group per batch row: sv-scaling and T_n in LDS,
-//                   then fp16 activations (per-row power-of-two scaled) and the
-//                   per-8-column sums used for the +-1/4 shift term.
-//   mv_tiled_kernel the HBM-bound part.  Codes stream once from HBM in
-//                   16-row x 32-code tiles (one 16-byte load per lane); each
-//                   code is turned into eight fp16 weights by two 8-byte reads
-//                   from 4096-entry LDS tables (coordinates 0..3 and 4..7, signs
-//                   folded in) and fed to v_mfma_f32_16x16x32_f16 with the
-//                   activations as the 16-column operand (one column per batch
-//                   row).  The +-1/4 shifts become one more MFMA per tile:
-//                   sum_g shift_bit_g * S_g, S_g the sum of x over group g.
-//   yout_kernel     one work-group per batch row: sums the column-group
-//                   partials, scales, T_m in LDS, su, bias, output dtype.
+// This file holds the entry points (qs_linear_forward, qs_linear_forward_group,
+// qs_decode_matvec), the workspace layout, and the kernels for the shapes the
+// chunk-scheme kernels do not take: the LDS-radix row transforms xin_kernel /
+// yout_kernel (any n, m up to 32768; the input or output side of a pass whose
+// n or m is outside the chunk scheme), yout_chunk_kernel, and the row-major
+// decode-matvec of the generic code layout (mv_generic_kernel).  Which path a
+// call takes: one launch for 1-2 rows (qs_linear_fused.hip), passes of 16
+// rows through the batched decode-matvec (qs_linear_batched.hip), the wide
+// GEMM from kWideMinBatch rows (qs_linear_wide.hip).
 #include <cmath>
 
 #include <hip/hip_ext.h>
@@ -238,178 +233,6 @@ __global__ __launch_bounds__(kRowThreads) void xin_kernel(XinArgs A) {
   if (tid == 0) {
     A.xtot[b * kMaxParts + part] = tot;
     if (part == 0) A.xmul[b] = ldexpf(1.0f, e);
-  }
-}
-
-// ---------------------------------------------------------------------------
-// decode-matvec, tiled layout, matrix cores
-// ---------------------------------------------------------------------------
-struct MvArgs {
-  const uint16_t* codes0;
-  const uint8_t* codes1;
-  const _Float16* x2h;
-  const _Float16* sg;
-  float* y1p;
-  int m, n, B, S, SG, W;
-  float s0, s1;
-};
-
-__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
-  _Float16 a = (_Float16)lo, b = (_Float16)hi;
-  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
-}
-
-constexpr int kPrefetch = 4;  // code tiles loaded ahead per wave
-
-template <bool HAS2>
-__global__ __launch_bounds__(kMaxWaves * 64) void mv_tiled_kernel(MvArgs A) {
-  __shared__ uint2 lut_hi[4096];
-  __shared__ uint2 lut_lo[4096];
-  __shared__ uint4 lut1[HAS2 ? 256 : 1];
-  __shared__ uint4 tab16[256];
-  __shared__ float red[kMaxWaves][16][kMaxTileBatch];
-
-  const int tid = threadIdx.x, nthr = blockDim.x;
-  const int lane = tid & 63;
-  const int w = tid >> 6;
-  const int q = lane >> 4, r16 = lane & 15;
-  const int RB = A.m >> 4;
-  const int nitems = RB * A.SG;
-  const int T = A.n >> 3;
-
-  // Issue this wave's first code-tile loads before building the tables.
-  uint4 pre[kPrefetch];
-  uint2 pre1[kPrefetch];
-#pragma unroll
-  for (int k = 0; k < kPrefetch; ++k) {
-    const int it = blockIdx.x + k * gridDim.x;
-    pre[k] = make_uint4(0, 0, 0, 0);
-    pre1[k] = make_uint2(0, 0);
-    if (it < nitems) {
-      const int sg = it / RB, rb = it - sg * RB;
-      const int sl = sg * A.W + w;
-      if (sl < A.S) {
-        const size_t tile = ((size_t)rb * A.S + sl) * 64 + lane;
-        pre[k] = *reinterpret_cast<const uint4*>(A.codes0 + tile * 8);
-        if (HAS2) pre1[k] = *reinterpret_cast<const uint2*>(A.codes1 + tile * 8);
-      }
-    }
-  }
-
-  // fp16 copy of the abs table, then the signed half-codeword tables:
-  // hi[H*256 + a] = coordinates 0..3 of row a with flips (f0..f3) from
-  // H = (f1 f2 f3 q), f0 = q^f1^f2^f3; lo[q*2048 + a*8 + (f4 f5 f6)] =
-  // coordinates 4..7, coordinate 7 flipped by q^f4^f5^f6.
-  for (int r = tid; r < 256; r += nthr)
-    tab16[r] = make_uint4(pack_h2(kE8P.v[r][0], kE8P.v[r][1]), pack_h2(kE8P.v[r][2], kE8P.v[r][3]),
-                          pack_h2(kE8P.v[r][4], kE8P.v[r][5]), pack_h2(kE8P.v[r][6], kE8P.v[r][7]));
-  if (HAS2)
-    for (int e = tid; e < 256; e += nthr)
-      lut1[e] = make_uint4(pack_h2(kE81.v[e][0], kE81.v[e][1]), pack_h2(kE81.v[e][2], kE81.v[e][3]),
-                           pack_h2(kE81.v[e][4], kE81.v[e][5]), pack_h2(kE81.v[e][6], kE81.v[e][7]));
-  __syncthreads();
-  for (int e = tid; e < 4096; e += nthr) {
-    {
-      const uint32_t H = e >> 8, a = e & 255;
-      const uint32_t f1 = (H >> 3) & 1, f2 = (H >> 2) & 1, f3 = (H >> 1) & 1;
-      const uint32_t f0 = (H & 1) ^ f1 ^ f2 ^ f3;
-      const uint4 t = tab16[a];
-      lut_hi[e] = make_uint2(t.x ^ ((f0 << 15) | (f1 << 31)), t.y ^ ((f2 << 15) | (f3 << 31)));
-    }
-    {
-      const uint32_t qq = e >> 11, a = (e >> 3) & 255;
-      const uint32_t f4 = (e >> 2) & 1, f5 = (e >> 1) & 1, f6 = e & 1;
-      const uint32_t f7 = qq ^ f4 ^ f5 ^ f6;
-      const uint4 t = tab16[a];
-      lut_lo[e] = make_uint2(t.z ^ ((f4 << 15) | (f5 << 31)), t.w ^ ((f6 << 15) | (f7 << 31)));
-    }
-  }
-  __syncthreads();
-
-  const half8 hzero = {0, 0, 0, 0, 0, 0, 0, 0};
-  int cur_sg = -1;
-  half8 xb[8];
-  half8 xs = hzero;
-#pragma unroll
-  for (int c = 0; c < 8; ++c) xb[c] = hzero;
-
-  int k = 0;
-  for (int it = blockIdx.x; it < nitems; it += gridDim.x, ++k) {
-    const int sg = it / RB, rb = it - sg * RB;
-    const int sl = sg * A.W + w;
-    const bool active = sl < A.S;
-    if (sg != cur_sg) {
-      cur_sg = sg;
-      const bool have = active && r16 < A.B;
-      const _Float16* xrow = A.x2h + (size_t)r16 * A.n + (size_t)256 * sl + 64 * q;
-#pragma unroll
-      for (int c = 0; c < 8; ++c) xb[c] = have ? *reinterpret_cast<const half8*>(xrow + 8 * c) : hzero;
-      xs = have ? *reinterpret_cast<const half8*>(A.sg + (size_t)r16 * T + 32 * sl + 8 * q) : hzero;
-    }
-    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-    floatx4 accs = {0.f, 0.f, 0.f, 0.f};
-    floatx4 acc2 = {0.f, 0.f, 0.f, 0.f};
-    if (active) {
-      uint4 cw;
-      uint2 cw1 = make_uint2(0, 0);
-      if (k < kPrefetch) {
-        cw = pre[0];
-        cw1 = pre1[0];
-#pragma unroll
-        for (int j = 0; j + 1 < kPrefetch; ++j) {  // rotate the prefetch ring
-          pre[j] = pre[j + 1];
-          pre1[j] = pre1[j + 1];
-        }
-      } else {
-        const size_t tile = ((size_t)rb * A.S + sl) * 64 + lane;
-        cw = *reinterpret_cast<const uint4*>(A.codes0 + tile * 8);
-        if (HAS2) cw1 = *reinterpret_cast<const uint2*>(A.codes1 + tile * 8);
-      }
-      const uint32_t wd[4] = {cw.x, cw.y, cw.z, cw.w};
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const uint32_t wv = wd[c >> 1];
-        const uint32_t ha = (c & 1) ? ((wv >> 17) & 0x7FF8u) : ((wv >> 1) & 0x7FF8u);
-        const uint32_t la = (c & 1) ? ((wv >> 14) & 0x7FF8u) : ((wv << 2) & 0x7FF8u);
-        const uint2 hv = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(lut_hi) + ha);
-        const uint2 lv = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(lut_lo) + la);
-        const half8 av = __builtin_bit_cast(half8, make_uint4(hv.x, hv.y, lv.x, lv.y));
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, xb[c], acc, 0, 0, 0);
-        if (HAS2) {
-          const uint32_t idx = ((c < 4 ? cw1.x : cw1.y) >> (8 * (c & 3))) & 0xFFu;
-          const half8 a2 = __builtin_bit_cast(half8, lut1[idx]);
-          acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, xb[c], acc2, 0, 0, 0);
-        }
-      }
-      const half8 ash = __builtin_bit_cast(
-          half8, make_uint4((wd[0] & 0x10001u) * 0x3C00u, (wd[1] & 0x10001u) * 0x3C00u,
-                            (wd[2] & 0x10001u) * 0x3C00u, (wd[3] & 0x10001u) * 0x3C00u));
-      accs = __builtin_amdgcn_mfma_f32_16x16x32_f16(ash, xs, accs, 0, 0, 0);
-    } else if (k < kPrefetch) {
-#pragma unroll
-      for (int j = 0; j + 1 < kPrefetch; ++j) {
-        pre[j] = pre[j + 1];
-        pre1[j] = pre1[j + 1];
-      }
-    }
-    // lane holds rows 4q..4q+3 of the tile for batch column r16
-    if (r16 < A.B) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float v = A.s0 * (acc[j] + 0.5f * accs[j]);
-        if (HAS2) v = v + A.s1 * acc2[j];
-        red[w][4 * q + j][r16] = active ? v : 0.0f;
-      }
-    }
-    __syncthreads();
-    const int nw = A.S - sg * A.W < A.W ? A.S - sg * A.W : A.W;
-    for (int u = tid; u < 16 * A.B; u += nthr) {
-      const int row = u / A.B, bc = u - row * A.B;
-      float s = red[0][row][bc];
-      for (int ww = 1; ww < nw; ++ww) s += red[ww][row][bc];
-      A.y1p[((size_t)sg * A.B + bc) * A.m + rb * 16 + row] = s;
-    }
-    __syncthreads();
   }
 }
 
@@ -754,12 +577,13 @@ int launch_yout_rows(const float* y1p, int SG, int B, int64_t m, int p, const fl
 // allow): fp16 operand rows x2h (fragment-major with frag), group sums sg,
 // the rows' 2^e in xmul, partial group-sum totals in xtot.
 int launch_xin_rows(const void* x, int x_dtype, int64_t ldx, int64_t B, int64_t n, int p, const float* K,
-                    const float* sv, _Float16* x2h, _Float16* sg, float* xtot, float* xmul, int frag, hipStream_t s) {
+                    const float* sv, _Float16* x2h, _Float16* sg, float* xtot, float* xmul, int frag, hipStream_t s,
+                    bool identity = false) {
   const size_t xin_lds = ((size_t)padded_len((int)n) + (size_t)p * p) * 4;
-  const int G = parts_for(n, p);
+  const int G = identity ? 1 : parts_for(n, p);
   int rc = set_lds((const void*)xin_kernel, xin_lds, &g_xin_lds);
   if (rc) return rc;
-  const int L = (int)(n / p);
+  const int L = identity ? 1 : (int)(n / p);
   XinArgs XA{};
   XA.x = x;
   XA.x_dtype = x_dtype;
@@ -769,9 +593,9 @@ int launch_xin_rows(const void* x, int x_dtype, int64_t ldx, int64_t B, int64_t 
   XA.p = p;
   XA.G = G;
   XA.K = K;
-  XA.scale = inv_sqrt_len(L);
+  XA.scale = identity ? 1.0f : inv_sqrt_len(L);
   XA.sv = sv;
-  XA.identity = 0;
+  XA.identity = identity;
   XA.tiled = 1;
   XA.x2h = x2h;
   XA.sg = sg;
@@ -889,7 +713,7 @@ static int forward_batched(const void* x, int x_dtype, int64_t ldx, int64_t batc
   if (!identity && W.wide)
     return forward_wide(x, x_dtype, ldx, batch, n, m, codes0, codes1, sv, su, kron_pn, kron_n, kron_pm, kron_m, s0, s1,
                         layer_scale, bias, y, y_dtype, ldy, ws, W, mv_begin, mv_end, s);
-  if (!identity && layout == QS_LAYOUT_TILED) {
+  if (layout == QS_LAYOUT_TILED) {
     // passes of up to 16 rows: input transform, decode-matvec on all 16 MFMA
     // columns, output transform (qs_linear_batched.hip); an n or m outside
     // the chunk scheme takes the LDS-radix row kernel for that side
@@ -927,25 +751,26 @@ static int forward_batched(const void* x, int x_dtype, int64_t ldx, int64_t batc
       P.y1p = reinterpret_cast<float*>(ws + W.y1p);
       hipEvent_t ev0 = b0 == 0 ? reinterpret_cast<hipEvent_t>(mv_begin) : nullptr;
       hipEvent_t ev1 = b0 + kMaxTileBatch >= batch ? reinterpret_cast<hipEvent_t>(mv_end) : nullptr;
-      if (batched_eligible(n, kron_pn, m, kron_pm) && sv_aligned) {
+      if (!identity && batched_eligible(n, kron_pn, m, kron_pm) && sv_aligned) {
         rc = launch_linear_batched(P, s, ev0, ev1);
       } else {
-        if (chunk_transform_fits(n, kron_pn) && sv_aligned)
+        if (!identity && chunk_transform_fits(n, kron_pn) && sv_aligned)
           rc = launch_bx_rows(P, s);
         else
           rc = launch_xin_rows(P.x, x_dtype, ldx, P.B, n, kron_pn, kron_n, sv, P.x2h, P.sg,
-                               reinterpret_cast<float*>(ws + W.xtot), P.xmul, 0, s);
+                               reinterpret_cast<float*>(ws + W.xtot), P.xmul, 0, s, identity);
         if (!rc) rc = launch_bm(P, s, ev0, ev1);
-        if (!rc && chunk_transform_fits(m, kron_pm))
+        if (!rc && !identity && chunk_transform_fits(m, kron_pm))
           rc = launch_by_rows(P, s);
         else if (!rc)
           rc = launch_yout_rows(P.y1p, P.SG, P.B, m, kron_pm, kron_m, nullptr, 0, P.xmul, s0, layer_scale, su, bias,
-                                P.y, y_dtype, ldy, s);
+                                P.y, y_dtype, ldy, s, identity);
       }
       if (rc) return rc;
     }
     return QS_OK;
   }
+  // row-major (generic) code layout: fp32 operand rows, vector-unit decode-matvec
   const int Ln = identity ? 1 : (int)(n / kron_pn);
   const size_t xin_lds = ((size_t)padded_len((int)n) + (size_t)kron_pn * kron_pn) * 4;
   const int Gx = identity ? 1 : parts_for(n, kron_pn);
@@ -969,11 +794,7 @@ static int forward_batched(const void* x, int x_dtype, int64_t ldx, int64_t batc
     XA.scale = identity ? 1.0f : inv_sqrt_len(Ln);
     XA.sv = sv;
     XA.identity = identity;
-    XA.tiled = layout == QS_LAYOUT_TILED;
-    XA.x2h = reinterpret_cast<_Float16*>(ws + W.x2h);
-    XA.sg = reinterpret_cast<_Float16*>(ws + W.sg);
-    XA.xtot = reinterpret_cast<float*>(ws + W.xtot);
-    XA.xmul = reinterpret_cast<float*>(ws + W.xmul);
+    XA.tiled = 0;
     XA.x2 = reinterpret_cast<float*>(ws + W.x2);
     hipLaunchKernelGGL(xin_kernel, dim3(B * Gx), dim3(kRowThreads), xin_lds, s, XA);
     QS_LAUNCHED("xin_kernel");
@@ -981,52 +802,21 @@ static int forward_batched(const void* x, int x_dtype, int64_t ldx, int64_t batc
     float* y1p = reinterpret_cast<float*>(ws + W.y1p);
     hipEvent_t ev0 = b0 == 0 ? reinterpret_cast<hipEvent_t>(mv_begin) : nullptr;
     hipEvent_t ev1 = b0 + kMaxTileBatch >= batch ? reinterpret_cast<hipEvent_t>(mv_end) : nullptr;
-    if (layout == QS_LAYOUT_TILED) {
-      MvArgs MA{};
-      MA.codes0 = static_cast<const uint16_t*>(codes0);
-      MA.codes1 = static_cast<const uint8_t*>(codes1);
-      MA.x2h = XA.x2h;
-      MA.sg = XA.sg;
-      MA.y1p = y1p;
-      MA.m = (int)m;
-      MA.n = (int)n;
-      MA.B = B;
-      MA.S = W.S;
-      MA.SG = W.SG;
-      MA.W = W.W;
-      MA.s0 = s0;
-      MA.s1 = s1;
-      const int items = (int)(m / 16) * W.SG;
-      const int grid = items < cu_count() ? items : cu_count();
-      if (codes1)
-        hipExtLaunchKernelGGL(mv_tiled_kernel<true>, dim3(grid), dim3(W.W * 64), 0, s, ev0, ev1, 0, MA);
-      else
-        hipExtLaunchKernelGGL(mv_tiled_kernel<false>, dim3(grid), dim3(W.W * 64), 0, s, ev0, ev1, 0, MA);
-      QS_LAUNCHED("mv_tiled_kernel");
-    } else {
-      MvgArgs GA{};
-      GA.codes0 = static_cast<const uint16_t*>(codes0);
-      GA.codes1 = codes1;
-      GA.kind1 = kind1;
-      GA.x2 = XA.x2;
-      GA.y1p = y1p;
-      GA.m = (int)m;
-      GA.n = (int)n;
-      GA.B = B;
-      GA.s0 = s0;
-      GA.s1 = s1;
-      hipExtLaunchKernelGGL(mv_generic_kernel, dim3((unsigned)((m + 3) / 4)), dim3(256), 0, s, ev0, ev1, 0, GA);
-      QS_LAUNCHED("mv_generic_kernel");
-    }
-
-    const float* xtot = layout == QS_LAYOUT_TILED ? XA.xtot : nullptr;
-    const float* xmul = layout == QS_LAYOUT_TILED ? XA.xmul : nullptr;
-    if (!identity && chunk_transform_fits(m, kron_pm))
-      rc = launch_yout_chunk(y1p, W.SG, B, m, kron_pm, kron_m, xtot, Gx, xmul, s0, layer_scale, su, bias, yb, y_dtype,
-                             ldy, s);
-    else
-      rc = launch_yout_rows(y1p, W.SG, B, m, kron_pm, kron_m, xtot, Gx, xmul, s0, layer_scale, su, bias, yb, y_dtype,
-                            ldy, s, identity);
+    MvgArgs GA{};
+    GA.codes0 = static_cast<const uint16_t*>(codes0);
+    GA.codes1 = codes1;
+    GA.kind1 = kind1;
+    GA.x2 = XA.x2;
+    GA.y1p = y1p;
+    GA.m = (int)m;
+    GA.n = (int)n;
+    GA.B = B;
+    GA.s0 = s0;
+    GA.s1 = s1;
+    hipExtLaunchKernelGGL(mv_generic_kernel, dim3((unsigned)((m + 3) / 4)), dim3(256), 0, s, ev0, ev1, 0, GA);
+    QS_LAUNCHED("mv_generic_kernel");
+    rc = launch_yout_rows(y1p, W.SG, B, m, kron_pm, kron_m, nullptr, 0, nullptr, s0, layer_scale, su, bias, yb,
+                          y_dtype, ldy, s, identity);
     if (rc) return rc;
   }
   return QS_OK;
