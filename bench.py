@@ -78,7 +78,7 @@ def mv_bytes(m, n, B):
     return m * n // 8 * 2 + 2 * B * n + 4 * B * m
 
 
-MV_KERNEL = {True: "linear_fused_kernel", False: "mv_tiled_kernel"}
+MV_KERNEL = "linear_fused_kernel"  # the dominant kernel of the batch-1 step
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "linear_fused_llama2_7b_b1.md")
 
 
@@ -497,7 +497,7 @@ def main():
                                    "one qs_linear_forward per linear",
                    "code_bytes": stack.code_bytes(), "parallelism": "none (1 GPU)"},
         "tok_per_s": round(1e3 / ms, 1), "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
-        "roofline": {"bound": "hbm", "kernel": MV_KERNEL[True], "achieved": round(achieved, 1),
+        "roofline": {"bound": "hbm", "kernel": MV_KERNEL, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "avg_launch_us": round(mv_ms * 1e3, 3), "bytes_per_launch": int(mv_avg_bytes),
                      "traffic": measured_traffic() if args.layers == 32 and r1.grouped else None},
