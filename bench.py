@@ -69,10 +69,10 @@ def linear_bytes(m, n, B):
 
 
 def mv_bytes(m, n, B):
-    """Algorithmic bytes of one decode-matvec launch.  At B <= 2 the launch is
-    the one-kernel forward (codes, signs, bf16 activations in and out: the
-    whole linear); at larger batches it is the tiled matvec alone (codes, fp16
-    activations in, fp32 partial outputs)."""
+    """Algorithmic bytes of the decode-matvec of one linear.  At B <= 2 that
+    is the one-kernel forward (codes, signs, bf16 activations in and out: the
+    whole linear); at larger batches the decode-matvec kernel alone (codes,
+    fp16 activations in, fp32 partial outputs)."""
     if B <= 2:
         return linear_bytes(m, n, B)
     return m * n // 8 * 2 + 2 * B * n + 4 * B * m
@@ -136,8 +136,9 @@ def launch_bytes(names, B):
 
 class Runner:
     """Issues one step through the C ABI with preallocated buffers, so it can
-    be captured in a HIP graph.  grouped=True launches the linears that share
-    an input together (qs_linear_forward_group: q/k/v, gate/up); otherwise one
+    be captured in a HIP graph.  grouped=True runs the linears that share an
+    input as one group (qs_linear_forward_group: q/k/v, gate/up; one launch at
+    batch 1-2, one launch per stage of the path beyond); otherwise one
     qs_linear_forward per linear (the reference's call pattern)."""
 
     def __init__(self, stack, B, grouped=True):
@@ -146,7 +147,7 @@ class Runner:
         from quipsharp_amd import _lib
         from quipsharp_amd.hadamard import hartley_matrix
         self.stack, self.B = stack, B
-        self.grouped = grouped and B <= 2
+        self.grouped = grouped
         dev = stack.dev
         self.lib = _lib.lib()
         self._lib = _lib
@@ -446,23 +447,34 @@ def main():
         log(f"batch 1 ({'grouped' if r_alt.grouped else 'per-linear'}): {ms_alt:.3f} ms/step")
         del r_alt
     if not args.skip_batch16:
-        r16 = Runner(stack, 16)
+        r16 = Runner(stack, 16, grouped=not args.per_linear)
         ms16 = time_graph(r16, max(args.steps // 2, 1), args.warmup)
         mv16 = time_mv_kernels(r16, passes=1)
         flops = 2 * 16 * args.layers * sum(m * n for _, m, n in LLAMA2_7B)
         extra["batch16"] = {"ms_per_step": round(ms16, 4), "GBps": round(r16.bytes_per_step() / ms16 / 1e6, 1),
                             "tok_per_s": round(16 * 1e3 / ms16, 1), "TFLOPs": round(flops / ms16 / 1e9, 2),
-                            "mv_kernel_avg_us": round(mv16 * 1e3, 3)}
-        log(f"batch 16: {ms16:.3f} ms/step")
+                            "call_pattern": "grouped" if r16.grouped else "per-linear",
+                            "mv_launches_per_step": r16.launches_per_step(),
+                            "mv_kernel_avg_us": round(mv16 * 1e3, 3),
+                            "mv_kernel_GBps": round(r16.mv_bytes_per_step() / r16.launches_per_step() /
+                                                    (mv16 * 1e-3) / 1e9, 1)}
+        log(f"batch 16 ({'grouped' if r16.grouped else 'per-linear'}): {ms16:.3f} ms/step")
         del r16
+        if not args.skip_alt:
+            r16a = Runner(stack, 16, grouped=args.per_linear)
+            ms16a = time_graph(r16a, max(args.steps // 2, 1), args.warmup)
+            extra["batch16"]["grouped_ms_per_step" if r16a.grouped else "per_linear_ms_per_step"] = round(ms16a, 4)
+            log(f"batch 16 ({'grouped' if r16a.grouped else 'per-linear'}): {ms16a:.3f} ms/step")
+            del r16a
     if args.prefill > 0:
         P = args.prefill
-        rp = Runner(stack, P)
+        rp = Runner(stack, P, grouped=not args.per_linear)
         msp = time_eager(rp, max(args.steps // 4, 2), 2)
         flops = 2 * P * args.layers * sum(m * n for _, m, n in LLAMA2_7B)
         extra["prefill"] = {"rows": P, "ms_per_step": round(msp, 3), "tok_per_s": round(P * 1e3 / msp, 1),
                             "TFLOPs": round(flops / msp / 1e9, 1),
                             "mfma_frac_fp16_dense": round(flops / msp / 1e9 / MFMA_F16_PEAK_TFLOPS, 4),
+                            "call_pattern": "grouped" if rp.grouped else "per-linear",
                             "path": "wg_kernel: E8P decode inside the GEMM loop, fp16 x fp16 -> fp32 MFMA "
                                     "(16x16x32), codes' +-1/4 shifts via group-sum MFMAs"}
         log(f"prefill {P} rows: {msp:.3f} ms/step, {flops / msp / 1e9:.1f} TFLOP/s")

@@ -200,11 +200,15 @@ size_t qs_linear_group_workspace_bytes(int64_t n, int64_t batch, int count, cons
  * gate/up of a decoder layer).  No counterpart in the reference, whose
  * QuantizedLinear.forward (quipsharp/checkpoint.py:141-146) is one linear per
  * call; callers that own several linears of one input use it.
- * Requirements: 1 <= count <= QS_MAX_GROUP, batch <= 2, tiled layout, n a
- * multiple of 256 with n <= 12288 and n / kron_pn >= 256, codes1 NULL for all
- * jobs or for none.  The workspace (zero before first use, see
- * qs_linear_forward) holds one region per job.  mv_begin / mv_end bracket the
- * single decode-matvec kernel as in qs_linear_forward. */
+ * At 1-2 rows the group is one launch; from 3 rows each stage of the path
+ * (input transforms, decode-matvecs, output transforms) is one launch for the
+ * whole group, except the wide GEMM (17 rows and more), one launch per job.
+ * Every output is bit-identical to qs_linear_forward of that job.
+ * Requirements: 1 <= count <= QS_MAX_GROUP, tiled layout, n a multiple of 256
+ * with n <= 12288 and n / kron_pn >= 256, codes1 NULL for all jobs or for
+ * none.  The workspace (zero before first use, see qs_linear_forward) holds
+ * one region per job.  mv_begin / mv_end bracket the decode-matvec launch (or
+ * the wide GEMM launches) as in qs_linear_forward. */
 int qs_linear_forward_group(const void *x, int x_dtype, int64_t ldx, int64_t batch, int64_t n, int kron_pn,
                             const float *kron_n, int count, const qs_linear_job *jobs, int y_dtype,
                             void *workspace, size_t workspace_bytes, void *mv_begin, void *mv_end,

@@ -158,19 +158,20 @@ class QuantizedLinear(nn.Module):
 
 
 def grouped_forward(x: Tensor, linears):
-    """Outputs of several QuantizedLinear modules that read the same x, in
-    one launch when the library's grouped forward covers them (1-2 rows, rht /
-    krht transforms, n a multiple of 256 up to 12288; qs_linear_forward_group)
-    and one call each otherwise.  Each output equals ``lin(x)``.  No
-    counterpart in the reference, which calls the linears one by one; meant
-    for callers that own several linears of one input (q/k/v, gate/up)."""
+    """Outputs of several QuantizedLinear modules that read the same x, as one
+    grouped call when the library's grouped forward covers them (rht / krht
+    transforms, n a multiple of 256 up to 12288; qs_linear_forward_group: one
+    launch at 1-2 rows, one launch per stage for the group beyond) and one call
+    each otherwise.  Each output equals ``lin(x)``.  No counterpart in the
+    reference, which calls the linears one by one; meant for callers that own
+    several linears of one input (q/k/v, gate/up)."""
     from . import _lib
     from .hadamard import kron_factor
     from .quantize import forward_packed_group
     n = x.shape[-1]
     rows = x.numel() // n if n else 0
     fn = kron_factor(n) if n else None
-    ok = (1 <= len(linears) <= _lib.QS_MAX_GROUP and 1 <= rows <= 2 and n % 256 == 0 and n <= 12288
+    ok = (1 <= len(linears) <= _lib.QS_MAX_GROUP and rows >= 1 and n % 256 == 0 and n <= 12288
           and fn is not None and n // fn[0] >= 256
           and all(isinstance(l, QuantizedLinear) and l.transform_kind in ("rht", "krht") and l.in_features == n
                   for l in linears))

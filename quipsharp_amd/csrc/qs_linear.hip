@@ -910,9 +910,107 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
                          false);
 }
 
+// Grouped workspace: the completion counters of the one-launch kernel, one
+// per job at a fixed place (a region's offset depends on the row count, and a
+// counter must be zero whatever rows the previous call had), then one
+// ws_layout region per job; the counter slot at the start of each region is
+// unused.
+constexpr size_t kGroupCounterStride = 64;
+constexpr size_t kGroupCounterBytes = 256;
+static_assert(kGroupCounterStride * QS_MAX_GROUP <= kGroupCounterBytes, "group counters fit");
+
+// Grouped forward for three or more rows: the input transforms of all the
+// linears in one launch, their decode-matvecs in one launch (16-row pass) or
+// one wide GEMM each (kWideMinBatch rows and more), and their output
+// transforms in one launch (a linear whose m is outside the chunk scheme: the
+// whole-row output kernel).  Bit-identical to one qs_linear_forward per linear.
+static int forward_group_rows(const void* x, int x_dtype, int64_t ldx, int64_t batch, int64_t n, int kron_pn,
+                              const float* kron_n, int count, const qs_linear_job* jobs, int y_dtype, char* ws,
+                              void* mv_begin, void* mv_end, hipStream_t s) {
+  const bool wide = batch >= kWideMinBatch;
+  BatchedPass P[QS_MAX_GROUP];
+  size_t off = kGroupCounterBytes;
+  for (int g = 0; g < count; ++g) {
+    const qs_linear_job& j = jobs[g];
+    const WsLayout W = ws_layout(j.m, n, batch, QS_LAYOUT_TILED);
+    BatchedPass& Q = P[g];
+    Q = BatchedPass{};
+    Q.x = x;
+    Q.x_dtype = x_dtype;
+    Q.ldx = ldx;
+    Q.B = (int)batch;
+    Q.n = n;
+    Q.m = j.m;
+    Q.pn = kron_pn;
+    Q.pm = j.kron_pm;
+    Q.Kn = kron_n;
+    Q.Km = j.kron_m;
+    Q.sv = j.sv;
+    Q.su = j.su;
+    Q.codes0 = j.codes0;
+    Q.codes1 = j.codes1;
+    Q.s0 = j.s0;
+    Q.s1 = j.s1;
+    Q.layer_scale = j.layer_scale;
+    Q.bias = j.bias;
+    Q.y = j.y;
+    Q.y_dtype = y_dtype;
+    Q.ldy = j.ldy;
+    Q.S = W.S;
+    Q.SG = W.SG;
+    Q.W = W.W;
+    Q.ncu = cu_count();
+    Q.x2h = reinterpret_cast<_Float16*>(ws + off + W.x2h);
+    Q.sg = reinterpret_cast<_Float16*>(ws + off + W.sg);
+    Q.xmul = reinterpret_cast<float*>(ws + off + W.xmul);
+    Q.y1p = reinterpret_cast<float*>(ws + off + W.y1p);
+    Q.frag = wide ? 1 : 0;
+    off += W.total;
+  }
+  int rc = launch_bx_group(P, count, s);
+  if (rc) return rc;
+  if (wide) {
+    for (int g = 0; g < count; ++g) {
+      if (g == 0 && mv_begin) QS_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(mv_begin), s));
+      WideMfma F{};
+      F.codes0 = P[g].codes0;
+      F.codes1 = P[g].codes1;
+      F.m = P[g].m;
+      F.n = n;
+      F.B = (int)batch;
+      F.s0 = P[g].s0;
+      F.s1 = P[g].s1;
+      F.x2f = P[g].x2h;
+      F.sgf = P[g].sg;
+      F.y1p = P[g].y1p;
+      F.SGk = wide_splits(P[g].m, n, batch, cu_count(), P[g].codes1 != nullptr);
+      rc = launch_linear_wide_mfma(F, s);
+      if (rc) return rc;
+      P[g].SG = F.SGk;  // partial groups summed by the output kernels
+    }
+    if (mv_end) QS_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(mv_end), s));
+  } else {
+    rc = launch_bm_group(P, count, s, reinterpret_cast<hipEvent_t>(mv_begin), reinterpret_cast<hipEvent_t>(mv_end));
+    if (rc) return rc;
+  }
+  // output transforms: the chunk-scheme ones in one launch, the others one by one
+  BatchedPass Pc[QS_MAX_GROUP];
+  int nc = 0;
+  for (int g = 0; g < count; ++g) {
+    if (chunk_transform_fits(P[g].m, P[g].pm)) {
+      Pc[nc++] = P[g];
+      continue;
+    }
+    rc = launch_yout_rows(P[g].y1p, P[g].SG, (int)batch, P[g].m, P[g].pm, P[g].Km, nullptr, 0, P[g].xmul, P[g].s0,
+                          P[g].layer_scale, P[g].su, P[g].bias, P[g].y, y_dtype, P[g].ldy, s);
+    if (rc) return rc;
+  }
+  return nc ? launch_by_group(Pc, nc, s) : QS_OK;
+}
+
 extern "C" size_t qs_linear_group_workspace_bytes(int64_t n, int64_t batch, int count, const int64_t* ms) {
   if (n <= 0 || batch <= 0 || count < 1 || count > QS_MAX_GROUP || !ms) return 0;
-  size_t total = 0;
+  size_t total = kGroupCounterBytes;
   for (int g = 0; g < count; ++g) {
     if (ms[g] <= 0) return 0;
     total += ws_layout(ms[g], n, batch, QS_LAYOUT_TILED).total;
@@ -933,11 +1031,11 @@ extern "C" int qs_linear_forward_group(const void* x, int x_dtype, int64_t ldx, 
   if (batch == 0) return QS_OK;
   int rc = check_transform(n, kron_pn, kron_n, "input");
   if (rc) return rc;
-  QS_REQUIRE(batch <= 2 && chunk_transform_fits(n, kron_pn),
-             "grouped forward needs batch <= 2 and n a multiple of 256 with n <= %d (got batch %lld, n %lld)", kMaxN,
-             (long long)batch, (long long)n);
+  QS_REQUIRE(chunk_transform_fits(n, kron_pn),
+             "grouped forward needs n a multiple of 256 with n <= %d and n / kron_pn >= 256 (got n %lld)", kMaxN,
+             (long long)n);
   QS_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255) == 0, "workspace must be 256-byte aligned");
-  size_t need = 0;
+  size_t need = kGroupCounterBytes;
   for (int g = 0; g < count; ++g) {
     const qs_linear_job& j = jobs[g];
     QS_REQUIRE(j.codes0 && j.su && j.sv && j.y, "job %d: null pointer", g);
@@ -954,9 +1052,12 @@ extern "C" int qs_linear_forward_group(const void* x, int x_dtype, int64_t ldx, 
   QS_REQUIRE(workspace_bytes >= need, "workspace too small: %zu < %zu", workspace_bytes, need);
   hipStream_t s = as_stream(stream);
   char* ws = static_cast<char*>(workspace);
+  if (!fused_eligible(batch, n, jobs[0].m, kron_pn))
+    return forward_group_rows(x, x_dtype, ldx, batch, n, kron_pn, kron_n, count, jobs, y_dtype, ws, mv_begin, mv_end,
+                              s);
   FusedJobDesc d[QS_MAX_GROUP];
   WsLayout W0{};
-  size_t off = 0;
+  size_t off = kGroupCounterBytes;
   for (int g = 0; g < count; ++g) {
     const qs_linear_job& j = jobs[g];
     const WsLayout W = ws_layout(j.m, n, batch, QS_LAYOUT_TILED);
@@ -975,7 +1076,7 @@ extern "C" int qs_linear_forward_group(const void* x, int x_dtype, int64_t ldx, 
     d[g].bias = j.bias;
     d[g].y = j.y;
     d[g].ldy = j.ldy;
-    d[g].counter = reinterpret_cast<unsigned*>(ws + off);
+    d[g].counter = reinterpret_cast<unsigned*>(ws + kGroupCounterStride * g);
     d[g].xmul = reinterpret_cast<float*>(ws + off + W.xmul);
     d[g].y1p = reinterpret_cast<float*>(ws + off + W.y1p);
     off += W.total;

@@ -32,6 +32,15 @@ constexpr int kPrefetch = 4;
 // ---------------------------------------------------------------------------
 // input transform
 // ---------------------------------------------------------------------------
+// One linear of an input-transform launch (its own signs and operand); the
+// linears of a launch share x, n and the transform.
+struct BxJob {
+  const float* sv;
+  _Float16* x2h;  // [B][n] fp16 operand, index 256 slice + t
+  _Float16* sg;   // [B][n / 8] sums of 8 consecutive operand values
+  float* xmul;    // [B] 2^e
+};
+
 struct BxArgs {
   const void* x;
   int x_dtype, x_vec;
@@ -40,11 +49,9 @@ struct BxArgs {
   int n, Sn, lsh_n, pn;
   const float* Kn;
   float scale_n;
-  const float* sv;
-  _Float16* x2h;  // [B][n] fp16 operand, index 256 slice + t
-  _Float16* sg;   // [B][n / 8] sums of 8 consecutive operand values
-  float* xmul;    // [B] 2^e
   int frag;       // x2h and sg fragment-major (wide GEMM operands; sg / 4)
+  int per;        // work-groups per linear: linear blockIdx / per
+  BxJob job[QS_MAX_GROUP];
 };
 
 constexpr int kBxOffY = 0;                                  // kMaxS x kYStride floats
@@ -53,8 +60,8 @@ constexpr int kBxOffMl = kBxOffMh + kMBytes;
 constexpr int kBxOffMisc = kBxOffMl + kMBytes;              // row norm parts
 constexpr int kBxLds = kBxOffMisc + 4 * kWaves;
 
-// Rows b = blockIdx.x, + gridDim.x, ...: the next row's activations are
-// loaded while this row is transformed.
+// Rows b = lb, lb + per, ... of linear blockIdx / per (lb = blockIdx % per):
+// the next row's activations are loaded while this row is transformed.
 __global__ __launch_bounds__(kThreads) void bx_kernel(BxArgs A) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
   float* Y = reinterpret_cast<float*>(lds + kBxOffY);
@@ -66,19 +73,21 @@ __global__ __launch_bounds__(kThreads) void bx_kernel(BxArgs A) {
   const int q = lane >> 4, r16 = lane & 15;
   const LaneX lx = lane_x_init();
   const XSource X{A.x, A.x_dtype, A.x_vec, A.ldx, A.Sn};
-  const int stride = (int)gridDim.x;
+  const int stride = A.per;
+  const int g = (int)blockIdx.x / A.per, lb = (int)blockIdx.x - g * A.per;
+  const BxJob& J = A.job[g];
 
   XRaw xr;
-  load_x_raw(X, A.sv, (int)blockIdx.x, w, lane, xr);
+  load_x_raw(X, J.sv, lb, w, lane, xr);
   {
     float kmv[3];
     mmat_load(kmv, A.Sn, A.lsh_n, A.pn, A.Kn, tid);
     mmat_store(kmv, A.Sn, A.lsh_n, Mh, Ml, tid);
   }
-  for (int b = (int)blockIdx.x; b < A.B; b += stride) {
+  for (int b = lb; b < A.B; b += stride) {
     float xv[kCPW][4];
     finish_x(X, xr, w, xv);
-    if (b + stride < A.B) load_x_raw(X, A.sv, b + stride, w, lane, xr);  // the next row
+    if (b + stride < A.B) load_x_raw(X, J.sv, b + stride, w, lane, xr);  // the next row
     float ss = 0.0f;
 #pragma unroll
     for (int u = 0; u < kCPW; ++u)
@@ -94,7 +103,7 @@ __global__ __launch_bounds__(kThreads) void bx_kernel(BxArgs A) {
     for (int i = 0; i < kWaves; ++i) norm2 += wsum[i];
     const int e = operand_exponent(norm2);
     const float mul = ldexpf(A.scale_n, -e);
-    if (tid == 0) A.xmul[b] = ldexpf(1.0f, e);
+    if (tid == 0) J.xmul[b] = ldexpf(1.0f, e);
 
     // chunk stage: operand row (slice) s = 16 a + 4 q + j, column t = 16 w + r16
     const int t = 16 * w + r16;
@@ -110,8 +119,8 @@ __global__ __launch_bounds__(kThreads) void bx_kernel(BxArgs A) {
     }
     // destinations: natural rows, or the fragment-major operand whose index
     // is a row part plus a column part (frag_index, sg_frag_index)
-    _Float16* xrow = A.x2h + (A.frag ? frag_index(b, 0, A.Sn) : (size_t)b * A.n);
-    _Float16* srow = A.sg + (A.frag ? sg_frag_index(b, 0, A.Sn) : (size_t)b * (A.n / 8));
+    _Float16* xrow = J.x2h + (A.frag ? frag_index(b, 0, A.Sn) : (size_t)b * A.n);
+    _Float16* srow = J.sg + (A.frag ? sg_frag_index(b, 0, A.Sn) : (size_t)b * (A.n / 8));
     const int xcol = A.frag ? ((t >> 3) & 7) * 512 + (t >> 6) * 128 + (t & 7) : t;     // + 4096 s (frag) / 256 s
     const int scol = A.frag ? ((t >> 6) & 3) * 128 + ((t >> 3) & 7) : (t >> 3);        // + 512 s (frag) / 32 s
     const int xs = A.frag ? 4096 : 256, ss_ = A.frag ? 512 : 32;
@@ -142,15 +151,24 @@ __global__ __launch_bounds__(kThreads) void bx_kernel(BxArgs A) {
 // ---------------------------------------------------------------------------
 // decode-matvec
 // ---------------------------------------------------------------------------
-struct BmArgs {
+// One linear of a decode-matvec launch; the linears of a launch share n and
+// the batch rows, and split the grid: work-groups wg0 .. wg0 + Gr SG - 1 are
+// this linear's.
+struct BmJob {
   const uint16_t* codes0;
   const uint8_t* codes1;
-  const _Float16* x2h;
+  const _Float16* x2h;  // [B][n] operand of this linear
   const _Float16* sg;
   float* y1p;  // [SG][B][m]
-  int m, n, B, S, SG, W, Gr;
-  int tpo;  // threads per output of the reduction: a power of two, tpo * kBmSlots * 16 * B <= 1024
+  int m, Gr, wg0;
   float s0, s1;
+};
+
+struct BmArgs {
+  int n, B, S, SG, W;
+  int tpo;  // threads per output of the reduction: a power of two, tpo * kBmSlots * 16 * B <= 1024
+  int njobs;
+  BmJob job[QS_MAX_GROUP];
 };
 
 constexpr int kBmSlots = 2;                  // row blocks reduced together
@@ -175,8 +193,14 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
   const int q = lane >> 4, r16 = lane & 15;
-  const int RB = A.m >> 4;
-  const int sg = (int)blockIdx.x / A.Gr, jr = (int)blockIdx.x - sg * A.Gr;
+  int g = 0;
+#pragma unroll
+  for (int k = 1; k < QS_MAX_GROUP; ++k)
+    if (k < A.njobs && (int)blockIdx.x >= A.job[k].wg0) g = k;
+  const BmJob& J = A.job[g];
+  const int RB = J.m >> 4;
+  const int lb = (int)blockIdx.x - J.wg0;  // work-group index within this linear
+  const int sg = lb / J.Gr, jr = lb - sg * J.Gr;
   const int sl = sg * A.W + w;
   const bool active = w < A.W && sl < A.S;
   const LaneX lx = lane_x_init();
@@ -191,12 +215,12 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
   // slice, and the sums of its eight groups of 8 (columns b >= B and idle
   // waves compute values that are never stored)
   const bool have = active && r16 < A.B;
-  const _Float16* xrow = A.x2h + (have ? (size_t)r16 * A.n + 256 * sl + 64 * q : 0);
+  const _Float16* xrow = J.x2h + (have ? (size_t)r16 * A.n + 256 * sl + 64 * q : 0);
   half8 xb[8];
 #pragma unroll
   for (int c = 0; c < 8; ++c) xb[c] = *reinterpret_cast<const half8*>(xrow + 8 * c);
   const half8 xs =
-      *reinterpret_cast<const half8*>(A.sg + (have ? (size_t)r16 * (A.n / 8) + 32 * sl + 8 * q : 0));
+      *reinterpret_cast<const half8*>(J.sg + (have ? (size_t)r16 * (A.n / 8) + 32 * sl + 8 * q : 0));
   // code tiles stream through a ring of kPrefetch registers (see the row
   // loop); a tile past the end or of an idle wave reads tile 0 instead
   // byte offset of this lane's 16 code bytes of row block rb (tile 0 past
@@ -208,9 +232,9 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
   uint2 pre1[kPrefetch] = {};
 #pragma unroll
   for (int k = 0; k < kPrefetch; ++k) {
-    const uint32_t off = code_off(jr + k * A.Gr);
-    pre[k] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(A.codes0) + off);
-    if (HAS2) pre1[k] = *reinterpret_cast<const uint2*>(A.codes1 + off / 2);
+    const uint32_t off = code_off(jr + k * J.Gr);
+    pre[k] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(J.codes0) + off);
+    if (HAS2) pre1[k] = *reinterpret_cast<const uint2*>(J.codes1 + off / 2);
   }
   if (tid < 256) {
     tab16[tid] = trow;
@@ -232,10 +256,10 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
   // each step waits for its own tile only; an entry is refilled once its
   // tile is decoded.
   int k = 0;  // row blocks done: selects the reduction slot
-  for (int rb0 = jr; rb0 < RB; rb0 += kPrefetch * A.Gr) {
+  for (int rb0 = jr; rb0 < RB; rb0 += kPrefetch * J.Gr) {
 #pragma unroll
   for (int u = 0; u < kPrefetch; ++u) {
-    const int rb = rb0 + u * A.Gr;
+    const int rb = rb0 + u * J.Gr;
     const bool valid = rb < RB;
     floatx4 acc = {0.f, 0.f, 0.f, 0.f};
     floatx4 accs = {0.f, 0.f, 0.f, 0.f};
@@ -258,9 +282,9 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
       accs = __builtin_amdgcn_mfma_f32_16x16x32_f16(shift_operand(wd), xs, accs, 0, 0, 0);
     }
     {
-      const uint32_t off = code_off(rb + kPrefetch * A.Gr);
-      pre[u] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(A.codes0) + off);
-      if (HAS2) pre1[u] = *reinterpret_cast<const uint2*>(A.codes1 + off / 2);
+      const uint32_t off = code_off(rb + kPrefetch * J.Gr);
+      pre[u] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(J.codes0) + off);
+      if (HAS2) pre1[u] = *reinterpret_cast<const uint2*>(J.codes1 + off / 2);
     }
     // lane holds rows 4q..4q+3 of the tile for batch column r16
     const int slot = k % kBmSlots;
@@ -268,12 +292,12 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
     if (valid) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        float v = A.s0 * (acc[j] + 0.5f * accs[j] - 0.25f * slice_shift);
-        if (HAS2) v = v + A.s1 * acc2[j];
+        float v = J.s0 * (acc[j] + 0.5f * accs[j] - 0.25f * slice_shift);
+        if (HAS2) v = v + J.s1 * acc2[j];
         rbuf[(w * 16 + 4 * q + j) * kTB + r16] = active ? v : 0.0f;
       }
     }
-    if (valid && (slot == kBmSlots - 1 || rb + A.Gr >= RB)) {
+    if (valid && (slot == kBmSlots - 1 || rb + J.Gr >= RB)) {
       __syncthreads();
       // output o = (s * 16 + row) * B + b of slot s <= slot, summed over the
       // waves by tpo threads (waves part, part + tpo, ...), then across them;
@@ -295,8 +319,8 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
       if (tpo >= 8) v += lane_xor<4>(v, lx);
       if (tpo >= 16) v += lane_xor<8>(v, lx);
       if (o < nout && part == 0) {
-        const int rbs = rb - (slot - s) * A.Gr;  // row block of slot s
-        A.y1p[((size_t)sg * A.B + bc) * A.m + rbs * 16 + row] = v;
+        const int rbs = rb - (slot - s) * J.Gr;  // row block of slot s
+        J.y1p[((size_t)sg * A.B + bc) * J.m + rbs * 16 + row] = v;
       }
       __syncthreads();  // the slots are free again
     }
@@ -308,17 +332,25 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
 // ---------------------------------------------------------------------------
 // output transform
 // ---------------------------------------------------------------------------
-struct ByArgs {
+// One linear of an output-transform launch: work-groups wg0 .. wg0 + grid - 1
+// walk its rows.  The linears of a launch share B and the output dtype.
+struct ByJob {
   const float* y1p;  // [SG][B][m]
-  int SG, B, m, Sm, lsh_m, pm;
+  const float* xmul; // [B]
+  int SG, m, Sm, lsh_m, pm, wg0, grid;
   const float* Km;
-  const float* xmul;
   float scale_m, layer_scale;
   const float* su;
   const float* bias;
   void* y;
-  int y_dtype;
   int64_t ldy;
+};
+
+struct ByArgs {
+  int B;
+  int y_dtype;
+  int njobs;
+  ByJob job[QS_MAX_GROUP];
 };
 
 constexpr int kByOffY = 0;
@@ -326,11 +358,12 @@ constexpr int kByOffMh = kByOffY + kMaxS * kYStride * 4;
 constexpr int kByOffMl = kByOffMh + kMBytes;
 constexpr int kByLds = kByOffMl + kMBytes;
 
-// Rows b = blockIdx.x, + gridDim.x, ...; su, bias and M are loaded once.
-// With one partial group (G == 1) the next row's partial sums are loaded
-// while this row is transformed (with up to kMaxSG they would not fit the
-// registers alongside su and bias, and are loaded per row); G == 0 sums any
-// number of groups one at a time.
+// Rows b = lb, lb + grid, ... of the linear whose work-groups include this
+// one (lb its index among them); su, bias and M are loaded once.  With one
+// partial group (G == 1) the next row's partial sums are loaded while this
+// row is transformed (with up to kMaxSG they would not fit the registers
+// alongside su and bias, and are loaded per row); G == 0 sums any number of
+// groups one at a time.  A linear with fewer groups than G adds zeros.
 template <int G>
 __global__ __launch_bounds__(kThreads) void by_kernel(ByArgs A) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
@@ -340,21 +373,27 @@ __global__ __launch_bounds__(kThreads) void by_kernel(ByArgs A) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
   const int q = lane >> 4, r16 = lane & 15;
-  const int Sm = A.Sm;
+  int g = 0;
+#pragma unroll
+  for (int k = 1; k < QS_MAX_GROUP; ++k)
+    if (k < A.njobs && (int)blockIdx.x >= A.job[k].wg0) g = k;
+  const ByJob& J = A.job[g];
+  const int lb = (int)blockIdx.x - J.wg0;
+  const int Sm = J.Sm;
   const int t = 16 * w + r16;
   const LaneX lx = lane_x_init();
-  const int stride = (int)gridDim.x;
+  const int stride = J.grid;
 
   // loads in the order they are waited for: K entries of M, partial sums,
   // su and bias (unconditional loads from valid addresses)
   float kmv[3];
-  mmat_load(kmv, Sm, A.lsh_m, A.pm, A.Km, tid);
+  mmat_load(kmv, Sm, J.lsh_m, J.pm, J.Km, tid);
   PRaw<1> pr;
-  if constexpr (G == 1) load_partials_raw<false, 1>(A.y1p, A.m, Sm, A.SG, A.B, (int)blockIdx.x, w, lane, pr);
+  if constexpr (G == 1) load_partials_raw<false, 1>(J.y1p, J.m, Sm, J.SG, A.B, lb, w, lane, pr);
   int oidx[3][4];
   float suo[3][4], bio[3][4];
-  const float* const bsrc = A.bias ? A.bias : A.su;
-  const float bsel = A.bias ? 1.0f : 0.0f;
+  const float* const bsrc = J.bias ? J.bias : J.su;
+  const float bsel = J.bias ? 1.0f : 0.0f;
 #pragma unroll
   for (int a = 0; a < 3; ++a)
 #pragma unroll
@@ -362,23 +401,23 @@ __global__ __launch_bounds__(kThreads) void by_kernel(ByArgs A) {
       const int r = 16 * a + 4 * q + j;
       oidx[a][j] = r < Sm ? 256 * r + t : -1;
       const int ii = oidx[a][j] >= 0 ? oidx[a][j] : 0;
-      suo[a][j] = A.su[ii];
+      suo[a][j] = J.su[ii];
       bio[a][j] = bsrc[ii];
     }
-  mmat_store(kmv, Sm, A.lsh_m, Mh, Ml, tid);
-  for (int b = (int)blockIdx.x; b < A.B; b += stride) {
+  mmat_store(kmv, Sm, J.lsh_m, Mh, Ml, tid);
+  for (int b = lb; b < A.B; b += stride) {
     float zv[kCPW][4];
     if constexpr (G == 1) {
       sum_partials(pr, zv);
-      if (b + stride < A.B) load_partials_raw<false, 1>(A.y1p, A.m, Sm, A.SG, A.B, b + stride, w, lane, pr);
+      if (b + stride < A.B) load_partials_raw<false, 1>(J.y1p, J.m, Sm, J.SG, A.B, b + stride, w, lane, pr);
     } else if constexpr (G == 0) {
-      sum_partials_loop(A.y1p, A.m, Sm, A.SG, A.B, b, w, lane, zv);
+      sum_partials_loop(J.y1p, J.m, Sm, J.SG, A.B, b, w, lane, zv);
     } else {
       PRaw<G> pg;
-      load_partials_raw<false, G>(A.y1p, A.m, Sm, A.SG, A.B, b, w, lane, pg);
+      load_partials_raw<false, G>(J.y1p, J.m, Sm, J.SG, A.B, b, w, lane, pg);
       sum_partials(pg, zv);
     }
-    const float mul = A.scale_m * A.layer_scale * A.xmul[b];
+    const float mul = J.scale_m * J.layer_scale * J.xmul[b];
     h256_chunks(zv, Sm, lane, lx);
     store_chunks_lanes(Y, Sm, w, lane, zv);
     __syncthreads();
@@ -390,14 +429,14 @@ __global__ __launch_bounds__(kThreads) void by_kernel(ByArgs A) {
       const ZOperand z = z_operand(Y, Sm, t, q, kb);
 #pragma unroll
       for (int a = 0; a < 3; ++a)
-        if (a < nrt) acc[a] = mstage_step(acc[a], Mh, Ml, 16 * a, z, kb, A.pm > 1, q, r16);
+        if (a < nrt) acc[a] = mstage_step(acc[a], Mh, Ml, 16 * a, z, kb, J.pm > 1, q, r16);
     }
     float out[3][4];
 #pragma unroll
     for (int a = 0; a < 3; ++a)
 #pragma unroll
       for (int j = 0; j < 4; ++j) out[a][j] = acc[a][j] * mul * suo[a][j] + bsel * bio[a][j];
-    store_outputs(A.y, A.y_dtype, (int64_t)b * A.ldy, oidx, out);
+    store_outputs(J.y, A.y_dtype, (int64_t)b * J.ldy, oidx, out);
     __syncthreads();  // Y is rewritten for the next row
   }
 }
@@ -441,104 +480,147 @@ int check_lds() {
 
 }  // namespace
 
-int launch_bx_rows(const BatchedPass& P, hipStream_t stream) {
-  QS_REQUIRE(chunk_transform_fits(P.n, P.pn), "input transform: n outside the chunk scheme");
+int launch_bx_group(const BatchedPass* P, int count, hipStream_t stream) {
+  QS_REQUIRE(count >= 1 && count <= QS_MAX_GROUP, "input transform: 1..%d linears", QS_MAX_GROUP);
+  const BatchedPass& P0 = P[0];
+  QS_REQUIRE(chunk_transform_fits(P0.n, P0.pn), "input transform: n outside the chunk scheme");
   int rc = check_lds();
   if (rc) return rc;
   BxArgs X{};
-  X.x = P.x;
-  X.x_dtype = P.x_dtype;
+  X.x = P0.x;
+  X.x_dtype = P0.x_dtype;
   {
-    const uintptr_t align = P.x_dtype == QS_DTYPE_F32 ? 16 : 8;
-    X.x_vec = (reinterpret_cast<uintptr_t>(P.x) % align) == 0 && P.ldx % 4 == 0;
+    const uintptr_t align = P0.x_dtype == QS_DTYPE_F32 ? 16 : 8;
+    X.x_vec = (reinterpret_cast<uintptr_t>(P0.x) % align) == 0 && P0.ldx % 4 == 0;
   }
-  X.ldx = P.ldx;
-  X.B = P.B;
-  X.n = (int)P.n;
-  X.Sn = (int)(P.n / 256);
-  X.lsh_n = log2_exact((int)(P.n / P.pn / 256));
-  X.pn = P.pn;
-  X.Kn = P.Kn;
-  X.scale_n = inv_sqrt_len((int)(P.n / P.pn));
-  X.sv = P.sv;
-  X.x2h = P.x2h;
-  X.sg = P.sg;
-  X.xmul = P.xmul;
-  X.frag = P.frag;
-  hipLaunchKernelGGL(bx_kernel, dim3(row_grid(P.B, P.ncu)), dim3(kThreads), kBxLds, stream, X);
+  X.ldx = P0.ldx;
+  X.B = P0.B;
+  X.n = (int)P0.n;
+  X.Sn = (int)(P0.n / 256);
+  X.lsh_n = log2_exact((int)(P0.n / P0.pn / 256));
+  X.pn = P0.pn;
+  X.Kn = P0.Kn;
+  X.scale_n = inv_sqrt_len((int)(P0.n / P0.pn));
+  X.frag = P0.frag;
+  X.per = (int)row_grid(P0.B, P0.ncu);
+  for (int j = 0; j < count; ++j) {
+    const BatchedPass& Q = P[j];
+    QS_REQUIRE(Q.x == P0.x && Q.x_dtype == P0.x_dtype && Q.ldx == P0.ldx && Q.B == P0.B && Q.n == P0.n &&
+                   Q.pn == P0.pn && Q.Kn == P0.Kn && Q.frag == P0.frag,
+               "input transform: linears of one launch share x and its transform");
+    X.job[j] = BxJob{Q.sv, Q.x2h, Q.sg, Q.xmul};
+  }
+  hipLaunchKernelGGL(bx_kernel, dim3((unsigned)(X.per * count)), dim3(kThreads), kBxLds, stream, X);
   QS_LAUNCHED("bx_kernel");
   return QS_OK;
 }
 
-int launch_by_rows(const BatchedPass& P, hipStream_t stream) {
-  QS_REQUIRE(chunk_transform_fits(P.m, P.pm), "output transform: m outside the chunk scheme");
-  QS_REQUIRE(P.SG >= 1 && P.SG <= kWideMaxGroups, "output transform: 1..%d partial groups", kWideMaxGroups);
+int launch_bx_rows(const BatchedPass& P, hipStream_t stream) { return launch_bx_group(&P, 1, stream); }
+
+int launch_by_group(const BatchedPass* P, int count, hipStream_t stream) {
+  QS_REQUIRE(count >= 1 && count <= QS_MAX_GROUP, "output transform: 1..%d linears", QS_MAX_GROUP);
   int rc = check_lds();
   if (rc) return rc;
   ByArgs Y{};
-  Y.y1p = P.y1p;
-  Y.SG = P.SG;
-  Y.B = P.B;
-  Y.m = (int)P.m;
-  Y.Sm = (int)(P.m / 256);
-  Y.lsh_m = log2_exact((int)(P.m / P.pm / 256));
-  Y.pm = P.pm;
-  Y.Km = P.Km;
-  Y.xmul = P.xmul;
-  Y.scale_m = inv_sqrt_len((int)(P.m / P.pm));
-  Y.layer_scale = P.layer_scale;
-  Y.su = P.su;
-  Y.bias = P.bias;
-  Y.y = P.y;
-  Y.y_dtype = P.y_dtype;
-  Y.ldy = P.ldy;
-  if (P.SG == 1)
-    hipLaunchKernelGGL(by_kernel<1>, dim3(row_grid(P.B, P.ncu)), dim3(kThreads), kByLds, stream, Y);
-  else if (P.SG <= kMaxSG)
-    hipLaunchKernelGGL(by_kernel<kMaxSG>, dim3(row_grid(P.B, P.ncu)), dim3(kThreads), kByLds, stream, Y);
+  Y.B = P[0].B;
+  Y.y_dtype = P[0].y_dtype;
+  Y.njobs = count;
+  const unsigned per = row_grid(P[0].B, P[0].ncu);
+  int maxsg = 1;
+  for (int j = 0; j < count; ++j) {
+    const BatchedPass& Q = P[j];
+    QS_REQUIRE(chunk_transform_fits(Q.m, Q.pm), "output transform: m outside the chunk scheme");
+    QS_REQUIRE(Q.SG >= 1 && Q.SG <= kWideMaxGroups, "output transform: 1..%d partial groups", kWideMaxGroups);
+    QS_REQUIRE(Q.B == Y.B && Q.y_dtype == Y.y_dtype, "output transform: linears of one launch share rows and dtype");
+    ByJob& J = Y.job[j];
+    J.y1p = Q.y1p;
+    J.xmul = Q.xmul;
+    J.SG = Q.SG;
+    J.m = (int)Q.m;
+    J.Sm = (int)(Q.m / 256);
+    J.lsh_m = log2_exact((int)(Q.m / Q.pm / 256));
+    J.pm = Q.pm;
+    J.wg0 = (int)per * j;
+    J.grid = (int)per;
+    J.Km = Q.Km;
+    J.scale_m = inv_sqrt_len((int)(Q.m / Q.pm));
+    J.layer_scale = Q.layer_scale;
+    J.su = Q.su;
+    J.bias = Q.bias;
+    J.y = Q.y;
+    J.ldy = Q.ldy;
+    if (Q.SG > maxsg) maxsg = Q.SG;
+  }
+  const dim3 grid(per * (unsigned)count);
+  if (maxsg == 1)
+    hipLaunchKernelGGL(by_kernel<1>, grid, dim3(kThreads), kByLds, stream, Y);
+  else if (maxsg <= kMaxSG)
+    hipLaunchKernelGGL(by_kernel<kMaxSG>, grid, dim3(kThreads), kByLds, stream, Y);
   else
-    hipLaunchKernelGGL(by_kernel<0>, dim3(row_grid(P.B, P.ncu)), dim3(kThreads), kByLds, stream, Y);
+    hipLaunchKernelGGL(by_kernel<0>, grid, dim3(kThreads), kByLds, stream, Y);
   QS_LAUNCHED("by_kernel");
   return QS_OK;
 }
 
-int launch_bm(const BatchedPass& P, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop) {
-  QS_REQUIRE(P.B >= 1 && P.B <= kTB, "batched pass: 1..%d rows", kTB);
-  QS_REQUIRE(P.m % 16 == 0 && P.n % 256 == 0 && P.S == (int)(P.n / 256) && P.SG >= 1 && P.W >= 1 &&
-                 P.W <= kWaves && P.SG * P.W >= P.S,
+int launch_by_rows(const BatchedPass& P, hipStream_t stream) { return launch_by_group(&P, 1, stream); }
+
+int launch_bm_group(const BatchedPass* P, int count, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop) {
+  QS_REQUIRE(count >= 1 && count <= QS_MAX_GROUP, "decode-matvec: 1..%d linears", QS_MAX_GROUP);
+  const BatchedPass& P0 = P[0];
+  QS_REQUIRE(P0.B >= 1 && P0.B <= kTB, "batched pass: 1..%d rows", kTB);
+  QS_REQUIRE(P0.n % 256 == 0 && P0.S == (int)(P0.n / 256) && P0.SG >= 1 && P0.W >= 1 && P0.W <= kWaves &&
+                 P0.SG * P0.W >= P0.S,
              "decode-matvec: bad slice grouping");
   int rc = check_lds();
   if (rc) return rc;
   BmArgs M{};
-  M.codes0 = static_cast<const uint16_t*>(P.codes0);
-  M.codes1 = static_cast<const uint8_t*>(P.codes1);
-  M.x2h = P.x2h;
-  M.sg = P.sg;
-  M.y1p = P.y1p;
-  M.m = (int)P.m;
-  M.n = (int)P.n;
-  M.B = P.B;
-  M.S = P.S;
-  M.SG = P.SG;
-  M.W = P.W;
-  {
-    const int RB = (int)(P.m / 16);
-    int Gr = P.ncu / P.SG;
-    if (Gr < 1) Gr = 1;
-    if (Gr > RB) Gr = RB;
-    M.Gr = Gr;
-  }
+  M.n = (int)P0.n;
+  M.B = P0.B;
+  M.S = P0.S;
+  M.SG = P0.SG;
+  M.W = P0.W;
+  M.njobs = count;
   M.tpo = 16;
-  while (M.tpo > 1 && M.tpo * kBmSlots * 16 * P.B > kThreads) M.tpo >>= 1;
-  M.s0 = P.s0;
-  M.s1 = P.s1;
-  const unsigned grid = (unsigned)(M.Gr * P.SG);
-  if (P.codes1)
+  while (M.tpo > 1 && M.tpo * kBmSlots * 16 * P0.B > kThreads) M.tpo >>= 1;
+  // work-groups per slice group: one per CU over all the linears, dealt in
+  // proportion to their row blocks (at least one, at most one per row block)
+  int budget = P0.ncu / P0.SG;
+  if (budget < 1) budget = 1;
+  int64_t rb_total = 0;
+  for (int j = 0; j < count; ++j) rb_total += P[j].m / 16;
+  int wg = 0;
+  for (int j = 0; j < count; ++j) {
+    const BatchedPass& Q = P[j];
+    QS_REQUIRE(Q.m % 16 == 0 && Q.n == P0.n && Q.B == P0.B && (Q.codes1 != nullptr) == (P0.codes1 != nullptr),
+               "decode-matvec: linears of one launch share n, rows and stages");
+    BmJob& J = M.job[j];
+    const int RB = (int)(Q.m / 16);
+    int64_t gr = (int64_t)budget * RB / rb_total;
+    if (gr < 1) gr = 1;
+    if (gr > RB) gr = RB;
+    J.codes0 = static_cast<const uint16_t*>(Q.codes0);
+    J.codes1 = static_cast<const uint8_t*>(Q.codes1);
+    J.x2h = Q.x2h;
+    J.sg = Q.sg;
+    J.y1p = Q.y1p;
+    J.m = (int)Q.m;
+    J.Gr = (int)gr;
+    J.wg0 = wg;
+    J.s0 = Q.s0;
+    J.s1 = Q.s1;
+    wg += J.Gr * P0.SG;
+  }
+  const unsigned grid = (unsigned)wg;
+  if (P0.codes1)
     hipExtLaunchKernelGGL(bm_kernel<true>, dim3(grid), dim3(kThreads), kBmLds, stream, ev_start, ev_stop, 0, M);
   else
     hipExtLaunchKernelGGL(bm_kernel<false>, dim3(grid), dim3(kThreads), kBmLds, stream, ev_start, ev_stop, 0, M);
   QS_LAUNCHED("bm_kernel");
   return QS_OK;
+}
+
+int launch_bm(const BatchedPass& P, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop) {
+  return launch_bm_group(&P, 1, stream, ev_start, ev_stop);
 }
 
 int launch_linear_batched(const BatchedPass& P, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop) {

@@ -63,9 +63,20 @@ int launch_linear_batched(const BatchedPass& P, hipStream_t stream, hipEvent_t e
 // any number of rows P.B (the output reads P.SG partial groups of P.B rows).
 int launch_bx_rows(const BatchedPass& P, hipStream_t stream);
 int launch_by_rows(const BatchedPass& P, hipStream_t stream);
+// Input transforms of several linears of one x (each its own sv, x2h, sg,
+// xmul) in one launch, bit-identical to one launch_bx_rows per linear.
+int launch_bx_group(const BatchedPass* P, int count, hipStream_t stream);
 // The decode-matvec of a pass on its own (any n; operand rows in x2h / sg,
 // natural layout), y1p[SG][B][m].
 int launch_bm(const BatchedPass& P, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop);
+// The same for several linears of one operand (shared x2h, sg, n, B, slice
+// grouping, stages) in one launch: the work-groups are dealt to the linears in
+// proportion to their rows.  Bit-identical to one launch per linear.
+int launch_bm_group(const BatchedPass* P, int count, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop);
+// Output transforms of several linears (shared B, xmul and output dtype; each
+// its own P[j].SG partial groups) in one launch, bit-identical to one
+// launch_by_rows per linear.
+int launch_by_group(const BatchedPass* P, int count, hipStream_t stream);
 
 // Fragment-major fp16 operand of the wide GEMM: row b, columns k .. k + 7 (k
 // a multiple of 8) are one 16-byte word, words ordered by [b / 16][k / 256]

@@ -234,8 +234,11 @@ def forward_packed_group(x: Tensor, linears, out_dtype=None, workspace: Tensor =
     """Several linears that read the same x in one launch (qs_linear_forward_group):
     ``linears`` is a sequence of (packed, su, sv, s0, s1, layer_scale, bias);
     returns the list of outputs, each equal to ``forward_packed`` of that
-    linear.  Needs batch <= 2, the tiled layout and n a multiple of 256 up to
-    12288.  No counterpart in the reference (one linear per call there)."""
+    linear.  Needs the tiled layout and n a multiple of 256 up to 12288 (one
+    launch at 1-2 rows; from 3 rows one launch per stage -- input transforms,
+    decode-matvecs, output transforms -- for the whole group, the wide GEMM
+    one launch per linear).  No counterpart in the reference (one linear per
+    call there)."""
     count = len(linears)
     if not 1 <= count <= _lib.QS_MAX_GROUP:
         raise ValueError(f"1..{_lib.QS_MAX_GROUP} linears per group, got {count}")

@@ -276,10 +276,20 @@ def _rand_linear(dev, rng, m, n, stages=1, bias=False):
     ([4096, 1024, 11008, 512], 4096, 2, 1, False),
     ([4096, 1024], 4096, 1, 2, False),         # 3-bit residual VQ
     ([4096, 4096], 11008, 1, 1, False),        # odd-factor input
+    ([4096, 4096, 4096], 4096, 3, 1, False),   # 16-row pass: input transforms, decode-matvecs,
+    ([4096, 1024, 1024], 4096, 16, 1, True),   # output transforms one launch each for the group
+    ([11008, 11008], 4096, 8, 2, False),
+    ([4096, 14336], 4096, 8, 1, False),        # m = 56 x 256 outside the chunk scheme: own output kernel
+    ([4096, 4096], 11008, 5, 1, True),
+    ([4096, 1024, 1024], 4096, 24, 1, False),  # wide: one GEMM per linear between the grouped transforms
+    ([11008, 11008], 4096, 40, 2, True),
+    ([4096, 14336], 4096, 33, 1, False),
 ])
 def test_forward_group_equals_single(dev, shapes, n, B, stages, bias):
     """Each output of a grouped launch is bit-identical to the single-linear
-    call (same slices per work-group, same reduction order)."""
+    call (same slices per work-group, same reduction order; at 3 or more rows
+    the same kernels with the linears' work-groups in one grid)."""
+    print(f"case: group {shapes} n={n} B={B} stages={stages}", flush=True)
     from quipsharp_amd.quantize import forward_packed, forward_packed_group
     rng = np.random.default_rng(sum(shapes) + n + B)
     lins = [_rand_linear(dev, rng, m, n, stages, bias) for m in shapes]
@@ -303,17 +313,19 @@ def test_forward_group_equals_single(dev, shapes, n, B, stages, bias):
         assert np.all(np.abs(got - want) <= 2 ** -8 * np.abs(want) + 2e-3 * np.abs(want).max())
 
 
-def test_forward_group_graph_replays(dev):
+@pytest.mark.parametrize("B", [1, 16, 24])
+def test_forward_group_graph_replays(dev, B):
     from quipsharp_amd import _lib
     from quipsharp_amd.quantize import forward_packed_group
+    print(f"case: group graph B={B}", flush=True)
     rng = np.random.default_rng(77)
     lins = [_rand_linear(dev, rng, m, 4096) for m in (4096, 4096, 11008)]
-    x = torch.randn(1, 4096, device=dev).bfloat16()
+    x = torch.randn(B, 4096, device=dev).bfloat16()
     lib = _lib.lib()
     import ctypes
     ms = (ctypes.c_int64 * 3)(4096, 4096, 11008)
-    ws = torch.zeros(lib.qs_linear_group_workspace_bytes(4096, 1, 3, ms), dtype=torch.uint8, device=dev)
-    outs = [torch.empty(1, m, device=dev, dtype=torch.bfloat16) for m in (4096, 4096, 11008)]
+    ws = torch.zeros(lib.qs_linear_group_workspace_bytes(4096, B, 3, ms), dtype=torch.uint8, device=dev)
+    outs = [torch.empty(B, m, device=dev, dtype=torch.bfloat16) for m in (4096, 4096, 11008)]
     eager = [y.clone() for y in forward_packed_group(x, lins, workspace=ws)]
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -335,6 +347,28 @@ def test_forward_group_graph_replays(dev):
         torch.cuda.synchronize()
 
 
+def test_forward_group_workspace_reused_across_row_counts(dev):
+    """One group workspace serves calls of any row count in any order: the
+    one-launch kernel's completion counters sit at fixed places, so a wider
+    call before a 1- or 2-row call cannot leave them non-zero."""
+    from quipsharp_amd import _lib
+    from quipsharp_amd.quantize import forward_packed, forward_packed_group
+    import ctypes
+    rng = np.random.default_rng(31)
+    shapes = (1024, 2048, 1024)
+    lins = [_rand_linear(dev, rng, m, 1024) for m in shapes]
+    ms = (ctypes.c_int64 * 3)(*shapes)
+    lib = _lib.lib()
+    ws = torch.zeros(max(lib.qs_linear_group_workspace_bytes(1024, B, 3, ms) for B in (1, 2, 16, 40)),
+                     dtype=torch.uint8, device=dev)
+    for B in (40, 2, 1, 16, 2, 33, 1):
+        print(f"case: reuse B={B}", flush=True)
+        x = torch.randn(B, 1024, device=dev).bfloat16()
+        ys = forward_packed_group(x, lins, workspace=ws)
+        for lin, y in zip(lins, ys):
+            assert torch.equal(y, forward_packed(x, *lin)), B
+
+
 def test_forward_group_rejects(dev):
     from quipsharp_amd._lib import QuipHipError
     from quipsharp_amd.quantize import forward_packed_group
@@ -346,8 +380,9 @@ def test_forward_group_rejects(dev):
         forward_packed_group(x, [a] * 5)
     with pytest.raises(QuipHipError, match="stages"):
         forward_packed_group(x, [a, b])
-    with pytest.raises(QuipHipError, match="batch"):
-        forward_packed_group(torch.randn(3, 4096, device=dev), [a])
+    c = _rand_linear(dev, rng, 1024, 25600)  # n outside the chunk scheme (25 x 1024 > 12288)
+    with pytest.raises(QuipHipError, match="grouped forward needs n"):
+        forward_packed_group(torch.randn(3, 25600, device=dev), [c])
 
 
 def _dense_weights(codes0, codes1, s0, s1):
