@@ -86,7 +86,7 @@ WsLayout ws_layout(int64_t m, int64_t n, int64_t batch, int layout) {
     L.S = (int)(n / 256);
     L.SG = (L.S + kMaxWaves - 1) / kMaxWaves;
     L.W = (L.S + L.SG - 1) / L.SG;
-    const size_t xrows = L.wide ? (size_t)(B + 15) / 16 * 16 : (size_t)B;  // fragment-major rows: 16s
+    const size_t xrows = (size_t)(B + 15) / 16 * 16;  // fragment-major rows: 16s
     L.x2h = off; off = align256(off + xrows * n * 2);
     L.sg = off; off = align256(off + xrows * (n / 8) * 2);
     L.xtot = off; off = align256(off + (size_t)B * kMaxParts * 4);
@@ -749,6 +749,7 @@ static int forward_batched(const void* x, int x_dtype, int64_t ldx, int64_t batc
       P.sg = reinterpret_cast<_Float16*>(ws + W.sg);
       P.xmul = reinterpret_cast<float*>(ws + W.xmul);
       P.y1p = reinterpret_cast<float*>(ws + W.y1p);
+      P.frag = 1;
       hipEvent_t ev0 = b0 == 0 ? reinterpret_cast<hipEvent_t>(mv_begin) : nullptr;
       hipEvent_t ev1 = b0 + kMaxTileBatch >= batch ? reinterpret_cast<hipEvent_t>(mv_end) : nullptr;
       if (!identity && batched_eligible(n, kron_pn, m, kron_pm) && sv_aligned) {
@@ -758,7 +759,7 @@ static int forward_batched(const void* x, int x_dtype, int64_t ldx, int64_t batc
           rc = launch_bx_rows(P, s);
         else
           rc = launch_xin_rows(P.x, x_dtype, ldx, P.B, n, kron_pn, kron_n, sv, P.x2h, P.sg,
-                               reinterpret_cast<float*>(ws + W.xtot), P.xmul, 0, s, identity);
+                               reinterpret_cast<float*>(ws + W.xtot), P.xmul, P.frag, s, identity);
         if (!rc) rc = launch_bm(P, s, ev0, ev1);
         if (!rc && !identity && chunk_transform_fits(m, kron_pm))
           rc = launch_by_rows(P, s);
@@ -964,7 +965,7 @@ static int forward_group_rows(const void* x, int x_dtype, int64_t ldx, int64_t b
     Q.sg = reinterpret_cast<_Float16*>(ws + off + W.sg);
     Q.xmul = reinterpret_cast<float*>(ws + off + W.xmul);
     Q.y1p = reinterpret_cast<float*>(ws + off + W.y1p);
-    Q.frag = wide ? 1 : 0;
+    Q.frag = 1;
     off += W.total;
   }
   int rc = launch_bx_group(P, count, s);

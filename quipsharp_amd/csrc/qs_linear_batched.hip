@@ -6,7 +6,8 @@
 //   bx_kernel  input transform, one work-group per batch row: activation
 //              chunks times S_v, 256-point transforms in registers, the chunk
 //              stage on the matrix cores, fp16 operand (scaled by 2^-e from the
-//              row norm) and its group sums to the workspace;
+//              row norm) and its group sums to the workspace, both in the
+//              fragment-major order the MFMA B operand is read in;
 //   bm_kernel  decode-matvec: work-group j owns one slice group (one 256-column
 //              slice per wave) and a strided set of 16-row blocks; each wave's
 //              operand (16 batch rows of its slice) stays in registers, codes
@@ -157,7 +158,7 @@ __global__ __launch_bounds__(kThreads) void bx_kernel(BxArgs A) {
 struct BmJob {
   const uint16_t* codes0;
   const uint8_t* codes1;
-  const _Float16* x2h;  // [B][n] operand of this linear
+  const _Float16* x2h;  // fragment-major operand of this linear (16 rows)
   const _Float16* sg;
   float* y1p;  // [SG][B][m]
   int m, Gr, wg0;
@@ -211,16 +212,18 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
   uint4 trow = make_uint4(0, 0, 0, 0), t1row = make_uint4(0, 0, 0, 0);
   trow = *reinterpret_cast<const uint4*>(kE8Ph.w[tid & 255]);
   if (HAS2) t1row = *reinterpret_cast<const uint4*>(kE81h.w[tid & 255]);
-  // operand of lane (q, b = r16): columns 64 q .. 64 q + 63 of this wave's
-  // slice, and the sums of its eight groups of 8 (columns b >= B and idle
-  // waves compute values that are never stored)
-  const bool have = active && r16 < A.B;
-  const _Float16* xrow = J.x2h + (have ? (size_t)r16 * A.n + 256 * sl + 64 * q : 0);
+  // operand of lane (q, b = r16), fragment-major (frag_index): columns
+  // 256 sl + 64 q + 8 c .. + 7 of row r16 are the 16 bytes of lane l = 16 q +
+  // r16 in fragment c of slice sl, so each of the wave's loads reads 1 KiB of
+  // consecutive bytes; then the quarter-sums of its eight groups of 8
+  // (sg_frag_index).  Rows b >= B (padding to 16) and idle waves compute
+  // values that are never stored.
+  const size_t sla = active ? (size_t)sl : 0;
+  const _Float16* xfrag = J.x2h + sla * 4096 + 8 * lane;
   half8 xb[8];
 #pragma unroll
-  for (int c = 0; c < 8; ++c) xb[c] = *reinterpret_cast<const half8*>(xrow + 8 * c);
-  const half8 xs =
-      *reinterpret_cast<const half8*>(J.sg + (have ? (size_t)r16 * (A.n / 8) + 32 * sl + 8 * q : 0));
+  for (int c = 0; c < 8; ++c) xb[c] = *reinterpret_cast<const half8*>(xfrag + 512 * c);
+  const half8 xs = *reinterpret_cast<const half8*>(J.sg + sla * 512 + 8 * lane);
   // code tiles stream through a ring of kPrefetch registers (see the row
   // loop); a tile past the end or of an idle wave reads tile 0 instead
   // byte offset of this lane's 16 code bytes of row block rb (tile 0 past
@@ -244,7 +247,7 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
   fill_luts(tab16, lut_hi, lut_lo, tid);
   __syncthreads();
 
-  float slice_shift = 0.0f;  // sum_g S_g over the slice, batch row r16
+  float slice_shift = 0.0f;  // sum_g S_g / 4 over the slice, batch row r16
 #pragma unroll
   for (int c = 0; c < 8; ++c) slice_shift += (float)xs[c];
   slice_shift += lane_xor<16>(slice_shift, lx);
@@ -292,7 +295,7 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
     if (valid) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        float v = J.s0 * (acc[j] + 0.5f * accs[j] - 0.25f * slice_shift);
+        float v = J.s0 * (acc[j] + 2.0f * accs[j] - slice_shift);
         if (HAS2) v = v + J.s1 * acc2[j];
         rbuf[(w * 16 + 4 * q + j) * kTB + r16] = active ? v : 0.0f;
       }
@@ -593,6 +596,7 @@ int launch_bm_group(const BatchedPass* P, int count, hipStream_t stream, hipEven
     const BatchedPass& Q = P[j];
     QS_REQUIRE(Q.m % 16 == 0 && Q.n == P0.n && Q.B == P0.B && (Q.codes1 != nullptr) == (P0.codes1 != nullptr),
                "decode-matvec: linears of one launch share n, rows and stages");
+    QS_REQUIRE(Q.frag, "decode-matvec: the operand must be fragment-major");
     BmJob& J = M.job[j];
     const int RB = (int)(Q.m / 16);
     int64_t gr = (int64_t)budget * RB / rb_total;

@@ -53,7 +53,8 @@ struct BatchedPass {
   int S, SG, W, ncu;     // slices, slice groups, waves per group, CUs
   _Float16* x2h;         // workspace: [B][n] fp16 operand (fragment-major with frag)
   _Float16* sg;          // workspace: [B][n / 8] group sums (fragment-major / 4 with frag)
-  int frag;              // input transform writes x2h and sg in the wide GEMM's fragment-major order
+  int frag;              // input transform writes x2h and sg fragment-major (the order the decode-matvec
+                         // and the wide GEMM read; the decode-matvec requires it)
   float* xmul;           // workspace: [B]
   float* y1p;            // workspace: [SG][B][m]
 };
@@ -66,8 +67,8 @@ int launch_by_rows(const BatchedPass& P, hipStream_t stream);
 // Input transforms of several linears of one x (each its own sv, x2h, sg,
 // xmul) in one launch, bit-identical to one launch_bx_rows per linear.
 int launch_bx_group(const BatchedPass* P, int count, hipStream_t stream);
-// The decode-matvec of a pass on its own (any n; operand rows in x2h / sg,
-// natural layout), y1p[SG][B][m].
+// The decode-matvec of a pass on its own (any n; operand in x2h / sg,
+// fragment-major, 16 rows), y1p[SG][B][m].
 int launch_bm(const BatchedPass& P, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop);
 // The same for several linears of one operand (shared x2h, sg, n, B, slice
 // grouping, stages) in one launch: the work-groups are dealt to the linears in
