@@ -463,10 +463,12 @@ bool batched_eligible(int64_t n, int pn, int64_t m, int pm) {
 
 namespace {
 
-// Work-groups of a per-row kernel: one per row up to two per CU (each then
-// walks its rows with the next row's loads in flight).
+// Work-groups of a per-row kernel: one per row up to one per CU (the
+// kernels' registers allow one 1024-thread work-group per CU; each walks its
+// rows with the next row's loads in flight).  A launch for several linears
+// passes its share of the CUs.
 unsigned row_grid(int B, int ncu) {
-  const int cap = 2 * (ncu > 0 ? ncu : 256);
+  const int cap = ncu > 0 ? ncu : 256;
   return (unsigned)(B < cap ? B : cap);
 }
 
@@ -505,7 +507,7 @@ int launch_bx_group(const BatchedPass* P, int count, hipStream_t stream) {
   X.Kn = P0.Kn;
   X.scale_n = inv_sqrt_len((int)(P0.n / P0.pn));
   X.frag = P0.frag;
-  X.per = (int)row_grid(P0.B, P0.ncu);
+  X.per = (int)row_grid(P0.B, P0.ncu / count);
   for (int j = 0; j < count; ++j) {
     const BatchedPass& Q = P[j];
     QS_REQUIRE(Q.x == P0.x && Q.x_dtype == P0.x_dtype && Q.ldx == P0.ldx && Q.B == P0.B && Q.n == P0.n &&
@@ -528,7 +530,7 @@ int launch_by_group(const BatchedPass* P, int count, hipStream_t stream) {
   Y.B = P[0].B;
   Y.y_dtype = P[0].y_dtype;
   Y.njobs = count;
-  const unsigned per = row_grid(P[0].B, P[0].ncu);
+  const unsigned per = row_grid(P[0].B, P[0].ncu / count);
   int maxsg = 1;
   for (int j = 0; j < count; ++j) {
     const BatchedPass& Q = P[j];
