@@ -214,16 +214,18 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
   if (HAS2) t1row = *reinterpret_cast<const uint4*>(kE81h.w[tid & 255]);
   // operand of lane (q, b = r16), fragment-major (frag_index): columns
   // 256 sl + 64 q + 8 c .. + 7 of row r16 are the 16 bytes of lane l = 16 q +
-  // r16 in fragment c of slice sl, so each of the wave's loads reads 1 KiB of
-  // consecutive bytes; then the quarter-sums of its eight groups of 8
-  // (sg_frag_index).  Rows b >= B (padding to 16) and idle waves compute
-  // values that are never stored.
+  // r16 in fragment c of slice sl, so each of the wave's loads reads one run
+  // of consecutive bytes; then the quarter-sums of its eight groups of 8
+  // (sg_frag_index).  Lanes of rows b >= B read row 0 again (no extra bytes;
+  // the padding rows are never written) and, like idle waves, compute values
+  // that are never stored.
   const size_t sla = active ? (size_t)sl : 0;
-  const _Float16* xfrag = J.x2h + sla * 4096 + 8 * lane;
+  const int lrow = 16 * q + (r16 < A.B ? r16 : 0);
+  const _Float16* xfrag = J.x2h + sla * 4096 + 8 * lrow;
   half8 xb[8];
 #pragma unroll
   for (int c = 0; c < 8; ++c) xb[c] = *reinterpret_cast<const half8*>(xfrag + 512 * c);
-  const half8 xs = *reinterpret_cast<const half8*>(J.sg + sla * 512 + 8 * lane);
+  const half8 xs = *reinterpret_cast<const half8*>(J.sg + sla * 512 + 8 * lrow);
   // code tiles stream through a ring of kPrefetch registers (see the row
   // loop); a tile past the end or of an idle wave reads tile 0 instead
   // byte offset of this lane's 16 code bytes of row block rb (tile 0 past
@@ -364,9 +366,10 @@ constexpr int kByLds = kByOffMl + kMBytes;
 // Rows b = lb, lb + grid, ... of the linear whose work-groups include this
 // one (lb its index among them); su, bias and M are loaded once.  With one
 // partial group (G == 1) the next row's partial sums are loaded while this
-// row is transformed (with up to kMaxSG they would not fit the registers
-// alongside su and bias, and are loaded per row); G == 0 sums any number of
-// groups one at a time.  A linear with fewer groups than G adds zeros.
+// row is transformed (with up to kMaxSG or 4 they would not fit the registers
+// alongside su and bias, and are loaded per row, all groups at once); G == 0
+// sums any number of groups one at a time.  A linear with fewer groups than G
+// adds zeros.
 template <int G>
 __global__ __launch_bounds__(kThreads) void by_kernel(ByArgs A) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
@@ -473,12 +476,13 @@ unsigned row_grid(int B, int ncu) {
 }
 
 int check_lds() {
-  static int done_x = 0, done_m0 = 0, done_m1 = 0, done_y1 = 0, done_y3 = 0, done_y0 = 0;
+  static int done_x = 0, done_m0 = 0, done_m1 = 0, done_y1 = 0, done_y3 = 0, done_y4 = 0, done_y0 = 0;
   int rc = lds_checked((const void*)bx_kernel, kBxLds, &done_x);
   if (!rc) rc = lds_checked((const void*)bm_kernel<false>, kBmLds, &done_m0);
   if (!rc) rc = lds_checked((const void*)bm_kernel<true>, kBmLds, &done_m1);
   if (!rc) rc = lds_checked((const void*)by_kernel<1>, kByLds, &done_y1);
   if (!rc) rc = lds_checked((const void*)by_kernel<kMaxSG>, kByLds, &done_y3);
+  if (!rc) rc = lds_checked((const void*)by_kernel<4>, kByLds, &done_y4);
   if (!rc) rc = lds_checked((const void*)by_kernel<0>, kByLds, &done_y0);
   return rc;
 }
@@ -561,6 +565,8 @@ int launch_by_group(const BatchedPass* P, int count, hipStream_t stream) {
     hipLaunchKernelGGL(by_kernel<1>, grid, dim3(kThreads), kByLds, stream, Y);
   else if (maxsg <= kMaxSG)
     hipLaunchKernelGGL(by_kernel<kMaxSG>, grid, dim3(kThreads), kByLds, stream, Y);
+  else if (maxsg <= 4)
+    hipLaunchKernelGGL(by_kernel<4>, grid, dim3(kThreads), kByLds, stream, Y);
   else
     hipLaunchKernelGGL(by_kernel<0>, grid, dim3(kThreads), kByLds, stream, Y);
   QS_LAUNCHED("by_kernel");
