@@ -284,6 +284,8 @@ def _rand_linear(dev, rng, m, n, stages=1, bias=False):
     ([4096, 1024, 1024], 4096, 24, 1, False),  # wide: one GEMM per linear between the grouped transforms
     ([11008, 11008], 4096, 40, 2, True),
     ([4096, 14336], 4096, 33, 1, False),
+    ([4096, 1024, 11008, 512], 4096, 16, 1, True),  # four linears, one of each output size
+    ([4096, 1024, 11008, 512], 4096, 24, 1, False),
 ])
 def test_forward_group_equals_single(dev, shapes, n, B, stages, bias):
     """Each output of a grouped launch is bit-identical to the single-linear
