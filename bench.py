@@ -398,8 +398,83 @@ def cpu_baseline(dev_layers_sample=1):
     return {
         "forward_GBps": nbytes / t_fwd / 1e9, "forward_s_per_decoder_layer": t_fwd,
         "quantize_s_per_layer_extrapolated": q_total, "quantize_step_s": {"base": t_base, "tune": t_tune},
-        "threads": threads,
+        "threads": threads, "host": host_cpu(),
     }
+
+
+def host_cpu():
+    """Model, sockets and physical cores of this host, from /proc/cpuinfo."""
+    model, cores = None, set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            phys = core = None
+            for line in f:
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "model name" and model is None:
+                    model = v
+                elif k == "physical id":
+                    phys = v
+                elif k == "core id":
+                    core = v
+                elif not k and phys is not None:
+                    cores.add((phys, core))
+                    phys = core = None
+            if phys is not None:
+                cores.add((phys, core))
+    except OSError:
+        pass
+    return {"model": model, "sockets": len({p for p, _ in cores}) or None, "physical_cores": len(cores) or None,
+            "threads_available": os.cpu_count()}
+
+
+def hbm_copy_peak(dev, nbytes=1 << 30, reps=10):
+    """Measured device-to-device copy rate (bytes read + written per second)
+    over a 1 GiB buffer: the practical HBM ceiling beside the 8 TB/s peak."""
+    import torch
+    a = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).uniform_()
+    b = torch.empty_like(a)
+    b.copy_(a)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        b.copy_(a)
+    e1.record()
+    torch.cuda.synchronize()
+    gbps = 2 * nbytes * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
+    del a, b
+    torch.cuda.empty_cache()
+    return round(gbps, 1)
+
+
+def kernel_rates(dev):
+    """Throughput of the quantize-time kernels: E8P nearest-codeword encode
+    (8-weight groups per second) and the RHT along rows and columns of a
+    4096 x 4096 fp32 matrix (8 bytes per element per pass)."""
+    import torch
+    from quipsharp_amd.codebooks.e8p import E8PCodebook
+    from quipsharp_amd.hadamard import fwht
+    g = torch.Generator(device=dev).manual_seed(3)
+    cb = E8PCodebook(device=dev)
+    ngroups = 1 << 21
+    x = torch.randn(ngroups, 8, generator=g, device=dev)
+    W = torch.randn(4096, 4096, generator=g, device=dev)
+    out = {}
+    for name, fn, reps in (("encode", lambda: cb.quantize(x), 5), ("fwht_rows", lambda: fwht(W, 1), 20),
+                           ("fwht_cols", lambda: fwht(W, 0), 20)):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = e0.elapsed_time(e1) * 1e-3 / reps
+    return {"e8p_encode_groups_per_s": round(ngroups / out["encode"], 0), "e8p_encode_groups": ngroups,
+            "fwht_4096x4096_rows_GBps": round(8 * W.numel() / out["fwht_rows"] / 1e9, 1),
+            "fwht_4096x4096_cols_GBps": round(8 * W.numel() / out["fwht_cols"] / 1e9, 1)}
 
 
 def main():
@@ -421,6 +496,9 @@ def main():
         Runner(stack, 512).step()          # prefill (wide GEMM)
         torch.cuda.synchronize()
         gpu_quantize(dev, n=1024, tune_iters=1)  # encode / LDLQ kernels
+        torch.cuda.synchronize()
+        from quipsharp_amd.codebooks.e8p import E8PCodebook
+        E8PCodebook(device=dev).quantize(torch.randn(1 << 20, 8, device=dev))  # one large encode
         torch.cuda.synchronize()
         a = torch.ones(64 << 20, dtype=torch.float32, device=dev)
         b = torch.empty_like(a)
@@ -490,11 +568,16 @@ def main():
     if not args.skip_quantize:
         extra["quantize_4096x4096_e8p_2bit"] = gpu_quantize(dev)
         log(f"quantize: {extra['quantize_4096x4096_e8p_2bit']}")
+        extra["quantize_kernels"] = kernel_rates(dev)
+        log(f"quantize kernels: {extra['quantize_kernels']}")
+    copy_peak = hbm_copy_peak(dev)
+    log(f"measured copy rate: {copy_peak} GB/s")
     cpu = None
     if not args.skip_cpu:
         log("timing the reference CPU path ...")
         c = cpu_baseline()
         cpu = {"value": round(c["forward_GBps"], 3), "unit": "GB/s", "cores": c["threads"], "kind": "port",
+               "host": c["host"],
                "sample": "reference forward (dense dequantize loop + fp32 matmul, RHT / RFFT transforms) of one "
                          "Llama-2-7B decoder layer's 7 linears at batch 1, torch-CPU restatement; quantize "
                          "4096x4096 E8P 2-bit extrapolated from 5 base-pass and 3 refinement steps",
@@ -519,6 +602,7 @@ def main():
         "roofline": {"bound": "hbm", "kernel": MV_KERNEL, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "avg_launch_us": round(mv_ms * 1e3, 3), "bytes_per_launch": int(mv_avg_bytes),
+                     "measured_copy_GBps": copy_peak,
                      "traffic": measured_traffic() if args.layers == 32 and r1.grouped else None},
         "cpu_baseline": cpu,
     }
