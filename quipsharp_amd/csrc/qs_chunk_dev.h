@@ -96,10 +96,15 @@ __device__ __forceinline__ void h256(float (*v)[4], int lane, LaneX lx) {
   lane_stage<32, NC>(v, lane, lx);
 }
 
-// h256 over the chunks a wave holds (one for S <= 16, else up to three).
-__device__ __forceinline__ void h256_chunks(float (*v)[4], int S, int lane, LaneX lx) {
-  if (S <= kWaves) h256<1>(v, lane, lx);
-  else h256<kCPW>(v, lane, lx);
+// h256 over the chunks a wave holds (one for S <= 16, else up to CPW).
+template <int CPW>
+__device__ __forceinline__ void h256_chunks(float (&v)[CPW][4], int S, int lane, LaneX lx) {
+  if constexpr (CPW == 1) {
+    h256<1>(v, lane, lx);
+  } else {
+    if (S <= kWaves) h256<1>(v, lane, lx);
+    else h256<CPW>(v, lane, lx);
+  }
 }
 
 

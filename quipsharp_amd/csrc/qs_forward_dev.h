@@ -101,14 +101,20 @@ struct XSource {
 };
 
 // Activation chunks of batch row b as loaded (the words of x and of sv), so
-// that a row's loads can be issued one row ahead of their use.
-struct XRaw {
-  uint4 v[kCPW];
-  float4 s[kCPW];
+// that a row's loads can be issued one row ahead of their use.  CPW: chunks
+// per wave the caller holds (S <= 16 CPW); the helpers below take it from
+// their array arguments.
+template <int CPW = kCPW>
+struct XRawT {
+  uint4 v[CPW];
+  float4 s[CPW];
 };
-__device__ __forceinline__ void load_x_raw(const XSource& X, const float* sv, int b, int w, int lane, XRaw& r) {
+using XRaw = XRawT<>;
+template <int CPW>
+__device__ __forceinline__ void load_x_raw(const XSource& X, const float* sv, int b, int w, int lane,
+                                           XRawT<CPW>& r) {
 #pragma unroll
-  for (int u = 0; u < kCPW; ++u) {
+  for (int u = 0; u < CPW; ++u) {
     const int c = w + kWaves * u;
     r.v[u] = make_uint4(0, 0, 0, 0);
     r.s[u] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -132,9 +138,10 @@ __device__ __forceinline__ void load_x_raw(const XSource& X, const float* sv, in
 }
 
 // Activation chunks (times sv), chunk c = w + 16 u, as element t = 4 lane + j.
-__device__ __forceinline__ void finish_x(const XSource& X, const XRaw& r, int w, float (&v)[kCPW][4]) {
+template <int CPW>
+__device__ __forceinline__ void finish_x(const XSource& X, const XRawT<CPW>& r, int w, float (&v)[CPW][4]) {
 #pragma unroll
-  for (int u = 0; u < kCPW; ++u) {
+  for (int u = 0; u < CPW; ++u) {
     const int c = w + kWaves * u;
 #pragma unroll
     for (int j = 0; j < 4; ++j) v[u][j] = 0.0f;
@@ -160,17 +167,19 @@ __device__ __forceinline__ void finish_x(const XSource& X, const XRaw& r, int w,
   }
 }
 
+template <int CPW>
 __device__ __forceinline__ void load_x(const XSource& X, const float* sv, int b, int w, int lane,
-                                       float (&v)[kCPW][4]) {
-  XRaw r;
+                                       float (&v)[CPW][4]) {
+  XRawT<CPW> r;
   load_x_raw(X, sv, b, w, lane, r);
   finish_x(X, r, w, v);
 }
 
 // Chunks held as element t = 4 lane + j (the layout of load_x).
-__device__ __forceinline__ void store_chunks(float* Y, int S, int w, int lane, const float (&v)[kCPW][4]) {
+template <int CPW>
+__device__ __forceinline__ void store_chunks(float* Y, int S, int w, int lane, const float (&v)[CPW][4]) {
 #pragma unroll
-  for (int u = 0; u < kCPW; ++u) {
+  for (int u = 0; u < CPW; ++u) {
     const int c = w + kWaves * u;
     if (c < S)
       *reinterpret_cast<float4*>(Y + c * kYStride + 4 * lane) = make_float4(v[u][0], v[u][1], v[u][2], v[u][3]);
@@ -178,9 +187,10 @@ __device__ __forceinline__ void store_chunks(float* Y, int S, int w, int lane, c
 }
 
 // Chunks held as element t = lane + 64 j (the layout of load_partials).
-__device__ __forceinline__ void store_chunks_lanes(float* Y, int S, int w, int lane, const float (&v)[kCPW][4]) {
+template <int CPW>
+__device__ __forceinline__ void store_chunks_lanes(float* Y, int S, int w, int lane, const float (&v)[CPW][4]) {
 #pragma unroll
-  for (int u = 0; u < kCPW; ++u) {
+  for (int u = 0; u < CPW; ++u) {
     const int c = w + kWaves * u;
     if (c < S) {
 #pragma unroll
@@ -309,17 +319,17 @@ constexpr int kMaxSG = (kMaxS + kWaves - 1) / kWaves;  // column groups of the p
 // loads (partials written by other work-groups of the same launch).  (The
 // 256-point transform is the same for any assignment of the index bits to
 // lanes and registers.)
-template <int G = kMaxSG>
+template <int G = kMaxSG, int CPW = kCPW>
 struct PRaw {
-  float v[G][kCPW][4];
+  float v[G][CPW][4];
 };
-template <bool ATOMIC, int G>
+template <bool ATOMIC, int G, int CPW>
 __device__ __forceinline__ void load_partials_raw(const float* y1p, int m, int Sm, int SG, int B, int b, int w,
-                                                  int lane, PRaw<G>& r) {
+                                                  int lane, PRaw<G, CPW>& r) {
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
-    for (int u = 0; u < kCPW; ++u) {
+    for (int u = 0; u < CPW; ++u) {
       const int c = w + kWaves * u;
 #pragma unroll
       for (int j = 0; j < 4; ++j) r.v[g][u][j] = 0.0f;
@@ -332,10 +342,10 @@ __device__ __forceinline__ void load_partials_raw(const float* y1p, int m, int S
       }
     }
 }
-template <int G>
-__device__ __forceinline__ void sum_partials(const PRaw<G>& r, float (&zv)[kCPW][4]) {
+template <int G, int CPW>
+__device__ __forceinline__ void sum_partials(const PRaw<G, CPW>& r, float (&zv)[CPW][4]) {
 #pragma unroll
-  for (int u = 0; u < kCPW; ++u)
+  for (int u = 0; u < CPW; ++u)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       float v = r.v[0][u][j];
@@ -346,15 +356,16 @@ __device__ __forceinline__ void sum_partials(const PRaw<G>& r, float (&zv)[kCPW]
 }
 // The same sum for any number of groups, one group at a time (groups in
 // ascending order, as sum_partials adds them).
+template <int CPW>
 __device__ __forceinline__ void sum_partials_loop(const float* y1p, int m, int Sm, int SG, int B, int b, int w,
-                                                  int lane, float (&zv)[kCPW][4]) {
+                                                  int lane, float (&zv)[CPW][4]) {
 #pragma unroll
-  for (int u = 0; u < kCPW; ++u)
+  for (int u = 0; u < CPW; ++u)
 #pragma unroll
     for (int j = 0; j < 4; ++j) zv[u][j] = 0.0f;
   for (int g = 0; g < SG; ++g)
 #pragma unroll
-    for (int u = 0; u < kCPW; ++u) {
+    for (int u = 0; u < CPW; ++u) {
       const int c = w + kWaves * u;
       if (c < Sm) {
         const float* src = y1p + ((size_t)g * B + b) * m + 256 * c + lane;
@@ -377,26 +388,27 @@ __device__ __forceinline__ void load_partials(const float* y1p, int m, int Sm, i
 
 // Output values out[a][j] to y[base + idx[a][j]] (idx < 0: no output), one
 // dtype dispatch for all of them.
-__device__ __forceinline__ void store_outputs(void* y, int dtype, int64_t base, const int (&idx)[3][4],
-                                              const float (&out)[3][4]) {
+template <int NA>
+__device__ __forceinline__ void store_outputs(void* y, int dtype, int64_t base, const int (&idx)[NA][4],
+                                              const float (&out)[NA][4]) {
   if (dtype == QS_DTYPE_F32) {
     float* p = static_cast<float*>(y) + base;
 #pragma unroll
-    for (int a = 0; a < 3; ++a)
+    for (int a = 0; a < NA; ++a)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         if (idx[a][j] >= 0) p[idx[a][j]] = out[a][j];
   } else if (dtype == QS_DTYPE_F16) {
     _Float16* p = static_cast<_Float16*>(y) + base;
 #pragma unroll
-    for (int a = 0; a < 3; ++a)
+    for (int a = 0; a < NA; ++a)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         if (idx[a][j] >= 0) p[idx[a][j]] = (_Float16)out[a][j];
   } else {
     uint16_t* p = static_cast<uint16_t*>(y) + base;
 #pragma unroll
-    for (int a = 0; a < 3; ++a)
+    for (int a = 0; a < NA; ++a)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         if (idx[a][j] >= 0) p[idx[a][j]] = f32_to_bf16(out[a][j]);

@@ -55,20 +55,31 @@ struct BxArgs {
   BxJob job[QS_MAX_GROUP];
 };
 
-constexpr int kBxOffY = 0;                                  // kMaxS x kYStride floats
-constexpr int kBxOffMh = kBxOffY + kMaxS * kYStride * 4;
-constexpr int kBxOffMl = kBxOffMh + kMBytes;
-constexpr int kBxOffMisc = kBxOffMl + kMBytes;              // row norm parts
-constexpr int kBxLds = kBxOffMisc + 4 * kWaves;
+// LDS of the per-row transform kernels holding CPW chunks per wave (S <= 16
+// CPW): the chunk rows, then the chunk matrix M as bf16 hi / lo, then the row
+// norm parts.  One chunk per wave (n <= 4096) keeps the registers and LDS of
+// a work-group small enough for two per CU.
+template <int CPW>
+struct RowLds {
+  static constexpr int kY = 0;
+  static constexpr int kMh = kY + 16 * CPW * kYStride * 4;
+  static constexpr int kMl = kMh + kMBytes;
+  static constexpr int kMisc = kMl + kMBytes;
+  static constexpr int kTotal = kMisc + 4 * kWaves;
+};
+static_assert(16 * kCPW >= kMaxS, "chunk rows");
+inline int chunks_per_wave(int64_t S) { return S <= kWaves ? 1 : S <= 2 * kWaves ? 2 : 3; }
 
 // Rows b = lb, lb + per, ... of linear blockIdx / per (lb = blockIdx % per):
 // the next row's activations are loaded while this row is transformed.
+template <int CPW>
 __global__ __launch_bounds__(kThreads) void bx_kernel(BxArgs A) {
+  using L = RowLds<CPW>;
   extern __shared__ __attribute__((aligned(16))) char lds[];
-  float* Y = reinterpret_cast<float*>(lds + kBxOffY);
-  uint16_t* Mh = reinterpret_cast<uint16_t*>(lds + kBxOffMh);
-  uint16_t* Ml = reinterpret_cast<uint16_t*>(lds + kBxOffMl);
-  float* wsum = reinterpret_cast<float*>(lds + kBxOffMisc);
+  float* Y = reinterpret_cast<float*>(lds + L::kY);
+  uint16_t* Mh = reinterpret_cast<uint16_t*>(lds + L::kMh);
+  uint16_t* Ml = reinterpret_cast<uint16_t*>(lds + L::kMl);
+  float* wsum = reinterpret_cast<float*>(lds + L::kMisc);
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
   const int q = lane >> 4, r16 = lane & 15;
@@ -78,7 +89,7 @@ __global__ __launch_bounds__(kThreads) void bx_kernel(BxArgs A) {
   const int g = (int)blockIdx.x / A.per, lb = (int)blockIdx.x - g * A.per;
   const BxJob& J = A.job[g];
 
-  XRaw xr;
+  XRawT<CPW> xr;
   load_x_raw(X, J.sv, lb, w, lane, xr);
   {
     float kmv[3];
@@ -86,12 +97,12 @@ __global__ __launch_bounds__(kThreads) void bx_kernel(BxArgs A) {
     mmat_store(kmv, A.Sn, A.lsh_n, Mh, Ml, tid);
   }
   for (int b = lb; b < A.B; b += stride) {
-    float xv[kCPW][4];
+    float xv[CPW][4];
     finish_x(X, xr, w, xv);
     if (b + stride < A.B) load_x_raw(X, J.sv, b + stride, w, lane, xr);  // the next row
     float ss = 0.0f;
 #pragma unroll
-    for (int u = 0; u < kCPW; ++u)
+    for (int u = 0; u < CPW; ++u)
 #pragma unroll
       for (int j = 0; j < 4; ++j) ss = __builtin_fmaf(xv[u][j], xv[u][j], ss);
     ss = wave_sum(ss, lx);
@@ -109,13 +120,13 @@ __global__ __launch_bounds__(kThreads) void bx_kernel(BxArgs A) {
     // chunk stage: operand row (slice) s = 16 a + 4 q + j, column t = 16 w + r16
     const int t = 16 * w + r16;
     const int nrt = (A.Sn + 15) >> 4, nkb = (A.Sn + 31) >> 5;
-    floatx4 acc[3];
+    floatx4 acc[CPW];
 #pragma unroll
-    for (int a = 0; a < 3; ++a) acc[a] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int a = 0; a < CPW; ++a) acc[a] = floatx4{0.f, 0.f, 0.f, 0.f};
     for (int kb = 0; kb < nkb; ++kb) {
       const ZOperand z = z_operand(Y, A.Sn, t, q, kb);
 #pragma unroll
-      for (int a = 0; a < 3; ++a)
+      for (int a = 0; a < CPW; ++a)
         if (a < nrt) acc[a] = mstage_step(acc[a], Mh, Ml, 16 * a, z, kb, A.pn > 1, q, r16);
     }
     // destinations: natural rows, or the fragment-major operand whose index
@@ -127,7 +138,7 @@ __global__ __launch_bounds__(kThreads) void bx_kernel(BxArgs A) {
     const int xs = A.frag ? 4096 : 256, ss_ = A.frag ? 512 : 32;
     const _Float16 sgmul = A.frag ? (_Float16)0.25f : (_Float16)1.0f;
 #pragma unroll
-    for (int a = 0; a < 3; ++a) {
+    for (int a = 0; a < CPW; ++a) {
       if (a < nrt) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -358,24 +369,20 @@ struct ByArgs {
   ByJob job[QS_MAX_GROUP];
 };
 
-constexpr int kByOffY = 0;
-constexpr int kByOffMh = kByOffY + kMaxS * kYStride * 4;
-constexpr int kByOffMl = kByOffMh + kMBytes;
-constexpr int kByLds = kByOffMl + kMBytes;
-
 // Rows b = lb, lb + grid, ... of the linear whose work-groups include this
 // one (lb its index among them); su, bias and M are loaded once.  With one
 // partial group (G == 1) the next row's partial sums are loaded while this
 // row is transformed (with up to kMaxSG or 4 they would not fit the registers
 // alongside su and bias, and are loaded per row, all groups at once); G == 0
 // sums any number of groups one at a time.  A linear with fewer groups than G
-// adds zeros.
-template <int G>
+// adds zeros.  CPW: chunks per wave, as bx_kernel.
+template <int G, int CPW>
 __global__ __launch_bounds__(kThreads) void by_kernel(ByArgs A) {
+  using L = RowLds<CPW>;
   extern __shared__ __attribute__((aligned(16))) char lds[];
-  float* Y = reinterpret_cast<float*>(lds + kByOffY);
-  uint16_t* Mh = reinterpret_cast<uint16_t*>(lds + kByOffMh);
-  uint16_t* Ml = reinterpret_cast<uint16_t*>(lds + kByOffMl);
+  float* Y = reinterpret_cast<float*>(lds + L::kY);
+  uint16_t* Mh = reinterpret_cast<uint16_t*>(lds + L::kMh);
+  uint16_t* Ml = reinterpret_cast<uint16_t*>(lds + L::kMl);
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
   const int q = lane >> 4, r16 = lane & 15;
@@ -394,14 +401,14 @@ __global__ __launch_bounds__(kThreads) void by_kernel(ByArgs A) {
   // su and bias (unconditional loads from valid addresses)
   float kmv[3];
   mmat_load(kmv, Sm, J.lsh_m, J.pm, J.Km, tid);
-  PRaw<1> pr;
+  PRaw<1, CPW> pr;
   if constexpr (G == 1) load_partials_raw<false, 1>(J.y1p, J.m, Sm, J.SG, A.B, lb, w, lane, pr);
-  int oidx[3][4];
-  float suo[3][4], bio[3][4];
+  int oidx[CPW][4];
+  float suo[CPW][4], bio[CPW][4];
   const float* const bsrc = J.bias ? J.bias : J.su;
   const float bsel = J.bias ? 1.0f : 0.0f;
 #pragma unroll
-  for (int a = 0; a < 3; ++a)
+  for (int a = 0; a < CPW; ++a)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int r = 16 * a + 4 * q + j;
@@ -412,14 +419,14 @@ __global__ __launch_bounds__(kThreads) void by_kernel(ByArgs A) {
     }
   mmat_store(kmv, Sm, J.lsh_m, Mh, Ml, tid);
   for (int b = lb; b < A.B; b += stride) {
-    float zv[kCPW][4];
+    float zv[CPW][4];
     if constexpr (G == 1) {
       sum_partials(pr, zv);
       if (b + stride < A.B) load_partials_raw<false, 1>(J.y1p, J.m, Sm, J.SG, A.B, b + stride, w, lane, pr);
     } else if constexpr (G == 0) {
       sum_partials_loop(J.y1p, J.m, Sm, J.SG, A.B, b, w, lane, zv);
     } else {
-      PRaw<G> pg;
+      PRaw<G, CPW> pg;
       load_partials_raw<false, G>(J.y1p, J.m, Sm, J.SG, A.B, b, w, lane, pg);
       sum_partials(pg, zv);
     }
@@ -428,18 +435,18 @@ __global__ __launch_bounds__(kThreads) void by_kernel(ByArgs A) {
     store_chunks_lanes(Y, Sm, w, lane, zv);
     __syncthreads();
     const int nrt = (Sm + 15) >> 4, nkb = (Sm + 31) >> 5;
-    floatx4 acc[3];
+    floatx4 acc[CPW];
 #pragma unroll
-    for (int a = 0; a < 3; ++a) acc[a] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int a = 0; a < CPW; ++a) acc[a] = floatx4{0.f, 0.f, 0.f, 0.f};
     for (int kb = 0; kb < nkb; ++kb) {
       const ZOperand z = z_operand(Y, Sm, t, q, kb);
 #pragma unroll
-      for (int a = 0; a < 3; ++a)
+      for (int a = 0; a < CPW; ++a)
         if (a < nrt) acc[a] = mstage_step(acc[a], Mh, Ml, 16 * a, z, kb, J.pm > 1, q, r16);
     }
-    float out[3][4];
+    float out[CPW][4];
 #pragma unroll
-    for (int a = 0; a < 3; ++a)
+    for (int a = 0; a < CPW; ++a)
 #pragma unroll
       for (int j = 0; j < 4; ++j) out[a][j] = acc[a][j] * mul * suo[a][j] + bsel * bio[a][j];
     store_outputs(J.y, A.y_dtype, (int64_t)b * J.ldy, oidx, out);
@@ -466,25 +473,52 @@ bool batched_eligible(int64_t n, int pn, int64_t m, int pm) {
 
 namespace {
 
-// Work-groups of a per-row kernel: one per row up to one per CU (the
-// kernels' registers allow one 1024-thread work-group per CU; each walks its
-// rows with the next row's loads in flight).  A launch for several linears
-// passes its share of the CUs.
+// Work-groups of a per-row kernel: one per row up to one per CU, or two with
+// one chunk per wave, whose registers and LDS let two 1024-thread work-groups
+// share a CU (each walks its rows with the next row's loads in flight).  A
+// launch for several linears passes its share of the CUs.
+constexpr int kRowWgsPerCu1 = 2;
+inline int row_wgs_per_cu(int cpw) { return cpw == 1 ? kRowWgsPerCu1 : 1; }
 unsigned row_grid(int B, int ncu) {
   const int cap = ncu > 0 ? ncu : 256;
   return (unsigned)(B < cap ? B : cap);
 }
 
 int check_lds() {
-  static int done_x = 0, done_m0 = 0, done_m1 = 0, done_y1 = 0, done_y3 = 0, done_y4 = 0, done_y0 = 0;
-  int rc = lds_checked((const void*)bx_kernel, kBxLds, &done_x);
-  if (!rc) rc = lds_checked((const void*)bm_kernel<false>, kBmLds, &done_m0);
+  static int done_m0 = 0, done_m1 = 0;
+  int rc = lds_checked((const void*)bm_kernel<false>, kBmLds, &done_m0);
   if (!rc) rc = lds_checked((const void*)bm_kernel<true>, kBmLds, &done_m1);
-  if (!rc) rc = lds_checked((const void*)by_kernel<1>, kByLds, &done_y1);
-  if (!rc) rc = lds_checked((const void*)by_kernel<kMaxSG>, kByLds, &done_y3);
-  if (!rc) rc = lds_checked((const void*)by_kernel<4>, kByLds, &done_y4);
-  if (!rc) rc = lds_checked((const void*)by_kernel<0>, kByLds, &done_y0);
   return rc;
+}
+
+template <int CPW>
+int launch_bx_cpw(const BxArgs& X, unsigned grid, hipStream_t stream) {
+  static int done = 0;
+  const int rc = lds_checked((const void*)bx_kernel<CPW>, RowLds<CPW>::kTotal, &done);
+  if (rc) return rc;
+  hipLaunchKernelGGL(bx_kernel<CPW>, dim3(grid), dim3(kThreads), RowLds<CPW>::kTotal, stream, X);
+  QS_LAUNCHED("bx_kernel");
+  return QS_OK;
+}
+
+template <int G, int CPW>
+int launch_by_gc(const ByArgs& Y, unsigned grid, hipStream_t stream) {
+  static int done = 0;
+  const int rc = lds_checked((const void*)by_kernel<G, CPW>, RowLds<CPW>::kTotal, &done);
+  if (rc) return rc;
+  hipLaunchKernelGGL((by_kernel<G, CPW>), dim3(grid), dim3(kThreads), RowLds<CPW>::kTotal, stream, Y);
+  QS_LAUNCHED("by_kernel");
+  return QS_OK;
+}
+
+// With one partial group the next row's sums are prefetched (by_kernel<1>);
+// up to 3 or 4 groups are loaded together; more, one group at a time.
+template <int CPW>
+int launch_by_cpw(const ByArgs& Y, unsigned grid, int maxsg, hipStream_t stream) {
+  if (maxsg == 1) return launch_by_gc<1, CPW>(Y, grid, stream);
+  if (maxsg <= kMaxSG) return launch_by_gc<kMaxSG, CPW>(Y, grid, stream);
+  if (maxsg <= 4) return launch_by_gc<4, CPW>(Y, grid, stream);
+  return launch_by_gc<0, CPW>(Y, grid, stream);
 }
 
 }  // namespace
@@ -511,7 +545,8 @@ int launch_bx_group(const BatchedPass* P, int count, hipStream_t stream) {
   X.Kn = P0.Kn;
   X.scale_n = inv_sqrt_len((int)(P0.n / P0.pn));
   X.frag = P0.frag;
-  X.per = (int)row_grid(P0.B, P0.ncu / count);
+  const int cpw = chunks_per_wave(X.Sn);
+  X.per = (int)row_grid(P0.B, P0.ncu * row_wgs_per_cu(cpw) / count);
   for (int j = 0; j < count; ++j) {
     const BatchedPass& Q = P[j];
     QS_REQUIRE(Q.x == P0.x && Q.x_dtype == P0.x_dtype && Q.ldx == P0.ldx && Q.B == P0.B && Q.n == P0.n &&
@@ -519,9 +554,12 @@ int launch_bx_group(const BatchedPass* P, int count, hipStream_t stream) {
                "input transform: linears of one launch share x and its transform");
     X.job[j] = BxJob{Q.sv, Q.x2h, Q.sg, Q.xmul};
   }
-  hipLaunchKernelGGL(bx_kernel, dim3((unsigned)(X.per * count)), dim3(kThreads), kBxLds, stream, X);
-  QS_LAUNCHED("bx_kernel");
-  return QS_OK;
+  const unsigned grid = (unsigned)(X.per * count);
+  switch (cpw) {
+    case 1: return launch_bx_cpw<1>(X, grid, stream);
+    case 2: return launch_bx_cpw<2>(X, grid, stream);
+    default: return launch_bx_cpw<3>(X, grid, stream);
+  }
 }
 
 int launch_bx_rows(const BatchedPass& P, hipStream_t stream) { return launch_bx_group(&P, 1, stream); }
@@ -534,8 +572,10 @@ int launch_by_group(const BatchedPass* P, int count, hipStream_t stream) {
   Y.B = P[0].B;
   Y.y_dtype = P[0].y_dtype;
   Y.njobs = count;
-  const unsigned per = row_grid(P[0].B, P[0].ncu / count);
-  int maxsg = 1;
+  int maxsg = 1, cpw = 1;
+  for (int j = 0; j < count; ++j)
+    if (chunks_per_wave(P[j].m / 256) > cpw) cpw = chunks_per_wave(P[j].m / 256);
+  const unsigned per = row_grid(P[0].B, P[0].ncu * row_wgs_per_cu(cpw) / count);
   for (int j = 0; j < count; ++j) {
     const BatchedPass& Q = P[j];
     QS_REQUIRE(chunk_transform_fits(Q.m, Q.pm), "output transform: m outside the chunk scheme");
@@ -560,17 +600,12 @@ int launch_by_group(const BatchedPass* P, int count, hipStream_t stream) {
     J.ldy = Q.ldy;
     if (Q.SG > maxsg) maxsg = Q.SG;
   }
-  const dim3 grid(per * (unsigned)count);
-  if (maxsg == 1)
-    hipLaunchKernelGGL(by_kernel<1>, grid, dim3(kThreads), kByLds, stream, Y);
-  else if (maxsg <= kMaxSG)
-    hipLaunchKernelGGL(by_kernel<kMaxSG>, grid, dim3(kThreads), kByLds, stream, Y);
-  else if (maxsg <= 4)
-    hipLaunchKernelGGL(by_kernel<4>, grid, dim3(kThreads), kByLds, stream, Y);
-  else
-    hipLaunchKernelGGL(by_kernel<0>, grid, dim3(kThreads), kByLds, stream, Y);
-  QS_LAUNCHED("by_kernel");
-  return QS_OK;
+  const unsigned grid = per * (unsigned)count;
+  switch (cpw) {
+    case 1: return launch_by_cpw<1>(Y, grid, maxsg, stream);
+    case 2: return launch_by_cpw<2>(Y, grid, maxsg, stream);
+    default: return launch_by_cpw<3>(Y, grid, maxsg, stream);
+  }
 }
 
 int launch_by_rows(const BatchedPass& P, hipStream_t stream) { return launch_by_group(&P, 1, stream); }
