@@ -124,6 +124,9 @@ class Stack:
 
 
 GROUPS = [("q", "k", "v"), ("o",), ("gate", "up"), ("down",)]   # linears of one launch, per layer
+# (m, n) of a Qwen3-32B decoder layer's linears: q, k, v, o, gate, up, down
+QWEN3_32B_LINEARS = [(8192, 5120), (1024, 5120), (1024, 5120), (5120, 8192), (25600, 5120), (25600, 5120),
+                     (5120, 25600)]
 SOURCE = {"q": None, "k": None, "v": None, "o": "q", "gate": "o", "up": "o", "down": "gate"}
 SHAPE = {name: (m, n) for name, m, n in LLAMA2_7B}
 
@@ -395,7 +398,25 @@ def cpu_baseline(dev_layers_sample=1):
     torch_path.quantize_steps(what, L, hhat, tune_k, tune=True)
     t_tune = (time.perf_counter() - t0) / len(tune_k)
     q_total = t_setup + T * t_base + 10 * T * t_tune
+    # Qwen3-32B-shaped decode: one decoder layer's 7 linears at batch 1 (RHT
+    # where both dims are powers of two, RFFT otherwise, as the reference
+    # chooses), times 64 layers
+    t_q3 = 0.0
+    for m, n in QWEN3_32B_LINEARS:
+        codes = torch.randint(0, 65536, (m, n // 8), generator=g)
+        x = torch.randn(1, n, generator=g)
+        if m & (m - 1) == 0 and n & (n - 1) == 0:
+            kw = dict(su=torch.randint(0, 2, (m,), generator=g).float() * 2 - 1,
+                      sv=torch.randint(0, 2, (n,), generator=g).float() * 2 - 1)
+        else:
+            ph = lambda k: torch.polar(torch.ones(k), torch.rand(k, generator=g) * 2 * math.pi)
+            kw = dict(phase_u=ph(m // 2), phase_v=ph(n // 2))
+        t0 = time.perf_counter()
+        torch_path.linear_forward(x, codes, 0.0135, **kw)
+        t_q3 += time.perf_counter() - t0
+        del codes
     return {
+        "qwen3_32b_decode_s_per_token_extrapolated": 64 * t_q3,
         "forward_GBps": nbytes / t_fwd / 1e9, "forward_s_per_decoder_layer": t_fwd,
         "quantize_s_per_layer_extrapolated": q_total, "quantize_step_s": {"base": t_base, "tune": t_tune},
         "threads": threads, "host": host_cpu(),
@@ -582,6 +603,8 @@ def main():
                          "Llama-2-7B decoder layer's 7 linears at batch 1, torch-CPU restatement; quantize "
                          "4096x4096 E8P 2-bit extrapolated from 5 base-pass and 3 refinement steps",
                "forward_s_per_decoder_layer": round(c["forward_s_per_decoder_layer"], 3),
+               "qwen3_32b_decode_s_per_token": round(c["qwen3_32b_decode_s_per_token_extrapolated"], 1),
+               "qwen3_32b_sample": "one decoder layer's 7 linears at batch 1 timed, x 64 layers",
                "quantize_s_per_layer": round(c["quantize_s_per_layer_extrapolated"], 1)}
         if "quantize_4096x4096_e8p_2bit" in extra:
             extra["quantize_speedup_vs_cpu"] = round(
