@@ -349,6 +349,47 @@ def test_forward_group_graph_replays(dev, B):
         torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_forward_group_random_sweep(dev, seed):
+    """Seeded random groups: 1-4 linears with output sizes inside and outside
+    the chunk scheme, inputs of 512..4096 columns (some with an odd factor),
+    1..40 rows, one or two stages.  Every output is bit-identical to its
+    single-linear call; the first is checked against the dense fp64 oracle."""
+    from quipsharp_amd.quantize import forward_packed, forward_packed_group
+    rng = np.random.default_rng(1000 + seed)
+    count = int(rng.integers(1, 5))
+    n = int(rng.choice([512, 768, 1024, 2048, 3072, 4096]))
+    ms = [int(rng.choice([256, 512, 768, 1024, 2304, 4096, 11008, 14336])) for _ in range(count)]
+    B = int(rng.choice([1, 2, 3, 5, 8, 16, 17, 24, 40]))
+    stages = int(rng.choice([1, 2]))
+    bias = bool(rng.integers(0, 2))
+    print(f"case: sweep seed={seed} n={n} ms={ms} B={B} stages={stages} bias={bias}", flush=True)
+    from quipsharp_amd.quantize import PackedCodes
+    lins, host = [], []
+    for m in ms:
+        c0 = rng.integers(0, 65536, (m, n // 8))
+        c1 = rng.integers(0, 256, (m, n // 8)) if stages == 2 else None
+        su, sv = rng.choice([-1.0, 1.0], m), rng.choice([-1.0, 1.0], n)
+        bv = rng.standard_normal(m).astype(np.float32) if bias else None
+        c = torch.from_numpy(c0).to(dev) if c1 is None else torch.stack(
+            [torch.from_numpy(c0), torch.from_numpy(c1)]).to(dev)
+        packed = PackedCodes(c, m, n, [0] if c1 is None else [0, 1])
+        t = lambda a: torch.from_numpy(np.asarray(a, dtype=np.float32)).to(dev)
+        lins.append((packed, t(su), t(sv), 0.97, 0.45 if stages == 2 else 0.0, 0.0135,
+                     None if bv is None else t(bv)))
+        host.append((c0, c1, su, sv, bv))
+    x = torch.from_numpy(rng.standard_normal((B, n)).astype(np.float32)).to(dev).bfloat16()
+    ys = forward_packed_group(x, lins)
+    for lin, y in zip(lins, ys):
+        assert torch.equal(y, forward_packed(x, *lin))
+    c0, c1, su, sv, bv = host[0]
+    _, _, _, s0, s1, sc, _ = lins[0]
+    want = dense_forward(x.float().cpu().numpy(), c0, c1, s0, s1, su, sv, sc, bv)
+    err = rel_err(ys[0].float().cpu().numpy(), want)
+    print(f"  rel err {err:.2e}", flush=True)
+    assert err < 1e-2  # bf16 output rounding
+
+
 def test_forward_group_workspace_reused_across_row_counts(dev):
     """One group workspace serves calls of any row count in any order: the
     one-launch kernel's completion counters sit at fixed places, so a wider
