@@ -18,6 +18,10 @@
 //   by_kernel  output transform, one work-group per batch row: partial sums,
 //              256-point transforms, chunk stage on the matrix cores,
 //              S_u (.) * scales + bias.
+// Each kernel takes a table of up to QS_MAX_GROUP linears that read the same
+// x (their work-groups side by side in one grid), so a group of linears is
+// three launches in all; bx_kernel and by_kernel also serve the wide path and
+// are instantiated for 1, 2 or 3 chunks of 256 per wave.
 #include <hip/hip_ext.h>
 
 #include "qs_forward_dev.h"
@@ -484,7 +488,7 @@ unsigned row_grid(int B, int ncu) {
   return (unsigned)(B < cap ? B : cap);
 }
 
-int check_lds() {
+int check_bm_lds() {
   static int done_m0 = 0, done_m1 = 0;
   int rc = lds_checked((const void*)bm_kernel<false>, kBmLds, &done_m0);
   if (!rc) rc = lds_checked((const void*)bm_kernel<true>, kBmLds, &done_m1);
@@ -527,8 +531,6 @@ int launch_bx_group(const BatchedPass* P, int count, hipStream_t stream) {
   QS_REQUIRE(count >= 1 && count <= QS_MAX_GROUP, "input transform: 1..%d linears", QS_MAX_GROUP);
   const BatchedPass& P0 = P[0];
   QS_REQUIRE(chunk_transform_fits(P0.n, P0.pn), "input transform: n outside the chunk scheme");
-  int rc = check_lds();
-  if (rc) return rc;
   BxArgs X{};
   X.x = P0.x;
   X.x_dtype = P0.x_dtype;
@@ -566,8 +568,6 @@ int launch_bx_rows(const BatchedPass& P, hipStream_t stream) { return launch_bx_
 
 int launch_by_group(const BatchedPass* P, int count, hipStream_t stream) {
   QS_REQUIRE(count >= 1 && count <= QS_MAX_GROUP, "output transform: 1..%d linears", QS_MAX_GROUP);
-  int rc = check_lds();
-  if (rc) return rc;
   ByArgs Y{};
   Y.B = P[0].B;
   Y.y_dtype = P[0].y_dtype;
@@ -617,7 +617,7 @@ int launch_bm_group(const BatchedPass* P, int count, hipStream_t stream, hipEven
   QS_REQUIRE(P0.n % 256 == 0 && P0.S == (int)(P0.n / 256) && P0.SG >= 1 && P0.W >= 1 && P0.W <= kWaves &&
                  P0.SG * P0.W >= P0.S,
              "decode-matvec: bad slice grouping");
-  int rc = check_lds();
+  int rc = check_bm_lds();
   if (rc) return rc;
   BmArgs M{};
   M.n = (int)P0.n;
