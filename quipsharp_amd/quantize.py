@@ -161,6 +161,22 @@ class PackedCodes:
                                           self.codes1.element_size())
 
 
+def _out_rows(out: Tensor, B: int, m: int) -> Tensor:
+    """``out`` as B rows of m outputs written in place: a (B, m) view with unit
+    column stride (its row stride is passed to the library), never a copy."""
+    if out.shape[-1] != m or out.numel() != B * m:
+        raise ValueError(f"out has shape {tuple(out.shape)}, expected (..., {m}) with {B} rows")
+    y = out.reshape(B, m)
+    if y.untyped_storage().data_ptr() != out.untyped_storage().data_ptr() or (B > 0 and y.stride(1) != 1):
+        raise ValueError("out must be viewable as (rows, m) with unit column stride without a copy")
+    return y
+
+
+def _ld(y: Tensor, m: int) -> int:
+    """Row stride of the (B, m) output view (any stride >= m serves one row)."""
+    return y.stride(0) if y.shape[0] > 1 else max(y.stride(0), m)
+
+
 def forward_packed(x: Tensor, packed: PackedCodes, su: Tensor, sv: Tensor, s0: float, s1: float,
                    layer_scale: float, bias: Tensor = None, out_dtype=None, workspace: Tensor = None,
                    out: Tensor = None, mv_events=None) -> Tensor:
@@ -177,9 +193,9 @@ def forward_packed(x: Tensor, packed: PackedCodes, su: Tensor, sv: Tensor, s0: f
     if x2.stride(-1) != 1:
         x2 = x2.contiguous()
     B = x2.shape[0]
-    y = out.reshape(B, m) if out is not None else torch.empty(B, m, dtype=out_dtype, device=x.device)
+    y = _out_rows(out, B, m) if out is not None else torch.empty(B, m, dtype=out_dtype, device=x.device)
     if B == 0:
-        return y.reshape(*lead, m)
+        return out if out is not None else y.reshape(*lead, m)
     fm, fn = kron_factor(m), kron_factor(n)
     if fm is None or fn is None:
         raise ValueError(f"dims ({m}, {n}) need the form p * 2^k with odd p <= {_lib.QS_MAX_KRON}")
@@ -194,10 +210,10 @@ def forward_packed(x: Tensor, packed: PackedCodes, su: Tensor, sv: Tensor, s0: f
         _lib.ptr(x2), _lib.dtype_code(x2.dtype), x2.stride(0), B, n, m, _lib.ptr(packed.codes0),
         _lib.ptr(packed.codes1), packed.kind1, packed.layout, _lib.ptr(sv), _lib.ptr(su), fn[0], _lib.ptr(Kn),
         fm[0], _lib.ptr(Km), float(s0), float(s1), float(layer_scale), _lib.ptr(bias), _lib.ptr(y),
-        _lib.dtype_code(y.dtype), m, _lib.ptr(workspace), workspace.numel(),
+        _lib.dtype_code(y.dtype), _ld(y, m), _lib.ptr(workspace), workspace.numel(),
         None if mv_events is None else _lib._vp(mv_events[0]), None if mv_events is None else _lib._vp(mv_events[1]),
         _lib.stream_of(x2)))
-    return y.reshape(*lead, m)
+    return out if out is not None else y.reshape(*lead, m)
 
 
 def decode_matvec(x: Tensor, packed: PackedCodes, s0: float, s1: float, layer_scale: float,
@@ -264,16 +280,16 @@ def forward_packed_group(x: Tensor, linears, out_dtype=None, workspace: Tensor =
         if fm is None:
             raise ValueError(f"m = {m} needs the form p * 2^k with odd p <= {_lib.QS_MAX_KRON}")
         Km = hartley_matrix(fm[0], x.device) if fm[0] > 1 else None
-        y = outs[g].reshape(B, m) if outs is not None else torch.empty(B, m, dtype=out_dtype, device=x.device)
+        y = _out_rows(outs[g], B, m) if outs is not None else torch.empty(B, m, dtype=out_dtype, device=x.device)
         ys.append(y)
         jobs[g] = _lib.LinearJob(packed.codes0.data_ptr(), None if packed.codes1 is None else packed.codes1.data_ptr(),
                                  m, su.data_ptr(), sv.data_ptr(), fm[0], None if Km is None else Km.data_ptr(),
                                  float(s0), float(s1), float(layer_scale),
-                                 None if bias is None else bias.data_ptr(), y.data_ptr(), m)
+                                 None if bias is None else bias.data_ptr(), y.data_ptr(), _ld(y, m) if B else m)
         if packed.layout != _lib.QS_LAYOUT_TILED:
             raise ValueError("grouped forward needs the tiled code layout")
     if B == 0:
-        return [y.reshape(*lead, y.shape[-1]) for y in ys]
+        return list(outs) if outs is not None else [y.reshape(*lead, y.shape[-1]) for y in ys]
     if len({y.dtype for y in ys}) != 1:
         raise ValueError("all outputs of a group share one dtype")
     lib = _lib.lib()
@@ -286,7 +302,7 @@ def forward_packed_group(x: Tensor, linears, out_dtype=None, workspace: Tensor =
         _lib.dtype_code(ys[0].dtype), _lib.ptr(workspace), workspace.numel(),
         None if mv_events is None else _lib._vp(mv_events[0]), None if mv_events is None else _lib._vp(mv_events[1]),
         _lib.stream_of(x2)))
-    return [y.reshape(*lead, y.shape[-1]) for y in ys]
+    return list(outs) if outs is not None else [y.reshape(*lead, y.shape[-1]) for y in ys]
 
 
 def _forward_params(codebook, num_stages):

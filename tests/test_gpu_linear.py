@@ -390,6 +390,31 @@ def test_forward_group_random_sweep(dev, seed):
     assert err < 1e-2  # bf16 output rounding
 
 
+@pytest.mark.parametrize("B", [1, 16, 24])
+def test_forward_into_strided_outputs(dev, B):
+    """out / outs may be column slices of wider buffers: the results land in
+    place (row stride passed to the library), the other columns stay as they
+    were, and the values equal those of contiguous outputs."""
+    from quipsharp_amd.quantize import forward_packed, forward_packed_group
+    rng = np.random.default_rng(60 + B)
+    lins = [_rand_linear(dev, rng, m, 1024, 1, True) for m in (512, 768)]
+    x = torch.randn(B, 1024, device=dev).bfloat16()
+    want = [forward_packed(x, *lin) for lin in lins]
+    big = torch.full((B, 512 + 768 + 64), 7.0, device=dev, dtype=torch.bfloat16)
+    outs = [big[:, 0:512], big[:, 512:1280]]
+    got = forward_packed_group(x, lins, outs=outs)
+    assert got[0] is outs[0] and got[1] is outs[1]
+    for w, o in zip(want, outs):
+        assert torch.equal(o, w)
+    assert torch.all(big[:, 1280:] == 7.0)
+    big2 = torch.full((B, 600), 7.0, device=dev, dtype=torch.bfloat16)
+    y = forward_packed(x, *lins[0], out=big2[:, 40:552])
+    assert torch.equal(y, want[0]) and torch.all(big2[:, :40] == 7.0) and torch.all(big2[:, 552:] == 7.0)
+    if B > 1:  # rows that are not contiguous along m: refused, never written to a copy
+        with pytest.raises(ValueError):
+            forward_packed(x, *lins[0], out=torch.empty(512, B, device=dev, dtype=torch.bfloat16).T)
+
+
 def test_forward_group_workspace_reused_across_row_counts(dev):
     """One group workspace serves calls of any row count in any order: the
     one-launch kernel's completion counters sit at fixed places, so a wider
