@@ -94,3 +94,25 @@ def test_group_argument_errors(L):
     rc = L.qs_linear_forward_group(ct.c_void_p(256), 0, 16384, 3, 16384, 1, None, 1, jobs, 0, ct.c_void_p(256),
                                    1 << 20, None, None, None)  # n = 2^14 > 12288: outside the chunk scheme
     assert rc == 1 and b"grouped forward needs n" in L.qs_last_error()
+
+
+def test_out_rows_views_without_copy():
+    """Output views for the forward: (rows, m) in place with their row stride,
+    never a copy; views that would need one are refused (host logic only)."""
+    import torch
+    from quipsharp_amd.quantize import _ld, _out_rows
+    big = torch.zeros(4, 40)
+    y = _out_rows(big[:, 8:24], 4, 16)
+    assert y.data_ptr() == big[:, 8:24].data_ptr() and y.stride() == (40, 1) and _ld(y, 16) == 40
+    y3 = _out_rows(torch.zeros(2, 3, 16), 6, 16)
+    assert y3.shape == (6, 16) and _ld(y3, 16) == 16
+    one = torch.zeros(16, 1).T  # a single row: contiguous along m, any row stride
+    assert _ld(_out_rows(one, 1, 16), 16) == 16
+    with pytest.raises(ValueError):
+        _out_rows(torch.zeros(16, 4).T, 4, 16)  # rows not contiguous along m
+    with pytest.raises(ValueError):
+        _out_rows(torch.zeros(4, 15), 4, 16)
+    y4 = _out_rows(torch.zeros(2, 3, 40)[:, :, :16], 6, 16)  # the two leading dims collapse: row stride 40
+    assert y4.stride() == (40, 1) and _ld(y4, 16) == 40
+    with pytest.raises(ValueError):
+        _out_rows(torch.zeros(2, 3, 40)[:, :2, :16], 4, 16)  # (4, 16) only as a copy
