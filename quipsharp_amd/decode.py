@@ -18,7 +18,7 @@ import torch
 from torch import nn
 
 from .architectures import get_decoder_layers, get_linear_groups
-from .checkpoint import QuantizedLinear, build_codebook, grouped_forward
+from .checkpoint import QuantizedLinear, build_codebook, grouped_forward, link_sibling_linears
 from .hadamard import is_pow2, kron_factor, rademacher
 
 QWEN3_32B = dict(hidden_size=5120, intermediate_size=25600, num_hidden_layers=64, num_attention_heads=64,
@@ -83,6 +83,7 @@ def random_quantized_model(config, device="cuda", seed=0):
             if b is not None and b.is_meta:
                 setattr(mod, k, torch.zeros(b.shape, dtype=b.dtype, device=device))
     model.eval()
+    link_sibling_linears(model)
     return model
 
 

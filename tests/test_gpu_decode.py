@@ -102,3 +102,67 @@ def test_grouped_forward_equals_separate_calls(dev, rows):
             assert len(got) == len(want)
             for g_, w_ in zip(got, want):
                 assert g_.dtype == w_.dtype and torch.equal(g_, w_)
+
+
+@pytest.mark.parametrize("rows", [1, 16])
+def test_linked_siblings_called_one_by_one(dev, rows, monkeypatch):
+    """link_sibling_linears: q/k/v (and gate/up) called one by one, as a
+    transformers model does, run one grouped forward per group; every output
+    is bit-identical to the unlinked call, and an input changed in place or a
+    different tensor is recomputed, never served from the group's results."""
+    from quipsharp_amd import quantize
+    from quipsharp_amd.architectures import get_decoder_layers
+    from quipsharp_amd.decode import random_quantized_model
+    model = random_quantized_model(_tiny_config(), dev, seed=4)
+    layer = get_decoder_layers(model)[0]
+    mods = [layer.self_attn.q_proj, layer.self_attn.k_proj, layer.self_attn.v_proj]
+    assert all(m._siblings is mods[0]._siblings for m in mods) and len(mods[0]._siblings) == 3
+    x = torch.randn(rows, 512, generator=torch.Generator().manual_seed(rows)).to(dev).bfloat16()
+    with torch.no_grad():
+        want = [m._forward_one(x) for m in mods]
+        calls = {"group": 0}
+        real = quantize.forward_packed_group
+
+        def counting(*a, **k):
+            calls["group"] += 1
+            return real(*a, **k)
+        monkeypatch.setattr(quantize, "forward_packed_group", counting)
+        # eager: one call per linear, no grouping
+        got = [m(x) for m in mods]
+        assert calls["group"] == 0
+        for g_, w_ in zip(got, want):
+            assert torch.equal(g_, w_)
+        # captured: the first member computes the group, the others take theirs
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            [m(x) for m in mods]
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            got = [m(x) for m in mods]
+        assert calls["group"] == 1
+        for rep in range(3):
+            for g_ in got:
+                g_.zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            for g_, w_ in zip(got, want):
+                assert torch.equal(g_, w_), rep
+        del graph
+        monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)  # group eagerly from here on
+        calls["group"] = 0
+        got = [m(x) for m in mods]
+        assert calls["group"] == 1
+        for g_, w_ in zip(got, want):
+            assert torch.equal(g_, w_)
+        # q again recomputes the group; an in-place change of x before k does too
+        mods[0](x)
+        x.mul_(2.0)
+        k2 = mods[1](x)
+        assert torch.equal(k2, mods[1]._forward_one(x))
+        # a different tensor with the same values is not served from the group of x
+        mods[0](x)
+        x2 = x.clone()
+        assert torch.equal(mods[2](x2), mods[2]._forward_one(x2))
