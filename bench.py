@@ -626,6 +626,7 @@ def main():
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "avg_launch_us": round(mv_ms * 1e3, 3), "bytes_per_launch": int(mv_avg_bytes),
                      "measured_copy_GBps": copy_peak,
+                     "frac_of_measured_copy": round(achieved / copy_peak, 4) if copy_peak else None,
                      "traffic": measured_traffic() if args.layers == 32 and r1.grouped else None},
         "cpu_baseline": cpu,
     }
