@@ -168,18 +168,22 @@ class Runner:
             ws = max(self.lib.qs_linear_workspace_bytes(m, n, B, _lib.QS_LAYOUT_TILED) for _, m, n in LLAMA2_7B)
         self.ws = torch.zeros(ws, dtype=torch.uint8, device=dev)  # counter regions must start at zero
         # per (layer, launch): the ctypes job array, built once
-        self.jobs = []
+        # signs as packed bits (QS_SIGNS_BITS), as QuantizedLinear passes them
+        from quipsharp_amd.quantize import pack_signs
+        self.jobs, self._bits = [], []
         for lin in stack.layers:
             per = []
             for names in self.plan:
                 arr = (_lib.LinearJob * len(names))()
                 for j, k in enumerate(names):
                     packed, su, sv, scale = lin[k]
+                    su, sv = pack_signs(su), pack_signs(sv)
+                    self._bits += [su, sv]
                     m = SHAPE[k][0]
                     km = 43 if m == 11008 else 1
                     arr[j] = _lib.LinearJob(packed.codes0.data_ptr(), None, m, su.data_ptr(), sv.data_ptr(), km,
                                             self.K43.data_ptr() if km > 1 else None, 1.0, 0.0, scale, None,
-                                            self.buf[k].data_ptr(), m)
+                                            self.buf[k].data_ptr(), m, 1)
                 per.append(arr)
             self.jobs.append(per)
 
@@ -197,7 +201,8 @@ class Runner:
             j = self.jobs[li][gi][0]
             m = j.m
             rc = L.qs_linear_forward(
-                x.data_ptr(), _lib.QS_DTYPE_BF16, n, self.B, n, m, j.codes0, None, 0, _lib.QS_LAYOUT_TILED, j.sv, j.su,
+                x.data_ptr(), _lib.QS_DTYPE_BF16, n, self.B, n, m, j.codes0, None, 0, _lib.QS_LAYOUT_TILED | _lib.QS_SIGNS_BITS,
+                j.sv, j.su,
                 kn, Kn, j.kron_pm, j.kron_m, 1.0, 0.0, j.layer_scale, None, j.y, _lib.QS_DTYPE_BF16, m,
                 self.ws.data_ptr(), self.ws.numel(), e0, e1, stream)
         if rc:

@@ -39,6 +39,13 @@ enum {
 enum { QS_STAGE_E8P = 0, QS_STAGE_E8_1BIT = 1 };          /* residual-VQ stage codebooks */
 enum { QS_DTYPE_F32 = 0, QS_DTYPE_F16 = 1, QS_DTYPE_BF16 = 2 };
 enum { QS_LAYOUT_ROWMAJOR = 0, QS_LAYOUT_TILED = 1 };     /* packed-code layouts */
+/* Flag OR'd into qs_linear_forward's layout (QS_LAYOUT_TILED only): su and sv
+ * point to packed sign bits instead of fp32 vectors -- uint32 words, bit
+ * (i % 32) of word i / 32 set for element i = -1, clear for +1 -- a 32nd of
+ * the bytes every work-group of the transforms reads.  Accepted when n and m
+ * are both on the chunk scheme (multiples of 256, at most 12288, length / odd
+ * factor >= 256); QS_ERR_UNSUPPORTED otherwise. */
+#define QS_SIGNS_BITS 0x100
 
 #define QS_ABI_VERSION 1
 #define QS_MAX_STAGES 4
@@ -149,7 +156,8 @@ size_t qs_linear_workspace_bytes(int64_t m, int64_t n, int64_t batch, int layout
  *   x      [batch][ldx] in x_dtype, y [batch][ldy] in y_dtype
  *   codes0 packed E8P codes; codes1 packed second-stage codes or NULL, of kind
  *          kind1 (QS_STAGE_E8_1BIT, or QS_STAGE_E8P on the row-major layout)
- *   sv [n], su [m] fp32 sign vectors; kron_* as in qs_rht_f32 (p = 1: FWHT)
+ *   sv [n], su [m] fp32 sign vectors (packed bits with QS_SIGNS_BITS in
+ *          layout); kron_* as in qs_rht_f32 (p = 1: FWHT)
  *   bias [m] fp32 or NULL
  * Activations enter the matrix cores as fp16 (per-row power-of-two scaled),
  * decoded weights are exact in fp16, accumulation is fp32.
@@ -188,6 +196,7 @@ typedef struct qs_linear_job {
   const float *bias;    /* [m] fp32 or NULL */
   void *y;              /* [batch][ldy] in the call's y_dtype */
   int64_t ldy;
+  int sign_bits;        /* nonzero: su and sv are packed sign bits (see QS_SIGNS_BITS); the same for every job */
 } qs_linear_job;
 
 /* Workspace bytes for qs_linear_forward_group: ms[count] output sizes. */

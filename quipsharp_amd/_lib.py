@@ -17,6 +17,7 @@ QS_STAGE_E8P = 0
 QS_STAGE_E8_1BIT = 1
 QS_DTYPE_F32, QS_DTYPE_F16, QS_DTYPE_BF16 = 0, 1, 2
 QS_LAYOUT_ROWMAJOR, QS_LAYOUT_TILED = 0, 1
+QS_SIGNS_BITS = 0x100  # layout flag: su / sv are packed sign bits
 QS_MAX_STAGES = 4
 QS_MAX_KRON = 64
 QS_MAX_GROUP = 4
@@ -30,7 +31,7 @@ class LinearJob(ctypes.Structure):
                 ("su", ctypes.c_void_p), ("sv", ctypes.c_void_p), ("kron_pm", ctypes.c_int),
                 ("kron_m", ctypes.c_void_p), ("s0", ctypes.c_float), ("s1", ctypes.c_float),
                 ("layer_scale", ctypes.c_float), ("bias", ctypes.c_void_p), ("y", ctypes.c_void_p),
-                ("ldy", ctypes.c_int64)]
+                ("ldy", ctypes.c_int64), ("sign_bits", ctypes.c_int)]
 
 _i64 = ctypes.c_int64
 _int = ctypes.c_int

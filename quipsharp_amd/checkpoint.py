@@ -119,11 +119,13 @@ class QuantizedLinear(nn.Module):
 
     def _load_from_state_dict(self, *args, **kwargs):
         self._packed = None
+        self._bits_key = None
         self._sib_out = None
         return super()._load_from_state_dict(*args, **kwargs)
 
     def _apply(self, fn, *args, **kwargs):
         self._packed = None
+        self._bits_key = None
         self._ws = None
         self._group_ws = None
         self._sib_out = None
@@ -136,6 +138,23 @@ class QuantizedLinear(nn.Module):
             self._packed_key = key
             self._scale_f = float(self.scale.item())
         return self._packed
+
+    def signs(self):
+        """(su, sv) for the forward: packed sign bits (a 32nd of the fp32 bytes,
+        read by every work-group of the transforms) where both sizes fit the
+        library's chunk scheme, else the fp32 vectors.  Packed once per sign
+        buffer, outside graph capture."""
+        su, sv = self.su, self.sv
+        if not all(d % 256 == 0 and d <= 12288 for d in (self.in_features, self.out_features)):
+            return su, sv
+        key = (su.data_ptr(), su._version, sv.data_ptr(), sv._version)
+        if getattr(self, "_bits_key", None) != key:
+            if torch.cuda.is_current_stream_capturing():
+                return su, sv
+            from .quantize import pack_signs
+            self._bits = (pack_signs(su), pack_signs(sv))
+            self._bits_key = key
+        return self._bits
 
     def forward(self, x: Tensor) -> Tensor:
         """quipsharp/checkpoint.py:141-146: y = transform_output(x2 @ W_hat^T) + bias
@@ -177,7 +196,8 @@ class QuantizedLinear(nn.Module):
         kinds, s0, s1 = _forward_params(self.codebook, self.num_stages)
         packed = self.packed(kinds)
         ws = self._workspace(x, packed)
-        return forward_packed(x, packed, self.su, self.sv, s0, s1, self._scale_f, bias=self.bias,
+        su, sv = self.signs()
+        return forward_packed(x, packed, su, sv, s0, s1, self._scale_f, bias=self.bias,
                               out_dtype=x.dtype, workspace=ws)
 
     def _workspace(self, x, packed):
@@ -256,7 +276,7 @@ def _grouped(x: Tensor, linears):
     jobs = []
     for l in linears:
         kinds, s0, s1 = _forward_params(l.codebook, l.num_stages)
-        jobs.append((l.packed(kinds), l.su, l.sv, s0, s1, l._scale_f, l.bias))
+        jobs.append((l.packed(kinds), *l.signs(), s0, s1, l._scale_f, l.bias))
     lead = linears[0]
     ms = (ctypes.c_int64 * len(linears))(*[l.out_features for l in linears])
     need = _lib.lib().qs_linear_group_workspace_bytes(n, rows, len(linears), ms)

@@ -25,6 +25,14 @@ int hip_status(hipError_t e, const char* what);
     }                                                         \
   } while (0)
 
+#define QS_SUPPORTED(cond, ...)                               \
+  do {                                                        \
+    if (!(cond)) {                                            \
+      ::qs::set_error(__VA_ARGS__);                           \
+      return QS_ERR_UNSUPPORTED;                              \
+    }                                                         \
+  } while (0)
+
 #define QS_HIP(expr)                                          \
   do {                                                        \
     hipError_t e_ = (expr);                                   \

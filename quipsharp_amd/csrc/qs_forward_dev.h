@@ -98,7 +98,14 @@ struct XSource {
   int vec;  // rows of 4 elements can be loaded as one 8- or 16-byte word
   int64_t ldx;
   int S;    // chunks of 256
+  int sbits;  // sv holds packed sign bits (QS_SIGNS_BITS), not fp32 values
 };
+
+// x times the sign of bit k of b (set: -1), as a sign-bit flip: the same
+// value as x * -1.0f / x * 1.0f.
+__device__ __forceinline__ float flip_by_bit(float x, uint32_t b, int k) {
+  return __uint_as_float(__float_as_uint(x) ^ (((b >> k) & 1u) << 31));
+}
 
 // Activation chunks of batch row b as loaded (the words of x and of sv), so
 // that a row's loads can be issued one row ahead of their use.  CPW: chunks
@@ -120,7 +127,10 @@ __device__ __forceinline__ void load_x_raw(const XSource& X, const float* sv, in
     r.s[u] = make_float4(0.f, 0.f, 0.f, 0.f);
     if (c < X.S) {
       const int i0 = 256 * c + 4 * lane;
-      r.s[u] = *reinterpret_cast<const float4*>(sv + i0);
+      // sign bits: the word of elements i0 .. i0 + 3, kept raw in s.x and
+      // applied in finish_x (no wait for the load here)
+      if (X.sbits) r.s[u].x = __uint_as_float(reinterpret_cast<const uint32_t*>(sv)[i0 >> 5]);
+      else r.s[u] = *reinterpret_cast<const float4*>(sv + i0);
       const int64_t xi = (int64_t)b * X.ldx + i0;
       if (X.vec && X.dtype == QS_DTYPE_F32) {
         r.v[u] = *reinterpret_cast<const uint4*>(static_cast<const float*>(X.x) + xi);
@@ -139,7 +149,8 @@ __device__ __forceinline__ void load_x_raw(const XSource& X, const float* sv, in
 
 // Activation chunks (times sv), chunk c = w + 16 u, as element t = 4 lane + j.
 template <int CPW>
-__device__ __forceinline__ void finish_x(const XSource& X, const XRawT<CPW>& r, int w, float (&v)[CPW][4]) {
+__device__ __forceinline__ void finish_x(const XSource& X, const XRawT<CPW>& r, int w, int lane,
+                                         float (&v)[CPW][4]) {
 #pragma unroll
   for (int u = 0; u < CPW; ++u) {
     const int c = w + kWaves * u;
@@ -159,10 +170,18 @@ __device__ __forceinline__ void finish_x(const XSource& X, const XRawT<CPW>& r, 
       } else {
         x0 = __uint_as_float(t.x), x1 = __uint_as_float(t.y), x2 = __uint_as_float(t.z), x3 = __uint_as_float(t.w);
       }
-      v[u][0] = x0 * r.s[u].x;
-      v[u][1] = x1 * r.s[u].y;
-      v[u][2] = x2 * r.s[u].z;
-      v[u][3] = x3 * r.s[u].w;
+      if (X.sbits) {
+        const uint32_t b = __float_as_uint(r.s[u].x) >> (4 * (lane & 7));
+        v[u][0] = flip_by_bit(x0, b, 0);
+        v[u][1] = flip_by_bit(x1, b, 1);
+        v[u][2] = flip_by_bit(x2, b, 2);
+        v[u][3] = flip_by_bit(x3, b, 3);
+      } else {
+        v[u][0] = x0 * r.s[u].x;
+        v[u][1] = x1 * r.s[u].y;
+        v[u][2] = x2 * r.s[u].z;
+        v[u][3] = x3 * r.s[u].w;
+      }
     }
   }
 }
@@ -172,7 +191,7 @@ __device__ __forceinline__ void load_x(const XSource& X, const float* sv, int b,
                                        float (&v)[CPW][4]) {
   XRawT<CPW> r;
   load_x_raw(X, sv, b, w, lane, r);
-  finish_x(X, r, w, v);
+  finish_x(X, r, w, lane, v);
 }
 
 // Chunks held as element t = 4 lane + j (the layout of load_x).
@@ -384,6 +403,15 @@ __device__ __forceinline__ void load_partials(const float* y1p, int m, int Sm, i
   PRaw<kMaxSG> r;
   load_partials_raw<ATOMIC, kMaxSG>(y1p, m, Sm, SG, B, b, w, lane, r);
   sum_partials(r, zv);
+}
+
+// su entry i for the output stage: the fp32 value, or with sign bits the raw
+// word holding bit i (kept as float bits; applied by apply_su at the end).
+__device__ __forceinline__ float load_su(const float* su, int sbits, int i) {
+  return sbits ? __uint_as_float(reinterpret_cast<const uint32_t*>(su)[i >> 5]) : su[i];
+}
+__device__ __forceinline__ float apply_su(float v, float suo, int sbits, int i) {
+  return sbits ? flip_by_bit(v, __float_as_uint(suo), i & 31) : v * suo;
 }
 
 // Output values out[a][j] to y[base + idx[a][j]] (idx < 0: no output), one

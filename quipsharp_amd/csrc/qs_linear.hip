@@ -643,7 +643,7 @@ static int forward_wide(const void* x, int x_dtype, int64_t ldx, int64_t batch, 
                         const void* codes0, const void* codes1, const float* sv, const float* su, int kron_pn,
                         const float* kron_n, int kron_pm, const float* kron_m, float s0, float s1, float layer_scale,
                         const float* bias, void* y, int y_dtype, int64_t ldy, char* ws, const WsLayout& W,
-                        void* mv_begin, void* mv_end, hipStream_t s) {
+                        void* mv_begin, void* mv_end, hipStream_t s, int sbits) {
   QS_REQUIRE(batch <= (int64_t)1 << 30, "wide forward: at most 2^30 rows");
   BatchedPass P{};
   P.x = x;
@@ -670,8 +670,9 @@ static int forward_wide(const void* x, int x_dtype, int64_t ldx, int64_t batch, 
   P.xmul = reinterpret_cast<float*>(ws + W.xmul);
   P.y1p = reinterpret_cast<float*>(ws + W.y1p);
   P.frag = 1;
+  P.sbits = sbits;
   int rc = QS_OK;
-  const bool sv_aligned = (reinterpret_cast<uintptr_t>(sv) & 15) == 0;
+  const bool sv_aligned = (reinterpret_cast<uintptr_t>(sv) & (sbits ? 3 : 15)) == 0;
   if (chunk_transform_fits(n, kron_pn) && sv_aligned)
     rc = launch_bx_rows(P, s);
   else
@@ -708,16 +709,17 @@ static int forward_batched(const void* x, int x_dtype, int64_t ldx, int64_t batc
                     const void* codes0, const void* codes1, int kind1, int layout, const float* sv, const float* su,
                     int kron_pn, const float* kron_n, int kron_pm, const float* kron_m, float s0, float s1,
                     float layer_scale, const float* bias, void* y, int y_dtype, int64_t ldy, char* ws,
-                    const WsLayout& W, void* mv_begin, void* mv_end, hipStream_t s, bool identity) {
+                    const WsLayout& W, void* mv_begin, void* mv_end, hipStream_t s, bool identity,
+                    int sbits = 0) {
   int rc = QS_OK;
   if (!identity && W.wide)
     return forward_wide(x, x_dtype, ldx, batch, n, m, codes0, codes1, sv, su, kron_pn, kron_n, kron_pm, kron_m, s0, s1,
-                        layer_scale, bias, y, y_dtype, ldy, ws, W, mv_begin, mv_end, s);
+                        layer_scale, bias, y, y_dtype, ldy, ws, W, mv_begin, mv_end, s, sbits);
   if (layout == QS_LAYOUT_TILED) {
     // passes of up to 16 rows: input transform, decode-matvec on all 16 MFMA
     // columns, output transform (qs_linear_batched.hip); an n or m outside
     // the chunk scheme takes the LDS-radix row kernel for that side
-    const bool sv_aligned = (reinterpret_cast<uintptr_t>(sv) & 15) == 0;
+    const bool sv_aligned = (reinterpret_cast<uintptr_t>(sv) & (sbits ? 3 : 15)) == 0;
     for (int64_t b0 = 0; b0 < batch; b0 += kMaxTileBatch) {
       BatchedPass P{};
       P.B = (int)(batch - b0 < kMaxTileBatch ? batch - b0 : kMaxTileBatch);
@@ -750,6 +752,7 @@ static int forward_batched(const void* x, int x_dtype, int64_t ldx, int64_t batc
       P.xmul = reinterpret_cast<float*>(ws + W.xmul);
       P.y1p = reinterpret_cast<float*>(ws + W.y1p);
       P.frag = 1;
+      P.sbits = sbits;
       hipEvent_t ev0 = b0 == 0 ? reinterpret_cast<hipEvent_t>(mv_begin) : nullptr;
       hipEvent_t ev1 = b0 + kMaxTileBatch >= batch ? reinterpret_cast<hipEvent_t>(mv_end) : nullptr;
       if (!identity && batched_eligible(n, kron_pn, m, kron_pm) && sv_aligned) {
@@ -854,6 +857,8 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
   QS_REQUIRE(x_dtype >= QS_DTYPE_F32 && x_dtype <= QS_DTYPE_BF16 && y_dtype >= QS_DTYPE_F32 &&
                  y_dtype <= QS_DTYPE_BF16,
              "bad dtype");
+  const int sbits = (layout & QS_SIGNS_BITS) ? 1 : 0;
+  layout &= ~QS_SIGNS_BITS;
   QS_REQUIRE(layout == QS_LAYOUT_TILED || layout == QS_LAYOUT_ROWMAJOR, "bad layout");
   if (batch == 0) return QS_OK;
   QS_REQUIRE(x && y && codes0 && sv && su && workspace, "null pointer");
@@ -862,6 +867,13 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
   if (rc) return rc;
   rc = check_transform(m, kron_pm, kron_m, "output");
   if (rc) return rc;
+  if (sbits) {
+    QS_SUPPORTED(layout == QS_LAYOUT_TILED && chunk_transform_fits(n, kron_pn) && chunk_transform_fits(m, kron_pm),
+                 "packed sign bits need the tiled layout with n and m on the chunk scheme (got m %lld, n %lld)",
+                 (long long)m, (long long)n);
+    QS_REQUIRE((reinterpret_cast<uintptr_t>(sv) & 3) == 0 && (reinterpret_cast<uintptr_t>(su) & 3) == 0,
+               "packed sign bits must be 4-byte aligned");
+  }
   if (layout == QS_LAYOUT_TILED)
     QS_REQUIRE(m % 16 == 0 && n % 256 == 0, "tiled layout needs m %% 16 == 0 and n %% 256 == 0");
   QS_REQUIRE(!codes1 || kind1 == QS_STAGE_E8_1BIT || (kind1 == QS_STAGE_E8P && layout == QS_LAYOUT_ROWMAJOR),
@@ -877,7 +889,7 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
   hipStream_t s = as_stream(stream);
   char* ws = static_cast<char*>(workspace);
   if (layout == QS_LAYOUT_TILED && fused_eligible(batch, n, m, kron_pn) &&
-      (reinterpret_cast<uintptr_t>(sv) & 15) == 0) {
+      (reinterpret_cast<uintptr_t>(sv) & (sbits ? 3 : 15)) == 0) {
     FusedJobDesc d{};
     d.codes0 = codes0;
     d.codes1 = codes1;
@@ -895,7 +907,8 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
     d.counter = reinterpret_cast<unsigned*>(ws);
     d.xmul = reinterpret_cast<float*>(ws + W.xmul);
     d.y1p = reinterpret_cast<float*>(ws + W.y1p);
-    rc = launch_linear_fused(x, x_dtype, ldx, (int)batch, (int)n, kron_pn, kron_n, y_dtype, 1, &d, W.S, W.SG, W.W,
+    rc = launch_linear_fused(x, x_dtype, ldx, (int)batch, (int)n, kron_pn, kron_n, y_dtype, sbits, 1, &d, W.S, W.SG,
+                             W.W,
                              cu_count(), s, reinterpret_cast<hipEvent_t>(mv_begin),
                              reinterpret_cast<hipEvent_t>(mv_end));
     if (rc) return rc;
@@ -908,7 +921,7 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
   }
   return forward_batched(x, x_dtype, ldx, batch, n, m, codes0, codes1, kind1, layout, sv, su, kron_pn, kron_n,
                          kron_pm, kron_m, s0, s1, layer_scale, bias, y, y_dtype, ldy, ws, W, mv_begin, mv_end, s,
-                         false);
+                         false, sbits);
 }
 
 // Grouped workspace.  First the one-launch kernel's data (1-2 rows), at
@@ -950,7 +963,7 @@ size_t group_prefix_bytes(int count, int64_t n, M m_of) {
 // whole-row output kernel).  Bit-identical to one qs_linear_forward per linear.
 static int forward_group_rows(const void* x, int x_dtype, int64_t ldx, int64_t batch, int64_t n, int kron_pn,
                               const float* kron_n, int count, const qs_linear_job* jobs, int y_dtype, char* ws,
-                              void* mv_begin, void* mv_end, hipStream_t s) {
+                              void* mv_begin, void* mv_end, hipStream_t s, int sbits) {
   const bool wide = batch >= kWideMinBatch;
   BatchedPass P[QS_MAX_GROUP];
   size_t off = group_prefix_bytes(count, n, [&](int g) { return jobs[g].m; });
@@ -989,6 +1002,7 @@ static int forward_group_rows(const void* x, int x_dtype, int64_t ldx, int64_t b
     Q.xmul = reinterpret_cast<float*>(ws + off + W.xmul);
     Q.y1p = reinterpret_cast<float*>(ws + off + W.y1p);
     Q.frag = 1;
+    Q.sbits = sbits;
     off += W.total;
   }
   int rc = launch_bx_group(P, count, s);
@@ -1065,10 +1079,15 @@ extern "C" int qs_linear_forward_group(const void* x, int x_dtype, int64_t ldx, 
     QS_REQUIRE(j.m > 0 && j.m % 16 == 0 && j.ldy >= j.m, "job %d: bad m %lld / ldy", g, (long long)j.m);
     rc = check_transform(j.m, j.kron_pm, j.kron_m, "output");
     if (rc) return rc;
+    QS_REQUIRE((j.sign_bits != 0) == (jobs[0].sign_bits != 0), "all jobs need the same sign format");
     QS_REQUIRE((reinterpret_cast<uintptr_t>(j.codes0) & 15) == 0 &&
                    (!j.codes1 || (reinterpret_cast<uintptr_t>(j.codes1) & 7) == 0) &&
-                   (reinterpret_cast<uintptr_t>(j.sv) & 15) == 0,
-               "job %d: packed codes and sv must be 16-byte aligned", g);
+                   (reinterpret_cast<uintptr_t>(j.sv) & (j.sign_bits ? 3 : 15)) == 0 &&
+                   (reinterpret_cast<uintptr_t>(j.su) & 3) == 0,
+               "job %d: packed codes and sv must be 16-byte aligned (4 bytes for sign bits)", g);
+    if (j.sign_bits)
+      QS_SUPPORTED(chunk_transform_fits(j.m, j.kron_pm),
+                   "job %d: packed sign bits need m on the chunk scheme (got %lld)", g, (long long)j.m);
     QS_REQUIRE((j.codes1 != nullptr) == (jobs[0].codes1 != nullptr), "all jobs need the same number of stages");
     need += ws_layout(j.m, n, batch, QS_LAYOUT_TILED).total;
   }
@@ -1078,7 +1097,7 @@ extern "C" int qs_linear_forward_group(const void* x, int x_dtype, int64_t ldx, 
   char* ws = static_cast<char*>(workspace);
   if (!fused_eligible(batch, n, jobs[0].m, kron_pn))
     return forward_group_rows(x, x_dtype, ldx, batch, n, kron_pn, kron_n, count, jobs, y_dtype, ws, mv_begin, mv_end,
-                              s);
+                              s, jobs[0].sign_bits ? 1 : 0);
   FusedJobDesc d[QS_MAX_GROUP];
   const WsLayout W0 = ws_layout(jobs[0].m, n, batch, QS_LAYOUT_TILED);
   size_t off = 0, off2 = 0;  // the job's block; its two-row area
@@ -1106,7 +1125,8 @@ extern "C" int qs_linear_forward_group(const void* x, int x_dtype, int64_t ldx, 
     off += F.total;
     off2 += F.two_rows;
   }
-  rc = launch_linear_fused(x, x_dtype, ldx, (int)batch, (int)n, kron_pn, kron_n, y_dtype, count, d, W0.S, W0.SG,
+  rc = launch_linear_fused(x, x_dtype, ldx, (int)batch, (int)n, kron_pn, kron_n, y_dtype, jobs[0].sign_bits ? 1 : 0,
+                           count, d, W0.S, W0.SG,
                            W0.W, cu_count(), s, reinterpret_cast<hipEvent_t>(mv_begin),
                            reinterpret_cast<hipEvent_t>(mv_end));
   if (rc) return rc;

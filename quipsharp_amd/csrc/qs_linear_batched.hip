@@ -55,6 +55,7 @@ struct BxArgs {
   const float* Kn;
   float scale_n;
   int frag;       // x2h and sg fragment-major (wide GEMM operands; sg / 4)
+  int sbits;      // sv of every linear is packed sign bits
   int per;        // work-groups per linear: linear blockIdx / per
   BxJob job[QS_MAX_GROUP];
 };
@@ -76,7 +77,7 @@ inline int chunks_per_wave(int64_t S) { return S <= kWaves ? 1 : S <= 2 * kWaves
 
 // Rows b = lb, lb + per, ... of linear blockIdx / per (lb = blockIdx % per):
 // the next row's activations are loaded while this row is transformed.
-template <int CPW>
+template <int CPW, bool SB>
 __global__ __launch_bounds__(kThreads) void bx_kernel(BxArgs A) {
   using L = RowLds<CPW>;
   extern __shared__ __attribute__((aligned(16))) char lds[];
@@ -88,7 +89,7 @@ __global__ __launch_bounds__(kThreads) void bx_kernel(BxArgs A) {
   const int lane = tid & 63, w = tid >> 6;
   const int q = lane >> 4, r16 = lane & 15;
   const LaneX lx = lane_x_init();
-  const XSource X{A.x, A.x_dtype, A.x_vec, A.ldx, A.Sn};
+  const XSource X{A.x, A.x_dtype, A.x_vec, A.ldx, A.Sn, SB ? 1 : 0};
   const int stride = A.per;
   const int g = (int)blockIdx.x / A.per, lb = (int)blockIdx.x - g * A.per;
   const BxJob& J = A.job[g];
@@ -102,7 +103,7 @@ __global__ __launch_bounds__(kThreads) void bx_kernel(BxArgs A) {
   }
   for (int b = lb; b < A.B; b += stride) {
     float xv[CPW][4];
-    finish_x(X, xr, w, xv);
+    finish_x(X, xr, w, lane, xv);
     if (b + stride < A.B) load_x_raw(X, J.sv, b + stride, w, lane, xr);  // the next row
     float ss = 0.0f;
 #pragma unroll
@@ -369,6 +370,7 @@ struct ByJob {
 struct ByArgs {
   int B;
   int y_dtype;
+  int sbits;  // su of every linear is packed sign bits
   int njobs;
   ByJob job[QS_MAX_GROUP];
 };
@@ -380,7 +382,7 @@ struct ByArgs {
 // alongside su and bias, and are loaded per row, all groups at once); G == 0
 // sums any number of groups one at a time.  A linear with fewer groups than G
 // adds zeros.  CPW: chunks per wave, as bx_kernel.
-template <int G, int CPW>
+template <int G, int CPW, bool SB>
 __global__ __launch_bounds__(kThreads) void by_kernel(ByArgs A) {
   using L = RowLds<CPW>;
   extern __shared__ __attribute__((aligned(16))) char lds[];
@@ -409,7 +411,9 @@ __global__ __launch_bounds__(kThreads) void by_kernel(ByArgs A) {
   if constexpr (G == 1) load_partials_raw<false, 1>(J.y1p, J.m, Sm, J.SG, A.B, lb, w, lane, pr);
   int oidx[CPW][4];
   float suo[CPW][4], bio[CPW][4];
-  const float* const bsrc = J.bias ? J.bias : J.su;
+  // no bias: a dummy load (times 0) from the partial sums, which hold m
+  // floats; su may be m / 32 words of sign bits
+  const float* const bsrc = J.bias ? J.bias : J.y1p;
   const float bsel = J.bias ? 1.0f : 0.0f;
 #pragma unroll
   for (int a = 0; a < CPW; ++a)
@@ -418,7 +422,7 @@ __global__ __launch_bounds__(kThreads) void by_kernel(ByArgs A) {
       const int r = 16 * a + 4 * q + j;
       oidx[a][j] = r < Sm ? 256 * r + t : -1;
       const int ii = oidx[a][j] >= 0 ? oidx[a][j] : 0;
-      suo[a][j] = J.su[ii];
+      suo[a][j] = load_su(J.su, SB, ii);
       bio[a][j] = bsrc[ii];
     }
   mmat_store(kmv, Sm, J.lsh_m, Mh, Ml, tid);
@@ -452,7 +456,8 @@ __global__ __launch_bounds__(kThreads) void by_kernel(ByArgs A) {
 #pragma unroll
     for (int a = 0; a < CPW; ++a)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) out[a][j] = acc[a][j] * mul * suo[a][j] + bsel * bio[a][j];
+      for (int j = 0; j < 4; ++j)
+        out[a][j] = apply_su(acc[a][j] * mul, suo[a][j], SB, oidx[a][j]) + bsel * bio[a][j];
     store_outputs(J.y, A.y_dtype, (int64_t)b * J.ldy, oidx, out);
     __syncthreads();  // Y is rewritten for the next row
   }
@@ -495,34 +500,42 @@ int check_bm_lds() {
   return rc;
 }
 
-template <int CPW>
-int launch_bx_cpw(const BxArgs& X, unsigned grid, hipStream_t stream) {
+template <int CPW, bool SB>
+int launch_bx_cs(const BxArgs& X, unsigned grid, hipStream_t stream) {
   static int done = 0;
-  const int rc = lds_checked((const void*)bx_kernel<CPW>, RowLds<CPW>::kTotal, &done);
+  const int rc = lds_checked((const void*)bx_kernel<CPW, SB>, RowLds<CPW>::kTotal, &done);
   if (rc) return rc;
-  hipLaunchKernelGGL(bx_kernel<CPW>, dim3(grid), dim3(kThreads), RowLds<CPW>::kTotal, stream, X);
+  hipLaunchKernelGGL((bx_kernel<CPW, SB>), dim3(grid), dim3(kThreads), RowLds<CPW>::kTotal, stream, X);
   QS_LAUNCHED("bx_kernel");
   return QS_OK;
 }
 
-template <int G, int CPW>
+template <int G, int CPW, bool SB>
 int launch_by_gc(const ByArgs& Y, unsigned grid, hipStream_t stream) {
   static int done = 0;
-  const int rc = lds_checked((const void*)by_kernel<G, CPW>, RowLds<CPW>::kTotal, &done);
+  const int rc = lds_checked((const void*)by_kernel<G, CPW, SB>, RowLds<CPW>::kTotal, &done);
   if (rc) return rc;
-  hipLaunchKernelGGL((by_kernel<G, CPW>), dim3(grid), dim3(kThreads), RowLds<CPW>::kTotal, stream, Y);
+  hipLaunchKernelGGL((by_kernel<G, CPW, SB>), dim3(grid), dim3(kThreads), RowLds<CPW>::kTotal, stream, Y);
   QS_LAUNCHED("by_kernel");
   return QS_OK;
 }
 
 // With one partial group the next row's sums are prefetched (by_kernel<1>);
 // up to 3 or 4 groups are loaded together; more, one group at a time.
+template <int CPW, bool SB>
+int launch_by_cs(const ByArgs& Y, unsigned grid, int maxsg, hipStream_t stream) {
+  if (maxsg == 1) return launch_by_gc<1, CPW, SB>(Y, grid, stream);
+  if (maxsg <= kMaxSG) return launch_by_gc<kMaxSG, CPW, SB>(Y, grid, stream);
+  if (maxsg <= 4) return launch_by_gc<4, CPW, SB>(Y, grid, stream);
+  return launch_by_gc<0, CPW, SB>(Y, grid, stream);
+}
+template <int CPW>
+int launch_bx_cpw(const BxArgs& X, unsigned grid, hipStream_t stream) {
+  return X.sbits ? launch_bx_cs<CPW, true>(X, grid, stream) : launch_bx_cs<CPW, false>(X, grid, stream);
+}
 template <int CPW>
 int launch_by_cpw(const ByArgs& Y, unsigned grid, int maxsg, hipStream_t stream) {
-  if (maxsg == 1) return launch_by_gc<1, CPW>(Y, grid, stream);
-  if (maxsg <= kMaxSG) return launch_by_gc<kMaxSG, CPW>(Y, grid, stream);
-  if (maxsg <= 4) return launch_by_gc<4, CPW>(Y, grid, stream);
-  return launch_by_gc<0, CPW>(Y, grid, stream);
+  return Y.sbits ? launch_by_cs<CPW, true>(Y, grid, maxsg, stream) : launch_by_cs<CPW, false>(Y, grid, maxsg, stream);
 }
 
 }  // namespace
@@ -547,12 +560,13 @@ int launch_bx_group(const BatchedPass* P, int count, hipStream_t stream) {
   X.Kn = P0.Kn;
   X.scale_n = inv_sqrt_len((int)(P0.n / P0.pn));
   X.frag = P0.frag;
+  X.sbits = P0.sbits;
   const int cpw = chunks_per_wave(X.Sn);
   X.per = (int)row_grid(P0.B, P0.ncu * row_wgs_per_cu(cpw) / count);
   for (int j = 0; j < count; ++j) {
     const BatchedPass& Q = P[j];
     QS_REQUIRE(Q.x == P0.x && Q.x_dtype == P0.x_dtype && Q.ldx == P0.ldx && Q.B == P0.B && Q.n == P0.n &&
-                   Q.pn == P0.pn && Q.Kn == P0.Kn && Q.frag == P0.frag,
+                   Q.pn == P0.pn && Q.Kn == P0.Kn && Q.frag == P0.frag && Q.sbits == P0.sbits,
                "input transform: linears of one launch share x and its transform");
     X.job[j] = BxJob{Q.sv, Q.x2h, Q.sg, Q.xmul};
   }
@@ -571,6 +585,7 @@ int launch_by_group(const BatchedPass* P, int count, hipStream_t stream) {
   ByArgs Y{};
   Y.B = P[0].B;
   Y.y_dtype = P[0].y_dtype;
+  Y.sbits = P[0].sbits;
   Y.njobs = count;
   int maxsg = 1, cpw = 1;
   for (int j = 0; j < count; ++j)
@@ -580,7 +595,8 @@ int launch_by_group(const BatchedPass* P, int count, hipStream_t stream) {
     const BatchedPass& Q = P[j];
     QS_REQUIRE(chunk_transform_fits(Q.m, Q.pm), "output transform: m outside the chunk scheme");
     QS_REQUIRE(Q.SG >= 1 && Q.SG <= kWideMaxGroups, "output transform: 1..%d partial groups", kWideMaxGroups);
-    QS_REQUIRE(Q.B == Y.B && Q.y_dtype == Y.y_dtype, "output transform: linears of one launch share rows and dtype");
+    QS_REQUIRE(Q.B == Y.B && Q.y_dtype == Y.y_dtype && Q.sbits == Y.sbits,
+               "output transform: linears of one launch share rows, dtype and sign format");
     ByJob& J = Y.job[j];
     J.y1p = Q.y1p;
     J.xmul = Q.xmul;

@@ -25,7 +25,7 @@ struct FusedJobDesc {
 };
 
 int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, int pn, const float* Kn, int y_dtype,
-                        int count, const FusedJobDesc* jobs, int S, int SG, int W, int ncu, hipStream_t stream,
+                        int sbits, int count, const FusedJobDesc* jobs, int S, int SG, int W, int ncu, hipStream_t stream,
                         hipEvent_t ev_start, hipEvent_t ev_stop);
 bool fused_eligible(int64_t batch, int64_t n, int64_t m, int pn);
 bool fused_output_in_kernel(int64_t m, int pm);
@@ -53,6 +53,7 @@ struct BatchedPass {
   int S, SG, W, ncu;     // slices, slice groups, waves per group, CUs
   _Float16* x2h;         // workspace: [B][n] fp16 operand (fragment-major with frag)
   _Float16* sg;          // workspace: [B][n / 8] group sums (fragment-major / 4 with frag)
+  int sbits;             // sv and su are packed sign bits (QS_SIGNS_BITS)
   int frag;              // input transform writes x2h and sg fragment-major (the order the decode-matvec
                          // and the wide GEMM read; the decode-matvec requires it)
   float* xmul;           // workspace: [B]

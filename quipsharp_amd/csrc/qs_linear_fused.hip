@@ -82,6 +82,7 @@ struct FusedArgs {
   float scale_n;
   int S, SG, W;
   int y_dtype;
+  int sbits;  // su, sv of every job are packed sign bits
   int njobs;
   FusedJob job[kMaxJobs];
 };
@@ -113,7 +114,7 @@ static_assert(kRedSlots * 16 * kMaxB * 4 == kThreads && kRedSlots * 16 * 8 == kT
               "one reduction pass: 8 threads per output at B = 1, 4 at B = 2");
 
 
-template <bool HAS2>
+template <bool HAS2, bool SB>
 __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
   uint32_t* lut_hi = reinterpret_cast<uint32_t*>(lds + kOffHi);
@@ -147,7 +148,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   // 1. loads: the activations first (the transform waits for them), then the
   //    abs table and K; the code tiles once the activations are in.  The
   //    LUTs are built from the table while the activations are in flight.
-  const XSource X{A.x, A.x_dtype, A.x_vec, A.ldx, A.Sn};
+  const XSource X{A.x, A.x_dtype, A.x_vec, A.ldx, A.Sn, SB ? 1 : 0};
   XRaw xr;
   load_x_raw(X, J.sv, 0, w, lane, xr);
   uint4 trow = make_uint4(0, 0, 0, 0), t1row = make_uint4(0, 0, 0, 0);  // fp16 table rows
@@ -166,7 +167,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   __syncthreads();  // staged table complete
   fill_luts(tab16, lut_hi, lut_lo, tid);
   float xv[kCPW][4];
-  finish_x(X, xr, w, xv);
+  finish_x(X, xr, w, lane, xv);
   // Code tiles stream through a ring of kPrefetch registers, refilled as
   // they are consumed.  The loads are unconditional (a tile past the end or
   // of an idle wave reads tile 0 instead) and the ring is unrolled, so the
@@ -378,7 +379,9 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
     load_partials<true>(J.y1p, J.m, Sm, A.SG, A.B, 0, w, lane, zv);
     int oidx[3][4];
     float suo[3][4], bio[3][4];
-    const float* const bsrc = J.bias ? J.bias : J.su;
+    // no bias: a dummy load (times 0) from the partial sums, which hold m
+    // floats; su may be m / 32 words of sign bits
+    const float* const bsrc = J.bias ? J.bias : J.y1p;
     const float bsel = J.bias ? 1.0f : 0.0f;
 #pragma unroll
     for (int a = 0; a < 3; ++a)
@@ -387,7 +390,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
         const int r = 16 * a + 4 * q + j;
         oidx[a][j] = r < Sm ? 256 * r + t : -1;
         const int ii = oidx[a][j] >= 0 ? oidx[a][j] : 0;
-        suo[a][j] = J.su[ii];
+        suo[a][j] = load_su(J.su, SB, ii);
         bio[a][j] = bsrc[ii];
       }
     // M = K_p (x) H_{2^lsh_m} as bf16 hi / lo, zero-padded to 48 x 64
@@ -419,7 +422,8 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
 #pragma unroll
       for (int a = 0; a < 3; ++a)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) out[a][j] = acc[a][j] * mul * suo[a][j] + bsel * bio[a][j];
+        for (int j = 0; j < 4; ++j)
+          out[a][j] = apply_su(acc[a][j] * mul, suo[a][j], SB, oidx[a][j]) + bsel * bio[a][j];
       store_outputs(yp, ydt, (int64_t)b * ldy, oidx, out);
     }
   }
@@ -431,8 +435,27 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
 // Host launcher used by qs_linear_forward and qs_linear_forward_group
 // (qs_linear.hip).  The CUs are shared between the linears in proportion to
 // their rows; each linear's work-groups form a contiguous block of the grid.
+namespace {
+template <bool HAS2, bool SB>
+int launch_fused_variant(const FusedArgs& A, int wg, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop) {
+  static int attr_done = 0;
+  if (!attr_done) {
+    hipFuncAttributes fa{};
+    QS_HIP(hipFuncGetAttributes(&fa, (const void*)linear_fused_kernel<HAS2, SB>));
+    QS_REQUIRE(fa.sharedSizeBytes == 0, "linear_fused_kernel: static LDS would move the LUT off address 0");
+    QS_HIP(hipFuncSetAttribute((const void*)linear_fused_kernel<HAS2, SB>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                               kLdsBytes));
+    attr_done = 1;
+  }
+  hipExtLaunchKernelGGL((linear_fused_kernel<HAS2, SB>), dim3((unsigned)wg), dim3(kThreads), kLdsBytes, stream,
+                        ev_start, ev_stop, 0, A);
+  QS_LAUNCHED("linear_fused_kernel");
+  return QS_OK;
+}
+}  // namespace
+
 int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, int pn, const float* Kn, int y_dtype,
-                        int count, const FusedJobDesc* jobs, int S, int SG, int W, int ncu, hipStream_t stream,
+                        int sbits, int count, const FusedJobDesc* jobs, int S, int SG, int W, int ncu, hipStream_t stream,
                         hipEvent_t ev_start, hipEvent_t ev_stop) {
   QS_REQUIRE(count >= 1 && count <= kMaxJobs, "1..%d linears per launch", kMaxJobs);
   FusedArgs A{};
@@ -454,6 +477,7 @@ int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, i
   A.SG = SG;
   A.W = W;
   A.y_dtype = y_dtype;
+  A.sbits = sbits;
   A.njobs = count;
   int64_t mtot = 0;
   for (int g = 0; g < count; ++g) mtot += jobs[g].m;
@@ -493,27 +517,12 @@ int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, i
     J.y = d.y;
     J.ldy = d.ldy;
   }
-  static int attr_done = 0;
-  if (!attr_done) {
-    hipFuncAttributes fa{};
-    QS_HIP(hipFuncGetAttributes(&fa, (const void*)linear_fused_kernel<false>));
-    QS_REQUIRE(fa.sharedSizeBytes == 0, "linear_fused_kernel: static LDS would move the LUT off address 0");
-    QS_HIP(hipFuncGetAttributes(&fa, (const void*)linear_fused_kernel<true>));
-    QS_REQUIRE(fa.sharedSizeBytes == 0, "linear_fused_kernel: static LDS would move the LUT off address 0");
-    QS_HIP(hipFuncSetAttribute((const void*)linear_fused_kernel<false>,
-                               hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes));
-    QS_HIP(hipFuncSetAttribute((const void*)linear_fused_kernel<true>,
-                               hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes));
-    attr_done = 1;
+  if (has2) {
+    if (sbits) return launch_fused_variant<true, true>(A, wg, stream, ev_start, ev_stop);
+    return launch_fused_variant<true, false>(A, wg, stream, ev_start, ev_stop);
   }
-  if (has2)
-    hipExtLaunchKernelGGL(linear_fused_kernel<true>, dim3((unsigned)wg), dim3(kThreads), kLdsBytes, stream, ev_start,
-                          ev_stop, 0, A);
-  else
-    hipExtLaunchKernelGGL(linear_fused_kernel<false>, dim3((unsigned)wg), dim3(kThreads), kLdsBytes, stream,
-                          ev_start, ev_stop, 0, A);
-  QS_LAUNCHED("linear_fused_kernel");
-  return QS_OK;
+  if (sbits) return launch_fused_variant<false, true>(A, wg, stream, ev_start, ev_stop);
+  return launch_fused_variant<false, false>(A, wg, stream, ev_start, ev_stop);
 }
 
 bool fused_output_in_kernel(int64_t m, int pm) { return chunk_transform_fits(m, pm); }

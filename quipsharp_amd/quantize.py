@@ -161,6 +161,27 @@ class PackedCodes:
                                           self.codes1.element_size())
 
 
+def pack_signs(s: Tensor) -> Tensor:
+    """+-1 sign vector -> int32 words for the forward's packed-sign format
+    (QS_SIGNS_BITS): bit i % 32 of word i // 32 set where s[i] < 0.  A 32nd of
+    the fp32 bytes, which every work-group of the transforms reads."""
+    flat = s.reshape(-1)
+    n = flat.numel()
+    nw = (n + 31) // 32
+    neg = torch.zeros(nw * 32, dtype=torch.int64, device=s.device)
+    neg[:n] = (flat < 0).to(torch.int64)
+    w = (neg.view(nw, 32) << torch.arange(32, device=s.device)).sum(1)
+    return (w - ((w >= 2 ** 31).to(torch.int64) << 32)).to(torch.int32)  # two's-complement words
+
+
+def _sign_format(su: Tensor, sv: Tensor) -> bool:
+    """True for packed sign bits (int32 words), False for fp32 sign vectors."""
+    bits = su.dtype == torch.int32
+    if bits != (sv.dtype == torch.int32):
+        raise ValueError("su and sv must both be fp32 signs or both packed sign bits")
+    return bits
+
+
 def _out_rows(out: Tensor, B: int, m: int) -> Tensor:
     """``out`` as B rows of m outputs written in place: a (B, m) view with unit
     column stride (its row stride is passed to the library), never a copy."""
@@ -208,7 +229,8 @@ def forward_packed(x: Tensor, packed: PackedCodes, su: Tensor, sv: Tensor, s0: f
         workspace = torch.zeros(max(need, 256), dtype=torch.uint8, device=x.device)
     _lib.check(lib.qs_linear_forward(
         _lib.ptr(x2), _lib.dtype_code(x2.dtype), x2.stride(0), B, n, m, _lib.ptr(packed.codes0),
-        _lib.ptr(packed.codes1), packed.kind1, packed.layout, _lib.ptr(sv), _lib.ptr(su), fn[0], _lib.ptr(Kn),
+        _lib.ptr(packed.codes1), packed.kind1, packed.layout | (_lib.QS_SIGNS_BITS if _sign_format(su, sv) else 0),
+        _lib.ptr(sv), _lib.ptr(su), fn[0], _lib.ptr(Kn),
         fm[0], _lib.ptr(Km), float(s0), float(s1), float(layer_scale), _lib.ptr(bias), _lib.ptr(y),
         _lib.dtype_code(y.dtype), _ld(y, m), _lib.ptr(workspace), workspace.numel(),
         None if mv_events is None else _lib._vp(mv_events[0]), None if mv_events is None else _lib._vp(mv_events[1]),
@@ -285,7 +307,8 @@ def forward_packed_group(x: Tensor, linears, out_dtype=None, workspace: Tensor =
         jobs[g] = _lib.LinearJob(packed.codes0.data_ptr(), None if packed.codes1 is None else packed.codes1.data_ptr(),
                                  m, su.data_ptr(), sv.data_ptr(), fm[0], None if Km is None else Km.data_ptr(),
                                  float(s0), float(s1), float(layer_scale),
-                                 None if bias is None else bias.data_ptr(), y.data_ptr(), _ld(y, m) if B else m)
+                                 None if bias is None else bias.data_ptr(), y.data_ptr(), _ld(y, m) if B else m,
+                                 1 if _sign_format(su, sv) else 0)
         if packed.layout != _lib.QS_LAYOUT_TILED:
             raise ValueError("grouped forward needs the tiled code layout")
     if B == 0:

@@ -116,3 +116,19 @@ def test_out_rows_views_without_copy():
     assert y4.stride() == (40, 1) and _ld(y4, 16) == 40
     with pytest.raises(ValueError):
         _out_rows(torch.zeros(2, 3, 40)[:, :2, :16], 4, 16)  # (4, 16) only as a copy
+
+
+def test_pack_signs_words():
+    """Bit i % 32 of word i // 32 is set where s[i] < 0 (int32 two's complement),
+    the tail of the last word zero."""
+    import torch
+    from quipsharp_amd.quantize import pack_signs
+    rng = np.random.default_rng(3)
+    for n in (1, 31, 32, 33, 256, 4160):
+        s = rng.choice([-1.0, 1.0], n).astype(np.float32)
+        w = pack_signs(torch.from_numpy(s)).numpy().view(np.uint32)
+        assert w.shape == ((n + 31) // 32,)
+        bits = np.unpackbits(w.view(np.uint8), bitorder="little")
+        assert np.array_equal(bits[:n], (s < 0).astype(np.uint8))
+        assert not bits[n:].any()
+    assert pack_signs(torch.tensor([-1.0] * 32)).item() == -1

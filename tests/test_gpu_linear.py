@@ -496,3 +496,48 @@ def test_qwen25_7b_shapes(dev, m, n):
 def test_qwen3_32b_shapes(dev, m, n):
     """Qwen3-32B layer shapes (5120 = 5 x 1024, 25600 = 25 x 1024), batch 1 and 8."""
     _check_shape(dev, m, n, [1, 8], 1, m + 7 * n)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("m,n", [(4096, 4096), (11008, 4096), (4096, 11008), (1536, 768)])
+@pytest.mark.parametrize("B", [1, 2, 16, 24])
+def test_packed_sign_bits_bit_identical(dev, m, n, B):
+    """su / sv as packed sign bits (QS_SIGNS_BITS) give outputs bit-identical
+    to the fp32 sign vectors, single and grouped, on every path (one launch at
+    1-2 rows, the batched passes, the wide GEMM)."""
+    from quipsharp_amd.quantize import forward_packed, forward_packed_group, pack_signs
+    print(f"case: sign bits m={m} n={n} B={B}", flush=True)
+    rng = np.random.default_rng(77 + B)
+    lins = [_rand_linear(dev, rng, m, n, stages=s, bias=bool(s - 1)) for s in (1, 2)]
+    x = torch.from_numpy(rng.standard_normal((B, n)).astype(np.float32)).to(dev).bfloat16()
+    for lin in lins:
+        packed, su, sv, s0, s1, ls, bias = lin
+        bits = (packed, pack_signs(su), pack_signs(sv), s0, s1, ls, bias)
+        want = forward_packed(x, packed, su, sv, s0, s1, ls, bias)
+        got = forward_packed(x, packed, bits[1], bits[2], s0, s1, ls, bias)
+        assert torch.equal(got, want)
+        g_want = forward_packed_group(x, [lin, lin])
+        g_got = forward_packed_group(x, [bits, bits])
+        for a, b in zip(g_got, g_want):
+            assert torch.equal(a, b)
+        assert torch.equal(g_want[0], want)
+
+
+@pytest.mark.gpu
+def test_packed_sign_bits_rejected_outside_chunk_scheme(dev):
+    from quipsharp_amd._lib import QuipHipError
+    from quipsharp_amd.quantize import forward_packed, pack_signs
+    rng = np.random.default_rng(9)
+    packed, su, sv, s0, s1, ls, bias = _rand_linear(dev, rng, 13312, 1024)  # m = 52 chunks of 256, beyond 48
+    x = torch.randn(1, 1024, device=dev)
+    forward_packed(x, packed, su, sv, s0, s1, ls)
+    with pytest.raises(QuipHipError):
+        forward_packed(x, packed, pack_signs(su), pack_signs(sv), s0, s1, ls)
+    with pytest.raises(ValueError):
+        forward_packed(x, packed, pack_signs(su), sv, s0, s1, ls)
+    from quipsharp_amd.quantize import forward_packed_group
+    rng2 = np.random.default_rng(10)
+    a = _rand_linear(dev, rng2, 1024, 1024)
+    bits = (a[0], pack_signs(a[1]), pack_signs(a[2])) + a[3:]
+    with pytest.raises(QuipHipError, match="same sign format"):
+        forward_packed_group(x, [bits, a])
