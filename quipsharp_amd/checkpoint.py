@@ -120,34 +120,55 @@ class QuantizedLinear(nn.Module):
     def _load_from_state_dict(self, *args, **kwargs):
         self._packed = None
         self._bits_key = None
+        self._f32_cache = {}
         self._sib_out = None
         return super()._load_from_state_dict(*args, **kwargs)
 
     def _apply(self, fn, *args, **kwargs):
         self._packed = None
         self._bits_key = None
+        self._f32_cache = {}
         self._ws = None
         self._group_ws = None
         self._sib_out = None
         return super()._apply(fn, *args, **kwargs)
 
     def packed(self, kinds):
-        key = (self.codes.data_ptr(), self.codes.device, tuple(kinds))
+        # the tensor's identity and version too: a buffer replaced by
+        # assignment can reuse a freed block's address
+        key = (id(self.codes), self.codes.data_ptr(), self.codes._version, self.codes.device, tuple(kinds))
         if self._packed is None or self._packed_key != key:
             self._packed = PackedCodes(self.codes, self.out_features, self.in_features, kinds)
             self._packed_key = key
             self._scale_f = float(self.scale.item())
         return self._packed
 
+    def _fp32(self, name):
+        """Buffer ``name`` as float32 for the kernels.  After ``.half()`` or
+        ``.to(torch.bfloat16)`` su / sv / bias keep the module's dtype, as in the
+        reference, whose forward promotes them to fp32 at use
+        (quipsharp/checkpoint.py:141-146); the fp32 copy is made once per buffer
+        version."""
+        t = getattr(self, name)
+        if t is None or t.dtype == torch.float32:
+            return t
+        cache = self.__dict__.setdefault("_f32_cache", {})
+        key = (id(t), t.data_ptr(), t._version, t.dtype)
+        hit = cache.get(name)
+        if hit is None or hit[0] != key:
+            hit = (key, t.float().contiguous())
+            cache[name] = hit
+        return hit[1]
+
     def signs(self):
         """(su, sv) for the forward: packed sign bits (a 32nd of the fp32 bytes,
         read by every work-group of the transforms) where both sizes fit the
         library's chunk scheme, else the fp32 vectors.  Packed once per sign
         buffer, outside graph capture."""
-        su, sv = self.su, self.sv
+        su, sv = self._fp32("su"), self._fp32("sv")
         if not all(d % 256 == 0 and d <= 12288 for d in (self.in_features, self.out_features)):
             return su, sv
-        key = (su.data_ptr(), su._version, sv.data_ptr(), sv._version)
+        key = (id(self.su), self.su.data_ptr(), self.su._version, id(self.sv), self.sv.data_ptr(), self.sv._version)
         if getattr(self, "_bits_key", None) != key:
             if torch.cuda.is_current_stream_capturing():
                 return su, sv
@@ -197,7 +218,7 @@ class QuantizedLinear(nn.Module):
         packed = self.packed(kinds)
         ws = self._workspace(x, packed)
         su, sv = self.signs()
-        return forward_packed(x, packed, su, sv, s0, s1, self._scale_f, bias=self.bias,
+        return forward_packed(x, packed, su, sv, s0, s1, self._scale_f, bias=self._fp32("bias"),
                               out_dtype=x.dtype, workspace=ws)
 
     def _workspace(self, x, packed):
@@ -274,9 +295,15 @@ def _grouped(x: Tensor, linears):
     n = x.shape[-1]
     rows = x.numel() // n
     jobs = []
-    for l in linears:
+    signs = [l.signs() for l in linears]
+    if not all(su.dtype == torch.int32 for su, _ in signs):
+        # one sign format per launch: packed bits only when every member has them
+        # (a member whose out_features is off the chunk scheme, or whose bits are
+        # stale under capture, has fp32 signs)
+        signs = [(l._fp32("su"), l._fp32("sv")) for l in linears]
+    for l, (su, sv) in zip(linears, signs):
         kinds, s0, s1 = _forward_params(l.codebook, l.num_stages)
-        jobs.append((l.packed(kinds), *l.signs(), s0, s1, l._scale_f, l.bias))
+        jobs.append((l.packed(kinds), su, sv, s0, s1, l._scale_f, l._fp32("bias")))
     lead = linears[0]
     ms = (ctypes.c_int64 * len(linears))(*[l.out_features for l in linears])
     need = _lib.lib().qs_linear_group_workspace_bytes(n, rows, len(linears), ms)

@@ -913,6 +913,8 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
                              reinterpret_cast<hipEvent_t>(mv_end));
     if (rc) return rc;
     if (fused_output_in_kernel(m, kron_pm)) return QS_OK;
+    // the output kernels below read su as m fp32 values
+    QS_REQUIRE(!sbits, "packed sign bits reached an fp32-sign output path (m %lld)", (long long)m);
     if (chunk_transform_fits(m, kron_pm))
       return launch_yout_chunk(d.y1p, W.SG, (int)batch, m, kron_pm, kron_m, nullptr, 0, d.xmul, s0, layer_scale, su,
                                bias, y, y_dtype, ldy, s);
@@ -1136,6 +1138,8 @@ extern "C" int qs_linear_forward_group(const void* x, int x_dtype, int64_t ldx, 
   for (int g = 0; g < count; ++g) {
     const qs_linear_job& j = jobs[g];
     if (fused_output_in_kernel(j.m, j.kron_pm)) continue;
+    // the output kernels below read su as m fp32 values
+    QS_REQUIRE(!j.sign_bits, "job %d: packed sign bits reached an fp32-sign output path (m %lld)", g, (long long)j.m);
     if (chunk_transform_fits(j.m, j.kron_pm)) {
       yc[nyc++] = yc_args(d[g].y1p, W0.SG, (int)batch, j.m, j.kron_pm, j.kron_m, nullptr, 0, d[g].xmul, j.s0,
                           j.layer_scale, j.su, j.bias, j.y, y_dtype, j.ldy);

@@ -411,10 +411,11 @@ __global__ __launch_bounds__(kThreads) void by_kernel(ByArgs A) {
   if constexpr (G == 1) load_partials_raw<false, 1>(J.y1p, J.m, Sm, J.SG, A.B, lb, w, lane, pr);
   int oidx[CPW][4];
   float suo[CPW][4], bio[CPW][4];
-  // no bias: a dummy load (times 0) from the partial sums, which hold m
-  // floats; su may be m / 32 words of sign bits
+  // no bias: a dummy load from the partial sums (at least m floats; su may
+  // be m / 32 words of sign bits), never used: the bias term is selected,
+  // not multiplied by 0, so a non-finite dummy cannot reach the output
   const float* const bsrc = J.bias ? J.bias : J.y1p;
-  const float bsel = J.bias ? 1.0f : 0.0f;
+  const bool has_bias = J.bias != nullptr;
 #pragma unroll
   for (int a = 0; a < CPW; ++a)
 #pragma unroll
@@ -457,7 +458,7 @@ __global__ __launch_bounds__(kThreads) void by_kernel(ByArgs A) {
     for (int a = 0; a < CPW; ++a)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        out[a][j] = apply_su(acc[a][j] * mul, suo[a][j], SB, oidx[a][j]) + bsel * bio[a][j];
+        out[a][j] = apply_su(acc[a][j] * mul, suo[a][j], SB, oidx[a][j]) + (has_bias ? bio[a][j] : 0.0f);
     store_outputs(J.y, A.y_dtype, (int64_t)b * J.ldy, oidx, out);
     __syncthreads();  // Y is rewritten for the next row
   }

@@ -379,10 +379,11 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
     load_partials<true>(J.y1p, J.m, Sm, A.SG, A.B, 0, w, lane, zv);
     int oidx[3][4];
     float suo[3][4], bio[3][4];
-    // no bias: a dummy load (times 0) from the partial sums, which hold m
-    // floats; su may be m / 32 words of sign bits
+    // no bias: a dummy load from the partial sums (at least m floats; su may
+    // be m / 32 words of sign bits), never used: the bias term is selected,
+    // not multiplied by 0, so a non-finite dummy cannot reach the output
     const float* const bsrc = J.bias ? J.bias : J.y1p;
-    const float bsel = J.bias ? 1.0f : 0.0f;
+    const bool has_bias = J.bias != nullptr;
 #pragma unroll
     for (int a = 0; a < 3; ++a)
 #pragma unroll
@@ -423,7 +424,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
       for (int a = 0; a < 3; ++a)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          out[a][j] = apply_su(acc[a][j] * mul, suo[a][j], SB, oidx[a][j]) + bsel * bio[a][j];
+          out[a][j] = apply_su(acc[a][j] * mul, suo[a][j], SB, oidx[a][j]) + (has_bias ? bio[a][j] : 0.0f);
       store_outputs(yp, ydt, (int64_t)b * ldy, oidx, out);
     }
   }

@@ -182,6 +182,37 @@ def _sign_format(su: Tensor, sv: Tensor) -> bool:
     return bits
 
 
+def check_linear_args(x: Tensor, m: int, n: int, su: Tensor, sv: Tensor, bias: Tensor = None,
+                      out: Tensor = None, workspace: Tensor = None) -> bool:
+    """Host-side checks of one linear's tensors before their pointers go to
+    the library, which reads su / sv as m / n fp32 values (or as packed sign
+    words), bias as m fp32 values and writes out / workspace on x's device.
+    Returns True for packed sign bits.  Raises ValueError on a tensor that
+    would make the kernels read or write out of bounds or on another device."""
+    dev = x.device
+    bits = _sign_format(su, sv)
+    for name, t, length in (("su", su, m), ("sv", sv, n)):
+        if t.device != dev:
+            raise ValueError(f"{name} is on {t.device}, x on {dev}")
+        if not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+        if bits:
+            if t.numel() < (length + 31) // 32:
+                raise ValueError(f"{name}: {t.numel()} sign words for {length} signs")
+        elif t.dtype != torch.float32 or t.numel() != length:
+            raise ValueError(f"{name} must be {length} float32 signs, got {t.numel()} x {t.dtype}")
+    if bias is not None:
+        if bias.device != dev or bias.dtype != torch.float32 or bias.numel() != m or not bias.is_contiguous():
+            raise ValueError(f"bias must be {m} contiguous float32 values on {dev}, got {bias.numel()} x "
+                             f"{bias.dtype} on {bias.device}")
+    if out is not None and out.device != dev:
+        raise ValueError(f"out is on {out.device}, x on {dev}")
+    if workspace is not None and (workspace.device != dev or not workspace.is_contiguous()
+                                  or workspace.dtype != torch.uint8):
+        raise ValueError(f"workspace must be a contiguous uint8 tensor on {dev}")
+    return bits
+
+
 def _out_rows(out: Tensor, B: int, m: int) -> Tensor:
     """``out`` as B rows of m outputs written in place: a (B, m) view with unit
     column stride (its row stride is passed to the library), never a copy."""
@@ -208,6 +239,9 @@ def forward_packed(x: Tensor, packed: PackedCodes, su: Tensor, sv: Tensor, s0: f
     m, n = packed.m, packed.n
     if x.shape[-1] != n:
         raise ValueError(f"expected last dim {n}, got {x.shape[-1]}")
+    bits = check_linear_args(x, m, n, su, sv, bias, out, workspace)
+    if packed.codes0.device != x.device:
+        raise ValueError(f"codes are on {packed.codes0.device}, x on {x.device}")
     out_dtype = out_dtype or x.dtype
     lead = x.shape[:-1]
     x2 = x.reshape(-1, n)
@@ -229,7 +263,7 @@ def forward_packed(x: Tensor, packed: PackedCodes, su: Tensor, sv: Tensor, s0: f
         workspace = torch.zeros(max(need, 256), dtype=torch.uint8, device=x.device)
     _lib.check(lib.qs_linear_forward(
         _lib.ptr(x2), _lib.dtype_code(x2.dtype), x2.stride(0), B, n, m, _lib.ptr(packed.codes0),
-        _lib.ptr(packed.codes1), packed.kind1, packed.layout | (_lib.QS_SIGNS_BITS if _sign_format(su, sv) else 0),
+        _lib.ptr(packed.codes1), packed.kind1, packed.layout | (_lib.QS_SIGNS_BITS if bits else 0),
         _lib.ptr(sv), _lib.ptr(su), fn[0], _lib.ptr(Kn),
         fm[0], _lib.ptr(Km), float(s0), float(s1), float(layer_scale), _lib.ptr(bias), _lib.ptr(y),
         _lib.dtype_code(y.dtype), _ld(y, m), _lib.ptr(workspace), workspace.numel(),
@@ -296,8 +330,14 @@ def forward_packed_group(x: Tensor, linears, out_dtype=None, workspace: Tensor =
     Kn = hartley_matrix(fn[0], x.device) if fn[0] > 1 else None
     jobs = (_lib.LinearJob * count)()
     ys = []
+    formats = set()
     for g, (packed, su, sv, s0, s1, layer_scale, bias) in enumerate(linears):
         m = packed.m
+        formats.add(check_linear_args(x, m, n, su, sv, bias, None if outs is None else outs[g], workspace))
+        if packed.codes0.device != x.device:
+            raise ValueError(f"linear {g}: codes are on {packed.codes0.device}, x on {x.device}")
+        if len(formats) > 1:
+            raise ValueError("all linears of a group pass their signs in one format (fp32 or packed bits)")
         fm = kron_factor(m)
         if fm is None:
             raise ValueError(f"m = {m} needs the form p * 2^k with odd p <= {_lib.QS_MAX_KRON}")
@@ -308,7 +348,7 @@ def forward_packed_group(x: Tensor, linears, out_dtype=None, workspace: Tensor =
                                  m, su.data_ptr(), sv.data_ptr(), fm[0], None if Km is None else Km.data_ptr(),
                                  float(s0), float(s1), float(layer_scale),
                                  None if bias is None else bias.data_ptr(), y.data_ptr(), _ld(y, m) if B else m,
-                                 1 if _sign_format(su, sv) else 0)
+                                 1 if True in formats else 0)
         if packed.layout != _lib.QS_LAYOUT_TILED:
             raise ValueError("grouped forward needs the tiled code layout")
     if B == 0:

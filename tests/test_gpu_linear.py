@@ -539,5 +539,17 @@ def test_packed_sign_bits_rejected_outside_chunk_scheme(dev):
     rng2 = np.random.default_rng(10)
     a = _rand_linear(dev, rng2, 1024, 1024)
     bits = (a[0], pack_signs(a[1]), pack_signs(a[2])) + a[3:]
-    with pytest.raises(QuipHipError, match="same sign format"):
+    with pytest.raises(ValueError, match="one format"):       # refused on the host
         forward_packed_group(x, [bits, a])
+    # and by the library itself, for callers of the C ABI
+    from quipsharp_amd import _lib
+    y = torch.empty(2, 1, 1024, device=dev)
+    jobs = (_lib.LinearJob * 2)()
+    for g, (lin, fmt) in enumerate(((bits, 1), (a, 0))):
+        jobs[g] = _lib.LinearJob(lin[0].codes0.data_ptr(), None, 1024, lin[1].data_ptr(), lin[2].data_ptr(), 1, None,
+                                 lin[3], lin[4], lin[5], None, y[g].data_ptr(), 1024, fmt)
+    ws = torch.zeros(1 << 20, dtype=torch.uint8, device=dev)
+    rc = _lib.lib().qs_linear_forward_group(_lib.ptr(x), _lib.QS_DTYPE_F32, 1024, 1, 1024, 1, None, 2, jobs,
+                                            _lib.QS_DTYPE_F32, _lib.ptr(ws), ws.numel(), None, None,
+                                            _lib.stream_of(x))
+    assert rc == 1 and b"same sign format" in _lib.lib().qs_last_error()
