@@ -174,6 +174,26 @@ int qs_linear_forward(const void *x, int x_dtype, int64_t ldx, int64_t batch, in
                       const float *bias, void *y, int y_dtype, int64_t ldy, void *workspace,
                       size_t workspace_bytes, void *mv_begin, void *mv_end, qs_stream_t stream);
 
+/* The forward of qs_linear_forward without a workspace argument, for callers
+ * that cannot allocate one (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * The workspace is a device array in the library's code object, one copy of
+ * QS_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; this entry
+ * point calls no hipMalloc / hipFree.  Shapes whose workspace
+ * (qs_linear_workspace_bytes) exceeds it return QS_ERR_UNSUPPORTED before
+ * anything is launched: decode batches (1..16 rows) of m, n up to 25600 fit,
+ * wide prefill batches generally do not.  Every call on one GPU shares that
+ * GPU's array: calls that may overlap on one GPU (other streams, other host
+ * threads) race and must be serialised by the caller.  The array is zero when
+ * loaded and every call leaves its completion counter (first 256 bytes) zero.
+ * Outputs are bit-identical to qs_linear_forward on the same inputs. */
+#define QS_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
+int qs_linear_forward_noalloc(const void *x, int x_dtype, int64_t ldx, int64_t batch, int64_t n, int64_t m,
+                              const void *codes0, const void *codes1, int kind1, int layout, const float *sv,
+                              const float *su, int kron_pn, const float *kron_n, int kron_pm,
+                              const float *kron_m, float s0, float s1, float layer_scale,
+                              const float *bias, void *y, int y_dtype, int64_t ldy, qs_stream_t stream);
+
 /* y = layer_scale * W_hat @ x for batch rows, no transforms: the decode-matvec
  * alone, for inputs already in the transformed basis (the reference's RFFT
  * layers, whose transforms run as FFTs: quipsharp/rfft.py:37-60 around

@@ -21,6 +21,7 @@ QS_SIGNS_BITS = 0x100  # layout flag: su / sv are packed sign bits
 QS_MAX_STAGES = 4
 QS_MAX_KRON = 64
 QS_MAX_GROUP = 4
+QS_NOALLOC_SCRATCH_BYTES = 8 << 20
 
 _vp = ctypes.c_void_p
 
@@ -56,6 +57,8 @@ _SIGNATURES = {
     "qs_linear_forward": ([_vp, _int, _i64, _i64, _i64, _i64, _vp, _vp, _int, _int, _vp, _vp, _int, _vp,
                            _int, _vp, _f32, _f32, _f32, _vp, _vp, _int, _i64, _vp, ctypes.c_size_t, _vp, _vp,
                            _vp], _int),
+    "qs_linear_forward_noalloc": ([_vp, _int, _i64, _i64, _i64, _i64, _vp, _vp, _int, _int, _vp, _vp, _int, _vp,
+                                   _int, _vp, _f32, _f32, _f32, _vp, _vp, _int, _i64, _vp], _int),
     "qs_decode_matvec": ([_vp, _int, _i64, _i64, _i64, _i64, _vp, _vp, _int, _int, _f32, _f32, _f32, _vp, _int,
                           _i64, _vp, ctypes.c_size_t, _vp], _int),
     "qs_linear_group_workspace_bytes": ([_i64, _i64, _int, ctypes.POINTER(ctypes.c_int64)], ctypes.c_size_t),

@@ -13,6 +13,7 @@
 // call takes: one launch for 1-2 rows (qs_linear_fused.hip), passes of 16
 // rows through the batched decode-matvec (qs_linear_batched.hip), the wide
 // GEMM from kWideMinBatch rows (qs_linear_wide.hip).
+#include <atomic>
 #include <cmath>
 
 #include <hip/hip_ext.h>
@@ -924,6 +925,60 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
   return forward_batched(x, x_dtype, ldx, batch, n, m, codes0, codes1, kind1, layout, sv, su, kron_pn, kron_n,
                          kron_pm, kron_m, s0, s1, layer_scale, bias, y, y_dtype, ldy, ws, W, mv_begin, mv_end, s,
                          false, sbits);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free forward: the workspace lives in a file-scope device array
+// ---------------------------------------------------------------------------
+// `scratch` is part of the library's code object: each GPU the library runs
+// on holds one copy (QS_NOALLOC_SCRATCH_BYTES) from load until the process
+// ends, zero-filled at load.  Host code never passes the array's name to a
+// kernel (on the host it only names a stand-in): the device address comes
+// from hipGetSymbolAddress, looked up once per device with that device
+// current, and only that address is used.
+static __device__ __align__(256) char scratch[QS_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+
+// Device address of `scratch` on the current device.
+int scratch_address(void** out) {
+  int dev = 0;
+  QS_HIP(hipGetDevice(&dev));
+  QS_REQUIRE(dev >= 0 && dev < kMaxDevices, "device %d out of range", dev);
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    QS_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    QS_REQUIRE(p != nullptr, "no device address for the scratch array");
+    g_scratch_ptr[dev].store(p, std::memory_order_release);
+  }
+  *out = p;
+  return QS_OK;
+}
+}  // namespace
+
+extern "C" int qs_linear_forward_noalloc(const void* x, int x_dtype, int64_t ldx, int64_t batch, int64_t n,
+                                         int64_t m, const void* codes0, const void* codes1, int kind1, int layout,
+                                         const float* sv, const float* su, int kron_pn, const float* kron_n,
+                                         int kron_pm, const float* kron_m, float s0, float s1, float layer_scale,
+                                         const float* bias, void* y, int y_dtype, int64_t ldy, qs_stream_t stream) {
+  QS_REQUIRE(batch >= 0 && n > 0 && m > 0, "bad shape batch=%lld n=%lld m=%lld", (long long)batch, (long long)n,
+             (long long)m);
+  const int lay = layout & ~QS_SIGNS_BITS;
+  QS_REQUIRE(lay == QS_LAYOUT_TILED || lay == QS_LAYOUT_ROWMAJOR, "bad layout");
+  if (batch == 0) return QS_OK;
+  const size_t need = ws_layout(m, n, batch, lay).total;
+  QS_SUPPORTED(need <= QS_NOALLOC_SCRATCH_BYTES,
+               "qs_linear_forward_noalloc: m %lld, n %lld, %lld rows need %zu bytes of scratch; the "
+               "allocation-free forward has %zu (use qs_linear_forward with a workspace)",
+               (long long)m, (long long)n, (long long)batch, need, (size_t)QS_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc) return rc;
+  return qs_linear_forward(x, x_dtype, ldx, batch, n, m, codes0, codes1, kind1, layout, sv, su, kron_pn, kron_n,
+                           kron_pm, kron_m, s0, s1, layer_scale, bias, y, y_dtype, ldy, ws,
+                           QS_NOALLOC_SCRATCH_BYTES, nullptr, nullptr, stream);
 }
 
 // Grouped workspace.  First the one-launch kernel's data (1-2 rows), at
