@@ -405,10 +405,111 @@ __device__ __forceinline__ void load_partials(const float* y1p, int m, int Sm, i
   sum_partials(r, zv);
 }
 
+// Tagged partial sums.  Each work-group of a one-launch forward writes its
+// partial sums as 64-bit slots {fp32 value (low word), launch tag (high
+// word)} with one agent-scope store each, and the job's first work-group
+// polls the slots until every one carries this launch's tag: no completion
+// counter, no wait for the stores to complete before signalling.  The tag of
+// a launch is the workspace's epoch word plus one (zero skipped, so a zeroed
+// workspace matches no launch); the polling work-group stores it as the new
+// epoch at its end, after every slot of the launch has been read.
+__device__ __forceinline__ uint32_t next_tag(uint32_t epoch) { return epoch + 1u == 0u ? 1u : epoch + 1u; }
+
+__device__ __forceinline__ unsigned long long tagged(float v, uint32_t tag) {
+  return ((unsigned long long)tag << 32) | __float_as_uint(v);
+}
+
+// Bound on the polling rounds (each one a device-scope load round trip,
+// about a microsecond): a slot still missing after it reads as NaN, so a
+// failure shows in the output instead of keeping the GPU busy.
+constexpr int kMaxPolls = 1 << 20;
+
+// Polling the tagged partial sums of batch row b for the chunks
+// c = w + 16 u < Sm of this wave (element t = lane + 64 j, as
+// load_partials_raw), summed over the SG groups in ascending order once every
+// slot holds `tag`.  One group at a time (4 CPW slots per lane in flight).
+// poll_issue only issues the first group's loads, so that loads issued after
+// it share its round trip; poll_finish waits, reloads the slots that do not
+// carry the tag yet, and moves on to the next group.
+template <int CPW>
+struct PollState {
+  unsigned long long v[CPW][4];
+};
+template <int CPW>
+__device__ __forceinline__ void poll_load(const unsigned long long* y1t, int m, int Sm, int B, int b, int g, int w,
+                                          int lane, uint32_t tag, PollState<CPW>& p, bool only_missing) {
+  const unsigned long long fill = tagged(0.0f, tag);  // chunks past Sm: present, zero
+#pragma unroll
+  for (int u = 0; u < CPW; ++u) {
+    const int c = w + kWaves * u;
+    const unsigned long long* src = y1t + ((size_t)g * B + b) * m + 256 * c + lane;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (only_missing) {
+        if ((uint32_t)(p.v[u][j] >> 32) != tag)
+          p.v[u][j] = __hip_atomic_load(src + 64 * j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        p.v[u][j] = c < Sm ? __hip_atomic_load(src + 64 * j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : fill;
+      }
+    }
+  }
+}
+template <int CPW>
+__device__ __forceinline__ void poll_issue(const unsigned long long* y1t, int m, int Sm, int B, int b, int w,
+                                           int lane, uint32_t tag, PollState<CPW>& p) {
+  poll_load(y1t, m, Sm, B, b, 0, w, lane, tag, p, false);
+}
+template <int CPW>
+__device__ __forceinline__ void poll_finish(const unsigned long long* y1t, int m, int Sm, int SG, int B, int b,
+                                            int w, int lane, uint32_t tag, PollState<CPW>& p, float (&zv)[CPW][4]) {
+  for (int g = 0; g < SG; ++g) {
+    if (g > 0) poll_load(y1t, m, Sm, B, b, g, w, lane, tag, p, false);
+    for (int round = 0;; ++round) {
+      bool ok = true;
+#pragma unroll
+      for (int u = 0; u < CPW; ++u)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ok = ok && (uint32_t)(p.v[u][j] >> 32) == tag;
+      if (ok) break;
+      if (round == kMaxPolls) {
+#pragma unroll
+        for (int u = 0; u < CPW; ++u)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if ((uint32_t)(p.v[u][j] >> 32) != tag) p.v[u][j] = tagged(__builtin_nanf(""), tag);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+      poll_load(y1t, m, Sm, B, b, g, w, lane, tag, p, true);
+    }
+#pragma unroll
+    for (int u = 0; u < CPW; ++u)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float x = __uint_as_float((uint32_t)p.v[u][j]);
+        zv[u][j] = g == 0 ? x : zv[u][j] + x;
+      }
+  }
+}
+
 // su entry i for the output stage: the fp32 value, or with sign bits the raw
 // word holding bit i (kept as float bits; applied by apply_su at the end).
+// Element i of a buffer as a 32-bit byte offset from its (uniform) base: the
+// address is the scalar base plus one 32-bit vector register, instead of a
+// 64-bit vector address per element (which the compiler would otherwise keep
+// live, and spill, across the tail's polling loop).
+template <class T>
+__device__ __forceinline__ const T& at_off(const T* base, uint32_t i) {
+  return *reinterpret_cast<const T*>(reinterpret_cast<const char*>(base) + i * (uint32_t)sizeof(T));
+}
+template <class T>
+__device__ __forceinline__ T& at_off(T* base, uint32_t i) {
+  return *reinterpret_cast<T*>(reinterpret_cast<char*>(base) + i * (uint32_t)sizeof(T));
+}
+
 __device__ __forceinline__ float load_su(const float* su, int sbits, int i) {
-  return sbits ? __uint_as_float(reinterpret_cast<const uint32_t*>(su)[i >> 5]) : su[i];
+  return sbits ? __uint_as_float(at_off(reinterpret_cast<const uint32_t*>(su), (uint32_t)i >> 5))
+               : at_off(su, (uint32_t)i);
 }
 __device__ __forceinline__ float apply_su(float v, float suo, int sbits, int i) {
   return sbits ? flip_by_bit(v, __float_as_uint(suo), i & 31) : v * suo;
@@ -425,21 +526,21 @@ __device__ __forceinline__ void store_outputs(void* y, int dtype, int64_t base, 
     for (int a = 0; a < NA; ++a)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        if (idx[a][j] >= 0) p[idx[a][j]] = out[a][j];
+        if (idx[a][j] >= 0) at_off(p, (uint32_t)idx[a][j]) = out[a][j];
   } else if (dtype == QS_DTYPE_F16) {
     _Float16* p = static_cast<_Float16*>(y) + base;
 #pragma unroll
     for (int a = 0; a < NA; ++a)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        if (idx[a][j] >= 0) p[idx[a][j]] = (_Float16)out[a][j];
+        if (idx[a][j] >= 0) at_off(p, (uint32_t)idx[a][j]) = (_Float16)out[a][j];
   } else {
     uint16_t* p = static_cast<uint16_t*>(y) + base;
 #pragma unroll
     for (int a = 0; a < NA; ++a)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        if (idx[a][j] >= 0) p[idx[a][j]] = f32_to_bf16(out[a][j]);
+        if (idx[a][j] >= 0) at_off(p, (uint32_t)idx[a][j]) = f32_to_bf16(out[a][j]);
   }
 }
 

@@ -41,7 +41,7 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 constexpr int kMaxParts = 16;  // work-groups per batch row for odd-factor transforms
 
 struct WsLayout {
-  size_t x2h, sg, xtot, xmul, x2, y1p, total;
+  size_t x2h, sg, xtot, xmul, x2, y1p, y1t, total;
   int S, SG, W;
   bool wide;
 };
@@ -76,8 +76,11 @@ int cu_count() {
   return cached[dev];
 }
 
-// The first 256 bytes of every workspace hold the fused kernel's completion
-// counter; it must be zero before the first call and every call leaves it zero.
+// The first 256 bytes of every workspace hold the one-launch kernel's epoch
+// (the tag of its last launch's partial sums; zero before the first call).
+// With the tiled layout the next region holds that kernel's tagged partial
+// sums (8 bytes per slot, up to two rows), which no other kernel writes, so a
+// slot can only carry a tag of an earlier launch of the same workspace.
 WsLayout ws_layout(int64_t m, int64_t n, int64_t batch, int layout) {
   WsLayout L{};
   L.wide = layout == QS_LAYOUT_TILED && batch >= kWideMinBatch;
@@ -87,6 +90,7 @@ WsLayout ws_layout(int64_t m, int64_t n, int64_t batch, int layout) {
     L.S = (int)(n / 256);
     L.SG = (L.S + kMaxWaves - 1) / kMaxWaves;
     L.W = (L.S + L.SG - 1) / L.SG;
+    L.y1t = off; off = align256(off + (size_t)L.SG * 2 * m * 8);
     const size_t xrows = (size_t)(B + 15) / 16 * 16;  // fragment-major rows: 16s
     L.x2h = off; off = align256(off + xrows * n * 2);
     L.sg = off; off = align256(off + xrows * (n / 8) * 2);
@@ -905,9 +909,10 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
     d.bias = bias;
     d.y = y;
     d.ldy = ldy;
-    d.counter = reinterpret_cast<unsigned*>(ws);
+    d.epoch = reinterpret_cast<unsigned*>(ws);
     d.xmul = reinterpret_cast<float*>(ws + W.xmul);
     d.y1p = reinterpret_cast<float*>(ws + W.y1p);
+    d.y1t = reinterpret_cast<unsigned long long*>(ws + W.y1t);
     rc = launch_linear_fused(x, x_dtype, ldx, (int)batch, (int)n, kron_pn, kron_n, y_dtype, sbits, 1, &d, W.S, W.SG,
                              W.W,
                              cu_count(), s, reinterpret_cast<hipEvent_t>(mv_begin),
@@ -981,35 +986,29 @@ extern "C" int qs_linear_forward_noalloc(const void* x, int x_dtype, int64_t ldx
                            QS_NOALLOC_SCRATCH_BYTES, nullptr, nullptr, stream);
 }
 
-// Grouped workspace.  First the one-launch kernel's data (1-2 rows), at
-// offsets that do not depend on the call's row count (a completion counter
-// must be zero whatever rows the previous call had; every call leaves it
-// zero): one block per job [counter | one row's worth of unused space |
-// row multipliers | one row of partial sums], then per job the partial sums
-// of a two-row call; then one ws_layout region per job for the kernels of
-// wider calls.  The one-row block keeps the spacing of the single-linear
-// layout: denser arrangements (counters in a block of their own, or beside
-// the partial sums) measured 0.7-1.1 % slower on the grouped 7B step.
+// Grouped workspace.  First one block per job for the one-launch kernel
+// (1-2 rows), at offsets that do not depend on the call's row count (the
+// job's epoch word must survive calls of any row count): [epoch | row
+// multipliers | tagged partial sums of up to two rows | fp32 partial sums of
+// up to two rows (output transform in a separate kernel)]; then one ws_layout
+// region per job for the kernels of wider calls.  Only one-launch calls of
+// the job write its tagged slots.
 struct FusedBlock {
-  size_t xmul, y1p, total;  // the counter at offset 0
-  size_t two_rows;          // bytes of a two-row partial-sum area
+  size_t xmul, y1t, y1p, total;  // the epoch at offset 0
 };
 FusedBlock fused_block(int64_t m, int64_t n) {
   const WsLayout W = ws_layout(m, n, 2, QS_LAYOUT_TILED);
   FusedBlock F{};
-  F.xmul = 256 + align256((size_t)n * 2) + align256((size_t)(n / 8) * 2) + align256((size_t)kMaxParts * 4);
-  F.y1p = F.xmul + 256;
-  F.total = F.y1p + align256((size_t)W.SG * (size_t)m * 4);
-  F.two_rows = align256((size_t)W.SG * 2 * (size_t)m * 4);
+  F.xmul = 256;
+  F.y1t = F.xmul + 256;
+  F.y1p = F.y1t + align256((size_t)W.SG * 2 * (size_t)m * 8);
+  F.total = F.y1p + align256((size_t)W.SG * 2 * (size_t)m * 4);
   return F;
 }
 template <class M>
 size_t group_prefix_bytes(int count, int64_t n, M m_of) {
   size_t total = 0;
-  for (int g = 0; g < count; ++g) {
-    const FusedBlock F = fused_block(m_of(g), n);
-    total += F.total + F.two_rows;
-  }
+  for (int g = 0; g < count; ++g) total += fused_block(m_of(g), n).total;
   return total;
 }
 
@@ -1157,8 +1156,7 @@ extern "C" int qs_linear_forward_group(const void* x, int x_dtype, int64_t ldx, 
                               s, jobs[0].sign_bits ? 1 : 0);
   FusedJobDesc d[QS_MAX_GROUP];
   const WsLayout W0 = ws_layout(jobs[0].m, n, batch, QS_LAYOUT_TILED);
-  size_t off = 0, off2 = 0;  // the job's block; its two-row area
-  for (int g = 0; g < count; ++g) off2 += fused_block(jobs[g].m, n).total;
+  size_t off = 0;  // the job's block
   for (int g = 0; g < count; ++g) {
     const qs_linear_job& j = jobs[g];
     const FusedBlock F = fused_block(j.m, n);
@@ -1176,11 +1174,11 @@ extern "C" int qs_linear_forward_group(const void* x, int x_dtype, int64_t ldx, 
     d[g].bias = j.bias;
     d[g].y = j.y;
     d[g].ldy = j.ldy;
-    d[g].counter = reinterpret_cast<unsigned*>(ws + off);
+    d[g].epoch = reinterpret_cast<unsigned*>(ws + off);
     d[g].xmul = reinterpret_cast<float*>(ws + off + F.xmul);
-    d[g].y1p = reinterpret_cast<float*>(ws + (batch == 1 ? off + F.y1p : off2));
+    d[g].y1p = reinterpret_cast<float*>(ws + off + F.y1p);
+    d[g].y1t = reinterpret_cast<unsigned long long*>(ws + off + F.y1t);
     off += F.total;
-    off2 += F.two_rows;
   }
   rc = launch_linear_fused(x, x_dtype, ldx, (int)batch, (int)n, kron_pn, kron_n, y_dtype, jobs[0].sign_bits ? 1 : 0,
                            count, d, W0.S, W0.SG,

@@ -19,9 +19,10 @@ struct FusedJobDesc {
   const float* bias;
   void* y;
   int64_t ldy;
-  unsigned* counter;    // workspace: completion counter (zero between calls)
+  unsigned* epoch;      // workspace: tag of the last launch's partial sums (zero before the first call)
   float* xmul;          // workspace: [B] activation scales
-  float* y1p;           // workspace: [SG][B][m] partial sums
+  float* y1p;           // workspace: [SG][B][m] fp32 partial sums (output transform in a separate kernel)
+  unsigned long long* y1t;  // workspace: [SG][B][m] tagged partial sums (output transform in the kernel)
 };
 
 int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, int pn, const float* Kn, int y_dtype,

@@ -23,18 +23,23 @@
 //      stage) into one of 8 LDS slots; every 8 row blocks (and after the
 //      last) the slots are reduced across the waves and the partial sums go
 //      to the workspace as write-through stores;
-//   4. completion: the stores are waited for, then one atomic per work-group
-//      on a counter; the last work-group reads the partials (write-through
-//      loads), applies S_u T_m(.) + bias with the same chunk scheme and
-//      resets the counter (every m of the scheme: m = p 2^k, 256 | m,
-//      m <= 12288).
+//   4. completion: the partial sums go out as 64-bit slots {value, launch
+//      tag}, one agent-scope store each, and the work-group is done; the
+//      job's first work-group, after its own row blocks, polls the slots until
+//      every one carries this launch's tag, then applies S_u T_m(.) + bias
+//      with the same chunk scheme (every m of the scheme: m = p 2^k, 256 | m,
+//      m <= 12288) and stores the tag as the workspace's new epoch.
 //
-// Cross-work-group visibility.  Partial sums are written with agent-scope
-// relaxed atomic stores and read with agent-scope relaxed atomic loads, which
-// on gfx950 are write-through / read-through at the device coherence point
-// (no per-XCD L2 copy is involved), and every work-group waits for its own
-// stores to complete (s_waitcnt) before its counter increment.  This avoids
-// an L2 write-back per wave that a device-scope fence would cost.
+// Cross-work-group visibility.  Slots are written with agent-scope relaxed
+// atomic stores and read with agent-scope relaxed atomic loads, which on
+// gfx950 are write-through / read-through at the device coherence point (no
+// per-XCD L2 copy is involved).  A 64-bit atomic store makes value and tag
+// visible together, so the reader needs no counter and the writers no wait
+// for their stores to complete (that wait plus a counter round trip cost
+// ~3 us per launch).  Only the polling work-group ever waits, and only for
+// work-groups that never wait themselves, so the launch cannot deadlock
+// whatever order its work-groups are dispatched in; the poll is bounded
+// (kMaxPolls, NaN outputs if exceeded).
 #include <hip/hip_ext.h>
 
 #include "qs_forward_dev.h"
@@ -58,8 +63,9 @@ struct FusedJob {
   const uint8_t* codes1;
   int m, Gr, wg0;      // rows; row-block stride; first work-group of this linear
   float s0, s1;
-  float* y1p;          // [SG][B][m]
-  unsigned* counter;   // zero between launches
+  float* y1p;          // [SG][B][m] fp32 partials (output transform in a separate kernel)
+  unsigned long long* y1t;  // [SG][B][m] tagged partials (output transform here)
+  unsigned* epoch;     // tag of the last launch (zero before the first)
   float* xmul;         // [B] 2^e per batch row (for a separate output kernel)
   int out_in_kernel;
   int Sm, lsh_m, pm;
@@ -114,7 +120,9 @@ static_assert(kRedSlots * 16 * kMaxB * 4 == kThreads && kRedSlots * 16 * 8 == kT
               "one reduction pass: 8 threads per output at B = 1, 4 at B = 2");
 
 
-template <bool HAS2, bool SB>
+// OCPW: output chunks of 256 per wave in the output transform (1: m <= 4096,
+// 3: m <= 12288), which sizes the registers the polling tail keeps live.
+template <bool HAS2, bool SB, int OCPW>
 __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
   uint32_t* lut_hi = reinterpret_cast<uint32_t*>(lds + kOffHi);
@@ -128,10 +136,10 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   _Float16* XS = reinterpret_cast<_Float16*>(lds + kOffXS);
   float* Y = reinterpret_cast<float*>(lds + kOffY);
   float* wsum = reinterpret_cast<float*>(lds + kOffMisc);
-  int& s_last = *reinterpret_cast<int*>(lds + kOffMisc + 4 * kWaves);
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, w = tid >> 6;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, in a scalar register
   const int q = lane >> 4, r16 = lane & 15;
   int g = 0;
 #pragma unroll
@@ -146,8 +154,11 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   const LaneX lx = lane_x_init();
 
   // 1. loads: the activations first (the transform waits for them), then the
-  //    abs table and K; the code tiles once the activations are in.  The
-  //    LUTs are built from the table while the activations are in flight.
+  //    abs table and K; the code tiles once the activations are in, then the
+  //    launch tag.  (The table staging below waits for every load issued so
+  //    far: the compiler cannot count the activation loads' conditional paths,
+  //    so issuing the table first would only delay the activations, and the
+  //    tag, read from the device coherence point, would delay the staging.)
   const XSource X{A.x, A.x_dtype, A.x_vec, A.ldx, A.Sn, SB ? 1 : 0};
   XRaw xr;
   load_x_raw(X, J.sv, 0, w, lane, xr);
@@ -174,11 +185,22 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   // compiler waits for exactly the tile in use, never for the whole ring.
   uint4 pre[kPrefetch];
   uint2 pre1[kPrefetch] = {};
-  // byte offset of this lane's 16 code bytes of row block rb (tile 0 past
-  // the end or for an idle wave); m n / 4 < 2^32 bytes of codes
+  // byte offset of this lane's 16 code bytes of row block rb; past the end,
+  // the work-group's own last row block again (an L2 hit, and spread over the
+  // chip: every wave of every work-group clamping to one tile made that tile's
+  // cache lines a hot spot), and the last slice for an idle wave.  jr < Gr <=
+  // RB, so rb_last is a valid row block; m n / 4 < 2^32 bytes of codes.
+  const int rb_last = jr + ((RB - 1 - jr) / J.Gr) * J.Gr;
+  const uint32_t slc = (uint32_t)(sl < A.S ? sl : A.S - 1);
   auto code_off = [&](int rb) -> uint32_t {
-    return ((active && rb < RB) ? ((uint32_t)rb * (uint32_t)A.S + (uint32_t)sl) * 1024u : 0u) + 16u * lane;
+    const uint32_t r = (uint32_t)(rb < RB ? rb : rb_last);
+    return (r * (uint32_t)A.S + slc) * 1024u + 16u * lane;
   };
+
+  // tag of this launch's partial sums, read (below, after the first code
+  // tiles) by every work-group before it stores any slot; the epoch only
+  // changes after every slot of the launch has been read
+  uint32_t epoch = 0;
 
   // 2. input transform, one batch row at a time, into fp16 operand rows
   float emul0 = 1.0f, emul1 = 1.0f;  // 2^e of batch rows 0 and 1
@@ -211,6 +233,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
         pre[k] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(J.codes0) + off);
         if (HAS2) pre1[k] = *reinterpret_cast<const uint2*>(J.codes1 + off / 2);
       }
+      if (J.out_in_kernel) epoch = __hip_atomic_load(J.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (b > 0) __syncthreads();  // the previous row's reads of Y are done
     store_chunks(Y, A.Sn, w, lane, xv);
@@ -270,6 +293,8 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   slice_shift += lane_xor<16>(slice_shift, lx);
   slice_shift += lane_xor<32>(slice_shift, lx);
   if (lb == 0 && tid < A.B) J.xmul[tid] = tid == 0 ? emul0 : emul1;
+
+  const uint32_t tag = J.out_in_kernel ? next_tag(epoch) : 0u;
 
   // 3. row blocks
   const int nw = A.S - sg * A.W < A.W ? A.S - sg * A.W : A.W;
@@ -346,8 +371,11 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
       if (tpo == 8) v += lane_xor<4>(v, lx);
       if (o < nout && part == 0) {
         const int rbs = rb - (slot - s) * J.Gr;  // row block of slot s
-        __hip_atomic_store(&J.y1p[((size_t)sg * A.B + bc) * J.m + rbs * 16 + row], v, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+        const size_t idx = ((size_t)sg * A.B + bc) * J.m + rbs * 16 + row;
+        if (J.out_in_kernel)
+          __hip_atomic_store(&J.y1t[idx], tagged(v, tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+          J.y1p[idx] = v;  // read by a separate output kernel after this one
       }
       __syncthreads();  // the slots are free again
     }
@@ -355,80 +383,93 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   }
   }
 
-  // 4. completion: the last work-group applies the output transform
-  if (!J.out_in_kernel) return;
-  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial-sum stores have completed
-  __syncthreads();
-  if (tid == 0)
-    s_last = __hip_atomic_fetch_add(J.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-             (unsigned)(J.Gr * A.SG - 1);
-  __syncthreads();
-  if (!s_last) return;
+  // 4. completion: the job's first work-group waits for every tagged
+  //    partial sum of this launch and applies the output transform
+  if (!J.out_in_kernel || lb != 0) return;
   {
     // Output chunk stage on the matrix cores (mstage_tile): lane (q, r16) of
     // wave w produces column t = 16 w + r16 of rows r = 16 a + 4 q + j.
     const int Sm = J.Sm;
     const int t = 16 * w + r16;
     // Loads, in the order they are waited for: the K entries of M (odd
-    // factor), the partial sums of batch row 0, su and bias; all in flight
+    // factor), the first partial-sum slots, su and bias, all in flight
     // together (unconditional loads from valid addresses, selected where they
     // are used: a load under a branch is waited for at the branch's end).
+    // With three output chunks per wave su and bias are loaded once the slots
+    // are in instead (their registers would not fit beside the slots); the
+    // transforms in between hide most of that round trip.
     float kmv[3];
     mmat_load(kmv, Sm, J.lsh_m, J.pm, J.Km, tid);
-    float zv[kCPW][4];
-    load_partials<true>(J.y1p, J.m, Sm, A.SG, A.B, 0, w, lane, zv);
-    int oidx[3][4];
-    float suo[3][4], bio[3][4];
-    // no bias: a dummy load from the partial sums (at least m floats; su may
-    // be m / 32 words of sign bits), never used: the bias term is selected,
-    // not multiplied by 0, so a non-finite dummy cannot reach the output
-    const float* const bsrc = J.bias ? J.bias : J.y1p;
+    float suo[OCPW][4], bio[OCPW][4];
+    // no bias: a dummy load from the partial-sum slots (at least m floats;
+    // su may be m / 32 words of sign bits), never used: the bias term is
+    // selected, not multiplied by 0, so a non-finite dummy cannot reach the
+    // output
+    const float* const bsrc = J.bias ? J.bias : reinterpret_cast<const float*>(J.y1t);
     const bool has_bias = J.bias != nullptr;
+    auto load_su_bias = [&]() {
 #pragma unroll
-    for (int a = 0; a < 3; ++a)
+      for (int a = 0; a < OCPW; ++a)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int r = 16 * a + 4 * q + j;
-        oidx[a][j] = r < Sm ? 256 * r + t : -1;
-        const int ii = oidx[a][j] >= 0 ? oidx[a][j] : 0;
-        suo[a][j] = load_su(J.su, SB, ii);
-        bio[a][j] = bsrc[ii];
-      }
+        for (int j = 0; j < 4; ++j) {
+          const int r = 16 * a + 4 * q + j;
+          const int ii = r < Sm ? 256 * r + t : 0;
+          suo[a][j] = load_su(J.su, SB, ii);
+          bio[a][j] = at_off(bsrc, (uint32_t)ii);
+        }
+    };
     // M = K_p (x) H_{2^lsh_m} as bf16 hi / lo, zero-padded to 48 x 64
     uint16_t* Mh = reinterpret_cast<uint16_t*>(lds + kOffMh);
     uint16_t* Ml = reinterpret_cast<uint16_t*>(lds + kOffMl);
-    mmat_store(kmv, Sm, J.lsh_m, Mh, Ml, tid);
     void* const yp = J.y;
     const int64_t ldy = J.ldy;
     const int ydt = A.y_dtype;
     const float mul0 = J.scale_m * J.layer_scale;
     const int nrt = (Sm + 15) >> 4, nkb = (Sm + 31) >> 5;
-    for (int b = 0; b < A.B; ++b) {
-      if (b > 0) load_partials<true>(J.y1p, J.m, Sm, A.SG, A.B, b, w, lane, zv);
+    // one batch row (B <= 2); called once per row rather than looped, so that
+    // no address arithmetic is hoisted out of a loop and kept live (and
+    // spilled) across the polling
+    auto row = [&](const int b) {
+      PollState<OCPW> ps;
+      poll_issue(J.y1t, J.m, Sm, A.B, b, w, lane, tag, ps);
+      if (b == 0) {
+        if (OCPW == 1) load_su_bias();
+        mmat_store(kmv, Sm, J.lsh_m, Mh, Ml, tid);  // waits for the K loads only
+      }
+      float zv[OCPW][4];
+      poll_finish(J.y1t, J.m, Sm, A.SG, A.B, b, w, lane, tag, ps, zv);
+      if (b == 0 && OCPW > 1) load_su_bias();
       h256_chunks(zv, Sm, lane, lx);
       if (b > 0) __syncthreads();  // the previous row's reads of Y are done
       store_chunks_lanes(Y, Sm, w, lane, zv);
       __syncthreads();  // chunks (and, the first time, M) complete
       const float mul = mul0 * (b == 0 ? emul0 : emul1);
-      floatx4 acc[3];
+      floatx4 acc[OCPW];
 #pragma unroll
-      for (int a = 0; a < 3; ++a) acc[a] = floatx4{0.f, 0.f, 0.f, 0.f};
+      for (int a = 0; a < OCPW; ++a) acc[a] = floatx4{0.f, 0.f, 0.f, 0.f};
       for (int kb = 0; kb < nkb; ++kb) {
         const ZOperand z = z_operand(Y, Sm, t, q, kb);
 #pragma unroll
-        for (int a = 0; a < 3; ++a)
+        for (int a = 0; a < OCPW; ++a)
           if (a < nrt) acc[a] = mstage_step(acc[a], Mh, Ml, 16 * a, z, kb, J.pm > 1, q, r16);
       }
-      float out[3][4];
+      float out[OCPW][4];
+      int oidx[OCPW][4];  // output element of out[a][j] (-1: none)
 #pragma unroll
-      for (int a = 0; a < 3; ++a)
+      for (int a = 0; a < OCPW; ++a)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 4; ++j) {
+          const int r = 16 * a + 4 * q + j;
+          oidx[a][j] = r < Sm ? 256 * r + t : -1;
           out[a][j] = apply_su(acc[a][j] * mul, suo[a][j], SB, oidx[a][j]) + (has_bias ? bio[a][j] : 0.0f);
+        }
       store_outputs(yp, ydt, (int64_t)b * ldy, oidx, out);
-    }
+    };
+    row(0);
+    if (A.B > 1) row(1);
   }
-  if (tid == 0) __hip_atomic_store(J.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // every slot of this launch has been read: the next launch's tag follows this one
+  if (tid == 0) __hip_atomic_store(J.epoch, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace
@@ -437,18 +478,18 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
 // (qs_linear.hip).  The CUs are shared between the linears in proportion to
 // their rows; each linear's work-groups form a contiguous block of the grid.
 namespace {
-template <bool HAS2, bool SB>
+template <bool HAS2, bool SB, int OCPW>
 int launch_fused_variant(const FusedArgs& A, int wg, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop) {
   static int attr_done = 0;
   if (!attr_done) {
     hipFuncAttributes fa{};
-    QS_HIP(hipFuncGetAttributes(&fa, (const void*)linear_fused_kernel<HAS2, SB>));
+    QS_HIP(hipFuncGetAttributes(&fa, (const void*)linear_fused_kernel<HAS2, SB, OCPW>));
     QS_REQUIRE(fa.sharedSizeBytes == 0, "linear_fused_kernel: static LDS would move the LUT off address 0");
-    QS_HIP(hipFuncSetAttribute((const void*)linear_fused_kernel<HAS2, SB>, hipFuncAttributeMaxDynamicSharedMemorySize,
+    QS_HIP(hipFuncSetAttribute((const void*)linear_fused_kernel<HAS2, SB, OCPW>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                kLdsBytes));
     attr_done = 1;
   }
-  hipExtLaunchKernelGGL((linear_fused_kernel<HAS2, SB>), dim3((unsigned)wg), dim3(kThreads), kLdsBytes, stream,
+  hipExtLaunchKernelGGL((linear_fused_kernel<HAS2, SB, OCPW>), dim3((unsigned)wg), dim3(kThreads), kLdsBytes, stream,
                         ev_start, ev_stop, 0, A);
   QS_LAUNCHED("linear_fused_kernel");
   return QS_OK;
@@ -502,7 +543,8 @@ int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, i
     J.s0 = d.s0;
     J.s1 = d.s1;
     J.y1p = d.y1p;
-    J.counter = d.counter;
+    J.y1t = d.y1t;
+    J.epoch = d.epoch;
     J.xmul = d.xmul;
     J.out_in_kernel = chunk_transform_fits(d.m, d.pm);
     if (J.out_in_kernel) {
@@ -518,12 +560,20 @@ int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, i
     J.y = d.y;
     J.ldy = d.ldy;
   }
-  if (has2) {
-    if (sbits) return launch_fused_variant<true, true>(A, wg, stream, ev_start, ev_stop);
-    return launch_fused_variant<true, false>(A, wg, stream, ev_start, ev_stop);
+  // output chunks per wave of the widest in-kernel output transform
+  int sm_max = 0;
+  for (int g = 0; g < count; ++g)
+    if (A.job[g].out_in_kernel && A.job[g].Sm > sm_max) sm_max = A.job[g].Sm;
+  if (sm_max <= kWaves) {
+    if (has2) return sbits ? launch_fused_variant<true, true, 1>(A, wg, stream, ev_start, ev_stop)
+                           : launch_fused_variant<true, false, 1>(A, wg, stream, ev_start, ev_stop);
+    return sbits ? launch_fused_variant<false, true, 1>(A, wg, stream, ev_start, ev_stop)
+                 : launch_fused_variant<false, false, 1>(A, wg, stream, ev_start, ev_stop);
   }
-  if (sbits) return launch_fused_variant<false, true>(A, wg, stream, ev_start, ev_stop);
-  return launch_fused_variant<false, false>(A, wg, stream, ev_start, ev_stop);
+  if (has2) return sbits ? launch_fused_variant<true, true, kCPW>(A, wg, stream, ev_start, ev_stop)
+                         : launch_fused_variant<true, false, kCPW>(A, wg, stream, ev_start, ev_stop);
+  return sbits ? launch_fused_variant<false, true, kCPW>(A, wg, stream, ev_start, ev_stop)
+               : launch_fused_variant<false, false, kCPW>(A, wg, stream, ev_start, ev_stop);
 }
 
 bool fused_output_in_kernel(int64_t m, int pm) { return chunk_transform_fits(m, pm); }

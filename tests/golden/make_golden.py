@@ -192,5 +192,60 @@ def main(ref_root):
     print("golden fixtures written to", OUT)
 
 
+def c1_full(ref_root):
+    """The full-size 4096x4096 E8P 2-bit quantize with the reference's recipe:
+    W = 0.02 N(0,1), H = X^T X / 2048 with X in R^{2048x4096}, x in R^4096,
+    all drawn from Generator().manual_seed(0) in that order; torch.manual_seed(0)
+    right before quantize_linear (su then sv from the global CPU RNG);
+    build_codebook("2bit", "cpu", 0); damping 1e-2, tune_iters 10
+    (quipsharp/quantize.py:48-104, ldlq.py:97-141, checkpoint.py:56-77).
+
+    Writes c1_full.npz: every code (u16 [4096, 512]) with its SHA-256,
+    layer_scale, y = linear_forward(x), the signs (int8), and the reference's
+    own relative proxy loss tr(E H E^T) / tr(W H W^T) in the transformed basis.
+    Takes ~20 minutes on 8 cores."""
+    import time
+    sys.path.insert(0, ref_root)
+    import torch
+    from quipsharp.checkpoint import build_codebook
+    from quipsharp.quantize import quantize_linear, linear_forward
+    from quipsharp.incoherence import incoherence_process
+
+    torch.set_num_threads(int(os.environ.get("C1_THREADS", "8")))
+    g = torch.Generator().manual_seed(0)
+    W = torch.randn(4096, 4096, generator=g) * 0.02
+    X = torch.randn(2048, 4096, generator=g)
+    H = X.T @ X / 2048
+    x = torch.randn(4096, generator=g)
+    cb, s = build_codebook("2bit", "cpu", 0)
+    t0 = time.time()
+    torch.manual_seed(0)
+    layer, what_q = quantize_linear(W, H, cb, g=8, damping=1e-2, codebook_scale=s, tune_iters=10)
+    t_q = time.time() - t0
+    y = linear_forward(x, layer, cb)
+    # proxy loss in the transformed basis (the basis BlockLDLQ minimizes in)
+    Hd = H + 1e-2 * H.diagonal().mean() * torch.eye(4096)
+    torch.manual_seed(0)
+    what, hhat, signs = incoherence_process(W, Hd)
+    assert torch.equal(signs.su, layer.signs.su) and torch.equal(signs.sv, layer.signs.sv)
+    E = (what_q - what).double()
+    Wd = what.double()
+    Hh = hhat.double()
+    proxy_rel = (torch.trace(E @ Hh @ E.T) / torch.trace(Wd @ Hh @ Wd.T)).item()
+    codes = layer.codes.numpy().astype(np.uint16)
+    np.savez_compressed(os.path.join(OUT, "c1_full.npz"), codes=codes,
+                        codes_sha256=np.frombuffer(hashlib.sha256(codes.tobytes()).digest(), np.uint8),
+                        layer_scale=np.float64(layer.scale), y=y.numpy(),
+                        su=layer.signs.su.numpy().astype(np.int8),
+                        sv=layer.signs.sv.numpy().astype(np.int8),
+                        proxy_rel=np.float64(proxy_rel), quantize_seconds=np.float64(t_q),
+                        threads=np.int32(torch.get_num_threads()))
+    print(f"c1_full.npz written: quantize {t_q:.0f} s, proxy_rel {proxy_rel:.5e}", flush=True)
+
+
 if __name__ == "__main__":
-    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
+    root = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
+    if len(sys.argv) > 2 and sys.argv[2] == "c1":
+        c1_full(root)
+    else:
+        main(root)
