@@ -161,9 +161,9 @@ size_t qs_linear_workspace_bytes(int64_t m, int64_t n, int64_t batch, int layout
  *   bias [m] fp32 or NULL
  * Activations enter the matrix cores as fp16 (per-row power-of-two scaled),
  * decoded weights are exact in fp16, accumulation is fp32.
- * The workspace must be zero before its first use (its first 256 bytes are a
- * completion counter that every call leaves at zero); calls that may run
- * concurrently need separate workspaces.
+ * The workspace must be zero before its first use (its first 256 bytes hold
+ * the epoch: the tag of the one-launch kernel's last partial sums, which each
+ * call advances); calls that may run concurrently need separate workspaces.
  * mv_begin / mv_end: optional hipEvent_t attached to the start of the first
  * and the end of the last decode-matvec kernel (hipExtLaunchKernelGGL start /
  * stop events, so the interval is kernel execution only; NULL: none). */
@@ -185,7 +185,7 @@ int qs_linear_forward(const void *x, int x_dtype, int64_t ldx, int64_t batch, in
  * wide prefill batches generally do not.  Every call on one GPU shares that
  * GPU's array: calls that may overlap on one GPU (other streams, other host
  * threads) race and must be serialised by the caller.  The array is zero when
- * loaded and every call leaves its completion counter (first 256 bytes) zero.
+ * loaded; every call advances the epoch in its first 256 bytes.
  * Outputs are bit-identical to qs_linear_forward on the same inputs. */
 #define QS_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
 int qs_linear_forward_noalloc(const void *x, int x_dtype, int64_t ldx, int64_t batch, int64_t n, int64_t m,

@@ -348,19 +348,37 @@ def is_quantized_checkpoint(path) -> bool:
     return (Path(path) / MANIFEST_NAME).exists()
 
 
-def load_quantized_checkpoint(save_path, model: nn.Module, device="cuda") -> nn.Module:
-    """quipsharp/checkpoint.py:193-275 for a caller-supplied architecture
-    skeleton (`model`, e.g. built with ``from_config`` on the meta device):
-    every manifest entry becomes an empty QuantizedLinear of the recorded
-    shape and transform, the saved state dict is loaded with ``assign=True``
-    through ``torch.load(weights_only=True)`` (tensors only, nothing executed
-    from the file), the model moves to ``device`` and each QuantizedLinear
-    gets the codebook rebuilt from the manifest's bits and seed.  (The
-    reference builds the skeleton from the hub model id and can spread layers
-    over several devices; both are outside this library.)"""
-    save_path = Path(save_path)
-    manifest = json.loads((save_path / MANIFEST_NAME).read_text())
-    state = torch.load(save_path / STATE_NAME, map_location="cpu", weights_only=True)
+def build_meta_model(model_id, save_path=None) -> nn.Module:
+    """The causal-LM architecture for ``model_id`` with its parameters on the
+    meta device, in the config's dtype (bf16 if it names none), as
+    quipsharp/lazy_weights.py:149-179 builds it: ``get_text_config()`` unwraps multimodal wrappers.  The config
+    comes from ``model_id`` when it is a local directory, else from
+    ``save_path`` when the checkpoint directory holds a config.json (a copy
+    saved beside the checkpoint, for machines without hub access), else from
+    the hub / local cache by id."""
+    from transformers import AutoConfig, AutoModelForCausalLM
+    if Path(str(model_id)).is_dir():
+        src = str(model_id)
+    elif save_path is not None and (Path(save_path) / "config.json").exists():
+        src = str(save_path)
+    else:
+        src = model_id
+    full_config = AutoConfig.from_pretrained(src)
+    text_config = full_config.get_text_config()
+    dtype = getattr(full_config, "dtype", None) or getattr(full_config, "torch_dtype", None) or torch.bfloat16
+    # parameters on the meta device, buffers real (non-persistent ones such as
+    # rotary frequencies are not in the saved state), as the reference's
+    # accelerate.init_empty_weights() does
+    from accelerate import init_empty_weights
+    with init_empty_weights():
+        model = AutoModelForCausalLM.from_config(text_config, dtype=dtype)
+    return model
+
+
+def install_quantized_placeholders(model: nn.Module, manifest: dict) -> None:
+    """Swaps an empty QuantizedLinear of the recorded shape, transform, stage
+    count and bias into ``model`` at every module the manifest lists
+    (quipsharp/checkpoint.py:216-223), ready for ``load_state_dict``."""
     stages = num_rvq_stages(manifest["bits"])
     for info in manifest["quantized_modules"]:
         parent_name, _, attr = info["name"].rpartition(".")
@@ -368,7 +386,37 @@ def load_quantized_checkpoint(save_path, model: nn.Module, device="cuda") -> nn.
         qlin = QuantizedLinear(info["in_features"], info["out_features"], manifest["block_size"],
                                info["transform_kind"], num_stages=stages, has_bias=info.get("has_bias", False))
         setattr(parent, attr, qlin)
+
+
+def load_quantized_checkpoint(save_path, device="cuda", gpu_devices=None, gpu_budget_bytes=None,
+                              cpu_budget_bytes=0, model: nn.Module = None) -> nn.Module:
+    """quipsharp/checkpoint.py:193-275, same call (quipsharp/model_loading.py:57
+    passes ``device``, ``gpu_devices``, ``gpu_budget_bytes``,
+    ``cpu_budget_bytes``): the architecture skeleton is built on the meta
+    device from the manifest's model id (``build_meta_model``; or pass
+    ``model``, a skeleton built by the caller), every manifest entry becomes an
+    empty QuantizedLinear of the recorded shape and transform, the saved state
+    dict is loaded with ``assign=True`` through ``torch.load(weights_only=True)``
+    (tensors only, nothing executed from the file), the model moves to
+    ``gpu_devices[0]`` (or ``device``) and each QuantizedLinear gets the
+    codebook rebuilt from the manifest's bits and seed.  A checkpoint larger
+    than ``gpu_budget_bytes``, which the reference spreads over several devices
+    with accelerate, raises NotImplementedError: this library runs on one GPU."""
+    save_path = Path(save_path)
+    manifest = json.loads((save_path / MANIFEST_NAME).read_text())
+    state = torch.load(save_path / STATE_NAME, map_location="cpu", weights_only=True)
+    total_bytes = sum(t.numel() * t.element_size() for t in state.values())
+    fits_one_device = gpu_devices is None or gpu_budget_bytes is None or total_bytes <= gpu_budget_bytes
+    if not fits_one_device:
+        raise NotImplementedError(
+            f"the checkpoint holds {total_bytes} bytes, more than gpu_budget_bytes={gpu_budget_bytes}: spreading "
+            "layers over several devices (accelerate.dispatch_model in the reference) is not implemented; this "
+            "library runs on one GPU")
+    if model is None:
+        model = build_meta_model(manifest["model_id"], save_path)
+    install_quantized_placeholders(model, manifest)
     model.load_state_dict(state, strict=True, assign=True)
+    device = gpu_devices[0] if gpu_devices else device
     model.to(device)
     codebook, _ = build_codebook(manifest["bits"], device, manifest["seed"])
     for info in manifest["quantized_modules"]:

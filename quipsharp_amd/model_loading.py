@@ -1,0 +1,50 @@
+"""The loading entry point the reference's evaluation scripts call
+(quipsharp/model_loading.py; scripts/eval_ppl.py:18, eval_zeroshot.py),
+for this library's compact quantized checkpoints on one GPU.
+
+``load_eval_model`` returns ``(model, main_device)`` like the reference.  A
+directory holding a quantized checkpoint loads through
+``checkpoint.load_quantized_checkpoint``; any other model (a dense baseline)
+loads with ``transformers``' ``from_pretrained`` onto the first device.
+Spreading a model over several devices or offloading to the CPU (the
+reference's accelerate paths) is not implemented: this library runs on one
+GPU."""
+from pathlib import Path
+
+from .checkpoint import is_quantized_checkpoint, load_quantized_checkpoint
+
+
+def resolve_gpu_budget_bytes(arg, headroom_frac: float = 0.15) -> int:
+    """quipsharp/model_loading.py:12-22: a number is taken as GB; "auto" is
+    the free memory of the least-free visible device minus ``headroom_frac``
+    of its total."""
+    if arg != "auto":
+        return int(float(arg) * 1024 ** 3)
+    import torch
+    budgets = [free - int(headroom_frac * total)
+               for free, total in (torch.cuda.mem_get_info(i) for i in range(torch.cuda.device_count()))]
+    return min(budgets) if budgets else 0
+
+
+def resolve_cpu_budget_bytes(arg, use_frac: float = 0.8) -> int:
+    """quipsharp/model_loading.py:25-33: a number is taken as GB; "auto" is
+    ``use_frac`` of the available host memory (MemAvailable)."""
+    if arg != "auto":
+        return int(float(arg) * 1024 ** 3)
+    with open("/proc/meminfo") as f:
+        avail_kb = next(int(line.split()[1]) for line in f if line.startswith("MemAvailable"))
+    return int(avail_kb * 1024 * use_frac)
+
+
+def load_eval_model(model_id_or_path: str, gpu_devices=("cuda:0",), gpu_budget_bytes: int = 20 * 1024 ** 3,
+                    cpu_budget_bytes: int = 60 * 1024 ** 3, offload_folder: str = None):
+    """quipsharp/model_loading.py:36-96 for one device: (model, main_device)."""
+    main_device = gpu_devices[0] if gpu_devices else "cpu"
+    if Path(model_id_or_path).is_dir() and is_quantized_checkpoint(model_id_or_path):
+        model = load_quantized_checkpoint(model_id_or_path, device=main_device, gpu_devices=list(gpu_devices),
+                                          gpu_budget_bytes=gpu_budget_bytes, cpu_budget_bytes=cpu_budget_bytes)
+        return model, main_device
+    from transformers import AutoModelForCausalLM
+    model = AutoModelForCausalLM.from_pretrained(model_id_or_path, dtype="auto", low_cpu_mem_usage=True)
+    model.to(main_device).eval()
+    return model, main_device

@@ -243,9 +243,75 @@ def c1_full(ref_root):
     print(f"c1_full.npz written: quantize {t_q:.0f} s, proxy_rel {proxy_rel:.5e}", flush=True)
 
 
+def ref_checkpoint(ref_root):
+    """A checkpoint written by the reference's own save path
+    (quipsharp/checkpoint.py:149-186, driven as scripts/quantize_model.py:72-126
+    drives it): a one-layer Llama-shaped model, hidden 256 (power of two:
+    "rht" layers, with q/k/v/o biases) and intermediate 384 (not: "rfft"
+    layers), every decoder linear quantized by quantize_linear with a
+    synthetic Hessian and swapped in by replace_with_quantized_linear_.
+    Writes tests/golden/ref_ckpt/ (quantized_state.pt, quip_config.json and the
+    model's config.json, which the loader uses when the manifest's model id
+    cannot be resolved offline) and ref_ckpt_outputs.npz (each quantized
+    module's output for a fixed input, and the model's logits, from the
+    reference's CPU forward)."""
+    sys.path.insert(0, ref_root)
+    import torch
+    from transformers import AutoModelForCausalLM, LlamaConfig
+    from quipsharp.architectures import get_decoder_layers, get_linear_groups
+    from quipsharp.checkpoint import build_codebook, replace_with_quantized_linear_, save_quantized_checkpoint
+    from quipsharp.quantize import quantize_linear
+
+    torch.set_num_threads(8)
+    out_dir = os.path.join(OUT, "ref_ckpt")
+    os.makedirs(out_dir, exist_ok=True)
+    cfg = LlamaConfig(hidden_size=256, intermediate_size=384, num_hidden_layers=1, num_attention_heads=4,
+                      num_key_value_heads=2, vocab_size=128, max_position_embeddings=64, attention_bias=True,
+                      torch_dtype="float32")
+    torch.manual_seed(0)
+    model = AutoModelForCausalLM.from_config(cfg).float().eval()
+    cb, scale = build_codebook("2bit", "cpu", 0)
+    g = torch.Generator().manual_seed(21)
+    quantized_modules = []
+    for li, layer in enumerate(get_decoder_layers(model)):
+        for group in get_linear_groups(layer, li):
+            for name, module in group:
+                W = module.weight.data.float()
+                bias = module.bias.data.float().clone() if module.bias is not None else None
+                X = torch.randn(4 * W.shape[1], W.shape[1], generator=g)
+                H = X.T @ X / X.shape[0]
+                qlayer, _ = quantize_linear(W, H, cb, g=8, damping=1e-2, codebook_scale=scale, tune_iters=2)
+                parent_name, _, attr = name.rpartition(".")
+                parent = layer.get_submodule(parent_name) if parent_name else layer
+                replace_with_quantized_linear_(parent, attr, qlayer, cb, bias=bias)
+                quantized_modules.append({"name": f"model.layers.{li}.{name}", "in_features": qlayer.shape[1],
+                                          "out_features": qlayer.shape[0],
+                                          "transform_kind": "rht" if hasattr(qlayer.signs, "su") else "rfft",
+                                          "has_bias": bias is not None})
+    save_quantized_checkpoint(model, "tiny-llama-quipsharp", out_dir, bits="2bit", block_size=8, seed=0,
+                              quantized_modules=quantized_modules)
+    cfg.save_pretrained(out_dir)
+    outs = {}
+    gx = torch.Generator().manual_seed(22)
+    with torch.no_grad():
+        for info in quantized_modules:
+            mod = model.get_submodule(info["name"])
+            x = torch.randn(3, info["in_features"], generator=gx)
+            key = info["name"].replace(".", "_")
+            outs[key + "_x"] = x.numpy()
+            outs[key + "_y"] = mod(x).numpy()
+        ids = torch.randint(0, 128, (1, 16), generator=gx)
+        outs["ids"] = ids.numpy()
+        outs["logits"] = model(ids).logits.float().numpy()
+    np.savez_compressed(os.path.join(OUT, "ref_ckpt_outputs.npz"), **outs)
+    print("reference checkpoint written to", out_dir, [m["transform_kind"] for m in quantized_modules], flush=True)
+
+
 if __name__ == "__main__":
     root = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
     if len(sys.argv) > 2 and sys.argv[2] == "c1":
         c1_full(root)
+    elif len(sys.argv) > 2 and sys.argv[2] == "ckpt":
+        ref_checkpoint(root)
     else:
         main(root)

@@ -121,7 +121,7 @@ def test_checkpoint_round_trip(dev, tmp_path):
     assert is_quantized_checkpoint(tmp_path)
     with torch.device("meta"):
         skel = Net()
-    loaded = load_quantized_checkpoint(tmp_path, skel, device=dev)
+    loaded = load_quantized_checkpoint(tmp_path, device=dev, model=skel)
     got = loaded.b(loaded.a(x))
     assert torch.equal(got, want)
     for k, v in net.state_dict().items():
