@@ -1,22 +1,30 @@
 #!/usr/bin/env python3
 """E8P decode-matvec benchmark on one MI355X.
 
-Workload: the Llama-2-7B quantized-linear stack -- per decoder layer q, k, v,
-o (4096x4096), gate, up (11008x4096) and down (4096x11008) -- 32 decoder
-layers (1.62 GB of E8P codes, about 6x the Infinity Cache), bf16
-activations, batch 1 (decode; batch 16 reported alongside).  E8P 2-bit codes
-are random uint16 from a seeded generator with an fp16 per-layer scale and
-seeded RHT signs; the 11008-wide dims use the Kronecker transform (43 x 256).
-A step is one pass through the 224 linears in dependency order (q/k/v read
-the layer input, o reads q, gate/up read o, down reads gate, the next layer
-reads down), replayed from a HIP graph.  By default the linears that share an
-input run as one grouped launch (q/k/v, gate/up: qs_linear_forward_group), 4
-launches per layer; --per-linear makes the headline one qs_linear_forward per
-linear (7 per layer), and the other pattern is always reported alongside.
+Headline workload: the Llama-2-7B quantized-linear stack -- per decoder layer
+q, k, v, o (4096x4096), gate, up (11008x4096) and down (4096x11008) -- 32
+decoder layers (1.62 GB of E8P codes, about 6x the Infinity Cache), bf16
+activations, batch 1.  E8P 2-bit codes are random uint16 from a seeded
+generator with an fp16 per-layer scale and seeded RHT signs; the 11008-wide
+dims use the Kronecker transform (43 x 256).  A step is one pass through the
+224 linears in dependency order (q/k/v read the layer input, o reads q,
+gate/up read o, down reads gate, the next layer reads down), replayed from a
+HIP graph: W warm-up replays, then K replays timed with HIP events (the
+median replay is reported beside the mean).  By default the linears that
+share an input run as one grouped launch (q/k/v, gate/up:
+qs_linear_forward_group), 4 launches per layer; --per-linear makes the
+headline one qs_linear_forward per linear (7 per layer), and the other
+pattern is always reported alongside.
 
-Also reported: quantize s/layer for a 4096x4096 layer (E8P 2-bit
-BlockLDLQ with 10 refinement sweeps) and the reference's CPU path timed on
-this host (torch-CPU restatement, oracle/torch_path.py).
+Also reported, each in its own object: batch 16 and a 512-row prefill of the
+same stack; the Llama-3-8B 3-bit RVQ stack (32 layers, 2.6 GB of codes) at
+batch 1 / 4 / 16 and the Qwen2.5-7B stack (36 layers, 2.1 GB) at batch 1,
+both rotated through more codes than the Infinity Cache holds; the
+Qwen3-32B-shaped greedy decode (64 layers, batch 1 and 8, tok/s, the
+linears' share of a step, per-linear GB/s across all 64 layers); quantize
+s/layer for the 4096x4096 E8P 2-bit layer and the Llama-3-8B / Qwen2.5-7B
+layer shapes; and the reference's CPU path timed on this host (torch-CPU
+restatement, oracle/torch_path.py).
 
 Prints one JSON line.
 """
@@ -24,6 +32,7 @@ import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 
@@ -33,20 +42,42 @@ if ROOT not in sys.path:
 
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0  # dense fp16 / bf16 matrix-core peak
-LLAMA2_7B = [("q", 4096, 4096), ("k", 4096, 4096), ("v", 4096, 4096), ("o", 4096, 4096),
-             ("gate", 11008, 4096), ("up", 11008, 4096), ("down", 4096, 11008)]
+
+# Decoder-layer linear stacks: (name, m = out_features, n = in_features) per
+# layer, residual-VQ stages (1: E8P 2-bit; 2: E8P + E8 1-bit, 3 bits per
+# weight), layer count.
+MODELS = {
+    "llama2_7b": dict(title="Llama-2-7B", layers=32, stages=1,
+                      lin=[("q", 4096, 4096), ("k", 4096, 4096), ("v", 4096, 4096), ("o", 4096, 4096),
+                           ("gate", 11008, 4096), ("up", 11008, 4096), ("down", 4096, 11008)]),
+    "llama3_8b": dict(title="Llama-3-8B, 3-bit RVQ (E8P + E8 1-bit)", layers=32, stages=2,
+                      lin=[("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
+                           ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]),
+    "qwen25_7b": dict(title="Qwen2.5-7B", layers=36, stages=1,
+                      lin=[("q", 3584, 3584), ("k", 512, 3584), ("v", 512, 3584), ("o", 3584, 3584),
+                           ("gate", 18944, 3584), ("up", 18944, 3584), ("down", 3584, 18944)]),
+}
+LLAMA2_7B = MODELS["llama2_7b"]["lin"]
+GROUPS = [("q", "k", "v"), ("o",), ("gate", "up"), ("down",)]   # linears of one launch, per layer
+SOURCE = {"q": None, "k": None, "v": None, "o": "q", "gate": "o", "up": "o", "down": "gate"}
+# (m, n) of a Qwen3-32B decoder layer's linears: q, k, v, o, gate, up, down
+QWEN3_32B_LINEARS = [(8192, 5120), (1024, 5120), (1024, 5120), (5120, 8192), (25600, 5120), (25600, 5120),
+                     (5120, 25600)]
 
 
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--layers", type=int, default=32)
     p.add_argument("--skip-quantize", action="store_true")
     p.add_argument("--skip-cpu", action="store_true")
     p.add_argument("--skip-batch16", action="store_true")
     p.add_argument("--skip-alt", action="store_true", help="do not time the other call pattern")
+    p.add_argument("--skip-shapes", action="store_true", help="skip the Llama-3-8B and Qwen2.5-7B stacks")
+    p.add_argument("--skip-decode", action="store_true", help="skip the Qwen3-32B-shaped greedy decode")
+    p.add_argument("--decode-new", type=int, default=64, help="tokens generated per batch size in the decode")
     p.add_argument("--prefill", type=int, default=512,
                    help="rows of the prefill (wide-batch) step also timed; 0 skips it")
     p.add_argument("--per-linear", action="store_true",
@@ -62,79 +93,78 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def linear_bytes(m, n, B):
-    """Algorithmic HBM bytes of one quantized-linear call: 2-byte codes per 8
-    weights, bf16 activations in and out, 1-bit signs, fp16 scale."""
-    return m * n // 8 * 2 + 2 * B * (n + m) + math.ceil((m + n) / 8) + 2
+def linear_bytes(m, n, B, stages=1):
+    """Algorithmic HBM bytes of one quantized-linear call: 2-byte E8P codes
+    (plus 1-byte E8 1-bit codes at 3 bits) per 8 weights, bf16 activations in
+    and out, 1-bit signs, fp16 scale."""
+    return m * n // 8 * (2 + (1 if stages == 2 else 0)) + 2 * B * (n + m) + math.ceil((m + n) / 8) + 2
 
 
-def mv_bytes(m, n, B):
+def mv_bytes(m, n, B, stages=1):
     """Algorithmic bytes of the decode-matvec of one linear.  At B <= 2 that
     is the one-kernel forward (codes, signs, bf16 activations in and out: the
     whole linear); at larger batches the decode-matvec kernel alone (codes,
     fp16 activations in, fp32 partial outputs)."""
     if B <= 2:
-        return linear_bytes(m, n, B)
-    return m * n // 8 * 2 + 2 * B * n + 4 * B * m
+        return linear_bytes(m, n, B, stages)
+    return m * n // 8 * (2 + (1 if stages == 2 else 0)) + 2 * B * n + 4 * B * m
 
 
 MV_KERNEL = "linear_fused_kernel"  # the dominant kernel of the batch-1 step
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "linear_fused_llama2_7b_b1.md")
 
 
-def measured_traffic():
-    """HBM bytes per launch of the batch-1 kernel, from the committed
-    hardware-counter summary (FETCH_SIZE + WRITE_SIZE, calibrated), or None."""
+def profile_figures():
+    """HBM bytes per launch (FETCH_SIZE + WRITE_SIZE, calibrated) and the
+    kernel-only average duration of the batch-1 kernel, from the committed
+    rocprofv3 summary of this bench (labelled as such in the output)."""
+    out = {}
     try:
         with open(TRAFFIC_PROFILE) as f:
             for line in f:
                 if line.startswith("traffic_bytes_per_launch:"):
-                    return int(line.split(":")[1])
+                    out["traffic"] = int(line.split(":")[1])
+                elif line.startswith("kernel_avg_us:"):
+                    out["kernel_avg_us"] = float(line.split(":")[1])
     except OSError:
         pass
-    return None
+    return out
 
 
 class Stack:
-    """The synthetic 32-layer Llama-2-7B linear stack on the GPU."""
+    """A synthetic decoder-linear stack (``MODELS`` entry) on the GPU: random
+    codes (E8P, plus E8 1-bit for 3-bit layers) packed once, seeded signs."""
 
-    def __init__(self, layers, dev):
+    def __init__(self, spec, dev, layers=None):
         import torch
-        from quipsharp_amd.quantize import PackedCodes
         from quipsharp_amd.hadamard import rademacher
-        self.dev = dev
+        from quipsharp_amd.quantize import PackedCodes
+        self.spec, self.dev = spec, dev
+        self.stages = spec["stages"]
+        self.shape = {name: (m, n) for name, m, n in spec["lin"]}
         gen = torch.Generator(device=dev).manual_seed(0)
         cpu_gen = torch.Generator().manual_seed(0)
-        scale = float(torch.tensor(0.0135, dtype=torch.float16).float())
+        f16 = lambda v: float(torch.tensor(v, dtype=torch.float16).float())
+        self.s0, self.s1, self.scale = 1.0, f16(0.47) if self.stages == 2 else 0.0, f16(0.0135)
         self.layers = []
-        for _ in range(layers):
+        for _ in range(layers or spec["layers"]):
             lin = {}
-            for name, m, n in LLAMA2_7B:
+            for name, m, n in spec["lin"]:
                 codes = torch.randint(0, 65536, (m, n // 8), generator=gen, device=dev, dtype=torch.int32)
-                packed = PackedCodes(codes, m, n, [0])
+                kinds = [0]
+                if self.stages == 2:
+                    codes = torch.stack([codes, torch.randint(0, 256, (m, n // 8), generator=gen, device=dev,
+                                                              dtype=torch.int32)])
+                    kinds = [0, 1]
+                packed = PackedCodes(codes, m, n, kinds)
                 del codes
-                su = rademacher(m, device=dev, generator=cpu_gen)
-                sv = rademacher(n, device=dev, generator=cpu_gen)
-                lin[name] = (packed, su, sv, scale)
+                lin[name] = (packed, rademacher(m, device=dev, generator=cpu_gen),
+                             rademacher(n, device=dev, generator=cpu_gen))
             self.layers.append(lin)
         torch.cuda.synchronize()
 
     def code_bytes(self):
         return sum(p[0].nbytes() for lin in self.layers for p in lin.values())
-
-
-GROUPS = [("q", "k", "v"), ("o",), ("gate", "up"), ("down",)]   # linears of one launch, per layer
-# (m, n) of a Qwen3-32B decoder layer's linears: q, k, v, o, gate, up, down
-QWEN3_32B_LINEARS = [(8192, 5120), (1024, 5120), (1024, 5120), (5120, 8192), (25600, 5120), (25600, 5120),
-                     (5120, 25600)]
-SOURCE = {"q": None, "k": None, "v": None, "o": "q", "gate": "o", "up": "o", "down": "gate"}
-SHAPE = {name: (m, n) for name, m, n in LLAMA2_7B}
-
-
-def launch_bytes(names, B):
-    """Algorithmic bytes of one launch of the linears `names` (one shared input)."""
-    m0, n = SHAPE[names[0]]
-    return sum(linear_bytes(*SHAPE[k], B) for k in names) - (len(names) - 1) * 2 * B * n
 
 
 class Runner:
@@ -148,79 +178,91 @@ class Runner:
         import ctypes
         import torch
         from quipsharp_amd import _lib
-        from quipsharp_amd.hadamard import hartley_matrix
+        from quipsharp_amd.hadamard import hartley_matrix, kron_factor
+        from quipsharp_amd.quantize import pack_signs
         self.stack, self.B = stack, B
         self.grouped = grouped
         dev = stack.dev
+        shape = stack.shape
         self.lib = _lib.lib()
         self._lib = _lib
         g = torch.Generator(device=dev).manual_seed(1)
-        self.x = torch.randn(B, 4096, generator=g, device=dev).bfloat16()
-        self.buf = {k: torch.empty(B, m, dtype=torch.bfloat16, device=dev) for k, m, _ in LLAMA2_7B}
-        self.K43 = hartley_matrix(43, dev)
-        self.plan = GROUPS if self.grouped else [(name,) for name, _, _ in LLAMA2_7B]
-        if self.grouped:
-            ws = 0
-            for names in self.plan:
-                ms = (ctypes.c_int64 * len(names))(*[SHAPE[k][0] for k in names])
-                ws = max(ws, self.lib.qs_linear_group_workspace_bytes(SHAPE[names[0]][1], B, len(names), ms))
-        else:
-            ws = max(self.lib.qs_linear_workspace_bytes(m, n, B, _lib.QS_LAYOUT_TILED) for _, m, n in LLAMA2_7B)
-        self.ws = torch.zeros(ws, dtype=torch.uint8, device=dev)  # counter regions must start at zero
-        # per (layer, launch): the ctypes job array, built once
-        # signs as packed bits (QS_SIGNS_BITS), as QuantizedLinear passes them
-        from quipsharp_amd.quantize import pack_signs
-        self.jobs, self._bits = [], []
+        n0 = shape["q"][1]
+        self.x = torch.randn(B, n0, generator=g, device=dev).bfloat16()
+        self.buf = {k: torch.empty(B, m, dtype=torch.bfloat16, device=dev) for k, (m, _) in shape.items()}
+        self.K = {}
+        for m, n in shape.values():
+            for d in (m, n):
+                p = kron_factor(d)[0]
+                if p > 1 and p not in self.K:
+                    self.K[p] = hartley_matrix(p, dev)
+        self.plan = GROUPS if self.grouped else [(name,) for name in shape]
+        # the grouped entry point takes n a multiple of 256 up to 12288; a
+        # launch of one linear outside that range is a qs_linear_forward call
+        self.as_group = [self.grouped and shape[names[0]][1] % 256 == 0 and shape[names[0]][1] <= 12288
+                         for names in self.plan]
+        ws = 0
+        for names, grp in zip(self.plan, self.as_group):
+            if grp:
+                ms = (ctypes.c_int64 * len(names))(*[shape[k][0] for k in names])
+                ws = max(ws, self.lib.qs_linear_group_workspace_bytes(shape[names[0]][1], B, len(names), ms))
+            else:
+                ws = max(ws, self.lib.qs_linear_workspace_bytes(*shape[names[0]], B, _lib.QS_LAYOUT_TILED))
+        self.ws = torch.zeros(ws, dtype=torch.uint8, device=dev)  # zero before first use (epoch words)
+        # per (layer, launch): the ctypes job array, built once; signs as
+        # packed bits (QS_SIGNS_BITS) where both sizes fit the chunk scheme,
+        # as QuantizedLinear passes them
+        self.jobs, self._keep = [], []
+        fits = lambda d: d % 256 == 0 and d <= 12288
         for lin in stack.layers:
             per = []
             for names in self.plan:
                 arr = (_lib.LinearJob * len(names))()
+                bits = all(fits(shape[k][0]) and fits(shape[k][1]) for k in names)
                 for j, k in enumerate(names):
-                    packed, su, sv, scale = lin[k]
-                    su, sv = pack_signs(su), pack_signs(sv)
-                    self._bits += [su, sv]
-                    m = SHAPE[k][0]
-                    km = 43 if m == 11008 else 1
-                    arr[j] = _lib.LinearJob(packed.codes0.data_ptr(), None, m, su.data_ptr(), sv.data_ptr(), km,
-                                            self.K43.data_ptr() if km > 1 else None, 1.0, 0.0, scale, None,
-                                            self.buf[k].data_ptr(), m, 1)
+                    packed, su, sv = lin[k]
+                    if bits:
+                        su, sv = pack_signs(su), pack_signs(sv)
+                    self._keep += [su, sv]
+                    m = shape[k][0]
+                    km = kron_factor(m)[0]
+                    arr[j] = _lib.LinearJob(packed.codes0.data_ptr(),
+                                            None if packed.codes1 is None else packed.codes1.data_ptr(), m,
+                                            su.data_ptr(), sv.data_ptr(), km,
+                                            self.K[km].data_ptr() if km > 1 else None, stack.s0, stack.s1,
+                                            stack.scale, None, self.buf[k].data_ptr(), m, 1 if bits else 0)
                 per.append(arr)
             self.jobs.append(per)
 
-    def _launch(self, li, gi, names, x, stream, events):
+    def _launch(self, li, gi, names, x, stream):
+        from quipsharp_amd.hadamard import kron_factor
         L, _lib = self.lib, self._lib
-        n = SHAPE[names[0]][1]
-        kn = 43 if n == 11008 else 1
-        Kn = self.K43.data_ptr() if kn > 1 else None
-        e0, e1 = (events[0], events[1]) if events else (None, None)
-        if self.grouped:
+        n = self.stack.shape[names[0]][1]
+        kn = kron_factor(n)[0]
+        Kn = self.K[kn].data_ptr() if kn > 1 else None
+        if self.as_group[gi]:
             rc = L.qs_linear_forward_group(x.data_ptr(), _lib.QS_DTYPE_BF16, n, self.B, n, kn, Kn, len(names),
                                            self.jobs[li][gi], _lib.QS_DTYPE_BF16, self.ws.data_ptr(), self.ws.numel(),
-                                           e0, e1, stream)
+                                           None, None, stream)
         else:
+            assert len(names) == 1, names
             j = self.jobs[li][gi][0]
-            m = j.m
+            layout = _lib.QS_LAYOUT_TILED | (_lib.QS_SIGNS_BITS if j.sign_bits else 0)
             rc = L.qs_linear_forward(
-                x.data_ptr(), _lib.QS_DTYPE_BF16, n, self.B, n, m, j.codes0, None, 0, _lib.QS_LAYOUT_TILED | _lib.QS_SIGNS_BITS,
-                j.sv, j.su,
-                kn, Kn, j.kron_pm, j.kron_m, 1.0, 0.0, j.layer_scale, None, j.y, _lib.QS_DTYPE_BF16, m,
-                self.ws.data_ptr(), self.ws.numel(), e0, e1, stream)
+                x.data_ptr(), _lib.QS_DTYPE_BF16, n, self.B, n, j.m, j.codes0, j.codes1, _lib.QS_STAGE_E8_1BIT,
+                layout, j.sv, j.su, kn, Kn, j.kron_pm, j.kron_m, j.s0, j.s1, j.layer_scale, None, j.y,
+                _lib.QS_DTYPE_BF16, j.m, self.ws.data_ptr(), self.ws.numel(), None, None, stream)
         if rc:
             _lib.check(rc)
 
-    def step(self, events=None):
+    def step(self):
         import torch
         stream = torch.cuda.current_stream(self.stack.dev).cuda_stream
         x = self.x
-        ei = 0
         for li in range(len(self.stack.layers)):
             for gi, names in enumerate(self.plan):
                 src = x if SOURCE[names[0]] is None else self.buf[SOURCE[names[0]]]
-                ev = None
-                if events is not None:
-                    ev = events[ei]
-                    ei += 1
-                self._launch(li, gi, names, src, stream, ev)
+                self._launch(li, gi, names, src, stream)
             x = self.buf["down"]
         return self.buf["down"]
 
@@ -228,19 +270,29 @@ class Runner:
         return len(self.stack.layers) * len(self.plan)
 
     def bytes_per_step(self):
-        return len(self.stack.layers) * sum(linear_bytes(m, n, self.B) for _, m, n in LLAMA2_7B)
+        st = self.stack.stages
+        return len(self.stack.layers) * sum(linear_bytes(m, n, self.B, st) for m, n in self.stack.shape.values())
 
     def mv_bytes_per_step(self):
-        """Algorithmic bytes of the step's decode-matvec launches."""
-        if self.B <= 2:
-            return len(self.stack.layers) * sum(launch_bytes(names, self.B) for names in self.plan)
-        return len(self.stack.layers) * sum(mv_bytes(m, n, self.B) for _, m, n in LLAMA2_7B)
+        """Algorithmic bytes of the step's decode-matvec launches (at 1-2 rows
+        a grouped launch reads its shared input once)."""
+        st, shape, B = self.stack.stages, self.stack.shape, self.B
+        if B <= 2:
+            per = 0
+            for names in self.plan:
+                n = shape[names[0]][1]
+                per += sum(linear_bytes(*shape[k], B, st) for k in names) - (len(names) - 1) * 2 * B * n
+            return len(self.stack.layers) * per
+        return len(self.stack.layers) * sum(mv_bytes(m, n, B, st) for m, n in shape.values())
 
 
 def time_graph(runner, steps, warmup):
+    """Captures one step in a HIP graph (checked against the eager step),
+    replays it ``warmup`` times, then times ``steps`` replays back to back
+    with a HIP event after each: returns the mean (the whole timed region
+    over ``steps``) and the median replay, in ms."""
     import torch
     dev = runner.stack.dev
-    # eager reference output for the graph check
     ref = runner.step().clone()
     torch.cuda.synchronize()
     s = torch.cuda.Stream(device=dev)
@@ -255,20 +307,21 @@ def time_graph(runner, steps, warmup):
     for _ in range(max(warmup, 1)):
         graph.replay()
     torch.cuda.synchronize()
-    out = runner.buf["down"]
-    if not torch.equal(out, ref):
+    if not torch.equal(runner.buf["down"], ref):
         raise RuntimeError("graph replay differs from the eager step")
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     torch.cuda.synchronize()
-    e0.record()
-    for _ in range(steps):
+    ev[0].record()
+    for i in range(steps):
         graph.replay()
-    e1.record()
+        ev[i + 1].record()
     torch.cuda.synchronize()
     if not torch.equal(runner.buf["down"], ref):
         raise RuntimeError("graph replays are not reproducible")
-    return e0.elapsed_time(e1) / steps  # ms
+    per = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
+    del graph
+    return {"mean_ms": ev[0].elapsed_time(ev[steps]) / steps, "median_ms": statistics.median(per),
+            "min_ms": min(per), "max_ms": max(per)}
 
 
 def time_eager(runner, steps, warmup):
@@ -289,31 +342,6 @@ def time_eager(runner, steps, warmup):
     if not torch.equal(runner.buf["down"], ref):
         raise RuntimeError("prefill steps are not reproducible")
     return e0.elapsed_time(e1) / steps
-
-
-def time_mv_kernels(runner, passes=3):
-    """Average duration of the decode-matvec kernels, from HIP events attached
-    to each kernel's dispatch (hipExtLaunchKernelGGL start / stop events, the
-    interval a kernel trace reports as its duration).  The stream is kept busy
-    first so the launches queue back to back."""
-    import torch
-    from quipsharp_amd import _lib
-    n = runner.launches_per_step()
-    evs = []
-    for _ in range(n):
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        b.record()
-        evs.append((a, b))
-    torch.cuda.synchronize()
-    handles = [(a.cuda_event, b.cuda_event) for a, b in evs]
-    total_ms = 0.0
-    for _ in range(passes):
-        _lib.check(_lib.lib().qs_busy_wait(30_000_000, _lib._vp(torch.cuda.current_stream().cuda_stream)))
-        runner.step(events=handles)
-        torch.cuda.synchronize()
-        total_ms += sum(a.elapsed_time(b) for a, b in evs)
-    return total_ms / passes / n  # ms per launch
 
 
 def gpu_quantize(dev, n=4096, tune_iters=10):
@@ -503,6 +531,48 @@ def kernel_rates(dev):
             "fwht_4096x4096_cols_GBps": round(8 * W.numel() / out["fwht_cols"] / 1e9, 1)}
 
 
+def stack_batches(key, batches, steps, warmup, dev):
+    """ms/step, GB/s and tok/s of a ``MODELS`` stack at each batch size
+    (grouped launches, graph-replayed steps)."""
+    import torch
+    spec = MODELS[key]
+    t0 = time.perf_counter()
+    stack = Stack(spec, dev)
+    out = {"workload": f"{spec['title']} quantized-linear stack, {spec['layers']} decoder layers",
+           "linears": {name: [m, n] for name, m, n in spec["lin"]}, "bits": 3 if spec["stages"] == 2 else 2,
+           "code_bytes": stack.code_bytes(), "setup_s": round(time.perf_counter() - t0, 1), "batches": []}
+    for B in batches:
+        r = Runner(stack, B)
+        t = time_graph(r, steps, warmup)
+        ms = t["mean_ms"]
+        out["batches"].append({"batch": B, "ms_per_step": round(ms, 4), "median_ms_per_step": round(t["median_ms"], 4),
+                               "GBps": round(r.bytes_per_step() / ms / 1e6, 1), "tok_per_s": round(B * 1e3 / ms, 1),
+                               "launches_per_step": r.launches_per_step()})
+        log(f"{key} batch {B}: {ms:.3f} ms/step, {r.bytes_per_step() / ms / 1e6:.1f} GB/s")
+        del r
+    del stack
+    torch.cuda.empty_cache()
+    return out
+
+
+def shape_quantize(dev, tune_iters=10):
+    """Quantize s/layer at the Llama-3-8B (3-bit RVQ) and Qwen2.5-7B (2-bit,
+    1 % Student-t(3) outliers) layer shapes (quipsharp_amd.shapes_bench)."""
+    from quipsharp_amd.checkpoint import build_codebook
+    from quipsharp_amd.shapes_bench import LLAMA3_8B, QWEN25_7B, quantize_layer
+    out = {}
+    for key, shapes, bits, heavy, seed in (("llama3_8b_3bit", LLAMA3_8B, "3bit", False, 11),
+                                          ("qwen25_7b_2bit_heavy_tailed", QWEN25_7B, "2bit", True, 21)):
+        cbs = {bits: build_codebook(bits, dev, 0)}
+        rows = []
+        for i, (m, n) in enumerate(shapes):
+            _, t_q, proxy = quantize_layer(m, n, bits, heavy, seed + i, tune_iters, dev, cbs)
+            rows.append({"m": m, "n": n, "quantize_s": round(t_q, 3), "relative_proxy_loss": round(proxy, 5)})
+            log(f"quantize {key} {m}x{n}: {t_q:.3f} s")
+        out[key] = rows
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -512,8 +582,9 @@ def main():
     import torch
     dev = torch.device("cuda:0")
     torch.manual_seed(0)
+    spec = MODELS["llama2_7b"]
     if args.probe:
-        stack = Stack(2, dev)
+        stack = Stack(spec, dev, 2)
         r1 = Runner(stack, 1)
         r1.step()
         torch.cuda.synchronize()
@@ -533,54 +604,52 @@ def main():
         print(json.dumps({"probe": "done", "linears": r1.launches_per_step(), "copy_bytes": a.numel() * 4}))
         return
     t_setup = time.perf_counter()
-    stack = Stack(args.layers, dev)
+    stack = Stack(spec, dev, args.layers)
     log(f"stack: {args.layers} layers, {stack.code_bytes() / 1e9:.2f} GB of codes, "
         f"setup {time.perf_counter() - t_setup:.1f}s")
     r1 = Runner(stack, 1, grouped=not args.per_linear)
-    ms = time_graph(r1, args.steps, args.warmup)
-    mv_ms = time_mv_kernels(r1)
+    t1 = time_graph(r1, args.steps, args.warmup)
+    ms = t1["mean_ms"]
     bps = r1.bytes_per_step()
     value = bps / (ms * 1e-3) / 1e9
-    mv_avg_bytes = r1.mv_bytes_per_step() / r1.launches_per_step()
+    launches = r1.launches_per_step()
+    # every launch of the batch-1 step is the dominant kernel: its average
+    # launch duration over the timed region is the step over the launches
+    # (the gaps between the dependent launches included)
+    mv_ms = ms / launches
+    mv_avg_bytes = r1.mv_bytes_per_step() / launches
     achieved = mv_avg_bytes / (mv_ms * 1e-3) / 1e9
-    log(f"batch 1 ({'grouped' if r1.grouped else 'per-linear'}): {ms:.3f} ms/step, {value:.1f} GB/s, "
-        f"mv kernel avg {mv_ms * 1e3:.2f} us -> {achieved:.1f} GB/s")
+    log(f"batch 1 ({'grouped' if r1.grouped else 'per-linear'}): {ms:.3f} ms/step (median {t1['median_ms']:.3f}), "
+        f"{value:.1f} GB/s, {mv_ms * 1e3:.2f} us per launch -> {achieved:.1f} GB/s")
     extra = {}
     if not args.skip_alt:
         # the other call pattern, for comparison
         r_alt = Runner(stack, 1, grouped=args.per_linear)
-        ms_alt = time_graph(r_alt, args.steps, args.warmup)
-        mv_alt = time_mv_kernels(r_alt, passes=1)
+        ta = time_graph(r_alt, args.steps, args.warmup)
+        ms_alt = ta["mean_ms"]
         extra["grouped" if r_alt.grouped else "per_linear"] = {
-            "ms_per_step": round(ms_alt, 4), "GBps": round(bps / ms_alt / 1e6, 1), "tok_per_s": round(1e3 / ms_alt, 1),
-            "launches_per_step": r_alt.launches_per_step(), "mv_kernel_avg_us": round(mv_alt * 1e3, 3),
-            "mv_kernel_GBps": round(r_alt.mv_bytes_per_step() / r_alt.launches_per_step() / (mv_alt * 1e-3) / 1e9, 1)}
+            "ms_per_step": round(ms_alt, 4), "median_ms_per_step": round(ta["median_ms"], 4),
+            "GBps": round(bps / ms_alt / 1e6, 1), "tok_per_s": round(1e3 / ms_alt, 1),
+            "launches_per_step": r_alt.launches_per_step(),
+            "avg_launch_us": round(ms_alt * 1e3 / r_alt.launches_per_step(), 3)}
         log(f"batch 1 ({'grouped' if r_alt.grouped else 'per-linear'}): {ms_alt:.3f} ms/step")
         del r_alt
     if not args.skip_batch16:
         r16 = Runner(stack, 16, grouped=not args.per_linear)
-        ms16 = time_graph(r16, max(args.steps // 2, 1), args.warmup)
-        mv16 = time_mv_kernels(r16, passes=1)
+        t16 = time_graph(r16, args.steps, args.warmup)
+        ms16 = t16["mean_ms"]
         flops = 2 * 16 * args.layers * sum(m * n for _, m, n in LLAMA2_7B)
-        extra["batch16"] = {"ms_per_step": round(ms16, 4), "GBps": round(r16.bytes_per_step() / ms16 / 1e6, 1),
+        extra["batch16"] = {"ms_per_step": round(ms16, 4), "median_ms_per_step": round(t16["median_ms"], 4),
+                            "GBps": round(r16.bytes_per_step() / ms16 / 1e6, 1),
                             "tok_per_s": round(16 * 1e3 / ms16, 1), "TFLOPs": round(flops / ms16 / 1e9, 2),
                             "call_pattern": "grouped" if r16.grouped else "per-linear",
-                            "mv_launches_per_step": r16.launches_per_step(),
-                            "mv_kernel_avg_us": round(mv16 * 1e3, 3),
-                            "mv_kernel_GBps": round(r16.mv_bytes_per_step() / r16.launches_per_step() /
-                                                    (mv16 * 1e-3) / 1e9, 1)}
+                            "launch_groups_per_step": r16.launches_per_step()}
         log(f"batch 16 ({'grouped' if r16.grouped else 'per-linear'}): {ms16:.3f} ms/step")
         del r16
-        if not args.skip_alt:
-            r16a = Runner(stack, 16, grouped=args.per_linear)
-            ms16a = time_graph(r16a, max(args.steps // 2, 1), args.warmup)
-            extra["batch16"]["grouped_ms_per_step" if r16a.grouped else "per_linear_ms_per_step"] = round(ms16a, 4)
-            log(f"batch 16 ({'grouped' if r16a.grouped else 'per-linear'}): {ms16a:.3f} ms/step")
-            del r16a
     if args.prefill > 0:
         P = args.prefill
         rp = Runner(stack, P, grouped=not args.per_linear)
-        msp = time_eager(rp, max(args.steps // 4, 2), 2)
+        msp = time_eager(rp, max(args.steps // 10, 3), 2)
         flops = 2 * P * args.layers * sum(m * n for _, m, n in LLAMA2_7B)
         extra["prefill"] = {"rows": P, "ms_per_step": round(msp, 3), "tok_per_s": round(P * 1e3 / msp, 1),
                             "TFLOPs": round(flops / msp / 1e9, 1),
@@ -590,10 +659,21 @@ def main():
                                     "(16x16x32), codes' +-1/4 shifts via group-sum MFMAs"}
         log(f"prefill {P} rows: {msp:.3f} ms/step, {flops / msp / 1e9:.1f} TFLOP/s")
         del rp
-        torch.cuda.empty_cache()
+    del stack
+    torch.cuda.empty_cache()
+    if not args.skip_shapes:
+        extra["llama3_8b_3bit_stack"] = stack_batches("llama3_8b", [1, 4, 16], args.steps, args.warmup, dev)
+        extra["qwen25_7b_stack"] = stack_batches("qwen25_7b", [1], args.steps, args.warmup, dev)
+    if not args.skip_decode:
+        from quipsharp_amd.decode import measure_decode
+        extra["qwen3_32b_decode"] = measure_decode(new=args.decode_new, device=str(dev))
+        for run in extra["qwen3_32b_decode"]["runs"]:
+            log(f"qwen3-32b decode batch {run['batch']}: {run['tok_per_s']} tok/s, {run['ms_per_step']} ms/step "
+                f"({run['linears_ms_per_step']} ms in the quantized linears)")
     if not args.skip_quantize:
         extra["quantize_4096x4096_e8p_2bit"] = gpu_quantize(dev)
         log(f"quantize: {extra['quantize_4096x4096_e8p_2bit']}")
+        extra["quantize_layer_shapes"] = shape_quantize(dev)
         extra["quantize_kernels"] = kernel_rates(dev)
         log(f"quantize kernels: {extra['quantize_kernels']}")
     copy_peak = hbm_copy_peak(dev)
@@ -614,25 +694,33 @@ def main():
         if "quantize_4096x4096_e8p_2bit" in extra:
             extra["quantize_speedup_vs_cpu"] = round(
                 c["quantize_s_per_layer_extrapolated"] / extra["quantize_4096x4096_e8p_2bit"]["quantize_s_per_layer"], 1)
+    prof = profile_figures()
     line = {
         "metric": "E8P decode-matvec HBM GB/s (% peak) + batch-1 tok/s; quantize s/layer",
         "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "ms_per_step": round(ms, 4), "median_ms_per_step": round(t1["median_ms"], 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "e8p-2bit codes, fp16 x fp16 -> fp32 accumulate (bf16 in/out)", "data": "synthetic",
         "config": {"workload": "Llama-2-7B quantized-linear stack (q,k,v,o 4096x4096; gate,up 11008x4096; "
                                "down 4096x11008) x %d decoder layers, E8P 2-bit random codes, batch 1" % args.layers,
                    "global_batch": 1, "layers": args.layers, "linears_per_step": 7 * args.layers,
-                   "launches_per_step": r1.launches_per_step(),
+                   "launches_per_step": launches,
                    "call_pattern": "grouped (q/k/v and gate/up share a launch)" if r1.grouped else
                                    "one qs_linear_forward per linear",
-                   "code_bytes": stack.code_bytes(), "parallelism": "none (1 GPU)"},
+                   "code_bytes": int(sum(2 * m * n // 8 for _, m, n in LLAMA2_7B) * args.layers),
+                   "parallelism": "none (1 GPU)"},
         "tok_per_s": round(1e3 / ms, 1), "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "kernel": MV_KERNEL, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "avg_launch_us": round(mv_ms * 1e3, 3), "bytes_per_launch": int(mv_avg_bytes),
+                     "launch_time_source": "timed graph replays: step time / launches (the gaps between the "
+                                           "dependent launches included)",
+                     "profile_kernel_avg_us": prof.get("kernel_avg_us"),
                      "measured_copy_GBps": copy_peak,
                      "frac_of_measured_copy": round(achieved / copy_peak, 4) if copy_peak else None,
-                     "traffic": measured_traffic() if args.layers == 32 and r1.grouped else None},
+                     "traffic": prof.get("traffic") if args.layers == 32 and r1.grouped else None,
+                     "traffic_source": "committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary "
+                                       "(profiles/linear_fused_llama2_7b_b1.md), not measured in this run"},
         "cpu_baseline": cpu,
     }
     line.update(extra)

@@ -249,6 +249,110 @@ def linear_gbps(model, batches, reps=20):
     return out
 
 
+def _graph_time(fn, replays=10):
+    """Median ms of one replay of ``fn`` captured in a HIP graph (after a
+    warm-up call outside capture and two warm-up replays)."""
+    import statistics
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    for _ in range(2):
+        g.replay()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(replays + 1)]
+    ev[0].record()
+    for i in range(replays):
+        g.replay()
+        ev[i + 1].record()
+    torch.cuda.synchronize()
+    ms = statistics.median(ev[i].elapsed_time(ev[i + 1]) for i in range(replays))
+    del g
+    return ms
+
+
+@torch.no_grad()
+def linears_step_ms(model, batch):
+    """ms of the decoder linears alone for one decode step of ``batch`` rows,
+    in StaticDecoder's order and call pattern (q/k/v grouped, o, gate/up
+    grouped, down; each layer's input the previous layer's output), replayed
+    from a HIP graph."""
+    layers = get_decoder_layers(model)
+    dev = next(model.parameters()).device
+    h = torch.randn(batch, model.config.hidden_size, device=dev).bfloat16()
+
+    def run():
+        x = h
+        for L in layers:
+            a = L.self_attn
+            qo, _, _ = grouped_forward(x, [a.q_proj, a.k_proj, a.v_proj])
+            o = a.o_proj(qo)
+            go, _ = grouped_forward(o, [L.mlp.gate_proj, L.mlp.up_proj])
+            x = L.mlp.down_proj(go)
+        return x
+    return _graph_time(run)
+
+
+@torch.no_grad()
+def linear_gbps_rotated(model, batch):
+    """Per decoder linear (q, k, v, o, gate, up, down): us and GB/s
+    (algorithmic bytes) of one call, from a HIP graph that calls that linear
+    of every decoder layer in turn, so the codes read per replay (for gate /
+    up, 64 x 33 MB) far exceed the 256 MB Infinity Cache."""
+    layers = get_decoder_layers(model)
+    dev = next(model.parameters()).device
+    out = []
+    for name in ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj"):
+        mods = [getattr(L.self_attn if name[0] in "qkvo" else L.mlp, name) for L in layers]
+        n, m = mods[0].in_features, mods[0].out_features
+        x = torch.randn(batch, n, device=dev).bfloat16()
+        # _forward_one: this linear alone (a linked q or gate called under
+        # capture would run its whole group)
+        ms = _graph_time(lambda: [mod._forward_one(x) for mod in mods])
+        us = ms * 1e3 / len(mods)
+        out.append({"linear": name, "m": m, "n": n, "batch": batch, "us": round(us, 2),
+                    "GBps": round(linear_bytes(m, n, batch) / (us * 1e-6) / 1e9, 1)})
+    return out
+
+
+def measure_decode(layers=64, batches=(1, 8), prompt=512, new=64, device="cuda:0"):
+    """The Qwen3-32B-shaped greedy decode of ``new`` tokens after a ``prompt``
+    -token random prompt, per batch size: prefill s, decode tok/s and ms per
+    step (graph-replayed steps), the decoder linears' ms per step and the
+    rest, and per-linear GB/s rotated over all layers."""
+    from transformers import Qwen3Config
+    cfg = Qwen3Config(**dict(QWEN3_32B, num_hidden_layers=layers))
+    dev = torch.device(device)
+    t0 = time.perf_counter()
+    model = random_quantized_model(cfg, dev)
+    torch.cuda.synchronize()
+    res = {"model": "Qwen3-32B shape (64 layers, hidden 5120, intermediate 25600, 64 q / 8 kv heads, "
+                    "vocab 151936), random init, every decoder linear E8P 2-bit", "layers": layers,
+           "code_bytes": sum(m.codes.numel() * 2 for m in model.modules() if isinstance(m, QuantizedLinear)),
+           "build_s": round(time.perf_counter() - t0, 1), "prompt": prompt, "new_tokens": new, "runs": []}
+    for B in batches:
+        g = torch.Generator().manual_seed(B)
+        ids = torch.randint(0, cfg.vocab_size, (B, prompt), generator=g).to(dev)
+        greedy_decode(model, ids[:, :16], 4)  # warm-up
+        toks, pre_s, dec_s = greedy_decode_static(model, ids, new)
+        steps = new - 1
+        step_ms = 1e3 * dec_s / steps
+        lin_ms = linears_step_ms(model, B)
+        res["runs"].append({"batch": B, "prefill_s": round(pre_s, 3), "tok_per_s": round(B * steps / dec_s, 2),
+                            "ms_per_step": round(step_ms, 3), "linears_ms_per_step": round(lin_ms, 3),
+                            "other_ms_per_step": round(step_ms - lin_ms, 3),
+                            "linears_GBps": round(res["code_bytes"] / (lin_ms * 1e-3) / 1e9, 1),
+                            "per_linear": linear_gbps_rotated(model, B), "first_tokens": toks[0, :8].tolist()})
+    del model
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--layers", type=int, default=64)

@@ -89,8 +89,10 @@ def time_forward(packed, su, sv, s0, s1, scale, m, n, B, dev, reps=20):
     return us
 
 
-def measure_layer(m, n, bits, heavy, seed, batches, tune_iters, dev, codebooks):
-    from quipsharp_amd.quantize import PackedCodes, _forward_params, quantize_linear
+def quantize_layer(m, n, bits, heavy, seed, tune_iters, dev, codebooks):
+    """quantize_linear of one synthetic layer on the GPU: (layer, seconds
+    (synchronized), relative proxy loss tr(E H E^T) / tr(W H W^T))."""
+    from quipsharp_amd.quantize import quantize_linear
     W, X = make_weights(m, n, heavy, seed)
     Wd, Xd = W.to(dev), X.to(dev)
     H = Xd.T @ Xd / 4096
@@ -105,6 +107,14 @@ def measure_layer(m, n, bits, heavy, seed, batches, tune_iters, dev, codebooks):
     E = layer.signs.reconstruct_weight(what_q) - Wd
     proxy = (torch.trace(E.double() @ H.double() @ E.T.double()) /
              torch.trace(Wd.double() @ H.double() @ Wd.T.double())).item()
+    del H, Wd, what_q, E
+    return layer, t_q, proxy
+
+
+def measure_layer(m, n, bits, heavy, seed, batches, tune_iters, dev, codebooks):
+    from quipsharp_amd.quantize import PackedCodes, _forward_params
+    cb, _ = codebooks[bits]
+    layer, t_q, proxy = quantize_layer(m, n, bits, heavy, seed, tune_iters, dev, codebooks)
     stages = layer.codes.shape[0] if layer.codes.dim() == 3 else 1
     kinds, s0, s1 = _forward_params(cb, stages)
     packed = PackedCodes(layer.codes, m, n, kinds)
@@ -117,7 +127,6 @@ def measure_layer(m, n, bits, heavy, seed, batches, tune_iters, dev, codebooks):
     rec = {"m": m, "n": n, "stages": stages, "transform": getattr(layer.signs, "kind", "rht"),
            "quantize_s": round(t_q, 3), "relative_proxy_loss": round(proxy, 5), "forward": fw}
     log(json.dumps(rec))
-    del H, Wd, what_q, E
     torch.cuda.empty_cache()
     return rec
 
