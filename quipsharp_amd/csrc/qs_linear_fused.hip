@@ -115,13 +115,20 @@ static_assert(kLdsBytes <= 160 * 1024 - 128, "LDS budget");
 constexpr int kOffMh = 0;
 constexpr int kOffMl = kOffMh + kMBytes;
 static_assert(kOffMl + kMBytes <= kOffLut1, "M fits the LUT region");
+// Split output transform (m > 4096): one 16-chunk tile of M . Y1 per
+// work-group, staged here for the per-chunk 256-point transforms (the LUT,
+// table and reduction regions are dead by then; Y is untouched).
+constexpr int kOffZ2 = 16384;
+static_assert(kOffZ2 >= kOffMl + kMBytes && kOffZ2 + 16 * kYStride * 4 <= kOffY, "tile stage fits below Y");
 static_assert(kRedSlots * kRedSlot * 4 >= 4096, "table staging fits the reduction buffer");
 static_assert(kRedSlots * 16 * kMaxB * 4 == kThreads && kRedSlots * 16 * 8 == kThreads,
               "one reduction pass: 8 threads per output at B = 1, 4 at B = 2");
 
 
-// OCPW: output chunks of 256 per wave in the output transform (1: m <= 4096,
-// 3: m <= 12288), which sizes the registers the polling tail keeps live.
+// OCPW: output side.  1 (m <= 4096): the job's first work-group applies the
+// whole output transform, 256-point transforms first.  3 (m <= 12288): the
+// output transform is split over the job's first ceil(m / 4096) work-groups,
+// M first (see the completion section).
 template <bool HAS2, bool SB, int OCPW>
 __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
@@ -383,10 +390,15 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   }
   }
 
-  // 4. completion: the job's first work-group waits for every tagged
-  //    partial sum of this launch and applies the output transform
-  if (!J.out_in_kernel || lb != 0) return;
-  {
+  // 4. completion: the tail work-group(s) of the job wait for every tagged
+  //    partial sum of this launch and apply the output transform
+  if (!J.out_in_kernel) return;
+  if (OCPW == 1 || J.Sm <= kWaves) {
+    // m <= 4096, in either instantiation (a linear's output does not depend
+    // on the others of its group): the job's first work-group, one output
+    // chunk per wave, 256-point transforms first
+    if (lb != 0) return;
+    constexpr int OC = 1;
     // Output chunk stage on the matrix cores (mstage_tile): lane (q, r16) of
     // wave w produces column t = 16 w + r16 of rows r = 16 a + 4 q + j.
     const int Sm = J.Sm;
@@ -395,12 +407,9 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
     // factor), the first partial-sum slots, su and bias, all in flight
     // together (unconditional loads from valid addresses, selected where they
     // are used: a load under a branch is waited for at the branch's end).
-    // With three output chunks per wave su and bias are loaded once the slots
-    // are in instead (their registers would not fit beside the slots); the
-    // transforms in between hide most of that round trip.
     float kmv[3];
     mmat_load(kmv, Sm, J.lsh_m, J.pm, J.Km, tid);
-    float suo[OCPW][4], bio[OCPW][4];
+    float suo[OC][4], bio[OC][4];
     // no bias: a dummy load from the partial-sum slots (at least m floats;
     // su may be m / 32 words of sign bits), never used: the bias term is
     // selected, not multiplied by 0, so a non-finite dummy cannot reach the
@@ -409,7 +418,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
     const bool has_bias = J.bias != nullptr;
     auto load_su_bias = [&]() {
 #pragma unroll
-      for (int a = 0; a < OCPW; ++a)
+      for (int a = 0; a < OC; ++a)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int r = 16 * a + 4 * q + j;
@@ -430,33 +439,32 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
     // no address arithmetic is hoisted out of a loop and kept live (and
     // spilled) across the polling
     auto row = [&](const int b) {
-      PollState<OCPW> ps;
+      PollState<OC> ps;
       poll_issue(J.y1t, J.m, Sm, A.B, b, w, lane, tag, ps);
       if (b == 0) {
-        if (OCPW == 1) load_su_bias();
+        load_su_bias();
         mmat_store(kmv, Sm, J.lsh_m, Mh, Ml, tid);  // waits for the K loads only
       }
-      float zv[OCPW][4];
+      float zv[OC][4];
       poll_finish(J.y1t, J.m, Sm, A.SG, A.B, b, w, lane, tag, ps, zv);
-      if (b == 0 && OCPW > 1) load_su_bias();
       h256_chunks(zv, Sm, lane, lx);
       if (b > 0) __syncthreads();  // the previous row's reads of Y are done
       store_chunks_lanes(Y, Sm, w, lane, zv);
       __syncthreads();  // chunks (and, the first time, M) complete
       const float mul = mul0 * (b == 0 ? emul0 : emul1);
-      floatx4 acc[OCPW];
+      floatx4 acc[OC];
 #pragma unroll
-      for (int a = 0; a < OCPW; ++a) acc[a] = floatx4{0.f, 0.f, 0.f, 0.f};
+      for (int a = 0; a < OC; ++a) acc[a] = floatx4{0.f, 0.f, 0.f, 0.f};
       for (int kb = 0; kb < nkb; ++kb) {
         const ZOperand z = z_operand(Y, Sm, t, q, kb);
 #pragma unroll
-        for (int a = 0; a < OCPW; ++a)
+        for (int a = 0; a < OC; ++a)
           if (a < nrt) acc[a] = mstage_step(acc[a], Mh, Ml, 16 * a, z, kb, J.pm > 1, q, r16);
       }
-      float out[OCPW][4];
-      int oidx[OCPW][4];  // output element of out[a][j] (-1: none)
+      float out[OC][4];
+      int oidx[OC][4];  // output element of out[a][j] (-1: none)
 #pragma unroll
-      for (int a = 0; a < OCPW; ++a)
+      for (int a = 0; a < OC; ++a)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int r = 16 * a + 4 * q + j;
@@ -467,8 +475,81 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
     };
     row(0);
     if (A.B > 1) row(1);
+  } else if constexpr (OCPW > 1) {
+    // T_m = M (x) H_256 = (I (x) H_256)(M (x) I): output chunk r is
+    // H_256(z_r) with z_r = sum_c M[r][c] y1_c.  Work-group lb < ntile of the
+    // job takes the 16-chunk tile lb (tiles lb + nwg, ... when the job has
+    // fewer work-groups than tiles): it polls every slot of y1, stages the
+    // chunks in LDS, computes its tile of M . Y1 on the matrix cores (wave w:
+    // columns t = 16 w + r16), stages it, and each wave transforms output
+    // chunk r = 16 tile + w and stores it.  Each tail work-group transforms
+    // one chunk per wave instead of one work-group transforming all of them.
+    const int Sm = J.Sm;
+    const int ntile = (Sm + 15) >> 4;
+    const int nwg = J.Gr * A.SG;
+    if (lb >= ntile) return;
+    const int t = 16 * w + r16;
+    float* Z2 = reinterpret_cast<float*>(lds + kOffZ2);
+    uint16_t* Mh = reinterpret_cast<uint16_t*>(lds + kOffMh);
+    uint16_t* Ml = reinterpret_cast<uint16_t*>(lds + kOffMl);
+    float kmv[3];
+    mmat_load(kmv, Sm, J.lsh_m, J.pm, J.Km, tid);
+    const float* const bsrc = J.bias ? J.bias : reinterpret_cast<const float*>(J.y1t);  // dummy: never used
+    const bool has_bias = J.bias != nullptr;
+    const float mul0 = J.scale_m * J.layer_scale;
+    const int nkb = (Sm + 31) >> 5;
+    bool first = true;
+    for (int tile = lb; tile < ntile; tile += nwg) {
+      const int r = 16 * tile + w;  // this wave's output chunk
+      const bool rv = r < Sm;
+      // su and bias of the wave's output elements 256 r + lane + 64 j
+      // (issued before the polling; dummy element 0 for r >= Sm)
+      float suo[4], bio[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = rv ? 256 * r + lane + 64 * j : 0;
+        suo[j] = load_su(J.su, SB, i);
+        bio[j] = at_off(bsrc, (uint32_t)i);
+      }
+      auto row = [&](const int b) {
+        PollState<kCPW> ps;
+        poll_issue(J.y1t, J.m, Sm, A.B, b, w, lane, tag, ps);
+        if (first) mmat_store(kmv, Sm, J.lsh_m, Mh, Ml, tid);  // waits for the K loads only
+        float zv[kCPW][4];
+        poll_finish(J.y1t, J.m, Sm, A.SG, A.B, b, w, lane, tag, ps, zv);
+        if (!first) __syncthreads();  // the previous tile's / row's reads of Y and Z2 are done
+        first = false;
+        store_chunks_lanes(Y, Sm, w, lane, zv);
+        __syncthreads();  // chunks of y1 (and, the first time, M) complete
+        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+        for (int kb = 0; kb < nkb; ++kb)
+          acc = mstage_step(acc, Mh, Ml, 16 * tile, z_operand(Y, Sm, t, q, kb), kb, J.pm > 1, q, r16);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) Z2[(4 * q + j) * kYStride + t] = acc[j];
+        __syncthreads();  // the tile of M . Y1 is complete
+        if (rv) {
+          float v[1][4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) v[0][j] = Z2[w * kYStride + lane + 64 * j];
+          h256<1>(v, lane, lx);
+          const float mul = mul0 * (b == 0 ? emul0 : emul1);
+          float out[1][4];
+          int oidx[1][4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            oidx[0][j] = 256 * r + lane + 64 * j;
+            out[0][j] = apply_su(v[0][j] * mul, suo[j], SB, oidx[0][j]) + (has_bias ? bio[j] : 0.0f);
+          }
+          store_outputs(J.y, A.y_dtype, (int64_t)b * J.ldy, oidx, out);
+        }
+      };
+      row(0);
+      if (A.B > 1) row(1);
+    }
   }
-  // every slot of this launch has been read: the next launch's tag follows this one
+  // every slot of this launch has been read (by this work-group; any tail
+  // work-group may store it, all store the same): the next launch's tag
+  // follows this one
   if (tid == 0) __hip_atomic_store(J.epoch, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
