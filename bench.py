@@ -197,10 +197,10 @@ class Runner:
                 if p > 1 and p not in self.K:
                     self.K[p] = hartley_matrix(p, dev)
         self.plan = GROUPS if self.grouped else [(name,) for name in shape]
-        # the grouped entry point takes n a multiple of 256 up to 12288; a
-        # launch of one linear outside that range is a qs_linear_forward call
-        self.as_group = [self.grouped and shape[names[0]][1] % 256 == 0 and shape[names[0]][1] <= 12288
-                         for names in self.plan]
+        # the grouped entry point takes n a multiple of 256 (one launch at 1-2
+        # rows; one launch per stage at 3+ rows up to n = 12288, one forward
+        # per linear above)
+        self.as_group = [self.grouped and shape[names[0]][1] % 256 == 0 for names in self.plan]
         ws = 0
         for names, grp in zip(self.plan, self.as_group):
             if grp:
@@ -210,15 +210,16 @@ class Runner:
                 ws = max(ws, self.lib.qs_linear_workspace_bytes(*shape[names[0]], B, _lib.QS_LAYOUT_TILED))
         self.ws = torch.zeros(ws, dtype=torch.uint8, device=dev)  # zero before first use (epoch words)
         # per (layer, launch): the ctypes job array, built once; signs as
-        # packed bits (QS_SIGNS_BITS) where both sizes fit the chunk scheme,
-        # as QuantizedLinear passes them
+        # packed bits (QS_SIGNS_BITS) where the library takes them for this
+        # call, as QuantizedLinear passes them
+        from quipsharp_amd.quantize import sign_bits_ok
         self.jobs, self._keep = [], []
-        fits = lambda d: d % 256 == 0 and d <= 12288
         for lin in stack.layers:
             per = []
             for names in self.plan:
                 arr = (_lib.LinearJob * len(names))()
-                bits = all(fits(shape[k][0]) and fits(shape[k][1]) for k in names)
+                src = self.x if SOURCE[names[0]] is None else self.buf[SOURCE[names[0]]]
+                bits = all(sign_bits_ok(src, shape[k][0], shape[k][1]) for k in names)
                 for j, k in enumerate(names):
                     packed, su, sv = lin[k]
                     if bits:

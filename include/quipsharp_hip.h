@@ -44,7 +44,11 @@ enum { QS_LAYOUT_ROWMAJOR = 0, QS_LAYOUT_TILED = 1 };     /* packed-code layouts
  * (i % 32) of word i / 32 set for element i = -1, clear for +1 -- a 32nd of
  * the bytes every work-group of the transforms reads.  Accepted when n and m
  * are both on the chunk scheme (multiples of 256, at most 12288, length / odd
- * factor >= 256); QS_ERR_UNSUPPORTED otherwise. */
+ * factor >= 256), or for a call the one-launch kernel covers with its output
+ * transform in the launch (1-2 rows, x rows 8-byte aligned -- 16-byte for
+ * fp32 -- with a row stride that is a multiple of 4, m and n multiples of
+ * 256 up to 32768, n up to 16384 for fp16 / fp32 x); QS_ERR_UNSUPPORTED
+ * otherwise. */
 #define QS_SIGNS_BITS 0x100
 
 #define QS_ABI_VERSION 1
@@ -229,13 +233,14 @@ size_t qs_linear_group_workspace_bytes(int64_t n, int64_t batch, int count, cons
  * gate/up of a decoder layer).  No counterpart in the reference, whose
  * QuantizedLinear.forward (quipsharp/checkpoint.py:141-146) is one linear per
  * call; callers that own several linears of one input use it.
- * At 1-2 rows the group is one launch; from 3 rows each stage of the path
- * (input transforms, decode-matvecs, output transforms) is one launch for the
- * whole group, except the wide GEMM (17 rows and more), one launch per job.
- * Every output is bit-identical to qs_linear_forward of that job.
+ * At 1-2 rows the group is one launch (n up to 32768; 16384 for fp16 / fp32
+ * x); from 3 rows with n <= 12288 each stage of the path (input transforms,
+ * decode-matvecs, output transforms) is one launch for the whole group,
+ * except the wide GEMM (17 rows and more), one launch per job; otherwise one
+ * qs_linear_forward per job.  Every output is bit-identical to
+ * qs_linear_forward of that job.
  * Requirements: 1 <= count <= QS_MAX_GROUP, tiled layout, n a multiple of 256
- * with n <= 12288 and n / kron_pn >= 256, codes1 NULL for all jobs or for
- * none.  The workspace (zero before first use, see qs_linear_forward) holds
+ * with n / kron_pn >= 256, codes1 NULL for all jobs or for none.  The workspace (zero before first use, see qs_linear_forward) holds
  * one region per job.  mv_begin / mv_end bracket the decode-matvec launch (or
  * the wide GEMM launches) as in qs_linear_forward. */
 int qs_linear_forward_group(const void *x, int x_dtype, int64_t ldx, int64_t batch, int64_t n, int kron_pn,

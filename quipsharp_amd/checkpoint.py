@@ -160,13 +160,17 @@ class QuantizedLinear(nn.Module):
             cache[name] = hit
         return hit[1]
 
-    def signs(self):
-        """(su, sv) for the forward: packed sign bits (a 32nd of the fp32 bytes,
-        read by every work-group of the transforms) where both sizes fit the
-        library's chunk scheme, else the fp32 vectors.  Packed once per sign
-        buffer, outside graph capture."""
+    def signs(self, x: Tensor = None):
+        """(su, sv) for a forward of x: packed sign bits (a 32nd of the fp32
+        bytes, read by every work-group of the transforms) where the library
+        takes them (quantize.sign_bits_ok; without x: both sizes on the chunk
+        scheme), else the fp32 vectors.  Packed once per sign buffer, outside
+        graph capture."""
+        from .quantize import sign_bits_ok
         su, sv = self._fp32("su"), self._fp32("sv")
-        if not all(d % 256 == 0 and d <= 12288 for d in (self.in_features, self.out_features)):
+        m, n = self.out_features, self.in_features
+        ok = sign_bits_ok(x, m, n) if x is not None else all(d % 256 == 0 and d <= 12288 for d in (m, n))
+        if not ok:
             return su, sv
         key = (id(self.su), self.su.data_ptr(), self.su._version, id(self.sv), self.sv.data_ptr(), self.sv._version)
         if getattr(self, "_bits_key", None) != key:
@@ -217,7 +221,7 @@ class QuantizedLinear(nn.Module):
         kinds, s0, s1 = _forward_params(self.codebook, self.num_stages)
         packed = self.packed(kinds)
         ws = self._workspace(x, packed)
-        su, sv = self.signs()
+        su, sv = self.signs(x)
         return forward_packed(x, packed, su, sv, s0, s1, self._scale_f, bias=self._fp32("bias"),
                               out_dtype=x.dtype, workspace=ws)
 
@@ -232,14 +236,14 @@ class QuantizedLinear(nn.Module):
 
 def groupable(x: Tensor, linears) -> bool:
     """True when the library's grouped forward covers these linears for x (rht
-    / krht transforms, n a multiple of 256 up to 12288 with n / p >= 256, tiled
-    code layout, the same number of stages)."""
+    / krht transforms, n a multiple of 256 with n / p >= 256, tiled code
+    layout, the same number of stages)."""
     from . import _lib
     from .hadamard import kron_factor
     n = x.shape[-1] if x.dim() else 0
     rows = x.numel() // n if n else 0
     fn = kron_factor(n) if n else None
-    if not (1 <= len(linears) <= _lib.QS_MAX_GROUP and rows >= 1 and n % 256 == 0 and n <= 12288
+    if not (1 <= len(linears) <= _lib.QS_MAX_GROUP and rows >= 1 and n % 256 == 0
             and fn is not None and n // fn[0] >= 256):
         return False
     if not all(isinstance(l, QuantizedLinear) and l.transform_kind in ("rht", "krht") and l.in_features == n
@@ -277,9 +281,9 @@ def link_sibling_linears(model: nn.Module) -> int:
 def grouped_forward(x: Tensor, linears):
     """Outputs of several QuantizedLinear modules that read the same x, as one
     grouped call when the library's grouped forward covers them (rht / krht
-    transforms, n a multiple of 256 up to 12288; qs_linear_forward_group: one
-    launch at 1-2 rows, one launch per stage for the group beyond) and one call
-    each otherwise.  Each output equals ``lin(x)``.  No counterpart in the
+    transforms, n a multiple of 256; qs_linear_forward_group: one launch at
+    1-2 rows, one launch per stage for the group beyond up to n = 12288, one
+    forward per linear above) and one call each otherwise.  Each output equals ``lin(x)``.  No counterpart in the
     reference, which calls the linears one by one; meant for callers that own
     several linears of one input (q/k/v, gate/up)."""
     if not groupable(x, linears):
@@ -295,7 +299,7 @@ def _grouped(x: Tensor, linears):
     n = x.shape[-1]
     rows = x.numel() // n
     jobs = []
-    signs = [l.signs() for l in linears]
+    signs = [l.signs(x) for l in linears]
     if not all(su.dtype == torch.int32 for su, _ in signs):
         # one sign format per launch: packed bits only when every member has them
         # (a member whose out_features is off the chunk scheme, or whose bits are

@@ -107,10 +107,59 @@ __device__ __forceinline__ float flip_by_bit(float x, uint32_t b, int k) {
   return __uint_as_float(__float_as_uint(x) ^ (((b >> k) & 1u) << 31));
 }
 
-// Activation chunks of batch row b as loaded (the words of x and of sv), so
-// that a row's loads can be issued one row ahead of their use.  CPW: chunks
-// per wave the caller holds (S <= 16 CPW); the helpers below take it from
-// their array arguments.
+// One chunk's four activations t = 4 lane .. 4 lane + 3 of batch row b as
+// loaded (the words of x and of sv), so that loads can be issued ahead of
+// their use.  Sign bits: the word of elements i0 .. i0 + 3, kept raw in s.x
+// and applied by finish_chunk.
+__device__ __forceinline__ void load_chunk_raw(const XSource& X, const float* sv, int b, int c, int lane, uint4& v,
+                                               float4& s) {
+  const int i0 = 256 * c + 4 * lane;
+  if (X.sbits) s.x = __uint_as_float(reinterpret_cast<const uint32_t*>(sv)[i0 >> 5]);
+  else s = *reinterpret_cast<const float4*>(sv + i0);
+  const int64_t xi = (int64_t)b * X.ldx + i0;
+  if (X.vec && X.dtype == QS_DTYPE_F32) {
+    v = *reinterpret_cast<const uint4*>(static_cast<const float*>(X.x) + xi);
+  } else if (X.vec) {
+    const uint2 t = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(X.x) + xi);
+    v = make_uint4(t.x, t.y, 0, 0);
+  } else {
+    v = make_uint4(__float_as_uint(load_as_float(X.x, X.dtype, xi)), __float_as_uint(load_as_float(X.x, X.dtype, xi + 1)),
+                   __float_as_uint(load_as_float(X.x, X.dtype, xi + 2)),
+                   __float_as_uint(load_as_float(X.x, X.dtype, xi + 3)));
+  }
+}
+
+// The four activations times sv, as fp32.
+__device__ __forceinline__ void finish_chunk(const XSource& X, const uint4& t, const float4& s, int lane,
+                                             float (&o)[4]) {
+  float x0, x1, x2, x3;
+  if (X.vec && X.dtype == QS_DTYPE_BF16) {
+    x0 = __uint_as_float(t.x << 16), x1 = __uint_as_float(t.x & 0xFFFF0000u);
+    x2 = __uint_as_float(t.y << 16), x3 = __uint_as_float(t.y & 0xFFFF0000u);
+  } else if (X.vec && X.dtype == QS_DTYPE_F16) {
+    x0 = (float)__builtin_bit_cast(_Float16, (uint16_t)(t.x & 0xFFFFu));
+    x1 = (float)__builtin_bit_cast(_Float16, (uint16_t)(t.x >> 16));
+    x2 = (float)__builtin_bit_cast(_Float16, (uint16_t)(t.y & 0xFFFFu));
+    x3 = (float)__builtin_bit_cast(_Float16, (uint16_t)(t.y >> 16));
+  } else {
+    x0 = __uint_as_float(t.x), x1 = __uint_as_float(t.y), x2 = __uint_as_float(t.z), x3 = __uint_as_float(t.w);
+  }
+  if (X.sbits) {
+    const uint32_t b = __float_as_uint(s.x) >> (4 * (lane & 7));
+    o[0] = flip_by_bit(x0, b, 0);
+    o[1] = flip_by_bit(x1, b, 1);
+    o[2] = flip_by_bit(x2, b, 2);
+    o[3] = flip_by_bit(x3, b, 3);
+  } else {
+    o[0] = x0 * s.x;
+    o[1] = x1 * s.y;
+    o[2] = x2 * s.z;
+    o[3] = x3 * s.w;
+  }
+}
+
+// Activation chunks c = w + 16 u of batch row b (CPW: chunks per wave the
+// caller holds, S <= 16 CPW), as loaded.
 template <int CPW = kCPW>
 struct XRawT {
   uint4 v[CPW];
@@ -125,25 +174,7 @@ __device__ __forceinline__ void load_x_raw(const XSource& X, const float* sv, in
     const int c = w + kWaves * u;
     r.v[u] = make_uint4(0, 0, 0, 0);
     r.s[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (c < X.S) {
-      const int i0 = 256 * c + 4 * lane;
-      // sign bits: the word of elements i0 .. i0 + 3, kept raw in s.x and
-      // applied in finish_x (no wait for the load here)
-      if (X.sbits) r.s[u].x = __uint_as_float(reinterpret_cast<const uint32_t*>(sv)[i0 >> 5]);
-      else r.s[u] = *reinterpret_cast<const float4*>(sv + i0);
-      const int64_t xi = (int64_t)b * X.ldx + i0;
-      if (X.vec && X.dtype == QS_DTYPE_F32) {
-        r.v[u] = *reinterpret_cast<const uint4*>(static_cast<const float*>(X.x) + xi);
-      } else if (X.vec) {
-        const uint2 t = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(X.x) + xi);
-        r.v[u] = make_uint4(t.x, t.y, 0, 0);
-      } else {
-        r.v[u] = make_uint4(__float_as_uint(load_as_float(X.x, X.dtype, xi)),
-                            __float_as_uint(load_as_float(X.x, X.dtype, xi + 1)),
-                            __float_as_uint(load_as_float(X.x, X.dtype, xi + 2)),
-                            __float_as_uint(load_as_float(X.x, X.dtype, xi + 3)));
-      }
-    }
+    if (c < X.S) load_chunk_raw(X, sv, b, c, lane, r.v[u], r.s[u]);
   }
 }
 
@@ -156,33 +187,7 @@ __device__ __forceinline__ void finish_x(const XSource& X, const XRawT<CPW>& r, 
     const int c = w + kWaves * u;
 #pragma unroll
     for (int j = 0; j < 4; ++j) v[u][j] = 0.0f;
-    if (c < X.S) {
-      const uint4 t = r.v[u];
-      float x0, x1, x2, x3;
-      if (X.vec && X.dtype == QS_DTYPE_BF16) {
-        x0 = __uint_as_float(t.x << 16), x1 = __uint_as_float(t.x & 0xFFFF0000u);
-        x2 = __uint_as_float(t.y << 16), x3 = __uint_as_float(t.y & 0xFFFF0000u);
-      } else if (X.vec && X.dtype == QS_DTYPE_F16) {
-        x0 = (float)__builtin_bit_cast(_Float16, (uint16_t)(t.x & 0xFFFFu));
-        x1 = (float)__builtin_bit_cast(_Float16, (uint16_t)(t.x >> 16));
-        x2 = (float)__builtin_bit_cast(_Float16, (uint16_t)(t.y & 0xFFFFu));
-        x3 = (float)__builtin_bit_cast(_Float16, (uint16_t)(t.y >> 16));
-      } else {
-        x0 = __uint_as_float(t.x), x1 = __uint_as_float(t.y), x2 = __uint_as_float(t.z), x3 = __uint_as_float(t.w);
-      }
-      if (X.sbits) {
-        const uint32_t b = __float_as_uint(r.s[u].x) >> (4 * (lane & 7));
-        v[u][0] = flip_by_bit(x0, b, 0);
-        v[u][1] = flip_by_bit(x1, b, 1);
-        v[u][2] = flip_by_bit(x2, b, 2);
-        v[u][3] = flip_by_bit(x3, b, 3);
-      } else {
-        v[u][0] = x0 * r.s[u].x;
-        v[u][1] = x1 * r.s[u].y;
-        v[u][2] = x2 * r.s[u].z;
-        v[u][3] = x3 * r.s[u].w;
-      }
-    }
+    if (c < X.S) finish_chunk(X, r.v[u], r.s[u], lane, v[u]);
   }
 }
 

@@ -41,7 +41,7 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 constexpr int kMaxParts = 16;  // work-groups per batch row for odd-factor transforms
 
 struct WsLayout {
-  size_t x2h, sg, xtot, xmul, x2, y1p, y1t, total;
+  size_t x2h, sg, xtot, xmul, x2, y1p, y1t, h2t, total;
   int S, SG, W;
   bool wide;
 };
@@ -78,9 +78,10 @@ int cu_count() {
 
 // The first 256 bytes of every workspace hold the one-launch kernel's epoch
 // (the tag of its last launch's partial sums; zero before the first call).
-// With the tiled layout the next region holds that kernel's tagged partial
-// sums (8 bytes per slot, up to two rows), which no other kernel writes, so a
-// slot can only carry a tag of an earlier launch of the same workspace.
+// With the tiled layout the next regions hold that kernel's tagged partial
+// sums (8 bytes per slot, up to two rows) and tagged chunk transforms (its
+// two-level output transform), which no other kernel writes, so a slot can
+// only carry a tag of an earlier launch of the same workspace.
 WsLayout ws_layout(int64_t m, int64_t n, int64_t batch, int layout) {
   WsLayout L{};
   L.wide = layout == QS_LAYOUT_TILED && batch >= kWideMinBatch;
@@ -91,6 +92,7 @@ WsLayout ws_layout(int64_t m, int64_t n, int64_t batch, int layout) {
     L.SG = (L.S + kMaxWaves - 1) / kMaxWaves;
     L.W = (L.S + L.SG - 1) / L.SG;
     L.y1t = off; off = align256(off + (size_t)L.SG * 2 * m * 8);
+    L.h2t = off; off = align256(off + (size_t)2 * m * 8);
     const size_t xrows = (size_t)(B + 15) / 16 * 16;  // fragment-major rows: 16s
     L.x2h = off; off = align256(off + xrows * n * 2);
     L.sg = off; off = align256(off + xrows * (n / 8) * 2);
@@ -873,9 +875,15 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
   rc = check_transform(m, kron_pm, kron_m, "output");
   if (rc) return rc;
   if (sbits) {
-    QS_SUPPORTED(layout == QS_LAYOUT_TILED && chunk_transform_fits(n, kron_pn) && chunk_transform_fits(m, kron_pm),
-                 "packed sign bits need the tiled layout with n and m on the chunk scheme (got m %lld, n %lld)",
-                 (long long)m, (long long)n);
+    // every kernel of the chunk scheme reads sign bits; beyond it, the
+    // one-launch kernel with its output transform in the launch
+    const bool one = layout == QS_LAYOUT_TILED && fused_eligible(batch, n, x_dtype, kron_pn) &&
+                     fused_x_aligned(x, x_dtype, ldx) && fused_output_in_kernel(m, kron_pm);
+    QS_SUPPORTED(one || (layout == QS_LAYOUT_TILED && chunk_transform_fits(n, kron_pn) &&
+                         chunk_transform_fits(m, kron_pm)),
+                 "packed sign bits need the tiled layout with n and m on the chunk scheme, or a one-launch "
+                 "call (1-2 aligned rows, m and n up to 32768) (got m %lld, n %lld, %lld rows)",
+                 (long long)m, (long long)n, (long long)batch);
     QS_REQUIRE((reinterpret_cast<uintptr_t>(sv) & 3) == 0 && (reinterpret_cast<uintptr_t>(su) & 3) == 0,
                "packed sign bits must be 4-byte aligned");
   }
@@ -893,7 +901,7 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
 
   hipStream_t s = as_stream(stream);
   char* ws = static_cast<char*>(workspace);
-  if (layout == QS_LAYOUT_TILED && fused_eligible(batch, n, m, kron_pn) &&
+  if (layout == QS_LAYOUT_TILED && fused_eligible(batch, n, x_dtype, kron_pn) && fused_x_aligned(x, x_dtype, ldx) &&
       (reinterpret_cast<uintptr_t>(sv) & (sbits ? 3 : 15)) == 0) {
     FusedJobDesc d{};
     d.codes0 = codes0;
@@ -913,6 +921,7 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
     d.xmul = reinterpret_cast<float*>(ws + W.xmul);
     d.y1p = reinterpret_cast<float*>(ws + W.y1p);
     d.y1t = reinterpret_cast<unsigned long long*>(ws + W.y1t);
+    d.h2t = reinterpret_cast<unsigned long long*>(ws + W.h2t);
     rc = launch_linear_fused(x, x_dtype, ldx, (int)batch, (int)n, kron_pn, kron_n, y_dtype, sbits, 1, &d, W.S, W.SG,
                              W.W,
                              cu_count(), s, reinterpret_cast<hipEvent_t>(mv_begin),
@@ -989,19 +998,21 @@ extern "C" int qs_linear_forward_noalloc(const void* x, int x_dtype, int64_t ldx
 // Grouped workspace.  First one block per job for the one-launch kernel
 // (1-2 rows), at offsets that do not depend on the call's row count (the
 // job's epoch word must survive calls of any row count): [epoch | row
-// multipliers | tagged partial sums of up to two rows | fp32 partial sums of
-// up to two rows (output transform in a separate kernel)]; then one ws_layout
+// multipliers | tagged partial sums of up to two rows | tagged chunk
+// transforms of up to two rows | fp32 partial sums of up to two rows (output
+// transform in a separate kernel)]; then one ws_layout
 // region per job for the kernels of wider calls.  Only one-launch calls of
 // the job write its tagged slots.
 struct FusedBlock {
-  size_t xmul, y1t, y1p, total;  // the epoch at offset 0
+  size_t xmul, y1t, h2t, y1p, total;  // the epoch at offset 0
 };
 FusedBlock fused_block(int64_t m, int64_t n) {
   const WsLayout W = ws_layout(m, n, 2, QS_LAYOUT_TILED);
   FusedBlock F{};
   F.xmul = 256;
   F.y1t = F.xmul + 256;
-  F.y1p = F.y1t + align256((size_t)W.SG * 2 * (size_t)m * 8);
+  F.h2t = F.y1t + align256((size_t)W.SG * 2 * (size_t)m * 8);
+  F.y1p = F.h2t + align256((size_t)2 * (size_t)m * 8);
   F.total = F.y1p + align256((size_t)W.SG * 2 * (size_t)m * 4);
   return F;
 }
@@ -1124,9 +1135,9 @@ extern "C" int qs_linear_forward_group(const void* x, int x_dtype, int64_t ldx, 
   if (batch == 0) return QS_OK;
   int rc = check_transform(n, kron_pn, kron_n, "input");
   if (rc) return rc;
-  QS_REQUIRE(chunk_transform_fits(n, kron_pn),
-             "grouped forward needs n a multiple of 256 with n <= %d and n / kron_pn >= 256 (got n %lld)", kMaxN,
-             (long long)n);
+  const bool one_launch = fused_eligible(batch, n, x_dtype, kron_pn) && fused_x_aligned(x, x_dtype, ldx);
+  QS_REQUIRE(n % 256 == 0 && n / kron_pn >= 256,
+             "grouped forward needs n a multiple of 256 with n / kron_pn >= 256 (got n %lld)", (long long)n);
   QS_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255) == 0, "workspace must be 256-byte aligned");
   size_t need = 0;
   for (int g = 0; g < count; ++g) {
@@ -1142,8 +1153,10 @@ extern "C" int qs_linear_forward_group(const void* x, int x_dtype, int64_t ldx, 
                    (reinterpret_cast<uintptr_t>(j.su) & 3) == 0,
                "job %d: packed codes and sv must be 16-byte aligned (4 bytes for sign bits)", g);
     if (j.sign_bits)
-      QS_SUPPORTED(chunk_transform_fits(j.m, j.kron_pm),
-                   "job %d: packed sign bits need m on the chunk scheme (got %lld)", g, (long long)j.m);
+      QS_SUPPORTED(one_launch ? fused_output_in_kernel(j.m, j.kron_pm)
+                              : chunk_transform_fits(n, kron_pn) && chunk_transform_fits(j.m, j.kron_pm),
+                   "job %d: packed sign bits need m and n on the chunk scheme, or a one-launch call (got m %lld)",
+                   g, (long long)j.m);
     QS_REQUIRE((j.codes1 != nullptr) == (jobs[0].codes1 != nullptr), "all jobs need the same number of stages");
     need += ws_layout(j.m, n, batch, QS_LAYOUT_TILED).total;
   }
@@ -1151,9 +1164,25 @@ extern "C" int qs_linear_forward_group(const void* x, int x_dtype, int64_t ldx, 
   QS_REQUIRE(workspace_bytes >= need, "workspace too small: %zu < %zu", workspace_bytes, need);
   hipStream_t s = as_stream(stream);
   char* ws = static_cast<char*>(workspace);
-  if (!fused_eligible(batch, n, jobs[0].m, kron_pn))
+  if (!one_launch && chunk_transform_fits(n, kron_pn))
     return forward_group_rows(x, x_dtype, ldx, batch, n, kron_pn, kron_n, count, jobs, y_dtype, ws, mv_begin, mv_end,
                               s, jobs[0].sign_bits ? 1 : 0);
+  if (!one_launch) {
+    // n outside the chunk scheme of the multi-row kernels: one forward per
+    // linear, each in its own region after the one-launch blocks
+    size_t off = group_prefix_bytes(count, n, [&](int g) { return jobs[g].m; });
+    for (int g = 0; g < count; ++g) {
+      const qs_linear_job& j = jobs[g];
+      const size_t bytes = ws_layout(j.m, n, batch, QS_LAYOUT_TILED).total;
+      rc = qs_linear_forward(x, x_dtype, ldx, batch, n, j.m, j.codes0, j.codes1, QS_STAGE_E8_1BIT,
+                             QS_LAYOUT_TILED | (j.sign_bits ? QS_SIGNS_BITS : 0), j.sv, j.su, kron_pn, kron_n,
+                             j.kron_pm, j.kron_m, j.s0, j.s1, j.layer_scale, j.bias, j.y, y_dtype, j.ldy, ws + off,
+                             bytes, g == 0 ? mv_begin : nullptr, g == count - 1 ? mv_end : nullptr, stream);
+      if (rc) return rc;
+      off += bytes;
+    }
+    return QS_OK;
+  }
   FusedJobDesc d[QS_MAX_GROUP];
   const WsLayout W0 = ws_layout(jobs[0].m, n, batch, QS_LAYOUT_TILED);
   size_t off = 0;  // the job's block
@@ -1178,6 +1207,7 @@ extern "C" int qs_linear_forward_group(const void* x, int x_dtype, int64_t ldx, 
     d[g].xmul = reinterpret_cast<float*>(ws + off + F.xmul);
     d[g].y1p = reinterpret_cast<float*>(ws + off + F.y1p);
     d[g].y1t = reinterpret_cast<unsigned long long*>(ws + off + F.y1t);
+    d[g].h2t = reinterpret_cast<unsigned long long*>(ws + off + F.h2t);
     off += F.total;
   }
   rc = launch_linear_fused(x, x_dtype, ldx, (int)batch, (int)n, kron_pn, kron_n, y_dtype, jobs[0].sign_bits ? 1 : 0,

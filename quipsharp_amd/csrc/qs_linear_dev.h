@@ -23,12 +23,14 @@ struct FusedJobDesc {
   float* xmul;          // workspace: [B] activation scales
   float* y1p;           // workspace: [SG][B][m] fp32 partial sums (output transform in a separate kernel)
   unsigned long long* y1t;  // workspace: [SG][B][m] tagged partial sums (output transform in the kernel)
+  unsigned long long* h2t;  // workspace: [B][m] tagged chunk transforms (output transform in two levels)
 };
 
 int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, int pn, const float* Kn, int y_dtype,
                         int sbits, int count, const FusedJobDesc* jobs, int S, int SG, int W, int ncu, hipStream_t stream,
                         hipEvent_t ev_start, hipEvent_t ev_stop);
-bool fused_eligible(int64_t batch, int64_t n, int64_t m, int pn);
+bool fused_eligible(int64_t batch, int64_t n, int x_dtype, int pn);
+bool fused_x_aligned(const void* x, int x_dtype, int64_t ldx);
 bool fused_output_in_kernel(int64_t m, int pm);
 
 // One pass (up to 16 rows) of the batched forward (qs_linear_batched.hip):

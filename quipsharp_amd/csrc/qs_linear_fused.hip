@@ -1,34 +1,38 @@
 // One-launch quantized-linear forward for decode-size batches (B <= 2,
-// n <= 12288), the path QuantizedLinear.forward takes at generation time
+// n, m <= 32768 on the chunk scheme; n <= 16384 for fp16 / fp32 activations),
+// the path QuantizedLinear.forward takes at generation time
 // (quipsharp/checkpoint.py:141-146 -> quipsharp/quantize.py:116-124).
 //
 // Transforms.  A length-n transform T_n = K_p (x) H_L (n = p L, L = 2^k >= 256)
-// is split as T_n = M (x) H_256 over the index i = 256 c + t: a 256-point
-// Walsh-Hadamard inside each chunk c (one wave, four values per lane, two
-// stages in registers and six across lanes with DPP / permlane exchanges, no
-// barrier), then the S x S matrix M = K_p (x) H_{L/256} (S = n / 256 <= 48)
-// across chunks on the matrix cores (bf16 hi + lo operands, fp32 accumulate).
+// is split as T_n = M (x) H_256 over the index i = 256 c + t, with the S x S
+// chunk matrix M = K_p (x) H_{L/256} (S = n / 256 <= 128) applied on the
+// matrix cores (bf16 hi + lo operands, fp32 accumulate) and the 256-point
+// Walsh-Hadamard inside a chunk by one wave (four values per lane, two
+// stages in registers and six across lanes with DPP / permlane exchanges).
 //
 // Work-group j owns one slice group (up to 16 slices of 256 input columns,
 // one per wave) and a strided set of 16-row blocks, so each wave's activation
 // operand stays in registers for the whole launch.  Per work-group:
-//   1. issue the activation loads, then the abs-table and K loads; the first
-//      code tiles are requested once the activations have arrived, and the
-//      byte-per-value half-codeword LUTs are built after the input transform;
-//   2. input transform (every work-group; only its own 16 rows of M): chunks
-//      -> LDS, chunk stage, fp16 operand rows scaled by 2^-e (e from the row
-//      norm) plus the per-group sums for the +-1/4 shift term, whose
-//      -1/4 sum_g S_g part is folded in per slice;
+//   1. issue the activation loads, then the abs-table and K loads; the
+//      byte-per-value half-codeword LUTs are built while they arrive;
+//   2. input transform (every work-group, only its own slices), chunk
+//      combination first: activations times sv -> chunk table (bf16) ->
+//      slice rows sum_c M[s][c] x_c on the matrix cores -> per slice (one
+//      wave) the 256-point transform -> fp16 operand row scaled by 2^-e (e
+//      from the row norm) plus the per-group sums for the +-1/4 shift term,
+//      whose -1/4 sum_g S_g part is folded in per slice; the first code
+//      tiles are requested once the chunk table is complete;
 //   3. per row block: 8 MFMAs (+1 for the shift, +8 for an E8 1-bit second
 //      stage) into one of 8 LDS slots; every 8 row blocks (and after the
 //      last) the slots are reduced across the waves and the partial sums go
-//      to the workspace as write-through stores;
-//   4. completion: the partial sums go out as 64-bit slots {value, launch
-//      tag}, one agent-scope store each, and the work-group is done; the
-//      job's first work-group, after its own row blocks, polls the slots until
-//      every one carries this launch's tag, then applies S_u T_m(.) + bias
-//      with the same chunk scheme (every m of the scheme: m = p 2^k, 256 | m,
-//      m <= 12288) and stores the tag as the workspace's new epoch.
+//      out as 64-bit slots {value, launch tag}, one agent-scope store each;
+//   4. completion: tail work-groups poll the slots until every one they need
+//      carries this launch's tag and apply S_u T_m(.) + bias: for m <= 4096
+//      the job's first work-group alone (256-point transforms, then M); for
+//      larger m in two levels, chunk transforms spread over the job's first
+//      ceil(m / 4096) work-groups (one chunk per wave, results as tagged
+//      slots), then M over 16 column groups of 16 (one work-group each).
+//      The tail work-groups then store the tag as the workspace's new epoch.
 //
 // Cross-work-group visibility.  Slots are written with agent-scope relaxed
 // atomic stores and read with agent-scope relaxed atomic loads, which on
@@ -36,9 +40,10 @@
 // per-XCD L2 copy is involved).  A 64-bit atomic store makes value and tag
 // visible together, so the reader needs no counter and the writers no wait
 // for their stores to complete (that wait plus a counter round trip cost
-// ~3 us per launch).  Only the polling work-group ever waits, and only for
-// work-groups that never wait themselves, so the launch cannot deadlock
-// whatever order its work-groups are dispatched in; the poll is bounded
+// ~3 us per launch).  A work-group only waits for work-groups that wait for
+// nothing, or (second level) for those, so no cycle of waits exists; the
+// launch progresses as long as the work-groups that poll (at most 16 per
+// linear) leave a CU free for the others, and every poll is bounded
 // (kMaxPolls, NaN outputs if exceeded).
 #include <hip/hip_ext.h>
 
@@ -54,6 +59,7 @@ constexpr int kMaxB = 2;
 constexpr int kPrefetch = 4;
 constexpr int kMaxJobs = QS_MAX_GROUP;
 constexpr int kXStride = 264;               // halves per slice row of the fp16 operand buffer
+constexpr int kMaxSF = 128;                 // chunks of 256 (n, m <= 32768; n <= 16384 for fp16 / fp32 x)
 
 // One linear of a launch.  Linears in one launch share the input x (and n);
 // each has its own codes, signs, scales, output and workspace region.
@@ -65,6 +71,7 @@ struct FusedJob {
   float s0, s1;
   float* y1p;          // [SG][B][m] fp32 partials (output transform in a separate kernel)
   unsigned long long* y1t;  // [SG][B][m] tagged partials (output transform here)
+  unsigned long long* h2t;  // [B][m] tagged chunk transforms (two-level output transform)
   unsigned* epoch;     // tag of the last launch (zero before the first)
   float* xmul;         // [B] 2^e per batch row (for a separate output kernel)
   int out_in_kernel;
@@ -80,7 +87,6 @@ struct FusedJob {
 struct FusedArgs {
   const void* x;
   int x_dtype;
-  int x_vec;  // rows of 4 elements can be loaded as one 8- or 16-byte word
   int64_t ldx;
   int B;
   int n, Sn, lsh_n, pn;
@@ -93,43 +99,201 @@ struct FusedArgs {
   FusedJob job[kMaxJobs];
 };
 
-// LDS layout (bytes).  The abs-table staging area aliases the reduction
-// buffer (the table is dead before the first row block); the output
-// transform of the last work-group reuses the LUT and Y regions.
+// LDS layout (bytes).  The abs-table staging area and the slice rows of the
+// input transform alias the reduction buffer (both are dead before the first
+// row block); the output transform reuses everything.
 constexpr int kOffHi = 0;                                   // 4096 x uint32 (four fp16 high bytes)
 constexpr int kOffLo = 16384;                               // 4096 x uint32
 constexpr int kOffLut1 = 32768;                             // 256 x uint4
 constexpr int kRedSlots = 8;                                // row blocks reduced together
 constexpr int kRedSlot = kWaves * 16 * kMaxB;               // floats per slot: [wave][row][batch]
+constexpr int kZStride = 260;                               // floats per slice row (rows 16 banks apart)
+constexpr int kRedBytes = kRedSlots * kRedSlot * 4 > 16 * kZStride * 4 ? kRedSlots * kRedSlot * 4 : 16 * kZStride * 4;
 constexpr int kOffRed = kOffLut1 + 4096;                    // kRedSlots x kRedSlot floats
-constexpr int kOffMin = kOffRed + kRedSlots * kRedSlot * 4;  // 2 x 16 x kMStride bf16: input chunk stage (hi, lo)
-constexpr int kOffTab = kOffRed;                            // 256 x uint4 (table staging, before the row blocks)
-constexpr int kOffXH = kOffMin + 2 * 16 * kMStride * 2;     // kMaxB x 16 x kXStride halves
+constexpr int kOffTab = kOffRed;                            // 256 x uint4 (table staging, before the LUTs)
+constexpr int kOffZ = kOffRed;                              // 16 x kZStride floats (slice rows)
+constexpr int kMinStride = kMaxSF + 8;                      // bf16 per row of the input chunk matrix
+constexpr int kOffMin = kOffRed + kRedBytes;                // 2 x 16 x kMinStride bf16 (hi, lo)
+constexpr int kOffXH = kOffMin + 2 * 16 * kMinStride * 2;   // kMaxB x 16 x kXStride halves
 constexpr int kOffXS = kOffXH + kMaxB * 16 * kXStride * 2;  // kMaxB x 16 x 32 halves (group sums)
-constexpr int kOffY = kOffXS + kMaxB * 16 * 32 * 2;          // kMaxS x kYStride floats
-constexpr int kOffMisc = kOffY + kMaxS * kYStride * 4;      // row norms (16 floats), last-group flag
-constexpr int kLdsBytes = kOffMisc + 128;
+constexpr int kOffMisc = kOffXS + kMaxB * 16 * 32 * 2;      // row norms (16 floats)
+constexpr int kOffXR = kOffMisc + 128;                      // chunk table (bf16, one or two planes)
+constexpr int kXRBytes = 2 * 256 * (kMaxSF / 2 + 8) * 2;    // two planes of 64 chunks
+static_assert(256 * (kMaxSF + 8) * 2 <= kXRBytes, "one plane of kMaxSF chunks fits");
+constexpr int kLdsBytes = kOffXR + kXRBytes;
 static_assert(kLdsBytes <= 160 * 1024 - 128, "LDS budget");
-// Output chunk stage (last work-group, the LUTs are dead): the chunk matrix
-// M as bf16 hi / lo parts, rows and columns padded with zeros.
+static_assert(kOffMin % 16 == 0 && kOffXR % 16 == 0 && kOffZ % 16 == 0, "16-byte aligned regions");
+// Output transform in one work-group (m <= 4096): the chunk matrix M as bf16
+// hi / lo at address 0 (48 x 64, zero-padded), the chunks in the chunk
+// table's place.
 constexpr int kOffMh = 0;
 constexpr int kOffMl = kOffMh + kMBytes;
-static_assert(kOffMl + kMBytes <= kOffLut1, "M fits the LUT region");
-// Split output transform (m > 4096): one 16-chunk tile of M . Y1 per
-// work-group, staged here for the per-chunk 256-point transforms (the LUT,
-// table and reduction regions are dead by then; Y is untouched).
-constexpr int kOffZ2 = 16384;
-static_assert(kOffZ2 >= kOffMl + kMBytes && kOffZ2 + 16 * kYStride * 4 <= kOffY, "tile stage fits below Y");
+constexpr int kOffY1 = kOffXR;
+static_assert(kOffMl + kMBytes <= kOffXR && kOffY1 + 16 * kYStride * 4 <= kLdsBytes, "one-group output fits");
+// Output transform in two levels (m > 4096): all of M (rows padded to 16,
+// columns to 32; bf16 hi / lo) at address 0, the staged columns of h of
+// both batch rows (hi / lo) in the chunk table's place.
+constexpr int kOffM2 = 0;
+constexpr int kL2Groups = 16;                               // column groups of 16
+static_assert(2 * kMaxSF * kMinStride * 2 <= kOffXR, "M of kMaxSF chunks fits below the chunk table");
+constexpr int kOffHB = kOffXR;
+static_assert(kOffHB + 2 * kMaxB * 16 * kMinStride * 2 <= kLdsBytes, "staged columns fit");
 static_assert(kRedSlots * kRedSlot * 4 >= 4096, "table staging fits the reduction buffer");
 static_assert(kRedSlots * 16 * kMaxB * 4 == kThreads && kRedSlots * 16 * 8 == kThreads,
               "one reduction pass: 8 threads per output at B = 1, 4 at B = 2");
 
+// Activation quads of the input transform: thread (w, lane) holds chunks
+// c = c0 + i (i < 4, c0 = 64 round + 4 w) of one batch row at columns
+// t = 4 lane + u (u < 4), as loaded: x words (XT: 0 bf16, 1 fp16, 2 fp32;
+// rows of x 8- / 16-byte aligned) and sv (fp32, or with SB the word of sign
+// bits).  A thread holds one quad at a time, so a chunk table of more than
+// 64 chunks takes a second round of loads.
+template <int XT, bool SB>
+struct XQuad {
+  uint32_t v[4][XT == 2 ? 4 : 2];
+  uint32_t s[4][SB ? 1 : 4];
+};
+template <int XT, bool SB>
+__device__ __forceinline__ void load_x_quad(const void* x, int64_t ldx, const float* sv, int S, int b, int c0,
+                                            int lane, XQuad<XT, SB>& r) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int k = 0; k < (XT == 2 ? 4 : 2); ++k) r.v[i][k] = 0;
+#pragma unroll
+    for (int k = 0; k < (SB ? 1 : 4); ++k) r.s[i][k] = 0;
+    const int c = c0 + i;
+    if (c < S) {
+      const int i0 = 256 * c + 4 * lane;
+      if constexpr (SB) {
+        r.s[i][0] = reinterpret_cast<const uint32_t*>(sv)[i0 >> 5];
+      } else {
+        const uint4 t = *reinterpret_cast<const uint4*>(sv + i0);
+        r.s[i][0] = t.x, r.s[i][1] = t.y, r.s[i][2] = t.z, r.s[i][3] = t.w;
+      }
+      const int64_t xi = (int64_t)b * ldx + i0;
+      if constexpr (XT == 2) {
+        const uint4 t = *reinterpret_cast<const uint4*>(static_cast<const float*>(x) + xi);
+        r.v[i][0] = t.x, r.v[i][1] = t.y, r.v[i][2] = t.z, r.v[i][3] = t.w;
+      } else {
+        const uint2 t = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(x) + xi);
+        r.v[i][0] = t.x, r.v[i][1] = t.y;
+      }
+    }
+  }
+}
+// Chunk i of the quad times sv, as fp32 (zero past the S chunks: the loads
+// left zeros).
+template <int XT, bool SB>
+__device__ __forceinline__ void finish_quad_chunk(const XQuad<XT, SB>& r, int i, int lane, float (&o)[4]) {
+  float xv[4];
+  if constexpr (XT == 0) {
+    xv[0] = __uint_as_float(r.v[i][0] << 16), xv[1] = __uint_as_float(r.v[i][0] & 0xFFFF0000u);
+    xv[2] = __uint_as_float(r.v[i][1] << 16), xv[3] = __uint_as_float(r.v[i][1] & 0xFFFF0000u);
+  } else if constexpr (XT == 1) {
+    xv[0] = (float)__builtin_bit_cast(_Float16, (uint16_t)(r.v[i][0] & 0xFFFFu));
+    xv[1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(r.v[i][0] >> 16));
+    xv[2] = (float)__builtin_bit_cast(_Float16, (uint16_t)(r.v[i][1] & 0xFFFFu));
+    xv[3] = (float)__builtin_bit_cast(_Float16, (uint16_t)(r.v[i][1] >> 16));
+  } else {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) xv[u] = __uint_as_float(r.v[i][u]);
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    if constexpr (SB) o[u] = flip_by_bit(xv[u], r.s[i][0] >> (4 * (lane & 7)), u);
+    else o[u] = xv[u] * __uint_as_float(r.s[i][u]);
+  }
+}
+// The quad into the chunk table XR[t][c] (xrs halves per column t), one
+// chunk pair at a time: the truncated bf16 high parts, and (fp16 / fp32
+// activations) the truncated remainders into the second plane XR1.  Returns
+// the quad's sum of squares.
+template <int XT, bool SB>
+__device__ __forceinline__ float store_quad(const XQuad<XT, SB>& r, uint16_t* XR0, uint16_t* XR1, int xrs, int c0,
+                                            int lane, bool store) {
+  float ss = 0.0f;
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    float a[4], c[4];
+    finish_quad_chunk(r, 2 * p, lane, a);
+    finish_quad_chunk(r, 2 * p + 1, lane, c);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      ss = __builtin_fmaf(a[u], a[u], ss);
+      ss = __builtin_fmaf(c[u], c[u], ss);
+      uint32_t h, l;
+      split_bf2(a[u], c[u], h, l);
+      const int off = (4 * lane + u) * xrs + c0 + 2 * p;
+      if (store) {
+        *reinterpret_cast<uint32_t*>(XR0 + off) = h;
+        if constexpr (XT != 0) *reinterpret_cast<uint32_t*>(XR1 + off) = l;
+      }
+    }
+  }
+  return ss;
+}
+__device__ __forceinline__ bf16x8 lds_bf16x8(const uint16_t* p) {
+  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(p));
+}
 
-// OCPW: output side.  1 (m <= 4096): the job's first work-group applies the
-// whole output transform, 256-point transforms first.  3 (m <= 12288): the
-// output transform is split over the job's first ceil(m / 4096) work-groups,
-// M first (see the completion section).
-template <bool HAS2, bool SB, int OCPW>
+// Level 1 of the two-level output transform: h_c of one batch row as tagged
+// slots h2t[row][256 c + t], element t = lane + 64 j.
+__device__ __forceinline__ void store_h2(unsigned long long* h2t, int64_t row0, int c, int lane, uint32_t tag,
+                                         const float (&z)[1][4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    __hip_atomic_store(h2t + row0 + 256 * c + lane + 64 * j, tagged(z[0][j], tag), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+// Level 2: h[c][16 g + tt] of both batch rows, v = tid + 1024 k -> (c, tt) =
+// (v / 16, v % 16), polled until every slot carries the tag (bounded: NaN
+// for a slot still missing after kMaxPolls rounds); zero for c >= Sm.
+__device__ __forceinline__ void poll_columns(const unsigned long long* h2t, int m, int Sm, int B, int g, int tid,
+                                             uint32_t tag, float (&hv)[kMaxB][2]) {
+  const unsigned long long fill = tagged(0.0f, tag);
+  unsigned long long p[kMaxB][2];
+  auto load = [&](bool only_missing) {
+#pragma unroll
+    for (int b = 0; b < kMaxB; ++b)
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int v = tid + kThreads * k, c = v >> 4, tt = v & 15;
+        const unsigned long long* src = h2t + (int64_t)b * m + 256 * c + 16 * g + tt;
+        if (only_missing) {
+          if ((uint32_t)(p[b][k] >> 32) != tag)
+            p[b][k] = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+          p[b][k] = (b < B && c < Sm) ? __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : fill;
+        }
+      }
+  };
+  load(false);
+  for (int round = 0;; ++round) {
+    bool ok = true;
+#pragma unroll
+    for (int b = 0; b < kMaxB; ++b)
+#pragma unroll
+      for (int k = 0; k < 2; ++k) ok = ok && (uint32_t)(p[b][k] >> 32) == tag;
+    if (ok) break;
+    if (round == kMaxPolls) {
+#pragma unroll
+      for (int b = 0; b < kMaxB; ++b)
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+          if ((uint32_t)(p[b][k] >> 32) != tag) p[b][k] = tagged(__builtin_nanf(""), tag);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+    load(true);
+  }
+#pragma unroll
+  for (int b = 0; b < kMaxB; ++b)
+#pragma unroll
+    for (int k = 0; k < 2; ++k) hv[b][k] = __uint_as_float((uint32_t)p[b][k]);
+}
+
+template <bool HAS2, bool SB, int XT>
 __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
   uint32_t* lut_hi = reinterpret_cast<uint32_t*>(lds + kOffHi);
@@ -138,11 +302,12 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   uint4* tab16 = reinterpret_cast<uint4*>(lds + kOffTab);
   float* red = reinterpret_cast<float*>(lds + kOffRed);
   uint16_t* MinH = reinterpret_cast<uint16_t*>(lds + kOffMin);
-  uint16_t* MinL = MinH + 16 * kMStride;
+  uint16_t* MinL = MinH + 16 * kMinStride;
   _Float16* XH = reinterpret_cast<_Float16*>(lds + kOffXH);
   _Float16* XS = reinterpret_cast<_Float16*>(lds + kOffXS);
-  float* Y = reinterpret_cast<float*>(lds + kOffY);
+  float* Z = reinterpret_cast<float*>(lds + kOffZ);
   float* wsum = reinterpret_cast<float*>(lds + kOffMisc);
+  uint16_t* XR0 = reinterpret_cast<uint16_t*>(lds + kOffXR);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -160,32 +325,38 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   const bool active = w < A.W && sl < A.S;
   const LaneX lx = lane_x_init();
 
-  // 1. loads: the activations first (the transform waits for them), then the
-  //    abs table and K; the code tiles once the activations are in, then the
-  //    launch tag.  (The table staging below waits for every load issued so
-  //    far: the compiler cannot count the activation loads' conditional paths,
-  //    so issuing the table first would only delay the activations, and the
-  //    tag, read from the device coherence point, would delay the staging.)
-  const XSource X{A.x, A.x_dtype, A.x_vec, A.ldx, A.Sn, SB ? 1 : 0};
-  XRaw xr;
-  load_x_raw(X, J.sv, 0, w, lane, xr);
+  // 1. loads: the first activation quad (the transform waits for it), then
+  //    the abs table and this wave's row of K; the code tiles once the
+  //    activations are in, then the launch tag.  (The table staging below
+  //    waits for every load issued so far: the compiler cannot count the
+  //    activation loads' conditional paths, so issuing the table first would
+  //    only delay the activations, and the tag, read from the device
+  //    coherence point, would delay the staging.)
+  XQuad<XT, SB> xr;
+  load_x_quad(A.x, A.ldx, J.sv, A.Sn, 0, 4 * w, lane, xr);
   uint4 trow = make_uint4(0, 0, 0, 0), t1row = make_uint4(0, 0, 0, 0);  // fp16 table rows
   if (tid < 256) {
     trow = *reinterpret_cast<const uint4*>(kE8Ph.w[tid]);
     if (HAS2) t1row = *reinterpret_cast<const uint4*>(kE81h.w[tid]);
   }
-  // this wave's row of the input chunk stage: M[sl][c] for c = lane (Sn <= 48)
-  const bool m_ok = active && lane < A.Sn;
-  float mk = 1.0f;
-  if (A.pn > 1 && m_ok) mk = A.Kn[(sl >> A.lsh_n) * A.pn + (lane >> A.lsh_n)];
+  // this wave's row of the input chunk matrix (slice sl): K at columns
+  // c = lane, lane + 64 (unconditional loads; sv is a dummy source without K)
+  float mk[2];
+  {
+    const float* ksrc = A.pn > 1 ? A.Kn : J.sv;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = lane + 64 * h;
+      const int ki = (A.pn > 1 && active && c < A.Sn) ? (sl >> A.lsh_n) * A.pn + (c >> A.lsh_n) : 0;
+      mk[h] = at_off(ksrc, (uint32_t)ki);
+    }
+  }
   if (tid < 256) {
     tab16[tid] = trow;
     if (HAS2) lut1[tid] = t1row;
   }
   __syncthreads();  // staged table complete
   fill_luts(tab16, lut_hi, lut_lo, tid);
-  float xv[kCPW][4];
-  finish_x(X, xr, w, lane, xv);
   // Code tiles stream through a ring of kPrefetch registers, refilled as
   // they are consumed.  The loads are unconditional (a tile past the end or
   // of an idle wave reads tile 0 instead) and the ring is unrolled, so the
@@ -209,42 +380,67 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   // changes after every slot of the launch has been read
   uint32_t epoch = 0;
 
-  // 2. input transform, one batch row at a time, into fp16 operand rows
+  // 2. input transform, one batch row at a time, chunk combination first:
+  //    T_n = M (x) H_256 = (I (x) H_256)(M (x) I).  The activation chunks go
+  //    into the chunk table XR[t][c] as bf16 (exact for bf16 activations
+  //    times signs; fp16 / fp32 activations add a plane of low parts); the
+  //    slice rows z_s = sum_c M[sl][c] x_c of this work-group come out of the
+  //    matrix cores (wave w: columns t = 16 w + r16 of all 16 rows), and wave
+  //    w applies the 256-point transform to its own slice row and writes it
+  //    as its fp16 operand row (plus the per-group sums for the +-1/4 shift
+  //    term).
+  const int Spad = (A.Sn + 31) & ~31;  // chunks padded to the matrix cores' k-steps of 32
+  const int xrs = Spad + 8;            // halves per column of the chunk table
+  uint16_t* XR1 = XR0 + 256 * xrs;
   float emul0 = 1.0f, emul1 = 1.0f;  // 2^e of batch rows 0 and 1
-  for (int b = 0; b < A.B; ++b) {
-    if (b > 0) load_x(X, J.sv, b, w, lane, xv);
-    float ss = 0.0f;
-#pragma unroll
-    for (int u = 0; u < kCPW; ++u)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) ss = __builtin_fmaf(xv[u][j], xv[u][j], ss);
+  // one batch row; called once per row rather than looped, so that no
+  // activation registers are carried from one row to the next
+  auto input_row = [&](const int b) {
+    // quads inside the padded range are stored (zeros past the S chunks);
+    // the first quad of row 0 was loaded at the start
+    if (b > 0) load_x_quad(A.x, A.ldx, J.sv, A.Sn, b, 4 * w, lane, xr);
+    float ss = store_quad(xr, XR0, XR1, xrs, 4 * w, lane, 4 * w < Spad);
+    if (Spad > 64) {
+      XQuad<XT, SB> x2;
+      load_x_quad(A.x, A.ldx, J.sv, A.Sn, b, 64 + 4 * w, lane, x2);
+      ss += store_quad(x2, XR0, XR1, xrs, 64 + 4 * w, lane, 64 + 4 * w < Spad);
+    }
     ss = wave_sum(ss, lx);
     if (lane == 0) wsum[w] = ss;
-    h256_chunks(xv, A.Sn, lane, lx);
     if (b == 0) {
-      // K (read after the barrier below), before the code loads are issued
-      // so these stores do not wait for them
-      {
-        const int hm = (1 << A.lsh_n) - 1;
-        const float v = m_ok ? ((__builtin_popcount(sl & lane & hm) & 1) ? -mk : mk) : 0.0f;
-        uint32_t hi, lo;
-        split_bf2(v, 0.0f, hi, lo);
-        MinH[w * kMStride + lane] = (uint16_t)hi;
-        MinL[w * kMStride + lane] = (uint16_t)lo;
+      // row w of M = K_p (x) H_{2^lsh} (hi / lo), zero past the S chunks and
+      // for idle waves
+      const int hm = (1 << A.lsh_n) - 1;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int c = lane + 64 * h;
+        if (c < Spad) {
+          float v = (active && c < A.Sn) ? (A.pn > 1 ? mk[h] : 1.0f) : 0.0f;
+          if (__builtin_popcount(sl & c & hm) & 1) v = -v;
+          uint32_t hi, lo;
+          split_bf2(v, 0.0f, hi, lo);
+          MinH[w * kMinStride + c] = (uint16_t)hi;
+          MinL[w * kMinStride + c] = (uint16_t)lo;
+        }
       }
-      // first code tiles (issued once the activations are in, so the
-      // activation loads do not queue behind them)
+    }
+    __syncthreads();  // chunk table, norms (and, the first time, M and the LUTs) complete
+    if (b == 0) {
+      // first code tiles (issued once the activations are in the chunk
+      // table, so the activation loads do not queue behind them and the
+      // ring's registers are not live beside them)
 #pragma unroll
       for (int k = 0; k < kPrefetch; ++k) {
         const uint32_t off = code_off(jr + k * J.Gr);
         pre[k] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(J.codes0) + off);
         if (HAS2) pre1[k] = *reinterpret_cast<const uint2*>(J.codes1 + off / 2);
       }
-      if (J.out_in_kernel) epoch = __hip_atomic_load(J.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // unconditional (a load under a branch is waited for at the branch's
+      // end, which would wait for the code tiles too); sv is a dummy source
+      // for a linear whose output transform runs in another kernel
+      epoch = __hip_atomic_load(J.out_in_kernel ? J.epoch : reinterpret_cast<unsigned*>(const_cast<float*>(J.sv)),
+                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (b > 0) __syncthreads();  // the previous row's reads of Y are done
-    store_chunks(Y, A.Sn, w, lane, xv);
-    __syncthreads();  // chunks, norms (and, the first time, the staged table and K) complete
     float norm2 = 0.0f;
 #pragma unroll
     for (int i = 0; i < kWaves; ++i) norm2 += wsum[i];
@@ -252,36 +448,47 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
     if (b == 0) emul0 = ldexpf(1.0f, e);
     else emul1 = ldexpf(1.0f, e);
     const float mul = ldexpf(A.scale_n, -e);
-    // chunk stage for this group's 16 slice rows: X2[s][t] = sum_c
-    // M[sg W + s][c] Y[c][t]; wave w computes columns t = 16 w + r16, rows
-    // s = 4 q + j, and writes them as fp16 operand rows
     {
       const int t = 16 * w + r16;
       floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-      for (int kb = 0; kb < ((A.Sn + 31) >> 5); ++kb)
-        acc = mstage_step(acc, MinH, MinL, 0, z_operand(Y, A.Sn, t, q, kb), kb, A.pn > 1, q, r16);
-      float hs[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const _Float16 h = (_Float16)(acc[j] * mul);
-        XH[(b * 16 + 4 * q + j) * kXStride + t] = h;
-        hs[j] = (float)h;
+      for (int kb = 0; kb < (Spad >> 5); ++kb) {
+        const int k0 = 32 * kb + 8 * q;
+        const bf16x8 xh = lds_bf16x8(XR0 + t * xrs + k0);
+        const bf16x8 ah = lds_bf16x8(MinH + r16 * kMinStride + k0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, xh, acc, 0, 0, 0);
+        if (A.pn > 1)
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lds_bf16x8(MinL + r16 * kMinStride + k0), xh, acc, 0, 0, 0);
+        if constexpr (XT != 0)
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, lds_bf16x8(XR1 + t * xrs + k0), acc, 0, 0, 0);
       }
-      // group sums of the fp16 values, group t / 8: lanes r16 & 7 = 0..7
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        hs[j] += lane_xor<1>(hs[j], lx);
-        hs[j] += lane_xor<2>(hs[j], lx);
-        hs[j] += lane_xor<4>(hs[j], lx);
-      }
-      if ((r16 & 7) == 0) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) XS[(b * 16 + 4 * q + j) * 32 + (t >> 3)] = (_Float16)hs[j];
-      }
+      for (int j = 0; j < 4; ++j) Z[(4 * q + j) * kZStride + t] = acc[j];
     }
-  }
-  __syncthreads();  // operand rows complete
-  // MFMA operand of lane (q, b = r16): columns 64q..64q+63 of this wave's slice
+    __syncthreads();  // slice rows complete (the chunk table and the norms are free again)
+    {
+      const float4 z4 = *reinterpret_cast<const float4*>(Z + w * kZStride + 4 * lane);
+      float v[1][4] = {{z4.x, z4.y, z4.z, z4.w}};
+      h256<1>(v, lane, lx);
+      uint32_t hw[2];
+      float hs = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const _Float16 h0 = (_Float16)(v[0][2 * k] * mul), h1 = (_Float16)(v[0][2 * k + 1] * mul);
+        hs += (float)h0;
+        hs += (float)h1;
+        hw[k] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+      }
+      *reinterpret_cast<uint2*>(XH + (b * 16 + w) * kXStride + 4 * lane) = make_uint2(hw[0], hw[1]);
+      // group sums of the fp16 values, group t / 8: lane pairs
+      hs += lane_xor<1>(hs, lx);
+      if ((lane & 1) == 0) XS[(b * 16 + w) * 32 + (lane >> 1)] = (_Float16)hs;
+    }
+    };
+  input_row(0);
+  if (A.B > 1) input_row(1);
+  __syncthreads();  // slice rows read (their LDS becomes the reduction slots)
+  // MFMA operand of lane (q, b = r16): columns 64q..64q+63 of this wave's
+  // slice (its own operand rows)
   const half8 hzero = {0, 0, 0, 0, 0, 0, 0, 0};
   half8 xb[8];
   half8 xs = hzero;
@@ -390,15 +597,15 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   }
   }
 
-  // 4. completion: the tail work-group(s) of the job wait for every tagged
+  // 4. completion: the tail work-groups of the job wait for every tagged
   //    partial sum of this launch and apply the output transform
   if (!J.out_in_kernel) return;
-  if (OCPW == 1 || J.Sm <= kWaves) {
-    // m <= 4096, in either instantiation (a linear's output does not depend
-    // on the others of its group): the job's first work-group, one output
-    // chunk per wave, 256-point transforms first
+  if (J.Sm <= kWaves) {
+    // m <= 4096: the job's first work-group, one output chunk per wave,
+    // 256-point transforms first
     if (lb != 0) return;
     constexpr int OC = 1;
+    float* Y1 = reinterpret_cast<float*>(lds + kOffY1);
     // Output chunk stage on the matrix cores (mstage_tile): lane (q, r16) of
     // wave w produces column t = 16 w + r16 of rows r = 16 a + 4 q + j.
     const int Sm = J.Sm;
@@ -448,15 +655,15 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
       float zv[OC][4];
       poll_finish(J.y1t, J.m, Sm, A.SG, A.B, b, w, lane, tag, ps, zv);
       h256_chunks(zv, Sm, lane, lx);
-      if (b > 0) __syncthreads();  // the previous row's reads of Y are done
-      store_chunks_lanes(Y, Sm, w, lane, zv);
+      if (b > 0) __syncthreads();  // the previous row's reads of Y1 are done
+      store_chunks_lanes(Y1, Sm, w, lane, zv);
       __syncthreads();  // chunks (and, the first time, M) complete
       const float mul = mul0 * (b == 0 ? emul0 : emul1);
       floatx4 acc[OC];
 #pragma unroll
       for (int a = 0; a < OC; ++a) acc[a] = floatx4{0.f, 0.f, 0.f, 0.f};
       for (int kb = 0; kb < nkb; ++kb) {
-        const ZOperand z = z_operand(Y, Sm, t, q, kb);
+        const ZOperand z = z_operand(Y1, Sm, t, q, kb);
 #pragma unroll
         for (int a = 0; a < OC; ++a)
           if (a < nrt) acc[a] = mstage_step(acc[a], Mh, Ml, 16 * a, z, kb, J.pm > 1, q, r16);
@@ -474,82 +681,139 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
       store_outputs(yp, ydt, (int64_t)b * ldy, oidx, out);
     };
     row(0);
-    if (A.B > 1) row(1);
-  } else if constexpr (OCPW > 1) {
-    // T_m = M (x) H_256 = (I (x) H_256)(M (x) I): output chunk r is
-    // H_256(z_r) with z_r = sum_c M[r][c] y1_c.  Work-group lb < ntile of the
-    // job takes the 16-chunk tile lb (tiles lb + nwg, ... when the job has
-    // fewer work-groups than tiles): it polls every slot of y1, stages the
-    // chunks in LDS, computes its tile of M . Y1 on the matrix cores (wave w:
-    // columns t = 16 w + r16), stages it, and each wave transforms output
-    // chunk r = 16 tile + w and stores it.  Each tail work-group transforms
-    // one chunk per wave instead of one work-group transforming all of them.
+    if (A.B > 1) row(1);  } else {
+    // m > 4096 (S_m = m / 256 chunks): the output transform in two levels,
+    // each spread over the job's first work-groups.
+    //  1. chunk c = 16 j + w goes to wave w of work-group j < ceil(S_m / 16):
+    //     it polls the chunk's partial sums, sums the slice groups, applies
+    //     the 256-point transform and stores h_c as tagged slots (h2t);
+    //  2. column group g (16 columns) goes to work-group g < 16: it polls
+    //     h[c][16 g .. 16 g + 15] of every chunk, stages it as bf16 hi / lo,
+    //     and wave a < ceil(S_m / 16) computes rows 16 a .. 16 a + 15 of
+    //     M . h on the matrix cores, scales them, applies su and bias and
+    //     stores them.
+    // Level 1 only waits for work-groups that never wait; level 2 only for
+    // level 1, which every work-group does before its level 2.
     const int Sm = J.Sm;
-    const int ntile = (Sm + 15) >> 4;
-    const int nwg = J.Gr * A.SG;
-    if (lb >= ntile) return;
-    const int t = 16 * w + r16;
-    float* Z2 = reinterpret_cast<float*>(lds + kOffZ2);
-    uint16_t* Mh = reinterpret_cast<uint16_t*>(lds + kOffMh);
-    uint16_t* Ml = reinterpret_cast<uint16_t*>(lds + kOffMl);
-    float kmv[3];
-    mmat_load(kmv, Sm, J.lsh_m, J.pm, J.Km, tid);
-    const float* const bsrc = J.bias ? J.bias : reinterpret_cast<const float*>(J.y1t);  // dummy: never used
-    const bool has_bias = J.bias != nullptr;
+    const int nl1 = (Sm + 15) >> 4;
+    const int nwg = J.Gr * A.SG;  // work-groups of this linear (>= 1)
+    if (lb >= kL2Groups) return;
+    for (int cg = lb; cg < nl1; cg += nwg) {
+      const int c = 16 * cg + w;
+      if (c < Sm) {
+        PollState<1> p0, p1;
+        poll_issue(J.y1t, J.m, Sm, A.B, 0, c, lane, tag, p0);
+        if (A.B > 1) poll_issue(J.y1t, J.m, Sm, A.B, 1, c, lane, tag, p1);
+        float z[1][4];
+        poll_finish(J.y1t, J.m, Sm, A.SG, A.B, 0, c, lane, tag, p0, z);
+        h256<1>(z, lane, lx);
+        store_h2(J.h2t, 0, c, lane, tag, z);
+        if (A.B > 1) {
+          poll_finish(J.y1t, J.m, Sm, A.SG, A.B, 1, c, lane, tag, p1, z);
+          h256<1>(z, lane, lx);
+          store_h2(J.h2t, J.m, c, lane, tag, z);
+        }
+      }
+    }
+    const int Smpad = (Sm + 31) & ~31;
+    const int ms = Smpad + 8;  // halves per row of M and per staged column
+    const int rows = 16 * nl1;
+    uint16_t* M2h = reinterpret_cast<uint16_t*>(lds + kOffM2);
+    uint16_t* M2l = M2h + rows * ms;
+    uint16_t* HBh = reinterpret_cast<uint16_t*>(lds + kOffHB);  // [b][tt][c]
+    uint16_t* HBl = HBh + kMaxB * 16 * ms;
+    const bool m_lo = J.pm > 1;
     const float mul0 = J.scale_m * J.layer_scale;
-    const int nkb = (Sm + 31) >> 5;
-    bool first = true;
-    for (int tile = lb; tile < ntile; tile += nwg) {
-      const int r = 16 * tile + w;  // this wave's output chunk
-      const bool rv = r < Sm;
-      // su and bias of the wave's output elements 256 r + lane + 64 j
-      // (issued before the polling; dummy element 0 for r >= Sm)
+    // no bias: a dummy load from the partial-sum slots (at least m floats),
+    // never used (the bias term is selected, not multiplied by 0)
+    const float* const bsrc = J.bias ? J.bias : reinterpret_cast<const float*>(J.y1t);
+    const bool has_bias = J.bias != nullptr;
+    {
+      // M = K_p (x) H_{2^lsh_m}, entries e = tid + 1024 i at (e / 128, e % 128)
+      // (K loads first, unconditional: su is a dummy source without K)
+      const float* ksrc = m_lo ? J.Km : J.su;
+      const int hm = (1 << J.lsh_m) - 1;
+      float kv[kMaxSF * 128 / kThreads];
+#pragma unroll
+      for (int i = 0; i < kMaxSF * 128 / kThreads; ++i) {
+        const int e = tid + kThreads * i, r = e >> 7, c = e & 127;
+        const int ki = (m_lo && r < Sm && c < Sm) ? (r >> J.lsh_m) * J.pm + (c >> J.lsh_m) : 0;
+        kv[i] = at_off(ksrc, (uint32_t)ki);
+      }
+#pragma unroll
+      for (int i = 0; i < kMaxSF * 128 / kThreads; ++i) {
+        const int e = tid + kThreads * i, r = e >> 7, c = e & 127;
+        if (r < rows && c < Smpad) {
+          float v = (r < Sm && c < Sm) ? (m_lo ? kv[i] : 1.0f) : 0.0f;
+          if (__builtin_popcount(r & c & hm) & 1) v = -v;
+          uint32_t hi, lo;
+          split_bf2(v, 0.0f, hi, lo);
+          M2h[r * ms + c] = (uint16_t)hi;
+          M2l[r * ms + c] = (uint16_t)lo;
+        }
+      }
+    }
+    for (int g2 = lb; g2 < kL2Groups; g2 += nwg) {
+      const int t = 16 * g2 + r16;  // this lane's output column
+      // su and bias of this lane's outputs (rows 16 w + 4 q + j), before the poll
       float suo[4], bio[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int i = rv ? 256 * r + lane + 64 * j : 0;
+        const int r = 16 * w + 4 * q + j;
+        const int i = (w < nl1 && r < Sm) ? 256 * r + t : 0;
         suo[j] = load_su(J.su, SB, i);
         bio[j] = at_off(bsrc, (uint32_t)i);
       }
-      auto row = [&](const int b) {
-        PollState<kCPW> ps;
-        poll_issue(J.y1t, J.m, Sm, A.B, b, w, lane, tag, ps);
-        if (first) mmat_store(kmv, Sm, J.lsh_m, Mh, Ml, tid);  // waits for the K loads only
-        float zv[kCPW][4];
-        poll_finish(J.y1t, J.m, Sm, A.SG, A.B, b, w, lane, tag, ps, zv);
-        if (!first) __syncthreads();  // the previous tile's / row's reads of Y and Z2 are done
-        first = false;
-        store_chunks_lanes(Y, Sm, w, lane, zv);
-        __syncthreads();  // chunks of y1 (and, the first time, M) complete
-        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-        for (int kb = 0; kb < nkb; ++kb)
-          acc = mstage_step(acc, Mh, Ml, 16 * tile, z_operand(Y, Sm, t, q, kb), kb, J.pm > 1, q, r16);
+      float hv[kMaxB][2];
+      poll_columns(J.h2t, J.m, Sm, A.B, g2, tid, tag, hv);
+      if (g2 != lb) __syncthreads();  // the previous group's reads of the staged columns are done
 #pragma unroll
-        for (int j = 0; j < 4; ++j) Z2[(4 * q + j) * kYStride + t] = acc[j];
-        __syncthreads();  // the tile of M . Y1 is complete
-        if (rv) {
-          float v[1][4];
+      for (int k = 0; k < 2; ++k) {
+        const int v = tid + kThreads * k, c = v >> 4, tt = v & 15;
+        if (c < Smpad) {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) v[0][j] = Z2[w * kYStride + lane + 64 * j];
-          h256<1>(v, lane, lx);
+          for (int b = 0; b < kMaxB; ++b) {
+            uint32_t hi, lo;
+            split_bf2(hv[b][k], 0.0f, hi, lo);
+            HBh[(b * 16 + tt) * ms + c] = (uint16_t)hi;
+            HBl[(b * 16 + tt) * ms + c] = (uint16_t)lo;
+          }
+        }
+      }
+      __syncthreads();  // M (the first time) and the staged columns complete
+      if (w < nl1) {
+        auto row = [&](const int b) {
+          floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+          for (int kb = 0; kb < (Smpad >> 5); ++kb) {
+            const int k0 = 32 * kb + 8 * q;
+            const bf16x8 ah = lds_bf16x8(M2h + (16 * w + r16) * ms + k0);
+            const bf16x8 bh = lds_bf16x8(HBh + (b * 16 + r16) * ms + k0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, lds_bf16x8(HBl + (b * 16 + r16) * ms + k0), acc, 0,
+                                                          0, 0);
+            if (m_lo)
+              acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lds_bf16x8(M2l + (16 * w + r16) * ms + k0), bh, acc, 0,
+                                                            0, 0);
+          }
           const float mul = mul0 * (b == 0 ? emul0 : emul1);
           float out[1][4];
           int oidx[1][4];
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            oidx[0][j] = 256 * r + lane + 64 * j;
-            out[0][j] = apply_su(v[0][j] * mul, suo[j], SB, oidx[0][j]) + (has_bias ? bio[j] : 0.0f);
+            const int r = 16 * w + 4 * q + j;
+            oidx[0][j] = r < Sm ? 256 * r + t : -1;
+            out[0][j] = apply_su(acc[j] * mul, suo[j], SB, oidx[0][j]) + (has_bias ? bio[j] : 0.0f);
           }
           store_outputs(J.y, A.y_dtype, (int64_t)b * J.ldy, oidx, out);
-        }
-      };
-      row(0);
-      if (A.B > 1) row(1);
+        };
+        row(0);
+        if (A.B > 1) row(1);
+      }
     }
   }
-  // every slot of this launch has been read (by this work-group; any tail
-  // work-group may store it, all store the same): the next launch's tag
-  // follows this one
+  // every slot of this launch has been read (by this work-group; all the
+  // tail work-groups store the same value): the next launch's tag follows
+  // this one
   if (tid == 0) __hip_atomic_store(J.epoch, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -559,18 +823,18 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
 // (qs_linear.hip).  The CUs are shared between the linears in proportion to
 // their rows; each linear's work-groups form a contiguous block of the grid.
 namespace {
-template <bool HAS2, bool SB, int OCPW>
+template <bool HAS2, bool SB, int XT>
 int launch_fused_variant(const FusedArgs& A, int wg, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop) {
   static int attr_done = 0;
   if (!attr_done) {
     hipFuncAttributes fa{};
-    QS_HIP(hipFuncGetAttributes(&fa, (const void*)linear_fused_kernel<HAS2, SB, OCPW>));
+    QS_HIP(hipFuncGetAttributes(&fa, (const void*)linear_fused_kernel<HAS2, SB, XT>));
     QS_REQUIRE(fa.sharedSizeBytes == 0, "linear_fused_kernel: static LDS would move the LUT off address 0");
-    QS_HIP(hipFuncSetAttribute((const void*)linear_fused_kernel<HAS2, SB, OCPW>, hipFuncAttributeMaxDynamicSharedMemorySize,
+    QS_HIP(hipFuncSetAttribute((const void*)linear_fused_kernel<HAS2, SB, XT>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                kLdsBytes));
     attr_done = 1;
   }
-  hipExtLaunchKernelGGL((linear_fused_kernel<HAS2, SB, OCPW>), dim3((unsigned)wg), dim3(kThreads), kLdsBytes, stream,
+  hipExtLaunchKernelGGL((linear_fused_kernel<HAS2, SB, XT>), dim3((unsigned)wg), dim3(kThreads), kLdsBytes, stream,
                         ev_start, ev_stop, 0, A);
   QS_LAUNCHED("linear_fused_kernel");
   return QS_OK;
@@ -581,13 +845,12 @@ int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, i
                         int sbits, int count, const FusedJobDesc* jobs, int S, int SG, int W, int ncu, hipStream_t stream,
                         hipEvent_t ev_start, hipEvent_t ev_stop) {
   QS_REQUIRE(count >= 1 && count <= kMaxJobs, "1..%d linears per launch", kMaxJobs);
+  QS_REQUIRE(fused_eligible(B, n, x_dtype, pn) && SG * W >= S && W <= kWaves,
+             "one-launch forward: B %d, n %d (dtype %d) outside its shapes", B, n, x_dtype);
   FusedArgs A{};
   A.x = x;
   A.x_dtype = x_dtype;
-  {
-    const uintptr_t align = x_dtype == QS_DTYPE_F32 ? 16 : 8;
-    A.x_vec = (reinterpret_cast<uintptr_t>(x) % align) == 0 && ldx % 4 == 0;
-  }
+  QS_REQUIRE(fused_x_aligned(x, x_dtype, ldx), "one-launch forward: x rows must be 8-byte (fp32: 16-byte) aligned");
   A.ldx = ldx;
   A.B = B;
   A.n = n;
@@ -627,7 +890,8 @@ int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, i
     J.y1t = d.y1t;
     J.epoch = d.epoch;
     J.xmul = d.xmul;
-    J.out_in_kernel = chunk_transform_fits(d.m, d.pm);
+    J.h2t = d.h2t;
+    J.out_in_kernel = fused_output_in_kernel(d.m, d.pm);
     if (J.out_in_kernel) {
       J.Sm = (int)(d.m / 256);
       J.lsh_m = log2_exact(d.m / d.pm / 256);
@@ -641,27 +905,26 @@ int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, i
     J.y = d.y;
     J.ldy = d.ldy;
   }
-  // output chunks per wave of the widest in-kernel output transform
-  int sm_max = 0;
-  for (int g = 0; g < count; ++g)
-    if (A.job[g].out_in_kernel && A.job[g].Sm > sm_max) sm_max = A.job[g].Sm;
-  if (sm_max <= kWaves) {
-    if (has2) return sbits ? launch_fused_variant<true, true, 1>(A, wg, stream, ev_start, ev_stop)
-                           : launch_fused_variant<true, false, 1>(A, wg, stream, ev_start, ev_stop);
-    return sbits ? launch_fused_variant<false, true, 1>(A, wg, stream, ev_start, ev_stop)
-                 : launch_fused_variant<false, false, 1>(A, wg, stream, ev_start, ev_stop);
-  }
-  if (has2) return sbits ? launch_fused_variant<true, true, kCPW>(A, wg, stream, ev_start, ev_stop)
-                         : launch_fused_variant<true, false, kCPW>(A, wg, stream, ev_start, ev_stop);
-  return sbits ? launch_fused_variant<false, true, kCPW>(A, wg, stream, ev_start, ev_stop)
-               : launch_fused_variant<false, false, kCPW>(A, wg, stream, ev_start, ev_stop);
+  const int xt = x_dtype == QS_DTYPE_BF16 ? 0 : x_dtype == QS_DTYPE_F16 ? 1 : 2;
+#define QS_FUSED_XT(H, SBITS)                                                          \
+  (xt == 0 ? launch_fused_variant<H, SBITS, 0>(A, wg, stream, ev_start, ev_stop)      \
+   : xt == 1 ? launch_fused_variant<H, SBITS, 1>(A, wg, stream, ev_start, ev_stop)    \
+             : launch_fused_variant<H, SBITS, 2>(A, wg, stream, ev_start, ev_stop))
+  if (has2) return sbits ? QS_FUSED_XT(true, true) : QS_FUSED_XT(true, false);
+  return sbits ? QS_FUSED_XT(false, true) : QS_FUSED_XT(false, false);
+#undef QS_FUSED_XT
 }
 
-bool fused_output_in_kernel(int64_t m, int pm) { return chunk_transform_fits(m, pm); }
+bool fused_output_in_kernel(int64_t m, int pm) { return m % 256 == 0 && m / 256 <= kMaxSF && m / pm >= 256; }
 
-bool fused_eligible(int64_t batch, int64_t n, int64_t m, int pn) {
-  (void)m;
-  return batch >= 1 && batch <= kMaxB && chunk_transform_fits(n, pn);
+bool fused_x_aligned(const void* x, int x_dtype, int64_t ldx) {
+  const uintptr_t align = x_dtype == QS_DTYPE_F32 ? 16 : 8;
+  return (reinterpret_cast<uintptr_t>(x) % align) == 0 && ldx % 4 == 0;
+}
+
+bool fused_eligible(int64_t batch, int64_t n, int x_dtype, int pn) {
+  const int64_t smax = x_dtype == QS_DTYPE_BF16 ? kMaxSF : kMaxSF / 2;
+  return batch >= 1 && batch <= kMaxB && n % 256 == 0 && n / 256 <= smax && n / pn >= 256;
 }
 
 }  // namespace qs

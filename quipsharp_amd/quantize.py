@@ -213,6 +213,26 @@ def check_linear_args(x: Tensor, m: int, n: int, su: Tensor, sv: Tensor, bias: T
     return bits
 
 
+def sign_bits_ok(x: Tensor, m: int, n: int) -> bool:
+    """Whether the library takes packed sign bits for a forward of x at
+    (m, n): both sizes on the chunk scheme of every path (multiples of 256 up
+    to 12288), or a call of 1-2 rows that the one-launch kernel covers with
+    its output transform in the launch (multiples of 256 up to 32768, n up to
+    16384 for fp16 / fp32 activations, rows 8-byte aligned, 16-byte for
+    fp32)."""
+    fits = lambda d: d % 256 == 0 and d <= 12288
+    if fits(m) and fits(n):
+        return True
+    rows = x.numel() // n if n and x.dim() else 0
+    nmax = 32768 if x.dtype == torch.bfloat16 else 16384
+    if not (1 <= rows <= 2 and m % 256 == 0 and m <= 32768 and n % 256 == 0 and n <= nmax):
+        return False
+    x2 = x.reshape(-1, n)
+    if x2.stride(-1) != 1:
+        return True  # the forward copies it into a fresh (aligned) buffer
+    return x2.data_ptr() % (16 if x2.dtype == torch.float32 else 8) == 0 and x2.stride(0) % 4 == 0
+
+
 def _out_rows(out: Tensor, B: int, m: int) -> Tensor:
     """``out`` as B rows of m outputs written in place: a (B, m) view with unit
     column stride (its row stride is passed to the library), never a copy."""
@@ -306,11 +326,11 @@ def forward_packed_group(x: Tensor, linears, out_dtype=None, workspace: Tensor =
     """Several linears that read the same x in one launch (qs_linear_forward_group):
     ``linears`` is a sequence of (packed, su, sv, s0, s1, layer_scale, bias);
     returns the list of outputs, each equal to ``forward_packed`` of that
-    linear.  Needs the tiled layout and n a multiple of 256 up to 12288 (one
-    launch at 1-2 rows; from 3 rows one launch per stage -- input transforms,
-    decode-matvecs, output transforms -- for the whole group, the wide GEMM
-    one launch per linear).  No counterpart in the reference (one linear per
-    call there)."""
+    linear.  Needs the tiled layout and n a multiple of 256 (one launch at 1-2
+    rows; from 3 rows with n up to 12288 one launch per stage -- input
+    transforms, decode-matvecs, output transforms -- for the whole group, the
+    wide GEMM one launch per linear; one forward per linear otherwise).  No
+    counterpart in the reference (one linear per call there)."""
     count = len(linears)
     if not 1 <= count <= _lib.QS_MAX_GROUP:
         raise ValueError(f"1..{_lib.QS_MAX_GROUP} linears per group, got {count}")

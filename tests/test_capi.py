@@ -91,8 +91,8 @@ def test_group_argument_errors(L):
     rc = L.qs_linear_forward_group(ct.c_void_p(256), 0, 4096, 1, 4096, 1, None, 5, jobs, 0, ct.c_void_p(256), 1 << 20,
                                    None, None, None)
     assert rc == 1 and b"count" in L.qs_last_error()
-    rc = L.qs_linear_forward_group(ct.c_void_p(256), 0, 16384, 3, 16384, 1, None, 1, jobs, 0, ct.c_void_p(256),
-                                   1 << 20, None, None, None)  # n = 2^14 > 12288: outside the chunk scheme
+    rc = L.qs_linear_forward_group(ct.c_void_p(256), 0, 384, 3, 384, 3, ct.c_void_p(256), 1, jobs, 0,
+                                   ct.c_void_p(256), 1 << 20, None, None, None)  # n = 3 x 128: not a multiple of 256
     assert rc == 1 and b"grouped forward needs n" in L.qs_last_error()
 
 

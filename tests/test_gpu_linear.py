@@ -448,9 +448,6 @@ def test_forward_group_rejects(dev):
         forward_packed_group(x, [a] * 5)
     with pytest.raises(QuipHipError, match="stages"):
         forward_packed_group(x, [a, b])
-    c = _rand_linear(dev, rng, 1024, 25600)  # n outside the chunk scheme (25 x 1024 > 12288)
-    with pytest.raises(QuipHipError, match="grouped forward needs n"):
-        forward_packed_group(torch.randn(3, 25600, device=dev), [c])
 
 
 def _dense_weights(codes0, codes1, s0, s1):
@@ -529,10 +526,13 @@ def test_packed_sign_bits_rejected_outside_chunk_scheme(dev):
     from quipsharp_amd.quantize import forward_packed, pack_signs
     rng = np.random.default_rng(9)
     packed, su, sv, s0, s1, ls, bias = _rand_linear(dev, rng, 13312, 1024)  # m = 52 chunks of 256, beyond 48
-    x = torch.randn(1, 1024, device=dev)
-    forward_packed(x, packed, su, sv, s0, s1, ls)
+    x3 = torch.randn(3, 1024, device=dev)  # three rows: the multi-row kernels' chunk scheme ends at 48
+    forward_packed(x3, packed, su, sv, s0, s1, ls)
     with pytest.raises(QuipHipError):
-        forward_packed(x, packed, pack_signs(su), pack_signs(sv), s0, s1, ls)
+        forward_packed(x3, packed, pack_signs(su), pack_signs(sv), s0, s1, ls)
+    x = torch.randn(1, 1024, device=dev)  # one row: the one-launch kernel takes them
+    assert torch.equal(forward_packed(x, packed, pack_signs(su), pack_signs(sv), s0, s1, ls),
+                       forward_packed(x, packed, su, sv, s0, s1, ls))
     with pytest.raises(ValueError):
         forward_packed(x, packed, pack_signs(su), sv, s0, s1, ls)
     from quipsharp_amd.quantize import forward_packed_group
