@@ -56,6 +56,9 @@ MODELS = {
     "qwen25_7b": dict(title="Qwen2.5-7B", layers=36, stages=1,
                       lin=[("q", 3584, 3584), ("k", 512, 3584), ("v", 512, 3584), ("o", 3584, 3584),
                            ("gate", 18944, 3584), ("up", 18944, 3584), ("down", 3584, 18944)]),
+    "qwen3_32b": dict(title="Qwen3-32B", layers=64, stages=1,
+                      lin=[("q", 8192, 5120), ("k", 1024, 5120), ("v", 1024, 5120), ("o", 5120, 8192),
+                           ("gate", 25600, 5120), ("up", 25600, 5120), ("down", 5120, 25600)]),
 }
 LLAMA2_7B = MODELS["llama2_7b"]["lin"]
 GROUPS = [("q", "k", "v"), ("o",), ("gate", "up"), ("down",)]   # linears of one launch, per layer
@@ -145,7 +148,11 @@ class Stack:
         gen = torch.Generator(device=dev).manual_seed(0)
         cpu_gen = torch.Generator().manual_seed(0)
         f16 = lambda v: float(torch.tensor(v, dtype=torch.float16).float())
-        self.s0, self.s1, self.scale = 1.0, f16(0.47) if self.stages == 2 else 0.0, f16(0.0135)
+        self.s0, self.s1 = 1.0, f16(0.47) if self.stages == 2 else 0.0
+        # layer scale per linear ~ 0.86 / sqrt(n): each linear keeps the
+        # activation norm about level, so a deep stack of random layers stays
+        # finite (0.0135 at n = 4096)
+        self.scales = {name: f16(0.0135 * math.sqrt(4096 / n)) for name, _, n in spec["lin"]}
         self.layers = []
         for _ in range(layers or spec["layers"]):
             lin = {}
@@ -173,6 +180,8 @@ class Runner:
     input as one group (qs_linear_forward_group: q/k/v, gate/up; one launch at
     batch 1-2, one launch per stage of the path beyond); otherwise one
     qs_linear_forward per linear (the reference's call pattern)."""
+
+    only = None  # index into plan: steps of that launch only
 
     def __init__(self, stack, B, grouped=True):
         import ctypes
@@ -231,7 +240,7 @@ class Runner:
                                             None if packed.codes1 is None else packed.codes1.data_ptr(), m,
                                             su.data_ptr(), sv.data_ptr(), km,
                                             self.K[km].data_ptr() if km > 1 else None, stack.s0, stack.s1,
-                                            stack.scale, None, self.buf[k].data_ptr(), m, 1 if bits else 0)
+                                            stack.scales[k], None, self.buf[k].data_ptr(), m, 1 if bits else 0)
                 per.append(arr)
             self.jobs.append(per)
 
@@ -257,18 +266,26 @@ class Runner:
             _lib.check(rc)
 
     def step(self):
+        """One step: every launch of every layer (with ``only`` set, just
+        that launch of each layer, reading its usual input buffer)."""
         import torch
         stream = torch.cuda.current_stream(self.stack.dev).cuda_stream
         x = self.x
         for li in range(len(self.stack.layers)):
             for gi, names in enumerate(self.plan):
+                if self.only is not None and gi != self.only:
+                    continue
                 src = x if SOURCE[names[0]] is None else self.buf[SOURCE[names[0]]]
                 self._launch(li, gi, names, src, stream)
-            x = self.buf["down"]
-        return self.buf["down"]
+            if self.only is None:
+                x = self.buf["down"]
+        return self.out()
+
+    def out(self):
+        return self.buf["down" if self.only is None else self.plan[self.only][-1]]
 
     def launches_per_step(self):
-        return len(self.stack.layers) * len(self.plan)
+        return len(self.stack.layers) * (len(self.plan) if self.only is None else 1)
 
     def bytes_per_step(self):
         st = self.stack.stages
@@ -296,6 +313,8 @@ def time_graph(runner, steps, warmup):
     dev = runner.stack.dev
     ref = runner.step().clone()
     torch.cuda.synchronize()
+    if not torch.isfinite(ref).all():
+        raise RuntimeError("the stack's outputs are not finite")
     s = torch.cuda.Stream(device=dev)
     s.wait_stream(torch.cuda.current_stream(dev))
     with torch.cuda.stream(s):
@@ -308,7 +327,7 @@ def time_graph(runner, steps, warmup):
     for _ in range(max(warmup, 1)):
         graph.replay()
     torch.cuda.synchronize()
-    if not torch.equal(runner.buf["down"], ref):
+    if not torch.equal(runner.out(), ref):
         raise RuntimeError("graph replay differs from the eager step")
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     torch.cuda.synchronize()
@@ -317,7 +336,7 @@ def time_graph(runner, steps, warmup):
         graph.replay()
         ev[i + 1].record()
     torch.cuda.synchronize()
-    if not torch.equal(runner.buf["down"], ref):
+    if not torch.equal(runner.out(), ref):
         raise RuntimeError("graph replays are not reproducible")
     per = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
     del graph
@@ -546,13 +565,35 @@ def stack_batches(key, batches, steps, warmup, dev):
         r = Runner(stack, B)
         t = time_graph(r, steps, warmup)
         ms = t["mean_ms"]
-        out["batches"].append({"batch": B, "ms_per_step": round(ms, 4), "median_ms_per_step": round(t["median_ms"], 4),
-                               "GBps": round(r.bytes_per_step() / ms / 1e6, 1), "tok_per_s": round(B * 1e3 / ms, 1),
-                               "launches_per_step": r.launches_per_step()})
-        log(f"{key} batch {B}: {ms:.3f} ms/step, {r.bytes_per_step() / ms / 1e6:.1f} GB/s")
+        rec = {"batch": B, "ms_per_step": round(ms, 4), "median_ms_per_step": round(t["median_ms"], 4),
+               "GBps": round(r.bytes_per_step() / ms / 1e6, 1), "tok_per_s": round(B * 1e3 / ms, 1),
+               "launches_per_step": r.launches_per_step()}
+        if B <= 2:
+            rec["launches"] = launch_rates(r, steps, warmup)
+        out["batches"].append(rec)
+        log(f"{key} batch {B}: {ms:.3f} ms/step, {r.bytes_per_step() / ms / 1e6:.1f} GB/s"
+            + "".join(f"; {l['launch']} {l['us_per_launch']} us {l['GBps']} GB/s" for l in rec.get("launches", [])))
         del r
     del stack
     torch.cuda.empty_cache()
+    return out
+
+
+def launch_rates(runner, steps, warmup):
+    """Per launch of each group (q+k+v, o, gate+up, down), timed alone over
+    every layer of the stack (graph replays, codes rotated through HBM): us
+    per launch and algorithmic GB/s."""
+    out = []
+    stack, B = runner.stack, runner.B
+    for gi, names in enumerate(runner.plan):
+        runner.only = gi
+        t = time_graph(runner, steps, warmup)
+        us = t["mean_ms"] * 1e3 / len(stack.layers)
+        nbytes = sum(linear_bytes(*stack.shape[k], B, stack.stages) for k in names)
+        out.append({"launch": "+".join(names), "shapes": [list(stack.shape[k]) for k in names],
+                    "us_per_launch": round(us, 2), "median_us_per_launch": round(t["median_ms"] * 1e3 / len(stack.layers), 2),
+                    "GBps": round(nbytes / us / 1e3, 1)})
+    runner.only = None
     return out
 
 
@@ -623,6 +664,10 @@ def main():
     log(f"batch 1 ({'grouped' if r1.grouped else 'per-linear'}): {ms:.3f} ms/step (median {t1['median_ms']:.3f}), "
         f"{value:.1f} GB/s, {mv_ms * 1e3:.2f} us per launch -> {achieved:.1f} GB/s")
     extra = {}
+    if r1.grouped:
+        extra["launches_b1"] = launch_rates(r1, args.steps, args.warmup)
+        log("launches: " + "; ".join(f"{l['launch']} {l['us_per_launch']} us {l['GBps']} GB/s"
+                                     for l in extra["launches_b1"]))
     if not args.skip_alt:
         # the other call pattern, for comparison
         r_alt = Runner(stack, 1, grouped=args.per_linear)
@@ -665,6 +710,7 @@ def main():
     if not args.skip_shapes:
         extra["llama3_8b_3bit_stack"] = stack_batches("llama3_8b", [1, 4, 16], args.steps, args.warmup, dev)
         extra["qwen25_7b_stack"] = stack_batches("qwen25_7b", [1], args.steps, args.warmup, dev)
+        extra["qwen3_32b_stack"] = stack_batches("qwen3_32b", [1, 8], args.steps, args.warmup, dev)
     if not args.skip_decode:
         from quipsharp_amd.decode import measure_decode
         extra["qwen3_32b_decode"] = measure_decode(new=args.decode_new, device=str(dev))

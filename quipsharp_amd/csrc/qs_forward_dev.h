@@ -83,6 +83,20 @@ __device__ __forceinline__ half8 decode_code(uint32_t wv, int c, uint32_t off_hi
   return __builtin_bit_cast(half8, make_uint4(lut_pair_lo(hv), lut_pair_hi(hv), lut_pair_lo(lv), lut_pair_hi(lv)));
 }
 
+// The two LUT words of code word c (c odd: the upper 16 bits of wv), and the
+// MFMA A operand built from them, split so that a tile's 16 LDS reads can be
+// issued together before the first operand is built.
+__device__ __forceinline__ void code_lut_words(uint32_t wv, int c, uint32_t off_hi, uint32_t off_lo, uint32_t& hv,
+                                               uint32_t& lv) {
+  const uint32_t ha = (c & 1) ? ((wv >> 18) & 0x3FFCu) : ((wv >> 2) & 0x3FFCu);
+  const uint32_t la = (c & 1) ? ((wv >> 15) & 0x3FFCu) : ((wv << 1) & 0x3FFCu);
+  hv = lds_word(off_hi + ha);
+  lv = lds_word(off_lo + la);
+}
+__device__ __forceinline__ half8 code_operand(uint32_t hv, uint32_t lv) {
+  return __builtin_bit_cast(half8, make_uint4(lut_pair_lo(hv), lut_pair_hi(hv), lut_pair_lo(lv), lut_pair_hi(lv)));
+}
+
 // fp16 shift operand of a tile: 1.0 where a code's shift bit is set.
 __device__ __forceinline__ half8 shift_operand(const uint32_t (&wd)[4]) {
   return __builtin_bit_cast(half8, make_uint4((wd[0] & 0x10001u) * 0x3C00u, (wd[1] & 0x10001u) * 0x3C00u,

@@ -528,18 +528,28 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
     if (valid) {
       // (idle waves decode tile 0 with a zero operand; their results are
       // not stored)
+      // all of the tile's LUT reads first (one LDS round trip per tile, not
+      // one per code), then the MFMAs, alternating between two accumulators
+      // so that consecutive MFMAs do not wait for each other
       const uint32_t wd[4] = {cw.x, cw.y, cw.z, cw.w};
+      uint32_t hv[8], lv[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) code_lut_words(wd[c >> 1], c, kOffHi, kOffLo, hv[c], lv[c]);
+      floatx4 acc_b = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
-        const half8 av = decode_code(wd[c >> 1], c, kOffHi, kOffLo);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, xb[c], acc, 0, 0, 0);
-        if (HAS2) {
+        const half8 av = code_operand(hv[c], lv[c]);
+        if (c & 1) acc_b = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, xb[c], acc_b, 0, 0, 0);
+        else acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, xb[c], acc, 0, 0, 0);
+        if constexpr (HAS2) {
           const uint32_t idx = ((c < 4 ? cw1.x : cw1.y) >> (8 * (c & 3))) & 0xFFu;
           acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, lut1[idx]), xb[c], acc2, 0, 0,
                                                           0);
         }
       }
       accs = __builtin_amdgcn_mfma_f32_16x16x32_f16(shift_operand(wd), xs, accs, 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] += acc_b[j];
     }
     {
       // refill this ring entry (its tile is consumed) with the tile

@@ -140,3 +140,74 @@ def test_wide_dims_graph_replays(dev):
         torch.cuda.synchronize()
         for o, e in zip(outs, eager):
             assert torch.equal(o, e), rep
+
+
+@pytest.mark.parametrize("m,n", [(5120, 25600), (5120, 8192), (8192, 5120)])
+def test_qwen3_32b_shapes_bf16_one_launch(dev, m, n):
+    """Qwen3-32B's down (n = 25600: 7 slice groups into the two-level output
+    transform), o and q shapes with bf16 activations on the one-launch path."""
+    for B in (1, 2):
+        print(f"case: qwen3 shape m={m} n={n} B={B} bf16", flush=True)
+        err = _oracle_case(dev, m, n, B, 1, 5 * m + n + B, bias=(B == 2))
+        print(f"  rel err {err:.2e}", flush=True)
+        assert err < REL_TOL, (m, n, B, err)
+
+
+def test_shared_workspace_across_job_lists(dev):
+    """One workspace for grouped calls with different job lists and single
+    calls (a decoder layer's q+k+v, o, gate+up, down at Qwen3-32B shapes, as
+    a caller that keeps one workspace may issue them), eager and replayed
+    from a HIP graph: every output equals its own call on a fresh workspace."""
+    from quipsharp_amd.quantize import forward_packed, forward_packed_group
+    rng = np.random.default_rng(32)
+    shapes = {"q": (8192, 5120), "k": (1024, 5120), "v": (1024, 5120), "o": (5120, 8192),
+              "gate": (25600, 5120), "up": (25600, 5120), "down": (5120, 25600)}
+    lin = {k: _rand_linear(dev, rng, m, n, bias=(k == "o")) for k, (m, n) in shapes.items()}
+    plan = [("q", "k", "v"), ("o",), ("gate", "up"), ("down",)]
+    src = {"q": "x", "o": "q", "gate": "o", "down": "gate"}
+    x = torch.randn(1, 5120, device=dev).bfloat16()
+    buf = {k: torch.empty(1, m, device=dev, dtype=torch.bfloat16) for k, (m, _) in shapes.items()}
+    buf["x"] = x
+    import ctypes
+    from quipsharp_amd import _lib
+    L = _lib.lib()
+    need = max(L.qs_linear_group_workspace_bytes(shapes[g[0]][1], 1, len(g),
+                                                (ctypes.c_int64 * len(g))(*[shapes[k][0] for k in g]))
+               for g in plan)
+    ws = torch.zeros(need, dtype=torch.uint8, device=dev)
+
+    def step(layers=3):
+        for _ in range(layers):
+            for g in plan:
+                forward_packed_group(buf[src[g[0]]], [lin[k] for k in g], workspace=ws, outs=[buf[k] for k in g])
+            forward_packed(buf["o"], *lin["gate"], workspace=ws, out=buf["gate"])  # a single call in between
+
+    # the same chain with a fresh workspace per call
+    want = {}
+    cur = {"x": x}
+    for _ in range(3):
+        for g in plan:
+            ys = forward_packed_group(cur[src[g[0]]], [lin[k] for k in g])
+            cur.update(dict(zip(g, ys)))
+        cur["gate"] = forward_packed(cur["o"], *lin["gate"])
+    want = {k: v.clone() for k, v in cur.items()}
+    step()
+    torch.cuda.synchronize()
+    for k in shapes:
+        assert torch.equal(buf[k], want[k]), ("eager", k)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        step()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            step()
+    torch.cuda.current_stream().wait_stream(s)
+    for rep in range(4):
+        for k in shapes:
+            buf[k].fill_(0)
+        g.replay()
+        torch.cuda.synchronize()
+        for k in shapes:
+            assert torch.equal(buf[k], want[k]), (rep, k)
