@@ -97,12 +97,14 @@ def block_ldl(H, g):
     return L.reshape(n, n)
 
 
-def quantize_steps(W, L, H, k_list, tune=False):
+def quantize_steps(W, L, H, k_list, tune=False, Wq=None, targets=None):
     """Runs the reference's per-block work for the listed blocks (timing
-    sample): feedback (or full-residual tune) product, then the E8P encode."""
+    sample): feedback (or full-residual tune) product, then the E8P encode.
+    Wq: the quantized weights so far (updated in place; zeros if None);
+    targets: a list that receives each block's target."""
     m, n = W.shape
     g = 8
-    Wq = torch.zeros_like(W)
+    Wq = torch.zeros_like(W) if Wq is None else Wq
     out = []
     dinv = None
     if tune:
@@ -116,6 +118,8 @@ def quantize_steps(W, L, H, k_list, tune=False):
         else:
             tail = slice((k + 1) * g, n)
             target = W[:, ck] + (W[:, tail] - Wq[:, tail]) @ L[tail, ck]
+        if targets is not None:
+            targets.append(target.clone())
         vals, code = e8p_encode(target)
         Wq[:, ck] = vals
         out.append(code)

@@ -426,13 +426,22 @@ __device__ __forceinline__ void load_partials(const float* y1p, int m, int Sm, i
 
 // Tagged partial sums.  Each work-group of a one-launch forward writes its
 // partial sums as 64-bit slots {fp32 value (low word), launch tag (high
-// word)} with one agent-scope store each, and the job's first work-group
-// polls the slots until every one carries this launch's tag: no completion
-// counter, no wait for the stores to complete before signalling.  The tag of
-// a launch is the workspace's epoch word plus one (zero skipped, so a zeroed
-// workspace matches no launch); the polling work-group stores it as the new
-// epoch at its end, after every slot of the launch has been read.
-__device__ __forceinline__ uint32_t next_tag(uint32_t epoch) { return epoch + 1u == 0u ? 1u : epoch + 1u; }
+// word)} with one agent-scope store each, and the tail work-groups poll the
+// slots until every one carries this launch's tag: no completion counter, no
+// wait for the stores to complete before signalling.  A tag is a quiet-NaN
+// bit pattern (fp32 NaN, and an fp16 NaN in its upper half) holding a 20-bit
+// launch counter and the job's index g in the launch (0-3), so a slot can only
+// match the launch that wrote it: other jobs' tags differ in g, earlier
+// launches of job index g in the counter (for 2^20 launches), and any other
+// data left in the workspace would have to be a NaN.  The counter continues
+// the workspace's epoch word of job index g (zero: no launch yet); the tail
+// work-groups store the tag as the new epoch once every slot they poll has
+// been read.
+constexpr uint32_t kTagBase = 0x7FC00000u;
+__device__ __forceinline__ uint32_t next_tag(uint32_t epoch, int g) {
+  const uint32_t c = (((epoch >> 2) & 0xFFFFFu) + 1u) & 0xFFFFFu;
+  return kTagBase | ((c ? c : 1u) << 2) | (uint32_t)g;
+}
 
 __device__ __forceinline__ unsigned long long tagged(float v, uint32_t tag) {
   return ((unsigned long long)tag << 32) | __float_as_uint(v);

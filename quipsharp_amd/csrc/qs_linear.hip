@@ -995,30 +995,34 @@ extern "C" int qs_linear_forward_noalloc(const void* x, int x_dtype, int64_t ldx
                            QS_NOALLOC_SCRATCH_BYTES, nullptr, nullptr, stream);
 }
 
-// Grouped workspace.  First one block per job for the one-launch kernel
-// (1-2 rows), at offsets that do not depend on the call's row count (the
-// job's epoch word must survive calls of any row count): [epoch | row
-// multipliers | tagged partial sums of up to two rows | tagged chunk
-// transforms of up to two rows | fp32 partial sums of up to two rows (output
-// transform in a separate kernel)]; then one ws_layout
-// region per job for the kernels of wider calls.  Only one-launch calls of
-// the job write its tagged slots.
+// Grouped workspace.  A 256-byte header holding the one-launch kernel's
+// epoch word of each job index (job g at byte 4 g; a single-linear call uses
+// the word of job 0, at offset 0 of its own layout too), then one block per
+// job for the one-launch kernel (1-2 rows) at offsets that do not depend on
+// the call's row count: [tagged partial sums of up to two rows | tagged chunk
+// transforms of up to two rows | row multipliers | fp32 partial sums of up to
+// two rows (output transform in a separate kernel)]; then one ws_layout
+// region per job for the kernels of wider calls.  The tags carry the job
+// index and a per-index launch counter, so calls with other job lists (or
+// single calls) sharing the workspace cannot leave slots that pass for this
+// call's.
 struct FusedBlock {
-  size_t xmul, y1t, h2t, y1p, total;  // the epoch at offset 0
+  size_t y1t, h2t, xmul, y1p, total;  // offsets within the job's block
 };
+constexpr size_t kGroupHeader = 256;
 FusedBlock fused_block(int64_t m, int64_t n) {
   const WsLayout W = ws_layout(m, n, 2, QS_LAYOUT_TILED);
   FusedBlock F{};
-  F.xmul = 256;
-  F.y1t = F.xmul + 256;
+  F.y1t = 0;
   F.h2t = F.y1t + align256((size_t)W.SG * 2 * (size_t)m * 8);
-  F.y1p = F.h2t + align256((size_t)2 * (size_t)m * 8);
+  F.xmul = F.h2t + align256((size_t)2 * (size_t)m * 8);
+  F.y1p = F.xmul + 256;
   F.total = F.y1p + align256((size_t)W.SG * 2 * (size_t)m * 4);
   return F;
 }
 template <class M>
 size_t group_prefix_bytes(int count, int64_t n, M m_of) {
-  size_t total = 0;
+  size_t total = kGroupHeader;
   for (int g = 0; g < count; ++g) total += fused_block(m_of(g), n).total;
   return total;
 }
@@ -1185,7 +1189,7 @@ extern "C" int qs_linear_forward_group(const void* x, int x_dtype, int64_t ldx, 
   }
   FusedJobDesc d[QS_MAX_GROUP];
   const WsLayout W0 = ws_layout(jobs[0].m, n, batch, QS_LAYOUT_TILED);
-  size_t off = 0;  // the job's block
+  size_t off = kGroupHeader;  // the job's block
   for (int g = 0; g < count; ++g) {
     const qs_linear_job& j = jobs[g];
     const FusedBlock F = fused_block(j.m, n);
@@ -1203,7 +1207,7 @@ extern "C" int qs_linear_forward_group(const void* x, int x_dtype, int64_t ldx, 
     d[g].bias = j.bias;
     d[g].y = j.y;
     d[g].ldy = j.ldy;
-    d[g].epoch = reinterpret_cast<unsigned*>(ws + off);
+    d[g].epoch = reinterpret_cast<unsigned*>(ws) + g;
     d[g].xmul = reinterpret_cast<float*>(ws + off + F.xmul);
     d[g].y1p = reinterpret_cast<float*>(ws + off + F.y1p);
     d[g].y1t = reinterpret_cast<unsigned long long*>(ws + off + F.y1t);

@@ -508,7 +508,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   slice_shift += lane_xor<32>(slice_shift, lx);
   if (lb == 0 && tid < A.B) J.xmul[tid] = tid == 0 ? emul0 : emul1;
 
-  const uint32_t tag = J.out_in_kernel ? next_tag(epoch) : 0u;
+  const uint32_t tag = J.out_in_kernel ? next_tag(epoch, g) : 0u;
 
   // 3. row blocks
   const int nw = A.S - sg * A.W < A.W ? A.S - sg * A.W : A.W;

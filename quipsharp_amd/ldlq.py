@@ -16,40 +16,48 @@ from torch import Tensor
 from . import _lib
 
 
+def _cholesky_escalating(M: Tensor, scale: float, base: float):
+    """Lower Cholesky factor of M.  Failure semantics of the reference
+    (quipsharp/ldlq.py:58-75): when the fp32 factorization breaks down the
+    matrix is promoted to fp64 and factored again, and on further failures
+    diagonal loading grows tenfold per attempt (base, 10 base, 100 base times
+    the mean diagonal `scale`), four fp64 attempts in all.  Returns the factor
+    and the extra loading added (0.0 when fp32 sufficed)."""
+    try:
+        return torch.linalg.cholesky(M), 0.0
+    except torch.linalg.LinAlgError:
+        pass
+    M64 = M.double()
+    eye = torch.eye(M.shape[0], device=M.device, dtype=torch.float64)
+    added = 0.0
+    for attempt in range(4):
+        try:
+            return torch.linalg.cholesky(M64), added
+        except torch.linalg.LinAlgError:
+            if attempt == 3:
+                raise
+            loading = scale * base * 10.0 ** attempt
+            M64 = M64 + loading * eye
+            added += loading
+
+
 def block_ldl(H: Tensor, g: int, damping: float = 1e-2):
     """g-block LDL, H = L @ blockdiag(D) @ L^T (quipsharp/ldlq.py:39-84).
     Returns L (n, n) unit block-lower-triangular and D (T, g, g)."""
     n = H.shape[0]
-    assert n % g == 0, f"block size {g} must evenly divide n={n}"
+    assert n % g == 0, f"block_ldl: n = {n} is not a multiple of the block size {g}"
     T = n // g
-    M = H.clone()
-    mean_diag = M.diagonal().mean()
-    if damping:
-        M += damping * mean_diag * torch.eye(n, device=H.device, dtype=H.dtype)
-    try:
-        L0 = torch.linalg.cholesky(M)
-    except torch.linalg.LinAlgError:
-        # fp32 Cholesky failed: retry in fp64, adding damping only if needed
-        M = M.double()
-        extra = 0.0
-        for attempt in range(4):
-            try:
-                L0 = torch.linalg.cholesky(M)
-                break
-            except torch.linalg.LinAlgError:
-                if attempt == 3:
-                    raise
-                step = float(mean_diag) * (damping if damping else 1e-2) * 10 ** attempt
-                extra += step
-                M += step * torch.eye(n, device=H.device, dtype=torch.float64)
-        print(f"block_ldl: fp32 Cholesky failed (n={n}); succeeded in fp64 with "
-              f"{extra / float(mean_diag):.0e} x mean_diag extra damping", flush=True)
+    mean_diag = float(H.diagonal().mean())
+    M = H + damping * mean_diag * torch.eye(n, device=H.device, dtype=H.dtype) if damping else H.clone()
+    L0, added = _cholesky_escalating(M, mean_diag, damping if damping else 1e-2)
+    if L0.dtype != H.dtype:
+        print(f"[quipsharp_amd] {n}x{n} Hessian: Cholesky needed fp64 and {added / mean_diag:.0e} x mean(diag) "
+              "of extra diagonal loading", flush=True)
+    # the g x g diagonal blocks of the Cholesky factor, then each block column
+    # of L0 times the inverse of its diagonal block (one batched product)
     DL = torch.diagonal(L0.reshape(T, g, T, g), dim1=0, dim2=2).permute(2, 0, 1).contiguous()
     D = DL @ DL.transpose(-1, -2)
-    DL_inv = torch.linalg.inv(DL)
-    # block column i of L0 times DL_inv[i], all blocks in one batched product
-    Lb = L0.reshape(n, T, g).permute(1, 0, 2).contiguous()
-    L = torch.matmul(Lb, DL_inv).permute(1, 0, 2).reshape(n, n)
+    L = torch.matmul(L0.reshape(n, T, g).transpose(0, 1), torch.linalg.inv(DL)).transpose(0, 1).reshape(n, n)
     return L.to(H.dtype), D.to(H.dtype)
 
 
