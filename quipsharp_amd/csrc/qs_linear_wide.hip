@@ -5,10 +5,14 @@
 // rows the contraction is a real GEMM: wg_kernel decodes the codes inside
 // its K loop (byte LUTs in LDS, exactly as the narrow kernels) and feeds
 // every decoded fragment to several 16 x 16 x 32 fp16 MFMAs; the codes' +-1/4
-// shifts are one extra MFMA per slice against the operand's group sums.  The
+// shifts are one extra MFMA per slice against the operand's group sums.
+// Single-stage calls of more than 128 rows take wp_kernel instead, which
+// splits decoding and multiplying between the waves of a work-group.  The
 // input and output transforms around it are the per-row kernels of the
 // batched path (qs_linear_batched.hip) or, outside the chunk scheme, the
 // LDS-radix kernels of qs_linear.hip, writing the fragment-major operand.
+#include <type_traits>
+
 #include "qs_forward_dev.h"
 #include "qs_linear_dev.h"
 
@@ -297,6 +301,242 @@ int launch_wg(const WgArgs& A, unsigned grid, hipStream_t stream) {
 }
 
 
+// ---------------------------------------------------------------------------
+// Producer / consumer variant for long single-stage batches
+// ---------------------------------------------------------------------------
+// The wave that feeds the matrix cores should issue nothing but MFMAs and
+// their operand loads: VALU work issued by that wave is not hidden behind its
+// MFMAs.  So a work-group of 8 waves splits the roles, one of each per SIMD:
+// decode waves 4..7 turn the codes of 32 weight rows each into fp16 A
+// fragments (E8P value plus the code's +-1/4 shift, exact in fp16) in the
+// 32x32x16 MFMA layout, one half slice (128 columns) at a time into a double
+// buffer in LDS; MFMA waves 0..3 each multiply all 128 weight rows by 64
+// activation rows with v_mfma_f32_32x32x16_f16 (4 x 2 accumulator tiles),
+// reading the A fragments from LDS and the B fragments from the
+// fragment-major operand through a register ring.  One barrier per half
+// slice hands the buffers over.  The tile order, slice groups and partial
+// sums are wg_kernel's (with 256 activation rows per work-group).
+//
+// A fragment (R, k) of a half slice (R: 32-row weight tile, k: 16-column
+// step) is 64 lanes x 8 fp16: lane l holds row 32 R + l % 32, columns
+// 16 k + 8 (l / 32) .. + 7, i.e. one code.  Code (tile i, lane (q, r16),
+// step c = 4 h + cc) of the packed layout holds row 16 i + r16, columns
+// 32 c + 8 q: fragment (i / 2, 2 cc + q / 2), lane 16 (i % 2) + r16 + 32 (q % 2).
+constexpr int kWpThreads = 512;
+constexpr int kWpMfmaWaves = 4;
+constexpr int kWpOffA = 32768;                  // after the byte LUTs
+constexpr int kWpABuf = 32 * 1024;              // 4 x 8 fragments of 1 KiB
+constexpr int kWpLds = kWpOffA + 2 * kWpABuf;
+constexpr int kWpRing = 8;                      // B fragment steps in flight per MFMA wave (one half slice)
+static_assert(kWpLds <= 160 * 1024, "LDS budget");
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+__global__ __launch_bounds__(kWpThreads) void wp_kernel(WgArgs A) {
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  uint32_t* lut_hi = reinterpret_cast<uint32_t*>(lds + kDqOffHi);
+  uint32_t* lut_lo = reinterpret_cast<uint32_t*>(lds + kDqOffLo);
+  uint4* tab16 = reinterpret_cast<uint4*>(lds + kWpOffA);  // staging, before the first fragments
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  // tile order as wg_kernel (XCD-contiguous runs)
+  const int T = A.nrt * A.nct * A.SGk;
+  const int per = (T + 7) >> 3;
+  int bid = ((int)blockIdx.x & 7) * per + ((int)blockIdx.x >> 3);
+  if (bid >= T) return;
+  const int rt = bid % A.nrt;
+  bid /= A.nrt;
+  const int ct = bid % A.nct;
+  const int g = bid / A.nct;
+  const int s_begin = g * A.spg;
+  const int s_end = s_begin + A.spg < A.S ? s_begin + A.spg : A.S;
+  const int s_last = s_end > s_begin ? s_end - 1 : (A.S - 1);
+
+  // every wave issues its first global loads (code words, B fragments), then
+  // builds the LUTs while they are in flight
+  auto build_luts = [&]() {
+    if (tid < 256) tab16[tid] = *reinterpret_cast<const uint4*>(kE8Ph.w[tid]);
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kFwdThreads / kWpThreads; ++r) fill_luts(tab16, lut_hi, lut_lo, tid + kWpThreads * r);
+    __syncthreads();  // LUTs complete, staging area free
+  };
+
+  const int nsl = s_end > s_begin ? s_end - s_begin : 0;  // slices of this work-group
+  using H0 = std::integral_constant<int, 0>;
+  using H1 = std::integral_constant<int, 1>;
+  if (w >= kWpMfmaWaves) {
+    // ---------------- decode waves ----------------
+    const int d = w - kWpMfmaWaves;  // weight rows 32 d .. 32 d + 31: code tiles 2 d, 2 d + 1
+    const int q = lane >> 4, r16 = lane & 15;
+    auto words = [&](int ii, int s) -> uint4 {
+      int rb = rt * 8 + 2 * d + ii;
+      rb = rb < A.RB ? rb : A.RB - 1;  // past the end: the last row block (decoded, never stored)
+      s = s < s_last ? s : s_last;
+      return *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(A.codes0) +
+                                             ((size_t)rb * A.S + s) * 1024 + 16 * lane);
+    };
+    // half h of the slice whose code words are c0 / c1 into buffer h
+    auto decode_half = [&](auto hc, const uint4& c0, const uint4& c1) {
+      constexpr int h = decltype(hc)::value;
+      char* buf = lds + kWpOffA + h * kWpABuf;
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii) {
+        const uint4& cw = ii ? c1 : c0;
+        // the two code words of steps 4 h .. 4 h + 3
+        const uint32_t wd[2] = {h ? cw.z : cw.x, h ? cw.w : cw.y};
+        uint32_t hv[4], lv[4];
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) code_lut_words(wd[cc >> 1], cc & 1, kDqOffHi, kDqOffLo, hv[cc], lv[cc]);
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+          const uint32_t sh = (wd[cc >> 1] >> (16 * (cc & 1))) & 1u;  // shift bit: +1/4 set, -1/4 clear
+          half8 v = code_operand(hv[cc], lv[cc]);
+          v = v + (sh ? (_Float16)0.25f : (_Float16)-0.25f);
+          const int kk = 2 * cc + (q >> 1);
+          const int l = 16 * ii + r16 + 32 * (q & 1);
+          *reinterpret_cast<half8*>(buf + ((d * 8 + kk) * 64 + l) * 16) = v;
+        }
+      }
+    };
+    uint4 c0 = words(0, s_begin), c1 = words(1, s_begin);
+    build_luts();
+    if (nsl > 0) decode_half(H0{}, c0, c1);
+    __syncthreads();
+    for (int sl = 0; sl < nsl; ++sl) {
+      const uint4 n0 = words(0, s_begin + sl + 1), n1 = words(1, s_begin + sl + 1);  // next slice, in flight
+      decode_half(H1{}, c0, c1);  // while the MFMA waves take half 0
+      __syncthreads();
+      c0 = n0;
+      c1 = n1;
+      if (sl + 1 < nsl) decode_half(H0{}, c0, c1);  // while they take half 1
+      __syncthreads();
+    }
+    return;
+  }
+
+  // ---------------- MFMA waves ----------------
+  const int nbt = (A.B + 15) >> 4;  // 16-row fragments of the operand
+  const int row0 = (kWpMfmaWaves * ct + w) * 64;  // this wave's activation rows row0 .. row0 + 63
+  // B fragment (t, slice s, half h, step k): lane l reads activation row row0 + 32 t + l % 32,
+  // columns 128 h + 16 k + 8 (l / 32) of the slice; fragment-major operand: 16-row fragment
+  // c16, 32-column step st of slice s at ((c16 S + s) 8 + st) 512 halves, lane' = q' 16 + r16'
+  // at 8 lane' halves, q' = 2 (k % 2) + l / 32
+  const _Float16* xrow[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int r = row0 + 32 * t + (lane & 31);
+    int c16 = r >> 4;
+    c16 = c16 < nbt ? c16 : nbt - 1;  // rows past the batch: computed, never stored
+    xrow[t] = A.x2f + (size_t)c16 * A.S * 8 * 512 + 8 * ((lane >> 5) * 16 + (r & 15));
+  }
+  // slices past the work-group's last are clamped to it: those loads are in
+  // bounds and never used, so every load is unconditional
+  auto load_b = [&](int s, int h, int k, half8 (&dst)[2]) {
+    s = s < s_last ? s : s_last;
+    const size_t off = ((size_t)s * 8 + 4 * h + (k >> 1)) * 512 + 8 * 16 * 2 * (k & 1);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) dst[t] = *reinterpret_cast<const half8*>(xrow[t] + off);
+  };
+  auto a_frag = [&](int h, int R, int k) {
+    return *reinterpret_cast<const half8*>(lds + kWpOffA + h * kWpABuf + ((R * 8 + k) * 64 + lane) * 16);
+  };
+  floatx16 acc[4][2];
+#pragma unroll
+  for (int R = 0; R < 4; ++R)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) acc[R][t] = floatx16{};
+  // ring entry k holds step k of the half slice being multiplied; step k of
+  // the next half slice (slice sn, half hn) replaces it once its MFMAs are
+  // issued, one half slice of MFMAs ahead of its use.  The scheduling
+  // barriers keep that order (and the ring in the same registers across the
+  // loop): each step reads the next step's A fragments from LDS, issues its
+  // 8 MFMAs, then its 2 ring loads.
+  half8 ring[kWpRing][2];
+  auto mfma_half = [&](auto hc, int sn, int hn) {
+    constexpr int h = decltype(hc)::value;
+    half8 a[2][4];
+#pragma unroll
+    for (int R = 0; R < 4; ++R) a[0][R] = a_frag(h, R, 0);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (k < 7) {
+#pragma unroll
+        for (int R = 0; R < 4; ++R) a[(k + 1) & 1][R] = a_frag(h, R, k + 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int R = 0; R < 4; ++R)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          acc[R][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[k & 1][R], ring[k][t], acc[R][t], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      load_b(sn, hn, k, ring[k]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  const bool wave_on = row0 < A.B;
+  if (wave_on) {
+#pragma unroll
+    for (int k = 0; k < kWpRing; ++k) {
+      load_b(s_begin, 0, k, ring[k]);  // in the order the loop issues them
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    build_luts();
+    __syncthreads();  // the first half slice's fragments are in buffer 0
+    for (int sl = 0; sl < nsl; ++sl) {
+      const int s = s_begin + sl;
+      mfma_half(H0{}, s, 1);
+      __syncthreads();  // buffer 0 free; half 1 complete
+      mfma_half(H1{}, s + 1, 0);
+      __syncthreads();  // buffer 1 free; the next slice's half 0 complete
+    }
+  } else {
+    // no activation rows: only the barriers that hand the buffers over
+    build_luts();
+    __syncthreads();
+    for (int sl = 0; sl < nsl; ++sl) {
+      __syncthreads();
+      __syncthreads();
+    }
+    return;
+  }
+  // lane l, accumulator v of tile (R, t): weight row 32 R + 8 (v / 4) + 4 (l / 32) + v % 4,
+  // activation row row0 + 32 t + l % 32; four consecutive weight rows per float4
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int b = row0 + 32 * t + (lane & 31);
+    if (b >= A.B) continue;
+    float* yrow = A.y1p + ((size_t)g * A.B + b) * A.m;
+#pragma unroll
+    for (int R = 0; R < 4; ++R)
+#pragma unroll
+      for (int vg = 0; vg < 4; ++vg) {
+        const int row = rt * 128 + 32 * R + 8 * vg + 4 * (lane >> 5);
+        if (row >= A.m) continue;
+        floatx4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = A.s0 * acc[R][t][4 * vg + e];
+        *reinterpret_cast<floatx4*>(yrow + row) = v;
+      }
+  }
+}
+
+int launch_wp(const WgArgs& A, unsigned grid, hipStream_t stream) {
+  static int done = 0;
+  if (!done) {
+    hipFuncAttributes fa{};
+    QS_HIP(hipFuncGetAttributes(&fa, (const void*)wp_kernel));
+    QS_REQUIRE(fa.sharedSizeBytes == 0, "wp_kernel must not use static LDS");
+    QS_HIP(hipFuncSetAttribute((const void*)wp_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kWpLds));
+    done = 1;
+  }
+  hipLaunchKernelGGL(wp_kernel, dim3(grid), dim3(kWpThreads), kWpLds, stream, A);
+  QS_LAUNCHED("wp_kernel");
+  return QS_OK;
+}
+
 }  // namespace
 
 int wide_splits(int64_t m, int64_t n, int64_t B, int ncu, bool has2) {
@@ -335,6 +575,7 @@ int launch_linear_wide_mfma(const WideMfma& G, hipStream_t stream) {
   const int64_t grid = (tiles + 7) / 8 * 8;  // XCD-contiguous tile order (see wg_kernel)
   const unsigned g = (unsigned)grid;
   if (has2) return CT == 1 ? launch_wg<true, 1>(A, g, stream) : launch_wg<true, 2>(A, g, stream);
+  if (CT == 4) return launch_wp(A, g, stream);  // 256 activation rows per work-group, as wp_kernel's
   return CT == 1 ? launch_wg<false, 1>(A, g, stream)
                  : CT == 2 ? launch_wg<false, 2>(A, g, stream) : launch_wg<false, 4>(A, g, stream);
 }
