@@ -46,31 +46,55 @@ __device__ __forceinline__ uint32_t lut_pair_hi(uint32_t e) { return __builtin_a
 typedef const __attribute__((address_space(3))) uint32_t* lds_u32_ptr;
 __device__ __forceinline__ uint32_t lds_word(uint32_t a) { return *reinterpret_cast<lds_u32_ptr>((size_t)a); }
 
-// Fills the two 4096-entry LUTs from the fp16 abs table staged in LDS
-// (tab16[256], uint4 rows), 1024 threads.  Entry e = tid + 1024 k of hi:
+// The two 4096-entry LUTs (hi: words 0..4095, lo: 4096..8191), built at
+// compile time; kernels copy them into LDS at address 0.  Entry e of hi:
 // abs row e & 255, flip nibble H = e >> 8 = (f1 f2 f3 q), f0 = q^f1^f2^f3;
-// of lo: abs row (e >> 3) & 255, f4..f6 = e & 7, q = e >> 11, coordinate 7
-// flipped by q^f4^f5^f6.  A sign flip of value v is bit 7 of byte v (mod 4).
-__device__ __forceinline__ void fill_luts(const uint4* tab16, uint32_t* lut_hi, uint32_t* lut_lo, int tid) {
-  const uint4 th = tab16[tid & 255];
-  const uint32_t hh = __builtin_amdgcn_perm(th.y, th.x, 0x07050301u);  // high bytes of values 0..3
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const uint32_t H = (uint32_t)(tid >> 8) + 4u * k;
+// of lo: abs row (e >> 3) & 255 (+128 for odd e >> 10), f4..f6 = e & 7,
+// q = e >> 11, coordinate 7 flipped by q^f4^f5^f6.  A sign flip of value v
+// is bit 7 of byte v (mod 4).
+struct LutWords {
+  uint32_t w[8192];
+};
+constexpr uint32_t high_bytes(uint32_t a, uint32_t b) {  // bytes 1, 3 of a, then of b
+  return ((a >> 8) & 0xFFu) | ((a >> 16) & 0xFF00u) | (((b >> 8) & 0xFFu) << 16) | ((b >> 24) << 24);
+}
+constexpr LutWords make_luts(const Table8h& t) {
+  LutWords L{};
+  for (uint32_t e = 0; e < 4096; ++e) {
+    const uint32_t H = e >> 8;
     const uint32_t f1 = (H >> 3) & 1, f2 = (H >> 2) & 1, f3 = (H >> 1) & 1;
     const uint32_t f0 = (H & 1) ^ f1 ^ f2 ^ f3;
-    lut_hi[tid + kFwdThreads * k] = hh ^ ((f0 << 7) | (f1 << 15) | (f2 << 23) | (f3 << 31));
+    L.w[e] = high_bytes(t.w[e & 255][0], t.w[e & 255][1]) ^ ((f0 << 7) | (f1 << 15) | (f2 << 23) | (f3 << 31));
+    const uint32_t lt = e & 1023, k = e >> 10;
+    const uint32_t f4 = (lt >> 2) & 1, f5 = (lt >> 1) & 1, f6 = lt & 1;
+    const uint32_t f7 = (k >> 1) ^ f4 ^ f5 ^ f6;
+    const uint32_t r = ((lt >> 3) + ((k & 1) ? 128u : 0u)) & 255;
+    L.w[4096 + e] = high_bytes(t.w[r][2], t.w[r][3]) ^ ((f4 << 7) | (f5 << 15) | (f6 << 23)) ^ (f7 << 31);
   }
-  const uint32_t f4 = (tid >> 2) & 1, f5 = (tid >> 1) & 1, f6 = tid & 1;
-  const uint32_t m456 = (f4 << 7) | (f5 << 15) | (f6 << 23), p456 = f4 ^ f5 ^ f6;
-  const uint4 ta = tab16[(tid >> 3) & 255], tb = tab16[((tid >> 3) + 128) & 255];
-  const uint32_t la = __builtin_amdgcn_perm(ta.w, ta.z, 0x07050301u);  // high bytes of values 4..7
-  const uint32_t lb = __builtin_amdgcn_perm(tb.w, tb.z, 0x07050301u);
+  return L;
+}
+namespace {
+__device__ const LutWords kLuts = make_luts(pack_table_f16(make_e8p_table()));
+}  // namespace
+// Thread tid's share of the LUTs in a work-group of NT threads: 16-byte
+// words tid + NT k (loads issued by load_luts, stored by store_luts into LDS
+// at address 0 once they are needed).
+template <int NT>
+struct LutCopy {
+  static_assert(NT >= 256 && 2048 % NT == 0, "LUT copy: 2048 16-byte words over the work-group");
+  uint4 v[2048 / NT];
+};
+template <int NT>
+__device__ __forceinline__ void load_luts(int tid, LutCopy<NT>& r) {
+  const uint4* src = reinterpret_cast<const uint4*>(kLuts.w);
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const uint32_t f7 = (uint32_t)(k >> 1) ^ p456;
-    lut_lo[tid + kFwdThreads * k] = ((k & 1) ? lb : la) ^ m456 ^ (f7 << 31);
-  }
+  for (int k = 0; k < 2048 / NT; ++k) r.v[k] = src[tid + NT * k];
+}
+template <int NT>
+__device__ __forceinline__ void store_luts(char* lds_base, int tid, const LutCopy<NT>& r) {
+  uint4* dst = reinterpret_cast<uint4*>(lds_base);
+#pragma unroll
+  for (int k = 0; k < 2048 / NT; ++k) dst[tid + NT * k] = r.v[k];
 }
 
 // MFMA A operand (8 fp16 values) of code word c (c odd: the upper 16 bits of

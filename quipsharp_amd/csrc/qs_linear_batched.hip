@@ -193,18 +193,14 @@ constexpr int kBmSlot = kWaves * 16 * kTB;   // floats per slot: [wave][row][bat
 constexpr int kBmOffHi = 0;                  // 4096 x uint32 (four fp16 high bytes)
 constexpr int kBmOffLo = 16384;              // 4096 x uint32
 constexpr int kBmOffLut1 = 32768;            // 256 x uint4
-constexpr int kBmOffTab = kBmOffLut1 + 4096; // 256 x uint4 (table staging)
-constexpr int kBmOffRed = kBmOffTab + 4096;  // kBmSlots x kBmSlot floats
+constexpr int kBmOffRed = kBmOffLut1 + 4096; // kBmSlots x kBmSlot floats
 constexpr int kBmLds = kBmOffRed + kBmSlots * kBmSlot * 4;
 static_assert(kBmLds <= 160 * 1024, "LDS budget");
 
 template <bool HAS2>
 __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
-  uint32_t* lut_hi = reinterpret_cast<uint32_t*>(lds + kBmOffHi);
-  uint32_t* lut_lo = reinterpret_cast<uint32_t*>(lds + kBmOffLo);
   uint4* lut1 = reinterpret_cast<uint4*>(lds + kBmOffLut1);
-  uint4* tab16 = reinterpret_cast<uint4*>(lds + kBmOffTab);
   float* red = reinterpret_cast<float*>(lds + kBmOffRed);
 
   const int tid = threadIdx.x;
@@ -224,9 +220,10 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
 
   // All global loads here are unconditional (an idle lane reads a valid
   // address it does not use), so the compiler waits for exactly the data in
-  // use: first the table rows, then the operand, then the code tiles.
-  uint4 trow = make_uint4(0, 0, 0, 0), t1row = make_uint4(0, 0, 0, 0);
-  trow = *reinterpret_cast<const uint4*>(kE8Ph.w[tid & 255]);
+  // use: first the LUTs, then the operand, then the code tiles.
+  LutCopy<kThreads> lutw;
+  load_luts(tid, lutw);
+  uint4 t1row = make_uint4(0, 0, 0, 0);
   if (HAS2) t1row = *reinterpret_cast<const uint4*>(kE81h.w[tid & 255]);
   // operand of lane (q, b = r16), fragment-major (frag_index): columns
   // 256 sl + 64 q + 8 c .. + 7 of row r16 are the 16 bytes of lane l = 16 q +
@@ -257,12 +254,8 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
     pre[k] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(J.codes0) + off);
     if (HAS2) pre1[k] = *reinterpret_cast<const uint2*>(J.codes1 + off / 2);
   }
-  if (tid < 256) {
-    tab16[tid] = trow;
-    if (HAS2) lut1[tid] = t1row;
-  }
-  __syncthreads();
-  fill_luts(tab16, lut_hi, lut_lo, tid);
+  store_luts(lds, tid, lutw);
+  if (HAS2 && tid < 256) lut1[tid] = t1row;
   __syncthreads();
 
   float slice_shift = 0.0f;  // sum_g S_g / 4 over the slice, batch row r16

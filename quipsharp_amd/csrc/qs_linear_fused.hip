@@ -13,8 +13,8 @@
 // Work-group j owns one slice group (up to 16 slices of 256 input columns,
 // one per wave) and a strided set of 16-row blocks, so each wave's activation
 // operand stays in registers for the whole launch.  Per work-group:
-//   1. issue the activation loads, then the abs-table and K loads; the
-//      byte-per-value half-codeword LUTs are built while they arrive;
+//   1. issue the activation loads, then the decode LUTs (built at compile
+//      time, copied into LDS) and K;
 //   2. input transform (every work-group, only its own slices), chunk
 //      combination first: activations times sv -> chunk table (bf16) ->
 //      slice rows sum_c M[s][c] x_c on the matrix cores -> per slice (one
@@ -99,9 +99,9 @@ struct FusedArgs {
   FusedJob job[kMaxJobs];
 };
 
-// LDS layout (bytes).  The abs-table staging area and the slice rows of the
-// input transform alias the reduction buffer (both are dead before the first
-// row block); the output transform reuses everything.
+// LDS layout (bytes).  The slice rows of the input transform alias the
+// reduction buffer (both are dead before the first row block); the output
+// transform reuses everything.
 constexpr int kOffHi = 0;                                   // 4096 x uint32 (four fp16 high bytes)
 constexpr int kOffLo = 16384;                               // 4096 x uint32
 constexpr int kOffLut1 = 32768;                             // 256 x uint4
@@ -110,7 +110,6 @@ constexpr int kRedSlot = kWaves * 16 * kMaxB;               // floats per slot: 
 constexpr int kZStride = 260;                               // floats per slice row (rows 16 banks apart)
 constexpr int kRedBytes = kRedSlots * kRedSlot * 4 > 16 * kZStride * 4 ? kRedSlots * kRedSlot * 4 : 16 * kZStride * 4;
 constexpr int kOffRed = kOffLut1 + 4096;                    // kRedSlots x kRedSlot floats
-constexpr int kOffTab = kOffRed;                            // 256 x uint4 (table staging, before the LUTs)
 constexpr int kOffZ = kOffRed;                              // 16 x kZStride floats (slice rows)
 constexpr int kMinStride = kMaxSF + 8;                      // bf16 per row of the input chunk matrix
 constexpr int kOffMin = kOffRed + kRedBytes;                // 2 x 16 x kMinStride bf16 (hi, lo)
@@ -138,7 +137,6 @@ constexpr int kL2Groups = 16;                               // column groups of 
 static_assert(2 * kMaxSF * kMinStride * 2 <= kOffXR, "M of kMaxSF chunks fits below the chunk table");
 constexpr int kOffHB = kOffXR;
 static_assert(kOffHB + 2 * kMaxB * 16 * kMinStride * 2 <= kLdsBytes, "staged columns fit");
-static_assert(kRedSlots * kRedSlot * 4 >= 4096, "table staging fits the reduction buffer");
 static_assert(kRedSlots * 16 * kMaxB * 4 == kThreads && kRedSlots * 16 * 8 == kThreads,
               "one reduction pass: 8 threads per output at B = 1, 4 at B = 2");
 
@@ -296,10 +294,7 @@ __device__ __forceinline__ void poll_columns(const unsigned long long* h2t, int 
 template <bool HAS2, bool SB, int XT>
 __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
-  uint32_t* lut_hi = reinterpret_cast<uint32_t*>(lds + kOffHi);
-  uint32_t* lut_lo = reinterpret_cast<uint32_t*>(lds + kOffLo);
   uint4* lut1 = reinterpret_cast<uint4*>(lds + kOffLut1);
-  uint4* tab16 = reinterpret_cast<uint4*>(lds + kOffTab);
   float* red = reinterpret_cast<float*>(lds + kOffRed);
   uint16_t* MinH = reinterpret_cast<uint16_t*>(lds + kOffMin);
   uint16_t* MinL = MinH + 16 * kMinStride;
@@ -326,23 +321,15 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   const LaneX lx = lane_x_init();
 
   // 1. loads: the first activation quad (the transform waits for it), then
-  //    the abs table and this wave's row of K; the code tiles once the
-  //    activations are in, then the launch tag.  (The table staging below
-  //    waits for every load issued so far: the compiler cannot count the
-  //    activation loads' conditional paths, so issuing the table first would
-  //    only delay the activations, and the tag, read from the device
-  //    coherence point, would delay the staging.)
-  XQuad<XT, SB> xr;
-  load_x_quad(A.x, A.ldx, J.sv, A.Sn, 0, 4 * w, lane, xr);
-  uint4 trow = make_uint4(0, 0, 0, 0), t1row = make_uint4(0, 0, 0, 0);  // fp16 table rows
-  if (tid < 256) {
-    trow = *reinterpret_cast<const uint4*>(kE8Ph.w[tid]);
-    if (HAS2) t1row = *reinterpret_cast<const uint4*>(kE81h.w[tid]);
-  }
+  //    the decode LUTs (32 bytes per thread, stored into LDS before the first
+  //    barrier) and this wave's row of K; the code tiles once the activations
+  //    are in the chunk table, then the launch tag.
+  LutCopy<kThreads> lutw;
+  uint4 t1row = make_uint4(0, 0, 0, 0);  // E8 one-bit table row (fp16)
   // this wave's row of the input chunk matrix (slice sl): K at columns
   // c = lane, lane + 64 (unconditional loads; sv is a dummy source without K)
   float mk[2];
-  {
+  auto load_mk = [&]() {
     const float* ksrc = A.pn > 1 ? A.Kn : J.sv;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -350,13 +337,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
       const int ki = (A.pn > 1 && active && c < A.Sn) ? (sl >> A.lsh_n) * A.pn + (c >> A.lsh_n) : 0;
       mk[h] = at_off(ksrc, (uint32_t)ki);
     }
-  }
-  if (tid < 256) {
-    tab16[tid] = trow;
-    if (HAS2) lut1[tid] = t1row;
-  }
-  __syncthreads();  // staged table complete
-  fill_luts(tab16, lut_hi, lut_lo, tid);
+  };
   // Code tiles stream through a ring of kPrefetch registers, refilled as
   // they are consumed.  The loads are unconditional (a tile past the end or
   // of an idle wave reads tile 0 instead) and the ring is unrolled, so the
@@ -375,11 +356,46 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
     return (r * (uint32_t)A.S + slc) * 1024u + 16u * lane;
   };
 
-  // tag of this launch's partial sums, read (below, after the first code
-  // tiles) by every work-group before it stores any slot; the epoch only
-  // changes after every slot of the launch has been read
+  // tag of this launch's partial sums, read (after the first code tiles) by
+  // every work-group before it stores any slot; the epoch only changes after
+  // every slot of the launch has been read
   uint32_t epoch = 0;
+  auto prefetch_codes = [&]() {
+#pragma unroll
+    for (int k = 0; k < kPrefetch; ++k) {
+      const uint32_t off = code_off(jr + k * J.Gr);
+      pre[k] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(J.codes0) + off);
+      if (HAS2) pre1[k] = *reinterpret_cast<const uint2*>(J.codes1 + off / 2);
+    }
+    // unconditional (a load under a branch is waited for at the branch's
+    // end, which would wait for the code tiles too); sv is a dummy source
+    // for a linear whose output transform runs in another kernel
+    epoch = __hip_atomic_load(J.out_in_kernel ? J.epoch : reinterpret_cast<unsigned*>(const_cast<float*>(J.sv)),
+                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+  float emul0 = 1.0f, emul1 = 1.0f;  // 2^e of batch rows 0 and 1
+  // This wave's fp16 operand row of batch row b (slice values t = 4 lane + u
+  // times mul), and the per-group sums for the +-1/4 shift term (group t / 8).
+  auto store_operand_row = [&](const int b, const float (&v)[4], const float mul) {
+    uint32_t hw[2];
+    float hs = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const _Float16 h0 = (_Float16)(v[2 * k] * mul), h1 = (_Float16)(v[2 * k + 1] * mul);
+      hs += (float)h0;
+      hs += (float)h1;
+      hw[k] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+    }
+    *reinterpret_cast<uint2*>(XH + (b * 16 + w) * kXStride + 4 * lane) = make_uint2(hw[0], hw[1]);
+    hs += lane_xor<1>(hs, lx);  // lane pairs
+    if ((lane & 1) == 0) XS[(b * 16 + w) * 32 + (lane >> 1)] = (_Float16)hs;
+  };
 
+  XQuad<XT, SB> xr;
+  load_x_quad(A.x, A.ldx, J.sv, A.Sn, 0, 4 * w, lane, xr);
+  load_luts(tid, lutw);
+  if (HAS2 && tid < 256) t1row = *reinterpret_cast<const uint4*>(kE81h.w[tid]);
+  load_mk();
   // 2. input transform, one batch row at a time, chunk combination first:
   //    T_n = M (x) H_256 = (I (x) H_256)(M (x) I).  The activation chunks go
   //    into the chunk table XR[t][c] as bf16 (exact for bf16 activations
@@ -392,7 +408,6 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   const int Spad = (A.Sn + 31) & ~31;  // chunks padded to the matrix cores' k-steps of 32
   const int xrs = Spad + 8;            // halves per column of the chunk table
   uint16_t* XR1 = XR0 + 256 * xrs;
-  float emul0 = 1.0f, emul1 = 1.0f;  // 2^e of batch rows 0 and 1
   // one batch row; called once per row rather than looped, so that no
   // activation registers are carried from one row to the next
   auto input_row = [&](const int b) {
@@ -424,23 +439,15 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
         }
       }
     }
-    __syncthreads();  // chunk table, norms (and, the first time, M and the LUTs) complete
     if (b == 0) {
-      // first code tiles (issued once the activations are in the chunk
-      // table, so the activation loads do not queue behind them and the
-      // ring's registers are not live beside them)
-#pragma unroll
-      for (int k = 0; k < kPrefetch; ++k) {
-        const uint32_t off = code_off(jr + k * J.Gr);
-        pre[k] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(J.codes0) + off);
-        if (HAS2) pre1[k] = *reinterpret_cast<const uint2*>(J.codes1 + off / 2);
-      }
-      // unconditional (a load under a branch is waited for at the branch's
-      // end, which would wait for the code tiles too); sv is a dummy source
-      // for a linear whose output transform runs in another kernel
-      epoch = __hip_atomic_load(J.out_in_kernel ? J.epoch : reinterpret_cast<unsigned*>(const_cast<float*>(J.sv)),
-                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      store_luts(lds, tid, lutw);
+      if (HAS2 && tid < 256) lut1[tid] = t1row;
     }
+    __syncthreads();  // chunk table, norms (and, the first time, M and the LUTs) complete
+    // first code tiles (issued once the activations are in the chunk table,
+    // so the activation loads do not queue behind them and the ring's
+    // registers are not live beside them)
+    if (b == 0) prefetch_codes();
     float norm2 = 0.0f;
 #pragma unroll
     for (int i = 0; i < kWaves; ++i) norm2 += wsum[i];
@@ -469,19 +476,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
       const float4 z4 = *reinterpret_cast<const float4*>(Z + w * kZStride + 4 * lane);
       float v[1][4] = {{z4.x, z4.y, z4.z, z4.w}};
       h256<1>(v, lane, lx);
-      uint32_t hw[2];
-      float hs = 0.0f;
-#pragma unroll
-      for (int k = 0; k < 2; ++k) {
-        const _Float16 h0 = (_Float16)(v[0][2 * k] * mul), h1 = (_Float16)(v[0][2 * k + 1] * mul);
-        hs += (float)h0;
-        hs += (float)h1;
-        hw[k] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-      }
-      *reinterpret_cast<uint2*>(XH + (b * 16 + w) * kXStride + 4 * lane) = make_uint2(hw[0], hw[1]);
-      // group sums of the fp16 values, group t / 8: lane pairs
-      hs += lane_xor<1>(hs, lx);
-      if ((lane & 1) == 0) XS[(b * 16 + w) * 32 + (lane >> 1)] = (_Float16)hs;
+      store_operand_row(b, v[0], mul);
     }
     };
   input_row(0);

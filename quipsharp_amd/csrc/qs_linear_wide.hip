@@ -50,7 +50,7 @@ inline int wg_ct(int64_t B, bool has2) {
 }
 constexpr int kWgRows = 16 * kWgRowTiles;
 constexpr int kWgCodeBuf = kWgRowTiles * 1024;           // code bytes of one slice
-constexpr int kWgOffCodes = kDqOffLut1 + 4096;           // 2 slices (the table staging before them)
+constexpr int kWgOffCodes = kDqOffLut1 + 4096;           // 2 slices
 constexpr int kWgOffCodes1 = kWgOffCodes + 2 * kWgCodeBuf;  // 2 slices of second-stage bytes
 constexpr int kWgLds = kWgOffCodes1 + kWgCodeBuf;
 constexpr int kWgRing = 4;         // B fragments in flight per wave (steps of 32 columns)
@@ -58,7 +58,7 @@ constexpr int kWgAhead = 3;        // steps between a B load and its use
 static_assert(kWgLds <= 65536, "LDS budget");
 constexpr int kWgCopies = kWgCodeBuf / (16 * kWgThreads);  // 16-byte code copies per thread and slice
 static_assert(kWgCopies >= 1 && kWgCopies <= 2 && kWgCopies * 16 * kWgThreads == kWgCodeBuf, "code copy");
-static_assert(kWgThreads >= 256 && kFwdThreads % kWgThreads == 0, "table staging and LUT fill");
+static_assert(kWgThreads >= 256, "E8 one-bit table rows: one per thread of the first 256");
 
 struct WgArgs {
   const uint16_t* codes0;
@@ -75,10 +75,7 @@ struct WgArgs {
 template <bool HAS2, int kWgColTiles>
 __global__ __launch_bounds__(kWgThreads) void wg_kernel(WgArgs A) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
-  uint32_t* lut_hi = reinterpret_cast<uint32_t*>(lds + kDqOffHi);
-  uint32_t* lut_lo = reinterpret_cast<uint32_t*>(lds + kDqOffLo);
   uint4* lut1 = reinterpret_cast<uint4*>(lds + kDqOffLut1);
-  uint4* tab16 = reinterpret_cast<uint4*>(lds + kWgOffCodes);  // staging, before the first code tiles
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
   const int q = lane >> 4, r16 = lane & 15;
@@ -159,16 +156,16 @@ __global__ __launch_bounds__(kWgThreads) void wg_kernel(WgArgs A) {
 #pragma unroll
     for (int k = 0; k < kWgAhead; ++k) load_b(s_begin, k, bring[k]);
   }
-  if (tid < 256) {
-    tab16[tid] = *reinterpret_cast<const uint4*>(kE8Ph.w[tid]);
-    if (HAS2) lut1[tid] = *reinterpret_cast<const uint4*>(kE81h.w[tid]);
+  {
+    LutCopy<kWgThreads> lc;
+    load_luts(tid, lc);
+    uint4 t1 = make_uint4(0, 0, 0, 0);
+    if (HAS2 && tid < 256) t1 = *reinterpret_cast<const uint4*>(kE81h.w[tid]);
+    store_luts(lds, tid, lc);
+    if (HAS2 && tid < 256) lut1[tid] = t1;
   }
-  __syncthreads();
-#pragma unroll
-  for (int r = 0; r < kFwdThreads / kWgThreads; ++r) fill_luts(tab16, lut_hi, lut_lo, tid + kWgThreads * r);
-  __syncthreads();
   store_codes(0, gc);
-  __syncthreads();
+  __syncthreads();  // LUTs and the first slice's code tiles complete
 
   floatx4 acc[kWgRowTiles][kWgColTiles];
   floatx4 acc2[kWgRowTiles][kWgColTiles];
@@ -333,9 +330,6 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 __global__ __launch_bounds__(kWpThreads) void wp_kernel(WgArgs A) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
-  uint32_t* lut_hi = reinterpret_cast<uint32_t*>(lds + kDqOffHi);
-  uint32_t* lut_lo = reinterpret_cast<uint32_t*>(lds + kDqOffLo);
-  uint4* tab16 = reinterpret_cast<uint4*>(lds + kWpOffA);  // staging, before the first fragments
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -354,13 +348,12 @@ __global__ __launch_bounds__(kWpThreads) void wp_kernel(WgArgs A) {
   const int s_last = s_end > s_begin ? s_end - 1 : (A.S - 1);
 
   // every wave issues its first global loads (code words, B fragments), then
-  // builds the LUTs while they are in flight
+  // copies its share of the LUTs into LDS
   auto build_luts = [&]() {
-    if (tid < 256) tab16[tid] = *reinterpret_cast<const uint4*>(kE8Ph.w[tid]);
-    __syncthreads();
-#pragma unroll
-    for (int r = 0; r < kFwdThreads / kWpThreads; ++r) fill_luts(tab16, lut_hi, lut_lo, tid + kWpThreads * r);
-    __syncthreads();  // LUTs complete, staging area free
+    LutCopy<kWpThreads> lc;
+    load_luts(tid, lc);
+    store_luts(lds, tid, lc);
+    __syncthreads();  // LUTs complete
   };
 
   const int nsl = s_end > s_begin ? s_end - s_begin : 0;  // slices of this work-group
