@@ -479,7 +479,8 @@ constexpr int kMaxPolls = 1 << 20;
 // Polling the tagged partial sums of batch row b for the chunks
 // c = w + 16 u < Sm of this wave (element t = lane + 64 j, as
 // load_partials_raw), summed over the SG groups in ascending order once every
-// slot holds `tag`.  One group at a time (4 CPW slots per lane in flight).
+// slot holds `tag`.  One group at a time (4 CPW slots per lane in flight;
+// issuing four groups together measured slower).
 // poll_issue only issues the first group's loads, so that loads issued after
 // it share its round trip; poll_finish waits, reloads the slots that do not
 // carry the tag yet, and moves on to the next group.

@@ -42,7 +42,8 @@ constexpr int kMaxParts = 16;  // work-groups per batch row for odd-factor trans
 
 struct WsLayout {
   size_t x2h, sg, xtot, xmul, x2, y1p, y1t, h2t, total;
-  int S, SG, W;
+  int S, SG, W;    // chunks, slice groups and slices per group of the decode-matvec
+  FusedPlan fused;  // the one-launch kernel's (its partial sums: fused.SG groups)
   bool wide;
 };
 
@@ -91,7 +92,8 @@ WsLayout ws_layout(int64_t m, int64_t n, int64_t batch, int layout) {
     L.S = (int)(n / 256);
     L.SG = (L.S + kMaxWaves - 1) / kMaxWaves;
     L.W = (L.S + L.SG - 1) / L.SG;
-    L.y1t = off; off = align256(off + (size_t)L.SG * 2 * m * 8);
+    L.fused = fused_plan(L.S);
+    L.y1t = off; off = align256(off + (size_t)L.fused.SG * 2 * m * 8);
     L.h2t = off; off = align256(off + (size_t)2 * m * 8);
     const size_t xrows = (size_t)(B + 15) / 16 * 16;  // fragment-major rows: 16s
     L.x2h = off; off = align256(off + xrows * n * 2);
@@ -102,6 +104,7 @@ WsLayout ws_layout(int64_t m, int64_t n, int64_t batch, int layout) {
     L.S = 0;
     L.SG = 1;
     L.W = 0;
+    L.fused = FusedPlan{1, 0, 1};
     L.x2 = off; off = align256(off + (size_t)B * n * 4);
   }
   if (L.wide) {
@@ -111,7 +114,8 @@ WsLayout ws_layout(int64_t m, int64_t n, int64_t batch, int layout) {
     const size_t a = (size_t)(g0 > g1 ? g0 : g1) * B, b = (size_t)L.SG * kMaxTileBatch;
     L.y1p = off; off = align256(off + (a > b ? a : b) * m * 4);
   } else {
-    L.y1p = off; off = align256(off + (size_t)L.SG * B * m * 4);
+    const int sgp = L.SG > L.fused.SG ? L.SG : L.fused.SG;
+    L.y1p = off; off = align256(off + (size_t)sgp * B * m * 4);
   }
   L.total = off;
   return L;
@@ -922,8 +926,7 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
     d.y1p = reinterpret_cast<float*>(ws + W.y1p);
     d.y1t = reinterpret_cast<unsigned long long*>(ws + W.y1t);
     d.h2t = reinterpret_cast<unsigned long long*>(ws + W.h2t);
-    rc = launch_linear_fused(x, x_dtype, ldx, (int)batch, (int)n, kron_pn, kron_n, y_dtype, sbits, 1, &d, W.S, W.SG,
-                             W.W,
+    rc = launch_linear_fused(x, x_dtype, ldx, (int)batch, (int)n, kron_pn, kron_n, y_dtype, sbits, 1, &d, W.S, W.fused,
                              cu_count(), s, reinterpret_cast<hipEvent_t>(mv_begin),
                              reinterpret_cast<hipEvent_t>(mv_end));
     if (rc) return rc;
@@ -931,9 +934,9 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
     // the output kernels below read su as m fp32 values
     QS_REQUIRE(!sbits, "packed sign bits reached an fp32-sign output path (m %lld)", (long long)m);
     if (chunk_transform_fits(m, kron_pm))
-      return launch_yout_chunk(d.y1p, W.SG, (int)batch, m, kron_pm, kron_m, nullptr, 0, d.xmul, s0, layer_scale, su,
-                               bias, y, y_dtype, ldy, s);
-    return launch_yout_rows(d.y1p, W.SG, (int)batch, m, kron_pm, kron_m, nullptr, 0, d.xmul, s0, layer_scale, su,
+      return launch_yout_chunk(d.y1p, W.fused.SG, (int)batch, m, kron_pm, kron_m, nullptr, 0, d.xmul, s0, layer_scale,
+                               su, bias, y, y_dtype, ldy, s);
+    return launch_yout_rows(d.y1p, W.fused.SG, (int)batch, m, kron_pm, kron_m, nullptr, 0, d.xmul, s0, layer_scale, su,
                             bias, y, y_dtype, ldy, s);
   }
   return forward_batched(x, x_dtype, ldx, batch, n, m, codes0, codes1, kind1, layout, sv, su, kron_pn, kron_n,
@@ -1014,10 +1017,10 @@ FusedBlock fused_block(int64_t m, int64_t n) {
   const WsLayout W = ws_layout(m, n, 2, QS_LAYOUT_TILED);
   FusedBlock F{};
   F.y1t = 0;
-  F.h2t = F.y1t + align256((size_t)W.SG * 2 * (size_t)m * 8);
+  F.h2t = F.y1t + align256((size_t)W.fused.SG * 2 * (size_t)m * 8);
   F.xmul = F.h2t + align256((size_t)2 * (size_t)m * 8);
   F.y1p = F.xmul + 256;
-  F.total = F.y1p + align256((size_t)W.SG * 2 * (size_t)m * 4);
+  F.total = F.y1p + align256((size_t)W.fused.SG * 2 * (size_t)m * 4);
   return F;
 }
 template <class M>
@@ -1215,8 +1218,7 @@ extern "C" int qs_linear_forward_group(const void* x, int x_dtype, int64_t ldx, 
     off += F.total;
   }
   rc = launch_linear_fused(x, x_dtype, ldx, (int)batch, (int)n, kron_pn, kron_n, y_dtype, jobs[0].sign_bits ? 1 : 0,
-                           count, d, W0.S, W0.SG,
-                           W0.W, cu_count(), s, reinterpret_cast<hipEvent_t>(mv_begin),
+                           count, d, W0.S, W0.fused, cu_count(), s, reinterpret_cast<hipEvent_t>(mv_begin),
                            reinterpret_cast<hipEvent_t>(mv_end));
   if (rc) return rc;
   // outputs the kernel did not finish: chunked ones in one launch, others per job
@@ -1228,10 +1230,10 @@ extern "C" int qs_linear_forward_group(const void* x, int x_dtype, int64_t ldx, 
     // the output kernels below read su as m fp32 values
     QS_REQUIRE(!j.sign_bits, "job %d: packed sign bits reached an fp32-sign output path (m %lld)", g, (long long)j.m);
     if (chunk_transform_fits(j.m, j.kron_pm)) {
-      yc[nyc++] = yc_args(d[g].y1p, W0.SG, (int)batch, j.m, j.kron_pm, j.kron_m, nullptr, 0, d[g].xmul, j.s0,
+      yc[nyc++] = yc_args(d[g].y1p, W0.fused.SG, (int)batch, j.m, j.kron_pm, j.kron_m, nullptr, 0, d[g].xmul, j.s0,
                           j.layer_scale, j.su, j.bias, j.y, y_dtype, j.ldy);
     } else {
-      rc = launch_yout_rows(d[g].y1p, W0.SG, (int)batch, j.m, j.kron_pm, j.kron_m, nullptr, 0, d[g].xmul, j.s0,
+      rc = launch_yout_rows(d[g].y1p, W0.fused.SG, (int)batch, j.m, j.kron_pm, j.kron_m, nullptr, 0, d[g].xmul, j.s0,
                             j.layer_scale, j.su, j.bias, j.y, y_dtype, j.ldy, s);
       if (rc) return rc;
     }

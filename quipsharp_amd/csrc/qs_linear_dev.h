@@ -26,9 +26,16 @@ struct FusedJobDesc {
   unsigned long long* h2t;  // workspace: [B][m] tagged chunk transforms (output transform in two levels)
 };
 
+// How the one-launch kernel splits S chunks over a 16-wave work-group: SG
+// slice groups of W slices, each slice taken by P waves (row-block phases),
+// W P <= 16, P in {1, 2, 4}.
+struct FusedPlan {
+  int SG, W, P;
+};
+FusedPlan fused_plan(int S);
 int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, int pn, const float* Kn, int y_dtype,
-                        int sbits, int count, const FusedJobDesc* jobs, int S, int SG, int W, int ncu, hipStream_t stream,
-                        hipEvent_t ev_start, hipEvent_t ev_stop);
+                        int sbits, int count, const FusedJobDesc* jobs, int S, const FusedPlan& plan, int ncu,
+                        hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop);
 bool fused_eligible(int64_t batch, int64_t n, int x_dtype, int pn);
 bool fused_x_aligned(const void* x, int x_dtype, int64_t ldx);
 bool fused_output_in_kernel(int64_t m, int pm);

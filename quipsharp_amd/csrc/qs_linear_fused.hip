@@ -10,9 +10,12 @@
 // Walsh-Hadamard inside a chunk by one wave (four values per lane, two
 // stages in registers and six across lanes with DPP / permlane exchanges).
 //
-// Work-group j owns one slice group (up to 16 slices of 256 input columns,
-// one per wave) and a strided set of 16-row blocks, so each wave's activation
-// operand stays in registers for the whole launch.  Per work-group:
+// Work-group j owns one slice group (W <= 16 slices of 256 input columns)
+// and a strided set of 16-row blocks, so each wave's activation operand stays
+// in registers for the whole launch.  Each slice is taken by P = 1, 2 or 4
+// waves that split the row blocks (phases), so that W P waves of the 16 have
+// work (fused_plan: 20 chunks run as 5 groups of 4 slices x 4 phases rather
+// than 2 groups of 10 slices with 6 waves idle).  Per work-group:
 //   1. issue the activation loads, then the decode LUTs (built at compile
 //      time, copied into LDS) and K;
 //   2. input transform (every work-group, only its own slices), chunk
@@ -92,7 +95,7 @@ struct FusedArgs {
   int n, Sn, lsh_n, pn;
   const float* Kn;
   float scale_n;
-  int S, SG, W;
+  int S, SG, W, P, lgP;  // chunks, slice groups, slices per group, row-block phases (W P <= 16), log2 P
   int y_dtype;
   int sbits;  // su, sv of every job are packed sign bits
   int njobs;
@@ -137,8 +140,7 @@ constexpr int kL2Groups = 16;                               // column groups of 
 static_assert(2 * kMaxSF * kMinStride * 2 <= kOffXR, "M of kMaxSF chunks fits below the chunk table");
 constexpr int kOffHB = kOffXR;
 static_assert(kOffHB + 2 * kMaxB * 16 * kMinStride * 2 <= kLdsBytes, "staged columns fit");
-static_assert(kRedSlots * 16 * kMaxB * 4 == kThreads && kRedSlots * 16 * 8 == kThreads,
-              "one reduction pass: 8 threads per output at B = 1, 4 at B = 2");
+static_assert(kRedSlots * 16 * 8 == kThreads, "one reduction pass: 8 / (P B) threads per output, P B <= 8");
 
 // Activation quads of the input transform: thread (w, lane) holds chunks
 // c = c0 + i (i < 4, c0 = 64 round + 4 w) of one batch row at columns
@@ -316,8 +318,12 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   const int lb = (int)blockIdx.x - J.wg0;  // work-group index within this linear
   const int RB = J.m >> 4;
   const int sg = lb / J.Gr, jr = lb - sg * J.Gr;
-  const int sl = sg * A.W + w;
-  const bool active = w < A.W && sl < A.S;
+  // wave w = ph W + wsl takes slice wsl of the group and the row blocks of
+  // phase ph: at step i, row block jr + (P i + ph) Gr
+  const int ph = w / A.W, wsl = w - ph * A.W;
+  const int sl = sg * A.W + wsl;
+  const bool active = ph < A.P && sl < A.S;
+  auto own_rb = [&](int i) { return jr + (A.P * i + ph) * J.Gr; };
   const LaneX lx = lane_x_init();
 
   // 1. loads: the first activation quad (the transform waits for it), then
@@ -363,7 +369,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   auto prefetch_codes = [&]() {
 #pragma unroll
     for (int k = 0; k < kPrefetch; ++k) {
-      const uint32_t off = code_off(jr + k * J.Gr);
+      const uint32_t off = code_off(own_rb(k));
       pre[k] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(J.codes0) + off);
       if (HAS2) pre1[k] = *reinterpret_cast<const uint2*>(J.codes1 + off / 2);
     }
@@ -505,15 +511,18 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
 
   const uint32_t tag = J.out_in_kernel ? next_tag(epoch, g) : 0u;
 
-  // 3. row blocks
+  // 3. row blocks, in steps of P (one per phase)
   const int nw = A.S - sg * A.W < A.W ? A.S - sg * A.W : A.W;
-  int k = 0;  // row blocks done: selects the reduction slot
-  for (int rb0 = jr; rb0 < RB; rb0 += kPrefetch * J.Gr) {
+  const int stride = A.P * J.Gr;  // row blocks per step
+  int k = 0;  // steps done: selects the reduction slot
+  for (int i0 = 0; jr + i0 * stride < RB; i0 += kPrefetch) {
 #pragma unroll
   for (int u = 0; u < kPrefetch; ++u) {
     // every ring step runs (the ring registers are never copied); a step
     // past the last row block only refills its entry
-    const int rb = rb0 + u * J.Gr;
+    const int step = i0 + u;
+    const bool step_valid = jr + step * stride < RB;  // the work-group has row blocks at this step
+    const int rb = own_rb(step);
     const bool valid = rb < RB;
     floatx4 acc = {0.f, 0.f, 0.f, 0.f};
     floatx4 accs = {0.f, 0.f, 0.f, 0.f};
@@ -549,14 +558,14 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
     {
       // refill this ring entry (its tile is consumed) with the tile
       // kPrefetch row blocks ahead
-      const uint32_t off = code_off(rb + kPrefetch * J.Gr);
+      const uint32_t off = code_off(own_rb(step + kPrefetch));
       pre[u] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(J.codes0) + off);
       if (HAS2) pre1[u] = *reinterpret_cast<const uint2*>(J.codes1 + off / 2);
     }
     // partial of this slice for rows 4q..4q+3, batch column r16, into this
-    // row block's slot; the slots are reduced across the waves every
-    // kRedSlots row blocks (and after the last), so the waves decode without
-    // a barrier per row block
+    // step's slot; the slots are reduced across the waves every kRedSlots
+    // steps (and after the last), so the waves decode without a barrier per
+    // row block
     const int slot = k % kRedSlots;
     float* rbuf = red + slot * kRedSlot;
     if (valid && r16 < A.B) {
@@ -567,29 +576,35 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
         rbuf[(w * 16 + 4 * q + j) * kMaxB + r16] = active ? v : 0.0f;
       }
     }
-    if (valid && (slot == kRedSlots - 1 || rb + J.Gr >= RB)) {
+    if (step_valid && (slot == kRedSlots - 1 || jr + (step + 1) * stride >= RB)) {
       __syncthreads();
-      // output o = (s * 16 + row) * B + b of slot s <= slot, summed over the
-      // waves by tpo threads (waves part, part + tpo, ...), then across them;
-      // tpo depends on B only, so every output is summed in the same order
-      // whatever the number of row blocks pending
-      const int nout = (slot + 1) * 16 * A.B;
-      const int tpo = A.B == 1 ? 8 : 4;  // kThreads / (kRedSlots * 16 * B)
-      const int o = tid / tpo, part = tid - o * tpo;
+      // output o = ((s P + p) 16 + row) B + b of slot s <= slot, phase p,
+      // summed over the phase's waves by tpo threads (waves part, part +
+      // tpo, ...), then across them; tpo depends on B and P only, so every
+      // output is summed in the same order whatever the number of steps
+      // pending
+      // (P and B are powers of two: shifts, not divisions)
+      const int lgb = A.B - 1, lgpb = A.lgP + lgb;  // log2 B, log2 (P B)
+      const int nout = (slot + 1) << (4 + lgpb);
+      const int tpo = 8 >> lgpb;  // kThreads / (kRedSlots * 16 * P * B)
+      const int o = tid >> (3 - lgpb), part = tid & (tpo - 1);
       float v = 0.0f;
-      int s = 0, row = 0, bc = 0;
+      int s = 0, p = 0, row = 0, bc = 0;
       if (o < nout) {
-        s = o / (16 * A.B);
-        const int rr = o - s * 16 * A.B;
-        row = rr / A.B;
-        bc = rr - row * A.B;
-        for (int ww = part; ww < nw; ww += tpo) v += red[s * kRedSlot + (ww * 16 + row) * kMaxB + bc];
+        s = o >> (4 + lgpb);
+        const int rr = o & ((16 << lgpb) - 1);
+        p = rr >> (4 + lgb);
+        const int r2 = rr & ((16 << lgb) - 1);
+        row = r2 >> lgb;
+        bc = r2 & lgb;
+        for (int ww = part; ww < nw; ww += tpo)
+          v += red[s * kRedSlot + ((p * A.W + ww) * 16 + row) * kMaxB + bc];
       }
-      v += lane_xor<1>(v, lx);
-      v += lane_xor<2>(v, lx);
+      if (tpo >= 2) v += lane_xor<1>(v, lx);
+      if (tpo >= 4) v += lane_xor<2>(v, lx);
       if (tpo == 8) v += lane_xor<4>(v, lx);
-      if (o < nout && part == 0) {
-        const int rbs = rb - (slot - s) * J.Gr;  // row block of slot s
+      const int rbs = jr + (A.P * (step - (slot - s)) + p) * J.Gr;  // row block of slot s, phase p
+      if (o < nout && part == 0 && rbs < RB) {
         const size_t idx = ((size_t)sg * A.B + bc) * J.m + rbs * 16 + row;
         if (J.out_in_kernel)
           __hip_atomic_store(&J.y1t[idx], tagged(v, tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -598,7 +613,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
       }
       __syncthreads();  // the slots are free again
     }
-    k += valid;
+    k += step_valid;
   }
   }
 
@@ -846,11 +861,33 @@ int launch_fused_variant(const FusedArgs& A, int wg, hipStream_t stream, hipEven
 }
 }  // namespace
 
+// Slice groups first as few as fit (W = ceil(S / SG) <= 16), then more of
+// them where P phases then keep a tenth more of the 16 waves busy (S = 20:
+// 5 groups of 4 slices x 4 phases, all 16 waves, against 2 groups of 10).
+FusedPlan fused_plan(int S) {
+  const int base = (S + kWaves - 1) / kWaves;
+  FusedPlan best{0, 0, 0};
+  double best_eff = 0.0;
+  for (int sg = base; sg <= 2 * base + 3 && sg <= S; ++sg) {
+    const int w = (S + sg - 1) / sg;
+    const int fit = kWaves / w;
+    const int p = fit >= 4 ? 4 : fit >= 2 ? 2 : 1;
+    const double eff = (double)S * p / (double)(kWaves * sg);  // busy share of the waves
+    if (best.SG == 0 || eff > best_eff + 0.1) {
+      best = FusedPlan{sg, w, p};
+      best_eff = eff;
+    }
+  }
+  return best;
+}
+
 int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, int pn, const float* Kn, int y_dtype,
-                        int sbits, int count, const FusedJobDesc* jobs, int S, int SG, int W, int ncu, hipStream_t stream,
-                        hipEvent_t ev_start, hipEvent_t ev_stop) {
+                        int sbits, int count, const FusedJobDesc* jobs, int S, const FusedPlan& plan, int ncu,
+                        hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop) {
+  const int SG = plan.SG, W = plan.W, P = plan.P;
   QS_REQUIRE(count >= 1 && count <= kMaxJobs, "1..%d linears per launch", kMaxJobs);
-  QS_REQUIRE(fused_eligible(B, n, x_dtype, pn) && SG * W >= S && W <= kWaves,
+  QS_REQUIRE(fused_eligible(B, n, x_dtype, pn) && SG * W >= S && W * P <= kWaves && (P == 1 || P == 2 || P == 4) &&
+                 P * B <= 8,
              "one-launch forward: B %d, n %d (dtype %d) outside its shapes", B, n, x_dtype);
   FusedArgs A{};
   A.x = x;
@@ -867,6 +904,8 @@ int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, i
   A.S = S;
   A.SG = SG;
   A.W = W;
+  A.P = P;
+  A.lgP = P == 4 ? 2 : P == 2 ? 1 : 0;
   A.y_dtype = y_dtype;
   A.sbits = sbits;
   A.njobs = count;
