@@ -328,8 +328,9 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
 
   // 1. loads: the first activation quad (the transform waits for it), then
   //    the decode LUTs (32 bytes per thread, stored into LDS before the first
-  //    barrier) and this wave's row of K; the code tiles once the activations
-  //    are in the chunk table, then the launch tag.
+  //    barrier), this wave's row of K and its first code tiles; the rest of
+  //    the code tiles once the activations are in the chunk table, then the
+  //    launch tag.
   LutCopy<kThreads> lutw;
   uint4 t1row = make_uint4(0, 0, 0, 0);  // E8 one-bit table row (fp16)
   // this wave's row of the input chunk matrix (slice sl): K at columns
@@ -366,19 +367,20 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   // every work-group before it stores any slot; the epoch only changes after
   // every slot of the launch has been read
   uint32_t epoch = 0;
-  auto prefetch_codes = [&]() {
+  // ring entries k0 .. k1 - 1: the first kEarlyTiles are requested before the
+  // input transform (they arrive while it runs), the rest once the chunk
+  // table is complete (requesting the whole ring early, or the launch tag
+  // below, measured slower: they delay the activation loads)
+  auto prefetch_codes = [&](int k0, int k1) {
 #pragma unroll
     for (int k = 0; k < kPrefetch; ++k) {
+      if (k < k0 || k >= k1) continue;
       const uint32_t off = code_off(own_rb(k));
       pre[k] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(J.codes0) + off);
       if (HAS2) pre1[k] = *reinterpret_cast<const uint2*>(J.codes1 + off / 2);
     }
-    // unconditional (a load under a branch is waited for at the branch's
-    // end, which would wait for the code tiles too); sv is a dummy source
-    // for a linear whose output transform runs in another kernel
-    epoch = __hip_atomic_load(J.out_in_kernel ? J.epoch : reinterpret_cast<unsigned*>(const_cast<float*>(J.sv)),
-                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   };
+  constexpr int kEarlyTiles = 2;
   float emul0 = 1.0f, emul1 = 1.0f;  // 2^e of batch rows 0 and 1
   // This wave's fp16 operand row of batch row b (slice values t = 4 lane + u
   // times mul), and the per-group sums for the +-1/4 shift term (group t / 8).
@@ -402,6 +404,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   load_luts(tid, lutw);
   if (HAS2 && tid < 256) t1row = *reinterpret_cast<const uint4*>(kE81h.w[tid]);
   load_mk();
+  prefetch_codes(0, kEarlyTiles);
   // 2. input transform, one batch row at a time, chunk combination first:
   //    T_n = M (x) H_256 = (I (x) H_256)(M (x) I).  The activation chunks go
   //    into the chunk table XR[t][c] as bf16 (exact for bf16 activations
@@ -450,10 +453,14 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
       if (HAS2 && tid < 256) lut1[tid] = t1row;
     }
     __syncthreads();  // chunk table, norms (and, the first time, M and the LUTs) complete
-    // first code tiles (issued once the activations are in the chunk table,
-    // so the activation loads do not queue behind them and the ring's
-    // registers are not live beside them)
-    if (b == 0) prefetch_codes();
+    if (b == 0) {
+      prefetch_codes(kEarlyTiles, kPrefetch);
+      // unconditional (a load under a branch is waited for at the branch's
+      // end, which would wait for the code tiles too); sv is a dummy source
+      // for a linear whose output transform runs in another kernel
+      epoch = __hip_atomic_load(J.out_in_kernel ? J.epoch : reinterpret_cast<unsigned*>(const_cast<float*>(J.sv)),
+                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     float norm2 = 0.0f;
 #pragma unroll
     for (int i = 0; i < kWaves; ++i) norm2 += wsum[i];
