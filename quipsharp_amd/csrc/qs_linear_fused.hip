@@ -329,8 +329,8 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   // 1. loads: the first activation quad (the transform waits for it), then
   //    the decode LUTs (32 bytes per thread, stored into LDS before the first
   //    barrier), this wave's row of K and its first code tiles; the rest of
-  //    the code tiles once the activations are in the chunk table, then the
-  //    launch tag.
+  //    the code tiles once the activations are in the chunk table, the
+  //    launch tag after the transform.
   LutCopy<kThreads> lutw;
   uint4 t1row = make_uint4(0, 0, 0, 0);  // E8 one-bit table row (fp16)
   // this wave's row of the input chunk matrix (slice sl): K at columns
@@ -363,14 +363,13 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
     return (r * (uint32_t)A.S + slc) * 1024u + 16u * lane;
   };
 
-  // tag of this launch's partial sums, read (after the first code tiles) by
-  // every work-group before it stores any slot; the epoch only changes after
-  // every slot of the launch has been read
+  // tag of this launch's partial sums, read by every work-group before it
+  // stores any slot; the epoch only changes after every slot of the launch
+  // has been read
   uint32_t epoch = 0;
   // ring entries k0 .. k1 - 1: the first kEarlyTiles are requested before the
   // input transform (they arrive while it runs), the rest once the chunk
-  // table is complete (requesting the whole ring early, or the launch tag
-  // below, measured slower: they delay the activation loads)
+  // table is complete (requesting the whole ring early measured slower)
   auto prefetch_codes = [&](int k0, int k1) {
 #pragma unroll
     for (int k = 0; k < kPrefetch; ++k) {
@@ -453,14 +452,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
       if (HAS2 && tid < 256) lut1[tid] = t1row;
     }
     __syncthreads();  // chunk table, norms (and, the first time, M and the LUTs) complete
-    if (b == 0) {
-      prefetch_codes(kEarlyTiles, kPrefetch);
-      // unconditional (a load under a branch is waited for at the branch's
-      // end, which would wait for the code tiles too); sv is a dummy source
-      // for a linear whose output transform runs in another kernel
-      epoch = __hip_atomic_load(J.out_in_kernel ? J.epoch : reinterpret_cast<unsigned*>(const_cast<float*>(J.sv)),
-                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    if (b == 0) prefetch_codes(kEarlyTiles, kPrefetch);
     float norm2 = 0.0f;
 #pragma unroll
     for (int i = 0; i < kWaves; ++i) norm2 += wsum[i];
@@ -495,6 +487,11 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   input_row(0);
   if (A.B > 1) input_row(1);
   __syncthreads();  // slice rows read (their LDS becomes the reduction slots)
+  // the launch tag's epoch: read once the input transform is done (reading it
+  // earlier measured slower); sv is a dummy source for a linear whose output
+  // transform runs in another kernel
+  epoch = __hip_atomic_load(J.out_in_kernel ? J.epoch : reinterpret_cast<unsigned*>(const_cast<float*>(J.sv)),
+                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   // MFMA operand of lane (q, b = r16): columns 64q..64q+63 of this wave's
   // slice (its own operand rows)
   const half8 hzero = {0, 0, 0, 0, 0, 0, 0, 0};
