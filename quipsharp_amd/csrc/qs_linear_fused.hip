@@ -59,7 +59,7 @@ namespace {
 
 constexpr int kThreads = kFwdThreads;
 constexpr int kMaxB = 2;
-constexpr int kPrefetch = 4;
+constexpr int kPrefetch = 2;  // code tiles in flight per wave (deeper rings measured slower)
 constexpr int kMaxJobs = QS_MAX_GROUP;
 constexpr int kXStride = 264;               // halves per slice row of the fp16 operand buffer
 constexpr int kMaxSF = 128;                 // chunks of 256 (n, m <= 32768; n <= 16384 for fp16 / fp32 x)
@@ -379,7 +379,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
       if (HAS2) pre1[k] = *reinterpret_cast<const uint2*>(J.codes1 + off / 2);
     }
   };
-  constexpr int kEarlyTiles = 2;
+  constexpr int kEarlyTiles = 1;
   float emul0 = 1.0f, emul1 = 1.0f;  // 2^e of batch rows 0 and 1
   // This wave's fp16 operand row of batch row b (slice values t = 4 lane + u
   // times mul), and the per-group sums for the +-1/4 shift term (group t / 8).
@@ -561,7 +561,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
     }
     {
       // refill this ring entry (its tile is consumed) with the tile
-      // kPrefetch row blocks ahead
+      // kPrefetch steps ahead
       const uint32_t off = code_off(own_rb(step + kPrefetch));
       pre[u] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(J.codes0) + off);
       if (HAS2) pre1[u] = *reinterpret_cast<const uint2*>(J.codes1 + off / 2);
