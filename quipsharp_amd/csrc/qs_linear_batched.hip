@@ -32,7 +32,7 @@ namespace {
 
 constexpr int kThreads = kFwdThreads;
 constexpr int kTB = 16;  // batch rows per pass (the MFMA N dimension)
-constexpr int kPrefetch = 4;
+constexpr int kPrefetch = 2;  // code tiles in flight per wave (deeper rings measured slower)
 
 // ---------------------------------------------------------------------------
 // input transform
