@@ -240,11 +240,15 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
   for (int c = 0; c < 8; ++c) xb[c] = *reinterpret_cast<const half8*>(xfrag + 512 * c);
   const half8 xs = *reinterpret_cast<const half8*>(J.sg + sla * 512 + 8 * lrow);
   // code tiles stream through a ring of kPrefetch registers (see the row
-  // loop); a tile past the end or of an idle wave reads tile 0 instead
-  // byte offset of this lane's 16 code bytes of row block rb (tile 0 past
-  // the end or for an idle wave); m n / 4 < 2^32 bytes of codes
+  // loop).  Byte offset of this lane's 16 code bytes of row block rb; past
+  // the end, the work-group's own last row block again, and the last slice
+  // for an idle wave (spread over the chip: one tile read by every idle wave
+  // is a hot spot); m n / 4 < 2^32 bytes of codes
+  const int rb_last = jr + ((RB - 1 - jr) / J.Gr) * J.Gr;
+  const uint32_t slc = (uint32_t)(sl < A.S ? sl : A.S - 1);
   auto code_off = [&](int rb) -> uint32_t {
-    return ((active && rb < RB) ? ((uint32_t)rb * (uint32_t)A.S + (uint32_t)sl) * 1024u : 0u) + 16u * lane;
+    const uint32_t r = (uint32_t)(rb < RB ? rb : rb_last);
+    return (r * (uint32_t)A.S + slc) * 1024u + 16u * lane;
   };
   uint4 pre[kPrefetch];
   uint2 pre1[kPrefetch] = {};
