@@ -701,8 +701,8 @@ def main():
                             "TFLOPs": round(flops / msp / 1e9, 1),
                             "mfma_frac_fp16_dense": round(flops / msp / 1e9 / MFMA_F16_PEAK_TFLOPS, 4),
                             "call_pattern": "grouped" if rp.grouped else "per-linear",
-                            "path": "wg_kernel: E8P decode inside the GEMM loop, fp16 x fp16 -> fp32 MFMA "
-                                    "(16x16x32), codes' +-1/4 shifts via group-sum MFMAs"}
+                            "path": "wp_kernel: 4 waves decode E8P codes (with their +-1/4 shifts) into fp16 "
+                                    "32x32x16 MFMA fragments in LDS, 4 waves multiply them (fp32 accumulate)"}
         log(f"prefill {P} rows: {msp:.3f} ms/step, {flops / msp / 1e9:.1f} TFLOP/s")
         del rp
     del stack
