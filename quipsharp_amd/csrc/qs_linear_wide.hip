@@ -326,6 +326,7 @@ constexpr int kWpABuf = 32 * 1024;              // 4 x 8 fragments of 1 KiB
 constexpr int kWpLds = kWpOffA + 2 * kWpABuf;
 constexpr int kWpRing = 8;                      // B fragment steps in flight per MFMA wave (one half slice)
 static_assert(kWpLds <= 160 * 1024, "LDS budget");
+static_assert(kWpMfmaWaves * 32 * 528 <= kWpLds, "output staging fits");
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 __global__ __launch_bounds__(kWpThreads) void wp_kernel(WgArgs A) {
@@ -496,23 +497,35 @@ __global__ __launch_bounds__(kWpThreads) void wp_kernel(WgArgs A) {
     return;
   }
   // lane l, accumulator v of tile (R, t): weight row 32 R + 8 (v / 4) + 4 (l / 32) + v % 4,
-  // activation row row0 + 32 t + l % 32; four consecutive weight rows per float4
+  // activation row row0 + 32 t + l % 32; four consecutive weight rows per float4.
+  // The tiles go out through LDS (each MFMA wave its own 32 x 528-byte area
+  // in the LUT and fragment space, free after the last barrier), so that each
+  // store instruction writes two activation rows' 512 contiguous bytes
+  // instead of 32 rows' 32 bytes (2 % of the 512-row step).
+  char* stg = lds + w * (32 * 528);
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    const int b = row0 + 32 * t + (lane & 31);
-    if (b >= A.B) continue;
-    float* yrow = A.y1p + ((size_t)g * A.B + b) * A.m;
 #pragma unroll
     for (int R = 0; R < 4; ++R)
 #pragma unroll
       for (int vg = 0; vg < 4; ++vg) {
-        const int row = rt * 128 + 32 * R + 8 * vg + 4 * (lane >> 5);
-        if (row >= A.m) continue;
         floatx4 v;
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = A.s0 * acc[R][t][4 * vg + e];
-        *reinterpret_cast<floatx4*>(yrow + row) = v;
+        *reinterpret_cast<floatx4*>(stg + (lane & 31) * 528 + (32 * R + 8 * vg + 4 * (lane >> 5)) * 4) = v;
       }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+    const int row = rt * 128 + 4 * (lane & 31);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int r = 2 * k + (lane >> 5);
+      const int b = row0 + 32 * t + r;
+      const floatx4 v = *reinterpret_cast<const floatx4*>(stg + r * 528 + (lane & 31) * 16);
+      if (b < A.B && row < A.m) *reinterpret_cast<floatx4*>(A.y1p + ((size_t)g * A.B + b) * A.m + row) = v;
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
   }
 }
 
