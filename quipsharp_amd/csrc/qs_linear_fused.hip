@@ -634,10 +634,11 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
     // wave w produces column t = 16 w + r16 of rows r = 16 a + 4 q + j.
     const int Sm = J.Sm;
     const int t = 16 * w + r16;
-    // Loads, in the order they are waited for: the K entries of M (odd
-    // factor), the first partial-sum slots, su and bias, all in flight
-    // together (unconditional loads from valid addresses, selected where they
-    // are used: a load under a branch is waited for at the branch's end).
+    // Loads: the K entries of M (odd factor), su and bias, then the first
+    // partial-sum slots (su and bias before the slots measured slightly
+    // faster), all in flight together (unconditional loads from valid
+    // addresses, selected where they are used: a load under a branch is
+    // waited for at the branch's end).
     float kmv[3];
     mmat_load(kmv, Sm, J.lsh_m, J.pm, J.Km, tid);
     float suo[OC][4], bio[OC][4];
@@ -671,11 +672,9 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
     // spilled) across the polling
     auto row = [&](const int b) {
       PollState<OC> ps;
+      if (b == 0) load_su_bias();
       poll_issue(J.y1t, J.m, Sm, A.B, b, w, lane, tag, ps);
-      if (b == 0) {
-        load_su_bias();
-        mmat_store(kmv, Sm, J.lsh_m, Mh, Ml, tid);  // waits for the K loads only
-      }
+      if (b == 0) mmat_store(kmv, Sm, J.lsh_m, Mh, Ml, tid);  // waits for the K loads only
       float zv[OC][4];
       poll_finish(J.y1t, J.m, Sm, A.SG, A.B, b, w, lane, tag, ps, zv);
       h256_chunks(zv, Sm, lane, lx);
