@@ -183,7 +183,8 @@ struct BmJob {
 
 struct BmArgs {
   int n, B, S, SG, W;
-  int tpo;  // threads per output of the reduction: a power of two, tpo * kBmSlots * 16 * B <= 1024
+  int lgBp, lgtpo;  // log2 of B rounded up to a power of two, log2 of the threads per output of the
+                    // reduction (2^lgtpo kBmSlots 16 2^lgBp <= 1024)
   int njobs;
   BmJob job[QS_MAX_GROUP];
 };
@@ -317,26 +318,30 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
     }
     if (valid && (slot == kBmSlots - 1 || rb + J.Gr >= RB)) {
       __syncthreads();
-      // output o = (s * 16 + row) * B + b of slot s <= slot, summed over the
-      // waves by tpo threads (waves part, part + tpo, ...), then across them;
-      // tpo depends on B only (a fixed summation order per output)
-      const int nout = (slot + 1) * 16 * A.B;
-      const int tpo = A.tpo;
-      const int o = tid / tpo, part = tid - o * tpo;
+      // output o = (s * 16 + row) * Bp + b of slot s <= slot (Bp: B rounded
+      // up to a power of two, so that every index is a shift; columns b >= B
+      // are skipped), summed over the waves by tpo threads (waves part, part
+      // + tpo, ...), then across them; tpo depends on B only (a fixed
+      // summation order per output)
+      const int lgBp = A.lgBp, lgt = A.lgtpo;
+      const int nout = (slot + 1) << (4 + lgBp);
+      const int tpo = 1 << lgt;
+      const int o = tid >> lgt, part = tid & (tpo - 1);
       float v = 0.0f;
       int s = 0, row = 0, bc = 0;
       if (o < nout) {
-        s = o / (16 * A.B);
-        const int rr = o - s * 16 * A.B;
-        row = rr / A.B;
-        bc = rr - row * A.B;
-        for (int ww = part; ww < nw; ww += tpo) v += red[s * kBmSlot + (ww * 16 + row) * kTB + bc];
+        s = o >> (4 + lgBp);
+        const int rr = o & ((16 << lgBp) - 1);
+        row = rr >> lgBp;
+        bc = rr & ((1 << lgBp) - 1);
+        if (bc < A.B)
+          for (int ww = part; ww < nw; ww += tpo) v += red[s * kBmSlot + (ww * 16 + row) * kTB + bc];
       }
       if (tpo >= 2) v += lane_xor<1>(v, lx);
       if (tpo >= 4) v += lane_xor<2>(v, lx);
       if (tpo >= 8) v += lane_xor<4>(v, lx);
       if (tpo >= 16) v += lane_xor<8>(v, lx);
-      if (o < nout && part == 0) {
+      if (o < nout && part == 0 && bc < A.B) {
         const int rbs = rb - (slot - s) * J.Gr;  // row block of slot s
         J.y1p[((size_t)sg * A.B + bc) * J.m + rbs * 16 + row] = v;
       }
@@ -640,8 +645,10 @@ int launch_bm_group(const BatchedPass* P, int count, hipStream_t stream, hipEven
   M.SG = P0.SG;
   M.W = P0.W;
   M.njobs = count;
-  M.tpo = 16;
-  while (M.tpo > 1 && M.tpo * kBmSlots * 16 * P0.B > kThreads) M.tpo >>= 1;
+  M.lgBp = 0;
+  while ((1 << M.lgBp) < P0.B) ++M.lgBp;
+  M.lgtpo = 4;
+  while (M.lgtpo > 0 && (kBmSlots * 16 << (M.lgtpo + M.lgBp)) > kThreads) --M.lgtpo;
   // work-groups per slice group: one per CU over all the linears, dealt in
   // proportion to their row blocks (at least one, at most one per row block)
   int budget = P0.ncu / P0.SG;
