@@ -11,9 +11,9 @@
 //   bm_kernel  decode-matvec: work-group j owns one slice group (one 256-column
 //              slice per wave) and a strided set of 16-row blocks; each wave's
 //              operand (16 batch rows of its slice) stays in registers, codes
-//              stream through a 4-tile prefetch ring, the byte-per-value LUTs
+//              stream through a 2-tile prefetch ring, the byte-per-value LUTs
 //              feed 16x16x32 MFMAs with all 16 batch columns in use, and the
-//              per-wave partials are reduced across the waves every two row
+//              per-wave partials are reduced across the waves every four row
 //              blocks into the workspace;
 //   by_kernel  output transform, one work-group per batch row: partial sums,
 //              256-point transforms, chunk stage on the matrix cores,
@@ -189,7 +189,7 @@ struct BmArgs {
   BmJob job[QS_MAX_GROUP];
 };
 
-constexpr int kBmSlots = 2;                  // row blocks reduced together
+constexpr int kBmSlots = 4;                  // row blocks reduced together (2: 0.6 % slower at 16 rows)
 constexpr int kBmSlot = kWaves * 16 * kTB;   // floats per slot: [wave][row][batch]
 constexpr int kBmOffHi = 0;                  // 4096 x uint32 (four fp16 high bytes)
 constexpr int kBmOffLo = 16384;              // 4096 x uint32
