@@ -126,8 +126,11 @@ struct WideMfma {
   float* y1p;            // [SGk][B][m]
   int SGk;
 };
-// Slice groups for (m, n, B): enough work-groups for the chip, at most the
-// output kernel's partial-group limit.
+// Slice groups for (m, n, B): as many as keep the work-groups within one
+// round over the CUs (a partial second round costs more than the split
+// saves: 11008 x 4096 at 512 rows, 172 tiles, runs 3.7 % faster over the
+// step as 1 group than as 2), at most the output kernel's partial-group
+// limit.
 int wide_splits(int64_t m, int64_t n, int64_t B, int ncu, bool has2);
 int launch_linear_wide_mfma(const WideMfma& G, hipStream_t stream);
 

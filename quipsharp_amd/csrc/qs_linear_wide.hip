@@ -549,8 +549,8 @@ int wide_splits(int64_t m, int64_t n, int64_t B, int ncu, bool has2) {
   const int64_t cols = 16 * kWgWaves * wg_ct(B, has2);
   const int64_t tiles = ((m / 16 + kWgRowTiles - 1) / kWgRowTiles) * ((B + cols - 1) / cols);
   const int64_t S = n / 256;
-  int64_t g = 1;
-  while (g < kWideMaxGroups && g < S && tiles * g < ncu) ++g;
+  int64_t g = 1;  // as many groups as fit in one round of work-groups
+  while (g < kWideMaxGroups && g < S && tiles * (g + 1) <= ncu) ++g;
   return (int)g;
 }
 
