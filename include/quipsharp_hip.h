@@ -238,7 +238,11 @@ size_t qs_linear_group_workspace_bytes(int64_t n, int64_t batch, int count, cons
  * decode-matvecs, output transforms) is one launch for the whole group,
  * except the wide GEMM (17 rows and more), one launch per job; otherwise one
  * qs_linear_forward per job.  Every output is bit-identical to
- * qs_linear_forward of that job.
+ * qs_linear_forward of that job, with one exception: above 128 rows, jobs of
+ * one shape (m, one stage) whose GEMM tiles together fit one round over the
+ * CUs share one wide GEMM launch whose K range is split for the whole group
+ * (fewer splits than a job alone), so their outputs equal qs_linear_forward's
+ * up to the order of the fp32 partial sums.
  * Requirements: 1 <= count <= QS_MAX_GROUP, tiled layout, n a multiple of 256
  * with n / kron_pn >= 256, codes1 NULL for all jobs or for none.  The workspace (zero before first use, see qs_linear_forward) holds
  * one region per job.  mv_begin / mv_end bracket the decode-matvec launch (or

@@ -1032,9 +1032,12 @@ size_t group_prefix_bytes(int count, int64_t n, M m_of) {
 
 // Grouped forward for three or more rows: the input transforms of all the
 // linears in one launch, their decode-matvecs in one launch (16-row pass) or
-// one wide GEMM each (kWideMinBatch rows and more), and their output
-// transforms in one launch (a linear whose m is outside the chunk scheme: the
-// whole-row output kernel).  Bit-identical to one qs_linear_forward per linear.
+// one wide GEMM each (kWideMinBatch rows and more; above 128 rows one GEMM
+// for linears of one shape whose tiles fit one round over the CUs), and their
+// output transforms in one launch (a linear whose m is outside the chunk
+// scheme: the whole-row output kernel).  Bit-identical to one
+// qs_linear_forward per linear, except a shared GEMM: its slice groups are the
+// group's, so the outputs equal separate calls up to the fp32 summation order.
 static int forward_group_rows(const void* x, int x_dtype, int64_t ldx, int64_t batch, int64_t n, int kron_pn,
                               const float* kron_n, int count, const qs_linear_job* jobs, int y_dtype, char* ws,
                               void* mv_begin, void* mv_end, hipStream_t s, int sbits) {
@@ -1082,23 +1085,35 @@ static int forward_group_rows(const void* x, int x_dtype, int64_t ldx, int64_t b
   int rc = launch_bx_group(P, count, s);
   if (rc) return rc;
   if (wide) {
+    if (mv_begin) QS_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(mv_begin), s));
+    // linears of one shape whose tiles fit one round over the CUs: one GEMM
+    // launch with the slice groups chosen for the group
+    bool one_shape = true;
+    for (int g = 0; g < count; ++g) one_shape = one_shape && P[g].m == P[0].m && P[g].codes1 == nullptr;
+    const int gsk = one_shape ? wide_group_splits(P[0].m, n, batch, count, cu_count()) : 0;
+    WideMfma F[QS_MAX_GROUP];
     for (int g = 0; g < count; ++g) {
-      if (g == 0 && mv_begin) QS_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(mv_begin), s));
-      WideMfma F{};
-      F.codes0 = P[g].codes0;
-      F.codes1 = P[g].codes1;
-      F.m = P[g].m;
-      F.n = n;
-      F.B = (int)batch;
-      F.s0 = P[g].s0;
-      F.s1 = P[g].s1;
-      F.x2f = P[g].x2h;
-      F.sgf = P[g].sg;
-      F.y1p = P[g].y1p;
-      F.SGk = wide_splits(P[g].m, n, batch, cu_count(), P[g].codes1 != nullptr);
-      rc = launch_linear_wide_mfma(F, s);
+      F[g] = WideMfma{};
+      F[g].codes0 = P[g].codes0;
+      F[g].codes1 = P[g].codes1;
+      F[g].m = P[g].m;
+      F[g].n = n;
+      F[g].B = (int)batch;
+      F[g].s0 = P[g].s0;
+      F[g].s1 = P[g].s1;
+      F[g].x2f = P[g].x2h;
+      F[g].sgf = P[g].sg;
+      F[g].y1p = P[g].y1p;
+      F[g].SGk = gsk ? gsk : wide_splits(P[g].m, n, batch, cu_count(), P[g].codes1 != nullptr);
+      if (!gsk) {
+        rc = launch_linear_wide_mfma(F[g], s);
+        if (rc) return rc;
+      }
+      P[g].SG = F[g].SGk;  // partial groups summed by the output kernels
+    }
+    if (gsk) {
+      rc = launch_linear_wide_group(F, count, s);
       if (rc) return rc;
-      P[g].SG = F.SGk;  // partial groups summed by the output kernels
     }
     if (mv_end) QS_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(mv_end), s));
   } else {

@@ -132,6 +132,14 @@ struct WideMfma {
 // step as 1 group than as 2), at most the output kernel's partial-group
 // limit.
 int wide_splits(int64_t m, int64_t n, int64_t B, int ncu, bool has2);
+// Linears of one shape (m, n, B) with one stage above 128 rows whose tiles
+// together fit one round over the CUs share one producer / consumer GEMM
+// launch (launch_linear_wide_group), with the slice groups chosen for the
+// whole group (fewer than each would take alone, so their outputs equal
+// separate calls up to the fp32 summation order).  Returns those slice
+// groups, or 0 when the linears take one launch each.
+int wide_group_splits(int64_t m, int64_t n, int64_t B, int count, int ncu);
+int launch_linear_wide_group(const WideMfma* G, int count, hipStream_t stream);
 int launch_linear_wide_mfma(const WideMfma& G, hipStream_t stream);
 
 

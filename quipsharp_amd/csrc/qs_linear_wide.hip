@@ -60,6 +60,16 @@ constexpr int kWgCopies = kWgCodeBuf / (16 * kWgThreads);  // 16-byte code copie
 static_assert(kWgCopies >= 1 && kWgCopies <= 2 && kWgCopies * 16 * kWgThreads == kWgCodeBuf, "code copy");
 static_assert(kWgThreads >= 256, "E8 one-bit table rows: one per thread of the first 256");
 
+// One linear of a wp_kernel launch: linears of one shape (m, n, rows) that
+// read their own operands share a launch, job j taking tiles j T1 .. (j + 1)
+// T1 - 1 of the grid's tile order (T1 = nrt nct SGk).
+struct WpJob {
+  const uint16_t* codes0;
+  const _Float16* x2f;
+  float* y1p;
+  float s0;
+};
+
 struct WgArgs {
   const uint16_t* codes0;
   const uint8_t* codes1;
@@ -70,6 +80,8 @@ struct WgArgs {
   int nrt, nct;        // work-group tiles along the weight rows / activation rows
   int SGk, spg;        // slice groups, slices per group
   float s0, s1;
+  int njobs;           // wp_kernel: linears of the launch (job[0]: the fields above)
+  WpJob job[QS_MAX_GROUP];
 };
 
 template <bool HAS2, int kWgColTiles>
@@ -335,11 +347,18 @@ __global__ __launch_bounds__(kWpThreads) void wp_kernel(WgArgs A) {
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  // tile order as wg_kernel (XCD-contiguous runs)
-  const int T = A.nrt * A.nct * A.SGk;
+  // tile order as wg_kernel (XCD-contiguous runs), job after job
+  const int T1 = A.nrt * A.nct * A.SGk;
+  const int T = A.njobs * T1;
   const int per = (T + 7) >> 3;
   int bid = ((int)blockIdx.x & 7) * per + ((int)blockIdx.x >> 3);
   if (bid >= T) return;
+  int jj = 0;
+#pragma unroll
+  for (int k = 1; k < QS_MAX_GROUP; ++k)
+    if (k < A.njobs && bid >= k * T1) jj = k;
+  const WpJob& J = A.job[jj];
+  bid -= jj * T1;
   const int rt = bid % A.nrt;
   bid /= A.nrt;
   const int ct = bid % A.nct;
@@ -368,7 +387,7 @@ __global__ __launch_bounds__(kWpThreads) void wp_kernel(WgArgs A) {
       int rb = rt * 8 + 2 * d + ii;
       rb = rb < A.RB ? rb : A.RB - 1;  // past the end: the last row block (decoded, never stored)
       s = s < s_last ? s : s_last;
-      return *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(A.codes0) +
+      return *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(J.codes0) +
                                              ((size_t)rb * A.S + s) * 1024 + 16 * lane);
     };
     // half h of the slice whose code words are c0 / c1 into buffer h
@@ -423,7 +442,7 @@ __global__ __launch_bounds__(kWpThreads) void wp_kernel(WgArgs A) {
     const int r = row0 + 32 * t + (lane & 31);
     int c16 = r >> 4;
     c16 = c16 < nbt ? c16 : nbt - 1;  // rows past the batch: computed, never stored
-    xrow[t] = A.x2f + (size_t)c16 * A.S * 8 * 512 + 8 * ((lane >> 5) * 16 + (r & 15));
+    xrow[t] = J.x2f + (size_t)c16 * A.S * 8 * 512 + 8 * ((lane >> 5) * 16 + (r & 15));
   }
   // slices past the work-group's last are clamped to it: those loads are in
   // bounds and never used, so every load is unconditional
@@ -511,7 +530,7 @@ __global__ __launch_bounds__(kWpThreads) void wp_kernel(WgArgs A) {
       for (int vg = 0; vg < 4; ++vg) {
         floatx4 v;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = A.s0 * acc[R][t][4 * vg + e];
+        for (int e = 0; e < 4; ++e) v[e] = J.s0 * acc[R][t][4 * vg + e];
         *reinterpret_cast<floatx4*>(stg + (lane & 31) * 528 + (32 * R + 8 * vg + 4 * (lane >> 5)) * 4) = v;
       }
     __builtin_amdgcn_s_waitcnt(0xc07f);
@@ -522,7 +541,7 @@ __global__ __launch_bounds__(kWpThreads) void wp_kernel(WgArgs A) {
       const int r = 2 * k + (lane >> 5);
       const int b = row0 + 32 * t + r;
       const floatx4 v = *reinterpret_cast<const floatx4*>(stg + r * 528 + (lane & 31) * 16);
-      if (b < A.B && row < A.m) *reinterpret_cast<floatx4*>(A.y1p + ((size_t)g * A.B + b) * A.m + row) = v;
+      if (b < A.B && row < A.m) *reinterpret_cast<floatx4*>(J.y1p + ((size_t)g * A.B + b) * A.m + row) = v;
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
@@ -554,12 +573,20 @@ int wide_splits(int64_t m, int64_t n, int64_t B, int ncu, bool has2) {
   return (int)g;
 }
 
-int launch_linear_wide_mfma(const WideMfma& G, hipStream_t stream) {
-  QS_REQUIRE(G.m % 16 == 0 && G.n % 256 == 0 && G.B >= 1, "wide GEMM: m %% 16, n %% 256");
-  QS_REQUIRE(G.SGk >= 1 && G.SGk <= kWideMaxGroups, "wide GEMM: 1..%d slice groups", kWideMaxGroups);
-  QS_REQUIRE(G.m * G.n / 4 < ((int64_t)1 << 40), "wide GEMM: codes too large");
-  const bool has2 = G.codes1 != nullptr;
-  const int CT = wg_ct(G.B, has2);
+int wide_group_splits(int64_t m, int64_t n, int64_t B, int count, int ncu) {
+  if (count < 2 || wg_ct(B, false) != 4) return 0;
+  const int64_t cols = 16 * kWgWaves * 4;
+  const int64_t tiles = ((m / 16 + kWgRowTiles - 1) / kWgRowTiles) * ((B + cols - 1) / cols) * count;
+  if (tiles > ncu) return 0;
+  const int64_t S = n / 256;
+  int64_t g = 1;
+  while (g < kWideMaxGroups && g < S && tiles * (g + 1) <= ncu) ++g;
+  return (int)g;
+}
+
+namespace {
+WgArgs wide_args(const WideMfma& G) {
+  const int CT = wg_ct(G.B, G.codes1 != nullptr);
   WgArgs A{};
   A.codes0 = static_cast<const uint16_t*>(G.codes0);
   A.codes1 = static_cast<const uint8_t*>(G.codes1);
@@ -576,6 +603,24 @@ int launch_linear_wide_mfma(const WideMfma& G, hipStream_t stream) {
   A.spg = (A.S + G.SGk - 1) / G.SGk;
   A.s0 = G.s0;
   A.s1 = G.s1;
+  A.njobs = 1;
+  A.job[0] = WpJob{A.codes0, A.x2f, A.y1p, A.s0};
+  return A;
+}
+int check_wide(const WideMfma& G) {
+  QS_REQUIRE(G.m % 16 == 0 && G.n % 256 == 0 && G.B >= 1, "wide GEMM: m %% 16, n %% 256");
+  QS_REQUIRE(G.SGk >= 1 && G.SGk <= kWideMaxGroups, "wide GEMM: 1..%d slice groups", kWideMaxGroups);
+  QS_REQUIRE(G.m * G.n / 4 < ((int64_t)1 << 40), "wide GEMM: codes too large");
+  return QS_OK;
+}
+}  // namespace
+
+int launch_linear_wide_mfma(const WideMfma& G, hipStream_t stream) {
+  int rc = check_wide(G);
+  if (rc) return rc;
+  const bool has2 = G.codes1 != nullptr;
+  const int CT = wg_ct(G.B, has2);
+  const WgArgs A = wide_args(G);
   const int64_t tiles = (int64_t)A.nrt * A.nct * A.SGk;
   QS_REQUIRE(tiles < ((int64_t)1 << 30), "wide GEMM: grid too large");
   const int64_t grid = (tiles + 7) / 8 * 8;  // XCD-contiguous tile order (see wg_kernel)
@@ -584,6 +629,24 @@ int launch_linear_wide_mfma(const WideMfma& G, hipStream_t stream) {
   if (CT == 4) return launch_wp(A, g, stream);  // 256 activation rows per work-group, as wp_kernel's
   return CT == 1 ? launch_wg<false, 1>(A, g, stream)
                  : CT == 2 ? launch_wg<false, 2>(A, g, stream) : launch_wg<false, 4>(A, g, stream);
+}
+
+int launch_linear_wide_group(const WideMfma* G, int count, hipStream_t stream) {
+  QS_REQUIRE(count >= 1 && count <= QS_MAX_GROUP, "wide GEMM group: 1..%d linears", QS_MAX_GROUP);
+  for (int j = 0; j < count; ++j) {
+    const int rc = check_wide(G[j]);
+    if (rc) return rc;
+    QS_REQUIRE(G[j].m == G[0].m && G[j].n == G[0].n && G[j].B == G[0].B && G[j].SGk == G[0].SGk &&
+                   G[j].codes1 == nullptr && wg_ct(G[j].B, false) == 4,
+               "wide GEMM group: one shape, one stage, more than %d rows", 16 * kWgWaves * 2);
+  }
+  WgArgs A = wide_args(G[0]);
+  A.njobs = count;
+  for (int j = 0; j < count; ++j)
+    A.job[j] = WpJob{static_cast<const uint16_t*>(G[j].codes0), G[j].x2f, G[j].y1p, G[j].s0};
+  const int64_t tiles = (int64_t)A.nrt * A.nct * A.SGk * count;
+  QS_REQUIRE(tiles < ((int64_t)1 << 30), "wide GEMM: grid too large");
+  return launch_wp(A, (unsigned)((tiles + 7) / 8 * 8), stream);
 }
 
 }  // namespace qs

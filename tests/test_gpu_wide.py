@@ -117,3 +117,46 @@ def test_wide_matches_narrow_path(dev):
     yw, _ = run(dev, x, codes, None, 1.0, 0.0, su, sv, 0.0135)
     yn, _ = run(dev, x[:16], codes, None, 1.0, 0.0, su, sv, 0.0135)
     assert rel_err(yw[:16].cpu().numpy(), yn.cpu().numpy().astype(np.float64)) < 2e-4
+
+
+@pytest.mark.parametrize("shapes,n,B", [
+    ([4096, 4096, 4096], 4096, 300),  # 3 x 64 tiles: one shared launch, one slice group (4 alone)
+    ([2048, 2048], 2048, 140),        # 2 x 16 tiles: one shared launch, 8 slice groups as alone
+    ([11008, 11008], 4096, 300),      # 2 x 172 tiles, more than one round: one launch each
+    ([4096, 1024], 4096, 300),        # two shapes: one launch each
+])
+def test_wide_group_shared_gemm(dev, shapes, n, B):
+    """Linears of one shape above 128 rows whose GEMM tiles fit one round over
+    the CUs share one wp_kernel launch, with the slice groups chosen for the
+    group: each output equals the single call up to the fp32 summation order
+    (bit-identical when they take one launch each) and matches the dense fp64
+    oracle."""
+    print(f"case: wide group {shapes} n={n} B={B}", flush=True)
+    from test_gpu_linear import _rand_linear
+    from quipsharp_amd.quantize import forward_packed, forward_packed_group
+    seed = sum(shapes) + n + B + 5
+    rng = np.random.default_rng(seed)
+    lins = [_rand_linear(dev, rng, m, n, 1, True) for m in shapes]
+    x = torch.randn(B, n, generator=torch.Generator().manual_seed(seed)).to(dev).bfloat16()
+    ys = forward_packed_group(x, lins)
+    shared = len(set(shapes)) == 1 and shapes[0] * len(shapes) * ((B + 255) // 256) <= 128 * 256
+    for lin, y in zip(lins, ys):
+        want = forward_packed(x, *lin)
+        assert y.shape == want.shape
+        if shared:
+            a, b = y.float().cpu().numpy(), want.float().cpu().numpy()
+            assert np.all(np.abs(a - b) <= 2 ** -7 * np.abs(b) + 1e-4 * np.abs(b).max())
+        else:
+            assert torch.equal(y, want)
+    # the first linear against the dense oracle (its draws repeated)
+    rng2 = np.random.default_rng(seed)
+    m0 = shapes[0]
+    c0 = rng2.integers(0, 65536, (m0, n // 8))
+    su_np = rng2.choice([-1.0, 1.0], m0)
+    sv_np = rng2.choice([-1.0, 1.0], n)
+    b_np = rng2.standard_normal(m0).astype(np.float32)
+    packed, su, sv, s0, s1, sc, b = lins[0]
+    want = dense_forward(x.float().cpu().numpy(), c0, None, s0, 0.0, su_np, sv_np, sc, b_np)
+    got = ys[0].float().cpu().numpy()  # bf16 outputs: half an ulp of bf16 on top of the forward's error
+    print(f"  rel err {rel_err(got, want):.2e}", flush=True)
+    assert np.all(np.abs(got - want) <= 2 ** -8 * np.abs(want) + 2e-3 * np.abs(want).max())
