@@ -25,6 +25,8 @@ pytestmark = pytest.mark.gpu
     (1024, 2048, 500),    # two work-group columns of 256 rows, the second ragged
     (784, 1024, 420),     # 49 row blocks: the last work-group row holds one; m = 49 x 16
     (4096, 2048, 300),    # 64 work-group tiles: K split in 4 slice groups (the 4-group output kernel)
+    (1024, 2048, 1031),   # more rows than two transform work-groups per CU: two or three rows each
+    (512, 11008, 515),    # three chunks per wave in the transforms, two or three rows per work-group
 ])
 def test_wide_vs_dense_fp64(dev, m, n, B):
     print(f"case: wide m={m} n={n} B={B}", flush=True)
