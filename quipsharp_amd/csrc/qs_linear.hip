@@ -41,7 +41,7 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 constexpr int kMaxParts = 16;  // work-groups per batch row for odd-factor transforms
 
 struct WsLayout {
-  size_t x2h, sg, xtot, xmul, x2, y1p, y1t, h2t, total;
+  size_t x2h, sg, xtot, xmul, x2, y1p, y1t, h2t, y1bt, total;
   int S, SG, W;    // chunks, slice groups and slices per group of the decode-matvec
   FusedPlan fused;  // the one-launch kernel's (its partial sums: fused.SG groups)
   bool wide;
@@ -77,12 +77,14 @@ int cu_count() {
   return cached[dev];
 }
 
-// The first 256 bytes of every workspace hold the one-launch kernel's epoch
-// (the tag of its last launch's partial sums; zero before the first call).
-// With the tiled layout the next regions hold that kernel's tagged partial
-// sums (8 bytes per slot, up to two rows) and tagged chunk transforms (its
-// two-level output transform), which no other kernel writes, so a slot can
-// only carry a tag of an earlier launch of the same workspace.
+// The first 256 bytes of every workspace hold the epoch of the kernels with
+// tagged partial sums (the tag of the last such launch; zero before the
+// first call).  With the tiled layout the next regions hold the one-launch
+// kernel's tagged partial sums (8 bytes per slot, up to two rows) and tagged
+// chunk transforms (its two-level output transform), and the last region the
+// 16-row decode-matvec's tagged partial sums; each is written by its kernel
+// only, so a slot can only carry a tag of an earlier launch of the same
+// workspace.
 WsLayout ws_layout(int64_t m, int64_t n, int64_t batch, int layout) {
   WsLayout L{};
   L.wide = layout == QS_LAYOUT_TILED && batch >= kWideMinBatch;
@@ -116,6 +118,11 @@ WsLayout ws_layout(int64_t m, int64_t n, int64_t batch, int layout) {
   } else {
     const int sgp = L.SG > L.fused.SG ? L.SG : L.fused.SG;
     L.y1p = off; off = align256(off + (size_t)sgp * B * m * 4);
+    if (layout == QS_LAYOUT_TILED) {
+      // tagged partial sums of the 16-row decode-matvec that applies the
+      // output transform itself (written by no other kernel)
+      L.y1bt = off; off = align256(off + (size_t)L.SG * B * m * 8);
+    }
   }
   L.total = off;
   return L;
@@ -767,6 +774,8 @@ static int forward_batched(const void* x, int x_dtype, int64_t ldx, int64_t batc
       hipEvent_t ev0 = b0 == 0 ? reinterpret_cast<hipEvent_t>(mv_begin) : nullptr;
       hipEvent_t ev1 = b0 + kMaxTileBatch >= batch ? reinterpret_cast<hipEvent_t>(mv_end) : nullptr;
       if (!identity && batched_eligible(n, kron_pn, m, kron_pm) && sv_aligned) {
+        P.y1t = reinterpret_cast<unsigned long long*>(ws + W.y1bt);  // output transform in the decode-matvec
+        P.epoch = reinterpret_cast<unsigned*>(ws);
         rc = launch_linear_batched(P, s, ev0, ev1);
       } else {
         if (!identity && chunk_transform_fits(n, kron_pn) && sv_aligned)
@@ -1080,6 +1089,10 @@ static int forward_group_rows(const void* x, int x_dtype, int64_t ldx, int64_t b
     Q.y1p = reinterpret_cast<float*>(ws + off + W.y1p);
     Q.frag = 1;
     Q.sbits = sbits;
+    if (!wide) {
+      Q.y1t = reinterpret_cast<unsigned long long*>(ws + off + W.y1bt);
+      Q.epoch = reinterpret_cast<unsigned*>(ws) + g;
+    }
     off += W.total;
   }
   int rc = launch_bx_group(P, count, s);
@@ -1117,8 +1130,11 @@ static int forward_group_rows(const void* x, int x_dtype, int64_t ldx, int64_t b
     }
     if (mv_end) QS_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(mv_end), s));
   } else {
-    rc = launch_bm_group(P, count, s, reinterpret_cast<hipEvent_t>(mv_begin), reinterpret_cast<hipEvent_t>(mv_end));
+    bool tail = false;
+    rc = launch_bm_group(P, count, s, reinterpret_cast<hipEvent_t>(mv_begin), reinterpret_cast<hipEvent_t>(mv_end),
+                         &tail);
     if (rc) return rc;
+    if (tail) return QS_OK;  // the decode-matvec applied the output transforms
   }
   // output transforms: the chunk-scheme ones in one launch, the others one by one
   BatchedPass Pc[QS_MAX_GROUP];

@@ -176,15 +176,29 @@ struct BmJob {
   const uint8_t* codes1;
   const _Float16* x2h;  // fragment-major operand of this linear (16 rows)
   const _Float16* sg;
-  float* y1p;  // [SG][B][m]
+  float* y1p;  // [SG][B][m] partial sums for a separate output kernel
   int m, Gr, wg0;
   float s0, s1;
+  // output transform in this kernel (the tail instantiations): tagged
+  // partial sums [SG][B][m], the epoch word of the job, and by_kernel's
+  // per-linear arguments
+  unsigned long long* y1t;
+  unsigned* epoch;
+  const float* xmul;
+  int Sm, lsh_m, pm;
+  const float* Km;
+  float scale_m, layer_scale;
+  const float* su;
+  const float* bias;
+  void* y;
+  int64_t ldy;
 };
 
 struct BmArgs {
   int n, B, S, SG, W;
   int lgBp, lgtpo;  // log2 of B rounded up to a power of two, log2 of the threads per output of the
                     // reduction (2^lgtpo kBmSlots 16 2^lgBp <= 1024)
+  int y_dtype;      // tail instantiations: output dtype
   int njobs;
   BmJob job[QS_MAX_GROUP];
 };
@@ -198,7 +212,16 @@ constexpr int kBmOffRed = kBmOffLut1 + 4096; // kBmSlots x kBmSlot floats
 constexpr int kBmLds = kBmOffRed + kBmSlots * kBmSlot * 4;
 static_assert(kBmLds <= 160 * 1024, "LDS budget");
 
-template <bool HAS2>
+// OC > 0: the output transform runs in this kernel as well (OC output
+// chunks per wave, SB: su as packed sign bits).  The partial sums go out as
+// tagged 64-bit slots (as in the one-launch kernel, qs_forward_dev.h), and
+// work-group b < B of each linear, once its own row blocks are done, polls
+// batch row b's slots (every work-group of the linear writes every row's) and
+// applies by_kernel's output transform to that row: the same sums in the
+// same order, so the outputs are bit-identical to bm_kernel + by_kernel.  The
+// grid is at most one work-group per CU, so every polled work-group runs; a
+// poll is bounded (NaN outputs if a slot never arrives).
+template <bool HAS2, int OC, bool SB>
 __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
   uint4* lut1 = reinterpret_cast<uint4*>(lds + kBmOffLut1);
@@ -262,6 +285,10 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
   store_luts(lds, tid, lutw);
   if (HAS2 && tid < 256) lut1[tid] = t1row;
   __syncthreads();
+  // tag of this launch's partial sums (tail instantiations); the epoch only
+  // changes once a tail work-group has read every slot of its row
+  uint32_t tag = 0;
+  if constexpr (OC > 0) tag = next_tag(__hip_atomic_load(J.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), g);
 
   float slice_shift = 0.0f;  // sum_g S_g / 4 over the slice, batch row r16
 #pragma unroll
@@ -343,12 +370,77 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
       if (tpo >= 16) v += lane_xor<8>(v, lx);
       if (o < nout && part == 0 && bc < A.B) {
         const int rbs = rb - (slot - s) * J.Gr;  // row block of slot s
-        J.y1p[((size_t)sg * A.B + bc) * J.m + rbs * 16 + row] = v;
+        const size_t idx = ((size_t)sg * A.B + bc) * J.m + rbs * 16 + row;
+        if constexpr (OC > 0)
+          __hip_atomic_store(&J.y1t[idx], tagged(v, tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+          J.y1p[idx] = v;
       }
       __syncthreads();  // the slots are free again
     }
     k += valid;
   }
+  }
+  if constexpr (OC > 0) {
+    // output transform of batch row lb (by_kernel's, on polled slots)
+    if (lb >= A.B) return;
+    const int b = lb;
+    using L = RowLds<OC>;
+    __syncthreads();  // the LUT and reduction space becomes the row's chunk rows and M
+    float* Y = reinterpret_cast<float*>(lds + L::kY);
+    uint16_t* Mh = reinterpret_cast<uint16_t*>(lds + L::kMh);
+    uint16_t* Ml = reinterpret_cast<uint16_t*>(lds + L::kMl);
+    const int Sm = J.Sm;
+    const int t = 16 * w + r16;
+    float kmv[3];
+    mmat_load(kmv, Sm, J.lsh_m, J.pm, J.Km, tid);
+    int oidx[OC][4];
+    float suo[OC][4], bio[OC][4];
+    // no bias: a dummy load from the slots (at least m entries), selected
+    // away rather than multiplied by 0
+    const float* const bsrc = J.bias ? J.bias : reinterpret_cast<const float*>(J.y1t);
+    const bool has_bias = J.bias != nullptr;
+#pragma unroll
+    for (int a = 0; a < OC; ++a)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = 16 * a + 4 * q + j;
+        oidx[a][j] = r < Sm ? 256 * r + t : -1;
+        const int ii = oidx[a][j] >= 0 ? oidx[a][j] : 0;
+        suo[a][j] = load_su(J.su, SB, ii);
+        bio[a][j] = at_off(bsrc, (uint32_t)ii);
+      }
+    const float xm = J.xmul[b];
+    PollState<OC> ps;
+    poll_issue(J.y1t, J.m, Sm, A.B, b, w, lane, tag, ps);
+    mmat_store(kmv, Sm, J.lsh_m, Mh, Ml, tid);
+    float zv[OC][4];
+    poll_finish(J.y1t, J.m, Sm, A.SG, A.B, b, w, lane, tag, ps, zv);
+    const float mul = J.scale_m * J.layer_scale * xm;
+    h256_chunks(zv, Sm, lane, lx);
+    store_chunks_lanes(Y, Sm, w, lane, zv);
+    __syncthreads();  // chunk rows and M complete
+    const int nrt = (Sm + 15) >> 4, nkb = (Sm + 31) >> 5;
+    floatx4 acc[OC];
+#pragma unroll
+    for (int a = 0; a < OC; ++a) acc[a] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int kb = 0; kb < nkb; ++kb) {
+      const ZOperand z = z_operand(Y, Sm, t, q, kb);
+#pragma unroll
+      for (int a = 0; a < OC; ++a)
+        if (a < nrt) acc[a] = mstage_step(acc[a], Mh, Ml, 16 * a, z, kb, J.pm > 1, q, r16);
+    }
+    float out[OC][4];
+#pragma unroll
+    for (int a = 0; a < OC; ++a)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        out[a][j] = apply_su(acc[a][j] * mul, suo[a][j], SB, oidx[a][j]) + (has_bias ? bio[a][j] : 0.0f);
+    store_outputs(J.y, A.y_dtype, (int64_t)b * J.ldy, oidx, out);
+    // every slot of row b has been read, so every work-group of the linear has
+    // read the epoch: the next launch's tag follows this one (all the tail
+    // work-groups store the same value)
+    if (tid == 0) __hip_atomic_store(J.epoch, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -496,11 +588,27 @@ unsigned row_grid(int B, int ncu) {
   return (unsigned)(B < cap ? B : cap);
 }
 
-int check_bm_lds() {
-  static int done_m0 = 0, done_m1 = 0;
-  int rc = lds_checked((const void*)bm_kernel<false>, kBmLds, &done_m0);
-  if (!rc) rc = lds_checked((const void*)bm_kernel<true>, kBmLds, &done_m1);
-  return rc;
+template <bool HAS2, int OC, bool SB>
+int launch_bm_v(const BmArgs& M, unsigned grid, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop) {
+  static int done = 0;
+  const int rc = lds_checked((const void*)bm_kernel<HAS2, OC, SB>, kBmLds, &done);
+  if (rc) return rc;
+  hipExtLaunchKernelGGL((bm_kernel<HAS2, OC, SB>), dim3(grid), dim3(kThreads), kBmLds, stream, ev_start, ev_stop, 0, M);
+  QS_LAUNCHED("bm_kernel");
+  return QS_OK;
+}
+template <bool HAS2>
+int launch_bm_h(const BmArgs& M, int oc, bool sb, unsigned grid, hipStream_t stream, hipEvent_t ev_start,
+                hipEvent_t ev_stop) {
+  switch (oc) {
+    case 0: return launch_bm_v<HAS2, 0, false>(M, grid, stream, ev_start, ev_stop);
+    case 1: return sb ? launch_bm_v<HAS2, 1, true>(M, grid, stream, ev_start, ev_stop)
+                      : launch_bm_v<HAS2, 1, false>(M, grid, stream, ev_start, ev_stop);
+    case 2: return sb ? launch_bm_v<HAS2, 2, true>(M, grid, stream, ev_start, ev_stop)
+                      : launch_bm_v<HAS2, 2, false>(M, grid, stream, ev_start, ev_stop);
+    default: return sb ? launch_bm_v<HAS2, 3, true>(M, grid, stream, ev_start, ev_stop)
+                       : launch_bm_v<HAS2, 3, false>(M, grid, stream, ev_start, ev_stop);
+  }
 }
 
 template <int CPW, bool SB>
@@ -629,15 +737,14 @@ int launch_by_group(const BatchedPass* P, int count, hipStream_t stream) {
 
 int launch_by_rows(const BatchedPass& P, hipStream_t stream) { return launch_by_group(&P, 1, stream); }
 
-int launch_bm_group(const BatchedPass* P, int count, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop) {
+int launch_bm_group(const BatchedPass* P, int count, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop,
+                    bool* tail_done) {
   QS_REQUIRE(count >= 1 && count <= QS_MAX_GROUP, "decode-matvec: 1..%d linears", QS_MAX_GROUP);
   const BatchedPass& P0 = P[0];
   QS_REQUIRE(P0.B >= 1 && P0.B <= kTB, "batched pass: 1..%d rows", kTB);
   QS_REQUIRE(P0.n % 256 == 0 && P0.S == (int)(P0.n / 256) && P0.SG >= 1 && P0.W >= 1 && P0.W <= kWaves &&
                  P0.SG * P0.W >= P0.S,
              "decode-matvec: bad slice grouping");
-  int rc = check_bm_lds();
-  if (rc) return rc;
   BmArgs M{};
   M.n = (int)P0.n;
   M.B = P0.B;
@@ -678,25 +785,60 @@ int launch_bm_group(const BatchedPass* P, int count, hipStream_t stream, hipEven
     J.s1 = Q.s1;
     wg += J.Gr * P0.SG;
   }
+  // output transforms in this launch when every linear provides tagged
+  // partial-sum slots (bm_tail_eligible) and has a work-group per row
+  // (work-group b < B of each linear transforms row b), the grid fitting the
+  // CUs
+  bool tail = bm_tail_eligible(P, count) && wg <= (P0.ncu > 0 ? P0.ncu : 256);
+  for (int j = 0; j < count; ++j) tail = tail && M.job[j].Gr * P0.SG >= P0.B;
+  if (tail_done) *tail_done = tail;
+  int oc = 0;
+  if (tail) {
+    M.y_dtype = P0.y_dtype;
+    for (int j = 0; j < count; ++j) {
+      const BatchedPass& Q = P[j];
+      BmJob& J = M.job[j];
+      J.y1t = Q.y1t;
+      J.epoch = Q.epoch;
+      J.xmul = Q.xmul;
+      J.Sm = (int)(Q.m / 256);
+      J.lsh_m = log2_exact((int)(Q.m / Q.pm / 256));
+      J.pm = Q.pm;
+      J.Km = Q.Km;
+      J.scale_m = inv_sqrt_len((int)(Q.m / Q.pm));
+      J.layer_scale = Q.layer_scale;
+      J.su = Q.su;
+      J.bias = Q.bias;
+      J.y = Q.y;
+      J.ldy = Q.ldy;
+      const int c = chunks_per_wave(J.Sm);
+      if (c > oc) oc = c;
+    }
+  }
   const unsigned grid = (unsigned)wg;
-  if (P0.codes1)
-    hipExtLaunchKernelGGL(bm_kernel<true>, dim3(grid), dim3(kThreads), kBmLds, stream, ev_start, ev_stop, 0, M);
-  else
-    hipExtLaunchKernelGGL(bm_kernel<false>, dim3(grid), dim3(kThreads), kBmLds, stream, ev_start, ev_stop, 0, M);
-  QS_LAUNCHED("bm_kernel");
-  return QS_OK;
+  return P0.codes1 ? launch_bm_h<true>(M, oc, P0.sbits != 0, grid, stream, ev_start, ev_stop)
+                   : launch_bm_h<false>(M, oc, P0.sbits != 0, grid, stream, ev_start, ev_stop);
 }
 
-int launch_bm(const BatchedPass& P, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop) {
-  return launch_bm_group(&P, 1, stream, ev_start, ev_stop);
+bool bm_tail_eligible(const BatchedPass* P, int count) {
+  for (int j = 0; j < count; ++j)
+    if (!P[j].y1t || !P[j].epoch || P[j].B > kTB || !chunk_transform_fits(P[j].m, P[j].pm) ||
+        P[j].y_dtype != P[0].y_dtype || P[j].sbits != P[0].sbits)
+      return false;
+  return count >= 1;
+}
+
+int launch_bm(const BatchedPass& P, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop, bool* tail_done) {
+  return launch_bm_group(&P, 1, stream, ev_start, ev_stop, tail_done);
 }
 
 int launch_linear_batched(const BatchedPass& P, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop) {
   QS_REQUIRE(P.B >= 1 && P.B <= kTB, "batched pass: 1..%d rows", kTB);
   QS_REQUIRE(batched_eligible(P.n, P.pn, P.m, P.pm), "batched pass: shapes outside the chunk scheme");
   int rc = launch_bx_rows(P, stream);
-  if (!rc) rc = launch_bm(P, stream, ev_start, ev_stop);
-  if (!rc) rc = launch_by_rows(P, stream);
+  bool tail = false;
+  if (!rc) rc = launch_bm(P, stream, ev_start, ev_stop, &tail);
+  if (!rc && !tail) rc = launch_by_rows(P, stream);  // else done inside the decode-matvec
   return rc;
 }
 

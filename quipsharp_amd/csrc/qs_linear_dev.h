@@ -68,8 +68,16 @@ struct BatchedPass {
                          // and the wide GEMM read; the decode-matvec requires it)
   float* xmul;           // workspace: [B]
   float* y1p;            // workspace: [SG][B][m]
+  unsigned long long* y1t;  // workspace: [SG][B][m] tagged slots, or null: with them the decode-matvec
+                            // applies the output transform itself (bm_tail_eligible)
+  unsigned* epoch;       // the epoch word of the linear's tags (with y1t)
 };
 bool batched_eligible(int64_t n, int pn, int64_t m, int pm);
+// The decode-matvec of these linears may also apply their output transforms
+// (one launch fewer per pass; launch_bm / launch_bm_group report it in
+// tail_done) when every one has tagged slots (y1t, epoch), at most 16 rows, m
+// on the chunk scheme, and they share the output dtype and sign format.
+bool bm_tail_eligible(const BatchedPass* P, int count);
 int launch_linear_batched(const BatchedPass& P, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop);
 // The per-row input / output transform kernels of a pass on their own, for
 // any number of rows P.B (the output reads P.SG partial groups of P.B rows).
@@ -80,11 +88,13 @@ int launch_by_rows(const BatchedPass& P, hipStream_t stream);
 int launch_bx_group(const BatchedPass* P, int count, hipStream_t stream);
 // The decode-matvec of a pass on its own (any n; operand in x2h / sg,
 // fragment-major, 16 rows), y1p[SG][B][m].
-int launch_bm(const BatchedPass& P, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop);
+int launch_bm(const BatchedPass& P, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop,
+              bool* tail_done = nullptr);
 // The same for several linears of one operand (shared x2h, sg, n, B, slice
 // grouping, stages) in one launch: the work-groups are dealt to the linears in
 // proportion to their rows.  Bit-identical to one launch per linear.
-int launch_bm_group(const BatchedPass* P, int count, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop);
+int launch_bm_group(const BatchedPass* P, int count, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop,
+                    bool* tail_done = nullptr);
 // Output transforms of several linears (shared B, xmul and output dtype; each
 // its own P[j].SG partial groups) in one launch, bit-identical to one
 // launch_by_rows per linear.
