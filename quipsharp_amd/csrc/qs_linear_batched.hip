@@ -2,7 +2,8 @@
 // chunks, batched decode), the path QuantizedLinear.forward takes for more
 // than two activation rows (quipsharp/checkpoint.py:141-146 ->
 // quipsharp/quantize.py:116-124), on the chunk scheme of qs_chunk_dev.h.
-// Three launches per pass:
+// Two launches per pass (three where the output transform cannot run in the
+// decode-matvec):
 //   bx_kernel  input transform, one work-group per batch row: activation
 //              chunks times S_v, 256-point transforms in registers, the chunk
 //              stage on the matrix cores, fp16 operand (scaled by 2^-e from the
@@ -14,14 +15,18 @@
 //              stream through a 2-tile prefetch ring, the byte-per-value LUTs
 //              feed 16x16x32 MFMAs with all 16 batch columns in use, and the
 //              per-wave partials are reduced across the waves every four row
-//              blocks into the workspace;
+//              blocks into the workspace, as tagged slots when the kernel also
+//              applies the output transform (work-group b < B of each linear,
+//              after its own row blocks, polls row b's slots and runs
+//              by_kernel's row body on them);
 //   by_kernel  output transform, one work-group per batch row: partial sums,
 //              256-point transforms, chunk stage on the matrix cores,
-//              S_u (.) * scales + bias.
+//              S_u (.) * scales + bias (the wide path, and passes whose
+//              decode-matvec cannot take it: bm_tail_eligible).
 // Each kernel takes a table of up to QS_MAX_GROUP linears that read the same
 // x (their work-groups side by side in one grid), so a group of linears is
-// three launches in all; bx_kernel and by_kernel also serve the wide path and
-// are instantiated for 1, 2 or 3 chunks of 256 per wave.
+// two or three launches in all; bx_kernel and by_kernel also serve the wide
+// path and are instantiated for 1, 2 or 3 chunks of 256 per wave.
 #include <hip/hip_ext.h>
 
 #include "qs_forward_dev.h"
