@@ -235,7 +235,8 @@ size_t qs_linear_group_workspace_bytes(int64_t n, int64_t batch, int count, cons
  * call; callers that own several linears of one input use it.
  * At 1-2 rows the group is one launch (n up to 32768; 16384 for fp16 / fp32
  * x); from 3 rows with n <= 12288 each stage of the path (input transforms,
- * decode-matvecs, output transforms) is one launch for the whole group,
+ * decode-matvecs, output transforms; up to 16 rows the decode-matvec launch
+ * also applies the output transforms) is one launch for the whole group,
  * except the wide GEMM (17 rows and more), one launch per job; otherwise one
  * qs_linear_forward per job.  Every output is bit-identical to
  * qs_linear_forward of that job, with one exception: above 128 rows, jobs of
