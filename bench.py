@@ -80,6 +80,10 @@ def parse():
     p.add_argument("--skip-alt", action="store_true", help="do not time the other call pattern")
     p.add_argument("--skip-shapes", action="store_true", help="skip the Llama-3-8B and Qwen2.5-7B stacks")
     p.add_argument("--skip-decode", action="store_true", help="skip the Qwen3-32B-shaped greedy decode")
+    p.add_argument("--stack", choices=sorted(STACK_BATCHES), default=None,
+                   help="measure only this model's quantized-linear stack and print its record (for profiling)")
+    p.add_argument("--stack-batches", default=None,
+                   help="comma-separated batch sizes for --stack (default: the ones the full run reports)")
     p.add_argument("--decode-new", type=int, default=64, help="tokens generated per batch size in the decode")
     p.add_argument("--prefill", type=int, default=512,
                    help="rows of the prefill (wide-batch) step also timed; 0 skips it")
@@ -551,6 +555,10 @@ def kernel_rates(dev):
             "fwht_4096x4096_cols_GBps": round(8 * W.numel() / out["fwht_cols"] / 1e9, 1)}
 
 
+# batch sizes each layer stack is measured at
+STACK_BATCHES = {"llama3_8b": [1, 4, 16], "qwen25_7b": [1], "qwen3_32b": [1, 8]}
+
+
 def stack_batches(key, batches, steps, warmup, dev):
     """ms/step, GB/s and tok/s of a ``MODELS`` stack at each batch size
     (grouped launches, graph-replayed steps)."""
@@ -624,6 +632,11 @@ def main():
     import torch
     dev = torch.device("cuda:0")
     torch.manual_seed(0)
+    if args.stack:
+        batches = ([int(b) for b in args.stack_batches.split(",")] if args.stack_batches
+                   else STACK_BATCHES[args.stack])
+        print(json.dumps({"stack": args.stack, **stack_batches(args.stack, batches, args.steps, args.warmup, dev)}))
+        return
     spec = MODELS["llama2_7b"]
     if args.probe:
         stack = Stack(spec, dev, 2)
@@ -708,9 +721,10 @@ def main():
     del stack
     torch.cuda.empty_cache()
     if not args.skip_shapes:
-        extra["llama3_8b_3bit_stack"] = stack_batches("llama3_8b", [1, 4, 16], args.steps, args.warmup, dev)
-        extra["qwen25_7b_stack"] = stack_batches("qwen25_7b", [1], args.steps, args.warmup, dev)
-        extra["qwen3_32b_stack"] = stack_batches("qwen3_32b", [1, 8], args.steps, args.warmup, dev)
+        extra["llama3_8b_3bit_stack"] = stack_batches("llama3_8b", STACK_BATCHES["llama3_8b"], args.steps,
+                                                      args.warmup, dev)
+        extra["qwen25_7b_stack"] = stack_batches("qwen25_7b", STACK_BATCHES["qwen25_7b"], args.steps, args.warmup, dev)
+        extra["qwen3_32b_stack"] = stack_batches("qwen3_32b", STACK_BATCHES["qwen3_32b"], args.steps, args.warmup, dev)
     if not args.skip_decode:
         from quipsharp_amd.decode import measure_decode
         extra["qwen3_32b_decode"] = measure_decode(new=args.decode_new, device=str(dev))
