@@ -18,7 +18,7 @@ pattern is always reported alongside.
 
 Also reported, each in its own object: batch 16 and a 512-row prefill of the
 same stack; the Llama-3-8B 3-bit RVQ stack (32 layers, 2.6 GB of codes) at
-batch 1 / 4 / 16 and the Qwen2.5-7B stack (36 layers, 2.1 GB) at batch 1,
+batch 1 / 4 / 16 and the Qwen2.5-7B stack (28 layers, 1.6 GB) at batch 1,
 both rotated through more codes than the Infinity Cache holds; the
 Qwen3-32B-shaped greedy decode (64 layers, batch 1 and 8, tok/s, the
 linears' share of a step, per-linear GB/s across all 64 layers); quantize
@@ -53,7 +53,7 @@ MODELS = {
     "llama3_8b": dict(title="Llama-3-8B, 3-bit RVQ (E8P + E8 1-bit)", layers=32, stages=2,
                       lin=[("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
                            ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]),
-    "qwen25_7b": dict(title="Qwen2.5-7B", layers=36, stages=1,
+    "qwen25_7b": dict(title="Qwen2.5-7B", layers=28, stages=1,
                       lin=[("q", 3584, 3584), ("k", 512, 3584), ("v", 512, 3584), ("o", 3584, 3584),
                            ("gate", 18944, 3584), ("up", 18944, 3584), ("down", 3584, 18944)]),
     "qwen3_32b": dict(title="Qwen3-32B", layers=64, stages=1,
