@@ -1,7 +1,7 @@
 """CPU oracle for the QuIP# quantize/dequantize hot path.
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, ``__graft_entry__.smoke()`` and the
-``cpu_baseline`` leg of ``bench.py`` as the checker or the timed CPU baseline.
+``cpu_baseline`` leg of ``bench.py``: results are compared against it, or it is timed as the CPU baseline.
 The product package ``quipsharp_amd`` never imports anything from here.
 
 Two restatements of numbersletter/quipsharp live here:

@@ -2,7 +2,8 @@
  * CPU oracle for the QuIP# quantize/dequantize hot path.
  *
  * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
- * cpu_baseline leg of bench.py may load this library, and only as the checker.
+ * cpu_baseline leg of bench.py may load this library, only to compare results
+ * against it or to time it as the CPU baseline.
  * The product path (quipsharp_amd) never calls it.
  *
  * Every routine restates the scalar fp32 semantics of the reference's torch
