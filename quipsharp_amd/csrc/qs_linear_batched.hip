@@ -284,7 +284,7 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
 #pragma unroll
   for (int k = 0; k < kPrefetch; ++k) {
     const uint32_t off = code_off(jr + k * J.Gr);
-    pre[k] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(J.codes0) + off);
+    pre[k] = ld_nt_u4(reinterpret_cast<const char*>(J.codes0) + off);
     if (HAS2) pre1[k] = *reinterpret_cast<const uint2*>(J.codes1 + off / 2);
   }
   store_luts(lds, tid, lutw);
@@ -334,7 +334,7 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
     }
     {
       const uint32_t off = code_off(rb + kPrefetch * J.Gr);
-      pre[u] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(J.codes0) + off);
+      pre[u] = ld_nt_u4(reinterpret_cast<const char*>(J.codes0) + off);
       if (HAS2) pre1[u] = *reinterpret_cast<const uint2*>(J.codes1 + off / 2);
     }
     // lane holds rows 4q..4q+3 of the tile for batch column r16

@@ -375,7 +375,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
     for (int k = 0; k < kPrefetch; ++k) {
       if (k < k0 || k >= k1) continue;
       const uint32_t off = code_off(own_rb(k));
-      pre[k] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(J.codes0) + off);
+      pre[k] = ld_nt_u4(reinterpret_cast<const char*>(J.codes0) + off);
       if (HAS2) pre1[k] = *reinterpret_cast<const uint2*>(J.codes1 + off / 2);
     }
   };
@@ -563,7 +563,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
       // refill this ring entry (its tile is consumed) with the tile
       // kPrefetch steps ahead
       const uint32_t off = code_off(own_rb(step + kPrefetch));
-      pre[u] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(J.codes0) + off);
+      pre[u] = ld_nt_u4(reinterpret_cast<const char*>(J.codes0) + off);
       if (HAS2) pre1[u] = *reinterpret_cast<const uint2*>(J.codes1 + off / 2);
     }
     // partial of this slice for rows 4q..4q+3, batch column r16, into this

@@ -383,17 +383,12 @@ __global__ __launch_bounds__(kWpThreads) void wp_kernel(WgArgs A) {
     // ---------------- decode waves ----------------
     const int d = w - kWpMfmaWaves;  // weight rows 32 d .. 32 d + 31: code tiles 2 d, 2 d + 1
     const int q = lane >> 4, r16 = lane & 15;
-    // Code words are read once per work-group: nontemporal loads (the
-    // 512-row step measured 0.9 % faster than with ordinary loads; the HBM
-    // bytes fetched stayed the same).
-    typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+    // code words are read once per work-group (nontemporal loads)
     auto words = [&](int ii, int s) -> uint4 {
       int rb = rt * 8 + 2 * d + ii;
       rb = rb < A.RB ? rb : A.RB - 1;  // past the end: the last row block (decoded, never stored)
       s = s < s_last ? s : s_last;
-      const u32x4v v = __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(
-          reinterpret_cast<const char*>(J.codes0) + ((size_t)rb * A.S + s) * 1024 + 16 * lane));
-      return make_uint4(v.x, v.y, v.z, v.w);
+      return ld_nt_u4(reinterpret_cast<const char*>(J.codes0) + ((size_t)rb * A.S + s) * 1024 + 16 * lane);
     };
     // half h of the slice whose code words are c0 / c1 into buffer h
     auto decode_half = [&](auto hc, const uint4& c0, const uint4& c1) {
