@@ -285,7 +285,7 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
   for (int k = 0; k < kPrefetch; ++k) {
     const uint32_t off = code_off(jr + k * J.Gr);
     pre[k] = ld_nt_u4(reinterpret_cast<const char*>(J.codes0) + off);
-    if (HAS2) pre1[k] = *reinterpret_cast<const uint2*>(J.codes1 + off / 2);
+    if (HAS2) pre1[k] = ld_nt_u2(J.codes1 + off / 2);
   }
   store_luts(lds, tid, lutw);
   if (HAS2 && tid < 256) lut1[tid] = t1row;
@@ -335,7 +335,7 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
     {
       const uint32_t off = code_off(rb + kPrefetch * J.Gr);
       pre[u] = ld_nt_u4(reinterpret_cast<const char*>(J.codes0) + off);
-      if (HAS2) pre1[u] = *reinterpret_cast<const uint2*>(J.codes1 + off / 2);
+      if (HAS2) pre1[u] = ld_nt_u2(J.codes1 + off / 2);
     }
     // lane holds rows 4q..4q+3 of the tile for batch column r16
     const int slot = k % kBmSlots;

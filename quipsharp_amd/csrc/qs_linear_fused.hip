@@ -376,7 +376,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
       if (k < k0 || k >= k1) continue;
       const uint32_t off = code_off(own_rb(k));
       pre[k] = ld_nt_u4(reinterpret_cast<const char*>(J.codes0) + off);
-      if (HAS2) pre1[k] = *reinterpret_cast<const uint2*>(J.codes1 + off / 2);
+      if (HAS2) pre1[k] = ld_nt_u2(J.codes1 + off / 2);
     }
   };
   constexpr int kEarlyTiles = 1;
@@ -564,7 +564,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
       // kPrefetch steps ahead
       const uint32_t off = code_off(own_rb(step + kPrefetch));
       pre[u] = ld_nt_u4(reinterpret_cast<const char*>(J.codes0) + off);
-      if (HAS2) pre1[u] = *reinterpret_cast<const uint2*>(J.codes1 + off / 2);
+      if (HAS2) pre1[u] = ld_nt_u2(J.codes1 + off / 2);
     }
     // partial of this slice for rows 4q..4q+3, batch column r16, into this
     // step's slot; the slots are reduced across the waves every kRedSlots

@@ -126,12 +126,9 @@ __global__ __launch_bounds__(kWgThreads) void wg_kernel(WgArgs A) {
     CodeCopy r;
     const int b0 = 16 * tid, b1 = 16 * (tid + kWgThreads);
     const char* c0 = reinterpret_cast<const char*>(A.codes0);
-    r.c0 = *reinterpret_cast<const uint4*>(c0 + tile_of(b0 >> 10, s) * 1024 + (b0 & 1023));
-    r.c1 = kWgCopies > 1 ? *reinterpret_cast<const uint4*>(c0 + tile_of(b1 >> 10, s) * 1024 + (b1 & 1023))
-                         : make_uint4(0, 0, 0, 0);
-    r.c2 = HAS2 && tid < 256
-               ? *reinterpret_cast<const uint4*>(A.codes1 + tile_of(b0 >> 9, s) * 512 + (b0 & 511))
-               : make_uint4(0, 0, 0, 0);
+    r.c0 = ld_nt_u4(c0 + tile_of(b0 >> 10, s) * 1024 + (b0 & 1023));
+    r.c1 = kWgCopies > 1 ? ld_nt_u4(c0 + tile_of(b1 >> 10, s) * 1024 + (b1 & 1023)) : make_uint4(0, 0, 0, 0);
+    r.c2 = HAS2 && tid < 256 ? ld_nt_u4(A.codes1 + tile_of(b0 >> 9, s) * 512 + (b0 & 511)) : make_uint4(0, 0, 0, 0);
     return r;
   };
   auto store_codes = [&](int p, const CodeCopy& r) {
