@@ -1,30 +1,28 @@
 #!/usr/bin/env python3
 """E8P decode-matvec benchmark on one MI355X.
 
-Headline workload: the Llama-2-7B quantized-linear stack -- per decoder layer
-q, k, v, o (4096x4096), gate, up (11008x4096) and down (4096x11008) -- 32
-decoder layers (1.62 GB of E8P codes, about 6x the Infinity Cache), bf16
-activations, batch 1.  E8P 2-bit codes are random uint16 from a seeded
-generator with an fp16 per-layer scale and seeded RHT signs; the 11008-wide
-dims use the Kronecker transform (43 x 256).  A step is one pass through the
-224 linears in dependency order (q/k/v read the layer input, o reads q,
-gate/up read o, down reads gate, the next layer reads down), replayed from a
-HIP graph: W warm-up replays, then K replays timed with HIP events (the
-median replay is reported beside the mean).  By default the linears that
-share an input run as one grouped launch (q/k/v, gate/up:
-qs_linear_forward_group), 4 launches per layer; --per-linear makes the
-headline one qs_linear_forward per linear (7 per layer), and the other
-pattern is always reported alongside.
+Headline workload (the N=1 line's value, roofline and tok/s): the Qwen3-32B
+shape -- 64 decoder layers, each q 8192x5120, k, v 1024x5120, o 5120x8192,
+gate, up 25600x5120, down 5120x25600 (m x n), E8P 2-bit random codes (7.8 GB,
+30x the Infinity Cache), fp16 per-layer scales, seeded RHT signs (the
+non-power-of-two dims take the Kronecker transform: 5120 = 5 x 1024,
+25600 = 25 x 1024), bf16 activations, batch 1.  A step is one pass through
+the 448 quantized linears in dependency order, q/k/v and gate/up each one
+grouped launch (4 launches of linear_fused_kernel per layer), replayed from
+a HIP graph: W warm-up replays, then K replays timed with HIP events; value
+= algorithmic bytes / step time.  tok_per_s is the greedy decode of the same
+model (transformers Qwen3 skeleton, random weights, every decoder linear a
+random-code QuantizedLinear): a 512-token random prompt, then 256 new tokens
+at batch 1 (and 8), one HIP-graph replay per token.
 
-Also reported, each in its own object: batch 16 and a 512-row prefill of the
-same stack; the Llama-3-8B 3-bit RVQ stack (32 layers, 2.6 GB of codes) at
-batch 1 / 4 / 16 and the Qwen2.5-7B stack (28 layers, 1.6 GB) at batch 1,
-both rotated through more codes than the Infinity Cache holds; the
-Qwen3-32B-shaped greedy decode (64 layers, batch 1 and 8, tok/s, the
-linears' share of a step, per-linear GB/s across all 64 layers); quantize
-s/layer for the 4096x4096 E8P 2-bit layer and the Llama-3-8B / Qwen2.5-7B
-layer shapes; and the reference's CPU path timed on this host (torch-CPU
-restatement, oracle/torch_path.py).
+Also reported, each in its own object: the Qwen3-32B stack at batch 8; the
+Llama-2-7B stack (32 layers, 1.62 GB) at batch 1 (grouped and one launch per
+linear), 16 (with matrix-core utilisation) and a 512-row prefill; the
+Llama-3-8B 3-bit RVQ stack (2.6 GB) at batch 1 / 4 / 16; the Qwen2.5-7B stack
+(28 layers, 1.6 GB) at batch 1 with its 152064 x 3584 bf16 lm_head GEMV;
+quantize s/layer for the 4096x4096 E8P 2-bit layer and the Llama-3-8B /
+Qwen2.5-7B layer shapes; and the reference's CPU path timed on this host
+(torch-CPU restatement, oracle/torch_path.py).
 
 Prints one JSON line.
 """
@@ -68,23 +66,30 @@ QWEN3_32B_LINEARS = [(8192, 5120), (1024, 5120), (1024, 5120), (5120, 8192), (25
                      (5120, 25600)]
 
 
+# the distinct layer shapes (m, n) quantized per configuration
+LLAMA3_8B = [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]
+QWEN25_7B = [(3584, 3584), (512, 3584), (18944, 3584), (3584, 18944)]
+QWEN25_VOCAB, QWEN25_HIDDEN = 152064, 3584
+
+
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--layers", type=int, default=32)
+    p.add_argument("--layers", type=int, default=32, help="decoder layers of the Llama-2-7B stack")
     p.add_argument("--skip-quantize", action="store_true")
     p.add_argument("--skip-cpu", action="store_true")
     p.add_argument("--skip-batch16", action="store_true")
     p.add_argument("--skip-alt", action="store_true", help="do not time the other call pattern")
-    p.add_argument("--skip-shapes", action="store_true", help="skip the Llama-3-8B and Qwen2.5-7B stacks")
+    p.add_argument("--skip-shapes", action="store_true",
+                   help="skip the Llama-3-8B and Qwen2.5-7B stacks (and the Qwen2.5-7B lm_head GEMV)")
     p.add_argument("--skip-decode", action="store_true", help="skip the Qwen3-32B-shaped greedy decode")
     p.add_argument("--stack", choices=sorted(STACK_BATCHES), default=None,
                    help="measure only this model's quantized-linear stack and print its record (for profiling)")
     p.add_argument("--stack-batches", default=None,
                    help="comma-separated batch sizes for --stack (default: the ones the full run reports)")
-    p.add_argument("--decode-new", type=int, default=64, help="tokens generated per batch size in the decode")
+    p.add_argument("--decode-new", type=int, default=256, help="tokens generated per batch size in the decode")
     p.add_argument("--prefill", type=int, default=512,
                    help="rows of the prefill (wide-batch) step also timed; 0 skips it")
     p.add_argument("--per-linear", action="store_true",
@@ -118,16 +123,17 @@ def mv_bytes(m, n, B, stages=1):
 
 
 MV_KERNEL = "linear_fused_kernel"  # the dominant kernel of the batch-1 step
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "linear_fused_llama2_7b_b1.md")
+QWEN3_PROFILE = os.path.join(ROOT, "profiles", "linear_fused_qwen3_32b_b1.md")
+LLAMA2_PROFILE = os.path.join(ROOT, "profiles", "linear_fused_llama2_7b_b1.md")
 
 
-def profile_figures():
+def profile_figures(path):
     """HBM bytes per launch (FETCH_SIZE + WRITE_SIZE, calibrated) and the
     kernel-only average duration of the batch-1 kernel, from the committed
     rocprofv3 summary of this bench (labelled as such in the output)."""
     out = {}
     try:
-        with open(TRAFFIC_PROFILE) as f:
+        with open(path) as f:
             for line in f:
                 if line.startswith("traffic_bytes_per_launch:"):
                     out["traffic"] = int(line.split(":")[1])
@@ -472,8 +478,9 @@ def cpu_baseline(dev_layers_sample=1):
         torch_path.linear_forward(x, codes, 0.0135, **kw)
         t_q3 += time.perf_counter() - t0
         del codes
+    q3_bytes = sum(linear_bytes(m, n, 1) for m, n in QWEN3_32B_LINEARS)
     return {
-        "qwen3_32b_decode_s_per_token_extrapolated": 64 * t_q3,
+        "qwen3_32b_decode_s_per_token_extrapolated": 64 * t_q3, "qwen3_32b_GBps": q3_bytes / t_q3 / 1e9,
         "forward_GBps": nbytes / t_fwd / 1e9, "forward_s_per_decoder_layer": t_fwd,
         "quantize_s_per_layer_extrapolated": q_total, "quantize_step_s": {"base": t_base, "tune": t_tune},
         "threads": threads, "host": host_cpu(),
@@ -605,11 +612,49 @@ def launch_rates(runner, steps, warmup):
     return out
 
 
+def make_weights(m, n, heavy, seed):
+    """W (m, n) ~ 0.02 N(0, 1) and calibration rows X (4096, n) ~ N(0, 1) on
+    the CPU from one seeded generator; heavy: 1 % of the entries of W (seeded
+    Bernoulli mask) replaced by 0.02 x Student-t(3)."""
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    W = torch.randn(m, n, generator=g) * 0.02
+    if heavy:
+        mask = torch.rand(m, n, generator=g) < 0.01
+        z = torch.randn(m, n, generator=g)
+        chi2 = (torch.randn(3, m, n, generator=g) ** 2).sum(0)
+        W = torch.where(mask, 0.02 * z / torch.sqrt(chi2 / 3.0), W)
+    X = torch.randn(4096, n, generator=g)
+    return W, X
+
+
+def quantize_layer(m, n, bits, heavy, seed, tune_iters, dev, codebooks):
+    """quantize_linear of one synthetic layer on the GPU (H = X^T X / 4096):
+    (layer, seconds (synchronized), relative proxy loss tr(E H E^T) / tr(W H W^T))."""
+    import torch
+    from quipsharp_amd.quantize import quantize_linear
+    W, X = make_weights(m, n, heavy, seed)
+    Wd, Xd = W.to(dev), X.to(dev)
+    H = Xd.T @ Xd / 4096
+    del Xd
+    cb, scale_in = codebooks[bits]
+    torch.manual_seed(seed)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    layer, what_q = quantize_linear(Wd, H, cb, g=8, damping=1e-2, codebook_scale=scale_in, tune_iters=tune_iters)
+    torch.cuda.synchronize()
+    t_q = time.perf_counter() - t0
+    E = layer.signs.reconstruct_weight(what_q) - Wd
+    proxy = (torch.trace(E.double() @ H.double() @ E.T.double()) /
+             torch.trace(Wd.double() @ H.double() @ Wd.T.double())).item()
+    del H, Wd, what_q, E
+    return layer, t_q, proxy
+
+
 def shape_quantize(dev, tune_iters=10):
     """Quantize s/layer at the Llama-3-8B (3-bit RVQ) and Qwen2.5-7B (2-bit,
-    1 % Student-t(3) outliers) layer shapes (quipsharp_amd.shapes_bench)."""
+    1 % Student-t(3) outliers) layer shapes."""
     from quipsharp_amd.checkpoint import build_codebook
-    from quipsharp_amd.shapes_bench import LLAMA3_8B, QWEN25_7B, quantize_layer
     out = {}
     for key, shapes, bits, heavy, seed in (("llama3_8b_3bit", LLAMA3_8B, "3bit", False, 11),
                                           ("qwen25_7b_2bit_heavy_tailed", QWEN25_7B, "2bit", True, 21)):
@@ -620,6 +665,101 @@ def shape_quantize(dev, tune_iters=10):
             rows.append({"m": m, "n": n, "quantize_s": round(t_q, 3), "relative_proxy_loss": round(proxy, 5)})
             log(f"quantize {key} {m}x{n}: {t_q:.3f} s")
         out[key] = rows
+    return out
+
+
+def lm_head_gemv(dev, reps=20):
+    """The Qwen2.5-7B lm_head (152064 x 3584), left in bf16 as the reference
+    leaves it (only decoder linears are quantized): one library GEMV through
+    torch at batch 1, us and GB/s (weights + activations)."""
+    import torch
+    W = (torch.randn(QWEN25_VOCAB, QWEN25_HIDDEN, device=dev) * 0.02).bfloat16()
+    x = torch.randn(1, QWEN25_HIDDEN, device=dev).bfloat16()
+    y = x @ W.T
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        torch.matmul(x, W.T, out=y)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    nbytes = W.numel() * 2 + 2 * (QWEN25_HIDDEN + QWEN25_VOCAB)
+    del W
+    torch.cuda.empty_cache()
+    return {"m": QWEN25_VOCAB, "n": QWEN25_HIDDEN, "dtype": "bf16", "batch": 1, "us": round(us, 2),
+            "GBps": round(nbytes / us / 1e3, 1), "path": "torch.matmul (library GEMV), not quantized"}
+
+
+def llama2_7b_records(dev, args):
+    """The Llama-2-7B stack: batch 1 (grouped and one launch per linear,
+    per-launch rates), 16 rows (with matrix-core utilisation) and a prefill."""
+    import torch
+    spec = MODELS["llama2_7b"]
+    t_setup = time.perf_counter()
+    stack = Stack(spec, dev, args.layers)
+    log(f"llama2_7b stack: {args.layers} layers, {stack.code_bytes() / 1e9:.2f} GB of codes, "
+        f"setup {time.perf_counter() - t_setup:.1f}s")
+    out = {"workload": "Llama-2-7B quantized-linear stack (q,k,v,o 4096x4096; gate,up 11008x4096; down "
+                       "4096x11008) x %d decoder layers, E8P 2-bit random codes" % args.layers,
+           "code_bytes": stack.code_bytes()}
+    r1 = Runner(stack, 1, grouped=not args.per_linear)
+    t1 = time_graph(r1, args.steps, args.warmup)
+    ms = t1["mean_ms"]
+    launches = r1.launches_per_step()
+    mv_ms = ms / launches
+    achieved = r1.mv_bytes_per_step() / launches / (mv_ms * 1e-3) / 1e9
+    prof = profile_figures(LLAMA2_PROFILE)
+    out["batch1"] = {"ms_per_step": round(ms, 4), "median_ms_per_step": round(t1["median_ms"], 4),
+                     "GBps": round(r1.bytes_per_step() / ms / 1e6, 1),
+                     "linear_stack_steps_per_s": round(1e3 / ms, 1), "launches_per_step": launches,
+                     "call_pattern": "grouped" if r1.grouped else "per-linear",
+                     "roofline": {"kernel": MV_KERNEL, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                                  "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                                  "avg_launch_us": round(mv_ms * 1e3, 3),
+                                  "bytes_per_launch": int(r1.mv_bytes_per_step() / launches),
+                                  "profile_kernel_avg_us": prof.get("kernel_avg_us"),
+                                  "traffic": prof.get("traffic") if args.layers == 32 and r1.grouped else None}}
+    log(f"llama2_7b batch 1: {ms:.3f} ms/step, {out['batch1']['GBps']} GB/s")
+    if r1.grouped:
+        out["batch1"]["launches"] = launch_rates(r1, args.steps, args.warmup)
+    if not args.skip_alt:
+        r_alt = Runner(stack, 1, grouped=args.per_linear)
+        ta = time_graph(r_alt, args.steps, args.warmup)
+        out["batch1_" + ("grouped" if r_alt.grouped else "per_linear")] = {
+            "ms_per_step": round(ta["mean_ms"], 4), "median_ms_per_step": round(ta["median_ms"], 4),
+            "GBps": round(r1.bytes_per_step() / ta["mean_ms"] / 1e6, 1),
+            "launches_per_step": r_alt.launches_per_step()}
+        del r_alt
+    if not args.skip_batch16:
+        r16 = Runner(stack, 16, grouped=not args.per_linear)
+        t16 = time_graph(r16, args.steps, args.warmup)
+        ms16 = t16["mean_ms"]
+        flops = 2 * 16 * args.layers * sum(m * n for _, m, n in LLAMA2_7B)
+        tf = flops / ms16 / 1e9
+        out["batch16"] = {"ms_per_step": round(ms16, 4), "median_ms_per_step": round(t16["median_ms"], 4),
+                          "GBps": round(r16.bytes_per_step() / ms16 / 1e6, 1),
+                          "tok_per_s": round(16 * 1e3 / ms16, 1), "TFLOPs": round(tf, 2),
+                          "mfma_frac_fp16_dense": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
+                          "call_pattern": "grouped" if r16.grouped else "per-linear",
+                          "launches_per_step": r16.launches_per_step()}
+        log(f"llama2_7b batch 16: {ms16:.3f} ms/step")
+        del r16
+    if args.prefill > 0:
+        P = args.prefill
+        rp = Runner(stack, P, grouped=not args.per_linear)
+        msp = time_eager(rp, max(args.steps // 10, 3), 2)
+        flops = 2 * P * args.layers * sum(m * n for _, m, n in LLAMA2_7B)
+        out["prefill"] = {"rows": P, "ms_per_step": round(msp, 3), "tok_per_s": round(P * 1e3 / msp, 1),
+                          "TFLOPs": round(flops / msp / 1e9, 1),
+                          "mfma_frac_fp16_dense": round(flops / msp / 1e9 / MFMA_F16_PEAK_TFLOPS, 4),
+                          "call_pattern": "grouped" if rp.grouped else "per-linear",
+                          "path": "wp_kernel: 4 waves decode E8P codes (with their +-1/4 shifts) into fp16 "
+                                  "32x32x16 MFMA fragments in LDS, 4 waves multiply them (fp32 accumulate)"}
+        log(f"llama2_7b prefill {P} rows: {msp:.3f} ms/step")
+        del rp
+    del stack
+    torch.cuda.empty_cache()
     return out
 
 
@@ -637,9 +777,8 @@ def main():
                    else STACK_BATCHES[args.stack])
         print(json.dumps({"stack": args.stack, **stack_batches(args.stack, batches, args.steps, args.warmup, dev)}))
         return
-    spec = MODELS["llama2_7b"]
     if args.probe:
-        stack = Stack(spec, dev, 2)
+        stack = Stack(MODELS["llama2_7b"], dev, 2)
         r1 = Runner(stack, 1)
         r1.step()
         torch.cuda.synchronize()
@@ -658,11 +797,13 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"probe": "done", "linears": r1.launches_per_step(), "copy_bytes": a.numel() * 4}))
         return
+    # headline: the Qwen3-32B stack at batch 1 (and 8)
+    spec = MODELS["qwen3_32b"]
     t_setup = time.perf_counter()
-    stack = Stack(spec, dev, args.layers)
-    log(f"stack: {args.layers} layers, {stack.code_bytes() / 1e9:.2f} GB of codes, "
+    stack = Stack(spec, dev)
+    log(f"qwen3_32b stack: {len(stack.layers)} layers, {stack.code_bytes() / 1e9:.2f} GB of codes, "
         f"setup {time.perf_counter() - t_setup:.1f}s")
-    r1 = Runner(stack, 1, grouped=not args.per_linear)
+    r1 = Runner(stack, 1)
     t1 = time_graph(r1, args.steps, args.warmup)
     ms = t1["mean_ms"]
     bps = r1.bytes_per_step()
@@ -674,63 +815,39 @@ def main():
     mv_ms = ms / launches
     mv_avg_bytes = r1.mv_bytes_per_step() / launches
     achieved = mv_avg_bytes / (mv_ms * 1e-3) / 1e9
-    log(f"batch 1 ({'grouped' if r1.grouped else 'per-linear'}): {ms:.3f} ms/step (median {t1['median_ms']:.3f}), "
-        f"{value:.1f} GB/s, {mv_ms * 1e3:.2f} us per launch -> {achieved:.1f} GB/s")
-    extra = {}
-    if r1.grouped:
-        extra["launches_b1"] = launch_rates(r1, args.steps, args.warmup)
-        log("launches: " + "; ".join(f"{l['launch']} {l['us_per_launch']} us {l['GBps']} GB/s"
-                                     for l in extra["launches_b1"]))
-    if not args.skip_alt:
-        # the other call pattern, for comparison
-        r_alt = Runner(stack, 1, grouped=args.per_linear)
-        ta = time_graph(r_alt, args.steps, args.warmup)
-        ms_alt = ta["mean_ms"]
-        extra["grouped" if r_alt.grouped else "per_linear"] = {
-            "ms_per_step": round(ms_alt, 4), "median_ms_per_step": round(ta["median_ms"], 4),
-            "GBps": round(bps / ms_alt / 1e6, 1), "tok_per_s": round(1e3 / ms_alt, 1),
-            "launches_per_step": r_alt.launches_per_step(),
-            "avg_launch_us": round(ms_alt * 1e3 / r_alt.launches_per_step(), 3)}
-        log(f"batch 1 ({'grouped' if r_alt.grouped else 'per-linear'}): {ms_alt:.3f} ms/step")
-        del r_alt
-    if not args.skip_batch16:
-        r16 = Runner(stack, 16, grouped=not args.per_linear)
-        t16 = time_graph(r16, args.steps, args.warmup)
-        ms16 = t16["mean_ms"]
-        flops = 2 * 16 * args.layers * sum(m * n for _, m, n in LLAMA2_7B)
-        extra["batch16"] = {"ms_per_step": round(ms16, 4), "median_ms_per_step": round(t16["median_ms"], 4),
-                            "GBps": round(r16.bytes_per_step() / ms16 / 1e6, 1),
-                            "tok_per_s": round(16 * 1e3 / ms16, 1), "TFLOPs": round(flops / ms16 / 1e9, 2),
-                            "call_pattern": "grouped" if r16.grouped else "per-linear",
-                            "launch_groups_per_step": r16.launches_per_step()}
-        log(f"batch 16 ({'grouped' if r16.grouped else 'per-linear'}): {ms16:.3f} ms/step")
-        del r16
-    if args.prefill > 0:
-        P = args.prefill
-        rp = Runner(stack, P, grouped=not args.per_linear)
-        msp = time_eager(rp, max(args.steps // 10, 3), 2)
-        flops = 2 * P * args.layers * sum(m * n for _, m, n in LLAMA2_7B)
-        extra["prefill"] = {"rows": P, "ms_per_step": round(msp, 3), "tok_per_s": round(P * 1e3 / msp, 1),
-                            "TFLOPs": round(flops / msp / 1e9, 1),
-                            "mfma_frac_fp16_dense": round(flops / msp / 1e9 / MFMA_F16_PEAK_TFLOPS, 4),
-                            "call_pattern": "grouped" if rp.grouped else "per-linear",
-                            "path": "wp_kernel: 4 waves decode E8P codes (with their +-1/4 shifts) into fp16 "
-                                    "32x32x16 MFMA fragments in LDS, 4 waves multiply them (fp32 accumulate)"}
-        log(f"prefill {P} rows: {msp:.3f} ms/step, {flops / msp / 1e9:.1f} TFLOP/s")
-        del rp
+    log(f"qwen3_32b batch 1: {ms:.3f} ms/step (median {t1['median_ms']:.3f}), {value:.1f} GB/s, "
+        f"{mv_ms * 1e3:.2f} us per launch -> {achieved:.1f} GB/s")
+    extra = {"qwen3_32b_stack": {"workload": spec["title"] + " quantized-linear stack, 64 decoder layers",
+                                 "batch1_launches": launch_rates(r1, args.steps, args.warmup)}}
+    log("launches: " + "; ".join(f"{l['launch']} {l['us_per_launch']} us {l['GBps']} GB/s"
+                                 for l in extra["qwen3_32b_stack"]["batch1_launches"]))
+    del r1
+    for B in STACK_BATCHES["qwen3_32b"][1:]:
+        rb = Runner(stack, B)
+        tb = time_graph(rb, args.steps, args.warmup)
+        extra["qwen3_32b_stack"][f"batch{B}"] = {
+            "ms_per_step": round(tb["mean_ms"], 4), "median_ms_per_step": round(tb["median_ms"], 4),
+            "GBps": round(rb.bytes_per_step() / tb["mean_ms"] / 1e6, 1), "launches_per_step": rb.launches_per_step()}
+        log(f"qwen3_32b batch {B}: {tb['mean_ms']:.3f} ms/step")
+        del rb
+    code_bytes = stack.code_bytes()
     del stack
     torch.cuda.empty_cache()
+    decode = None
+    if not args.skip_decode:
+        from quipsharp_amd.decode import measure_decode
+        decode = measure_decode(new=args.decode_new, device=str(dev))
+        extra["qwen3_32b_decode"] = decode
+        for run in decode["runs"]:
+            log(f"qwen3-32b decode batch {run['batch']}: {run['tok_per_s']} tok/s, {run['ms_per_step']} ms/step "
+                f"({run['linears_ms_per_step']} ms in the quantized linears)")
+    extra["llama2_7b_stack"] = llama2_7b_records(dev, args)
     if not args.skip_shapes:
         extra["llama3_8b_3bit_stack"] = stack_batches("llama3_8b", STACK_BATCHES["llama3_8b"], args.steps,
                                                       args.warmup, dev)
         extra["qwen25_7b_stack"] = stack_batches("qwen25_7b", STACK_BATCHES["qwen25_7b"], args.steps, args.warmup, dev)
-        extra["qwen3_32b_stack"] = stack_batches("qwen3_32b", STACK_BATCHES["qwen3_32b"], args.steps, args.warmup, dev)
-    if not args.skip_decode:
-        from quipsharp_amd.decode import measure_decode
-        extra["qwen3_32b_decode"] = measure_decode(new=args.decode_new, device=str(dev))
-        for run in extra["qwen3_32b_decode"]["runs"]:
-            log(f"qwen3-32b decode batch {run['batch']}: {run['tok_per_s']} tok/s, {run['ms_per_step']} ms/step "
-                f"({run['linears_ms_per_step']} ms in the quantized linears)")
+        extra["qwen25_7b_lm_head_bf16"] = lm_head_gemv(dev)
+        log(f"qwen2.5-7b lm_head (bf16 GEMV): {extra['qwen25_7b_lm_head_bf16']}")
     if not args.skip_quantize:
         extra["quantize_4096x4096_e8p_2bit"] = gpu_quantize(dev)
         log(f"quantize: {extra['quantize_4096x4096_e8p_2bit']}")
@@ -743,34 +860,40 @@ def main():
     if not args.skip_cpu:
         log("timing the reference CPU path ...")
         c = cpu_baseline()
-        cpu = {"value": round(c["forward_GBps"], 3), "unit": "GB/s", "cores": c["threads"], "kind": "port",
-               "host": c["host"],
-               "sample": "reference forward (dense dequantize loop + fp32 matmul, RHT / RFFT transforms) of one "
-                         "Llama-2-7B decoder layer's 7 linears at batch 1, torch-CPU restatement; quantize "
-                         "4096x4096 E8P 2-bit extrapolated from 5 base-pass and 3 refinement steps",
-               "forward_s_per_decoder_layer": round(c["forward_s_per_decoder_layer"], 3),
-               "qwen3_32b_decode_s_per_token": round(c["qwen3_32b_decode_s_per_token_extrapolated"], 1),
-               "qwen3_32b_sample": "one decoder layer's 7 linears at batch 1 timed, x 64 layers",
-               "quantize_s_per_layer": round(c["quantize_s_per_layer_extrapolated"], 1)}
+        cpu = {"value": round(c["qwen3_32b_decode_s_per_token_extrapolated"], 1), "unit": "s/token",
+               "cores": c["threads"], "kind": "port", "host": c["host"],
+               "sample": "reference forward (dense dequantize loop + fp32 matmul; RHT where both dims are powers "
+                         "of two, RFFT otherwise, as the reference chooses) of one Qwen3-32B decoder layer's 7 "
+                         "linears at batch 1, torch-CPU restatement, x 64 layers = s per token of the decoder "
+                         "linears",
+               "qwen3_32b_GBps": round(c["qwen3_32b_GBps"], 3),
+               "llama2_7b_forward_GBps": round(c["forward_GBps"], 3),
+               "llama2_7b_forward_s_per_decoder_layer": round(c["forward_s_per_decoder_layer"], 3),
+               "quantize_s_per_layer": round(c["quantize_s_per_layer_extrapolated"], 1),
+               "quantize_sample": "4096x4096 E8P 2-bit, extrapolated from 5 base-pass and 3 refinement steps"}
         if "quantize_4096x4096_e8p_2bit" in extra:
             extra["quantize_speedup_vs_cpu"] = round(
                 c["quantize_s_per_layer_extrapolated"] / extra["quantize_4096x4096_e8p_2bit"]["quantize_s_per_layer"], 1)
-    prof = profile_figures()
+    prof = profile_figures(QWEN3_PROFILE)
+    runs = {r["batch"]: r for r in decode["runs"]} if decode else {}
     line = {
         "metric": "E8P decode-matvec HBM GB/s (% peak) + batch-1 tok/s; quantize s/layer",
         "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms, 4), "median_ms_per_step": round(t1["median_ms"], 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "e8p-2bit codes, fp16 x fp16 -> fp32 accumulate (bf16 in/out)", "data": "synthetic",
-        "config": {"workload": "Llama-2-7B quantized-linear stack (q,k,v,o 4096x4096; gate,up 11008x4096; "
-                               "down 4096x11008) x %d decoder layers, E8P 2-bit random codes, batch 1" % args.layers,
-                   "global_batch": 1, "layers": args.layers, "linears_per_step": 7 * args.layers,
-                   "launches_per_step": launches,
-                   "call_pattern": "grouped (q/k/v and gate/up share a launch)" if r1.grouped else
-                                   "one qs_linear_forward per linear",
-                   "code_bytes": int(sum(2 * m * n // 8 for _, m, n in LLAMA2_7B) * args.layers),
+        "config": {"workload": "Qwen3-32B quantized-linear stack: 64 decoder layers x (q 8192x5120; k, v "
+                               "1024x5120; o 5120x8192; gate, up 25600x5120; down 5120x25600), E8P 2-bit random "
+                               "codes, batch 1",
+                   "global_batch": 1, "layers": 64, "linears_per_step": 7 * 64, "launches_per_step": launches,
+                   "call_pattern": "grouped (q/k/v and gate/up share a launch)", "code_bytes": code_bytes,
                    "parallelism": "none (1 GPU)"},
-        "tok_per_s": round(1e3 / ms, 1), "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "tok_per_s": runs[1]["tok_per_s"] if 1 in runs else None,
+        "tok_per_s_source": "greedy decode of the Qwen3-32B-shaped model (512-token prompt, %d new tokens), "
+                            "batch 1, one HIP-graph replay per token" % args.decode_new,
+        "tok_per_s_batch8": runs[8]["tok_per_s"] if 8 in runs else None,
+        "linear_stack_steps_per_s": round(1e3 / ms, 1),
+        "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "kernel": MV_KERNEL, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "avg_launch_us": round(mv_ms * 1e3, 3), "bytes_per_launch": int(mv_avg_bytes),
@@ -779,9 +902,9 @@ def main():
                      "profile_kernel_avg_us": prof.get("kernel_avg_us"),
                      "measured_copy_GBps": copy_peak,
                      "frac_of_measured_copy": round(achieved / copy_peak, 4) if copy_peak else None,
-                     "traffic": prof.get("traffic") if args.layers == 32 and r1.grouped else None,
+                     "traffic": prof.get("traffic"),
                      "traffic_source": "committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary "
-                                       "(profiles/linear_fused_llama2_7b_b1.md), not measured in this run"},
+                                       "(profiles/linear_fused_qwen3_32b_b1.md), not measured in this run"},
         "cpu_baseline": cpu,
     }
     line.update(extra)

@@ -258,6 +258,48 @@ int qs_linear_forward_group(const void *x, int x_dtype, int64_t ldx, int64_t bat
  * back to back on the GPU while the host is still submitting. */
 int qs_busy_wait(int64_t nanoseconds, qs_stream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * Decode-step kernels of the greedy-decode harness (a Qwen3-style decoder
+ * around QuantizedLinear layers, one new token per batch row).  No
+ * counterpart in the reference, whose evaluation runs transformers' modules
+ * around QuantizedLinear.forward (scripts/eval_ppl.py:41-65); these do the
+ * same arithmetic as transformers' Qwen3RMSNorm, apply_rotary_pos_emb, the
+ * attention over the cache and act_fn(gate) * up, in a few launches per
+ * layer.  Tensors are bf16 (uint16 bits) unless stated; `pos` is a device
+ * int64, the position of the new token (the same for every row).
+ * --------------------------------------------------------------------------- */
+
+/* h_out = h + delta (bf16 add; skipped when delta is NULL, then h_out is
+ * unused; h_out may alias h), x = weight * bf16(h' * rsqrt(mean(h'^2) + eps))
+ * for each of `rows` rows of `dim` (a multiple of 8) with row stride ld;
+ * 16-byte aligned buffers. */
+int qs_dec_rmsnorm(const void *h, const void *delta, void *h_out, const void *weight, void *x, int64_t rows,
+                   int64_t dim, int64_t ld, float eps, qs_stream_t stream);
+
+/* Per row: q heads [rows][nh][128] get q_norm (RMSNorm over the head dim)
+ * then the rotary embedding cos_table / sin_table [max_len][128] at `pos`,
+ * into q_out [rows][nh][128]; k heads [rows][nkv][128] get k_norm and the
+ * rotary embedding, into k_cache [rows][nkv][max_len][128] at `pos`; v heads
+ * are copied into v_cache at `pos`.  head_dim 128. */
+int qs_dec_qk_norm_rope(const void *q, const void *k, const void *v, const void *q_norm_w, const void *k_norm_w,
+                        const void *cos_table, const void *sin_table, const int64_t *pos, void *q_out,
+                        void *k_cache, void *v_cache, int64_t rows, int nh, int nkv, int head_dim, int64_t max_len,
+                        float eps, qs_stream_t stream);
+
+/* Attention of the new token over cache positions 0 .. pos: out[row][h * 128
+ * + d] (row stride ldo) = softmax(scale q_h . k) . v over the kv head h / (nh /
+ * nkv) (at most 16 query heads per kv head), in splits of 64 positions (fp32
+ * scores and softmax, bf16 probabilities, fp32 accumulate) combined in a
+ * second launch.  workspace: qs_dec_attention_workspace_bytes bytes. */
+int64_t qs_dec_attention_workspace_bytes(int64_t rows, int nkv, int64_t max_len);
+int qs_dec_attention(const void *q, const void *k_cache, const void *v_cache, const int64_t *pos, void *out,
+                     int64_t ldo, void *workspace, int64_t workspace_bytes, int64_t rows, int nh, int nkv,
+                     int head_dim, int64_t max_len, float scale, qs_stream_t stream);
+
+/* out = bf16(silu(gate)) * up (each op rounded to bf16), rows x m (even). */
+int qs_dec_silu_mul(const void *gate, const void *up, void *out, int64_t rows, int64_t m, int64_t ldg, int64_t ldu,
+                    int64_t ldo, qs_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

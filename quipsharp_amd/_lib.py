@@ -65,6 +65,12 @@ _SIGNATURES = {
     "qs_linear_forward_group": ([_vp, _int, _i64, _i64, _i64, _int, _vp, _int, ctypes.POINTER(LinearJob), _int,
                                  _vp, ctypes.c_size_t, _vp, _vp, _vp], _int),
     "qs_busy_wait": ([_i64, _vp], _int),
+    "qs_dec_rmsnorm": ([_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _f32, _vp], _int),
+    "qs_dec_qk_norm_rope": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _int, _int, _int, _i64,
+                             _f32, _vp], _int),
+    "qs_dec_attention_workspace_bytes": ([_i64, _int, _i64], _i64),
+    "qs_dec_attention": ([_vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _int, _int, _int, _i64, _f32, _vp], _int),
+    "qs_dec_silu_mul": ([_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp], _int),
 }
 
 EXPORTED = tuple(_SIGNATURES)

@@ -1,0 +1,380 @@
+// Decode-step kernels of the greedy-decode harness: everything a Qwen3-style
+// decoder layer does around its quantized linears for one new token per
+// batch row, so that a step is a short chain of launches (per layer: norm,
+// q/k/v, q/k norm + rotary + cache write, attention, combine, o, norm,
+// gate/up, SiLU * up, down) instead of the ~50 small framework kernels of
+// transformers' modules.  The arithmetic follows transformers'
+// Qwen3RMSNorm, apply_rotary_pos_emb and SiLU MLP on bf16 tensors (each
+// framework op rounds to bf16; so do these kernels, at the same points);
+// attention keeps the scores and the softmax in fp32 with bf16 probabilities
+// into the value product (fp32 accumulate), over the filled cache prefix only.
+//
+// All row counts, head counts and lengths are checked on the host; the
+// position is read on the device (one int64 shared by every batch row), so a
+// captured step replays for any position below the cache length.
+#include "qs_chunk_dev.h"
+
+namespace qs {
+namespace {
+
+typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+__device__ __forceinline__ float rbf(float f) { return bf(f32_to_bf16(f)); }  // round through bf16
+
+// Sum over a 256-thread work-group (4 waves); red holds 4 floats.
+__device__ __forceinline__ float block_sum256(float v, float* red, LaneX lx) {
+  v += lane_xor<32>(v, lx);
+  v += lane_xor<16>(v, lx);
+  v += lane_xor<8>(v, lx);
+  v += lane_xor<4>(v, lx);
+  v += lane_xor<2>(v, lx);
+  v += lane_xor<1>(v, lx);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  const float s = (red[0] + red[1]) + (red[2] + red[3]);
+  __syncthreads();
+  return s;
+}
+
+// h_out = h + delta (bf16 add; h_out may be h); x = weight * bf16(h_out *
+// rsqrt(mean(h_out^2) + eps)) (transformers' Qwen3RMSNorm.forward).  One
+// work-group per row, 8 elements per thread and step.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* h, const uint16_t* delta, uint16_t* h_out,
+                                                      const uint16_t* weight, uint16_t* x, int dim, int64_t ld,
+                                                      float eps) {
+  __shared__ float red[4];
+  const LaneX lx = lane_x_init();
+  const int64_t r = blockIdx.x;
+  const uint16_t* hr = h + r * ld;
+  float ss = 0.0f;
+  for (int i0 = 8 * threadIdx.x; i0 < dim; i0 += 8 * 256) {
+    uint4 a = *reinterpret_cast<const uint4*>(hr + i0);
+    if (delta) {
+      const uint4 d = *reinterpret_cast<const uint4*>(delta + r * ld + i0);
+      const uint32_t* pa = &a.x;
+      const uint32_t* pd = &d.x;
+      uint32_t o[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint16_t lo = f32_to_bf16(bf((uint16_t)(pa[k] & 0xFFFF)) + bf((uint16_t)(pd[k] & 0xFFFF)));
+        const uint16_t hi = f32_to_bf16(bf((uint16_t)(pa[k] >> 16)) + bf((uint16_t)(pd[k] >> 16)));
+        o[k] = (uint32_t)lo | ((uint32_t)hi << 16);
+      }
+      a = make_uint4(o[0], o[1], o[2], o[3]);
+      *reinterpret_cast<uint4*>(h_out + r * ld + i0) = a;
+    }
+    const uint32_t* pa = &a.x;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float lo = bf((uint16_t)(pa[k] & 0xFFFF)), hi = bf((uint16_t)(pa[k] >> 16));
+      ss += lo * lo;
+      ss += hi * hi;
+    }
+  }
+  const float rs = 1.0f / sqrtf(block_sum256(ss, red, lx) / (float)dim + eps);
+  const uint16_t* src = delta ? h_out + r * ld : hr;
+  for (int i0 = 8 * threadIdx.x; i0 < dim; i0 += 8 * 256) {
+    const uint4 a = *reinterpret_cast<const uint4*>(src + i0);
+    const uint4 wv = *reinterpret_cast<const uint4*>(weight + i0);
+    const uint32_t* pa = &a.x;
+    const uint32_t* pw = &wv.x;
+    uint32_t o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float lo = rbf(bf((uint16_t)(pa[k] & 0xFFFF)) * rs), hi = rbf(bf((uint16_t)(pa[k] >> 16)) * rs);
+      o[k] = (uint32_t)f32_to_bf16(bf((uint16_t)(pw[k] & 0xFFFF)) * lo) |
+             ((uint32_t)f32_to_bf16(bf((uint16_t)(pw[k] >> 16)) * hi) << 16);
+    }
+    *reinterpret_cast<uint4*>(x + r * ld + i0) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+// One wave per head of one row: q heads get q_norm and the rotary embedding
+// (into q_out), k heads k_norm and the rotary embedding (into the key cache
+// at the position), v heads go to the value cache unchanged.  Head dim 128:
+// lane l holds dims l and l + 64 (the pair rotate_half mixes).
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                                           const uint16_t* qw, const uint16_t* kw,
+                                                           const uint16_t* cos_t, const uint16_t* sin_t,
+                                                           const int64_t* pos_p, uint16_t* q_out, uint16_t* kc,
+                                                           uint16_t* vc, int nh, int nkv, int64_t max_len,
+                                                           float eps) {
+  const LaneX lx = lane_x_init();
+  const int b = blockIdx.x;
+  const int hh = blockIdx.y * 4 + (threadIdx.x >> 6);
+  const int l = threadIdx.x & 63;
+  if (hh >= nh + 2 * nkv) return;
+  const int64_t pos = *pos_p;
+  if (hh >= nh + nkv) {  // value head: copy into the cache
+    const int g = hh - nh - nkv;
+    const uint16_t* src = v + ((int64_t)b * nkv + g) * 128;
+    uint16_t* dst = vc + (((int64_t)b * nkv + g) * max_len + pos) * 128;
+    dst[l] = src[l];
+    dst[l + 64] = src[l + 64];
+    return;
+  }
+  const bool isq = hh < nh;
+  const int g = isq ? hh : hh - nh;
+  const uint16_t* src = isq ? q + ((int64_t)b * nh + g) * 128 : k + ((int64_t)b * nkv + g) * 128;
+  const uint16_t* w = isq ? qw : kw;
+  const float x0 = bf(src[l]), x1 = bf(src[l + 64]);
+  float ss = x0 * x0 + x1 * x1;
+  ss += lane_xor<32>(ss, lx);
+  ss += lane_xor<16>(ss, lx);
+  ss += lane_xor<8>(ss, lx);
+  ss += lane_xor<4>(ss, lx);
+  ss += lane_xor<2>(ss, lx);
+  ss += lane_xor<1>(ss, lx);
+  const float rs = 1.0f / sqrtf(ss / 128.0f + eps);
+  const float y0 = rbf(bf(w[l]) * rbf(x0 * rs)), y1 = rbf(bf(w[l + 64]) * rbf(x1 * rs));
+  const float c0 = bf(cos_t[pos * 128 + l]), c1 = bf(cos_t[pos * 128 + l + 64]);
+  const float s0 = bf(sin_t[pos * 128 + l]), s1 = bf(sin_t[pos * 128 + l + 64]);
+  // q * cos + rotate_half(q) * sin, rotate_half(q) = (-q[64:], q[:64])
+  const uint16_t o0 = f32_to_bf16(rbf(y0 * c0) + (-rbf(y1 * s0)));
+  const uint16_t o1 = f32_to_bf16(rbf(y1 * c1) + rbf(y0 * s1));
+  uint16_t* dst = isq ? q_out + ((int64_t)b * nh + g) * 128 : kc + (((int64_t)b * nkv + g) * max_len + pos) * 128;
+  dst[l] = o0;
+  dst[l + 64] = o1;
+}
+
+constexpr int kSplit = 64;     // cache positions per attention work-group
+constexpr int kQStride = 136;  // bf16 per row of the staged queries / probabilities (rows 16 banks apart)
+constexpr int kPartFloats = 16 * 2 + 16 * 128;  // per (row, kv head, split): max, sum, unnormalised output
+
+// One work-group (4 waves) per (split of 64 cache positions, kv head, row):
+// scores of the G <= 16 query heads that share the kv head against the
+// split's keys on the matrix cores (bf16 16x16x32, rows past G zero), masked
+// past the filled length, split-local softmax in fp32, then the probabilities
+// (bf16) times the split's values on the matrix cores.  Writes the split's
+// per-head max, sum and unnormalised output for attn_combine_kernel.
+__global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
+                                                         const int64_t* pos_p, float* part, int nh, int nkv,
+                                                         int64_t max_len, int nsplit, float scale) {
+  __shared__ __attribute__((aligned(16))) uint16_t Qs[16 * kQStride];
+  __shared__ __attribute__((aligned(16))) uint16_t Ps[16 * kQStride];
+  __shared__ float red[2][4][16];
+  const int s = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+  const int64_t len = *pos_p + 1;
+  const int64_t p0 = (int64_t)s * kSplit;
+  if (p0 >= len) return;  // the combine reads only the filled splits
+  const int G = nh / nkv;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, qd = lane >> 4, r16 = lane & 15;
+  const LaneX lx = lane_x_init();
+  {
+    // queries of heads g G .. g G + G - 1: 16 rows x 128, 8 bf16 per thread
+    const int row = tid >> 4, c8 = (tid & 15) * 8;
+    uint4 val = make_uint4(0, 0, 0, 0);
+    if (row < G) val = *reinterpret_cast<const uint4*>(q + (((int64_t)b * nh + g * G + row) * 128 + c8));
+    *reinterpret_cast<uint4*>(Qs + row * kQStride + c8) = val;
+  }
+  __syncthreads();
+  const uint16_t* kbase = kc + ((int64_t)b * nkv + g) * max_len * 128;
+  const uint16_t* vbase = vc + ((int64_t)b * nkv + g) * max_len * 128;
+  // scores: wave w, positions p0 + 16 w + r16 (column r16 of the tile)
+  int64_t pk = p0 + 16 * w + r16;
+  const bool pvalid = pk < len;
+  if (!pvalid) pk = len - 1;  // a valid row, masked below
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const bf16x8v a = __builtin_bit_cast(bf16x8v, *reinterpret_cast<const uint4*>(Qs + r16 * kQStride + 32 * ks + 8 * qd));
+    const bf16x8v bb = __builtin_bit_cast(bf16x8v, *reinterpret_cast<const uint4*>(kbase + pk * 128 + 32 * ks + 8 * qd));
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bb, acc, 0, 0, 0);
+  }
+  // acc[j]: head 4 qd + j, position p0 + 16 w + r16
+  float sc[4], mx[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    sc[j] = pvalid ? acc[j] * scale : -INFINITY;
+    float m = sc[j];
+    m = fmaxf(m, lane_xor<8>(m, lx));
+    m = fmaxf(m, lane_xor<4>(m, lx));
+    m = fmaxf(m, lane_xor<2>(m, lx));
+    m = fmaxf(m, lane_xor<1>(m, lx));
+    mx[j] = m;
+  }
+  if (r16 == 0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) red[0][w][4 * qd + j] = mx[j];
+  }
+  __syncthreads();
+  float ps[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int h = 4 * qd + j;
+    const float m = fmaxf(fmaxf(red[0][0][h], red[0][1][h]), fmaxf(red[0][2][h], red[0][3][h]));
+    mx[j] = m;
+    const float e = pvalid ? __expf(sc[j] - m) : 0.0f;
+    const uint16_t eb = f32_to_bf16(e);
+    Ps[h * kQStride + 16 * w + r16] = eb;
+    float t = bf(eb);  // the sum of the probabilities the value product uses
+    t += lane_xor<8>(t, lx);
+    t += lane_xor<4>(t, lx);
+    t += lane_xor<2>(t, lx);
+    t += lane_xor<1>(t, lx);
+    ps[j] = t;
+  }
+  if (r16 == 0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) red[1][w][4 * qd + j] = ps[j];
+  }
+  __syncthreads();
+  float* out = part + (((int64_t)b * nkv + g) * nsplit + s) * kPartFloats;
+  if (tid < 16) {
+    out[tid] = fmaxf(fmaxf(red[0][0][tid], red[0][1][tid]), fmaxf(red[0][2][tid], red[0][3][tid]));
+    out[16 + tid] = (red[1][0][tid] + red[1][1][tid]) + (red[1][2][tid] + red[1][3][tid]);
+  }
+  // values: wave w, dims 32 w .. 32 w + 31 (two tiles of 16), positions in two k-steps of 32
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt) {
+    const int d = 32 * w + 16 * dt + r16;
+    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const bf16x8v a = __builtin_bit_cast(bf16x8v, *reinterpret_cast<const uint4*>(Ps + r16 * kQStride + 32 * ks + 8 * qd));
+      uint32_t vb[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        int64_t pa = p0 + 32 * ks + 8 * qd + 2 * i, pb = pa + 1;
+        pa = pa < len ? pa : len - 1;  // probability 0 there; any finite cached row
+        pb = pb < len ? pb : len - 1;
+        vb[i] = (uint32_t)vbase[pa * 128 + d] | ((uint32_t)vbase[pb * 128 + d] << 16);
+      }
+      o = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8v, make_uint4(vb[0], vb[1], vb[2], vb[3])),
+                                                  o, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) out[32 + (4 * qd + j) * 128 + d] = o[j];
+  }
+}
+
+// Output of head h (row b): the splits' outputs rescaled to the common max,
+// summed, divided by the summed probabilities; bf16 into [row][head * 128].
+__global__ __launch_bounds__(128) void attn_combine_kernel(const float* part, const int64_t* pos_p, uint16_t* out,
+                                                           int nh, int nkv, int nsplit, int64_t ldo) {
+  const int b = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
+  const int G = nh / nkv, g = h / G, hl = h - g * G;
+  const int64_t len = *pos_p + 1;
+  const int ns = (int)((len + kSplit - 1) / kSplit);
+  const float* base = part + ((int64_t)b * nkv + g) * nsplit * kPartFloats;
+  float M = -INFINITY;
+  for (int s = 0; s < ns; ++s) M = fmaxf(M, base[s * kPartFloats + hl]);
+  float L = 0.0f, O = 0.0f;
+  for (int s = 0; s < ns; ++s) {
+    const float* p = base + s * kPartFloats;
+    const float f = __expf(p[hl] - M);
+    L += f * p[16 + hl];
+    O += f * p[32 + hl * 128 + d];
+  }
+  out[(int64_t)b * ldo + h * 128 + d] = f32_to_bf16(O / L);
+}
+
+// act = bf16(silu(gate)) * up, each op rounded to bf16 (act_fn(gate) * up).
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* gt, const uint16_t* up, uint16_t* out,
+                                                       int64_t m, int64_t ldg, int64_t ldu, int64_t ldo) {
+  const int64_t r = blockIdx.y;
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 2;
+  if (i >= m) return;
+  const uint32_t a = *reinterpret_cast<const uint32_t*>(gt + r * ldg + i);
+  const uint32_t u = *reinterpret_cast<const uint32_t*>(up + r * ldu + i);
+  float gv[2] = {bf((uint16_t)(a & 0xFFFF)), bf((uint16_t)(a >> 16))};
+  float uv[2] = {bf((uint16_t)(u & 0xFFFF)), bf((uint16_t)(u >> 16))};
+  uint32_t o = 0;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const float sv = rbf(gv[k] / (1.0f + __expf(-gv[k])));
+    o |= (uint32_t)f32_to_bf16(sv * uv[k]) << (16 * k);
+  }
+  *reinterpret_cast<uint32_t*>(out + r * ldo + i) = o;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+}  // namespace qs
+
+using namespace qs;
+
+extern "C" int qs_dec_rmsnorm(const void* h, const void* delta, void* h_out, const void* weight, void* x,
+                              int64_t rows, int64_t dim, int64_t ld, float eps, qs_stream_t stream) {
+  QS_REQUIRE(h && weight && x && rows >= 1 && rows <= 65535 && dim >= 8 && dim % 8 == 0 && ld >= dim && ld % 8 == 0,
+             "qs_dec_rmsnorm: rows %lld, dim %lld (multiple of 8), ld %lld", (long long)rows, (long long)dim,
+             (long long)ld);
+  QS_REQUIRE(!delta || h_out, "qs_dec_rmsnorm: a residual delta needs h_out");
+  QS_REQUIRE(aligned16(h) && aligned16(weight) && aligned16(x) && (!delta || (aligned16(delta) && aligned16(h_out))),
+             "qs_dec_rmsnorm: buffers must be 16-byte aligned");
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)rows), dim3(256), 0, as_stream(stream),
+                     static_cast<const uint16_t*>(h), static_cast<const uint16_t*>(delta), static_cast<uint16_t*>(h_out),
+                     static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(x), (int)dim, ld, eps);
+  QS_LAUNCHED("rmsnorm_kernel");
+  return QS_OK;
+}
+
+extern "C" int qs_dec_qk_norm_rope(const void* q, const void* k, const void* v, const void* q_norm_w,
+                                   const void* k_norm_w, const void* cos_table, const void* sin_table,
+                                   const int64_t* pos, void* q_out, void* k_cache, void* v_cache, int64_t rows, int nh,
+                                   int nkv, int head_dim, int64_t max_len, float eps, qs_stream_t stream) {
+  QS_REQUIRE(q && k && v && q_norm_w && k_norm_w && cos_table && sin_table && pos && q_out && k_cache && v_cache,
+             "qs_dec_qk_norm_rope: null pointer");
+  QS_SUPPORTED(head_dim == 128, "qs_dec_qk_norm_rope: head_dim %d (128 only)", head_dim);
+  QS_REQUIRE(rows >= 1 && rows <= 65535 && nh >= 1 && nkv >= 1 && nh % nkv == 0 && max_len >= 1,
+             "qs_dec_qk_norm_rope: rows %lld, heads %d / %d, cache length %lld", (long long)rows, nh, nkv,
+             (long long)max_len);
+  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)rows, (unsigned)((nh + 2 * nkv + 3) / 4)), dim3(256), 0,
+                     as_stream(stream), static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                     static_cast<const uint16_t*>(v), static_cast<const uint16_t*>(q_norm_w),
+                     static_cast<const uint16_t*>(k_norm_w), static_cast<const uint16_t*>(cos_table),
+                     static_cast<const uint16_t*>(sin_table), pos, static_cast<uint16_t*>(q_out),
+                     static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), nh, nkv, max_len, eps);
+  QS_LAUNCHED("qk_norm_rope_kernel");
+  return QS_OK;
+}
+
+extern "C" int64_t qs_dec_attention_workspace_bytes(int64_t rows, int nkv, int64_t max_len) {
+  const int64_t ns = (max_len + kSplit - 1) / kSplit;
+  return rows * nkv * ns * kPartFloats * (int64_t)sizeof(float);
+}
+
+extern "C" int qs_dec_attention(const void* q, const void* k_cache, const void* v_cache, const int64_t* pos, void* out,
+                                int64_t ldo, void* workspace, int64_t workspace_bytes, int64_t rows, int nh, int nkv,
+                                int head_dim, int64_t max_len, float scale, qs_stream_t stream) {
+  QS_REQUIRE(q && k_cache && v_cache && pos && out && workspace, "qs_dec_attention: null pointer");
+  QS_SUPPORTED(head_dim == 128, "qs_dec_attention: head_dim %d (128 only)", head_dim);
+  QS_REQUIRE(rows >= 1 && rows <= 65535 && nh >= 1 && nkv >= 1 && nh % nkv == 0 && nh / nkv <= 16 && max_len >= 1 &&
+                 ldo >= (int64_t)nh * 128,
+             "qs_dec_attention: rows %lld, heads %d / %d (at most 16 per kv head), cache length %lld, ldo %lld",
+             (long long)rows, nh, nkv, (long long)max_len, (long long)ldo);
+  QS_REQUIRE(workspace_bytes >= qs_dec_attention_workspace_bytes(rows, nkv, max_len),
+             "qs_dec_attention: workspace of %lld bytes, %lld needed", (long long)workspace_bytes,
+             (long long)qs_dec_attention_workspace_bytes(rows, nkv, max_len));
+  QS_REQUIRE(aligned16(q) && aligned16(k_cache), "qs_dec_attention: q and the key cache must be 16-byte aligned");
+  const int ns = (int)((max_len + kSplit - 1) / kSplit);
+  QS_REQUIRE(ns <= 65535, "qs_dec_attention: cache length %lld", (long long)max_len);
+  hipLaunchKernelGGL(attn_split_kernel, dim3((unsigned)ns, (unsigned)nkv, (unsigned)rows), dim3(256), 0,
+                     as_stream(stream), static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k_cache),
+                     static_cast<const uint16_t*>(v_cache), pos, static_cast<float*>(workspace), nh, nkv, max_len, ns,
+                     scale);
+  QS_LAUNCHED("attn_split_kernel");
+  hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)rows, (unsigned)nh), dim3(128), 0, as_stream(stream),
+                     static_cast<const float*>(workspace), pos, static_cast<uint16_t*>(out), nh, nkv, ns, ldo);
+  QS_LAUNCHED("attn_combine_kernel");
+  return QS_OK;
+}
+
+extern "C" int qs_dec_silu_mul(const void* gate, const void* up, void* out, int64_t rows, int64_t m, int64_t ldg,
+                               int64_t ldu, int64_t ldo, qs_stream_t stream) {
+  QS_REQUIRE(gate && up && out && rows >= 1 && rows <= 65535 && m >= 2 && m % 2 == 0 && ldg >= m && ldu >= m &&
+                 ldo >= m && ldg % 2 == 0 && ldu % 2 == 0 && ldo % 2 == 0,
+             "qs_dec_silu_mul: rows %lld, m %lld (even)", (long long)rows, (long long)m);
+  QS_REQUIRE(((reinterpret_cast<uintptr_t>(gate) | reinterpret_cast<uintptr_t>(up) | reinterpret_cast<uintptr_t>(out)) &
+              3) == 0,
+             "qs_dec_silu_mul: buffers must be 4-byte aligned");
+  hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((m / 2 + 255) / 256), (unsigned)rows), dim3(256), 0,
+                     as_stream(stream), static_cast<const uint16_t*>(gate), static_cast<const uint16_t*>(up),
+                     static_cast<uint16_t*>(out), m, ldg, ldu, ldo);
+  QS_LAUNCHED("silu_mul_kernel");
+  return QS_OK;
+}

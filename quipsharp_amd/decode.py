@@ -3,8 +3,9 @@ default): every decoder linear is a QuantizedLinear with random E8P codes,
 the rest of the model (embeddings, norms, rotary tables, lm_head) is the
 transformers implementation in bf16 with random weights.  Built on the meta
 device and materialized on the GPU, so the 32B-parameter model never exists
-densely.  Decoding runs through StaticDecoder (static fp32 KV cache, device
-positions and mask) so that each step is one HIP-graph replay.  Reports
+densely.  Decoding runs through StaticDecoder (static bf16 KV cache, device
+positions, the decode step's own kernels around the quantized linears) so
+that each step is one HIP-graph replay.  Reports
 prefill time, decode tok/s and, per decoder linear of the first layer, the
 forward time and HBM GB/s at each batch size.
 
@@ -110,30 +111,64 @@ def greedy_decode(model, prompt_ids, new_tokens):
 
 
 class StaticDecoder:
-    """A graph-capturable decode step for Qwen3-style decoders built on the
-    transformers modules of ``model`` (embeddings, RMSNorms, q/k norms,
-    rotary tables, SwiGLU, lm_head) and its QuantizedLinear layers: a static
-    KV cache of ``max_len`` positions per layer, positions passed as a device
-    tensor, the causal mask built on the device, so one decode step can be
-    captured once and replayed.  Attention runs in fp32 (keys and values are
-    kept in fp32).  q/k/v and gate/up, which read the same input, go through
-    one grouped launch each when the step has at most two rows
-    (checkpoint.grouped_forward)."""
+    """A graph-capturable greedy-decode step for Qwen3-style decoders built on
+    the transformers modules of ``model`` (embeddings, RMSNorm and q/k-norm
+    weights, rotary tables, lm_head) and its QuantizedLinear layers, with a
+    static bf16 KV cache of ``max_len`` positions per layer and the position
+    passed as a device tensor, so one decode step can be captured once and
+    replayed.
+
+    A decode step (one new token per row) runs the layer's own kernels
+    (csrc/qs_decoder.hip): RMSNorm with the residual add folded in, q/k norm
+    plus rotary embedding plus the cache write in one launch, attention over
+    the filled cache prefix only (splits of 64 positions and a combine
+    launch), SiLU * up; q/k/v and gate/up each go through one grouped
+    quantized-linear launch (checkpoint.grouped_forward).  The prompt
+    (several tokens per row) runs transformers' modules with the same bf16
+    cache (attention in fp32)."""
 
     def __init__(self, model, batch, max_len):
+        from . import _lib
         cfg = model.config
         self.model = model
         self.layers = get_decoder_layers(model)
         self.B, self.max_len = batch, max_len
         self.nh, self.nkv, self.hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        self.hidden = cfg.hidden_size
+        self.eps = float(cfg.rms_norm_eps)
+        self.scale = self.hd ** -0.5
         dev = model.lm_head.weight.device
-        self.k = [torch.zeros(batch, self.nkv, max_len, self.hd, device=dev) for _ in self.layers]
-        self.v = [torch.zeros(batch, self.nkv, max_len, self.hd, device=dev) for _ in self.layers]
+        self.dev = dev
+        bf = torch.bfloat16
+        self.k = [torch.zeros(batch, self.nkv, max_len, self.hd, device=dev, dtype=bf) for _ in self.layers]
+        self.v = [torch.zeros(batch, self.nkv, max_len, self.hd, device=dev, dtype=bf) for _ in self.layers]
         self.kpos = torch.arange(max_len, device=dev)
+        # rotary tables of every cache position, as transformers computes them
+        m = model.model
+        with torch.no_grad():
+            cos, sin = m.rotary_emb(torch.zeros(1, 1, self.hidden, device=dev, dtype=bf), self.kpos[None])
+        self.cos, self.sin = cos[0].to(bf).contiguous(), sin[0].to(bf).contiguous()
+        L = _lib.lib()
+        self._L, self._lib = L, _lib
+        nbytes = L.qs_dec_attention_workspace_bytes(batch, self.nkv, max_len)
+        self.attn_ws = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=dev)
+        self.fused_ok = self.hd == 128 and self.nh % self.nkv == 0 and self.nh // self.nkv <= 16 \
+            and self.hidden % 8 == 0
+
+    def _weight(self, mod):
+        w = mod.weight
+        if w.dtype != torch.bfloat16 or not w.is_contiguous():
+            raise TypeError("the decode step takes bf16 norm weights")
+        return w
 
     @torch.no_grad()
     def step(self, ids, pos):
         """Logits of the last position; ids (B, q), pos (q,) int64 positions."""
+        if ids.shape[1] == 1 and self.fused_ok:
+            return self._decode_step(ids, pos)
+        return self._prompt_step(ids, pos)
+
+    def _prompt_step(self, ids, pos):
         from transformers.models.qwen3.modeling_qwen3 import apply_rotary_pos_emb
         import torch.nn.functional as F
         m = self.model.model
@@ -149,14 +184,56 @@ class StaticDecoder:
             ks = a.k_norm(ko.view(B, q, self.nkv, self.hd)).transpose(1, 2)
             vs = vo.view(B, q, self.nkv, self.hd).transpose(1, 2)
             qs, ks = apply_rotary_pos_emb(qs, ks, cos, sin)
-            self.k[i].index_copy_(2, pos, ks.float())
-            self.v[i].index_copy_(2, pos, vs.float())
-            o = F.scaled_dot_product_attention(qs.float(), self.k[i], self.v[i], attn_mask=mask, enable_gqa=True)
+            self.k[i].index_copy_(2, pos, ks.to(self.k[i].dtype))
+            self.v[i].index_copy_(2, pos, vs.to(self.v[i].dtype))
+            o = F.scaled_dot_product_attention(qs.float(), self.k[i].float(), self.v[i].float(), attn_mask=mask,
+                                               enable_gqa=True)
             h = h + a.o_proj(o.transpose(1, 2).reshape(B, q, self.nh * self.hd).to(h.dtype))
             x = L.post_attention_layernorm(h)
             go, uo = grouped_forward(x, [L.mlp.gate_proj, L.mlp.up_proj])
             h = h + L.mlp.down_proj(L.mlp.act_fn(go) * uo)
         return self.model.lm_head(m.norm(h[:, -1:]))[:, -1]
+
+    def _decode_step(self, ids, pos):
+        L, lib = self._L, self._lib
+        m = self.model.model
+        B = ids.shape[0]
+        H, nh, nkv, hd = self.hidden, self.nh, self.nkv, self.hd
+        stream = lib.stream_of(ids)
+        vp = lib.ptr
+        h = m.embed_tokens(ids).reshape(B, H)
+        if h.dtype != torch.bfloat16:
+            raise TypeError("the decode step runs bf16 models")
+        h = h.contiguous()
+        qbuf = torch.empty(B, nh * hd, dtype=torch.bfloat16, device=h.device)
+        attn = torch.empty(B, nh * hd, dtype=torch.bfloat16, device=h.device)
+        delta = None
+        for i, Ly in enumerate(self.layers):
+            a = Ly.self_attn
+            x = torch.empty_like(h)
+            lib.check(L.qs_dec_rmsnorm(vp(h), vp(delta), vp(h), vp(self._weight(Ly.input_layernorm)), vp(x), B, H, H,
+                                       self.eps, stream))
+            qo, ko, vo = grouped_forward(x, [a.q_proj, a.k_proj, a.v_proj])
+            lib.check(L.qs_dec_qk_norm_rope(vp(qo.contiguous()), vp(ko.contiguous()), vp(vo.contiguous()),
+                                            vp(self._weight(a.q_norm)), vp(self._weight(a.k_norm)), vp(self.cos),
+                                            vp(self.sin), vp(pos), vp(qbuf), vp(self.k[i]), vp(self.v[i]), B, nh, nkv,
+                                            hd, self.max_len, self.eps, stream))
+            lib.check(L.qs_dec_attention(vp(qbuf), vp(self.k[i]), vp(self.v[i]), vp(pos), vp(attn), nh * hd,
+                                         vp(self.attn_ws), self.attn_ws.numel(), B, nh, nkv, hd, self.max_len,
+                                         self.scale, stream))
+            o = a.o_proj(attn)
+            x = torch.empty_like(h)
+            lib.check(L.qs_dec_rmsnorm(vp(h), vp(o.contiguous()), vp(h), vp(self._weight(Ly.post_attention_layernorm)),
+                                       vp(x), B, H, H, self.eps, stream))
+            go, uo = grouped_forward(x, [Ly.mlp.gate_proj, Ly.mlp.up_proj])
+            go, uo = go.contiguous(), uo.contiguous()
+            act = torch.empty_like(go)
+            inter = go.shape[-1]
+            lib.check(L.qs_dec_silu_mul(vp(go), vp(uo), vp(act), B, inter, inter, inter, inter, stream))
+            delta = Ly.mlp.down_proj(act).contiguous()
+        x = torch.empty_like(h)
+        lib.check(L.qs_dec_rmsnorm(vp(h), vp(delta), vp(h), vp(self._weight(m.norm)), vp(x), B, H, H, self.eps, stream))
+        return self.model.lm_head(x)
 
 
 @torch.no_grad()

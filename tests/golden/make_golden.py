@@ -243,6 +243,60 @@ def c1_full(ref_root):
     print(f"c1_full.npz written: quantize {t_q:.0f} s, proxy_rel {proxy_rel:.5e}", flush=True)
 
 
+def c1_full_3bit(ref_root):
+    """The C1 recipe (same W, H, x draws and torch.manual_seed(0) before
+    quantize_linear) with the 3-bit RVQ codebook: build_codebook("3bit",
+    "cpu", 0), i.e. [E8P, E8 1-bit] stages with their fitted scales and the
+    RVQ's own input scale (checkpoint.py:60-77, rvq.py:69-88,
+    quantize.py:48-104).
+
+    Writes c1_full_3bit.npz: stage-1 codes (u16 [4096, 512]) and stage-2
+    codes (u8 [4096, 512]) with their SHA-256, layer_scale, the codebook
+    scales, y = linear_forward(x), the signs and the relative proxy loss
+    tr(E H E^T) / tr(W H W^T) in the transformed basis."""
+    import time
+    sys.path.insert(0, ref_root)
+    import torch
+    from quipsharp.checkpoint import build_codebook
+    from quipsharp.quantize import quantize_linear, linear_forward
+    from quipsharp.incoherence import incoherence_process
+
+    torch.set_num_threads(int(os.environ.get("C1_THREADS", "8")))
+    g = torch.Generator().manual_seed(0)
+    W = torch.randn(4096, 4096, generator=g) * 0.02
+    X = torch.randn(2048, 4096, generator=g)
+    H = X.T @ X / 2048
+    x = torch.randn(4096, generator=g)
+    cb, s = build_codebook("3bit", "cpu", 0)
+    t0 = time.time()
+    torch.manual_seed(0)
+    layer, what_q = quantize_linear(W, H, cb, g=8, damping=1e-2, codebook_scale=s, tune_iters=10)
+    t_q = time.time() - t0
+    y = linear_forward(x, layer, cb)
+    Hd = H + 1e-2 * H.diagonal().mean() * torch.eye(4096)
+    torch.manual_seed(0)
+    what, hhat, signs = incoherence_process(W, Hd)
+    assert torch.equal(signs.su, layer.signs.su) and torch.equal(signs.sv, layer.signs.sv)
+    E = (what_q - what).double()
+    Wd = what.double()
+    Hh = hhat.double()
+    proxy_rel = (torch.trace(E @ Hh @ E.T) / torch.trace(Wd @ Hh @ Wd.T)).item()
+    assert layer.codes.shape == (2, 4096, 512)
+    c0 = layer.codes[0].numpy().astype(np.uint16)
+    c1 = layer.codes[1].numpy().astype(np.uint8)
+    assert np.array_equal(c1.astype(np.int64), layer.codes[1].numpy())
+    sha = lambda a: np.frombuffer(hashlib.sha256(a.tobytes()).digest(), np.uint8)
+    np.savez_compressed(os.path.join(OUT, "c1_full_3bit.npz"), codes0=c0, codes1=c1,
+                        codes0_sha256=sha(c0), codes1_sha256=sha(c1),
+                        layer_scale=np.float64(layer.scale), codebook_scale=np.float64(s),
+                        stage_scales=np.array([st.scale for st in cb.stages], np.float64), y=y.numpy(),
+                        su=layer.signs.su.numpy().astype(np.int8),
+                        sv=layer.signs.sv.numpy().astype(np.int8),
+                        proxy_rel=np.float64(proxy_rel), quantize_seconds=np.float64(t_q),
+                        threads=np.int32(torch.get_num_threads()))
+    print(f"c1_full_3bit.npz written: quantize {t_q:.0f} s, proxy_rel {proxy_rel:.5e}", flush=True)
+
+
 def ref_checkpoint(ref_root):
     """A checkpoint written by the reference's own save path
     (quipsharp/checkpoint.py:149-186, driven as scripts/quantize_model.py:72-126
@@ -311,6 +365,8 @@ if __name__ == "__main__":
     root = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
     if len(sys.argv) > 2 and sys.argv[2] == "c1":
         c1_full(root)
+    elif len(sys.argv) > 2 and sys.argv[2] == "c1_3bit":
+        c1_full_3bit(root)
     elif len(sys.argv) > 2 and sys.argv[2] == "ckpt":
         ref_checkpoint(root)
     else:

@@ -1,0 +1,147 @@
+"""The decode-step kernels of the greedy-decode harness (csrc/qs_decoder.hip)
+against the transformers / torch ops they replace: Qwen3RMSNorm with the
+residual add, q/k norm + rotary embedding + cache write, attention over the
+filled cache prefix (reference in fp32 on the CPU), and act_fn(gate) * up."""
+import math
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _lib():
+    from quipsharp_amd import _lib
+    return _lib, _lib.lib()
+
+
+def _bf16_ulps(a, b):
+    """Largest distance in bf16 units in the last place between two bf16 tensors."""
+    ia = a.view(torch.int16).to(torch.int32)
+    ib = b.view(torch.int16).to(torch.int32)
+    # order-preserving map of the sign-magnitude bit patterns
+    ia = torch.where(ia < 0, -32768 - ia, ia)
+    ib = torch.where(ib < 0, -32768 - ib, ib)
+    return int((ia - ib).abs().max().item())
+
+
+@pytest.mark.parametrize("rows,dim", [(1, 5120), (8, 5120), (3, 512)])
+def test_rmsnorm_with_residual(dev, rows, dim):
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3RMSNorm
+    lib, L = _lib()
+    g = torch.Generator().manual_seed(rows)
+    h = (torch.randn(rows, dim, generator=g) * 3).bfloat16().to(dev)
+    d = torch.randn(rows, dim, generator=g).bfloat16().to(dev)
+    norm = Qwen3RMSNorm(dim, eps=1e-6).to(dev).bfloat16()
+    with torch.no_grad():
+        norm.weight.copy_((1 + 0.1 * torch.randn(dim, generator=g)).bfloat16())
+        want_h = h + d
+        want_x = norm(want_h)
+    hh = h.clone()
+    x = torch.empty_like(h)
+    lib.check(L.qs_dec_rmsnorm(lib.ptr(hh), lib.ptr(d), lib.ptr(hh), lib.ptr(norm.weight), lib.ptr(x), rows, dim, dim,
+                               1e-6, lib.stream_of(h)))
+    torch.cuda.synchronize()
+    assert torch.equal(hh, want_h)
+    assert _bf16_ulps(x, want_x) <= 1
+    # no residual: h untouched
+    x2 = torch.empty_like(h)
+    lib.check(L.qs_dec_rmsnorm(lib.ptr(h), None, None, lib.ptr(norm.weight), lib.ptr(x2), rows, dim, dim, 1e-6,
+                               lib.stream_of(h)))
+    torch.cuda.synchronize()
+    with torch.no_grad():
+        assert _bf16_ulps(x2, norm(h)) <= 1
+
+
+@pytest.mark.parametrize("rows,nh,nkv", [(1, 64, 8), (8, 64, 8), (2, 4, 2)])
+def test_qk_norm_rope_cache(dev, rows, nh, nkv):
+    from transformers import Qwen3Config
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3RMSNorm, Qwen3RotaryEmbedding, apply_rotary_pos_emb
+    lib, L = _lib()
+    max_len, p = 96, 37
+    cfg = Qwen3Config(hidden_size=nh * 128, num_attention_heads=nh, num_key_value_heads=nkv, head_dim=128)
+    rot = Qwen3RotaryEmbedding(cfg).to(dev)
+    g = torch.Generator().manual_seed(nh + rows)
+    q = torch.randn(rows, nh * 128, generator=g).bfloat16().to(dev)
+    k = torch.randn(rows, nkv * 128, generator=g).bfloat16().to(dev)
+    v = torch.randn(rows, nkv * 128, generator=g).bfloat16().to(dev)
+    qn, kn = Qwen3RMSNorm(128).to(dev).bfloat16(), Qwen3RMSNorm(128).to(dev).bfloat16()
+    with torch.no_grad():
+        qn.weight.copy_((1 + 0.1 * torch.randn(128, generator=g)).bfloat16())
+        kn.weight.copy_((1 + 0.1 * torch.randn(128, generator=g)).bfloat16())
+        cos, sin = rot(torch.zeros(1, 1, 8, device=dev, dtype=torch.bfloat16), torch.arange(max_len, device=dev)[None])
+        cos_t, sin_t = cos[0].contiguous(), sin[0].contiguous()
+        qs = qn(q.view(rows, 1, nh, 128)).transpose(1, 2)
+        ks = kn(k.view(rows, 1, nkv, 128)).transpose(1, 2)
+        qr, kr = apply_rotary_pos_emb(qs, ks, cos[:, p:p + 1], sin[:, p:p + 1])
+    kc = torch.zeros(rows, nkv, max_len, 128, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    qo = torch.empty(rows, nh * 128, dtype=torch.bfloat16, device=dev)
+    pos = torch.full((1,), p, dtype=torch.long, device=dev)
+    lib.check(L.qs_dec_qk_norm_rope(lib.ptr(q), lib.ptr(k), lib.ptr(v), lib.ptr(qn.weight), lib.ptr(kn.weight),
+                                    lib.ptr(cos_t), lib.ptr(sin_t), lib.ptr(pos), lib.ptr(qo), lib.ptr(kc), lib.ptr(vc),
+                                    rows, nh, nkv, 128, max_len, 1e-6, lib.stream_of(q)))
+    torch.cuda.synchronize()
+    assert _bf16_ulps(qo.view(rows, nh, 128), qr[:, :, 0]) <= 1
+    assert _bf16_ulps(kc[:, :, p], kr[:, :, 0]) <= 1
+    assert torch.equal(vc[:, :, p], v.view(rows, nkv, 128))
+    # nothing else of the caches is written
+    assert kc[:, :, :p].abs().sum().item() == 0 and vc[:, :, p + 1:].abs().sum().item() == 0
+
+
+@pytest.mark.parametrize("rows,nh,nkv,length", [(1, 64, 8, 1), (1, 64, 8, 64), (1, 64, 8, 577), (8, 64, 8, 300),
+                                                (2, 4, 2, 130)])
+def test_attention_over_prefix(dev, rows, nh, nkv, length):
+    lib, L = _lib()
+    max_len = 770
+    g = torch.Generator().manual_seed(length)
+    q = torch.randn(rows, nh, 128, generator=g).bfloat16()
+    kc = torch.randn(rows, nkv, max_len, 128, generator=g).bfloat16()
+    vc = torch.randn(rows, nkv, max_len, 128, generator=g).bfloat16()
+    # positions past the filled length hold large values that must not leak in
+    kc[:, :, length:] = 1e4
+    vc[:, :, length:] = 1e4
+    scale = 128 ** -0.5
+    G = nh // nkv
+    kk = kc[:, :, :length].float().repeat_interleave(G, dim=1)
+    vv = vc[:, :, :length].float().repeat_interleave(G, dim=1)
+    s = torch.einsum("bhd,bhpd->bhp", q.float(), kk) * scale
+    want = torch.einsum("bhp,bhpd->bhd", torch.softmax(s, -1), vv).reshape(rows, nh * 128)
+    qd, kd, vd = q.to(dev), kc.to(dev), vc.to(dev)
+    out = torch.empty(rows, nh * 128, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(int(L.qs_dec_attention_workspace_bytes(rows, nkv, max_len)), dtype=torch.uint8, device=dev)
+    pos = torch.full((1,), length - 1, dtype=torch.long, device=dev)
+    lib.check(L.qs_dec_attention(lib.ptr(qd), lib.ptr(kd), lib.ptr(vd), lib.ptr(pos), lib.ptr(out), nh * 128,
+                                 lib.ptr(ws), ws.numel(), rows, nh, nkv, 128, max_len, scale, lib.stream_of(qd)))
+    torch.cuda.synchronize()
+    got = out.float().cpu()
+    rel = ((got - want).norm() / want.norm()).item()
+    assert rel < 1e-2, rel
+    assert (got - want).abs().max().item() < 0.05
+
+
+def test_attention_workspace_and_argument_checks(dev):
+    lib, L = _lib()
+    assert L.qs_dec_attention_workspace_bytes(1, 8, 770) == 1 * 8 * math.ceil(770 / 64) * (32 + 16 * 128) * 4
+    x = torch.zeros(64, dtype=torch.bfloat16, device=dev)
+    pos = torch.zeros(1, dtype=torch.long, device=dev)
+    # head_dim other than 128, more than 16 query heads per kv head, short workspace
+    assert L.qs_dec_attention(lib.ptr(x), lib.ptr(x), lib.ptr(x), lib.ptr(pos), lib.ptr(x), 64 * 64, lib.ptr(x), 128,
+                              1, 64, 8, 64, 16, 0.1, None) != 0
+    assert L.qs_dec_attention(lib.ptr(x), lib.ptr(x), lib.ptr(x), lib.ptr(pos), lib.ptr(x), 64 * 128, lib.ptr(x), 1 << 20,
+                              1, 64, 2, 128, 16, 0.1, None) != 0
+    assert L.qs_dec_attention(lib.ptr(x), lib.ptr(x), lib.ptr(x), lib.ptr(pos), lib.ptr(x), 64 * 128, lib.ptr(x), 16,
+                              1, 64, 8, 128, 16, 0.1, None) != 0
+
+
+@pytest.mark.parametrize("rows,m", [(1, 25600), (8, 25600), (3, 1536)])
+def test_silu_mul(dev, rows, m):
+    lib, L = _lib()
+    g = torch.Generator().manual_seed(m + rows)
+    gt = (torch.randn(rows, m, generator=g) * 4).bfloat16().to(dev)
+    up = torch.randn(rows, m, generator=g).bfloat16().to(dev)
+    out = torch.empty_like(gt)
+    lib.check(L.qs_dec_silu_mul(lib.ptr(gt), lib.ptr(up), lib.ptr(out), rows, m, m, m, m, lib.stream_of(gt)))
+    torch.cuda.synchronize()
+    want = torch.nn.functional.silu(gt) * up
+    assert _bf16_ulps(out, want) <= 1
