@@ -49,7 +49,7 @@ def test_quantize_linear_vs_reference_run(dev, cbs, name, bits):
     codes = layer.codes.cpu().numpy()
     agree = (codes == q["codes"]).mean()
     print(f"{name}: code agreement with the reference run {agree:.4f}", flush=True)
-    assert agree > 0.9
+    assert agree >= 0.995  # measured 1.0000 at this size
     assert torch.equal(dequantize_linear(layer, cb), what_q)
     # proxy loss in the transformed basis, against the reference's own result
     from quipsharp_amd.incoherence import incoherence_process
