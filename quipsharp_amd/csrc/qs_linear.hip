@@ -8,7 +8,9 @@
 // qs_decode_matvec), the workspace layout, and the kernels for the shapes the
 // chunk-scheme kernels do not take: the LDS-radix row transforms xin_kernel /
 // yout_kernel (any n, m up to 32768; the input or output side of a pass whose
-// n or m is outside the chunk scheme), yout_chunk_kernel, and the row-major
+// n or m is outside both the per-row chunk kernels' 12288 and the 16-chunk
+// work-group kernels of qs_linear_big.hip, and the transform-free calls),
+// yout_chunk_kernel, and the row-major
 // decode-matvec of the generic code layout (mv_generic_kernel).  Which path a
 // call takes: one launch for 1-2 rows (qs_linear_fused.hip), passes of 16
 // rows through the batched decode-matvec (qs_linear_batched.hip), the wide
@@ -693,6 +695,8 @@ static int forward_wide(const void* x, int x_dtype, int64_t ldx, int64_t batch, 
   const bool sv_aligned = (reinterpret_cast<uintptr_t>(sv) & (sbits ? 3 : 15)) == 0;
   if (chunk_transform_fits(n, kron_pn) && sv_aligned)
     rc = launch_bx_rows(P, s);
+  else if (big_input_fits(n, kron_pn, x_dtype) && sv_aligned && fused_x_aligned(x, x_dtype, ldx))
+    rc = launch_bx_big(P, s);
   else
     rc = launch_xin_rows(x, x_dtype, ldx, batch, n, kron_pn, kron_n, sv, P.x2h, P.sg, reinterpret_cast<float*>(ws + W.xtot),
                          P.xmul, P.frag, s);
@@ -717,6 +721,7 @@ static int forward_wide(const void* x, int x_dtype, int64_t ldx, int64_t batch, 
   // partial groups summed by the output kernels; the +-1/4 shifts are in y1
   P.SG = F.SGk;
   if (chunk_transform_fits(m, kron_pm)) return launch_by_rows(P, s);
+  if (big_transform_fits(m, kron_pm)) return launch_by_big(&P, 1, s);
   return launch_yout_rows(P.y1p, F.SGk, (int)batch, m, kron_pm, kron_m, nullptr, 0, P.xmul, s0, layer_scale, su, bias,
                           y, y_dtype, ldy, s);
 }
@@ -780,12 +785,17 @@ static int forward_batched(const void* x, int x_dtype, int64_t ldx, int64_t batc
       } else {
         if (!identity && chunk_transform_fits(n, kron_pn) && sv_aligned)
           rc = launch_bx_rows(P, s);
+        else if (!identity && big_input_fits(n, kron_pn, x_dtype) && sv_aligned &&
+                 fused_x_aligned(P.x, x_dtype, ldx))
+          rc = launch_bx_big(P, s);
         else
           rc = launch_xin_rows(P.x, x_dtype, ldx, P.B, n, kron_pn, kron_n, sv, P.x2h, P.sg,
                                reinterpret_cast<float*>(ws + W.xtot), P.xmul, P.frag, s, identity);
         if (!rc) rc = launch_bm(P, s, ev0, ev1);
         if (!rc && !identity && chunk_transform_fits(m, kron_pm))
           rc = launch_by_rows(P, s);
+        else if (!rc && !identity && big_transform_fits(m, kron_pm))
+          rc = launch_by_big(&P, 1, s);
         else if (!rc)
           rc = launch_yout_rows(P.y1p, P.SG, P.B, m, kron_pm, kron_m, nullptr, 0, P.xmul, s0, layer_scale, su, bias,
                                 P.y, y_dtype, ldy, s, identity);
@@ -1136,16 +1146,25 @@ static int forward_group_rows(const void* x, int x_dtype, int64_t ldx, int64_t b
     if (rc) return rc;
     if (tail) return QS_OK;  // the decode-matvec applied the output transforms
   }
-  // output transforms: the chunk-scheme ones in one launch, the others one by one
-  BatchedPass Pc[QS_MAX_GROUP];
-  int nc = 0;
+  // output transforms: the chunk-scheme ones in one launch, those up to
+  // 32768 in another, the others one by one
+  BatchedPass Pc[QS_MAX_GROUP], Pb[QS_MAX_GROUP];
+  int nc = 0, nb = 0;
   for (int g = 0; g < count; ++g) {
     if (chunk_transform_fits(P[g].m, P[g].pm)) {
       Pc[nc++] = P[g];
       continue;
     }
+    if (big_transform_fits(P[g].m, P[g].pm)) {
+      Pb[nb++] = P[g];
+      continue;
+    }
     rc = launch_yout_rows(P[g].y1p, P[g].SG, (int)batch, P[g].m, P[g].pm, P[g].Km, nullptr, 0, P[g].xmul, P[g].s0,
                           P[g].layer_scale, P[g].su, P[g].bias, P[g].y, y_dtype, P[g].ldy, s);
+    if (rc) return rc;
+  }
+  if (nb) {
+    rc = launch_by_big(Pb, nb, s);
     if (rc) return rc;
   }
   return nc ? launch_by_group(Pc, nc, s) : QS_OK;

@@ -100,6 +100,18 @@ int launch_bm_group(const BatchedPass* P, int count, hipStream_t stream, hipEven
 // launch_by_rows per linear.
 int launch_by_group(const BatchedPass* P, int count, hipStream_t stream);
 
+// Per-row transforms for lengths past the chunk kernels' 12288, up to 32768
+// (qs_linear_big.hip): work-groups of 16 slices (input) or 16 output chunks
+// (output) per row.  big_input_fits also checks the activation dtype (fp16 /
+// fp32 rows: n <= 16384).  launch_bx_big writes the pass's operand (x2h, sg,
+// xmul) for P.B rows; launch_by_big applies the output transforms of up to
+// QS_MAX_GROUP linears (shared rows, output dtype and sign format) from their
+// P[g].SG partial groups.
+bool big_transform_fits(int64_t len, int p);
+bool big_input_fits(int64_t n, int p, int x_dtype);
+int launch_bx_big(const BatchedPass& P, hipStream_t stream);
+int launch_by_big(const BatchedPass* P, int count, hipStream_t stream);
+
 // Fragment-major fp16 operand of the wide GEMM: row b, columns k .. k + 7 (k
 // a multiple of 8) are one 16-byte word, words ordered by [b / 16][k / 256]
 // [(k / 8) % 8][(k % 256) / 64][b % 16], so that the 64 lanes of a wave read

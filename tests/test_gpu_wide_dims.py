@@ -211,3 +211,57 @@ def test_shared_workspace_across_job_lists(dev):
         torch.cuda.synchronize()
         for k in shapes:
             assert torch.equal(buf[k], want[k]), (rep, k)
+
+
+@pytest.mark.parametrize("m,n", [
+    (25600, 1024),   # output: 100 chunks, K_25 (x) H_4, 7 work-groups per row
+    (1024, 25600),   # input: 100 chunks over 7 slice groups of 16
+    (14336, 512),    # K_7 (x) H_8
+    (768, 18944),    # K_37 (x) H_2
+    (32768, 256),    # 128 output chunks, Hadamard only
+    (256, 32768),    # 128 input chunks
+    (28672, 512),    # K_7 (x) H_16
+])
+@pytest.mark.parametrize("B", [3, 8, 16, 40])
+def test_wide_dims_multi_row(dev, m, n, B):
+    """Three rows and more beyond 12288: the per-row transforms run as
+    work-groups of 16 chunks (qs_linear_big.hip) around the 16-row
+    decode-matvec (3-16 rows) or the wide GEMM (40 rows)."""
+    print(f"case: wide dims multi-row m={m} n={n} B={B} bf16", flush=True)
+    err = _oracle_case(dev, m, n, B, 1, m + 5 * n + B, bias=(B == 8))
+    print(f"  rel err {err:.2e}", flush=True)
+    assert err < REL_TOL, (m, n, B, err)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_wide_dims_multi_row_fp16_fp32(dev, dtype):
+    """fp16 / fp32 rows: the 16-chunk input kernel keeps a low-part plane (n up
+    to 16384); beyond that the row kernel of any length takes them."""
+    for m, n, B in ((512, 16384, 5), (512, 18944, 4), (14336, 1024, 6)):
+        print(f"case: wide dims multi-row m={m} n={n} B={B} {dtype}", flush=True)
+        err = _oracle_case(dev, m, n, B, 1, m + n + B, dtype=dtype)
+        print(f"  rel err {err:.2e}", flush=True)
+        assert err < REL_TOL, (m, n, B, dtype, err)
+
+
+def test_wide_dims_multi_row_rvq3(dev):
+    for m, n, B in ((1024, 14336, 4), (14336, 1024, 16)):
+        print(f"case: wide dims multi-row rvq3 m={m} n={n} B={B}", flush=True)
+        err = _oracle_case(dev, m, n, B, 2, m + n + B)
+        print(f"  rel err {err:.2e}", flush=True)
+        assert err < REL_TOL, (m, n, B, err)
+
+
+@pytest.mark.parametrize("B", [8, 40])
+def test_wide_dims_multi_row_group_equals_single(dev, B):
+    """Linears of one input with outputs beyond 12288 (gate / up of the
+    Qwen3-32B MLP) share one output-transform launch; each output equals its
+    single call bit for bit."""
+    from quipsharp_amd.quantize import forward_packed, forward_packed_group
+    rng = np.random.default_rng(41 + B)
+    lins = [_rand_linear(dev, rng, 25600, 1024, bias=True), _rand_linear(dev, rng, 25600, 1024),
+            _rand_linear(dev, rng, 4096, 1024)]
+    x = torch.from_numpy(rng.standard_normal((B, 1024)).astype(np.float32)).to(dev).bfloat16()
+    ys = forward_packed_group(x, lins)
+    for lin, y in zip(lins, ys):
+        assert torch.equal(y, forward_packed(x, *lin))
