@@ -167,7 +167,9 @@ size_t qs_linear_workspace_bytes(int64_t m, int64_t n, int64_t batch, int layout
  * decoded weights are exact in fp16, accumulation is fp32.
  * The workspace must be zero before its first use (its first 256 bytes hold
  * the epoch: the tag of the one-launch kernel's last partial sums, which each
- * call advances); calls that may run concurrently need separate workspaces.
+ * call advances, and the count of the launch that clears old tags from the
+ * whole workspace once every 2^20 - 1 calls); calls that may run concurrently
+ * need separate workspaces.
  * mv_begin / mv_end: optional hipEvent_t attached to the start of the first
  * and the end of the last decode-matvec kernel (hipExtLaunchKernelGGL start /
  * stop events, so the interval is kernel execution only; NULL: none). */
@@ -185,13 +187,15 @@ int qs_linear_forward(const void *x, int x_dtype, int64_t ldx, int64_t batch, in
  * QS_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; this entry
  * point calls no hipMalloc / hipFree.  Shapes whose workspace
  * (qs_linear_workspace_bytes) exceeds it return QS_ERR_UNSUPPORTED before
- * anything is launched: decode batches (1..16 rows) of m, n up to 25600 fit,
- * wide prefill batches generally do not.  Every call on one GPU shares that
+ * anything is launched.  Every shape with m, n <= 32768 fits at 1..8 rows, and
+ * every shape with m * n <= 2^28 (all Qwen3-32B and Llama-2-70B layers) at
+ * 1..64 rows; 25600 x 25600 at 16 rows does not, nor do wide prefill batches
+ * (256 rows and more) of most shapes.  Every call on one GPU shares that
  * GPU's array: calls that may overlap on one GPU (other streams, other host
  * threads) race and must be serialised by the caller.  The array is zero when
  * loaded; every call advances the epoch in its first 256 bytes.
  * Outputs are bit-identical to qs_linear_forward on the same inputs. */
-#define QS_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
+#define QS_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
 int qs_linear_forward_noalloc(const void *x, int x_dtype, int64_t ldx, int64_t batch, int64_t n, int64_t m,
                               const void *codes0, const void *codes1, int kind1, int layout, const float *sv,
                               const float *su, int kron_pn, const float *kron_n, int kron_pm,

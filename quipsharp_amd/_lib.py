@@ -21,7 +21,7 @@ QS_SIGNS_BITS = 0x100  # layout flag: su / sv are packed sign bits
 QS_MAX_STAGES = 4
 QS_MAX_KRON = 64
 QS_MAX_GROUP = 4
-QS_NOALLOC_SCRATCH_BYTES = 8 << 20
+QS_NOALLOC_SCRATCH_BYTES = 32 << 20
 
 _vp = ctypes.c_void_p
 

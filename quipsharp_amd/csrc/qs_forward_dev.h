@@ -5,6 +5,7 @@
 #pragma once
 
 #include "qs_chunk_dev.h"
+#include "qs_tags.h"
 
 namespace qs {
 
@@ -452,21 +453,15 @@ __device__ __forceinline__ void load_partials(const float* y1p, int m, int Sm, i
 // partial sums as 64-bit slots {fp32 value (low word), launch tag (high
 // word)} with one agent-scope store each, and the tail work-groups poll the
 // slots until every one carries this launch's tag: no completion counter, no
-// wait for the stores to complete before signalling.  A tag is a quiet-NaN
-// bit pattern (fp32 NaN, and an fp16 NaN in its upper half) holding a 20-bit
-// launch counter and the job's index g in the launch (0-3), so a slot can only
-// match the launch that wrote it: other jobs' tags differ in g, earlier
-// launches of job index g in the counter (for 2^20 launches), and any other
-// data left in the workspace would have to be a NaN.  The counter continues
-// the workspace's epoch word of job index g (zero: no launch yet); the tail
-// work-groups store the tag as the new epoch once every slot they poll has
-// been read.
-constexpr uint32_t kTagBase = 0x7FC00000u;
-__device__ __forceinline__ uint32_t next_tag(uint32_t epoch, int g) {
-  const uint32_t c = (((epoch >> 2) & 0xFFFFFu) + 1u) & 0xFFFFFu;
-  return kTagBase | ((c ? c : 1u) << 2) | (uint32_t)g;
-}
-
+// wait for the stores to complete before signalling.  The tag (qs_tags.h)
+// holds a launch counter and the job's index g in the launch, so a slot can
+// only match the launch that wrote it: other jobs' tags differ in g, earlier
+// launches of job index g in the counter (slots left from 2^20 - 1 launches
+// earlier are cleared when the counter wraps: finish_tagged_launch), and any
+// other data left in the workspace would have to be a NaN.  The counter
+// continues the workspace's epoch word of job index g (zero: no launch yet);
+// the tail work-groups store the tag as the new epoch once every slot they
+// poll has been read.
 __device__ __forceinline__ unsigned long long tagged(float v, uint32_t tag) {
   return ((unsigned long long)tag << 32) | __float_as_uint(v);
 }
@@ -475,6 +470,46 @@ __device__ __forceinline__ unsigned long long tagged(float v, uint32_t tag) {
 // about a microsecond): a slot still missing after it reads as NaN, so a
 // failure shows in the output instead of keeping the GPU busy.
 constexpr int kMaxPolls = 1 << 20;
+
+// End of a tail work-group of a tagged launch, called by every thread once
+// every slot the work-group polls has been read: stores the tag as the epoch
+// (all the tail work-groups store the same value) and, on the launch with the
+// last counter value, clears the job's tags from the workspace (the counter
+// wrap, qs_tags.h).  `flag` is one int of LDS that is free by now.
+__device__ __forceinline__ void finish_tagged_launch(unsigned* epoch, uint32_t tag, int g, const TagWs ws, int* flag) {
+  const int tid = threadIdx.x;
+  if (tid == 0) {
+    __hip_atomic_store(epoch, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (wrap_reset_launch(tag)) __hip_atomic_store(ws.wrap, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (!wrap_launch(tag)) return;  // uniform over the work-group
+  __syncthreads();                // every wave has read its slots (and LDS)
+  if (tid == 0) {
+    const unsigned done = __hip_atomic_fetch_add(ws.wrap, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    const bool last = done == (unsigned)ws.ntail;
+    if (last) __hip_atomic_store(ws.wrap, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *flag = last;
+  }
+  __syncthreads();
+  if (!*flag) return;
+  // every work-group of the job has finished with the workspace: no slot of
+  // this launch is in flight, and other jobs' slots hold other tags
+  const int nt = (int)blockDim.x;
+  for (unsigned long long i = kWsHeaderWords + tid; i < ws.words; i += 4ull * nt) {
+    unsigned long long v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const unsigned long long e = i + (unsigned long long)k * nt;
+      v[k] = e < ws.words ? __hip_atomic_load(ws.base + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const unsigned long long e = i + (unsigned long long)k * nt;
+      if (e < ws.words && slot_of_job(v[k], g))
+        __hip_atomic_store(ws.base + e, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
 
 // Polling the tagged partial sums of batch row b for the chunks
 // c = w + 16 u < Sm of this wave (element t = lane + 64 j, as

@@ -79,14 +79,15 @@ int cu_count() {
   return cached[dev];
 }
 
-// The first 256 bytes of every workspace hold the epoch of the kernels with
-// tagged partial sums (the tag of the last such launch; zero before the
-// first call).  With the tiled layout the next regions hold the one-launch
-// kernel's tagged partial sums (8 bytes per slot, up to two rows) and tagged
-// chunk transforms (its two-level output transform), and the last region the
-// 16-row decode-matvec's tagged partial sums; each is written by its kernel
-// only, so a slot can only carry a tag of an earlier launch of the same
-// workspace.
+// The first 256 bytes of every workspace hold the epoch words of the kernels
+// with tagged partial sums (per job index, the tag of the last such launch;
+// zero before the first call) and their wrap words (qs_tags.h).  With the
+// tiled layout the next regions hold the one-launch kernel's tagged partial
+// sums (8 bytes per slot, up to two rows) and tagged chunk transforms (its
+// two-level output transform), and the last region the 16-row
+// decode-matvec's tagged partial sums; each is written by its kernel only, so
+// a slot can only carry a tag of an earlier launch of the same workspace, and
+// those of 2^20 - 1 launches earlier are cleared when the counter wraps.
 WsLayout ws_layout(int64_t m, int64_t n, int64_t batch, int layout) {
   WsLayout L{};
   L.wide = layout == QS_LAYOUT_TILED && batch >= kWideMinBatch;
@@ -732,7 +733,7 @@ static int forward_batched(const void* x, int x_dtype, int64_t ldx, int64_t batc
                     const void* codes0, const void* codes1, int kind1, int layout, const float* sv, const float* su,
                     int kron_pn, const float* kron_n, int kron_pm, const float* kron_m, float s0, float s1,
                     float layer_scale, const float* bias, void* y, int y_dtype, int64_t ldy, char* ws,
-                    const WsLayout& W, void* mv_begin, void* mv_end, hipStream_t s, bool identity,
+                    size_t ws_bytes, const WsLayout& W, void* mv_begin, void* mv_end, hipStream_t s, bool identity,
                     int sbits = 0) {
   int rc = QS_OK;
   if (!identity && W.wide)
@@ -781,6 +782,7 @@ static int forward_batched(const void* x, int x_dtype, int64_t ldx, int64_t batc
       if (!identity && batched_eligible(n, kron_pn, m, kron_pm) && sv_aligned) {
         P.y1t = reinterpret_cast<unsigned long long*>(ws + W.y1bt);  // output transform in the decode-matvec
         P.epoch = reinterpret_cast<unsigned*>(ws);
+        P.tw = tag_ws(ws, ws_bytes, 0);
         rc = launch_linear_batched(P, s, ev0, ev1);
       } else {
         if (!identity && chunk_transform_fits(n, kron_pn) && sv_aligned)
@@ -941,6 +943,7 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
     d.y = y;
     d.ldy = ldy;
     d.epoch = reinterpret_cast<unsigned*>(ws);
+    d.tw = tag_ws(ws, workspace_bytes, 0);
     d.xmul = reinterpret_cast<float*>(ws + W.xmul);
     d.y1p = reinterpret_cast<float*>(ws + W.y1p);
     d.y1t = reinterpret_cast<unsigned long long*>(ws + W.y1t);
@@ -959,8 +962,8 @@ extern "C" int qs_linear_forward(const void* x, int x_dtype, int64_t ldx, int64_
                             bias, y, y_dtype, ldy, s);
   }
   return forward_batched(x, x_dtype, ldx, batch, n, m, codes0, codes1, kind1, layout, sv, su, kron_pn, kron_n,
-                         kron_pm, kron_m, s0, s1, layer_scale, bias, y, y_dtype, ldy, ws, W, mv_begin, mv_end, s,
-                         false, sbits);
+                         kron_pm, kron_m, s0, s1, layer_scale, bias, y, y_dtype, ldy, ws, workspace_bytes, W, mv_begin,
+                         mv_end, s, false, sbits);
 }
 
 // ---------------------------------------------------------------------------
@@ -1059,7 +1062,7 @@ size_t group_prefix_bytes(int count, int64_t n, M m_of) {
 // group's, so the outputs equal separate calls up to the fp32 summation order.
 static int forward_group_rows(const void* x, int x_dtype, int64_t ldx, int64_t batch, int64_t n, int kron_pn,
                               const float* kron_n, int count, const qs_linear_job* jobs, int y_dtype, char* ws,
-                              void* mv_begin, void* mv_end, hipStream_t s, int sbits) {
+                              size_t ws_bytes, void* mv_begin, void* mv_end, hipStream_t s, int sbits) {
   const bool wide = batch >= kWideMinBatch;
   BatchedPass P[QS_MAX_GROUP];
   size_t off = group_prefix_bytes(count, n, [&](int g) { return jobs[g].m; });
@@ -1102,6 +1105,7 @@ static int forward_group_rows(const void* x, int x_dtype, int64_t ldx, int64_t b
     if (!wide) {
       Q.y1t = reinterpret_cast<unsigned long long*>(ws + off + W.y1bt);
       Q.epoch = reinterpret_cast<unsigned*>(ws) + g;
+      Q.tw = tag_ws(ws, ws_bytes, g);
     }
     off += W.total;
   }
@@ -1222,21 +1226,19 @@ extern "C" int qs_linear_forward_group(const void* x, int x_dtype, int64_t ldx, 
   hipStream_t s = as_stream(stream);
   char* ws = static_cast<char*>(workspace);
   if (!one_launch && chunk_transform_fits(n, kron_pn))
-    return forward_group_rows(x, x_dtype, ldx, batch, n, kron_pn, kron_n, count, jobs, y_dtype, ws, mv_begin, mv_end,
-                              s, jobs[0].sign_bits ? 1 : 0);
+    return forward_group_rows(x, x_dtype, ldx, batch, n, kron_pn, kron_n, count, jobs, y_dtype, ws, workspace_bytes,
+                              mv_begin, mv_end, s, jobs[0].sign_bits ? 1 : 0);
   if (!one_launch) {
     // n outside the chunk scheme of the multi-row kernels: one forward per
-    // linear, each in its own region after the one-launch blocks
-    size_t off = group_prefix_bytes(count, n, [&](int g) { return jobs[g].m; });
+    // linear, one after the other on the stream, each with the whole
+    // workspace (so that its tags continue the workspace's epoch of job 0)
     for (int g = 0; g < count; ++g) {
       const qs_linear_job& j = jobs[g];
-      const size_t bytes = ws_layout(j.m, n, batch, QS_LAYOUT_TILED).total;
       rc = qs_linear_forward(x, x_dtype, ldx, batch, n, j.m, j.codes0, j.codes1, QS_STAGE_E8_1BIT,
                              QS_LAYOUT_TILED | (j.sign_bits ? QS_SIGNS_BITS : 0), j.sv, j.su, kron_pn, kron_n,
-                             j.kron_pm, j.kron_m, j.s0, j.s1, j.layer_scale, j.bias, j.y, y_dtype, j.ldy, ws + off,
-                             bytes, g == 0 ? mv_begin : nullptr, g == count - 1 ? mv_end : nullptr, stream);
+                             j.kron_pm, j.kron_m, j.s0, j.s1, j.layer_scale, j.bias, j.y, y_dtype, j.ldy, workspace,
+                             workspace_bytes, g == 0 ? mv_begin : nullptr, g == count - 1 ? mv_end : nullptr, stream);
       if (rc) return rc;
-      off += bytes;
     }
     return QS_OK;
   }
@@ -1261,6 +1263,7 @@ extern "C" int qs_linear_forward_group(const void* x, int x_dtype, int64_t ldx, 
     d[g].y = j.y;
     d[g].ldy = j.ldy;
     d[g].epoch = reinterpret_cast<unsigned*>(ws) + g;
+    d[g].tw = tag_ws(ws, workspace_bytes, g);
     d[g].xmul = reinterpret_cast<float*>(ws + off + F.xmul);
     d[g].y1p = reinterpret_cast<float*>(ws + off + F.y1p);
     d[g].y1t = reinterpret_cast<unsigned long long*>(ws + off + F.y1t);
@@ -1318,6 +1321,6 @@ extern "C" int qs_decode_matvec(const void* x, int x_dtype, int64_t ldx, int64_t
                    (!codes1 || (reinterpret_cast<uintptr_t>(codes1) & 7) == 0),
                "packed codes must be 16-byte aligned");
   return forward_batched(x, x_dtype, ldx, batch, n, m, codes0, codes1, kind1, layout, nullptr, nullptr, 1, nullptr, 1,
-                         nullptr, s0, s1, layer_scale, nullptr, y, y_dtype, ldy, static_cast<char*>(workspace), W,
-                         nullptr, nullptr, as_stream(stream), true);
+                         nullptr, s0, s1, layer_scale, nullptr, y, y_dtype, ldy, static_cast<char*>(workspace),
+                         workspace_bytes, W, nullptr, nullptr, as_stream(stream), true);
 }

@@ -206,6 +206,10 @@ struct BmArgs {
   int y_dtype;      // tail instantiations: output dtype
   int njobs;
   BmJob job[QS_MAX_GROUP];
+  // tail instantiations: the workspace (its tags are cleared when a job's
+  // counter wraps); after the jobs so that their fields keep their offsets
+  unsigned long long* ws;
+  unsigned long long ws_words;
 };
 
 constexpr int kBmSlots = 4;                  // row blocks reduced together (2: 0.6 % slower at 16 rows)
@@ -443,9 +447,9 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
         out[a][j] = apply_su(acc[a][j] * mul, suo[a][j], SB, oidx[a][j]) + (has_bias ? bio[a][j] : 0.0f);
     store_outputs(J.y, A.y_dtype, (int64_t)b * J.ldy, oidx, out);
     // every slot of row b has been read, so every work-group of the linear has
-    // read the epoch: the next launch's tag follows this one (all the tail
-    // work-groups store the same value)
-    if (tid == 0) __hip_atomic_store(J.epoch, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // read the epoch: the next launch's tag follows this one
+    finish_tagged_launch(J.epoch, tag, g, TagWs{J.epoch + kWrapWord, A.ws, A.ws_words, A.B},
+                         reinterpret_cast<int*>(lds));  // the tails: work-groups b < B
   }
 }
 
@@ -805,6 +809,12 @@ int launch_bm_group(const BatchedPass* P, int count, hipStream_t stream, hipEven
       BmJob& J = M.job[j];
       J.y1t = Q.y1t;
       J.epoch = Q.epoch;
+      // the wrap word sits kWrapWord words past the epoch word, in one
+      // workspace for every linear of the launch
+      QS_REQUIRE(Q.tw.wrap == Q.epoch + kWrapWord, "linear %d: wrap word not beside the epoch", j);
+      QS_REQUIRE(j == 0 || (Q.tw.base == M.ws && Q.tw.words == M.ws_words), "linear %d: another workspace", j);
+      M.ws = Q.tw.base;
+      M.ws_words = Q.tw.words;
       J.xmul = Q.xmul;
       J.Sm = (int)(Q.m / 256);
       J.lsh_m = log2_exact((int)(Q.m / Q.pm / 256));
@@ -827,7 +837,8 @@ int launch_bm_group(const BatchedPass* P, int count, hipStream_t stream, hipEven
 
 bool bm_tail_eligible(const BatchedPass* P, int count) {
   for (int j = 0; j < count; ++j)
-    if (!P[j].y1t || !P[j].epoch || P[j].B > kTB || !chunk_transform_fits(P[j].m, P[j].pm) ||
+    if (!P[j].y1t || !P[j].epoch || !P[j].tw.wrap || !P[j].tw.base || P[j].tw.words <= kWsHeaderWords ||
+        P[j].B > kTB || !chunk_transform_fits(P[j].m, P[j].pm) ||
         P[j].y_dtype != P[0].y_dtype || P[j].sbits != P[0].sbits)
       return false;
   return count >= 1;

@@ -3,6 +3,7 @@
 #pragma once
 
 #include "qs_common.h"
+#include "qs_tags.h"
 
 namespace qs {
 
@@ -20,6 +21,7 @@ struct FusedJobDesc {
   void* y;
   int64_t ldy;
   unsigned* epoch;      // workspace: tag of the last launch's partial sums (zero before the first call)
+  TagWs tw;             // workspace: wrap word and extent (tag_ws; ntail set by the launcher)
   float* xmul;          // workspace: [B] activation scales
   float* y1p;           // workspace: [SG][B][m] fp32 partial sums (output transform in a separate kernel)
   unsigned long long* y1t;  // workspace: [SG][B][m] tagged partial sums (output transform in the kernel)
@@ -71,6 +73,7 @@ struct BatchedPass {
   unsigned long long* y1t;  // workspace: [SG][B][m] tagged slots, or null: with them the decode-matvec
                             // applies the output transform itself (bm_tail_eligible)
   unsigned* epoch;       // the epoch word of the linear's tags (with y1t)
+  TagWs tw;              // the linear's wrap word and the workspace (tag_ws; with y1t)
 };
 bool batched_eligible(int64_t n, int pn, int64_t m, int pm);
 // The decode-matvec of these linears may also apply their output transforms

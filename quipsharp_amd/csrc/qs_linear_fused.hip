@@ -72,6 +72,7 @@ struct FusedJob {
   const uint8_t* codes1;
   int m, Gr, wg0;      // rows; row-block stride; first work-group of this linear
   float s0, s1;
+  int ntail;           // tail work-groups (output transform here; fills the alignment gap before y1p)
   float* y1p;          // [SG][B][m] fp32 partials (output transform in a separate kernel)
   unsigned long long* y1t;  // [SG][B][m] tagged partials (output transform here)
   unsigned long long* h2t;  // [B][m] tagged chunk transforms (two-level output transform)
@@ -100,6 +101,10 @@ struct FusedArgs {
   int sbits;  // su, sv of every job are packed sign bits
   int njobs;
   FusedJob job[kMaxJobs];
+  // the workspace (its tags are cleared when a job's counter wraps); after
+  // the jobs so that their fields keep the offsets the kernel loads them from
+  unsigned long long* ws;
+  unsigned long long ws_words;
 };
 
 // LDS layout (bytes).  The slice rows of the input transform alias the
@@ -834,10 +839,10 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
       }
     }
   }
-  // every slot of this launch has been read (by this work-group; all the
-  // tail work-groups store the same value): the next launch's tag follows
-  // this one
-  if (tid == 0) __hip_atomic_store(J.epoch, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // every slot this work-group polls has been read: the next launch's tag
+  // follows this one
+  finish_tagged_launch(J.epoch, tag, g, TagWs{J.epoch + kWrapWord, A.ws, A.ws_words, J.ntail},
+                       reinterpret_cast<int*>(lds));
 }
 
 }  // namespace
@@ -942,6 +947,16 @@ int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, i
     if (J.out_in_kernel) {
       J.Sm = (int)(d.m / 256);
       J.lsh_m = log2_exact(d.m / d.pm / 256);
+      // tail work-groups: the first one (m <= 4096), else the first
+      // kL2Groups (or all, if fewer)
+      J.ntail = J.Sm <= kWaves ? 1 : (Gr * SG < kL2Groups ? Gr * SG : kL2Groups);
+      // the wrap word sits kWrapWord words past the epoch word, in one
+      // workspace for every job of the launch
+      QS_REQUIRE(d.tw.wrap == d.epoch + kWrapWord && d.tw.base && d.tw.words > kWsHeaderWords,
+                 "job %d: no workspace for the tags", g);
+      QS_REQUIRE(!A.ws || (A.ws == d.tw.base && A.ws_words == d.tw.words), "job %d: another workspace", g);
+      A.ws = d.tw.base;
+      A.ws_words = d.tw.words;
     }
     J.pm = d.pm;
     J.Km = d.Km;

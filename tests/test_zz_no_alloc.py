@@ -60,6 +60,7 @@ def _noalloc(L, x, y=None):
     [(11008, 4096, 2, True, True), (4096, 11008, 1, True, False)],       # odd-factor output / input
     [(4096, 4096, 24, True, False), (4096, 4096, 5, False, True), (512, 1024, 2, True, True)],
     [(14336, 4096, 8, False, False), (4096, 4096, 2, True, False)],      # m off the chunk scheme
+    [(25600, 5120, 16, False, True), (25600, 5120, 8, False, False), (5120, 25600, 1, False, False)],  # Qwen3-32B MLP
 ])
 def test_noalloc_equals_workspace_forward(dev, calls):
     for i, (m, n, rows, bits, bias) in enumerate(calls):
@@ -99,13 +100,13 @@ def test_noalloc_graph_replays(dev):
         torch.cuda.synchronize()
 
 
-def test_noalloc_rejects_oversized(dev):
-    """A shape whose workspace exceeds the array: QS_ERR_UNSUPPORTED on the
-    host, nothing launched, the output untouched."""
+@pytest.mark.parametrize("m,n,rows", [(12288, 12288, 512), (25600, 25600, 16)])
+def test_noalloc_rejects_oversized(dev, m, n, rows):
+    """A shape whose workspace exceeds the array (a wide prefill batch; a
+    decode batch of the widest layers): QS_ERR_UNSUPPORTED on the host,
+    nothing launched, the output untouched."""
     from quipsharp_amd import _lib
     lib = _lib.lib()
-    m = n = 12288
-    rows = 512
     need = lib.qs_linear_workspace_bytes(m, n, rows, _lib.QS_LAYOUT_TILED)
     assert need > _lib.QS_NOALLOC_SCRATCH_BYTES
     L = _linear(dev, m, n, 9, False, False)
