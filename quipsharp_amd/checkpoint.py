@@ -12,6 +12,7 @@ and write the reference's format (state dict + manifest).
 """
 import ctypes
 import json
+import warnings
 import weakref
 from pathlib import Path
 
@@ -138,6 +139,11 @@ class QuantizedLinear(nn.Module):
         # assignment can reuse a freed block's address
         key = (id(self.codes), self.codes.data_ptr(), self.codes._version, self.codes.device, tuple(kinds))
         if self._packed is None or self._packed_key != key:
+            if self.codes.is_cuda and torch.cuda.is_current_stream_capturing():
+                raise RuntimeError(
+                    "QuantizedLinear: the first forward after the module is built, moved, cast or loaded packs "
+                    "the codes and reads the scale on the host, which HIP graph capture does not allow: run one "
+                    "forward outside capture first")
             self._packed = PackedCodes(self.codes, self.out_features, self.in_features, kinds)
             self._packed_key = key
             self._scale_f = float(self.scale.item())
@@ -148,7 +154,9 @@ class QuantizedLinear(nn.Module):
         ``.to(torch.bfloat16)`` su / sv / bias keep the module's dtype, as in the
         reference, whose forward promotes them to fp32 at use
         (quipsharp/checkpoint.py:141-146); the fp32 copy is made once per buffer
-        version."""
+        version.  Under HIP graph capture a missing copy is made uncached: made
+        there, it would live in the graph's pool and only be written on replay,
+        so an eager call before the first replay would read unwritten memory."""
         t = getattr(self, name)
         if t is None or t.dtype == torch.float32:
             return t
@@ -156,6 +164,8 @@ class QuantizedLinear(nn.Module):
         key = (id(t), t.data_ptr(), t._version, t.dtype)
         hit = cache.get(name)
         if hit is None or hit[0] != key:
+            if t.is_cuda and torch.cuda.is_current_stream_capturing():
+                return t.float().contiguous()
             hit = (key, t.float().contiguous())
             cache[name] = hit
         return hit[1]
@@ -392,6 +402,35 @@ def install_quantized_placeholders(model: nn.Module, manifest: dict) -> None:
         setattr(parent, attr, qlin)
 
 
+def checkpoint_placement(total_bytes, device="cuda", gpu_devices=None, gpu_budget_bytes=None,
+                         cpu_budget_bytes=0):
+    """The device a checkpoint of ``total_bytes`` loads onto, and a warning
+    (or None).  The reference (quipsharp/checkpoint.py:228-263) puts
+    everything on ``gpu_devices[0]`` (else ``device``) when it fits
+    ``gpu_budget_bytes``, and otherwise bin-packs the decoder layers over
+    ``gpu_devices``, then the CPU when ``cpu_budget_bytes`` is nonzero, the
+    last device taking what is left.  Here the forward runs on one GPU and has
+    no CPU path: with one GPU listed the whole model goes on it (with no CPU
+    budget that is where the reference's packing ends as well; with one, the
+    layers it would have put on the CPU stay on the GPU, and the warning says
+    so); with several GPUs listed and a checkpoint above the budget,
+    NotImplementedError names the two ways out (one device, or a larger
+    budget: an MI355X holds 288 GB)."""
+    if gpu_devices is None or gpu_budget_bytes is None or total_bytes <= gpu_budget_bytes:
+        return (gpu_devices[0] if gpu_devices else device), None
+    gpus = list(gpu_devices)
+    if len(gpus) == 1:
+        where = (" (the reference would put the layers past the budget on the CPU; the forward here runs on the "
+                 "GPU only)") if cpu_budget_bytes else ""
+        return gpus[0], (f"the checkpoint holds {total_bytes} bytes, more than gpu_budget_bytes={gpu_budget_bytes}: "
+                         f"all of it goes on {gpus[0]}{where}")
+    raise NotImplementedError(
+        f"the checkpoint holds {total_bytes} bytes, more than gpu_budget_bytes={gpu_budget_bytes}, and "
+        f"{len(gpus)} devices are listed: spreading layers over several devices (accelerate.dispatch_model in the "
+        "reference) is not implemented; pass one device in gpu_devices, or a gpu_budget_bytes of at least the "
+        "checkpoint's size")
+
+
 def load_quantized_checkpoint(save_path, device="cuda", gpu_devices=None, gpu_budget_bytes=None,
                               cpu_budget_bytes=0, model: nn.Module = None) -> nn.Module:
     """quipsharp/checkpoint.py:193-275, same call (quipsharp/model_loading.py:57
@@ -403,24 +442,19 @@ def load_quantized_checkpoint(save_path, device="cuda", gpu_devices=None, gpu_bu
     dict is loaded with ``assign=True`` through ``torch.load(weights_only=True)``
     (tensors only, nothing executed from the file), the model moves to
     ``gpu_devices[0]`` (or ``device``) and each QuantizedLinear gets the
-    codebook rebuilt from the manifest's bits and seed.  A checkpoint larger
-    than ``gpu_budget_bytes``, which the reference spreads over several devices
-    with accelerate, raises NotImplementedError: this library runs on one GPU."""
+    codebook rebuilt from the manifest's bits and seed.  Placement for a
+    checkpoint larger than ``gpu_budget_bytes``: see ``checkpoint_placement``."""
     save_path = Path(save_path)
     manifest = json.loads((save_path / MANIFEST_NAME).read_text())
     state = torch.load(save_path / STATE_NAME, map_location="cpu", weights_only=True)
     total_bytes = sum(t.numel() * t.element_size() for t in state.values())
-    fits_one_device = gpu_devices is None or gpu_budget_bytes is None or total_bytes <= gpu_budget_bytes
-    if not fits_one_device:
-        raise NotImplementedError(
-            f"the checkpoint holds {total_bytes} bytes, more than gpu_budget_bytes={gpu_budget_bytes}: spreading "
-            "layers over several devices (accelerate.dispatch_model in the reference) is not implemented; this "
-            "library runs on one GPU")
+    device, note = checkpoint_placement(total_bytes, device, gpu_devices, gpu_budget_bytes, cpu_budget_bytes)
+    if note:
+        warnings.warn(note, stacklevel=2)
     if model is None:
         model = build_meta_model(manifest["model_id"], save_path)
     install_quantized_placeholders(model, manifest)
     model.load_state_dict(state, strict=True, assign=True)
-    device = gpu_devices[0] if gpu_devices else device
     model.to(device)
     codebook, _ = build_codebook(manifest["bits"], device, manifest["seed"])
     for info in manifest["quantized_modules"]:

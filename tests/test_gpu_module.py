@@ -7,6 +7,7 @@
   forward promotes signs and bias to fp32 and reads the rounded scale.
 * Linears grouped by the library whose signs cannot all be packed bits (an
   output size off the chunk scheme) still run, eagerly and under capture.
+* A buffer changed in place and next used under HIP graph capture.
 * ``replace_with_quantized_linear_`` (quipsharp/checkpoint.py:149-156)."""
 import copy
 
@@ -120,6 +121,37 @@ def test_linked_mixed_group_under_capture(dev, B):
         assert torch.equal(ya, want_a) and torch.equal(yb, want_b)
         a(x)                # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_changed_buffer_first_used_under_capture(dev):
+    """A bf16 module whose bias changed in place after its last forward, next
+    called under HIP graph capture: the fp32 copy of the bias is made uncached
+    there (cached, it would live in the graph's pool, unwritten until a
+    replay), so an eager call before the first replay, and every replay,
+    equal a copy of the module run eagerly.  A forward that would have to pack
+    the codes (the first after a cast) refuses capture with a clear error."""
+    q = _qlin(dev, 4096, 4096, 31, bias=True).bfloat16()
+    x = torch.randn(2, 4096, generator=torch.Generator().manual_seed(3)).to(dev).bfloat16()
+    q(x)                    # workspace, packed codes and signs, fp32 copies
+    torch.cuda.synchronize()
+    with torch.no_grad():
+        q.bias.add_(0.5)    # a new version of the bias
+    want = copy.deepcopy(q)(x).clone()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y = q(x)
+    got = q(x)              # eager, before any replay
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    for _ in range(2):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, want)
+    q2 = _qlin(dev, 4096, 4096, 32).half()
+    with pytest.raises(RuntimeError, match="run one forward outside capture first"):
+        with torch.cuda.graph(torch.cuda.CUDAGraph()):
+            q2(x.half())
 
 
 def test_replace_with_quantized_linear(dev):

@@ -74,3 +74,21 @@ def test_linear_args_accepts_fp32_and_bits():
 def test_linear_args_rejects(bad, msg):
     with pytest.raises(ValueError, match=msg):
         check_linear_args(**_args(**bad))
+
+
+def test_checkpoint_placement():
+    """Where a checkpoint loads (quipsharp/checkpoint.py:228-263 places it on
+    gpu_devices[0] when it fits the budget): one GPU listed and over the budget
+    -> still that GPU, with a warning (naming the CPU share the reference
+    would have offloaded when cpu_budget_bytes is set); several GPUs over the
+    budget -> NotImplementedError that names the ways out."""
+    from quipsharp_amd.checkpoint import checkpoint_placement
+    assert checkpoint_placement(10, "cuda:3") == ("cuda:3", None)
+    assert checkpoint_placement(10, "cpu", ["cuda:1"], None) == ("cuda:1", None)
+    assert checkpoint_placement(10, "cpu", ["cuda:1", "cuda:2"], 10) == ("cuda:1", None)
+    dev, note = checkpoint_placement(26 << 30, "cpu", ["cuda:0"], 20 << 30, 0)
+    assert dev == "cuda:0" and "all of it goes on cuda:0" in note and "CPU" not in note
+    dev, note = checkpoint_placement(26 << 30, "cpu", ["cuda:0"], 20 << 30, 60 << 30)
+    assert dev == "cuda:0" and "on the CPU" in note
+    with pytest.raises(NotImplementedError, match="pass one device"):
+        checkpoint_placement(26 << 30, "cpu", ["cuda:0", "cuda:1"], 20 << 30, 60 << 30)
