@@ -14,26 +14,43 @@ from pathlib import Path
 from .checkpoint import is_quantized_checkpoint, load_quantized_checkpoint
 
 
+_GIB = 1 << 30
+
+
+def _gib(arg) -> int:
+    return int(float(arg) * _GIB)
+
+
 def resolve_gpu_budget_bytes(arg, headroom_frac: float = 0.15) -> int:
-    """quipsharp/model_loading.py:12-22: a number is taken as GB; "auto" is
-    the free memory of the least-free visible device minus ``headroom_frac``
-    of its total."""
+    """quipsharp/model_loading.py:12-22 (same meaning): a number is a size in
+    GiB; "auto" is what the tightest visible GPU can still take -- its free
+    bytes less ``headroom_frac`` of its capacity (0 with no GPU)."""
     if arg != "auto":
-        return int(float(arg) * 1024 ** 3)
+        return _gib(arg)
     import torch
-    budgets = [free - int(headroom_frac * total)
-               for free, total in (torch.cuda.mem_get_info(i) for i in range(torch.cuda.device_count()))]
-    return min(budgets) if budgets else 0
+    best = None
+    for dev in range(torch.cuda.device_count()):
+        free, capacity = torch.cuda.mem_get_info(dev)
+        room = free - int(capacity * headroom_frac)
+        best = room if best is None else min(best, room)
+    return best or 0
+
+
+def _host_available_bytes() -> int:
+    """MemAvailable of /proc/meminfo, in bytes."""
+    for line in Path("/proc/meminfo").read_text().splitlines():
+        key, _, rest = line.partition(":")
+        if key == "MemAvailable":
+            return int(rest.split()[0]) * 1024
+    raise RuntimeError("/proc/meminfo has no MemAvailable line")
 
 
 def resolve_cpu_budget_bytes(arg, use_frac: float = 0.8) -> int:
-    """quipsharp/model_loading.py:25-33: a number is taken as GB; "auto" is
-    ``use_frac`` of the available host memory (MemAvailable)."""
+    """quipsharp/model_loading.py:25-33 (same meaning): a number is a size in
+    GiB; "auto" is ``use_frac`` of the host memory available now."""
     if arg != "auto":
-        return int(float(arg) * 1024 ** 3)
-    with open("/proc/meminfo") as f:
-        avail_kb = next(int(line.split()[1]) for line in f if line.startswith("MemAvailable"))
-    return int(avail_kb * 1024 * use_frac)
+        return _gib(arg)
+    return int(_host_available_bytes() * use_frac)
 
 
 def load_eval_model(model_id_or_path: str, gpu_devices=("cuda:0",), gpu_budget_bytes: int = 20 * 1024 ** 3,

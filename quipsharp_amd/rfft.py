@@ -30,7 +30,7 @@ def random_phase(n_half: int, device=None, generator=None) -> Tensor:
 
 def _enter(x: Tensor, phase: Tensor) -> Tensor:
     n = x.shape[-1]
-    assert n == 2 * phase.shape[-1], f"expected last dim {2 * phase.shape[-1]}, got {n}"
+    assert n == 2 * phase.shape[-1], f"{phase.shape[-1]} phases pair {2 * phase.shape[-1]} values per row; the rows have {n}"
     shape = x.shape
     xc = torch.view_as_complex(x.reshape(*shape[:-1], n // 2, 2).contiguous())
     return torch.view_as_real(torch.fft.fft(xc * phase, norm="ortho")).reshape(shape)
@@ -38,7 +38,7 @@ def _enter(x: Tensor, phase: Tensor) -> Tensor:
 
 def _exit(y: Tensor, phase: Tensor) -> Tensor:
     n = y.shape[-1]
-    assert n == 2 * phase.shape[-1], f"expected last dim {2 * phase.shape[-1]}, got {n}"
+    assert n == 2 * phase.shape[-1], f"{phase.shape[-1]} phases pair {2 * phase.shape[-1]} values per row; the rows have {n}"
     shape = y.shape
     yc = torch.view_as_complex(y.reshape(*shape[:-1], n // 2, 2).contiguous())
     return torch.view_as_real(torch.fft.ifft(yc, norm="ortho") * torch.conj(phase)).reshape(shape)
@@ -77,8 +77,8 @@ def rfft_incoherence_process(W: Tensor, H: Tensor, generator=None):
     """quipsharp/rfft.py:80-95 (Algorithm 4): W_hat, H_hat and the phases.
     Phase draw order u then v, as the reference."""
     m, n = W.shape
-    assert m % 2 == 0 and n % 2 == 0, "RFFT incoherence processing requires even dimensions"
-    assert H.shape == (n, n)
+    assert m % 2 == 0 and n % 2 == 0, f"the FFT pairs neighbouring entries: {m} x {n} has an odd side"
+    assert H.shape == (n, n), f"H is {tuple(H.shape)}, W has {n} columns"
     phase_u = random_phase(m // 2, device=W.device, generator=generator)
     phase_v = random_phase(n // 2, device=W.device, generator=generator)
     what = to_transformed_space(to_transformed_space(W, phase_u, dim=0), phase_v, dim=1)

@@ -55,8 +55,9 @@ def test_reference_checkpoint_keys_match():
 
 
 def test_multi_device_split_refused():
-    """A checkpoint above gpu_budget_bytes (the reference spreads it over
-    devices with accelerate) is refused before anything is placed."""
+    """A checkpoint above gpu_budget_bytes with several GPUs listed (the
+    reference spreads it over them with accelerate) is refused before anything
+    is placed; with one GPU listed it would go there whole (a warning)."""
     from quipsharp_amd.checkpoint import load_quantized_checkpoint
-    with pytest.raises(NotImplementedError, match="one GPU"):
+    with pytest.raises(NotImplementedError, match="pass one device"):
         load_quantized_checkpoint(CKPT, device="cuda:0", gpu_devices=["cuda:0", "cuda:1"], gpu_budget_bytes=1)
