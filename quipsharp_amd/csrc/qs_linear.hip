@@ -793,8 +793,18 @@ static int forward_batched(const void* x, int x_dtype, int64_t ldx, int64_t batc
         else
           rc = launch_xin_rows(P.x, x_dtype, ldx, P.B, n, kron_pn, kron_n, sv, P.x2h, P.sg,
                                reinterpret_cast<float*>(ws + W.xtot), P.xmul, P.frag, s, identity);
-        if (!rc) rc = launch_bm(P, s, ev0, ev1);
-        if (!rc && !identity && chunk_transform_fits(m, kron_pm))
+        // m on the chunk scheme: the decode-matvec applies the output
+        // transform itself where it can (tagged slots), whatever n
+        bool tail = false;
+        if (!identity && chunk_transform_fits(m, kron_pm)) {
+          P.y1t = reinterpret_cast<unsigned long long*>(ws + W.y1bt);
+          P.epoch = reinterpret_cast<unsigned*>(ws);
+          P.tw = tag_ws(ws, ws_bytes, 0);
+        }
+        if (!rc) rc = launch_bm(P, s, ev0, ev1, &tail);
+        if (!rc && tail) {
+          // done in the decode-matvec
+        } else if (!rc && !identity && chunk_transform_fits(m, kron_pm))
           rc = launch_by_rows(P, s);
         else if (!rc && !identity && big_transform_fits(m, kron_pm))
           rc = launch_by_big(&P, 1, s);

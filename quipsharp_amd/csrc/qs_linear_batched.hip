@@ -486,7 +486,8 @@ struct ByArgs {
 // sums any number of groups one at a time.  A linear with fewer groups than G
 // adds zeros.  CPW: chunks per wave, as bx_kernel.
 template <int G, int CPW, bool SB>
-__global__ __launch_bounds__(kThreads) void by_kernel(ByArgs A) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(CPW == 1 ? 8 : 1)))
+void by_kernel(ByArgs A) {
   using L = RowLds<CPW>;
   extern __shared__ __attribute__((aligned(16))) char lds[];
   float* Y = reinterpret_cast<float*>(lds + L::kY);
@@ -512,7 +513,11 @@ __global__ __launch_bounds__(kThreads) void by_kernel(ByArgs A) {
   mmat_load(kmv, Sm, J.lsh_m, J.pm, J.Km, tid);
   PRaw<1, CPW> pr;
   if constexpr (G == 1) load_partials_raw<false, 1>(J.y1p, J.m, Sm, J.SG, A.B, lb, w, lane, pr);
-  int oidx[CPW][4];
+  // output element of out[a][j] (-1: none), recomputed where it is used
+  auto out_index = [&](int a, int j) {
+    const int r = 16 * a + 4 * q + j;
+    return r < Sm ? 256 * r + t : -1;
+  };
   float suo[CPW][4], bio[CPW][4];
   // no bias: a dummy load from the partial sums (at least m floats; su may
   // be m / 32 words of sign bits), never used: the bias term is selected,
@@ -523,9 +528,8 @@ __global__ __launch_bounds__(kThreads) void by_kernel(ByArgs A) {
   for (int a = 0; a < CPW; ++a)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int r = 16 * a + 4 * q + j;
-      oidx[a][j] = r < Sm ? 256 * r + t : -1;
-      const int ii = oidx[a][j] >= 0 ? oidx[a][j] : 0;
+      const int oi = out_index(a, j);
+      const int ii = oi >= 0 ? oi : 0;
       suo[a][j] = load_su(J.su, SB, ii);
       bio[a][j] = bsrc[ii];
     }
@@ -557,11 +561,14 @@ __global__ __launch_bounds__(kThreads) void by_kernel(ByArgs A) {
         if (a < nrt) acc[a] = mstage_step(acc[a], Mh, Ml, 16 * a, z, kb, J.pm > 1, q, r16);
     }
     float out[CPW][4];
+    int oidx[CPW][4];
 #pragma unroll
     for (int a = 0; a < CPW; ++a)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < 4; ++j) {
+        oidx[a][j] = out_index(a, j);
         out[a][j] = apply_su(acc[a][j] * mul, suo[a][j], SB, oidx[a][j]) + (has_bias ? bio[a][j] : 0.0f);
+      }
     store_outputs(J.y, A.y_dtype, (int64_t)b * J.ldy, oidx, out);
     __syncthreads();  // Y is rewritten for the next row
   }
