@@ -5,6 +5,7 @@
 #pragma once
 
 #include "qs_chunk_dev.h"
+#include "qs_slots.h"
 #include "qs_tags.h"
 
 namespace qs {
@@ -397,11 +398,11 @@ __device__ __forceinline__ void load_partials_raw(const float* y1p, int m, int S
 #pragma unroll
       for (int j = 0; j < 4; ++j) r.v[g][u][j] = 0.0f;
       if (g < SG && c < Sm) {
-        const float* src = y1p + ((size_t)g * B + b) * m + 256 * c + lane;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          r.v[g][u][j] = ATOMIC ? __hip_atomic_load(src + 64 * j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                : src[64 * j];
+        for (int j = 0; j < 4; ++j) {
+          const float* src = y1p + partial_index(g, B, b, m, chunk_elem(c, lane, j));
+          r.v[g][u][j] = ATOMIC ? __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *src;
+        }
       }
     }
 }
@@ -431,10 +432,9 @@ __device__ __forceinline__ void sum_partials_loop(const float* y1p, int m, int S
     for (int u = 0; u < CPW; ++u) {
       const int c = w + kWaves * u;
       if (c < Sm) {
-        const float* src = y1p + ((size_t)g * B + b) * m + 256 * c + lane;
         float t[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) t[j] = src[64 * j];
+        for (int j = 0; j < 4; ++j) t[j] = y1p[partial_index(g, B, b, m, chunk_elem(c, lane, j))];
 #pragma unroll
         for (int j = 0; j < 4; ++j) zv[u][j] = g == 0 ? t[j] : zv[u][j] + t[j];
       }
@@ -530,14 +530,14 @@ __device__ __forceinline__ void poll_load(const unsigned long long* y1t, int m, 
 #pragma unroll
   for (int u = 0; u < CPW; ++u) {
     const int c = w + kWaves * u;
-    const unsigned long long* src = y1t + ((size_t)g * B + b) * m + 256 * c + lane;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+      const unsigned long long* src = y1t + partial_index(g, B, b, m, chunk_elem(c, lane, j));
       if (only_missing) {
         if ((uint32_t)(p.v[u][j] >> 32) != tag)
-          p.v[u][j] = __hip_atomic_load(src + 64 * j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          p.v[u][j] = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       } else {
-        p.v[u][j] = c < Sm ? __hip_atomic_load(src + 64 * j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : fill;
+        p.v[u][j] = c < Sm ? __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : fill;
       }
     }
   }

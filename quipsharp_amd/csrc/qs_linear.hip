@@ -22,6 +22,7 @@
 
 #include "qs_chunk_dev.h"
 #include "qs_linear_dev.h"
+#include "qs_slots.h"
 
 namespace qs {
 
@@ -98,8 +99,8 @@ WsLayout ws_layout(int64_t m, int64_t n, int64_t batch, int layout) {
     L.SG = (L.S + kMaxWaves - 1) / kMaxWaves;
     L.W = (L.S + L.SG - 1) / L.SG;
     L.fused = fused_plan(L.S);
-    L.y1t = off; off = align256(off + (size_t)L.fused.SG * 2 * m * 8);
-    L.h2t = off; off = align256(off + (size_t)2 * m * 8);
+    L.y1t = off; off = align256(off + fused_slot_count(L.fused.SG, m) * 8);
+    L.h2t = off; off = align256(off + h2_slot_count(m) * 8);
     const size_t xrows = (size_t)(B + 15) / 16 * 16;  // fragment-major rows: 16s
     L.x2h = off; off = align256(off + xrows * n * 2);
     L.sg = off; off = align256(off + xrows * (n / 8) * 2);
@@ -124,7 +125,7 @@ WsLayout ws_layout(int64_t m, int64_t n, int64_t batch, int layout) {
     if (layout == QS_LAYOUT_TILED) {
       // tagged partial sums of the 16-row decode-matvec that applies the
       // output transform itself (written by no other kernel)
-      L.y1bt = off; off = align256(off + (size_t)L.SG * B * m * 8);
+      L.y1bt = off; off = align256(off + batched_slot_count(L.SG, B, m) * 8);
     }
   }
   L.total = off;
@@ -1049,8 +1050,8 @@ FusedBlock fused_block(int64_t m, int64_t n) {
   const WsLayout W = ws_layout(m, n, 2, QS_LAYOUT_TILED);
   FusedBlock F{};
   F.y1t = 0;
-  F.h2t = F.y1t + align256((size_t)W.fused.SG * 2 * (size_t)m * 8);
-  F.xmul = F.h2t + align256((size_t)2 * (size_t)m * 8);
+  F.h2t = F.y1t + align256(fused_slot_count(W.fused.SG, m) * 8);
+  F.xmul = F.h2t + align256(h2_slot_count(m) * 8);
   F.y1p = F.xmul + 256;
   F.total = F.y1p + align256((size_t)W.fused.SG * 2 * (size_t)m * 4);
   return F;

@@ -379,7 +379,7 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
       if (tpo >= 16) v += lane_xor<8>(v, lx);
       if (o < nout && part == 0 && bc < A.B) {
         const int rbs = rb - (slot - s) * J.Gr;  // row block of slot s
-        const size_t idx = ((size_t)sg * A.B + bc) * J.m + rbs * 16 + row;
+        const size_t idx = partial_index(sg, A.B, bc, J.m, block_elem(rbs, row));
         if constexpr (OC > 0)
           __hip_atomic_store(&J.y1t[idx], tagged(v, tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         else
@@ -414,7 +414,7 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int r = 16 * a + 4 * q + j;
-        oidx[a][j] = r < Sm ? 256 * r + t : -1;
+        oidx[a][j] = r < Sm ? out_elem(r, t) : -1;
         const int ii = oidx[a][j] >= 0 ? oidx[a][j] : 0;
         suo[a][j] = load_su(J.su, SB, ii);
         bio[a][j] = at_off(bsrc, (uint32_t)ii);
@@ -516,7 +516,7 @@ void by_kernel(ByArgs A) {
   // output element of out[a][j] (-1: none), recomputed where it is used
   auto out_index = [&](int a, int j) {
     const int r = 16 * a + 4 * q + j;
-    return r < Sm ? 256 * r + t : -1;
+    return r < Sm ? out_elem(r, t) : -1;
   };
   float suo[CPW][4], bio[CPW][4];
   // no bias: a dummy load from the partial sums (at least m floats; su may

@@ -258,8 +258,8 @@ __global__ __launch_bounds__(kThreads) void by_big_kernel(ByBigArgs A) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int r = 16 * k + 4 * q + j;
-    oidx[0][j] = r < Sm ? 256 * r + t : -1;
-    const int ii = r < Sm ? 256 * r + t : 0;
+    oidx[0][j] = r < Sm ? out_elem(r, t) : -1;
+    const int ii = r < Sm ? out_elem(r, t) : 0;
     suo[j] = load_su(J.su, SB, ii);
     bio[j] = bsrc[ii];
   }

@@ -242,13 +242,13 @@ __device__ __forceinline__ bf16x8 lds_bf16x8(const uint16_t* p) {
   return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(p));
 }
 
-// Level 1 of the two-level output transform: h_c of one batch row as tagged
-// slots h2t[row][256 c + t], element t = lane + 64 j.
-__device__ __forceinline__ void store_h2(unsigned long long* h2t, int64_t row0, int c, int lane, uint32_t tag,
+// Level 1 of the two-level output transform: h_c of batch row b as tagged
+// slots h2t[b][256 c + t], element t = lane + 64 j.
+__device__ __forceinline__ void store_h2(unsigned long long* h2t, int b, int m, int c, int lane, uint32_t tag,
                                          const float (&z)[1][4]) {
 #pragma unroll
   for (int j = 0; j < 4; ++j)
-    __hip_atomic_store(h2t + row0 + 256 * c + lane + 64 * j, tagged(z[0][j], tag), __ATOMIC_RELAXED,
+    __hip_atomic_store(h2t + h2_index(b, m, chunk_elem(c, lane, j)), tagged(z[0][j], tag), __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
 }
 // Level 2: h[c][16 g + tt] of both batch rows, v = tid + 1024 k -> (c, tt) =
@@ -264,7 +264,7 @@ __device__ __forceinline__ void poll_columns(const unsigned long long* h2t, int 
 #pragma unroll
       for (int k = 0; k < 2; ++k) {
         const int v = tid + kThreads * k, c = v >> 4, tt = v & 15;
-        const unsigned long long* src = h2t + (int64_t)b * m + 256 * c + 16 * g + tt;
+        const unsigned long long* src = h2t + h2_index(b, m, column_elem(c, g, tt));
         if (only_missing) {
           if ((uint32_t)(p[b][k] >> 32) != tag)
             p[b][k] = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -614,7 +614,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
       if (tpo == 8) v += lane_xor<4>(v, lx);
       const int rbs = jr + (A.P * (step - (slot - s)) + p) * J.Gr;  // row block of slot s, phase p
       if (o < nout && part == 0 && rbs < RB) {
-        const size_t idx = ((size_t)sg * A.B + bc) * J.m + rbs * 16 + row;
+        const size_t idx = partial_index(sg, A.B, bc, J.m, block_elem(rbs, row));
         if (J.out_in_kernel)
           __hip_atomic_store(&J.y1t[idx], tagged(v, tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         else
@@ -659,7 +659,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int r = 16 * a + 4 * q + j;
-          const int ii = r < Sm ? 256 * r + t : 0;
+          const int ii = r < Sm ? out_elem(r, t) : 0;
           suo[a][j] = load_su(J.su, SB, ii);
           bio[a][j] = at_off(bsrc, (uint32_t)ii);
         }
@@ -703,7 +703,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int r = 16 * a + 4 * q + j;
-          oidx[a][j] = r < Sm ? 256 * r + t : -1;
+          oidx[a][j] = r < Sm ? out_elem(r, t) : -1;
           out[a][j] = apply_su(acc[a][j] * mul, suo[a][j], SB, oidx[a][j]) + (has_bias ? bio[a][j] : 0.0f);
         }
       store_outputs(yp, ydt, (int64_t)b * ldy, oidx, out);
@@ -735,11 +735,11 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
         float z[1][4];
         poll_finish(J.y1t, J.m, Sm, A.SG, A.B, 0, c, lane, tag, p0, z);
         h256<1>(z, lane, lx);
-        store_h2(J.h2t, 0, c, lane, tag, z);
+        store_h2(J.h2t, 0, J.m, c, lane, tag, z);
         if (A.B > 1) {
           poll_finish(J.y1t, J.m, Sm, A.SG, A.B, 1, c, lane, tag, p1, z);
           h256<1>(z, lane, lx);
-          store_h2(J.h2t, J.m, c, lane, tag, z);
+          store_h2(J.h2t, 1, J.m, c, lane, tag, z);
         }
       }
     }
@@ -788,7 +788,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int r = 16 * w + 4 * q + j;
-        const int i = (w < nl1 && r < Sm) ? 256 * r + t : 0;
+        const int i = (w < nl1 && r < Sm) ? out_elem(r, t) : 0;
         suo[j] = load_su(J.su, SB, i);
         bio[j] = at_off(bsrc, (uint32_t)i);
       }
@@ -829,7 +829,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int r = 16 * w + 4 * q + j;
-            oidx[0][j] = r < Sm ? 256 * r + t : -1;
+            oidx[0][j] = r < Sm ? out_elem(r, t) : -1;
             out[0][j] = apply_su(acc[j] * mul, suo[j], SB, oidx[0][j]) + (has_bias ? bio[j] : 0.0f);
           }
           store_outputs(J.y, A.y_dtype, (int64_t)b * J.ldy, oidx, out);

@@ -2,101 +2,168 @@
 
 The output transforms that run inside the decode-matvec kernels read and
 write tagged 64-bit slots in the workspace and take dummy loads for absent
-operands.  For every shape the kernels accept, each index they form under
-their own guards is enumerated here and checked against the size of the
-region it addresses; a plausible slip (a dropped guard, B where the region
-holds 2 rows, a stride of m + 256) fails one of these cases.
+operands.  The kernels form every such index with the functions of
+quipsharp_amd/csrc/qs_slots.h, and the workspace layout sizes the regions with
+the same file's slot counts; this test compiles that header with g++ into a
+small checker that enumerates each index the kernels form, under the kernels'
+own guards and over their thread layout (16 waves of 64 lanes, chunk
+c = w + 16 u, element t = lane + 64 j), for every shape they accept, and
+checks it against the size of the region it addresses.  An edit of a formula
+in the header reaches the kernels and this check alike; a plausible slip (a
+dropped guard, B where the region holds 2 rows, a stride of m + 256) fails.
 
-Index forms (qs_forward_dev.h, qs_linear_fused.hip, qs_linear_batched.hip):
-  poll_load / poll_issue / poll_finish: y1t + ((g B + b) m + 256 c + lane + 64 j)
-      for c = w + 16 u < S_m, g < SG, b < B, lane < 64, j < 4; re-polls only
-      reload entries whose first load was a real one
-  bm_kernel reduction store: ((sg B + bc) m + 16 rb + row), rb < m / 16, row < 16
-  store_h2 / poll_columns: h2t + (b m + 256 c + 16 g + tt), c < S_m, g < 16, tt < 16
-  output index and dummy loads: 256 r + t, r < S_m, t < 256 (su words: that / 32)
-Region sizes (ws_layout, fused_block in qs_linear.hip): one-launch slots
-SG_f 2 m, its chunk transforms 2 m, the 16-row decode-matvec's slots SG B m.
+Guards and loops followed (qs_forward_dev.h, qs_linear_fused.hip,
+qs_linear_batched.hip, qs_linear_big.hip):
+  poll_load / load_partials_raw: c < S_m, g < SG, b < B
+  reduction stores (both decode loops): row blocks rb < m / 16, rows < 16
+  store_h2 (level 1): c < S_m, b < B (B <= 2)
+  poll_columns (level 2): v = tid + 1024 k, (c, tt) = (v / 16, v % 16), c < S_m
+  output stage and dummy loads: r < S_m, t < 256 (su words: that / 32)
 """
-import numpy as np
+import shutil
+import subprocess
+from pathlib import Path
+
 import pytest
 
+CSRC = Path(__file__).resolve().parents[1] / "quipsharp_amd" / "csrc"
 
-def slot_indices(m, B, SG):
-    """Every slot a tail work-group polls: poll_load's address under its guards."""
-    Sm = m // 256
-    g, b, w, u, lane, j = np.meshgrid(np.arange(SG), np.arange(B), np.arange(16), np.arange(3),
-                                      np.arange(64), np.arange(4), indexing="ij", sparse=True)
-    c = w + 16 * u
-    idx = (g * B + b) * m + 256 * c + lane + 64 * j
-    return idx[np.broadcast_to(c < Sm, idx.shape)]
+CHECKER = r"""
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+#include "qs_slots.h"
+using namespace qs;
+
+static int fails = 0;
+static void check(size_t idx, size_t cap, const char* what, int S, int B, int SG) {
+  if (idx >= cap) {
+    if (fails < 5) std::printf("OUT %s: index %zu outside %zu (S %d B %d SG %d)\n", what, idx, cap, S, B, SG);
+    ++fails;
+  }
+}
+
+// every slot a tail polls (poll_load / load_partials_raw); unguarded: the
+// planted slip without c < S_m
+static void polls(int S, int B, int SG, size_t cap, const char* what, bool unguarded) {
+  const int m = 256 * S, cpw = (S + 15) / 16;
+  for (int g = 0; g < SG; ++g)
+    for (int b = 0; b < B; ++b)
+      for (int w = 0; w < 16; ++w)
+        for (int u = 0; u < cpw + (unguarded ? 1 : 0); ++u) {
+          const int c = w + 16 * u;
+          if (!unguarded && c >= S) continue;
+          for (int lane = 0; lane < 64; ++lane)
+            for (int j = 0; j < 4; ++j) check(partial_index(g, B, b, m, chunk_elem(c, lane, j)), cap, what, S, B, SG);
+        }
+}
+
+// the reduction stores: each slot written once
+static void reductions(int S, int B, int SG, size_t cap) {
+  const int m = 256 * S;
+  std::vector<unsigned char> seen(cap, 0);
+  for (int sg = 0; sg < SG; ++sg)
+    for (int bc = 0; bc < B; ++bc)
+      for (int rb = 0; rb < m / 16; ++rb)
+        for (int row = 0; row < 16; ++row) {
+          const size_t i = partial_index(sg, B, bc, m, block_elem(rb, row));
+          check(i, cap, "reduction store", S, B, SG);
+          if (i < cap) {
+            if (seen[i]) { std::printf("TWICE reduction store %zu\n", i); ++fails; }
+            seen[i] = 1;
+          }
+        }
+  for (size_t i = 0; i < cap; ++i)
+    if (!seen[i]) { std::printf("UNWRITTEN slot %zu (S %d B %d SG %d)\n", i, S, B, SG); ++fails; break; }
+}
+
+// level 1 (store_h2) and level 2 (poll_columns) of the two-level transform
+static void two_level(int S, int B) {
+  const int m = 256 * S;
+  const size_t cap = h2_slot_count(m);
+  for (int b = 0; b < B; ++b) {
+    for (int c = 0; c < S; ++c)
+      for (int lane = 0; lane < 64; ++lane)
+        for (int j = 0; j < 4; ++j) check(h2_index(b, m, chunk_elem(c, lane, j)), cap, "store_h2", S, B, 0);
+    for (int g = 0; g < 16; ++g)
+      for (int tid = 0; tid < 1024; ++tid)
+        for (int k = 0; k < 2; ++k) {
+          const int v = tid + 1024 * k, c = v >> 4, tt = v & 15;
+          if (c < S) check(h2_index(b, m, column_elem(c, g, tt)), cap, "poll_columns", S, B, 0);
+        }
+  }
+}
+
+// output stage: outputs, su (values or sign-bit words), bias, and the
+// dummy loads that stand in for an absent bias (from >= 2 m slots)
+static void outputs(int S) {
+  const int m = 256 * S;
+  for (int r = 0; r < S; ++r)
+    for (int t = 0; t < 256; ++t) {
+      const int o = out_elem(r, t);
+      check(o, m, "output / bias / su", S, 0, 0);
+      check(o >> 5, (m + 31) / 32, "su sign-bit words", S, 0, 0);
+      check(o, h2_slot_count(m), "dummy load from the slots", S, 0, 0);
+    }
+}
+
+int main(int argc, char** argv) {
+  const char* mode = argc > 1 ? argv[1] : "";
+  if (!std::strcmp(mode, "batched")) {        // the 16-row decode-matvec's tail
+    for (int S : {1, 2, 3, 7, 16, 20, 43, 48})
+      for (int B : {3, 8, 15, 16})
+        for (int SG : {1, 2, 3, 7}) {
+          const size_t cap = batched_slot_count(SG, B, 256 * S);
+          polls(S, B, SG, cap, "poll", false);
+          reductions(S, B, SG, cap);
+        }
+  } else if (!std::strcmp(mode, "one_launch")) {  // the one-launch kernel (1-2 rows)
+    for (int S : {1, 4, 16, 20, 43, 64, 100, 128})
+      for (int B : {1, 2})
+        for (int SG : {1, 2, 5, 8}) {
+          if (S <= 16) polls(S, B, SG, fused_slot_count(SG, 256 * S), "one-launch poll", false);
+          else two_level(S, B);
+          reductions(S, B, SG, fused_slot_count(SG, 256 * S) / 2 * B);
+        }
+  } else if (!std::strcmp(mode, "outputs")) {
+    for (int S : {1, 16, 43, 48, 100, 128}) outputs(S);
+  } else if (!std::strcmp(mode, "slip")) {     // a poll without its c < S_m guard
+    polls(20, 16, 2, batched_slot_count(2, 16, 256 * 20), "unguarded poll", true);
+  } else {
+    std::printf("usage: checker batched|one_launch|outputs|slip\n");
+    return 2;
+  }
+  std::printf("fails %d\n", fails);
+  return fails ? 1 : 0;
+}
+"""
 
 
-def reduction_indices(m, B, SG):
-    sg, bc, rb, row = np.meshgrid(np.arange(SG), np.arange(B), np.arange(m // 16), np.arange(16),
-                                  indexing="ij", sparse=True)
-    return ((sg * B + bc) * m + 16 * rb + row).ravel()
+@pytest.fixture(scope="module")
+def checker(tmp_path_factory):
+    gxx = shutil.which("g++")
+    if gxx is None:
+        pytest.skip("g++ not found")
+    d = tmp_path_factory.mktemp("tailbounds")
+    (d / "checker.cpp").write_text(CHECKER)
+    exe = d / "checker"
+    subprocess.run([gxx, "-O2", "-std=c++17", "-Wall", "-I", str(CSRC), str(d / "checker.cpp"), "-o", str(exe)],
+                   check=True, capture_output=True, text=True)
+    return exe
 
 
-def column_indices(m, B):
-    """poll_columns: v = tid + 1024 k -> (c, tt) = (v / 16, v % 16), column group g."""
-    Sm = m // 256
-    b, g, v = np.meshgrid(np.arange(B), np.arange(16), np.arange(2048), indexing="ij", sparse=True)
-    c, tt = v >> 4, v & 15
-    idx = b * m + 256 * c + 16 * g + tt
-    return idx[np.broadcast_to(c < Sm, idx.shape)]
+def _run(exe, mode):
+    return subprocess.run([str(exe), mode], capture_output=True, text=True, timeout=300)
 
 
-def output_indices(m):
-    r, t = np.meshgrid(np.arange(m // 256), np.arange(256), indexing="ij")
-    return (256 * r + t).ravel()
+@pytest.mark.parametrize("mode", ["batched", "one_launch", "outputs"])
+def test_tail_indices_in_bounds(checker, mode):
+    r = _run(checker, mode)
+    assert r.returncode == 0 and "fails 0" in r.stdout, r.stdout + r.stderr
 
 
-def check(idx, cap, what):
-    assert idx.size > 0, what
-    assert idx.min() >= 0 and idx.max() < cap, f"{what}: index {idx.max()} outside {cap}"
-
-
-@pytest.mark.parametrize("S", [1, 2, 3, 7, 16, 20, 43, 48])
-@pytest.mark.parametrize("B", [3, 8, 15, 16])
-@pytest.mark.parametrize("SG", [1, 2, 3])
-def test_batched_tail_slots_in_bounds(S, B, SG):
-    m = 256 * S
-    cap = SG * B * m  # the 16-row decode-matvec's tagged slots
-    check(slot_indices(m, B, SG), cap, "poll")
-    red = reduction_indices(m, B, SG)
-    check(red, cap, "reduction store")
-    assert np.unique(red).size == cap  # every slot written once: each poll finds its value
-
-
-@pytest.mark.parametrize("S", [1, 4, 16, 20, 43, 64, 100, 128])
-@pytest.mark.parametrize("B", [1, 2])
-@pytest.mark.parametrize("SG", [1, 2, 5, 8])
-def test_one_launch_tail_in_bounds(S, B, SG):
-    m = 256 * S
-    if S <= 16:  # one work-group polls the slots (m <= 4096)
-        check(slot_indices(m, B, SG), SG * 2 * m, "one-launch poll")
-    else:  # two levels: chunk transforms as slots, then 16 column groups
-        check(column_indices(m, B), 2 * m, "column poll")
-        c, lane, j = np.meshgrid(np.arange(S), np.arange(64), np.arange(4), indexing="ij", sparse=True)
-        for b in range(B):
-            check((b * m + 256 * c + lane + 64 * j).ravel(), 2 * m, "store_h2")
-
-
-@pytest.mark.parametrize("S", [1, 16, 43, 48, 128])
-def test_output_and_dummy_indices_in_bounds(S):
-    m = 256 * S
-    o = output_indices(m)
-    check(o, m, "output / bias / su")
-    check(o >> 5, -(-m // 32), "su sign-bit words")
-    # a dummy source stands in for an absent bias: the slots hold >= 2 m floats
-    check(o, 2 * m, "dummy load from the slots")
-
-
-def test_a_planted_slip_is_caught():
+def test_a_planted_slip_is_caught(checker):
     """A poll that skipped its c < S_m guard would read past the region."""
-    m, B, SG = 256 * 20, 16, 2
-    g, b, w, u, lane, j = np.meshgrid(np.arange(SG), np.arange(B), np.arange(16), np.arange(3),
-                                      np.arange(64), np.arange(4), indexing="ij", sparse=True)
-    unguarded = ((g * B + b) * m + 256 * (w + 16 * u) + lane + 64 * j).ravel()
-    with pytest.raises(AssertionError):
-        check(unguarded, SG * B * m, "unguarded poll")
+    r = _run(checker, "slip")
+    assert r.returncode == 1 and "OUT unguarded poll" in r.stdout, r.stdout + r.stderr
