@@ -257,6 +257,36 @@ int qs_linear_forward_group(const void *x, int x_dtype, int64_t ldx, int64_t bat
                             void *workspace, size_t workspace_bytes, void *mv_begin, void *mv_end,
                             qs_stream_t stream);
 
+/* A pre-operation on the bf16 input rows of a grouped one-launch forward:
+ * QS_PREOP_RMSNORM: h' = x + x2 (bf16 add; x itself when x2 is NULL), input =
+ * bf16(weight * bf16(h' * rsqrt(mean(h'^2) + eps))) (transformers' residual
+ * add and Qwen3RMSNorm), h' written to h_out when it is not NULL.  The
+ * results equal qs_dec_rmsnorm followed by qs_linear_forward_group bit for
+ * bit. */
+enum { QS_PREOP_RMSNORM = 1 };
+typedef struct qs_preop {
+  int kind;
+  const void *x2;      /* residual delta [batch][ldx2] or NULL */
+  int64_t ldx2;
+  const void *weight;  /* norm weights [n] bf16 */
+  void *h_out;         /* h' [batch][ldo] or NULL; must not overlap x or x2 */
+  int64_t ldo;
+  float eps;
+} qs_preop;
+
+/* qs_linear_forward_group on the rows the pre-operation makes of x (bf16),
+ * in the same launch: no counterpart in the reference (its decoder runs the
+ * norm as a framework kernel before each QuantizedLinear.forward,
+ * scripts/eval_ppl.py:41-65); for decode loops that would otherwise launch it
+ * on its own (every work-group of the launch redoes the norm, so it pays at
+ * one row).  One-launch calls only: 1-2 rows, n a multiple of 256 up to
+ * 16384, rows of x, x2 and h_out 8-byte aligned with strides that are
+ * multiples of 4, weight 8-byte aligned; anything else returns
+ * QS_ERR_UNSUPPORTED (the caller runs the norm on its own). */
+int qs_linear_forward_group_pre(const void *x, int64_t ldx, int64_t batch, int64_t n, int kron_pn,
+                                const float *kron_n, int count, const qs_linear_job *jobs, const qs_preop *pre,
+                                int y_dtype, void *workspace, size_t workspace_bytes, qs_stream_t stream);
+
 /* Measurement helper: enqueue a kernel that keeps `stream` busy for about
  * `nanoseconds` (bounded; at most 1 s), so that work enqueued after it runs
  * back to back on the GPU while the host is still submitting. */
@@ -275,8 +305,10 @@ int qs_busy_wait(int64_t nanoseconds, qs_stream_t stream);
 
 /* h_out = h + delta (bf16 add; skipped when delta is NULL, then h_out is
  * unused; h_out may alias h), x = weight * bf16(h' * rsqrt(mean(h'^2) + eps))
- * for each of `rows` rows of `dim` (a multiple of 8) with row stride ld;
- * 16-byte aligned buffers. */
+ * for each of `rows` rows of `dim` (a multiple of 8, at most 32768) with row
+ * stride ld; 16-byte aligned buffers.  The sum of squares is taken in the
+ * order of the RMSNorm pre-operation of qs_linear_forward_group_pre, so the
+ * two give the same rows bit for bit. */
 int qs_dec_rmsnorm(const void *h, const void *delta, void *h_out, const void *weight, void *x, int64_t rows,
                    int64_t dim, int64_t ld, float eps, qs_stream_t stream);
 

@@ -22,6 +22,7 @@ QS_MAX_STAGES = 4
 QS_MAX_KRON = 64
 QS_MAX_GROUP = 4
 QS_NOALLOC_SCRATCH_BYTES = 32 << 20
+QS_PREOP_RMSNORM, QS_PREOP_SILU_MUL = 1, 2
 
 _vp = ctypes.c_void_p
 
@@ -33,6 +34,14 @@ class LinearJob(ctypes.Structure):
                 ("kron_m", ctypes.c_void_p), ("s0", ctypes.c_float), ("s1", ctypes.c_float),
                 ("layer_scale", ctypes.c_float), ("bias", ctypes.c_void_p), ("y", ctypes.c_void_p),
                 ("ldy", ctypes.c_int64), ("sign_bits", ctypes.c_int)]
+
+
+
+class PreOp(ctypes.Structure):
+    """qs_preop (include/quipsharp_hip.h)."""
+    _fields_ = [("kind", ctypes.c_int), ("x2", ctypes.c_void_p), ("ldx2", ctypes.c_int64),
+                ("weight", ctypes.c_void_p), ("h_out", ctypes.c_void_p), ("ldo", ctypes.c_int64),
+                ("eps", ctypes.c_float)]
 
 _i64 = ctypes.c_int64
 _int = ctypes.c_int
@@ -64,6 +73,8 @@ _SIGNATURES = {
     "qs_linear_group_workspace_bytes": ([_i64, _i64, _int, ctypes.POINTER(ctypes.c_int64)], ctypes.c_size_t),
     "qs_linear_forward_group": ([_vp, _int, _i64, _i64, _i64, _int, _vp, _int, ctypes.POINTER(LinearJob), _int,
                                  _vp, ctypes.c_size_t, _vp, _vp, _vp], _int),
+    "qs_linear_forward_group_pre": ([_vp, _i64, _i64, _i64, _int, _vp, _int, ctypes.POINTER(LinearJob),
+                                     ctypes.POINTER(PreOp), _int, _vp, ctypes.c_size_t, _vp], _int),
     "qs_busy_wait": ([_i64, _vp], _int),
     "qs_dec_rmsnorm": ([_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _f32, _vp], _int),
     "qs_dec_qk_norm_rope": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _int, _int, _int, _i64,

@@ -302,7 +302,50 @@ def grouped_forward(x: Tensor, linears):
     return _grouped(x, linears)
 
 
-def _grouped(x: Tensor, linears):
+def run_preop(x: Tensor, pre: dict) -> Tensor:
+    """The rows a pre-operation makes of bf16 x, on their own launch
+    (qs_dec_rmsnorm: RMSNorm(x + delta), with x + delta written to h_out)."""
+    from . import _lib
+    L = _lib.lib()
+    n = x.shape[-1]
+    rows = x.numel() // n
+    xs = x.reshape(rows, n).contiguous()
+    out = torch.empty_like(xs)
+    stream = _lib.stream_of(xs)
+    if pre["kind"] == "rmsnorm":
+        delta, h_out = pre.get("delta"), pre.get("h_out")
+        d = delta.reshape(rows, n).contiguous() if delta is not None else None
+        if d is not None and h_out is None:
+            h_out = torch.empty_like(xs)
+        o = h_out.reshape(rows, n) if h_out is not None else None
+        if o is not None and (not o.is_contiguous() or o.data_ptr() != h_out.data_ptr()):
+            raise ValueError("h_out must be contiguous rows")
+        _lib.check(L.qs_dec_rmsnorm(_lib.ptr(xs), _lib.ptr(d), _lib.ptr(o), _lib.ptr(pre["weight"]), _lib.ptr(out),
+                                    rows, n, n, float(pre.get("eps", 1e-6)), stream))
+        if d is None and o is not None:
+            o.copy_(xs)  # h' = x: what the pre-operation in the launch writes
+    else:
+        raise ValueError(f"unknown pre-operation {pre['kind']!r}")
+    return out.reshape(x.shape)
+
+
+def grouped_forward_pre(x: Tensor, linears, pre: dict):
+    """``grouped_forward`` on the rows a pre-operation makes of bf16 x
+    (``quantize.forward_packed_group``'s ``pre``: RMSNorm with the residual
+    add), inside the same launch for one row (``quantize.pre_ok``; every
+    work-group of the launch redoes the norm, which measured faster than the
+    norm's own launch at one row and slower at two), otherwise the norm on its
+    own launch first (``run_preop``); the outputs are the same either way.  No
+    counterpart in the reference, whose decoder runs the norm as a framework
+    kernel before each QuantizedLinear.forward."""
+    from .quantize import pre_ok
+    n = x.shape[-1]
+    if x.numel() == n and groupable(x, linears) and pre_ok(x, n, pre):
+        return _grouped(x, linears, pre=pre)
+    return grouped_forward(run_preop(x, pre), linears)
+
+
+def _grouped(x: Tensor, linears, pre: dict = None):
     """The grouped forward proper, for linears that groupable() accepts."""
     from . import _lib
     from .quantize import forward_packed_group
@@ -325,7 +368,8 @@ def _grouped(x: Tensor, linears):
     if ws is None or ws.numel() < need or ws.device != x.device:
         ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=x.device)  # zeroed once, reused
         lead._group_ws = ws
-    return forward_packed_group(x, jobs, out_dtype=x.dtype, workspace=ws)
+    return forward_packed_group(x, jobs, out_dtype=x.dtype, workspace=ws, pre=pre)
+
 
 def replace_with_quantized_linear_(parent: nn.Module, attr: str, layer: QuantizedLayer, codebook,
                                    bias: Tensor = None) -> QuantizedLinear:

@@ -61,6 +61,17 @@ __device__ __forceinline__ float lane_xor(float v, LaneX lx) {
   return __builtin_bit_cast(float, r);
 }
 
+// Sum of a float over the 64 lanes of a wave (DPP / permlane exchanges).
+__device__ __forceinline__ float wave_sum(float v, LaneX lx) {
+  v += lane_xor<32>(v, lx);
+  v += lane_xor<16>(v, lx);
+  v += lane_xor<8>(v, lx);
+  v += lane_xor<4>(v, lx);
+  v += lane_xor<2>(v, lx);
+  v += lane_xor<1>(v, lx);
+  return v;
+}
+
 // Butterfly across lanes: the lane with the bit clear keeps a + b, its
 // partner a - b (exact: fma with +-1).
 template <int MASK, int NC>

@@ -12,7 +12,7 @@
 // All row counts, head counts and lengths are checked on the host; the
 // position is read on the device (one int64 shared by every batch row), so a
 // captured step replays for any position below the cache length.
-#include "qs_chunk_dev.h"
+#include "qs_preop_dev.h"
 
 namespace qs {
 namespace {
@@ -23,72 +23,63 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float bf(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 __device__ __forceinline__ float rbf(float f) { return bf(f32_to_bf16(f)); }  // round through bf16
 
-// Sum over a 256-thread work-group (4 waves); red holds 4 floats.
-__device__ __forceinline__ float block_sum256(float v, float* red, LaneX lx) {
-  v += lane_xor<32>(v, lx);
-  v += lane_xor<16>(v, lx);
-  v += lane_xor<8>(v, lx);
-  v += lane_xor<4>(v, lx);
-  v += lane_xor<2>(v, lx);
-  v += lane_xor<1>(v, lx);
-  const int w = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) red[w] = v;
-  __syncthreads();
-  const float s = (red[0] + red[1]) + (red[2] + red[3]);
-  __syncthreads();
-  return s;
-}
-
 // h_out = h + delta (bf16 add; h_out may be h); x = weight * bf16(h_out *
 // rsqrt(mean(h_out^2) + eps)) (transformers' Qwen3RMSNorm.forward).  One
-// work-group per row, 8 elements per thread and step.
-__global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* h, const uint16_t* delta, uint16_t* h_out,
-                                                      const uint16_t* weight, uint16_t* x, int dim, int64_t ld,
-                                                      float eps) {
-  __shared__ float red[4];
+// 1024-thread work-group per row in the activation-quad layout of the
+// one-launch forward's loader, with its order of the sum of squares
+// (qs_preop_dev.h), so a norm there equals this kernel's bit for bit; each
+// element is read and written by one thread, so h_out may alias h.
+__global__ __launch_bounds__(1024) void rmsnorm_kernel(const uint16_t* h, const uint16_t* delta, uint16_t* h_out,
+                                                       const uint16_t* weight, uint16_t* x, int dim, int64_t ld,
+                                                       float eps) {
+  __shared__ float wsum[kWaves];
   const LaneX lx = lane_x_init();
   const int64_t r = blockIdx.x;
-  const uint16_t* hr = h + r * ld;
-  float ss = 0.0f;
-  for (int i0 = 8 * threadIdx.x; i0 < dim; i0 += 8 * 256) {
-    uint4 a = *reinterpret_cast<const uint4*>(hr + i0);
-    if (delta) {
-      const uint4 d = *reinterpret_cast<const uint4*>(delta + r * ld + i0);
-      const uint32_t* pa = &a.x;
-      const uint32_t* pd = &d.x;
-      uint32_t o[4];
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int S = (dim + 255) / 256;
+  const bool two = S > 64;
+  uint32_t hv[2][4][2], dv[2][4][2], wv[2][4][2];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const uint16_t lo = f32_to_bf16(bf((uint16_t)(pa[k] & 0xFFFF)) + bf((uint16_t)(pd[k] & 0xFFFF)));
-        const uint16_t hi = f32_to_bf16(bf((uint16_t)(pa[k] >> 16)) + bf((uint16_t)(pd[k] >> 16)));
-        o[k] = (uint32_t)lo | ((uint32_t)hi << 16);
+  for (int rr = 0; rr < 2; ++rr)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = 64 * rr + 4 * w + i, e = 256 * c + 4 * lane;
+      const bool valid = (rr == 0 || two) && c < S && e < dim;
+      uint2 a = make_uint2(0, 0), d = make_uint2(0, 0), wt = make_uint2(0, 0);
+      if (valid) {
+        a = *reinterpret_cast<const uint2*>(h + r * ld + e);
+        if (delta) d = *reinterpret_cast<const uint2*>(delta + r * ld + e);
+        wt = *reinterpret_cast<const uint2*>(weight + e);
       }
-      a = make_uint4(o[0], o[1], o[2], o[3]);
-      *reinterpret_cast<uint4*>(h_out + r * ld + i0) = a;
+      hv[rr][i][0] = a.x, hv[rr][i][1] = a.y;
+      dv[rr][i][0] = d.x, dv[rr][i][1] = d.y;
+      wv[rr][i][0] = wt.x, wv[rr][i][1] = wt.y;
     }
-    const uint32_t* pa = &a.x;
+  const bool has_delta = delta != nullptr;
+  float ss = rms_quad_resid(hv[0], dv[0], has_delta);
+  if (two) ss += rms_quad_resid(hv[1], dv[1], has_delta);
+  ss = wave_sum(ss, lx);
+  if (lane == 0) wsum[w] = ss;
+  __syncthreads();
+  float tot = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const float lo = bf((uint16_t)(pa[k] & 0xFFFF)), hi = bf((uint16_t)(pa[k] >> 16));
-      ss += lo * lo;
-      ss += hi * hi;
-    }
-  }
-  const float rs = 1.0f / sqrtf(block_sum256(ss, red, lx) / (float)dim + eps);
-  const uint16_t* src = delta ? h_out + r * ld : hr;
-  for (int i0 = 8 * threadIdx.x; i0 < dim; i0 += 8 * 256) {
-    const uint4 a = *reinterpret_cast<const uint4*>(src + i0);
-    const uint4 wv = *reinterpret_cast<const uint4*>(weight + i0);
-    const uint32_t* pa = &a.x;
-    const uint32_t* pw = &wv.x;
-    uint32_t o[4];
+  for (int i = 0; i < kWaves; ++i) tot += wsum[i];
+  const float rs = rms_scale(tot, dim, eps);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const float lo = rbf(bf((uint16_t)(pa[k] & 0xFFFF)) * rs), hi = rbf(bf((uint16_t)(pa[k] >> 16)) * rs);
-      o[k] = (uint32_t)f32_to_bf16(bf((uint16_t)(pw[k] & 0xFFFF)) * lo) |
-             ((uint32_t)f32_to_bf16(bf((uint16_t)(pw[k] >> 16)) * hi) << 16);
+  for (int rr = 0; rr < 2; ++rr) {
+    if (rr == 1 && !two) break;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = 64 * rr + 4 * w + i, e = 256 * c + 4 * lane;
+      if (has_delta && c < S && e < dim)
+        *reinterpret_cast<uint2*>(h_out + r * ld + e) = make_uint2(hv[rr][i][0], hv[rr][i][1]);
     }
-    *reinterpret_cast<uint4*>(x + r * ld + i0) = make_uint4(o[0], o[1], o[2], o[3]);
+    rms_quad_apply(hv[rr], wv[rr], rs);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = 64 * rr + 4 * w + i, e = 256 * c + 4 * lane;
+      if (c < S && e < dim) *reinterpret_cast<uint2*>(x + r * ld + e) = make_uint2(hv[rr][i][0], hv[rr][i][1]);
+    }
   }
 }
 
@@ -284,10 +275,7 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* gt, const
   float uv[2] = {bf((uint16_t)(u & 0xFFFF)), bf((uint16_t)(u >> 16))};
   uint32_t o = 0;
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const float sv = rbf(gv[k] / (1.0f + __expf(-gv[k])));
-    o |= (uint32_t)f32_to_bf16(sv * uv[k]) << (16 * k);
-  }
+  for (int k = 0; k < 2; ++k) o |= (uint32_t)f32_to_bf16(silu_bf16(gv[k]) * uv[k]) << (16 * k);
   *reinterpret_cast<uint32_t*>(out + r * ldo + i) = o;
 }
 
@@ -300,13 +288,14 @@ using namespace qs;
 
 extern "C" int qs_dec_rmsnorm(const void* h, const void* delta, void* h_out, const void* weight, void* x,
                               int64_t rows, int64_t dim, int64_t ld, float eps, qs_stream_t stream) {
-  QS_REQUIRE(h && weight && x && rows >= 1 && rows <= 65535 && dim >= 8 && dim % 8 == 0 && ld >= dim && ld % 8 == 0,
-             "qs_dec_rmsnorm: rows %lld, dim %lld (multiple of 8), ld %lld", (long long)rows, (long long)dim,
-             (long long)ld);
+  QS_REQUIRE(h && weight && x && rows >= 1 && rows <= 65535 && dim >= 8 && dim % 8 == 0 && dim <= 32768 &&
+                 ld >= dim && ld % 8 == 0,
+             "qs_dec_rmsnorm: rows %lld, dim %lld (multiple of 8, at most 32768), ld %lld", (long long)rows,
+             (long long)dim, (long long)ld);
   QS_REQUIRE(!delta || h_out, "qs_dec_rmsnorm: a residual delta needs h_out");
   QS_REQUIRE(aligned16(h) && aligned16(weight) && aligned16(x) && (!delta || (aligned16(delta) && aligned16(h_out))),
              "qs_dec_rmsnorm: buffers must be 16-byte aligned");
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)rows), dim3(256), 0, as_stream(stream),
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)rows), dim3(1024), 0, as_stream(stream),
                      static_cast<const uint16_t*>(h), static_cast<const uint16_t*>(delta), static_cast<uint16_t*>(h_out),
                      static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(x), (int)dim, ld, eps);
   QS_LAUNCHED("rmsnorm_kernel");

@@ -263,16 +263,6 @@ __device__ __forceinline__ void store_chunks_lanes(float* Y, int S, int w, int l
   }
 }
 
-// Sum of a float over the 64 lanes of a wave (DPP / permlane exchanges).
-__device__ __forceinline__ float wave_sum(float v, LaneX lx) {
-  v += lane_xor<32>(v, lx);
-  v += lane_xor<16>(v, lx);
-  v += lane_xor<8>(v, lx);
-  v += lane_xor<4>(v, lx);
-  v += lane_xor<2>(v, lx);
-  v += lane_xor<1>(v, lx);
-  return v;
-}
 
 // 2^e with |x2_i| <= ||x|| 2^-e < 2^14 for the fp16 operand of a row of
 // squared norm norm2 (e = 0 for a zero or non-finite norm).

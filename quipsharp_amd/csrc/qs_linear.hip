@@ -1194,10 +1194,10 @@ extern "C" size_t qs_linear_group_workspace_bytes(int64_t n, int64_t batch, int 
   return total;
 }
 
-extern "C" int qs_linear_forward_group(const void* x, int x_dtype, int64_t ldx, int64_t batch, int64_t n,
-                                       int kron_pn, const float* kron_n, int count, const qs_linear_job* jobs,
-                                       int y_dtype, void* workspace, size_t workspace_bytes, void* mv_begin,
-                                       void* mv_end, qs_stream_t stream) {
+static int forward_group_impl(const void* x, int x_dtype, int64_t ldx, int64_t batch, int64_t n, int kron_pn,
+                              const float* kron_n, int count, const qs_linear_job* jobs, int y_dtype,
+                              void* workspace, size_t workspace_bytes, void* mv_begin, void* mv_end,
+                              qs_stream_t stream, const FusedPre* pre) {
   QS_REQUIRE(count >= 1 && count <= QS_MAX_GROUP, "count must be in [1, %d]", QS_MAX_GROUP);
   QS_REQUIRE(jobs && x && workspace, "null pointer");
   QS_REQUIRE(x_dtype >= QS_DTYPE_F32 && x_dtype <= QS_DTYPE_BF16 && y_dtype >= QS_DTYPE_F32 &&
@@ -1210,6 +1210,8 @@ extern "C" int qs_linear_forward_group(const void* x, int x_dtype, int64_t ldx, 
   const bool one_launch = fused_eligible(batch, n, x_dtype, kron_pn) && fused_x_aligned(x, x_dtype, ldx);
   QS_REQUIRE(n % 256 == 0 && n / kron_pn >= 256,
              "grouped forward needs n a multiple of 256 with n / kron_pn >= 256 (got n %lld)", (long long)n);
+  if (pre) QS_SUPPORTED(one_launch, "a pre-operation runs in one-launch calls only (batch %lld, n %lld)",
+                        (long long)batch, (long long)n);
   QS_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255) == 0, "workspace must be 256-byte aligned");
   size_t need = 0;
   for (int g = 0; g < count; ++g) {
@@ -1283,7 +1285,7 @@ extern "C" int qs_linear_forward_group(const void* x, int x_dtype, int64_t ldx, 
   }
   rc = launch_linear_fused(x, x_dtype, ldx, (int)batch, (int)n, kron_pn, kron_n, y_dtype, jobs[0].sign_bits ? 1 : 0,
                            count, d, W0.S, W0.fused, cu_count(), s, reinterpret_cast<hipEvent_t>(mv_begin),
-                           reinterpret_cast<hipEvent_t>(mv_end));
+                           reinterpret_cast<hipEvent_t>(mv_end), pre);
   if (rc) return rc;
   // outputs the kernel did not finish: chunked ones in one launch, others per job
   YcArgs yc[QS_MAX_GROUP];
@@ -1304,6 +1306,47 @@ extern "C" int qs_linear_forward_group(const void* x, int x_dtype, int64_t ldx, 
   }
   if (nyc) return launch_yout_chunk_group(nyc, yc, s);
   return QS_OK;
+}
+
+extern "C" int qs_linear_forward_group(const void* x, int x_dtype, int64_t ldx, int64_t batch, int64_t n,
+                                       int kron_pn, const float* kron_n, int count, const qs_linear_job* jobs,
+                                       int y_dtype, void* workspace, size_t workspace_bytes, void* mv_begin,
+                                       void* mv_end, qs_stream_t stream) {
+  return forward_group_impl(x, x_dtype, ldx, batch, n, kron_pn, kron_n, count, jobs, y_dtype, workspace,
+                            workspace_bytes, mv_begin, mv_end, stream, nullptr);
+}
+
+// [a, a + abytes) and [b, b + bbytes) share a byte
+static bool overlaps(const void* a, size_t abytes, const void* b, size_t bbytes) {
+  const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+  return pa < pb + bbytes && pb < pa + abytes;
+}
+
+extern "C" int qs_linear_forward_group_pre(const void* x, int64_t ldx, int64_t batch, int64_t n, int kron_pn,
+                                           const float* kron_n, int count, const qs_linear_job* jobs,
+                                           const qs_preop* pre, int y_dtype, void* workspace,
+                                           size_t workspace_bytes, qs_stream_t stream) {
+  QS_REQUIRE(pre && x, "null pointer");
+  QS_REQUIRE(pre->kind == QS_PREOP_RMSNORM, "bad pre-operation kind %d", pre->kind);
+  QS_REQUIRE(batch >= 0 && n > 0 && ldx >= n, "bad shape batch=%lld n=%lld", (long long)batch, (long long)n);
+  if (batch == 0) return QS_OK;
+  QS_REQUIRE(pre->weight != nullptr, "RMSNorm pre-operation: null weight");
+  QS_REQUIRE(!pre->x2 || pre->ldx2 >= n, "pre-operation: ldx2 %lld < n", (long long)pre->ldx2);
+  QS_REQUIRE(!pre->h_out || pre->ldo >= n, "pre-operation: ldo %lld < n", (long long)pre->ldo);
+  auto a8 = [](const void* p, int64_t ld) { return (reinterpret_cast<uintptr_t>(p) & 7) == 0 && ld % 4 == 0; };
+  QS_SUPPORTED(batch <= 2 && n % 256 == 0 && n / 256 <= 64 && a8(x, ldx) && (!pre->x2 || a8(pre->x2, pre->ldx2)) &&
+                   (reinterpret_cast<uintptr_t>(pre->weight) & 7) == 0 && (!pre->h_out || a8(pre->h_out, pre->ldo)),
+               "pre-operation: 1-2 rows, n a multiple of 256 up to 16384, 8-byte aligned rows (got batch %lld, "
+               "n %lld)", (long long)batch, (long long)n);
+  if (pre->h_out) {
+    const size_t out_bytes = (size_t)((batch - 1) * pre->ldo + n) * 2;
+    QS_REQUIRE(!overlaps(pre->h_out, out_bytes, x, (size_t)((batch - 1) * ldx + n) * 2) &&
+                   (!pre->x2 || !overlaps(pre->h_out, out_bytes, pre->x2, (size_t)((batch - 1) * pre->ldx2 + n) * 2)),
+               "pre-operation: h_out overlaps x or x2 (every work-group reads them while one writes h_out)");
+  }
+  FusedPre fp{pre->kind, pre->x2, pre->ldx2, pre->weight, pre->h_out, pre->ldo, pre->eps};
+  return forward_group_impl(x, QS_DTYPE_BF16, ldx, batch, n, kron_pn, kron_n, count, jobs, y_dtype, workspace,
+                            workspace_bytes, nullptr, nullptr, stream, &fp);
 }
 
 extern "C" int qs_decode_matvec(const void* x, int x_dtype, int64_t ldx, int64_t batch, int64_t n, int64_t m,

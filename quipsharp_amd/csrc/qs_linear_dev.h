@@ -35,9 +35,20 @@ struct FusedPlan {
   int SG, W, P;
 };
 FusedPlan fused_plan(int S);
+// A pre-operation on the bf16 input rows of a one-launch forward
+// (qs_preop_dev.h; the fields of qs_preop, include/quipsharp_hip.h).
+struct FusedPre {
+  int kind;             // QS_PREOP_RMSNORM
+  const void* x2;       // the residual delta (or NULL)
+  int64_t ldx2;
+  const void* weight;   // norm weights [n]
+  void* h_out;          // x + delta [B][ldo] (or NULL)
+  int64_t ldo;
+  float eps;
+};
 int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, int pn, const float* Kn, int y_dtype,
                         int sbits, int count, const FusedJobDesc* jobs, int S, const FusedPlan& plan, int ncu,
-                        hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop);
+                        hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop, const FusedPre* pre = nullptr);
 bool fused_eligible(int64_t batch, int64_t n, int x_dtype, int pn);
 bool fused_x_aligned(const void* x, int x_dtype, int64_t ldx);
 bool fused_output_in_kernel(int64_t m, int pm);

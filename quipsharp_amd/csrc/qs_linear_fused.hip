@@ -52,6 +52,7 @@
 
 #include "qs_forward_dev.h"
 #include "qs_linear_dev.h"
+#include "qs_preop_dev.h"
 
 namespace qs {
 namespace {
@@ -105,6 +106,14 @@ struct FusedArgs {
   // the jobs so that their fields keep the offsets the kernel loads them from
   unsigned long long* ws;
   unsigned long long ws_words;
+  // pre-operation on the input rows (XT 3: RMSNorm of x + x2 with weight nw,
+  // h' to h_out by work-group 0), qs_preop_dev.h
+  const uint16_t* x2;
+  int64_t ldx2;
+  const uint16_t* nw;
+  uint16_t* h_out;
+  int64_t ldo;
+  float eps;
 };
 
 // LDS layout (bytes).  The slice rows of the input transform alias the
@@ -123,7 +132,7 @@ constexpr int kMinStride = kMaxSF + 8;                      // bf16 per row of t
 constexpr int kOffMin = kOffRed + kRedBytes;                // 2 x 16 x kMinStride bf16 (hi, lo)
 constexpr int kOffXH = kOffMin + 2 * 16 * kMinStride * 2;   // kMaxB x 16 x kXStride halves
 constexpr int kOffXS = kOffXH + kMaxB * 16 * kXStride * 2;  // kMaxB x 16 x 32 halves (group sums)
-constexpr int kOffMisc = kOffXS + kMaxB * 16 * 32 * 2;      // row norms (16 floats)
+constexpr int kOffMisc = kOffXS + kMaxB * 16 * 32 * 2;      // row norms (16 floats; 16 more for a norm pre-op)
 constexpr int kOffXR = kOffMisc + 128;                      // chunk table (bf16, one or two planes)
 constexpr int kXRBytes = 2 * 256 * (kMaxSF / 2 + 8) * 2;    // two planes of 64 chunks
 static_assert(256 * (kMaxSF + 8) * 2 <= kXRBytes, "one plane of kMaxSF chunks fits");
@@ -153,22 +162,41 @@ static_assert(kRedSlots * 16 * 8 == kThreads, "one reduction pass: 8 / (P B) thr
 // rows of x 8- / 16-byte aligned) and sv (fp32, or with SB the word of sign
 // bits).  A thread holds one quad at a time, so a chunk table of more than
 // 64 chunks takes a second round of loads.
+// XT 3: bf16 rows with the RMSNorm pre-operation (qs_preop_dev.h): v2 holds
+// the residual delta's words and nw the norm weights; after the
+// pre-operation v holds the bf16 operand.
 template <int XT, bool SB>
 struct XQuad {
   uint32_t v[4][XT == 2 ? 4 : 2];
   uint32_t s[4][SB ? 1 : 4];
+  uint32_t v2[4][2];
+  uint32_t nw[4][2];
 };
 template <int XT, bool SB>
 __device__ __forceinline__ void load_x_quad(const void* x, int64_t ldx, const float* sv, int S, int b, int c0,
-                                            int lane, XQuad<XT, SB>& r) {
+                                            int lane, XQuad<XT, SB>& r, const uint16_t* x2 = nullptr,
+                                            int64_t ldx2 = 0, const uint16_t* nw = nullptr) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
 #pragma unroll
     for (int k = 0; k < (XT == 2 ? 4 : 2); ++k) r.v[i][k] = 0;
 #pragma unroll
     for (int k = 0; k < (SB ? 1 : 4); ++k) r.s[i][k] = 0;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) r.v2[i][k] = r.nw[i][k] = 0;
     const int c = c0 + i;
     if (c < S) {
+      if constexpr (XT >= 3) {
+        const int e = 256 * c + 4 * lane;
+        if (x2) {
+          const uint2 t = *reinterpret_cast<const uint2*>(x2 + (int64_t)b * ldx2 + e);
+          r.v2[i][0] = t.x, r.v2[i][1] = t.y;
+        }
+        if constexpr (XT == 3) {
+          const uint2 t = *reinterpret_cast<const uint2*>(nw + e);
+          r.nw[i][0] = t.x, r.nw[i][1] = t.y;
+        }
+      }
       const int i0 = 256 * c + 4 * lane;
       if constexpr (SB) {
         r.s[i][0] = reinterpret_cast<const uint32_t*>(sv)[i0 >> 5];
@@ -192,7 +220,7 @@ __device__ __forceinline__ void load_x_quad(const void* x, int64_t ldx, const fl
 template <int XT, bool SB>
 __device__ __forceinline__ void finish_quad_chunk(const XQuad<XT, SB>& r, int i, int lane, float (&o)[4]) {
   float xv[4];
-  if constexpr (XT == 0) {
+  if constexpr (XT == 0 || XT >= 3) {
     xv[0] = __uint_as_float(r.v[i][0] << 16), xv[1] = __uint_as_float(r.v[i][0] & 0xFFFF0000u);
     xv[2] = __uint_as_float(r.v[i][1] << 16), xv[3] = __uint_as_float(r.v[i][1] & 0xFFFF0000u);
   } else if constexpr (XT == 1) {
@@ -232,7 +260,7 @@ __device__ __forceinline__ float store_quad(const XQuad<XT, SB>& r, uint16_t* XR
       const int off = (4 * lane + u) * xrs + c0 + 2 * p;
       if (store) {
         *reinterpret_cast<uint32_t*>(XR0 + off) = h;
-        if constexpr (XT != 0) *reinterpret_cast<uint32_t*>(XR1 + off) = l;
+        if constexpr (XT == 1 || XT == 2) *reinterpret_cast<uint32_t*>(XR1 + off) = l;
       }
     }
   }
@@ -404,7 +432,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   };
 
   XQuad<XT, SB> xr;
-  load_x_quad(A.x, A.ldx, J.sv, A.Sn, 0, 4 * w, lane, xr);
+  load_x_quad(A.x, A.ldx, J.sv, A.Sn, 0, 4 * w, lane, xr, A.x2, A.ldx2, A.nw);
   load_luts(tid, lutw);
   if (HAS2 && tid < 256) t1row = *reinterpret_cast<const uint4*>(kE81h.w[tid]);
   load_mk();
@@ -426,12 +454,44 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   auto input_row = [&](const int b) {
     // quads inside the padded range are stored (zeros past the S chunks);
     // the first quad of row 0 was loaded at the start
-    if (b > 0) load_x_quad(A.x, A.ldx, J.sv, A.Sn, b, 4 * w, lane, xr);
-    float ss = store_quad(xr, XR0, XR1, xrs, 4 * w, lane, 4 * w < Spad);
-    if (Spad > 64) {
-      XQuad<XT, SB> x2;
-      load_x_quad(A.x, A.ldx, J.sv, A.Sn, b, 64 + 4 * w, lane, x2);
-      ss += store_quad(x2, XR0, XR1, xrs, 64 + 4 * w, lane, 64 + 4 * w < Spad);
+    if (b > 0) load_x_quad(A.x, A.ldx, J.sv, A.Sn, b, 4 * w, lane, xr, A.x2, A.ldx2, A.nw);
+    float ss;
+    if constexpr (XT == 3) {
+      // the norm needs the whole row before the chunk table (one quad: n <=
+      // 16384, checked on the host)
+      const bool has_delta = A.x2 != nullptr;
+      float ssn = rms_quad_resid(xr.v, xr.v2, has_delta);
+      ssn = wave_sum(ssn, lx);
+      if (lane == 0) wsum[kWaves + w] = ssn;
+      if (b == 0) {
+        // the LUTs at the first barrier, as without a pre-operation (their
+        // registers are not kept across the norm)
+        store_luts(lds, tid, lutw);
+        if (HAS2 && tid < 256) lut1[tid] = t1row;
+      }
+      __syncthreads();  // the row's sums of squares
+      float tot = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kWaves; ++i) tot += wsum[kWaves + i];
+      const float rs = rms_scale(tot, A.n, A.eps);
+      if (blockIdx.x == 0 && A.h_out) {  // the residual stream h', once
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int c = 4 * w + i;
+          if (c < A.Sn)
+            *reinterpret_cast<uint2*>(A.h_out + (int64_t)b * A.ldo + 256 * c + 4 * lane) =
+                make_uint2(xr.v[i][0], xr.v[i][1]);
+        }
+      }
+      rms_quad_apply(xr.v, xr.nw, rs);
+      ss = store_quad(xr, XR0, XR1, xrs, 4 * w, lane, 4 * w < Spad);
+    } else {
+      ss = store_quad(xr, XR0, XR1, xrs, 4 * w, lane, 4 * w < Spad);
+      if (Spad > 64) {
+        XQuad<XT, SB> x2;
+        load_x_quad(A.x, A.ldx, J.sv, A.Sn, b, 64 + 4 * w, lane, x2);
+        ss += store_quad(x2, XR0, XR1, xrs, 64 + 4 * w, lane, 64 + 4 * w < Spad);
+      }
     }
     ss = wave_sum(ss, lx);
     if (lane == 0) wsum[w] = ss;
@@ -452,7 +512,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
         }
       }
     }
-    if (b == 0) {
+    if (b == 0 && XT != 3) {
       store_luts(lds, tid, lutw);
       if (HAS2 && tid < 256) lut1[tid] = t1row;
     }
@@ -475,7 +535,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, xh, acc, 0, 0, 0);
         if (A.pn > 1)
           acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lds_bf16x8(MinL + r16 * kMinStride + k0), xh, acc, 0, 0, 0);
-        if constexpr (XT != 0)
+        if constexpr (XT == 1 || XT == 2)
           acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, lds_bf16x8(XR1 + t * xrs + k0), acc, 0, 0, 0);
       }
 #pragma unroll
@@ -891,7 +951,7 @@ FusedPlan fused_plan(int S) {
 
 int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, int pn, const float* Kn, int y_dtype,
                         int sbits, int count, const FusedJobDesc* jobs, int S, const FusedPlan& plan, int ncu,
-                        hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop) {
+                        hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop, const FusedPre* pre) {
   const int SG = plan.SG, W = plan.W, P = plan.P;
   QS_REQUIRE(count >= 1 && count <= kMaxJobs, "1..%d linears per launch", kMaxJobs);
   QS_REQUIRE(fused_eligible(B, n, x_dtype, pn) && SG * W >= S && W * P <= kWaves && (P == 1 || P == 2 || P == 4) &&
@@ -967,11 +1027,23 @@ int launch_linear_fused(const void* x, int x_dtype, int64_t ldx, int B, int n, i
     J.y = d.y;
     J.ldy = d.ldy;
   }
-  const int xt = x_dtype == QS_DTYPE_BF16 ? 0 : x_dtype == QS_DTYPE_F16 ? 1 : 2;
+  int xt = x_dtype == QS_DTYPE_BF16 ? 0 : x_dtype == QS_DTYPE_F16 ? 1 : 2;
+  if (pre) {
+    QS_REQUIRE(x_dtype == QS_DTYPE_BF16 && pre->kind == QS_PREOP_RMSNORM,
+               "one-launch forward: the norm pre-operation needs bf16 rows");
+    xt = 3;
+    A.x2 = static_cast<const uint16_t*>(pre->x2);
+    A.ldx2 = pre->ldx2;
+    A.nw = static_cast<const uint16_t*>(pre->weight);
+    A.h_out = static_cast<uint16_t*>(pre->h_out);
+    A.ldo = pre->ldo;
+    A.eps = pre->eps;
+  }
 #define QS_FUSED_XT(H, SBITS)                                                          \
   (xt == 0 ? launch_fused_variant<H, SBITS, 0>(A, wg, stream, ev_start, ev_stop)      \
    : xt == 1 ? launch_fused_variant<H, SBITS, 1>(A, wg, stream, ev_start, ev_stop)    \
-             : launch_fused_variant<H, SBITS, 2>(A, wg, stream, ev_start, ev_stop))
+   : xt == 2 ? launch_fused_variant<H, SBITS, 2>(A, wg, stream, ev_start, ev_stop)    \
+             : launch_fused_variant<H, SBITS, 3>(A, wg, stream, ev_start, ev_stop))
   if (has2) return sbits ? QS_FUSED_XT(true, true) : QS_FUSED_XT(true, false);
   return sbits ? QS_FUSED_XT(false, true) : QS_FUSED_XT(false, false);
 #undef QS_FUSED_XT

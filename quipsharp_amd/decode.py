@@ -19,7 +19,8 @@ import torch
 from torch import nn
 
 from .architectures import get_decoder_layers, get_linear_groups
-from .checkpoint import QuantizedLinear, build_codebook, grouped_forward, link_sibling_linears
+from .checkpoint import (QuantizedLinear, build_codebook, grouped_forward, grouped_forward_pre,
+                         link_sibling_linears)
 from .hadamard import is_pow2, kron_factor, rademacher
 
 QWEN3_32B = dict(hidden_size=5120, intermediate_size=25600, num_hidden_layers=64, num_attention_heads=64,
@@ -119,11 +120,13 @@ class StaticDecoder:
     replayed.
 
     A decode step (one new token per row) runs the layer's own kernels
-    (csrc/qs_decoder.hip): RMSNorm with the residual add folded in, q/k norm
-    plus rotary embedding plus the cache write in one launch, attention over
-    the filled cache prefix only (splits of 64 positions and a combine
-    launch), SiLU * up; q/k/v and gate/up each go through one grouped
-    quantized-linear launch (checkpoint.grouped_forward).  The prompt
+    (csrc/qs_decoder.hip): q/k norm plus rotary embedding plus the cache
+    write in one launch, attention over the filled cache prefix only (splits
+    of 64 positions and a combine launch), SiLU * up; q/k/v and gate/up each
+    go through one grouped quantized-linear launch that, at one row, also
+    does the residual add and the RMSNorm before it
+    (checkpoint.grouped_forward_pre; at more rows the norm runs on its own
+    launch first).  The prompt
     (several tokens per row) runs transformers' modules with the same bf16
     cache (attention in fp32)."""
 
@@ -205,15 +208,20 @@ class StaticDecoder:
         if h.dtype != torch.bfloat16:
             raise TypeError("the decode step runs bf16 models")
         h = h.contiguous()
+        # the residual stream alternates between two buffers: a norm inside a
+        # grouped launch reads h + delta while one work-group writes the sum
+        h_alt = torch.empty_like(h)
         qbuf = torch.empty(B, nh * hd, dtype=torch.bfloat16, device=h.device)
         attn = torch.empty(B, nh * hd, dtype=torch.bfloat16, device=h.device)
         delta = None
         for i, Ly in enumerate(self.layers):
             a = Ly.self_attn
-            x = torch.empty_like(h)
-            lib.check(L.qs_dec_rmsnorm(vp(h), vp(delta), vp(h), vp(self._weight(Ly.input_layernorm)), vp(x), B, H, H,
-                                       self.eps, stream))
-            qo, ko, vo = grouped_forward(x, [a.q_proj, a.k_proj, a.v_proj])
+            # residual add + input norm inside the q/k/v launch (one row; on
+            # their own launch otherwise)
+            qo, ko, vo = grouped_forward_pre(h, [a.q_proj, a.k_proj, a.v_proj],
+                                             {"kind": "rmsnorm", "delta": delta, "h_out": h_alt, "eps": self.eps,
+                                              "weight": self._weight(Ly.input_layernorm)})
+            h, h_alt = h_alt, h
             lib.check(L.qs_dec_qk_norm_rope(vp(qo.contiguous()), vp(ko.contiguous()), vp(vo.contiguous()),
                                             vp(self._weight(a.q_norm)), vp(self._weight(a.k_norm)), vp(self.cos),
                                             vp(self.sin), vp(pos), vp(qbuf), vp(self.k[i]), vp(self.v[i]), B, nh, nkv,
@@ -221,11 +229,11 @@ class StaticDecoder:
             lib.check(L.qs_dec_attention(vp(qbuf), vp(self.k[i]), vp(self.v[i]), vp(pos), vp(attn), nh * hd,
                                          vp(self.attn_ws), self.attn_ws.numel(), B, nh, nkv, hd, self.max_len,
                                          self.scale, stream))
-            o = a.o_proj(attn)
-            x = torch.empty_like(h)
-            lib.check(L.qs_dec_rmsnorm(vp(h), vp(o.contiguous()), vp(h), vp(self._weight(Ly.post_attention_layernorm)),
-                                       vp(x), B, H, H, self.eps, stream))
-            go, uo = grouped_forward(x, [Ly.mlp.gate_proj, Ly.mlp.up_proj])
+            o = a.o_proj(attn).contiguous()
+            go, uo = grouped_forward_pre(h, [Ly.mlp.gate_proj, Ly.mlp.up_proj],
+                                         {"kind": "rmsnorm", "delta": o, "h_out": h_alt, "eps": self.eps,
+                                          "weight": self._weight(Ly.post_attention_layernorm)})
+            h, h_alt = h_alt, h
             go, uo = go.contiguous(), uo.contiguous()
             act = torch.empty_like(go)
             inter = go.shape[-1]

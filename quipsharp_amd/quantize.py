@@ -322,7 +322,7 @@ def decode_matvec(x: Tensor, packed: PackedCodes, s0: float, s1: float, layer_sc
 
 
 def forward_packed_group(x: Tensor, linears, out_dtype=None, workspace: Tensor = None, outs=None,
-                         mv_events=None):
+                         mv_events=None, pre: dict = None):
     """Several linears that read the same x in one launch (qs_linear_forward_group):
     ``linears`` is a sequence of (packed, su, sv, s0, s1, layer_scale, bias);
     returns the list of outputs, each equal to ``forward_packed`` of that
@@ -330,7 +330,14 @@ def forward_packed_group(x: Tensor, linears, out_dtype=None, workspace: Tensor =
     rows; from 3 rows with n up to 12288 one launch per stage -- input
     transforms, decode-matvecs, output transforms -- for the whole group, the
     wide GEMM one launch per linear; one forward per linear otherwise).  No
-    counterpart in the reference (one linear per call there)."""
+    counterpart in the reference (one linear per call there).
+
+    ``pre`` (qs_linear_forward_group_pre): the linears read the rows a
+    pre-operation makes of the bf16 ``x`` inside the same launch --
+    ``{"kind": "rmsnorm", "delta": Tensor or None, "weight": Tensor, "h_out":
+    Tensor or None, "eps": float}`` (input = RMSNorm(x + delta), x + delta
+    written to h_out); 1-2 rows only (``pre_ok``), bit-identical to
+    ``qs_dec_rmsnorm`` followed by the grouped forward."""
     count = len(linears)
     if not 1 <= count <= _lib.QS_MAX_GROUP:
         raise ValueError(f"1..{_lib.QS_MAX_GROUP} linears per group, got {count}")
@@ -380,12 +387,61 @@ def forward_packed_group(x: Tensor, linears, out_dtype=None, workspace: Tensor =
     need = lib.qs_linear_group_workspace_bytes(n, B, count, ms)
     if workspace is None or workspace.numel() < need:
         workspace = torch.zeros(max(need, 256), dtype=torch.uint8, device=x.device)
+    if pre is not None:
+        op = _pre_struct(x2, pre, n)
+        _lib.check(lib.qs_linear_forward_group_pre(
+            _lib.ptr(x2), x2.stride(0), B, n, fn[0], _lib.ptr(Kn), count, jobs, ctypes.byref(op),
+            _lib.dtype_code(ys[0].dtype), _lib.ptr(workspace), workspace.numel(), _lib.stream_of(x2)))
+        return list(outs) if outs is not None else [y.reshape(*lead, y.shape[-1]) for y in ys]
     _lib.check(lib.qs_linear_forward_group(
         _lib.ptr(x2), _lib.dtype_code(x2.dtype), x2.stride(0), B, n, fn[0], _lib.ptr(Kn), count, jobs,
         _lib.dtype_code(ys[0].dtype), _lib.ptr(workspace), workspace.numel(),
         None if mv_events is None else _lib._vp(mv_events[0]), None if mv_events is None else _lib._vp(mv_events[1]),
         _lib.stream_of(x2)))
     return list(outs) if outs is not None else [y.reshape(*lead, y.shape[-1]) for y in ys]
+
+
+def _rows_of(t: Tensor, n: int, B: int, what: str) -> Tensor:
+    """``t`` as B bf16 rows of n with unit column stride on x's device (no copy)."""
+    if t.dtype != torch.bfloat16 or t.shape[-1] != n or t.numel() != B * n:
+        raise ValueError(f"{what} must be {B} bf16 rows of {n}, got {tuple(t.shape)} {t.dtype}")
+    r = t.reshape(B, n)
+    if r.stride(-1) != 1 or r.untyped_storage().data_ptr() != t.untyped_storage().data_ptr():
+        raise ValueError(f"{what} must be viewable as ({B}, {n}) rows with unit column stride")
+    return r
+
+
+def pre_ok(x: Tensor, n: int, pre: dict) -> bool:
+    """Whether a grouped forward of x can run ``pre`` in its launch: the norm,
+    bf16 rows, 1-2 of them, n a multiple of 256 up to 16384, 8-byte aligned
+    rows (qs_linear_forward_group_pre)."""
+    rows = x.numel() // n if n else 0
+    others = [pre.get("delta"), pre.get("h_out")]
+    return (pre.get("kind") == "rmsnorm" and x.dtype == torch.bfloat16 and 1 <= rows <= 2 and n % 256 == 0
+            and n <= 16384
+            and all(t is None or (t.dtype == torch.bfloat16 and t.data_ptr() % 8 == 0) for t in others)
+            and x.data_ptr() % 8 == 0 and (rows == 1 or x.reshape(-1, n).stride(0) % 4 == 0))
+
+
+def _pre_struct(x2: Tensor, pre: dict, n: int):
+    """The qs_preop of ``pre`` for the rows x2 (B x n bf16)."""
+    B = x2.shape[0]
+    dev = x2.device
+    kind = pre["kind"]
+    if kind == "rmsnorm":
+        delta, weight, h_out = pre.get("delta"), pre["weight"], pre.get("h_out")
+        if weight.dtype != torch.bfloat16 or weight.numel() != n or not weight.is_contiguous():
+            raise ValueError(f"norm weight must be {n} contiguous bf16 values")
+        _lib.require_gpu(weight, delta, h_out, what="rmsnorm pre-operation")
+        d = _rows_of(delta, n, B, "delta") if delta is not None else None
+        o = _rows_of(h_out, n, B, "h_out") if h_out is not None else None
+        for t in (weight, d, o):
+            if t is not None and t.device != dev:
+                raise ValueError(f"pre-operation tensors must be on {dev}")
+        return _lib.PreOp(_lib.QS_PREOP_RMSNORM, _lib.ptr(d), d.stride(0) if d is not None and B > 1 else n,
+                          _lib.ptr(weight), _lib.ptr(o), o.stride(0) if o is not None and B > 1 else n,
+                          float(pre.get("eps", 1e-6)))
+    raise ValueError(f"unknown pre-operation {kind!r}")
 
 
 def _forward_params(codebook, num_stages):

@@ -1,7 +1,9 @@
 """The decode-step kernels of the greedy-decode harness (csrc/qs_decoder.hip)
 against the transformers / torch ops they replace: Qwen3RMSNorm with the
 residual add, q/k norm + rotary embedding + cache write, attention over the
-filled cache prefix (reference in fp32 on the CPU), and act_fn(gate) * up."""
+filled cache prefix (reference in fp32 on the CPU), and act_fn(gate) * up;
+and the same norm done inside a grouped one-launch forward
+(qs_linear_forward_group_pre), bit-identical to the separate launches."""
 import math
 
 import pytest
@@ -25,7 +27,7 @@ def _bf16_ulps(a, b):
     return int((ia - ib).abs().max().item())
 
 
-@pytest.mark.parametrize("rows,dim", [(1, 5120), (8, 5120), (3, 512)])
+@pytest.mark.parametrize("rows,dim", [(1, 5120), (8, 5120), (3, 512), (2, 520), (1, 20480), (2, 32768)])
 def test_rmsnorm_with_residual(dev, rows, dim):
     from transformers.models.qwen3.modeling_qwen3 import Qwen3RMSNorm
     lib, L = _lib()
@@ -145,3 +147,71 @@ def test_silu_mul(dev, rows, m):
     torch.cuda.synchronize()
     want = torch.nn.functional.silu(gt) * up
     assert _bf16_ulps(out, want) <= 1
+
+
+def _lins(dev, shapes, n, seed):
+    import numpy as np
+    from test_gpu_linear import _rand_linear
+    rng = np.random.default_rng(seed)
+    return [_rand_linear(dev, rng, m, n, 1, g == 0) for g, m in enumerate(shapes)]
+
+
+@pytest.mark.parametrize("shapes,n", [([8192, 1024, 1024], 5120), ([4096, 4096, 4096], 4096), ([25600, 25600], 5120),
+                                      ([11008], 16384)])
+@pytest.mark.parametrize("B", [1, 2])
+@pytest.mark.parametrize("residual", [True, False])
+def test_group_pre_rmsnorm_equals_separate(dev, shapes, n, B, residual):
+    """RMSNorm (with the residual add) inside the grouped one-launch forward:
+    outputs and the residual stream bit-identical to qs_dec_rmsnorm followed
+    by the grouped forward."""
+    from quipsharp_amd.quantize import forward_packed_group, pre_ok
+    print(f"case: group pre rmsnorm {shapes} n={n} B={B} residual={residual}", flush=True)
+    lib, L = _lib()
+    g = torch.Generator().manual_seed(B + n)
+    h = (torch.randn(B, n, generator=g) * 3).bfloat16().to(dev)
+    d = torch.randn(B, n, generator=g).bfloat16().to(dev) if residual else None
+    w = (1 + 0.1 * torch.randn(n, generator=g)).bfloat16().to(dev)
+    lins = _lins(dev, shapes, n, n + len(shapes))
+    h_ref, x = torch.empty_like(h), torch.empty_like(h)
+    lib.check(L.qs_dec_rmsnorm(lib.ptr(h), lib.ptr(d), lib.ptr(h_ref if residual else None), lib.ptr(w), lib.ptr(x),
+                               B, n, n, 1e-6, lib.stream_of(h)))
+    want = forward_packed_group(x, lins)
+    h_out = torch.full_like(h, 7.0)
+    pre = {"kind": "rmsnorm", "delta": d, "weight": w, "h_out": h_out, "eps": 1e-6}
+    assert pre_ok(h, n, pre)
+    got = forward_packed_group(h, lins, pre=pre)
+    torch.cuda.synchronize()
+    for y, yw in zip(got, want):
+        assert torch.equal(y, yw)
+    assert torch.equal(h_out, h_ref if residual else h)
+
+
+def test_group_pre_refused_shapes(dev):
+    """Outside the one-launch kernel (3 rows), a norm wider than 16384 and an
+    h_out that overlaps x are refused on the host, nothing launched."""
+    from quipsharp_amd import _lib as lb
+    from quipsharp_amd.quantize import pre_ok
+    lib, L = _lib()
+    n = 4096
+    (lin,) = _lins(dev, [1024], n, 5)
+    packed, su, sv, s0, s1, sc, bias = lin
+    w = torch.ones(n, dtype=torch.bfloat16, device=dev)
+
+    def call(x, pre, y):
+        jobs = (lb.LinearJob * 1)()
+        jobs[0] = lb.LinearJob(packed.codes0.data_ptr(), None, 1024, su.data_ptr(), sv.data_ptr(), 1, None, s0, s1, sc,
+                               bias.data_ptr(), y.data_ptr(), 1024, 0)
+        ws = torch.zeros(1 << 22, dtype=torch.uint8, device=dev)
+        return L.qs_linear_forward_group_pre(lb.ptr(x), n, x.shape[0], n, 1, None, 1, jobs, pre, lb.QS_DTYPE_BF16,
+                                             lb.ptr(ws), ws.numel(), lb.stream_of(x))
+
+    x3 = torch.randn(3, n, device=dev).bfloat16()
+    y3 = torch.full((3, 1024), 5.0, dtype=torch.bfloat16, device=dev)
+    op = lb.PreOp(lb.QS_PREOP_RMSNORM, None, n, lb.ptr(w), None, n, 1e-6)
+    assert call(x3, op, y3) == 3 and not pre_ok(x3, n, {"kind": "rmsnorm"})
+    x1 = torch.randn(1, n, device=dev).bfloat16()
+    y1 = torch.full((1, 1024), 5.0, dtype=torch.bfloat16, device=dev)
+    op = lb.PreOp(lb.QS_PREOP_RMSNORM, None, n, lb.ptr(w), lb.ptr(x1), n, 1e-6)  # h_out == x
+    assert call(x1, op, y1) == 1 and b"overlaps" in L.qs_last_error()
+    torch.cuda.synchronize()
+    assert bool((y3 == 5.0).all()) and bool((y1 == 5.0).all())
