@@ -300,7 +300,8 @@ int qs_busy_wait(int64_t nanoseconds, qs_stream_t stream);
  * same arithmetic as transformers' Qwen3RMSNorm, apply_rotary_pos_emb, the
  * attention over the cache and act_fn(gate) * up, in a few launches per
  * layer.  Tensors are bf16 (uint16 bits) unless stated; `pos` is a device
- * int64, the position of the new token (the same for every row).
+ * int64, the position of the new token (the same for every row); the kernels
+ * that read it write nothing when it is max_len or more.
  * --------------------------------------------------------------------------- */
 
 /* h_out = h + delta (bf16 add; skipped when delta is NULL, then h_out is
@@ -331,6 +332,18 @@ int64_t qs_dec_attention_workspace_bytes(int64_t rows, int nkv, int64_t max_len)
 int qs_dec_attention(const void *q, const void *k_cache, const void *v_cache, const int64_t *pos, void *out,
                      int64_t ldo, void *workspace, int64_t workspace_bytes, int64_t rows, int nh, int nkv,
                      int head_dim, int64_t max_len, float scale, qs_stream_t stream);
+
+/* qs_dec_qk_norm_rope followed by qs_dec_attention in the attention's
+ * launches: q, k, v are the raw heads ([rows][nh][128], [rows][nkv][128]);
+ * each split forms the normed, rotated queries of its kv group, and the split
+ * holding `pos` writes that position's key (normed, rotated) and value into
+ * the caches before it reads them.  Same bits as the two calls, without the
+ * normed queries in memory. */
+int qs_dec_attention_rope(const void *q, const void *k, const void *v, const void *q_norm_w, const void *k_norm_w,
+                          const void *cos_table, const void *sin_table, const int64_t *pos, void *k_cache,
+                          void *v_cache, void *out, int64_t ldo, void *workspace, int64_t workspace_bytes,
+                          int64_t rows, int nh, int nkv, int head_dim, int64_t max_len, float eps, float scale,
+                          qs_stream_t stream);
 
 /* out = bf16(silu(gate)) * up (each op rounded to bf16), rows x m (even). */
 int qs_dec_silu_mul(const void *gate, const void *up, void *out, int64_t rows, int64_t m, int64_t ldg, int64_t ldu,

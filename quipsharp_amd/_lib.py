@@ -81,6 +81,8 @@ _SIGNATURES = {
                              _f32, _vp], _int),
     "qs_dec_attention_workspace_bytes": ([_i64, _int, _i64], _i64),
     "qs_dec_attention": ([_vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _int, _int, _int, _i64, _f32, _vp], _int),
+    "qs_dec_attention_rope": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _int,
+                               _int, _int, _i64, _f32, _f32, _vp], _int),
     "qs_dec_silu_mul": ([_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp], _int),
 }
 

@@ -211,7 +211,6 @@ class StaticDecoder:
         # the residual stream alternates between two buffers: a norm inside a
         # grouped launch reads h + delta while one work-group writes the sum
         h_alt = torch.empty_like(h)
-        qbuf = torch.empty(B, nh * hd, dtype=torch.bfloat16, device=h.device)
         attn = torch.empty(B, nh * hd, dtype=torch.bfloat16, device=h.device)
         delta = None
         for i, Ly in enumerate(self.layers):
@@ -222,13 +221,12 @@ class StaticDecoder:
                                              {"kind": "rmsnorm", "delta": delta, "h_out": h_alt, "eps": self.eps,
                                               "weight": self._weight(Ly.input_layernorm)})
             h, h_alt = h_alt, h
-            lib.check(L.qs_dec_qk_norm_rope(vp(qo.contiguous()), vp(ko.contiguous()), vp(vo.contiguous()),
-                                            vp(self._weight(a.q_norm)), vp(self._weight(a.k_norm)), vp(self.cos),
-                                            vp(self.sin), vp(pos), vp(qbuf), vp(self.k[i]), vp(self.v[i]), B, nh, nkv,
-                                            hd, self.max_len, self.eps, stream))
-            lib.check(L.qs_dec_attention(vp(qbuf), vp(self.k[i]), vp(self.v[i]), vp(pos), vp(attn), nh * hd,
-                                         vp(self.attn_ws), self.attn_ws.numel(), B, nh, nkv, hd, self.max_len,
-                                         self.scale, stream))
+            # q/k norm, rotary and the cache write inside the attention's launches
+            lib.check(L.qs_dec_attention_rope(vp(qo.contiguous()), vp(ko.contiguous()), vp(vo.contiguous()),
+                                              vp(self._weight(a.q_norm)), vp(self._weight(a.k_norm)), vp(self.cos),
+                                              vp(self.sin), vp(pos), vp(self.k[i]), vp(self.v[i]), vp(attn), nh * hd,
+                                              vp(self.attn_ws), self.attn_ws.numel(), B, nh, nkv, hd, self.max_len,
+                                              self.eps, self.scale, stream))
             o = a.o_proj(attn).contiguous()
             go, uo = grouped_forward_pre(h, [Ly.mlp.gate_proj, Ly.mlp.up_proj],
                                          {"kind": "rmsnorm", "delta": o, "h_out": h_alt, "eps": self.eps,

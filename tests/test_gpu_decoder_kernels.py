@@ -91,11 +91,13 @@ def test_qk_norm_rope_cache(dev, rows, nh, nkv):
     assert kc[:, :, :p].abs().sum().item() == 0 and vc[:, :, p + 1:].abs().sum().item() == 0
 
 
-@pytest.mark.parametrize("rows,nh,nkv,length", [(1, 64, 8, 1), (1, 64, 8, 64), (1, 64, 8, 577), (8, 64, 8, 300),
-                                                (2, 4, 2, 130)])
-def test_attention_over_prefix(dev, rows, nh, nkv, length):
+@pytest.mark.parametrize("rows,nh,nkv,length,max_len", [(1, 64, 8, 1, 770), (1, 64, 8, 64, 770), (1, 64, 8, 577, 770),
+                                                        (8, 64, 8, 300, 770), (2, 4, 2, 130, 770),
+                                                        (1, 64, 8, 4100, 4160)])
+def test_attention_over_prefix(dev, rows, nh, nkv, length, max_len):
+    """Against fp32 attention on the CPU; fills of one position, a whole
+    split, partial splits, and 65 splits of a longer cache."""
     lib, L = _lib()
-    max_len = 770
     g = torch.Generator().manual_seed(length)
     q = torch.randn(rows, nh, 128, generator=g).bfloat16()
     kc = torch.randn(rows, nkv, max_len, 128, generator=g).bfloat16()
@@ -122,8 +124,85 @@ def test_attention_over_prefix(dev, rows, nh, nkv, length):
     assert (got - want).abs().max().item() < 0.05
 
 
+@pytest.mark.parametrize("rows,nh,nkv,pos", [(1, 64, 8, 0), (1, 64, 8, 63), (1, 64, 8, 64), (1, 64, 8, 577),
+                                             (8, 64, 8, 300), (2, 4, 2, 130), (3, 40, 8, 769)])
+def test_attention_rope_equals_separate(dev, rows, nh, nkv, pos):
+    """qs_dec_attention_rope (q/k norm + rotary inside the attention's split
+    launch) gives the bits of qs_dec_qk_norm_rope then qs_dec_attention: the
+    output, the key and value caches at pos, and nothing else of the caches
+    written.  Positions at a split's first and last slot and the cache's end."""
+    lib, L = _lib()
+    max_len = 770
+    g = torch.Generator().manual_seed(pos + rows)
+    q = torch.randn(rows, nh * 128, generator=g).bfloat16().to(dev)
+    k = torch.randn(rows, nkv * 128, generator=g).bfloat16().to(dev)
+    v = torch.randn(rows, nkv * 128, generator=g).bfloat16().to(dev)
+    qw = (1 + 0.1 * torch.randn(128, generator=g)).bfloat16().to(dev)
+    kw = (1 + 0.1 * torch.randn(128, generator=g)).bfloat16().to(dev)
+    ang = torch.arange(max_len)[:, None] * (1e6 ** (-torch.arange(64) / 64))[None]
+    cos_t = torch.cat([ang.cos(), ang.cos()], 1).bfloat16().to(dev)
+    sin_t = torch.cat([ang.sin(), ang.sin()], 1).bfloat16().to(dev)
+    kc0 = torch.randn(rows, nkv, max_len, 128, generator=g).bfloat16().to(dev)
+    vc0 = torch.randn(rows, nkv, max_len, 128, generator=g).bfloat16().to(dev)
+    p = torch.full((1,), pos, dtype=torch.long, device=dev)
+    ws = torch.empty(int(L.qs_dec_attention_workspace_bytes(rows, nkv, max_len)), dtype=torch.uint8, device=dev)
+    st = lib.stream_of(q)
+    scale = 128 ** -0.5
+    kc1, vc1 = kc0.clone(), vc0.clone()
+    qn = torch.empty_like(q)
+    want = torch.empty_like(q)
+    lib.check(L.qs_dec_qk_norm_rope(lib.ptr(q), lib.ptr(k), lib.ptr(v), lib.ptr(qw), lib.ptr(kw), lib.ptr(cos_t),
+                                    lib.ptr(sin_t), lib.ptr(p), lib.ptr(qn), lib.ptr(kc1), lib.ptr(vc1), rows, nh, nkv,
+                                    128, max_len, 1e-6, st))
+    lib.check(L.qs_dec_attention(lib.ptr(qn), lib.ptr(kc1), lib.ptr(vc1), lib.ptr(p), lib.ptr(want), nh * 128,
+                                 lib.ptr(ws), ws.numel(), rows, nh, nkv, 128, max_len, scale, st))
+    kc2, vc2 = kc0.clone(), vc0.clone()
+    got = torch.empty_like(q)
+    lib.check(L.qs_dec_attention_rope(lib.ptr(q), lib.ptr(k), lib.ptr(v), lib.ptr(qw), lib.ptr(kw), lib.ptr(cos_t),
+                                      lib.ptr(sin_t), lib.ptr(p), lib.ptr(kc2), lib.ptr(vc2), lib.ptr(got), nh * 128,
+                                      lib.ptr(ws), ws.numel(), rows, nh, nkv, 128, max_len, 1e-6, scale, st))
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    assert torch.equal(kc2, kc1) and torch.equal(vc2, vc1)
+    # the separate path wrote the new position and nothing else
+    assert torch.equal(vc1[:, :, pos], v.view(rows, nkv, 128))
+    keep = torch.ones(max_len, dtype=torch.bool, device=dev)
+    keep[pos] = False
+    assert torch.equal(kc2[:, :, keep], kc0[:, :, keep]) and torch.equal(vc2[:, :, keep], vc0[:, :, keep])
+
+
+def test_position_past_the_cache_writes_nothing(dev):
+    """pos = max_len: the kernels see it on the device and leave the caches
+    and the output untouched."""
+    lib, L = _lib()
+    rows, nh, nkv, max_len = 1, 8, 2, 128
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(rows, nh * 128, generator=g).bfloat16().to(dev)
+    kv = torch.randn(rows, nkv * 128, generator=g).bfloat16().to(dev)
+    w = torch.ones(128, dtype=torch.bfloat16, device=dev)
+    tab = torch.ones(max_len, 128, dtype=torch.bfloat16, device=dev)
+    kc = torch.randn(rows, nkv, max_len, 128, generator=g).bfloat16().to(dev)
+    vc = kc.clone()
+    kc0 = kc.clone()
+    out = torch.full((rows, nh * 128), 7.0, dtype=torch.bfloat16, device=dev)
+    qo = out.clone()
+    p = torch.full((1,), max_len, dtype=torch.long, device=dev)
+    ws = torch.empty(int(L.qs_dec_attention_workspace_bytes(rows, nkv, max_len)), dtype=torch.uint8, device=dev)
+    st = lib.stream_of(q)
+    lib.check(L.qs_dec_qk_norm_rope(lib.ptr(q), lib.ptr(kv), lib.ptr(kv), lib.ptr(w), lib.ptr(w), lib.ptr(tab),
+                                    lib.ptr(tab), lib.ptr(p), lib.ptr(qo), lib.ptr(kc), lib.ptr(vc), rows, nh, nkv, 128,
+                                    max_len, 1e-6, st))
+    lib.check(L.qs_dec_attention_rope(lib.ptr(q), lib.ptr(kv), lib.ptr(kv), lib.ptr(w), lib.ptr(w), lib.ptr(tab),
+                                      lib.ptr(tab), lib.ptr(p), lib.ptr(kc), lib.ptr(vc), lib.ptr(out), nh * 128,
+                                      lib.ptr(ws), ws.numel(), rows, nh, nkv, 128, max_len, 1e-6, 0.1, st))
+    torch.cuda.synchronize()
+    assert torch.equal(kc, kc0) and torch.equal(vc, kc0)
+    assert (out == 7.0).all() and (qo == 7.0).all()
+
+
 def test_attention_workspace_and_argument_checks(dev):
     lib, L = _lib()
+    # per (row, kv head, split of 64): max and sum of 16 heads, 16 x 128 outputs
     assert L.qs_dec_attention_workspace_bytes(1, 8, 770) == 1 * 8 * math.ceil(770 / 64) * (32 + 16 * 128) * 4
     x = torch.zeros(64, dtype=torch.bfloat16, device=dev)
     pos = torch.zeros(1, dtype=torch.long, device=dev)
@@ -134,6 +213,11 @@ def test_attention_workspace_and_argument_checks(dev):
                               1, 64, 2, 128, 16, 0.1, None) != 0
     assert L.qs_dec_attention(lib.ptr(x), lib.ptr(x), lib.ptr(x), lib.ptr(pos), lib.ptr(x), 64 * 128, lib.ptr(x), 16,
                               1, 64, 8, 128, 16, 0.1, None) != 0
+    # the same refusals with the norm + rotary inside
+    X = lib.ptr(x)
+    for ldo, wsb, nkv, hd in [(64 * 64, 1 << 20, 8, 64), (64 * 128, 1 << 20, 2, 128), (64 * 128, 16, 8, 128)]:
+        assert L.qs_dec_attention_rope(X, X, X, X, X, X, X, lib.ptr(pos), X, X, X, ldo, X, wsb, 1, 64, nkv, hd, 16,
+                                       1e-6, 0.1, None) != 0
 
 
 @pytest.mark.parametrize("rows,m", [(1, 25600), (8, 25600), (3, 1536)])
