@@ -186,6 +186,34 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* q, uint
   const int G = nh / nkv;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, qd = lane >> 4, r16 = lane & 15;
   const LaneX lx = lane_x_init();
+  // the split's keys and values are requested first: they depend only on the
+  // position, and arrive while the queries are staged
+  const uint16_t* kbase = kc + ((int64_t)b * nkv + g) * max_len * 128;
+  const uint16_t* vbase = vc + ((int64_t)b * nkv + g) * max_len * 128;
+  // scores: wave w, positions p0 + 16 w + r16 (column r16 of the tile)
+  int64_t pk = p0 + 16 * w + r16;
+  const bool pvalid = pk < len;
+  if (!pvalid) pk = len - 1;  // a valid row, masked below
+  uint4 kg[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) kg[ks] = *reinterpret_cast<const uint4*>(kbase + pk * 128 + 32 * ks + 8 * qd);
+  // values: wave w, dims 32 w + 16 dt + r16, positions p0 + 32 ks + 8 qd + 2 i
+  // (+1), clamped into the filled prefix (probability 0 there; any finite
+  // cached row)
+  uint32_t vg[2][2][4][2];
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int d = 32 * w + 16 * dt + r16;
+        int64_t pa = p0 + 32 * ks + 8 * qd + 2 * i, pb = pa + 1;
+        pa = pa < len ? pa : len - 1;
+        pb = pb < len ? pb : len - 1;
+        vg[dt][ks][i][0] = vbase[pa * 128 + d];
+        vg[dt][ks][i][1] = vbase[pb * 128 + d];
+      }
   __shared__ __attribute__((aligned(16))) uint16_t Kn[ROPE ? 128 : 8], Vn[ROPE ? 128 : 8];
   const int64_t pos = len - 1;
   const bool own = ROPE && pos < p0 + kSplit;  // the split holds the new position
@@ -231,17 +259,11 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* q, uint
     *reinterpret_cast<uint4*>(Qs + row * kQStride + c8) = val;
   }
   __syncthreads();
-  const uint16_t* kbase = kc + ((int64_t)b * nkv + g) * max_len * 128;
-  const uint16_t* vbase = vc + ((int64_t)b * nkv + g) * max_len * 128;
-  // scores: wave w, positions p0 + 16 w + r16 (column r16 of the tile)
-  int64_t pk = p0 + 16 * w + r16;
-  const bool pvalid = pk < len;
-  if (!pvalid) pk = len - 1;  // a valid row, masked below
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
     const bf16x8v a = __builtin_bit_cast(bf16x8v, *reinterpret_cast<const uint4*>(Qs + r16 * kQStride + 32 * ks + 8 * qd));
-    uint4 kb = *reinterpret_cast<const uint4*>(kbase + pk * 128 + 32 * ks + 8 * qd);
+    uint4 kb = kg[ks];
     if constexpr (ROPE) {
       // the new position from LDS (its cache row is written at the end)
       const uint4 kl = *reinterpret_cast<const uint4*>(Kn + 32 * ks + 8 * qd);
@@ -293,6 +315,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* q, uint
     out[16 + tid] = (red[1][0][tid] + red[1][1][tid]) + (red[1][2][tid] + red[1][3][tid]);
   }
   // values: wave w, dims 32 w .. 32 w + 31 (two tiles of 16), positions in two k-steps of 32
+  // (loaded at the start)
 #pragma unroll
   for (int dt = 0; dt < 2; ++dt) {
     const int d = 32 * w + 16 * dt + r16;
@@ -304,11 +327,13 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t* q, uint
       uint32_t vb[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        int64_t pa = p0 + 32 * ks + 8 * qd + 2 * i, pb = pa + 1;
-        pa = pa < len ? pa : len - 1;  // probability 0 there; any finite cached row
-        pb = pb < len ? pb : len - 1;
-        uint32_t va = vbase[pa * 128 + d], vv = vbase[pb * 128 + d];
-        if constexpr (ROPE) {  // a select of loaded values: no wait on the global loads
+        uint32_t va = vg[dt][ks][i][0], vv = vg[dt][ks][i][1];
+        if constexpr (ROPE) {
+          // the positions the loads used (clamped like them): the new one
+          // takes its value from LDS, a select of loaded values
+          int64_t pa = p0 + 32 * ks + 8 * qd + 2 * i, pb = pa + 1;
+          pa = pa < len ? pa : len - 1;
+          pb = pb < len ? pb : len - 1;
           va = pa == pos ? vn : va;
           vv = pb == pos ? vn : vv;
         }
@@ -337,9 +362,12 @@ __global__ __launch_bounds__(128) void attn_combine_kernel(const float* part, co
   if (len > max_len) return;  // a position past the cache (a caller's error)
   const int ns = (int)((len + kSplit - 1) / kSplit);
   const float* base = part + ((int64_t)b * nkv + g) * nsplit * kPartFloats;
+  // the loads of four splits go out together (the same sums in split order)
   float M = -INFINITY;
+#pragma unroll 4
   for (int s = 0; s < ns; ++s) M = fmaxf(M, base[s * kPartFloats + hl]);
   float L = 0.0f, O = 0.0f;
+#pragma unroll 4
   for (int s = 0; s < ns; ++s) {
     const float* p = base + s * kPartFloats;
     const float f = __expf(p[hl] - M);
