@@ -275,14 +275,18 @@ typedef struct qs_preop {
 } qs_preop;
 
 /* qs_linear_forward_group on the rows the pre-operation makes of x (bf16),
- * in the same launch: no counterpart in the reference (its decoder runs the
+ * in its launches: no counterpart in the reference (its decoder runs the
  * norm as a framework kernel before each QuantizedLinear.forward,
  * scripts/eval_ppl.py:41-65); for decode loops that would otherwise launch it
- * on its own (every work-group of the launch redoes the norm, so it pays at
- * one row).  One-launch calls only: 1-2 rows, n a multiple of 256 up to
- * 16384, rows of x, x2 and h_out 8-byte aligned with strides that are
- * multiples of 4, weight 8-byte aligned; anything else returns
- * QS_ERR_UNSUPPORTED (the caller runs the norm on its own). */
+ * on its own.  1-2 rows with n a multiple of 256 up to 16384 (inside the
+ * one-launch kernel: every work-group redoes the norm, so it pays at one
+ * row), or 3-16 rows with n on the multi-row chunk scheme -- a multiple of
+ * 256 up to 12288 with n / kron_pn >= 256 -- (inside the input-transform
+ * launch, one work-group per row and linear); rows of x, x2 and h_out 8-byte
+ * aligned with strides that are multiples of 4, weight 8-byte aligned;
+ * anything else returns QS_ERR_UNSUPPORTED (the caller runs the norm on its
+ * own).  Outputs and h_out bit-identical to qs_dec_rmsnorm followed by
+ * qs_linear_forward_group. */
 int qs_linear_forward_group_pre(const void *x, int64_t ldx, int64_t batch, int64_t n, int kron_pn,
                                 const float *kron_n, int count, const qs_linear_job *jobs, const qs_preop *pre,
                                 int y_dtype, void *workspace, size_t workspace_bytes, qs_stream_t stream);

@@ -332,15 +332,17 @@ def run_preop(x: Tensor, pre: dict) -> Tensor:
 def grouped_forward_pre(x: Tensor, linears, pre: dict):
     """``grouped_forward`` on the rows a pre-operation makes of bf16 x
     (``quantize.forward_packed_group``'s ``pre``: RMSNorm with the residual
-    add), inside the same launch for one row (``quantize.pre_ok``; every
-    work-group of the launch redoes the norm, which measured faster than the
-    norm's own launch at one row and slower at two), otherwise the norm on its
-    own launch first (``run_preop``); the outputs are the same either way.  No
-    counterpart in the reference, whose decoder runs the norm as a framework
-    kernel before each QuantizedLinear.forward."""
+    add), inside the group's launches where ``quantize.pre_ok`` accepts it
+    except at two rows (at one row every work-group of the one-launch kernel
+    redoes the norm, which measured faster than the norm's own launch, and
+    slower at two; at 3-16 rows the input-transform launch does it once per
+    row and linear), otherwise the norm on its own launch first
+    (``run_preop``); the outputs are the same either way.  No counterpart in
+    the reference, whose decoder runs the norm as a framework kernel before
+    each QuantizedLinear.forward."""
     from .quantize import pre_ok
     n = x.shape[-1]
-    if x.numel() == n and groupable(x, linears) and pre_ok(x, n, pre):
+    if x.numel() != 2 * n and groupable(x, linears) and pre_ok(x, n, pre):
         return _grouped(x, linears, pre=pre)
     return grouped_forward(run_preop(x, pre), linears)
 

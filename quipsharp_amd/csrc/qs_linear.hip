@@ -1073,7 +1073,8 @@ size_t group_prefix_bytes(int count, int64_t n, M m_of) {
 // group's, so the outputs equal separate calls up to the fp32 summation order.
 static int forward_group_rows(const void* x, int x_dtype, int64_t ldx, int64_t batch, int64_t n, int kron_pn,
                               const float* kron_n, int count, const qs_linear_job* jobs, int y_dtype, char* ws,
-                              size_t ws_bytes, void* mv_begin, void* mv_end, hipStream_t s, int sbits) {
+                              size_t ws_bytes, void* mv_begin, void* mv_end, hipStream_t s, int sbits,
+                              const FusedPre* pre) {
   const bool wide = batch >= kWideMinBatch;
   BatchedPass P[QS_MAX_GROUP];
   size_t off = group_prefix_bytes(count, n, [&](int g) { return jobs[g].m; });
@@ -1120,7 +1121,7 @@ static int forward_group_rows(const void* x, int x_dtype, int64_t ldx, int64_t b
     }
     off += W.total;
   }
-  int rc = launch_bx_group(P, count, s);
+  int rc = launch_bx_group(P, count, s, pre);
   if (rc) return rc;
   if (wide) {
     if (mv_begin) QS_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(mv_begin), s));
@@ -1210,8 +1211,11 @@ static int forward_group_impl(const void* x, int x_dtype, int64_t ldx, int64_t b
   const bool one_launch = fused_eligible(batch, n, x_dtype, kron_pn) && fused_x_aligned(x, x_dtype, ldx);
   QS_REQUIRE(n % 256 == 0 && n / kron_pn >= 256,
              "grouped forward needs n a multiple of 256 with n / kron_pn >= 256 (got n %lld)", (long long)n);
-  if (pre) QS_SUPPORTED(one_launch, "a pre-operation runs in one-launch calls only (batch %lld, n %lld)",
-                        (long long)batch, (long long)n);
+  if (pre)
+    QS_SUPPORTED(one_launch || (batch >= 3 && batch <= 16 && chunk_transform_fits(n, kron_pn)),
+                 "a pre-operation runs in one-launch calls (1-2 rows) and in 3-16 row calls on the chunk scheme "
+                 "(batch %lld, n %lld)",
+                 (long long)batch, (long long)n);
   QS_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255) == 0, "workspace must be 256-byte aligned");
   size_t need = 0;
   for (int g = 0; g < count; ++g) {
@@ -1240,7 +1244,7 @@ static int forward_group_impl(const void* x, int x_dtype, int64_t ldx, int64_t b
   char* ws = static_cast<char*>(workspace);
   if (!one_launch && chunk_transform_fits(n, kron_pn))
     return forward_group_rows(x, x_dtype, ldx, batch, n, kron_pn, kron_n, count, jobs, y_dtype, ws, workspace_bytes,
-                              mv_begin, mv_end, s, jobs[0].sign_bits ? 1 : 0);
+                              mv_begin, mv_end, s, jobs[0].sign_bits ? 1 : 0, pre);
   if (!one_launch) {
     // n outside the chunk scheme of the multi-row kernels: one forward per
     // linear, one after the other on the stream, each with the whole
@@ -1334,10 +1338,13 @@ extern "C" int qs_linear_forward_group_pre(const void* x, int64_t ldx, int64_t b
   QS_REQUIRE(!pre->x2 || pre->ldx2 >= n, "pre-operation: ldx2 %lld < n", (long long)pre->ldx2);
   QS_REQUIRE(!pre->h_out || pre->ldo >= n, "pre-operation: ldo %lld < n", (long long)pre->ldo);
   auto a8 = [](const void* p, int64_t ld) { return (reinterpret_cast<uintptr_t>(p) & 7) == 0 && ld % 4 == 0; };
-  QS_SUPPORTED(batch <= 2 && n % 256 == 0 && n / 256 <= 64 && a8(x, ldx) && (!pre->x2 || a8(pre->x2, pre->ldx2)) &&
+  QS_SUPPORTED(((batch <= 2 && n % 256 == 0 && n / 256 <= 64) ||
+                (batch >= 3 && batch <= 16 && chunk_transform_fits(n, kron_pn))) &&
+                   a8(x, ldx) && (!pre->x2 || a8(pre->x2, pre->ldx2)) &&
                    (reinterpret_cast<uintptr_t>(pre->weight) & 7) == 0 && (!pre->h_out || a8(pre->h_out, pre->ldo)),
-               "pre-operation: 1-2 rows, n a multiple of 256 up to 16384, 8-byte aligned rows (got batch %lld, "
-               "n %lld)", (long long)batch, (long long)n);
+               "pre-operation: 1-2 rows with n a multiple of 256 up to 16384, or 3-16 rows with n on the chunk "
+               "scheme (up to 12288), 8-byte aligned rows (got batch %lld, n %lld)",
+               (long long)batch, (long long)n);
   if (pre->h_out) {
     const size_t out_bytes = (size_t)((batch - 1) * pre->ldo + n) * 2;
     QS_REQUIRE(!overlaps(pre->h_out, out_bytes, x, (size_t)((batch - 1) * ldx + n) * 2) &&

@@ -31,6 +31,7 @@
 
 #include "qs_forward_dev.h"
 #include "qs_linear_dev.h"
+#include "qs_preop_dev.h"
 
 namespace qs {
 namespace {
@@ -63,6 +64,16 @@ struct BxArgs {
   int sbits;      // sv of every linear is packed sign bits
   int per;        // work-groups per linear: linear blockIdx / per
   BxJob job[QS_MAX_GROUP];
+  // RMSNorm pre-operation (PRE kernels): x is the residual stream h (bf16
+  // rows, 8-byte loads), the linears read bf16(nw * bf16(h' * rs)) of
+  // h' = bf16(h + x2) (x2 may be null), and the first linear's work-groups
+  // write h' to h_out (may be null)
+  const uint16_t* x2;
+  int64_t ldx2;
+  const uint16_t* nw;
+  uint16_t* h_out;
+  int64_t ldo;
+  float eps;
 };
 
 // LDS of the per-row transform kernels holding CPW chunks per wave (S <= 16
@@ -75,14 +86,19 @@ struct RowLds {
   static constexpr int kMh = kY + 16 * CPW * kYStride * 4;
   static constexpr int kMl = kMh + kMBytes;
   static constexpr int kMisc = kMl + kMBytes;
-  static constexpr int kTotal = kMisc + 4 * kWaves;
+  static constexpr int kPre = kMisc + 4 * kWaves;  // the pre-operation's wave sums
+  static constexpr int kTotal = kPre + 4 * kWaves;
 };
 static_assert(16 * kCPW >= kMaxS, "chunk rows");
 inline int chunks_per_wave(int64_t S) { return S <= kWaves ? 1 : S <= 2 * kWaves ? 2 : 3; }
 
 // Rows b = lb, lb + per, ... of linear blockIdx / per (lb = blockIdx % per):
 // the next row's activations are loaded while this row is transformed.
-template <int CPW, bool SB>
+// PRE: each row is first put through the RMSNorm pre-operation -- its rs
+// taken in rmsnorm_kernel's layout and order (rms_row_scale), then h' and x'
+// formed element by element in this kernel's layout -- so the operand equals
+// that of qs_dec_rmsnorm followed by the plain kernel, bit for bit.
+template <int CPW, bool SB, bool PRE>
 __global__ __launch_bounds__(kThreads) void bx_kernel(BxArgs A) {
   using L = RowLds<CPW>;
   extern __shared__ __attribute__((aligned(16))) char lds[];
@@ -90,6 +106,7 @@ __global__ __launch_bounds__(kThreads) void bx_kernel(BxArgs A) {
   uint16_t* Mh = reinterpret_cast<uint16_t*>(lds + L::kMh);
   uint16_t* Ml = reinterpret_cast<uint16_t*>(lds + L::kMl);
   float* wsum = reinterpret_cast<float*>(lds + L::kMisc);
+  float* pre_wsum = reinterpret_cast<float*>(lds + L::kPre);
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
   const int q = lane >> 4, r16 = lane & 15;
@@ -101,6 +118,12 @@ __global__ __launch_bounds__(kThreads) void bx_kernel(BxArgs A) {
 
   XRawT<CPW> xr;
   load_x_raw(X, J.sv, lb, w, lane, xr);
+  uint2 nwq[CPW];  // PRE: the norm weights of this thread's quads
+#pragma unroll
+  for (int u = 0; u < CPW; ++u) {
+    const int c = w + kWaves * u;
+    nwq[u] = PRE && c < A.Sn ? *reinterpret_cast<const uint2*>(A.nw + 256 * c + 4 * lane) : make_uint2(0, 0);
+  }
   {
     float kmv[3];
     mmat_load(kmv, A.Sn, A.lsh_n, A.pn, A.Kn, tid);
@@ -108,7 +131,34 @@ __global__ __launch_bounds__(kThreads) void bx_kernel(BxArgs A) {
   }
   for (int b = lb; b < A.B; b += stride) {
     float xv[CPW][4];
-    finish_x(X, xr, w, lane, xv);
+    if constexpr (PRE) {
+      const uint16_t* hrow = static_cast<const uint16_t*>(A.x) + (int64_t)b * A.ldx;
+      const uint16_t* drow = A.x2 ? A.x2 + (int64_t)b * A.ldx2 : nullptr;
+      uint2 dq[CPW];
+#pragma unroll
+      for (int u = 0; u < CPW; ++u) {
+        const int c = w + kWaves * u;
+        dq[u] = drow && c < A.Sn ? *reinterpret_cast<const uint2*>(drow + 256 * c + 4 * lane) : make_uint2(0, 0);
+      }
+      const float rs = rms_row_scale(hrow, drow, A.n, A.eps, w, lane, lx, pre_wsum);
+#pragma unroll
+      for (int u = 0; u < CPW; ++u) {
+        const int c = w + kWaves * u;
+        uint32_t hp[2] = {xr.v[u].x, xr.v[u].y};  // h as loaded
+        if (drow) {
+          hp[0] = rms_pair_resid(hp[0], dq[u].x);
+          hp[1] = rms_pair_resid(hp[1], dq[u].y);
+        }
+        if (g == 0 && A.h_out && c < A.Sn)
+          *reinterpret_cast<uint2*>(A.h_out + (int64_t)b * A.ldo + 256 * c + 4 * lane) = make_uint2(hp[0], hp[1]);
+        const uint4 xq = make_uint4(rms_pair_apply(hp[0], nwq[u].x, rs), rms_pair_apply(hp[1], nwq[u].y, rs), 0, 0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xv[u][j] = 0.0f;
+        if (c < A.Sn) finish_chunk(X, xq, xr.s[u], lane, xv[u]);
+      }
+    } else {
+      finish_x(X, xr, w, lane, xv);
+    }
     if (b + stride < A.B) load_x_raw(X, J.sv, b + stride, w, lane, xr);  // the next row
     float ss = 0.0f;
 #pragma unroll
@@ -627,12 +677,12 @@ int launch_bm_h(const BmArgs& M, int oc, bool sb, unsigned grid, hipStream_t str
   }
 }
 
-template <int CPW, bool SB>
+template <int CPW, bool SB, bool PRE>
 int launch_bx_cs(const BxArgs& X, unsigned grid, hipStream_t stream) {
   static int done = 0;
-  const int rc = lds_checked((const void*)bx_kernel<CPW, SB>, RowLds<CPW>::kTotal, &done);
+  const int rc = lds_checked((const void*)bx_kernel<CPW, SB, PRE>, RowLds<CPW>::kTotal, &done);
   if (rc) return rc;
-  hipLaunchKernelGGL((bx_kernel<CPW, SB>), dim3(grid), dim3(kThreads), RowLds<CPW>::kTotal, stream, X);
+  hipLaunchKernelGGL((bx_kernel<CPW, SB, PRE>), dim3(grid), dim3(kThreads), RowLds<CPW>::kTotal, stream, X);
   QS_LAUNCHED("bx_kernel");
   return QS_OK;
 }
@@ -657,8 +707,10 @@ int launch_by_cs(const ByArgs& Y, unsigned grid, int maxsg, hipStream_t stream) 
   return launch_by_gc<0, CPW, SB>(Y, grid, stream);
 }
 template <int CPW>
-int launch_bx_cpw(const BxArgs& X, unsigned grid, hipStream_t stream) {
-  return X.sbits ? launch_bx_cs<CPW, true>(X, grid, stream) : launch_bx_cs<CPW, false>(X, grid, stream);
+int launch_bx_cpw(const BxArgs& X, unsigned grid, bool pre, hipStream_t stream) {
+  if (pre)
+    return X.sbits ? launch_bx_cs<CPW, true, true>(X, grid, stream) : launch_bx_cs<CPW, false, true>(X, grid, stream);
+  return X.sbits ? launch_bx_cs<CPW, true, false>(X, grid, stream) : launch_bx_cs<CPW, false, false>(X, grid, stream);
 }
 template <int CPW>
 int launch_by_cpw(const ByArgs& Y, unsigned grid, int maxsg, hipStream_t stream) {
@@ -667,7 +719,7 @@ int launch_by_cpw(const ByArgs& Y, unsigned grid, int maxsg, hipStream_t stream)
 
 }  // namespace
 
-int launch_bx_group(const BatchedPass* P, int count, hipStream_t stream) {
+int launch_bx_group(const BatchedPass* P, int count, hipStream_t stream, const FusedPre* pre) {
   QS_REQUIRE(count >= 1 && count <= QS_MAX_GROUP, "input transform: 1..%d linears", QS_MAX_GROUP);
   const BatchedPass& P0 = P[0];
   QS_REQUIRE(chunk_transform_fits(P0.n, P0.pn), "input transform: n outside the chunk scheme");
@@ -697,15 +749,26 @@ int launch_bx_group(const BatchedPass* P, int count, hipStream_t stream) {
                "input transform: linears of one launch share x and its transform");
     X.job[j] = BxJob{Q.sv, Q.x2h, Q.sg, Q.xmul};
   }
+  if (pre) {
+    QS_REQUIRE(pre->kind == QS_PREOP_RMSNORM && X.x_dtype == QS_DTYPE_BF16 && X.x_vec && pre->weight &&
+                   X.n <= 16384,
+               "input transform: the RMSNorm pre-operation needs bf16 rows loaded 8 bytes at a time");
+    X.x2 = static_cast<const uint16_t*>(pre->x2);
+    X.ldx2 = pre->ldx2;
+    X.nw = static_cast<const uint16_t*>(pre->weight);
+    X.h_out = static_cast<uint16_t*>(pre->h_out);
+    X.ldo = pre->ldo;
+    X.eps = pre->eps;
+  }
   const unsigned grid = (unsigned)(X.per * count);
   switch (cpw) {
-    case 1: return launch_bx_cpw<1>(X, grid, stream);
-    case 2: return launch_bx_cpw<2>(X, grid, stream);
-    default: return launch_bx_cpw<3>(X, grid, stream);
+    case 1: return launch_bx_cpw<1>(X, grid, pre != nullptr, stream);
+    case 2: return launch_bx_cpw<2>(X, grid, pre != nullptr, stream);
+    default: return launch_bx_cpw<3>(X, grid, pre != nullptr, stream);
   }
 }
 
-int launch_bx_rows(const BatchedPass& P, hipStream_t stream) { return launch_bx_group(&P, 1, stream); }
+int launch_bx_rows(const BatchedPass& P, hipStream_t stream) { return launch_bx_group(&P, 1, stream, nullptr); }
 
 int launch_by_group(const BatchedPass* P, int count, hipStream_t stream) {
   QS_REQUIRE(count >= 1 && count <= QS_MAX_GROUP, "output transform: 1..%d linears", QS_MAX_GROUP);

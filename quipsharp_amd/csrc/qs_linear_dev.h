@@ -99,7 +99,7 @@ int launch_bx_rows(const BatchedPass& P, hipStream_t stream);
 int launch_by_rows(const BatchedPass& P, hipStream_t stream);
 // Input transforms of several linears of one x (each its own sv, x2h, sg,
 // xmul) in one launch, bit-identical to one launch_bx_rows per linear.
-int launch_bx_group(const BatchedPass* P, int count, hipStream_t stream);
+int launch_bx_group(const BatchedPass* P, int count, hipStream_t stream, const FusedPre* pre = nullptr);
 // The decode-matvec of a pass on its own (any n; operand in x2h / sg,
 // fragment-major, 16 rows), y1p[SG][B][m].
 int launch_bm(const BatchedPass& P, hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop,

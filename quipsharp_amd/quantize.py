@@ -336,8 +336,8 @@ def forward_packed_group(x: Tensor, linears, out_dtype=None, workspace: Tensor =
     pre-operation makes of the bf16 ``x`` inside the same launch --
     ``{"kind": "rmsnorm", "delta": Tensor or None, "weight": Tensor, "h_out":
     Tensor or None, "eps": float}`` (input = RMSNorm(x + delta), x + delta
-    written to h_out); 1-2 rows only (``pre_ok``), bit-identical to
-    ``qs_dec_rmsnorm`` followed by the grouped forward."""
+    written to h_out); 1-2 rows, or 3-16 on the chunk scheme (``pre_ok``),
+    bit-identical to ``qs_dec_rmsnorm`` followed by the grouped forward."""
     count = len(linears)
     if not 1 <= count <= _lib.QS_MAX_GROUP:
         raise ValueError(f"1..{_lib.QS_MAX_GROUP} linears per group, got {count}")
@@ -412,13 +412,20 @@ def _rows_of(t: Tensor, n: int, B: int, what: str) -> Tensor:
 
 
 def pre_ok(x: Tensor, n: int, pre: dict) -> bool:
-    """Whether a grouped forward of x can run ``pre`` in its launch: the norm,
-    bf16 rows, 1-2 of them, n a multiple of 256 up to 16384, 8-byte aligned
-    rows (qs_linear_forward_group_pre)."""
+    """Whether a grouped forward of x can run ``pre`` in its launches: the
+    norm, bf16 rows, 8-byte aligned; 1-2 rows with n a multiple of 256 up to
+    16384 (in the one-launch kernel), or 3-16 rows with n on the multi-row
+    kernels' chunk scheme -- a multiple of 256 up to 12288 whose power-of-two
+    part is at least 256 -- (in the input-transform launch)
+    (qs_linear_forward_group_pre)."""
     rows = x.numel() // n if n else 0
     others = [pre.get("delta"), pre.get("h_out")]
-    return (pre.get("kind") == "rmsnorm" and x.dtype == torch.bfloat16 and 1 <= rows <= 2 and n % 256 == 0
-            and n <= 16384
+    fn = kron_factor(n) if n else None
+    if 1 <= rows <= 2:
+        shape_ok = n % 256 == 0 and n <= 16384
+    else:
+        shape_ok = 3 <= rows <= 16 and fn is not None and n % 256 == 0 and n <= 12288 and n // fn[0] >= 256
+    return (pre.get("kind") == "rmsnorm" and x.dtype == torch.bfloat16 and shape_ok
             and all(t is None or (t.dtype == torch.bfloat16 and t.data_ptr() % 8 == 0) for t in others)
             and x.data_ptr() % 8 == 0 and (rows == 1 or x.reshape(-1, n).stride(0) % 4 == 0))
 

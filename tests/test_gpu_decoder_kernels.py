@@ -248,14 +248,20 @@ def _lins(dev, shapes, n, seed):
     return [_rand_linear(dev, rng, m, n, 1, g == 0) for g, m in enumerate(shapes)]
 
 
-@pytest.mark.parametrize("shapes,n", [([8192, 1024, 1024], 5120), ([4096, 4096, 4096], 4096), ([25600, 25600], 5120),
-                                      ([11008], 16384)])
-@pytest.mark.parametrize("B", [1, 2])
+_PRE_SHAPES = [([8192, 1024, 1024], 5120), ([4096, 4096, 4096], 4096), ([25600, 25600], 5120), ([11008], 16384)]
+
+
+@pytest.mark.parametrize("shapes,n,B", [(sh, n, B) for sh, n in _PRE_SHAPES for B in (1, 2)]
+                         + [(sh, n, B) for sh, n in _PRE_SHAPES[:3] for B in (3, 8, 16)]
+                         + [([1536, 2304], 3584, 8), ([4096], 11008, 8)])
 @pytest.mark.parametrize("residual", [True, False])
 def test_group_pre_rmsnorm_equals_separate(dev, shapes, n, B, residual):
-    """RMSNorm (with the residual add) inside the grouped one-launch forward:
-    outputs and the residual stream bit-identical to qs_dec_rmsnorm followed
-    by the grouped forward."""
+    """RMSNorm (with the residual add) inside the grouped forward -- the
+    one-launch kernel at 1-2 rows, the input-transform launch at 3-16 rows
+    (n = 3584: odd factor 7; n = 11008: odd factor 43, three chunks per
+    wave) -- outputs and the
+    residual stream bit-identical to qs_dec_rmsnorm followed by the grouped
+    forward."""
     from quipsharp_amd.quantize import forward_packed_group, pre_ok
     print(f"case: group pre rmsnorm {shapes} n={n} B={B} residual={residual}", flush=True)
     lib, L = _lib()
@@ -279,8 +285,8 @@ def test_group_pre_rmsnorm_equals_separate(dev, shapes, n, B, residual):
 
 
 def test_group_pre_refused_shapes(dev):
-    """Outside the one-launch kernel (3 rows), a norm wider than 16384 and an
-    h_out that overlaps x are refused on the host, nothing launched."""
+    """Past 16 rows (the wide path), a norm wider than 16384 and an h_out
+    that overlaps x are refused on the host, nothing launched."""
     from quipsharp_amd import _lib as lb
     from quipsharp_amd.quantize import pre_ok
     lib, L = _lib()
@@ -297,8 +303,8 @@ def test_group_pre_refused_shapes(dev):
         return L.qs_linear_forward_group_pre(lb.ptr(x), n, x.shape[0], n, 1, None, 1, jobs, pre, lb.QS_DTYPE_BF16,
                                              lb.ptr(ws), ws.numel(), lb.stream_of(x))
 
-    x3 = torch.randn(3, n, device=dev).bfloat16()
-    y3 = torch.full((3, 1024), 5.0, dtype=torch.bfloat16, device=dev)
+    x3 = torch.randn(17, n, device=dev).bfloat16()
+    y3 = torch.full((17, 1024), 5.0, dtype=torch.bfloat16, device=dev)
     op = lb.PreOp(lb.QS_PREOP_RMSNORM, None, n, lb.ptr(w), None, n, 1e-6)
     assert call(x3, op, y3) == 3 and not pre_ok(x3, n, {"kind": "rmsnorm"})
     x1 = torch.randn(1, n, device=dev).bfloat16()
