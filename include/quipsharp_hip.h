@@ -187,10 +187,9 @@ int qs_linear_forward(const void *x, int x_dtype, int64_t ldx, int64_t batch, in
  * QS_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; this entry
  * point calls no hipMalloc / hipFree.  Shapes whose workspace
  * (qs_linear_workspace_bytes) exceeds it return QS_ERR_UNSUPPORTED before
- * anything is launched.  Every shape with m, n <= 32768 fits at 1..8 rows, and
- * every shape with m * n <= 2^28 (all Qwen3-32B and Llama-2-70B layers) at
- * 1..64 rows; 25600 x 25600 at 16 rows does not, nor do wide prefill batches
- * (256 rows and more) of most shapes.  Every call on one GPU shares that
+ * anything is launched.  Every shape with m, n <= 32768 fits at 1..128 rows;
+ * wide prefill batches (256 rows and more) of most shapes do not (11008 x
+ * 4096 at 4096 rows needs 219 MB).  Every call on one GPU shares that
  * GPU's array: calls that may overlap on one GPU (other streams, other host
  * threads) race and must be serialised by the caller.  The array is zero when
  * loaded; every call advances the epoch in its first 256 bytes.

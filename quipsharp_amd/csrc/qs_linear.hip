@@ -124,8 +124,10 @@ WsLayout ws_layout(int64_t m, int64_t n, int64_t batch, int layout) {
     L.y1p = off; off = align256(off + (size_t)sgp * B * m * 4);
     if (layout == QS_LAYOUT_TILED) {
       // tagged partial sums of the 16-row decode-matvec that applies the
-      // output transform itself (written by no other kernel)
-      L.y1bt = off; off = align256(off + batched_slot_count(L.SG, B, m) * 8);
+      // output transform itself (written by no other kernel; only for m on
+      // the chunk scheme, bm_tail_eligible)
+      L.y1bt = off;
+      if (m <= kMaxN) off = align256(off + batched_slot_count(L.SG, B, m) * 8);
     }
   }
   L.total = off;

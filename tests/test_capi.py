@@ -84,8 +84,8 @@ def test_workspace_size(L):
 def test_noalloc_bound(L):
     """The allocation-free forward's array is the size the header states, and
     the shapes the header says fit do: every m, n <= 32768 (multiples of 256)
-    at 1..8 rows, every m n <= 2^28 at 1..64 rows; 25600 x 25600 at 16 rows
-    does not (qs_linear_forward_noalloc refuses what exceeds the array)."""
+    at 1..128 rows; a wide prefill batch (11008 x 4096 at 4096 rows) does not
+    (qs_linear_forward_noalloc refuses what exceeds the array)."""
     from quipsharp_amd import _lib
     text = open(os.path.join(ROOT, "include", "quipsharp_hip.h")).read()
     mib = int(re.search(r"#define QS_NOALLOC_SCRATCH_BYTES \(\(size_t\)(\d+) << 20\)", text).group(1))
@@ -94,10 +94,9 @@ def test_noalloc_bound(L):
     dims = range(256, 32769, 256)
     ws = L.qs_linear_workspace_bytes
     tiled = _lib.QS_LAYOUT_TILED
-    worst8 = max(ws(m, n, b, tiled) for m in dims for n in dims for b in (1, 2, 4, 8))
-    worst64 = max(ws(m, n, b, tiled) for m in dims for n in dims if m * n <= 1 << 28 for b in (9, 16, 17, 32, 64))
-    assert worst8 <= cap and worst64 <= cap, (worst8, worst64, cap)
-    assert ws(25600, 25600, 16, tiled) > cap
+    worst = max(ws(m, n, b, tiled) for m in dims for n in dims for b in (1, 2, 4, 8, 9, 16, 17, 32, 64, 128))
+    assert worst <= cap, (worst, cap)
+    assert ws(11008, 4096, 4096, tiled) > cap
 
 
 def test_group_argument_errors(L):
