@@ -12,9 +12,11 @@
 //    accumulate), then per slice (one wave) the 256-point transform and the
 //    fragment-major fp16 operand and group sums the decode-matvec reads.
 //  * by_big_kernel (output, work-group = (row b, output chunks 16 k .. 16 k +
-//    15)): the slice groups' partial sums of every chunk, the 256-point
-//    transform of each (chunk rows in LDS), then its 16 rows of M . h on the
-//    matrix cores, scale, su and bias.
+//    15)): the slice groups' partial sums of every chunk (chunk rows in LDS),
+//    its 16 rows of M . z on the matrix cores, then per output chunk (one
+//    wave) the 256-point transform, scale, su and bias -- M first, as in the
+//    input kernel, so that a work-group transforms its own 16 chunks rather
+//    than all S of the row.
 // Both replace the LDS-radix row kernels (xin_kernel, yout_kernel) for these
 // lengths (Qwen3-32B at 8 rows: 26 and 21 us per launch).
 #include "qs_forward_dev.h"
@@ -247,48 +249,59 @@ __global__ __launch_bounds__(kThreads) void by_big_kernel(ByBigArgs A) {
   const int lb = (int)blockIdx.x - J.wg0;
   const int b = lb / J.ngrp, k = lb - b * J.ngrp;
   const int Sm = J.Sm, Spad = (Sm + 31) & ~31;
-  const int t = 16 * w + r16;
-  // su and bias of this lane's outputs (rows r = 16 k + 4 q + j, column t);
-  // no bias: a dummy load from the partial sums (at least m floats), never
-  // used (the bias term is selected, not multiplied by 0)
+  // wave w finishes output chunk r = 16 k + w (elements t = lane + 64 j):
+  // its su and bias (no bias: a dummy load from the partial sums, at least m
+  // floats, never used -- the bias term is selected, not multiplied by 0)
+  const int r = 16 * k + w;
   const float* const bsrc = J.bias ? J.bias : J.y1p;
   const bool has_bias = J.bias != nullptr;
   int oidx[1][4];
   float suo[4], bio[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int r = 16 * k + 4 * q + j;
+    const int t = lane + 64 * j;
     oidx[0][j] = r < Sm ? out_elem(r, t) : -1;
     const int ii = r < Sm ? out_elem(r, t) : 0;
     suo[j] = load_su(J.su, SB, ii);
     bio[j] = bsrc[ii];
   }
-  // 1. h_c = H_256 (sum over the slice groups of chunk c), chunks c = w + 16 u
+  // 1. z_c = the sum over the slice groups of chunk c, chunks c = w + 16 u
   //    (element t = lane + 64 j), into the chunk rows
   {
     float zv[kByCPW][4];
     sum_partials_loop<kByCPW>(J.y1p, J.m, Sm, J.SG, A.B, b, w, lane, zv);
-    h256<kByCPW>(zv, lane, lx);
     store_chunks_lanes<kByCPW>(Y, Sm, w, lane, zv);
   }
   // 2. this work-group's 16 rows of M
   build_m_rows(Mh, Ml, k, Sm, Spad, J.lsh_m, J.pm, J.Km, tid);
   __syncthreads();
-  // 3. rows 16 k .. 16 k + 15 of M . h, column t
+  // 3. rows 16 k .. 16 k + 15 of M . z, column t = 16 w + r16
   floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+  const int tc = 16 * w + r16;
   for (int kb = 0; kb < (Spad >> 5); ++kb) {
-    const ZOperand z = z_operand(Y, Sm, t, q, kb);
+    const ZOperand z = z_operand(Y, Sm, tc, q, kb);
     const int off = r16 * kMStr + 32 * kb + 8 * q;
     const bf16x8 ah = ld_bf16x8(Mh + off);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, z.h, acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, z.l, acc, 0, 0, 0);
     if (J.pm > 1) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ld_bf16x8(Ml + off), z.h, acc, 0, 0, 0);
   }
+  __syncthreads();  // every wave has read the chunk rows
+  // 4. the 16 rows into the first 16 chunk rows; wave w then applies the
+  //    256-point transform to row w (output chunk r), scale, su and bias
+#pragma unroll
+  for (int j = 0; j < 4; ++j) Y[(4 * q + j) * kYStride + tc] = acc[j];
+  __syncthreads();
+  if (r >= Sm) return;  // no barrier follows
+  float v[1][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[0][j] = Y[w * kYStride + lane + 64 * j];
+  h256<1>(v, lane, lx);
   const float mul = J.scale_m * J.layer_scale * J.xmul[b];
   float out[1][4];
 #pragma unroll
   for (int j = 0; j < 4; ++j)
-    out[0][j] = apply_su(acc[j] * mul, suo[j], SB, oidx[0][j]) + (has_bias ? bio[j] : 0.0f);
+    out[0][j] = apply_su(v[0][j] * mul, suo[j], SB, oidx[0][j]) + (has_bias ? bio[j] : 0.0f);
   store_outputs(J.y, A.y_dtype, (int64_t)b * J.ldy, oidx, out);
 }
 
