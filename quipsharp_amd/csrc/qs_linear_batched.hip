@@ -94,10 +94,11 @@ inline int chunks_per_wave(int64_t S) { return S <= kWaves ? 1 : S <= 2 * kWaves
 
 // Rows b = lb, lb + per, ... of linear blockIdx / per (lb = blockIdx % per):
 // the next row's activations are loaded while this row is transformed.
-// PRE: each row is first put through the RMSNorm pre-operation -- its rs
-// taken in rmsnorm_kernel's layout and order (rms_row_scale), then h' and x'
-// formed element by element in this kernel's layout -- so the operand equals
-// that of qs_dec_rmsnorm followed by the plain kernel, bit for bit.
+// PRE: each row is first put through the RMSNorm pre-operation -- h' formed
+// in this kernel's layout and staged in LDS, its rs taken from there in
+// rmsnorm_kernel's layout and order (rms_row_scale), then x' formed element
+// by element in this kernel's layout -- so the operand equals that of
+// qs_dec_rmsnorm followed by the plain kernel, bit for bit.
 template <int CPW, bool SB, bool PRE>
 __global__ __launch_bounds__(kThreads) void bx_kernel(BxArgs A) {
   using L = RowLds<CPW>;
@@ -118,7 +119,22 @@ __global__ __launch_bounds__(kThreads) void bx_kernel(BxArgs A) {
 
   XRawT<CPW> xr;
   load_x_raw(X, J.sv, lb, w, lane, xr);
-  uint2 nwq[CPW];  // PRE: the norm weights of this thread's quads
+  // PRE: the residual delta of row b (with up to two chunks per wave loaded
+  // with the row's h, ahead of its use; with three, at the row's start, which
+  // keeps the registers from spilling) and the norm weights of this thread's
+  // quads
+  constexpr bool kEarlyDelta = CPW <= 2;
+  auto load_delta = [&](int b, uint2 (&dst)[CPW]) {
+#pragma unroll
+    for (int u = 0; u < CPW; ++u) {
+      const int c = w + kWaves * u;
+      dst[u] = PRE && A.x2 && c < A.Sn ? *reinterpret_cast<const uint2*>(A.x2 + (int64_t)b * A.ldx2 + 256 * c + 4 * lane)
+                                       : make_uint2(0, 0);
+    }
+  };
+  uint2 dq_next[CPW];
+  if (kEarlyDelta && lb < A.B) load_delta(lb, dq_next);
+  uint2 nwq[CPW];
 #pragma unroll
   for (int u = 0; u < CPW; ++u) {
     const int c = w + kWaves * u;
@@ -132,23 +148,42 @@ __global__ __launch_bounds__(kThreads) void bx_kernel(BxArgs A) {
   for (int b = lb; b < A.B; b += stride) {
     float xv[CPW][4];
     if constexpr (PRE) {
-      const uint16_t* hrow = static_cast<const uint16_t*>(A.x) + (int64_t)b * A.ldx;
-      const uint16_t* drow = A.x2 ? A.x2 + (int64_t)b * A.ldx2 : nullptr;
+      const bool has_delta = A.x2 != nullptr;
       uint2 dq[CPW];
+      if constexpr (kEarlyDelta) {
 #pragma unroll
-      for (int u = 0; u < CPW; ++u) {
-        const int c = w + kWaves * u;
-        dq[u] = drow && c < A.Sn ? *reinterpret_cast<const uint2*>(drow + 256 * c + 4 * lane) : make_uint2(0, 0);
-      }
-      const float rs = rms_row_scale(hrow, drow, A.n, A.eps, w, lane, lx, pre_wsum);
+        for (int u = 0; u < CPW; ++u) dq[u] = dq_next[u];
+      } else {
+        const uint16_t* drow = A.x2 ? A.x2 + (int64_t)b * A.ldx2 : nullptr;
 #pragma unroll
-      for (int u = 0; u < CPW; ++u) {
-        const int c = w + kWaves * u;
-        uint32_t hp[2] = {xr.v[u].x, xr.v[u].y};  // h as loaded
-        if (drow) {
-          hp[0] = rms_pair_resid(hp[0], dq[u].x);
-          hp[1] = rms_pair_resid(hp[1], dq[u].y);
+        for (int u = 0; u < CPW; ++u) {
+          const int c = w + kWaves * u;
+          dq[u] = drow && c < A.Sn ? *reinterpret_cast<const uint2*>(drow + 256 * c + 4 * lane) : make_uint2(0, 0);
         }
+      }
+      // h' = bf16(h + delta) in this kernel's layout, staged as a bf16 row in
+      // the chunk rows' region (rewritten only after the norm), so that rs is
+      // taken in rmsnorm_kernel's layout and order from LDS rather than from
+      // a second read of the row in memory
+      uint16_t* hs = reinterpret_cast<uint16_t*>(lds + L::kY);
+      uint32_t hpv[CPW][2];
+#pragma unroll
+      for (int u = 0; u < CPW; ++u) {
+        const int c = w + kWaves * u;
+        hpv[u][0] = xr.v[u].x;  // h as loaded
+        hpv[u][1] = xr.v[u].y;
+        if (has_delta) {
+          hpv[u][0] = rms_pair_resid(hpv[u][0], dq[u].x);
+          hpv[u][1] = rms_pair_resid(hpv[u][1], dq[u].y);
+        }
+        if (c < A.Sn) *reinterpret_cast<uint2*>(hs + 256 * c + 4 * lane) = make_uint2(hpv[u][0], hpv[u][1]);
+      }
+      __syncthreads();  // the staged row is complete
+      const float rs = rms_row_scale(hs, nullptr, A.n, A.eps, w, lane, lx, pre_wsum);
+#pragma unroll
+      for (int u = 0; u < CPW; ++u) {
+        const int c = w + kWaves * u;
+        const uint32_t hp[2] = {hpv[u][0], hpv[u][1]};
         if (g == 0 && A.h_out && c < A.Sn)
           *reinterpret_cast<uint2*>(A.h_out + (int64_t)b * A.ldo + 256 * c + 4 * lane) = make_uint2(hp[0], hp[1]);
         const uint4 xq = make_uint4(rms_pair_apply(hp[0], nwq[u].x, rs), rms_pair_apply(hp[1], nwq[u].y, rs), 0, 0);
@@ -159,7 +194,10 @@ __global__ __launch_bounds__(kThreads) void bx_kernel(BxArgs A) {
     } else {
       finish_x(X, xr, w, lane, xv);
     }
-    if (b + stride < A.B) load_x_raw(X, J.sv, b + stride, w, lane, xr);  // the next row
+    if (b + stride < A.B) {  // the next row
+      load_x_raw(X, J.sv, b + stride, w, lane, xr);
+      if constexpr (PRE && kEarlyDelta) load_delta(b + stride, dq_next);
+    }
     float ss = 0.0f;
 #pragma unroll
     for (int u = 0; u < CPW; ++u)

@@ -67,8 +67,9 @@ __device__ __forceinline__ void rms_quad_apply(uint32_t (&h)[4][2], const uint32
 // rs of one bf16 row of n (a multiple of 256, at most 16384) with the
 // residual delta (may be null), for a work-group that holds the row in
 // another layout: thread (w, lane) of the 1024 reads its quad (chunks
-// 4 w + i, i < 4, columns 4 lane + u) of h and delta, and the sum runs in the
-// order above -- the same rs as rmsnorm_kernel's for the row.  wsum: kWaves
+// 4 w + i, i < 4, columns 4 lane + u) of h and delta (in memory or LDS; a
+// null delta with h' itself), and the sum runs in the order above -- the
+// same rs as rmsnorm_kernel's for the row.  wsum: kWaves
 // floats of LDS that no other thread reads meanwhile; one barrier inside.
 __device__ __forceinline__ float rms_row_scale(const uint16_t* h, const uint16_t* d, int n, float eps, int w,
                                                int lane, LaneX lx, float* wsum) {
