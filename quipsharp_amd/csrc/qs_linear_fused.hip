@@ -455,12 +455,16 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
     // quads inside the padded range are stored (zeros past the S chunks);
     // the first quad of row 0 was loaded at the start
     if (b > 0) load_x_quad(A.x, A.ldx, J.sv, A.Sn, b, 4 * w, lane, xr, A.x2, A.ldx2, A.nw);
+    // a wave whose quad lies past the row's chunks holds zeros, and past the
+    // padded chunk table stores nothing: it skips that arithmetic (a
+    // wave-uniform branch; its sums stay +0, added in the same order)
+    const bool row_quad = 4 * w < A.Sn, table_quad = 4 * w < Spad;
     float ss;
     if constexpr (XT == 3) {
       // the norm needs the whole row before the chunk table (one quad: n <=
       // 16384, checked on the host)
       const bool has_delta = A.x2 != nullptr;
-      float ssn = rms_quad_resid(xr.v, xr.v2, has_delta);
+      float ssn = row_quad ? rms_quad_resid(xr.v, xr.v2, has_delta) : 0.0f;
       ssn = wave_sum(ssn, lx);
       if (lane == 0) wsum[kWaves + w] = ssn;
       if (b == 0) {
@@ -483,14 +487,14 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
                 make_uint2(xr.v[i][0], xr.v[i][1]);
         }
       }
-      rms_quad_apply(xr.v, xr.nw, rs);
-      ss = store_quad(xr, XR0, XR1, xrs, 4 * w, lane, 4 * w < Spad);
+      if (row_quad) rms_quad_apply(xr.v, xr.nw, rs);
+      ss = table_quad ? store_quad(xr, XR0, XR1, xrs, 4 * w, lane, true) : 0.0f;
     } else {
-      ss = store_quad(xr, XR0, XR1, xrs, 4 * w, lane, 4 * w < Spad);
-      if (Spad > 64) {
+      ss = table_quad ? store_quad(xr, XR0, XR1, xrs, 4 * w, lane, true) : 0.0f;
+      if (64 + 4 * w < Spad) {
         XQuad<XT, SB> x2;
         load_x_quad(A.x, A.ldx, J.sv, A.Sn, b, 64 + 4 * w, lane, x2);
-        ss += store_quad(x2, XR0, XR1, xrs, 64 + 4 * w, lane, 64 + 4 * w < Spad);
+        ss += store_quad(x2, XR0, XR1, xrs, 64 + 4 * w, lane, true);
       }
     }
     ss = wave_sum(ss, lx);
