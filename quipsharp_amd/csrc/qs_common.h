@@ -175,11 +175,18 @@ __device__ __forceinline__ float load_as_float(const void* p, int dtype, int64_t
   return __uint_as_float(b);
 }
 
-// Round-to-nearest-even fp32 -> bf16, NaN kept quiet.
-__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  const uint32_t u = __float_as_uint(f);
-  const uint32_t r = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;  // round to nearest even
-  return (uint16_t)((u & 0x7FFFFFFFu) > 0x7F800000u ? ((u >> 16) | 0x40u) : r);  // NaN stays a quiet NaN
+// Round-to-nearest-even fp32 -> bf16, NaN kept quiet: (u + 0x7FFF + lsb) >> 16
+// of the bits u, and (u >> 16) | 0x40 for a NaN.  gfx950's conversion
+// instruction (v_cvt_pk_bf16_f32) gives exactly these bits for every one of
+// the 2^32 fp32 inputs (checked exhaustively on the device), in one
+// instruction for two values instead of six or seven integer operations per
+// value.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+// Two values: lo in bits 0-15, hi in bits 16-31.
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
 }
 
 __device__ __forceinline__ void store_from_float(void* p, int dtype, int64_t i, float v) {

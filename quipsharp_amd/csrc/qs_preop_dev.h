@@ -21,9 +21,7 @@ namespace qs {
 
 __device__ __forceinline__ float bf16_lo(uint32_t p) { return __uint_as_float(p << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t p) { return __uint_as_float(p & 0xFFFF0000u); }
-__device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {
-  return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
-}
+__device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) { return f32x2_to_bf16x2(lo, hi); }
 __device__ __forceinline__ float round_bf16(float f) { return __uint_as_float((uint32_t)f32_to_bf16(f) << 16); }
 
 // h' = bf16(x + delta) of one bf16 pair.
