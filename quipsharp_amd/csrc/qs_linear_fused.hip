@@ -546,7 +546,10 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
       for (int j = 0; j < 4; ++j) Z[(4 * q + j) * kZStride + t] = acc[j];
     }
     __syncthreads();  // slice rows complete (the chunk table and the norms are free again)
-    {
+    // the waves of the other phases hold the same slices as phase 0's: they
+    // read phase 0's operand rows; waves past the last slice read none (a
+    // wave-uniform branch)
+    if (ph == 0 && sl < A.S) {
       const float4 z4 = *reinterpret_cast<const float4*>(Z + w * kZStride + 4 * lane);
       float v[1][4] = {{z4.x, z4.y, z4.z, z4.w}};
       h256<1>(v, lane, lx);
@@ -562,7 +565,7 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
   epoch = __hip_atomic_load(J.out_in_kernel ? J.epoch : reinterpret_cast<unsigned*>(const_cast<float*>(J.sv)),
                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   // MFMA operand of lane (q, b = r16): columns 64q..64q+63 of this wave's
-  // slice (its own operand rows)
+  // slice (the operand rows of the phase-0 wave of the slice, wave wsl)
   const half8 hzero = {0, 0, 0, 0, 0, 0, 0, 0};
   half8 xb[8];
   half8 xs = hzero;
@@ -570,10 +573,10 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
 #pragma unroll
   for (int c = 0; c < 8; ++c) xb[c] = hzero;
   if (active && r16 < A.B) {
-    const _Float16* row = XH + (r16 * 16 + w) * kXStride + 64 * q;
+    const _Float16* row = XH + (r16 * 16 + wsl) * kXStride + 64 * q;
 #pragma unroll
     for (int c = 0; c < 8; ++c) xb[c] = *reinterpret_cast<const half8*>(row + 8 * c);
-    xs = *reinterpret_cast<const half8*>(XS + (r16 * 16 + w) * 32 + 8 * q);
+    xs = *reinterpret_cast<const half8*>(XS + (r16 * 16 + wsl) * 32 + 8 * q);
 #pragma unroll
     for (int c = 0; c < 8; ++c) slice_shift += (float)xs[c];
   }
