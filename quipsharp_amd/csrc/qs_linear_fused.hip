@@ -50,6 +50,8 @@
 // (kMaxPolls, NaN outputs if exceeded).
 #include <hip/hip_ext.h>
 
+#include <type_traits>
+
 #include "qs_forward_dev.h"
 #include "qs_linear_dev.h"
 #include "qs_preop_dev.h"
@@ -824,29 +826,41 @@ __global__ __launch_bounds__(kThreads) void linear_fused_kernel(FusedArgs A) {
     const float* const bsrc = J.bias ? J.bias : reinterpret_cast<const float*>(J.y1t);
     const bool has_bias = J.bias != nullptr;
     {
-      // M = K_p (x) H_{2^lsh_m}, entries e = tid + 1024 i at (e / 128, e % 128)
-      // (K loads first, unconditional: su is a dummy source without K)
+      // M = K_p (x) H_{2^lsh_m} over the rows < 16 ceil(S_m / 16) and columns
+      // < S_m padded to 32 in use: entry e = tid + 1024 i at (e >> LCS,
+      // e & (2^LCS - 1)), a row stride of 32, 64 or 128 columns (S_m <= 32:
+      // at most 32 rows, one entry per thread; <= 64: 64 rows, four; else
+      // sixteen) (K loads first, unconditional: su is a dummy source without K)
       const float* ksrc = m_lo ? J.Km : J.su;
       const int hm = (1 << J.lsh_m) - 1;
-      float kv[kMaxSF * 128 / kThreads];
+      auto build_m = [&](auto lcs, auto ni) {
+        constexpr int LCS = decltype(lcs)::value, NI = decltype(ni)::value;
+        // rows in use <= S_m padded to 32 <= 2^LCS
+        static_assert((1 << (2 * LCS)) <= NI * kThreads, "entries cover the rows in use");
+        float kv[NI];
 #pragma unroll
-      for (int i = 0; i < kMaxSF * 128 / kThreads; ++i) {
-        const int e = tid + kThreads * i, r = e >> 7, c = e & 127;
-        const int ki = (m_lo && r < Sm && c < Sm) ? (r >> J.lsh_m) * J.pm + (c >> J.lsh_m) : 0;
-        kv[i] = at_off(ksrc, (uint32_t)ki);
-      }
-#pragma unroll
-      for (int i = 0; i < kMaxSF * 128 / kThreads; ++i) {
-        const int e = tid + kThreads * i, r = e >> 7, c = e & 127;
-        if (r < rows && c < Smpad) {
-          float v = (r < Sm && c < Sm) ? (m_lo ? kv[i] : 1.0f) : 0.0f;
-          if (__builtin_popcount(r & c & hm) & 1) v = -v;
-          uint32_t hi, lo;
-          split_bf2(v, 0.0f, hi, lo);
-          M2h[r * ms + c] = (uint16_t)hi;
-          M2l[r * ms + c] = (uint16_t)lo;
+        for (int i = 0; i < NI; ++i) {
+          const int e = tid + kThreads * i, r = e >> LCS, c = e & ((1 << LCS) - 1);
+          const int ki = (m_lo && r < Sm && c < Sm) ? (r >> J.lsh_m) * J.pm + (c >> J.lsh_m) : 0;
+          kv[i] = at_off(ksrc, (uint32_t)ki);
         }
-      }
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          const int e = tid + kThreads * i, r = e >> LCS, c = e & ((1 << LCS) - 1);
+          if (r < rows && c < Smpad) {
+            float v = (r < Sm && c < Sm) ? (m_lo ? kv[i] : 1.0f) : 0.0f;
+            if (__builtin_popcount(r & c & hm) & 1) v = -v;
+            uint32_t hi, lo;
+            split_bf2(v, 0.0f, hi, lo);
+            M2h[r * ms + c] = (uint16_t)hi;
+            M2l[r * ms + c] = (uint16_t)lo;
+          }
+        }
+      };
+      using std::integral_constant;
+      if (Smpad <= 32) build_m(integral_constant<int, 5>{}, integral_constant<int, 1>{});
+      else if (Smpad <= 64) build_m(integral_constant<int, 6>{}, integral_constant<int, 4>{});
+      else build_m(integral_constant<int, 7>{}, integral_constant<int, 16>{});
     }
     for (int g2 = lb; g2 < kL2Groups; g2 += nwg) {
       const int t = 16 * g2 + r16;  // this lane's output column
