@@ -18,6 +18,7 @@ __constant__ Table8 kE81 = make_e81_table();
 
 constexpr int kWaves = 16;          // waves per encode work-group
 constexpr int kVecPerBlock = 64;    // one vector per lane
+constexpr int64_t kWaveEncodeMax = 32768;  // up to this many vectors: one vector per wave
 
 struct StageCfg {
   int n;
@@ -127,16 +128,9 @@ __device__ __forceinline__ uint32_t e8p_finish(const float x[8], int sb, int r, 
   return ((uint32_t)r << 8) | (sign7 << 1) | (uint32_t)sb;
 }
 
-__global__ __launch_bounds__(kWaves * 64) void rvq_encode_kernel(EncodeArgs A) {
-  __shared__ unsigned long long keys[2][kWaves][64];
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t v = (int64_t)blockIdx.x * kVecPerBlock + lane;
-  const bool valid = v < A.nvec;
-  const int64_t vv = valid ? v : 0;
-
-  // target (identical in every wave)
-  float res[8], tot[8];
+// The target of vector vv: base (+ delta, or + delta . dinv), divided by
+// in_div (one arithmetic for both encode kernels).
+__device__ __forceinline__ void encode_target(const EncodeArgs& A, int64_t vv, float (&res)[8]) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) res[i] = A.base[vv * A.ldbase + i];
   if (A.delta) {
@@ -160,6 +154,55 @@ __global__ __launch_bounds__(kWaves * 64) void rvq_encode_kernel(EncodeArgs A) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) res[i] = res[i] / A.in_div;
   }
+}
+
+// Key of E8P table row r at shift bit sb for the shifted magnitudes a and
+// the parities p_pos / p_neg: (distance, shift bit, row), ordered as the
+// lexicographic minimum.
+__device__ __forceinline__ unsigned long long e8p_key(const float a[8], bool p_pos, bool p_neg, int sb, int r) {
+  float T[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) T[i] = fabsf(kE8P.v[r][i]);
+  const bool odd = kE8P.v[r][7] < 0.0f ? p_neg : p_pos;
+  const float d2 = e8p_row_d2(a, T, odd);
+  return ((unsigned long long)__float_as_uint(d2) << 9) | ((unsigned)sb << 8) | (unsigned)r;
+}
+// Key of E8 one-bit table row r for x: (distance, row).
+__device__ __forceinline__ unsigned long long e81_key(const float x[8], int r) {
+  float d2 = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float d = x[i] - kE81.v[r][i];
+    float sq = d * d;
+    d2 = i == 0 ? sq : d2 + sq;
+  }
+  return ((unsigned long long)__float_as_uint(d2) << 8) | (unsigned)r;
+}
+// |x + 1/4| (sb 0) or |x - 1/4| (sb 1) and the parities of the signings.
+__device__ __forceinline__ void e8p_shifted(const float x[8], int sb, float a[8], bool& p_pos, bool& p_neg) {
+  uint32_t sx = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float xs = sb == 0 ? x[i] + 0.25f : x[i] - 0.25f;
+    a[i] = fabsf(xs);
+    sx ^= __float_as_uint(xs) >> 31;
+  }
+  const bool z7 = (sb == 0 ? x[7] + 0.25f : x[7] - 0.25f) == 0.0f;
+  p_pos = sx & 1;
+  p_neg = p_pos ^ !z7;
+}
+
+__global__ __launch_bounds__(kWaves * 64) void rvq_encode_kernel(EncodeArgs A) {
+  __shared__ unsigned long long keys[2][kWaves][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t v = (int64_t)blockIdx.x * kVecPerBlock + lane;
+  const bool valid = v < A.nvec;
+  const int64_t vv = valid ? v : 0;
+
+  // target (identical in every wave)
+  float res[8], tot[8];
+  encode_target(A, vv, res);
 #pragma unroll
   for (int i = 0; i < 8; ++i) tot[i] = 0.0f;
 
@@ -173,40 +216,17 @@ __global__ __launch_bounds__(kWaves * 64) void rvq_encode_kernel(EncodeArgs A) {
       best = ~0ull;
       for (int sb = 0; sb < 2; ++sb) {
         float a[8];
-        uint32_t sx = 0;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          float xs = sb == 0 ? x[i] + 0.25f : x[i] - 0.25f;
-          a[i] = fabsf(xs);
-          sx ^= __float_as_uint(xs) >> 31;
-        }
-        const bool z7 = (sb == 0 ? x[7] + 0.25f : x[7] - 0.25f) == 0.0f;
-        const bool p_pos = sx & 1;
-        const bool p_neg = p_pos ^ !z7;
+        bool p_pos, p_neg;
+        e8p_shifted(x, sb, a, p_pos, p_neg);
         for (int rr = 0; rr < 256 / kWaves; ++rr) {
-          const int r = wave * (256 / kWaves) + rr;
-          float T[8];
-#pragma unroll
-          for (int i = 0; i < 8; ++i) T[i] = fabsf(kE8P.v[r][i]);
-          const bool odd = kE8P.v[r][7] < 0.0f ? p_neg : p_pos;
-          const float d2 = e8p_row_d2(a, T, odd);
-          const unsigned long long key =
-              ((unsigned long long)__float_as_uint(d2) << 9) | ((unsigned)sb << 8) | (unsigned)r;
+          const unsigned long long key = e8p_key(a, p_pos, p_neg, sb, wave * (256 / kWaves) + rr);
           if (key < best) best = key;
         }
       }
     } else {
       best = ~0ull;
       for (int rr = 0; rr < 256 / kWaves; ++rr) {
-        const int r = wave * (256 / kWaves) + rr;
-        float d2 = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          float d = x[i] - kE81.v[r][i];
-          float sq = d * d;
-          d2 = i == 0 ? sq : d2 + sq;
-        }
-        const unsigned long long key = ((unsigned long long)__float_as_uint(d2) << 8) | (unsigned)r;
+        const unsigned long long key = e81_key(x, wave * (256 / kWaves) + rr);
         if (key < best) best = key;
       }
     }
@@ -255,8 +275,99 @@ __global__ __launch_bounds__(kWaves * 64) void rvq_encode_kernel(EncodeArgs A) {
   }
 }
 
+// Least 64-bit key over the wave.
+__device__ __forceinline__ unsigned long long wave_min_key(unsigned long long k) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const unsigned lo = __shfl_xor((unsigned)k, off), hi = __shfl_xor((unsigned)(k >> 32), off);
+    const unsigned long long o = ((unsigned long long)hi << 32) | lo;
+    k = o < k ? o : k;
+  }
+  return k;
+}
+
+// rvq_encode_kernel for short calls (the BlockLDLQ rounding step encodes one
+// 8-column block of m rows): one vector per wave, kWaves per work-group;
+// lane l evaluates table rows l + 64 k (k < 4) at both shifts and the wave
+// takes the least key.  The keys and their minimum are rvq_encode_kernel's,
+// so the codes and values are the same, with each vector's search over 64
+// lanes rather than one lane of each of 16 waves (a step of 4096 rows then
+// fills 256 work-groups instead of 64).
+__global__ __launch_bounds__(kWaves * 64) void rvq_encode_wave_kernel(EncodeArgs A) {
+  const int lane = threadIdx.x & 63;
+  const int64_t v = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (v >= A.nvec) return;  // wave-uniform (the kernel has no barrier)
+  float res[8], tot[8];
+  encode_target(A, v, res);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) tot[i] = 0.0f;
+  for (int s = 0; s < A.st.n; ++s) {
+    const float sc = A.st.scale[s];
+    float x[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = res[i] / sc;
+    unsigned long long best = ~0ull;
+    if (A.st.kind[s] == QS_STAGE_E8P) {
+      for (int sb = 0; sb < 2; ++sb) {
+        float a[8];
+        bool p_pos, p_neg;
+        e8p_shifted(x, sb, a, p_pos, p_neg);
+#pragma unroll
+        for (int k = 0; k < 256 / 64; ++k) {
+          const unsigned long long key = e8p_key(a, p_pos, p_neg, sb, lane + 64 * k);
+          if (key < best) best = key;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 256 / 64; ++k) {
+        const unsigned long long key = e81_key(x, lane + 64 * k);
+        if (key < best) best = key;
+      }
+    }
+    const unsigned long long win = wave_min_key(best);
+    float q[8];
+    uint32_t code;
+    if (A.st.kind[s] == QS_STAGE_E8P) {
+      code = e8p_finish(x, (int)((win >> 8) & 1), (int)(win & 0xFF), q);
+    } else {
+      const int r = (int)(win & 0xFF);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) q[i] = kE81.v[r][i];
+      code = (uint32_t)r;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float qs = q[i] * sc;
+      tot[i] = tot[i] + qs;
+      res[i] = res[i] - qs;
+    }
+    if (lane == 0 && A.codes) store_code(A.codes, A.code_bytes, s * A.code_stage_stride + v * A.code_stride, code);
+  }
+  if (A.out_mul != 1.0f) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) tot[i] = tot[i] * A.out_mul;
+  }
+  if (lane == 0) {
+    if (A.vals) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) A.vals[v * A.ldvals + i] = tot[i];
+    }
+    if (A.resid) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) A.resid[v * A.ldresid + i] = A.w[v * A.ldw + i] - tot[i];
+    }
+  }
+}
+
 int launch_encode(EncodeArgs& A, hipStream_t stream) {
   if (A.nvec == 0) return QS_OK;
+  if (A.nvec <= kWaveEncodeMax) {
+    const int64_t blocks = (A.nvec + kWaves - 1) / kWaves;
+    hipLaunchKernelGGL(rvq_encode_wave_kernel, dim3((unsigned)blocks), dim3(kWaves * 64), 0, stream, A);
+    QS_LAUNCHED("rvq_encode_wave_kernel");
+    return QS_OK;
+  }
   const int64_t blocks = (A.nvec + kVecPerBlock - 1) / kVecPerBlock;
   QS_REQUIRE(blocks < (1ll << 31), "too many vectors: %lld", (long long)A.nvec);
   hipLaunchKernelGGL(rvq_encode_kernel, dim3((unsigned)blocks), dim3(kWaves * 64), 0, stream, A);
