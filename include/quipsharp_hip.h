@@ -116,6 +116,26 @@ int qs_ldlq_step(const float *base, int64_t ldbase, const float *delta, const fl
                  void *codes, int code_bytes, int64_t code_stage_stride, int64_t code_stride,
                  qs_stream_t stream);
 
+/* A chunk of nb <= 16 blocks c0 .. c0 + nb - 1 of the BlockLDLQ refinement
+ * pass (ldlq.py:132-139), in descending block order, all in one launch: for
+ * each row r and block k
+ *   delta  = p[r][8 (k - c0) .. + 7] + sum_{c < 8 nb} e[r][8 c0 + c] * h[c][8 k .. 8 k + 7]
+ *   target = wq[r][8 k ..] + delta @ dinv[k]          (dinv: [T][8][8] fp32)
+ *   then as qs_ldlq_step: wq[r][8 k ..] = q, e[r][8 k ..] = w[r][8 k ..] - q, codes.
+ * w, wq, e, p are row-strided views of m rows (e is the error W - Wq, its
+ * chunk columns read as the pass leaves them); h points at row 8 c0 of H (ldh
+ * per row); p holds the product of E with H's block columns of the chunk
+ * over the columns outside the chunk (E @ H[:, chunk] - E[:, chunk] @
+ * H[chunk, chunk], taken at the chunk's start).  No counterpart in the
+ * reference, which forms E @ H[:, block] for each block: the library's
+ * BlockLDLQ reads E once per chunk of blocks, and launches once per chunk.
+ * Codes agree with qs_ldlq_step's except where the reassociated fp32 sums
+ * move a near-tie. */
+int qs_ldlq_chunk(const float *w, int64_t ldw, float *wq, int64_t ldwq, float *e, int64_t lde, const float *p,
+                  int64_t ldp, const float *h, int64_t ldh, const float *dinv, int c0, int nb, int64_t m,
+                  int nstages, const int *kinds, const float *scales, void *codes, int code_bytes,
+                  int64_t code_stage_stride, int64_t code_stride, qs_stream_t stream);
+
 /* ---------------------------------------------------------------------------
  * Randomized Hadamard transform
  * ------------------------------------------------------------------------- */

@@ -60,6 +60,8 @@ _SIGNATURES = {
     "qs_rvq_decode": ([_vp, _int, _i64, _i64, _int, _int_p, _f32_p, _f32, _vp, _vp], _int),
     "qs_ldlq_step": ([_vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _int, _int_p, _f32_p,
                       _vp, _int, _i64, _i64, _vp], _int),
+    "qs_ldlq_chunk": ([_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _int, _int, _i64, _int, _int_p,
+                       _f32_p, _vp, _int, _i64, _i64, _vp], _int),
     "qs_rht_f32": ([_vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _int, _vp, _vp], _int),
     "qs_pack_codes": ([_vp, _int, _i64, _i64, _int, _int, _vp, _vp], _int),
     "qs_linear_workspace_bytes": ([_i64, _i64, _i64, _int], ctypes.c_size_t),

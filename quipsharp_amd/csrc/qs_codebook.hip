@@ -19,6 +19,8 @@ __constant__ Table8 kE81 = make_e81_table();
 constexpr int kWaves = 16;          // waves per encode work-group
 constexpr int kVecPerBlock = 64;    // one vector per lane
 constexpr int64_t kWaveEncodeMax = 32768;  // up to this many vectors: one vector per wave
+constexpr int kVecWaves = 4;  // waves (vectors or rows) per work-group of the one-vector-per-wave kernels
+                              // (small work-groups: a wave may use up to 512 registers, no spills)
 
 struct StageCfg {
   int n;
@@ -128,6 +130,23 @@ __device__ __forceinline__ uint32_t e8p_finish(const float x[8], int sb, int r, 
   return ((uint32_t)r << 8) | (sign7 << 1) | (uint32_t)sb;
 }
 
+// res += dl . dinv (dinv 8 x 8, row-major), or res += dl without dinv (one
+// arithmetic for every rounding step).
+__device__ __forceinline__ void add_delta(float (&res)[8], const float (&dl)[8], const float* dinv) {
+  if (dinv) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float acc = dl[0] * dinv[i];
+#pragma unroll
+      for (int j = 1; j < 8; ++j) acc = __builtin_fmaf(dl[j], dinv[j * 8 + i], acc);
+      res[i] = res[i] + acc;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) res[i] = res[i] + dl[i];
+  }
+}
+
 // The target of vector vv: base (+ delta, or + delta . dinv), divided by
 // in_div (one arithmetic for both encode kernels).
 __device__ __forceinline__ void encode_target(const EncodeArgs& A, int64_t vv, float (&res)[8]) {
@@ -137,18 +156,7 @@ __device__ __forceinline__ void encode_target(const EncodeArgs& A, int64_t vv, f
     float dl[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) dl[i] = A.delta[vv * 8 + i];
-    if (A.dinv) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float acc = dl[0] * A.dinv[i];
-#pragma unroll
-        for (int j = 1; j < 8; ++j) acc = __builtin_fmaf(dl[j], A.dinv[j * 8 + i], acc);
-        res[i] = res[i] + acc;
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) res[i] = res[i] + dl[i];
-    }
+    add_delta(res, dl, A.dinv);
   }
   if (A.in_div != 1.0f) {
 #pragma unroll
@@ -286,40 +294,34 @@ __device__ __forceinline__ unsigned long long wave_min_key(unsigned long long k)
   return k;
 }
 
-// rvq_encode_kernel for short calls (the BlockLDLQ rounding step encodes one
-// 8-column block of m rows): one vector per wave, kWaves per work-group;
-// lane l evaluates table rows l + 64 k (k < 4) at both shifts and the wave
-// takes the least key.  The keys and their minimum are rvq_encode_kernel's,
-// so the codes and values are the same, with each vector's search over 64
-// lanes rather than one lane of each of 16 waves (a step of 4096 rows then
-// fills 256 work-groups instead of 64).
-__global__ __launch_bounds__(kWaves * 64) void rvq_encode_wave_kernel(EncodeArgs A) {
-  const int lane = threadIdx.x & 63;
-  const int64_t v = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
-  if (v >= A.nvec) return;  // wave-uniform (the kernel has no barrier)
-  float res[8], tot[8];
-  encode_target(A, v, res);
+// The stages of the target res (the same in every lane of the wave) on one
+// wave: lane l evaluates table rows l + 64 k (k < 4) at both shifts and the
+// wave takes the least key -- rvq_encode_kernel's keys and minimum, so its
+// codes and values.  tot = the sum of the stage values; res is left as the
+// residual; lane 0 stores the code of stage s at codes + s stage_stride + off.
+__device__ __forceinline__ void wave_encode(const StageCfg& st, float (&res)[8], float (&tot)[8], int lane,
+                                            void* codes, int code_bytes, int64_t stage_stride, int64_t off) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) tot[i] = 0.0f;
-  for (int s = 0; s < A.st.n; ++s) {
-    const float sc = A.st.scale[s];
+  for (int s = 0; s < st.n; ++s) {
+    const float sc = st.scale[s];
     float x[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) x[i] = res[i] / sc;
     unsigned long long best = ~0ull;
-    if (A.st.kind[s] == QS_STAGE_E8P) {
+    if (st.kind[s] == QS_STAGE_E8P) {
       for (int sb = 0; sb < 2; ++sb) {
         float a[8];
         bool p_pos, p_neg;
         e8p_shifted(x, sb, a, p_pos, p_neg);
-#pragma unroll
+#pragma unroll 1
         for (int k = 0; k < 256 / 64; ++k) {
           const unsigned long long key = e8p_key(a, p_pos, p_neg, sb, lane + 64 * k);
           if (key < best) best = key;
         }
       }
     } else {
-#pragma unroll
+#pragma unroll 1
       for (int k = 0; k < 256 / 64; ++k) {
         const unsigned long long key = e81_key(x, lane + 64 * k);
         if (key < best) best = key;
@@ -328,7 +330,7 @@ __global__ __launch_bounds__(kWaves * 64) void rvq_encode_wave_kernel(EncodeArgs
     const unsigned long long win = wave_min_key(best);
     float q[8];
     uint32_t code;
-    if (A.st.kind[s] == QS_STAGE_E8P) {
+    if (st.kind[s] == QS_STAGE_E8P) {
       code = e8p_finish(x, (int)((win >> 8) & 1), (int)(win & 0xFF), q);
     } else {
       const int r = (int)(win & 0xFF);
@@ -342,8 +344,20 @@ __global__ __launch_bounds__(kWaves * 64) void rvq_encode_wave_kernel(EncodeArgs
       tot[i] = tot[i] + qs;
       res[i] = res[i] - qs;
     }
-    if (lane == 0 && A.codes) store_code(A.codes, A.code_bytes, s * A.code_stage_stride + v * A.code_stride, code);
+    if (lane == 0 && codes) store_code(codes, code_bytes, s * stage_stride + off, code);
   }
+}
+
+// rvq_encode_kernel for short calls (the BlockLDLQ rounding step encodes one
+// 8-column block of m rows): one vector per wave (wave_encode), so a step of
+// 4096 rows runs 4096 waves instead of 64 work-groups of one vector per lane.
+__global__ __launch_bounds__(kVecWaves * 64) void rvq_encode_wave_kernel(EncodeArgs A) {
+  const int lane = threadIdx.x & 63;
+  const int64_t v = (int64_t)blockIdx.x * kVecWaves + (threadIdx.x >> 6);
+  if (v >= A.nvec) return;  // wave-uniform (the kernel has no barrier)
+  float res[8], tot[8];
+  encode_target(A, v, res);
+  wave_encode(A.st, res, tot, lane, A.codes, A.code_bytes, A.code_stage_stride, v * A.code_stride);
   if (A.out_mul != 1.0f) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) tot[i] = tot[i] * A.out_mul;
@@ -360,11 +374,98 @@ __global__ __launch_bounds__(kWaves * 64) void rvq_encode_wave_kernel(EncodeArgs
   }
 }
 
+// A chunk of blocks c0 .. c0 + nb - 1 of the BlockLDLQ refinement pass, the
+// blocks in descending order, one row per wave: for block k
+//   delta = p[row][8 (k - c0) ..] + E[row][chunk columns] . H[chunk rows][block k]
+//   target = wq[row][block k] + delta . dinv[k]
+// then the stages (wave_encode), wq and E of block k rewritten.  The chunk's
+// columns of E stay in registers (lane l: columns l and l + 64 of the chunk).
+constexpr int kChunkBlocks = 16;  // blocks per chunk (8 * 16 = 128 columns: two per lane)
+struct ChunkArgs {
+  const float* w;
+  int64_t ldw;
+  float* wq;
+  int64_t ldwq;
+  float* e;
+  int64_t lde;
+  const float* p;  // [m][8 nb]: the product of E with H's block columns outside the chunk
+  int64_t ldp;
+  const float* h;  // H's rows of the chunk (row c0 8 of H), ldh per row
+  int64_t ldh;
+  const float* dinv;  // [T][8][8]
+  int c0, nb;
+  int64_t m;
+  void* codes;
+  int code_bytes;
+  int64_t code_stage_stride, code_stride;
+  StageCfg st;
+};
+__global__ __launch_bounds__(kVecWaves * 64) void ldlq_chunk_kernel(ChunkArgs A) {
+  const int lane = threadIdx.x & 63;
+  const int64_t v = (int64_t)blockIdx.x * kVecWaves + (threadIdx.x >> 6);
+  if (v >= A.m) return;  // wave-uniform (the kernel has no barrier)
+  const int wc = 8 * A.nb;
+  float ec[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int c = lane + 64 * i;
+    ec[i] = c < wc ? A.e[v * A.lde + 8 * A.c0 + c] : 0.0f;
+  }
+  for (int kk = A.nb - 1; kk >= 0; --kk) {
+    const int k = A.c0 + kk;
+    float part[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) part[j] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      // rows past the chunk load row 0 and are selected away (no load under a branch)
+      const int c = lane + 64 * i;
+      const float* hr = A.h + (int64_t)(c < wc ? c : 0) * A.ldh + 8 * k;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float f = __builtin_fmaf(ec[i], hr[j], part[j]);
+        part[j] = c < wc ? f : part[j];
+      }
+    }
+    float dl[8], res[8], tot[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float t = part[j];
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) t = t + __shfl_xor(t, off);  // the same sum in every lane
+      dl[j] = A.p[v * A.ldp + 8 * kk + j] + t;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) res[i] = A.wq[v * A.ldwq + 8 * k + i];
+    add_delta(res, dl, A.dinv + 64 * k);
+    wave_encode(A.st, res, tot, lane, A.codes, A.code_bytes, A.code_stage_stride, v * A.code_stride + k);
+    float r8[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r8[i] = A.w[v * A.ldw + 8 * k + i] - tot[i];
+    if (lane == 0) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        A.wq[v * A.ldwq + 8 * k + i] = tot[i];
+        A.e[v * A.lde + 8 * k + i] = r8[i];
+      }
+    }
+    // block k's new E into the lanes that hold its columns
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int cb = lane + 64 * i - 8 * kk;
+      float nv = r8[0];
+#pragma unroll
+      for (int t = 1; t < 8; ++t) nv = cb == t ? r8[t] : nv;
+      if (cb >= 0 && cb < 8) ec[i] = nv;
+    }
+  }
+}
+
 int launch_encode(EncodeArgs& A, hipStream_t stream) {
   if (A.nvec == 0) return QS_OK;
   if (A.nvec <= kWaveEncodeMax) {
-    const int64_t blocks = (A.nvec + kWaves - 1) / kWaves;
-    hipLaunchKernelGGL(rvq_encode_wave_kernel, dim3((unsigned)blocks), dim3(kWaves * 64), 0, stream, A);
+    const int64_t blocks = (A.nvec + kVecWaves - 1) / kVecWaves;
+    hipLaunchKernelGGL(rvq_encode_wave_kernel, dim3((unsigned)blocks), dim3(kVecWaves * 64), 0, stream, A);
     QS_LAUNCHED("rvq_encode_wave_kernel");
     return QS_OK;
   }
@@ -580,6 +681,46 @@ extern "C" int qs_ldlq_step(const float* base, int64_t ldbase, const float* delt
   A.in_div = 1.0f;
   A.out_mul = 1.0f;
   return launch_encode(A, as_stream(stream));
+}
+
+extern "C" int qs_ldlq_chunk(const float* w, int64_t ldw, float* wq, int64_t ldwq, float* e, int64_t lde,
+                             const float* p, int64_t ldp, const float* h, int64_t ldh, const float* dinv, int c0,
+                             int nb, int64_t m, int nstages, const int* kinds, const float* scales, void* codes,
+                             int code_bytes, int64_t code_stage_stride, int64_t code_stride, qs_stream_t stream) {
+  QS_REQUIRE(m >= 0 && nb >= 1 && nb <= kChunkBlocks && c0 >= 0, "m %lld, nb %d (1..%d), c0 %d", (long long)m, nb,
+             kChunkBlocks, c0);
+  QS_REQUIRE(m == 0 || (w && wq && e && p && h && dinv), "w, wq, e, p, h and dinv are required");
+  QS_REQUIRE(ldw >= 8 * (c0 + nb) && ldwq >= 8 * (c0 + nb) && lde >= 8 * (c0 + nb) && ldp >= 8 * nb &&
+                 ldh >= 8 * (c0 + nb),
+             "row strides too small");
+  QS_REQUIRE(!codes || code_bytes == 2 || code_bytes == 4 || code_bytes == 8, "code_bytes must be 2, 4 or 8");
+  ChunkArgs A{};
+  int rc = fill_stages(A.st, nstages, kinds, scales);
+  if (rc) return rc;
+  if (m == 0) return QS_OK;
+  QS_REQUIRE((m + kVecWaves - 1) / kVecWaves < (1ll << 31), "m too large: %lld", (long long)m);
+  A.w = w;
+  A.ldw = ldw;
+  A.wq = wq;
+  A.ldwq = ldwq;
+  A.e = e;
+  A.lde = lde;
+  A.p = p;
+  A.ldp = ldp;
+  A.h = h;
+  A.ldh = ldh;
+  A.dinv = dinv;
+  A.c0 = c0;
+  A.nb = nb;
+  A.m = m;
+  A.codes = codes;
+  A.code_bytes = code_bytes;
+  A.code_stage_stride = code_stage_stride;
+  A.code_stride = code_stride;
+  hipLaunchKernelGGL(ldlq_chunk_kernel, dim3((unsigned)((m + kVecWaves - 1) / kVecWaves)), dim3(kVecWaves * 64), 0,
+                     as_stream(stream), A);
+  QS_LAUNCHED("ldlq_chunk_kernel");
+  return QS_OK;
 }
 
 extern "C" int qs_rvq_decode(const void* codes, int code_bytes, int64_t code_stage_stride, int64_t nvec,

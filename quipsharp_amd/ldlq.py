@@ -99,6 +99,10 @@ def block_ldlq(W: Tensor, L: Tensor, g: int, quantize_fn, H: Tensor = None, tune
     return Wq
 
 
+_TUNE_CHUNK = 16  # blocks per chunk of the refinement pass (qs_ldlq_chunk: at most 16)
+_TUNE_CHUNKED = True  # False: the refinement forms E @ H[:, block] for each block (ldlq.py:136-138's form)
+
+
 def block_ldlq_native(W: Tensor, L: Tensor, kinds, scales, H: Tensor = None, tune_iters: int = 10):
     """BlockLDLQ with the library's residual-VQ codebook (g = 8), one fused
     kernel per rounding step.  Returns (Wq (m, n), codes int64 (S, m, T))."""
@@ -138,9 +142,29 @@ def block_ldlq_native(W: Tensor, L: Tensor, kinds, scales, H: Tensor = None, tun
         H = H.float().contiguous()
         dinv = _diag_inv(H, g).contiguous()
         dp = dinv.data_ptr()
+        if not _TUNE_CHUNKED:
+            for _ in range(tune_iters):
+                for k in reversed(range(T)):
+                    ck = slice(k * g, (k + 1) * g)
+                    torch.mm(E, H[:, ck], out=fb)
+                    step(k, wqp + k * g * esz, dp + k * g * g * 4)
+            return Wq, codes
+        # E @ H[:, ck] for each block, with E as the pass leaves it: within a
+        # chunk of blocks only the chunk's columns of E change, so the product
+        # with the other columns is formed once per chunk (P = E @ H[:, cc] -
+        # E[:, cc] @ H[cc, cc]) and one launch runs the chunk's blocks, adding
+        # the chunk's current columns itself (qs_ldlq_chunk): E is read once
+        # per chunk, and there is one launch per chunk instead of two per block
+        C = min(_TUNE_CHUNK, T)
+        P = torch.empty(m, C * g, dtype=torch.float32, device=W.device)
+        hp = H.data_ptr()
         for _ in range(tune_iters):
-            for k in reversed(range(T)):
-                ck = slice(k * g, (k + 1) * g)
-                torch.mm(E, H[:, ck], out=fb)
-                step(k, wqp + k * g * esz, dp + k * g * g * 4)
+            for c0 in reversed(range(0, T, C)):
+                c1 = min(c0 + C, T)
+                cc = slice(c0 * g, c1 * g)
+                Pc = P if c1 - c0 == C else torch.empty(m, (c1 - c0) * g, dtype=torch.float32, device=W.device)
+                torch.mm(E, H[:, cc], out=Pc)
+                Pc.addmm_(E[:, cc], H[cc, cc], alpha=-1.0)
+                _lib.check(lib.qs_ldlq_chunk(wp, n, wqp, n, ep, n, Pc.data_ptr(), Pc.stride(0), hp + c0 * g * n * 4, n,
+                                             dp, c0, c1 - c0, m, S, kinds_c, scales_c, cp, 8, m * T, T, stream))
     return Wq, codes

@@ -131,6 +131,29 @@ def test_native_ldlq_matches_callback_ldlq(dev):
     assert (Wq_cb == Wq_nat).float().mean() > 0.95
 
 
+@pytest.mark.parametrize("m,n,kinds,scales", [(512, 1024, [0], [1.0]), (300, 392, [0, 1], [1.0, 0.47])])
+def test_chunked_refinement_matches_per_block(dev, monkeypatch, m, n, kinds, scales):
+    """The refinement pass run a chunk of blocks per launch with the feedback
+    formed in the kernel (qs_ldlq_chunk: E read once per chunk; n = 392: 49
+    blocks, a partial last chunk; a 3-bit residual stage) against the same
+    pass with E @ H[:, block] per block (qs_ldlq_step): the same sums
+    reassociated in fp32, so the codes agree except at near-ties and the proxy
+    loss is the same."""
+    from quipsharp_amd import ldlq
+    torch.manual_seed(11)
+    W = torch.randn(m, n, device=dev) * 0.5
+    H = psd(n, 9, dev)
+    L, _ = ldlq.block_ldl(H, 8)
+    Wq_c, codes_c = ldlq.block_ldlq_native(W, L, kinds, scales, H=H, tune_iters=4)
+    monkeypatch.setattr(ldlq, "_TUNE_CHUNKED", False)
+    Wq_b, codes_b = ldlq.block_ldlq_native(W, L, kinds, scales, H=H, tune_iters=4)
+    agree = (codes_c == codes_b).float().mean().item()
+    print(f"chunked vs per-block refinement: code agreement {agree:.5f}", flush=True)
+    assert agree > 0.999
+    pc, pb = proxy(Wq_c, W, H), proxy(Wq_b, W, H)
+    assert abs(pc - pb) <= 2e-3 * pb
+
+
 def test_refinement_does_not_worsen(dev):
     """quipsharp tests/test_ldlq.py:108-131 and test_quantize_e2e.py:126-151."""
     from quipsharp_amd.codebooks.e8p import E8PCodebook
