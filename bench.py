@@ -567,7 +567,7 @@ def kernel_rates(dev):
 
 
 # batch sizes each layer stack is measured at
-STACK_BATCHES = {"llama3_8b": [1, 4, 16], "qwen25_7b": [1], "qwen3_32b": [1, 8]}
+STACK_BATCHES = {"llama2_7b": [1, 16], "llama3_8b": [1, 4, 16], "qwen25_7b": [1], "qwen3_32b": [1, 8]}
 
 
 def stack_batches(key, batches, steps, warmup, dev):
