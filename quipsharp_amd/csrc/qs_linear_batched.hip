@@ -409,8 +409,9 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
     floatx4 acc2 = {0.f, 0.f, 0.f, 0.f};
     const uint4 cw = pre[u];
     const uint2 cw1 = pre1[u];
-    if (valid) {
-      // (idle waves decode tile 0; their results are not stored)
+    if (valid && active) {
+      // (idle waves skip the decode, a wave-uniform branch: they hold no
+      // slice, and their LUT reads would take LDS cycles from the others)
       const uint32_t wd[4] = {cw.x, cw.y, cw.z, cw.w};
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
