@@ -200,6 +200,11 @@ __device__ __forceinline__ void e8p_shifted(const float x[8], int sb, float a[8]
   p_neg = p_pos ^ !z7;
 }
 
+// One vector per lane; wave w evaluates table rows 16 w .. 16 w + 15 and the
+// waves' least keys meet in LDS.  The body is written out here rather than
+// through the helpers of the one-vector-per-wave kernels below (the same
+// arithmetic): built from them it took 90 SGPRs instead of 74 and ran
+// ~25 % slower on a 2^21-vector call.
 __global__ __launch_bounds__(kWaves * 64) void rvq_encode_kernel(EncodeArgs A) {
   __shared__ unsigned long long keys[2][kWaves][64];
   const int lane = threadIdx.x & 63;
@@ -210,7 +215,29 @@ __global__ __launch_bounds__(kWaves * 64) void rvq_encode_kernel(EncodeArgs A) {
 
   // target (identical in every wave)
   float res[8], tot[8];
-  encode_target(A, vv, res);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) res[i] = A.base[vv * A.ldbase + i];
+  if (A.delta) {
+    float dl[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dl[i] = A.delta[vv * 8 + i];
+    if (A.dinv) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float acc = dl[0] * A.dinv[i];
+#pragma unroll
+        for (int j = 1; j < 8; ++j) acc = __builtin_fmaf(dl[j], A.dinv[j * 8 + i], acc);
+        res[i] = res[i] + acc;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) res[i] = res[i] + dl[i];
+    }
+  }
+  if (A.in_div != 1.0f) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) res[i] = res[i] / A.in_div;
+  }
 #pragma unroll
   for (int i = 0; i < 8; ++i) tot[i] = 0.0f;
 
@@ -224,17 +251,40 @@ __global__ __launch_bounds__(kWaves * 64) void rvq_encode_kernel(EncodeArgs A) {
       best = ~0ull;
       for (int sb = 0; sb < 2; ++sb) {
         float a[8];
-        bool p_pos, p_neg;
-        e8p_shifted(x, sb, a, p_pos, p_neg);
+        uint32_t sx = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          float xs = sb == 0 ? x[i] + 0.25f : x[i] - 0.25f;
+          a[i] = fabsf(xs);
+          sx ^= __float_as_uint(xs) >> 31;
+        }
+        const bool z7 = (sb == 0 ? x[7] + 0.25f : x[7] - 0.25f) == 0.0f;
+        const bool p_pos = sx & 1;
+        const bool p_neg = p_pos ^ !z7;
         for (int rr = 0; rr < 256 / kWaves; ++rr) {
-          const unsigned long long key = e8p_key(a, p_pos, p_neg, sb, wave * (256 / kWaves) + rr);
+          const int r = wave * (256 / kWaves) + rr;
+          float T[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) T[i] = fabsf(kE8P.v[r][i]);
+          const bool odd = kE8P.v[r][7] < 0.0f ? p_neg : p_pos;
+          const float d2 = e8p_row_d2(a, T, odd);
+          const unsigned long long key =
+              ((unsigned long long)__float_as_uint(d2) << 9) | ((unsigned)sb << 8) | (unsigned)r;
           if (key < best) best = key;
         }
       }
     } else {
       best = ~0ull;
       for (int rr = 0; rr < 256 / kWaves; ++rr) {
-        const unsigned long long key = e81_key(x, wave * (256 / kWaves) + rr);
+        const int r = wave * (256 / kWaves) + rr;
+        float d2 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          float d = x[i] - kE81.v[r][i];
+          float sq = d * d;
+          d2 = i == 0 ? sq : d2 + sq;
+        }
+        const unsigned long long key = ((unsigned long long)__float_as_uint(d2) << 8) | (unsigned)r;
         if (key < best) best = key;
       }
     }
