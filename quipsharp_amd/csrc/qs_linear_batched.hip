@@ -362,11 +362,14 @@ __global__ __launch_bounds__(kThreads) void bm_kernel(BmArgs A) {
   const half8 xs = *reinterpret_cast<const half8*>(J.sg + sla * 512 + 8 * lrow);
   // code tiles stream through a ring of kPrefetch registers (see the row
   // loop).  Byte offset of this lane's 16 code bytes of row block rb; past
-  // the end, the work-group's own last row block again, and the last slice
-  // for an idle wave (spread over the chip: one tile read by every idle wave
-  // is a hot spot); m n / 4 < 2^32 bytes of codes
+  // the end, the work-group's own last row block again, and for an idle
+  // wave the group's first slice, the tile wave 0 of this work-group reads
+  // at the same time (an L2 hit; a slice index past the group's own would
+  // fetch another group's tiles, on another XCD's L2); m n / 4 < 2^32 bytes
+  // of codes
   const int rb_last = jr + ((RB - 1 - jr) / J.Gr) * J.Gr;
-  const uint32_t slc = (uint32_t)(sl < A.S ? sl : A.S - 1);
+  const int sl0 = sg * A.W < A.S ? sg * A.W : A.S - 1;
+  const uint32_t slc = (uint32_t)(active ? sl : sl0);
   auto code_off = [&](int rb) -> uint32_t {
     const uint32_t r = (uint32_t)(rb < RB ? rb : rb_last);
     return (r * (uint32_t)A.S + slc) * 1024u + 16u * lane;
