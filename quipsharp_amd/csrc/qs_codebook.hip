@@ -364,14 +364,17 @@ __device__ __forceinline__ void wave_encode(const StageCfg& st, float (&res)[8],
         float a[8];
         bool p_pos, p_neg;
         e8p_shifted(x, sb, a, p_pos, p_neg);
-#pragma unroll 1
+        // two table rows per iteration: their loads overlap (4096-row
+        // refinement chunk 2.3 % faster than one row per iteration; all four
+        // at once took 147 registers, too many for four waves per SIMD)
+#pragma unroll 2
         for (int k = 0; k < 256 / 64; ++k) {
           const unsigned long long key = e8p_key(a, p_pos, p_neg, sb, lane + 64 * k);
           if (key < best) best = key;
         }
       }
     } else {
-#pragma unroll 1
+#pragma unroll 2
       for (int k = 0; k < 256 / 64; ++k) {
         const unsigned long long key = e81_key(x, lane + 64 * k);
         if (key < best) best = key;
